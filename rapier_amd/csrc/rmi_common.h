@@ -1,0 +1,71 @@
+// rmi_common.h - shared definitions for the MI355X (gfx950) kernels behind the rapier_mi C ABI.
+//
+// Block formats are GGUF's (reference src/native_mmvq.cu:98-140): Q6_K 210 B per 256 weights, Q8_0 34 B per 32,
+// Q8_1 activations 36 B per 32 (fp16 d, fp16 sum, 32 int8 codes).  Everything here is wave64 CDNA4 code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/rapier_mi.h"
+
+namespace rmi {
+
+constexpr int kQ6KBytes = 210;
+constexpr int kQ8_0Bytes = 34;
+constexpr int kQ8_1Bytes = 36;
+constexpr int kMaxCols = 16;   // the reference's validate_shape limit (mmvq:2312-2318)
+
+// ---- error reporting: the C ABI returns codes, the message of the last failure is kept per thread ----
+void set_error(const char* msg);
+int fail(int code, const char* msg);
+int launch_status(const char* what);   // hipGetLastError after a launch -> RMI_ERR_LAUNCH with the HIP message
+
+inline bool aligned4(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+inline bool aligned16(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---- device helpers ----
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits & 0xffffu)));
+}
+
+// fp16 store with the Q8_1 finite policy: round to nearest even, saturated to +-65504
+__device__ __forceinline__ uint32_t float_to_half_sat(float v) {
+    v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v)));
+}
+
+// xor butterfly over groups of W lanes; every lane of a group ends with the same value
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, W);
+    return v;
+}
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int off = W / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, W));
+    return v;
+}
+
+// Quantizes one value per lane into the Q8_1 block its 32-lane group owns (lane & 31 = element).
+// d = amax / 127 in fp32, q = roundf(v / d) (0 for an all-zero block), ds = (fp16 d, fp16 sum) saturated.
+// amax and sum use the 32-lane xor butterfly, so every finite block has one defined bit pattern.
+__device__ __forceinline__ void q8_1_store_lane(float v, uint8_t* block) {
+    const float amax = group_max<32>(fabsf(v));
+    const float sum = group_sum<32>(v);
+    const float d = amax / 127.0f;
+    const int q = amax == 0.0f ? 0 : static_cast<int>(roundf(v / d));
+    const int lane = threadIdx.x & 31;
+    block[4 + lane] = static_cast<uint8_t>(static_cast<int8_t>(q));
+    if (lane == 0) {
+        *reinterpret_cast<uint32_t*>(block) = float_to_half_sat(d) | (float_to_half_sat(sum) << 16);
+    }
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+}  // namespace rmi

@@ -1,0 +1,361 @@
+"""Pins the CPU oracle before anything is compared against it.
+
+Each check uses a form independent of the oracle's own code: ggml's published dequantize_row_q6_K loop, the
+reference's lane-mapped dp4a form (mmvq:733-748), numpy fp64 matrix forms, the Gated DeltaNet paper's
+S(I - beta k k^T) update, complex-multiplication RoPE, and special cases with closed-form answers.
+"""
+import numpy as np
+import pytest
+
+
+# ---- fp16 ---------------------------------------------------------------------------------------------------------
+
+def test_f16_round_trip_matches_numpy(orc):
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([
+        rng.normal(size=2000).astype(np.float32),
+        (rng.normal(size=2000) * 1e-6).astype(np.float32),      # subnormal halves
+        (rng.normal(size=500) * 7e4).astype(np.float32),        # overflow region (numpy warns on inf)
+        np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, 2.0 ** -25, 2.0 ** -24, 1.5 * 2.0 ** -25], np.float32),
+    ])
+    L = orc.lib()
+    ours = np.array([L.orc_f32_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ours, ref)
+    back = np.array([L.orc_f16_to_f32(int(h)) for h in ours], dtype=np.float32)
+    assert np.array_equal(back.view(np.uint32), ref.view(np.float16).astype(np.float32).view(np.uint32))
+
+
+def test_f16_saturation_policy(orc):
+    L = orc.lib()
+    assert L.orc_f16_sat(1e9) == 0x7BFF and L.orc_f16_sat(-1e9) == 0xFBFF
+    assert L.orc_f16_sat(1.0) == 0x3C00
+
+
+# ---- Q6_K layout ----------------------------------------------------------------------------------------------------
+
+def ggml_dequant_q6k_block(b):
+    """ggml dequantize_row_q6_K for one 210-byte block, transcribed from its published loop structure."""
+    b = np.asarray(b, dtype=np.uint8)
+    ql, qh = b[0:128].astype(np.int32), b[128:192].astype(np.int32)
+    sc = b[192:208].view(np.int8).astype(np.int32)
+    d = np.float64(b[208:210].view(np.float16)[0])
+    y = np.zeros(256)
+    for half in range(2):
+        qlp, qhp, scp, yo = ql[64 * half:], qh[32 * half:], sc[8 * half:], 128 * half
+        for l in range(32):
+            is_ = l // 16
+            q1 = ((qlp[l] & 0xF) | (((qhp[l] >> 0) & 3) << 4)) - 32
+            q2 = ((qlp[l + 32] & 0xF) | (((qhp[l] >> 2) & 3) << 4)) - 32
+            q3 = ((qlp[l] >> 4) | (((qhp[l] >> 4) & 3) << 4)) - 32
+            q4 = ((qlp[l + 32] >> 4) | (((qhp[l] >> 6) & 3) << 4)) - 32
+            y[yo + l] = d * scp[is_ + 0] * q1
+            y[yo + l + 32] = d * scp[is_ + 2] * q2
+            y[yo + l + 64] = d * scp[is_ + 4] * q3
+            y[yo + l + 96] = d * scp[is_ + 6] * q4
+    return y
+
+
+def test_q6k_generator_matches_ggml_layout(orc):
+    n_in, n_out = 512, 3
+    w = orc.gen_q6k(n_out, n_in, seed=11)
+    assert w.size == n_out * 2 * 210
+    deq = orc.q6k_dequant(w, n_out, n_in)
+    for r in range(n_out):
+        for bi in range(2):
+            blk = w[(r * 2 + bi) * 210:(r * 2 + bi + 1) * 210]
+            np.testing.assert_array_equal(deq[r, 256 * bi:256 * (bi + 1)].astype(np.float64),
+                                          ggml_dequant_q6k_block(blk).astype(np.float32).astype(np.float64))
+
+
+def test_q6k_generator_distribution(orc):
+    w = orc.gen_q6k(64, 4096, seed=5).reshape(-1, 210)
+    codes = np.array([[orc.lib().orc_q6k_code(np.ascontiguousarray(b), e) for e in range(256)] for b in w[:40]])
+    assert codes.min() == 0 and codes.max() == 63 and abs(codes.mean() - 31.5) < 1.0
+    sc = w[:, 192:208].view(np.int8)
+    assert sc.min() == -32 and sc.max() == 31
+    d = w[:, 208:210].copy().view(np.float16).astype(np.float64)
+    assert (d >= 0).all() and 0.5e-3 < np.sqrt((d ** 2).mean()) < 1.5e-3
+
+
+def test_q6k_known_answer_block(orc):
+    # every code 33 (q = +1), sub-scales 1..16, d = 1: element e dequantizes to sc[8n + l/16 + 2k]
+    b = np.zeros(210, dtype=np.uint8)
+    b[0:128] = 0x11            # low and high nibble 1
+    b[128:192] = 0xAA          # every 2-bit field = 2  -> code = 1 | 2 << 4 = 33
+    b[192:208] = np.arange(1, 17, dtype=np.int8).view(np.uint8)
+    b[208:210] = np.array([1.0], dtype=np.float16).view(np.uint8)
+    y = orc.q6k_dequant(b, 1, 256)[0]
+    for e in range(256):
+        n, k, l = e // 128, (e % 128) // 32, e % 32
+        assert y[e] == 1 + 8 * n + l // 16 + 2 * k
+
+
+# ---- Q8_1 quantizer -------------------------------------------------------------------------------------------------
+
+def np_tree_sum32(v):
+    a = v.astype(np.float32).copy()
+    idx = np.arange(32)
+    for off in (16, 8, 4, 2, 1):
+        a = (a + a[idx ^ off]).astype(np.float32)
+    return a[0]
+
+
+def np_roundf(v):
+    r = np.trunc(v)
+    return r + np.sign(v) * (np.abs(v - r) >= 0.5)
+
+
+def np_quant_q8_1(x):
+    blocks = []
+    for blk in x.reshape(-1, 32).astype(np.float32):
+        amax = np.max(np.abs(blk))
+        d = np.float32(amax) / np.float32(127.0)
+        q = np.zeros(32, np.int8) if amax == 0 else np_roundf(blk / d).astype(np.int8)
+        s = np_tree_sum32(blk)
+        dh = np.float16(np.clip(d, -65504, 65504)).view(np.uint16)
+        sh = np.float16(np.clip(s, -65504, 65504)).view(np.uint16)
+        blocks.append(np.concatenate([np.array([dh, sh], np.uint16).view(np.uint8), q.view(np.uint8)]))
+    return np.concatenate(blocks)
+
+
+def test_quantize_q8_1_closed_form(orc):
+    x = orc.normal(4096 * 2, seed=3)
+    x[64:96] *= 1e4            # the finite-guard block: |sum| can exceed 65504
+    x[128:160] = 0.0           # amax == 0
+    x[160:192] = np.arange(32, dtype=np.float32) - 15.5   # exact halves
+    y = orc.quantize_q8_1(x, 4096, 2)
+    assert np.array_equal(y, np_quant_q8_1(x))
+    d, s, q = orc.q8_1_fields(y)
+    assert np.isfinite(d.view(np.float16)).all() and np.isfinite(s.view(np.float16)).all()
+    assert (q[4] == 0).all() and d[4] == 0
+
+
+def test_quantize_q8_1_dequant_error_bound(orc):
+    x = orc.normal(8192, seed=4)
+    deq = orc.dequantize_q8_1(orc.quantize_q8_1(x, 8192), 8192)
+    amax = np.abs(x.reshape(-1, 32)).max(axis=1, keepdims=True)
+    assert (np.abs(deq.reshape(-1, 32) - x.reshape(-1, 32)) <= amax / 127 * 0.5 + amax * 2e-3).all()
+
+
+# ---- integer block dots ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n_in,n_out", [(256, 1), (512, 7), (2048, 5)])
+def test_q6k_block_dots_match_reference_lane_form(orc, n_in, n_out):
+    w = orc.gen_q6k(n_out, n_in, seed=n_in + n_out)
+    xq = orc.quantize_q8_1(orc.normal(n_in, seed=9), n_in)
+    a = orc.q6k_block_dots(w, xq, n_in, n_out)
+    b = orc.q6k_block_dots(w, xq, n_in, n_out, lanes=True)
+    assert np.array_equal(a, b)
+
+
+def test_q6k_block_dots_match_dequant_dot(orc):
+    n_in, n_out = 1024, 4
+    w = orc.gen_q6k(n_out, n_in, seed=21)
+    xq = orc.quantize_q8_1(orc.normal(n_in, seed=22), n_in)
+    dots = orc.q6k_block_dots(w, xq, n_in, n_out)
+    _, _, q8 = orc.q8_1_fields(xq)
+    for r in range(n_out):
+        for bi in range(n_in // 256):
+            blk = w[(r * (n_in // 256) + bi) * 210:][:210].copy()
+            blk[208:210] = np.array([1.0], np.float16).view(np.uint8)      # d = 1: dequant = sc * (code - 32)
+            wdeq = ggml_dequant_q6k_block(blk)
+            for jj in range(8):
+                j = 8 * bi + jj
+                assert dots[r, j] == int(np.dot(wdeq[32 * jj:32 * jj + 32], q8[j].astype(np.float64)))
+
+
+def test_q8_0_block_dots(orc):
+    n_in, n_out = 512, 3
+    w = orc.gen_q8_0(n_out, n_in, seed=2)
+    xq = orc.quantize_q8_1(orc.normal(n_in, seed=8), n_in)
+    dots = orc.q8_0_block_dots(w, xq, n_in, n_out)
+    wq = w.reshape(n_out, n_in // 32, 34)[:, :, 2:].copy().view(np.int8).astype(np.int64)
+    _, _, q8 = orc.q8_1_fields(xq)
+    assert np.array_equal(dots, (wq * q8.astype(np.int64)[None]).sum(-1))
+
+
+# ---- fp64 GEMVs and their invariants ----------------------------------------------------------------------------------
+
+def test_q6k_gemv_matches_fp64_dequant_matmul(orc):
+    n_in, n_out = 2048, 37
+    w = orc.gen_q6k(n_out, n_in, seed=31)
+    x = orc.normal(2 * n_in, seed=32)
+    xq = orc.quantize_q8_1(x, n_in, 2)
+    y = orc.q6k_gemv(w, xq, n_in, n_out, ncols=2).reshape(2, n_out)
+    W = np.stack([np.concatenate([ggml_dequant_q6k_block(w[(r * 8 + b) * 210:][:210]) for b in range(8)])
+                  for r in range(n_out)])
+    d, _, q8 = orc.q8_1_fields(xq)
+    X = (d.view(np.float16).astype(np.float64)[:, None] * q8.astype(np.float64)).reshape(2, n_in)
+    ref = X @ W.T
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12 * np.abs(ref).max())
+
+
+def test_q6k_gemv_invariants(orc):
+    n_in, n_out = 1024, 30
+    w = orc.gen_q6k(n_out, n_in, seed=41)
+    xq = orc.quantize_q8_1(orc.normal(2 * n_in, seed=42), n_in, 2)
+    res = orc.normal(2 * n_out, seed=43)
+    y2, p2 = orc.q6k_gemv(w, xq, n_in, n_out, ncols=2, res=res, partials=True)
+    col_bytes = n_in // 32 * 36
+    for c in range(2):
+        y1 = orc.q6k_gemv(w, xq[c * col_bytes:(c + 1) * col_bytes], n_in, n_out)
+        assert np.array_equal(y2[c * n_out:(c + 1) * n_out], y1 + res[c * n_out:(c + 1) * n_out].astype(np.float64))
+        yc = y2[c * n_out:(c + 1) * n_out]
+        groups = [yc[4 * g:4 * g + 4] for g in range((n_out + 3) // 4)]
+        np.testing.assert_allclose(p2[c * 8:(c + 1) * 8], [np.sum(g ** 2) for g in groups], rtol=1e-14)
+
+
+def test_q8_0_gemv(orc):
+    n_in, n_out = 1024, 9
+    w = orc.gen_q8_0(n_out, n_in, seed=51)
+    xq = orc.quantize_q8_1(orc.normal(n_in, seed=52), n_in)
+    y = orc.q8_0_gemv(w, xq, n_in, n_out)
+    blk = w.reshape(n_out, n_in // 32, 34)
+    dw = blk[:, :, :2].copy().view(np.float16)[..., 0].astype(np.float64)
+    Wd = (dw[:, :, None] * blk[:, :, 2:].copy().view(np.int8)).reshape(n_out, n_in)
+    X = orc.dequantize_q8_1(xq, n_in).astype(np.float64)
+    np.testing.assert_allclose(y, Wd @ X, rtol=1e-12, atol=1e-12)
+
+
+def test_f32_timing_build_close_to_fp64(orc):
+    n_in, n_out = 4096, 64
+    w = orc.gen_q6k(n_out, n_in, seed=61)
+    xq = orc.quantize_q8_1(orc.normal(2 * n_in, seed=62), n_in, 2)
+    res = orc.normal(2 * n_out, seed=63)
+    y64 = orc.q6k_gemv(w, xq, n_in, n_out, ncols=2, res=res)
+    y32, _ = orc.q6k_gemv_f32(w, xq, n_in, n_out, ncols=2, res=res, threads=2)
+    np.testing.assert_allclose(y32, y64, rtol=1e-4, atol=1e-4 * np.abs(y64).max())
+
+
+# ---- GDN ---------------------------------------------------------------------------------------------------------------
+
+def test_gdn_conv_l2(orc):
+    ch, qk = 8192, 32
+    hist = orc.normal(3 * ch, seed=71, std=0.5)
+    w = orc.normal(4 * ch, seed=72, std=0.5)
+    x = orc.normal(ch, seed=73)
+    h, hist2 = orc.gdn_conv_l2(hist, x, w, qk, 1e-6)
+    win = np.concatenate([hist.reshape(ch, 3), x[:, None]], axis=1).astype(np.float64)
+    s = (win * w.reshape(ch, 4)).sum(1)
+    ref = s / (1 + np.exp(-s))
+    ref[:qk * 128] = (ref[:qk * 128].reshape(qk, 128) /
+                      np.sqrt((ref[:qk * 128].reshape(qk, 128) ** 2).sum(1, keepdims=True) + 1e-6)).reshape(-1)
+    np.testing.assert_allclose(h, ref, rtol=1e-12, atol=1e-14)
+    assert np.array_equal(hist2.reshape(ch, 3), win[:, 1:].astype(np.float32))
+    # identity tap: w = [0,0,0,1] gives silu(x) on the v channels
+    w_id = np.tile(np.array([0, 0, 0, 1], np.float32), ch)
+    h_id, _ = orc.gdn_conv_l2(hist, x, w_id, 0, 1e-6)
+    np.testing.assert_allclose(h_id, x / (1 + np.exp(-x.astype(np.float64))), rtol=1e-12)
+
+
+def _gdn_inputs(orc, h_k=16, h_v=32, seed=80):
+    S = 128
+    state = orc.normal(S * h_v * S, seed=seed, std=0.05).astype(np.float64)
+    q = orc.normal(h_k * S, seed=seed + 1); q /= np.linalg.norm(q.reshape(h_k, S), axis=1).repeat(S)
+    k = orc.normal(h_k * S, seed=seed + 2); k /= np.linalg.norm(k.reshape(h_k, S), axis=1).repeat(S)
+    v = orc.normal(h_v * S, seed=seed + 3)
+    gate = -np.abs(orc.normal(h_v, seed=seed + 4)).astype(np.float64)
+    beta = 1 / (1 + np.exp(-orc.normal(h_v, seed=seed + 5).astype(np.float64)))
+    z = orc.normal(h_v * S, seed=seed + 6)
+    gamma = (1 + orc.normal(S, seed=seed + 7, std=0.1)).astype(np.float32)
+    return state, q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), gate, beta, z, gamma
+
+
+def test_gdn_step_matches_delta_rule_matrix_form(orc):
+    h_k, h_v, S, eps = 16, 32, 128, 1e-6
+    state, q, k, v, gate, beta, z, gamma = _gdn_inputs(orc)
+    y, st = orc.gdn_step_norm(state, q, k, v, gate, beta, z, gamma, eps, h_k, h_v)
+    St = state.reshape(S, h_v, S)
+    st = st.reshape(S, h_v, S)
+    for h in range(h_v):
+        qh = h % h_k
+        P = St[:, h, :].T                               # paper layout: d_v x d_k
+        kk, qq = k[qh * S:(qh + 1) * S], q[qh * S:(qh + 1) * S]
+        a, b = np.exp(gate[h]), beta[h]
+        Pn = a * P @ (np.eye(S) - b * np.outer(kk, kk)) + b * np.outer(v[h * S:(h + 1) * S], kk)
+        np.testing.assert_allclose(st[:, h, :].T, Pn, rtol=1e-10, atol=1e-13)
+        o = Pn @ qq / np.sqrt(S)
+        zz = z[h * S:(h + 1) * S].astype(np.float64)
+        ref = o / np.sqrt(np.mean(o ** 2) + eps) * gamma * zz / (1 + np.exp(-zz))
+        np.testing.assert_allclose(y[h * S:(h + 1) * S], ref, rtol=1e-9, atol=1e-12)
+
+
+def test_gdn_step_zero_key_only_decays(orc):
+    h_k, h_v = 16, 32
+    state, q, k, v, gate, beta, z, gamma = _gdn_inputs(orc, seed=90)
+    _, st = orc.gdn_step_norm(state, q, np.zeros_like(k), v, gate, beta, z, gamma, 1e-6, h_k, h_v)
+    g = np.exp(gate)[None, :, None]
+    np.testing.assert_allclose(st.reshape(128, h_v, 128), g * state.reshape(128, h_v, 128), rtol=1e-14)
+
+
+# ---- attention ---------------------------------------------------------------------------------------------------------
+
+def _kv(orc, n_tok, n_kv=4, hd=256, seed=100):
+    k = orc.normal(n_tok * n_kv * hd, seed=seed).astype(np.float16).view(np.uint16)
+    v = orc.normal(n_tok * n_kv * hd, seed=seed + 1).astype(np.float16).view(np.uint16)
+    return k, v
+
+
+def test_gqa_decode_softmax(orc):
+    n_head, n_kv, hd, n_tok = 16, 4, 256, 77
+    q = orc.normal(n_head * hd, seed=110)
+    k, v = _kv(orc, n_tok)
+    o = orc.gqa_decode(q, k, v, n_head, n_kv, hd, n_tok, 1 / 16).reshape(n_head, hd)
+    K = k.view(np.float16).astype(np.float64).reshape(n_tok, n_kv, hd)
+    V = v.view(np.float16).astype(np.float64).reshape(n_tok, n_kv, hd)
+    for h in range(n_head):
+        s = K[:, h // 4, :] @ q[h * hd:(h + 1) * hd].astype(np.float64) / 16
+        p = np.exp(s - s.max()); p /= p.sum()
+        np.testing.assert_allclose(o[h], p @ V[:, h // 4, :], rtol=1e-12, atol=1e-13)
+
+
+def test_gqa_decode_special_cases(orc):
+    n_head, n_kv, hd = 16, 4, 256
+    q = orc.normal(n_head * hd, seed=120)
+    k, v = _kv(orc, 9, seed=121)
+    o1 = orc.gqa_decode(q, k, v, n_head, n_kv, hd, 1, 1 / 16).reshape(n_head, hd)
+    V = v.view(np.float16).astype(np.float64).reshape(9, n_kv, hd)
+    for h in range(n_head):
+        np.testing.assert_allclose(o1[h], V[0, h // 4], rtol=1e-15)
+    kc = np.tile(k.reshape(9, -1)[0], 9)
+    oc = orc.gqa_decode(q, kc, v, n_head, n_kv, hd, 9, 1 / 16).reshape(n_head, hd)
+    for h in range(n_head):
+        np.testing.assert_allclose(oc[h], V[:, h // 4].mean(0), rtol=1e-12, atol=1e-14)
+
+
+def test_rope_neox_complex_form(orc):
+    heads, hd, n_rot, pos, theta = 3, 256, 64, 1234, 1e7
+    x = orc.normal(heads * hd, seed=130).astype(np.float64)
+    y = orc.rope_neox(x, heads, hd, n_rot, pos, theta).reshape(heads, hd)
+    X = x.reshape(heads, hd)
+    half = n_rot // 2
+    ang = pos * theta ** (-np.arange(half) * 2.0 / n_rot)
+    zc = (X[:, :half] + 1j * X[:, half:n_rot]) * np.exp(1j * ang)
+    np.testing.assert_allclose(y[:, :half], zc.real, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(y[:, half:n_rot], zc.imag, rtol=1e-12, atol=1e-12)
+    assert np.array_equal(y[:, n_rot:], X[:, n_rot:])
+    assert np.allclose(orc.rope_neox(x, heads, hd, n_rot, 0, theta), x, rtol=0, atol=0)
+
+
+def test_argmax_lowest_index_tie(orc):
+    l = np.zeros(1000, np.float32)
+    l[[17, 400, 999]] = 3.0
+    assert orc.argmax(l) == 17
+    l[5] = np.float32(3.0000002)
+    assert orc.argmax(l) == 5
+
+
+def test_beta_gate_and_norms(orc):
+    b_in = orc.normal(32, seed=140); a = orc.normal(32, seed=141)
+    dt = np.zeros(32, np.float32); ssm_a = -np.exp(orc.normal(32, seed=142, std=0.5))
+    b, g = orc.beta_gate(b_in, a, dt, ssm_a)
+    np.testing.assert_allclose(b, 1 / (1 + np.exp(-b_in.astype(np.float64))), rtol=1e-14)
+    np.testing.assert_allclose(g, np.log(1 + np.exp(a.astype(np.float64))) * ssm_a, rtol=1e-12)
+    big = np.full(32, 30.0, np.float32)
+    _, g2 = orc.beta_gate(b_in, big, dt, ssm_a)
+    np.testing.assert_allclose(g2, 30.0 * ssm_a.astype(np.float64), rtol=1e-14)   # softplus cut-over above 20
+    x = orc.normal(4096, seed=143)
+    p = orc.row_sum_partials(x)
+    inv = orc.rms_inv(p, 4096, 1e-6)
+    np.testing.assert_allclose(inv, 1 / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6), rtol=1e-13)
