@@ -87,6 +87,93 @@ size_t rmi_native_mmvq_weight_bytes(int ggml_type, int n_in, int n_out);
  * it runs the same device decode as the GEMV. */
 int rmi_q6_k_block_dots(const void* w, const void* x_q8_1, int32_t* out, int n_in, int n_out, void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------------
+ * Norm / activation epilogues (qw:602-715).  `ncols` columns per launch; column c of x at x + c * cols, of partials
+ * at partials + c * cols / 4, of Q8_1 output at c * cols / 32 blocks.  Partials: one slot per 4 rows.
+ * ------------------------------------------------------------------------------------------------------------- */
+
+/* Q8_1 of (x * w) * rsqrt(sum(partials) / cols + eps).  Replaces rms_quant_apply_kernel (qw:627-655). */
+int rmi_rms_quant_apply(const float* x, const float* w, const float* partials, void* y_q8_1, int cols, float eps,
+                        int ncols, void* stream);
+/* fp32 out = (x * w) * rsqrt(...); out_partials (nullable) gets the output's own 4-row partials.
+ * Replaces rms_norm_out_kernel (qw:658-672) fused with row_sum_partials_kernel (qw:616-623). */
+int rmi_rms_norm_out(const float* x, const float* w, const float* partials, float* out, float* out_partials, int cols,
+                     float eps, int ncols, void* stream);
+/* partials of x.  Replaces row_sum_partials_kernel (qw:616-623). */
+int rmi_row_sum_partials(const float* x, float* partials, int n, int ncols, void* stream);
+/* x += o, then partials of x.  Replaces add_partials_1024_kernel (qw:602-614). */
+int rmi_add_partials(float* x, const float* o, float* partials, int n, int ncols, void* stream);
+/* Q8_1 of silu(gate) * up; column c reads up/gate at + c * col_stride.  Replaces swiglu_quant_kernel (qw:676-689). */
+int rmi_swiglu_quant(const float* up, const float* gate, void* y_q8_1, int n, int ncols, int col_stride, void* stream);
+/* Q8_1 of o * sigmoid(g).  Replaces sig_mul_quant_kernel (qw:692-704). */
+int rmi_sig_mul_quant(const float* o, const float* g, void* y_q8_1, int n, int ncols, int o_stride, int g_stride,
+                      void* stream);
+/* beta = sigmoid(beta) in place, ggate = softplus(alpha + dt) * ssm_a; per column [beta n | alpha n] (the
+ * reference's beta|alpha concat order, qw:2085).  Replaces beta_gate_kernel (qw:707-715). */
+int rmi_beta_gate(float* beta_alpha, const float* dt, const float* ssm_a, float* ggate, int n, int ncols,
+                  int ab_stride, void* stream);
+/* greedy argmax per column, lowest index wins ties; workspace of rmi_argmax_workspace_bytes(ncols) bytes.
+ * Replaces argmax_kernel / serve_argmax_dev (qw:70-94) and the host scan (qw:3199-3205), without the memset. */
+size_t rmi_argmax_workspace_bytes(int ncols);
+int rmi_argmax(const float* logits, int n, int ncols, int col_stride, int* out_idx, void* workspace, void* stream);
+/* Device-resident token embedding: x[c] = dequant(Q6_K row tokens[c]), partials of each row.  Replaces the host
+ * dequant + H2D copy of emb_dequant_block (qw:109-115, 1418-1430). */
+int rmi_embed_q6_k(const void* emb, const int* tokens, float* x, float* partials, int n_embd, int n_vocab, int ncols,
+                   void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Gated DeltaNet (fgdn:40-133)
+ * ------------------------------------------------------------------------------------------------------------- */
+
+/* causal width-4 conv + SiLU + L2 of the first qk_heads 128-channel heads; history [c][3] updated in place, h may
+ * alias qkv.  Replaces fused_gdn_conv_l2 (fgdn:167-176). */
+int rmi_fused_gdn_conv_l2(float* history, const float* qkv, const float* conv_w, float* h, int channels, int qk_heads,
+                          float eps, void* stream);
+/* one delta-rule step per value head, state [128][h_v][128] in place, y = rmsnorm(o) * gamma * silu(z), q8 (nullable)
+ * its Q8_1 blocks.  gate = decay logit (g = exp(gate)), beta after its sigmoid.  Replaces
+ * fused_gdn_step_norm_silu_q8 (fgdn:221-225, patches/0001:9-15). */
+int rmi_fused_gdn_step_norm_silu_q8(float* state, const float* q, const float* k, const float* v, const float* gate,
+                                    const float* beta, const float* z, const float* gamma, float eps, float* y,
+                                    uint8_t* q8, int h_k, int h_v, void* stream);
+/* The whole GDN chain of one layer for ntok = 1 (decode) or 2 (verify) tokens: conv + SiLU + L2, beta/decay from the
+ * raw beta|alpha GEMV output, the step with the state in registers across both tokens, norm * silu gate, Q8_1.
+ * state_a/state_b and hist_a/hist_b are the two buffers of the selector *sel (live = sel ? b : a).  With ntok = 2
+ * the state and history after token 0 go to the non-live buffers, so a rejected draft is rolled back by flipping
+ * *sel.  No reference counterpart as one call: replaces beta_gate + fused_gdn_conv_l2 + fused_gdn_step_norm_silu_q8
+ * per column and the snapshot copies of launch_token_verify (qw:1448-1478, 3225-3233). */
+int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_a, float* hist_b, const int* sel, float* qkvz,
+                         int qkvz_stride, const float* ab, int ab_stride, const float* conv_w, const float* dt,
+                         const float* ssm_a, const float* gamma, float eps, float* y, int y_stride, uint8_t* q8,
+                         int q8_stride, int h_k, int h_v, int ntok, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * GQA attention over an fp16 KV cache [pos][n_kv][head_dim]
+ * ------------------------------------------------------------------------------------------------------------- */
+
+/* per token t (position pos[0] + t): split q|gate, per-head RMSNorm (qn, kn), NEOX RoPE on n_rot dims, fp32 q to
+ * qout[t][head][d], fp16 K/V into the caches.  Replaces split_qg_kernel (qw:320-327), rms_norm_weighted,
+ * native_rope_apply and store_kv2_kernel (qw:340-345) as launched at qw:1532-1548. */
+int rmi_attn_prep(const float* q3, int q3_stride, const float* qn, const float* kn, uint16_t* kcache, uint16_t* vcache,
+                  const int* pos, float* qout, int n_head, int n_kv, int head_dim, int n_rot, float theta, float eps,
+                  int ntok, int max_ctx, void* stream);
+/* split-K flash decode for ntok query tokens at positions pos[0] + t, sigmoid gate from gate_src (the wq output,
+ * gate of head h at + h * 2 * head_dim + head_dim), fp32 y (nullable) and Q8_1 (nullable).  workspace holds
+ * rmi_gqa_workspace_bytes(max_ctx, n_kv, nsub) bytes; chunks are 64 * nsub positions.  Replaces gqa_head_kernel
+ * (qw:384-442) + sig_mul_quant_kernel (qw:692-704) per column. */
+size_t rmi_gqa_workspace_bytes(int max_ctx, int n_kv, int nsub);
+int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* pos,
+                         const float* gate_src, int gate_stride, float* y, int y_stride, uint8_t* q8, int q8_stride,
+                         void* workspace, int n_head, int n_kv, int head_dim, int ntok, int max_ctx, int nsub,
+                         float scale, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Seeded synthetic tensors in HBM (stand-in for a GGUF file: random-init weights; no reference counterpart)
+ * ------------------------------------------------------------------------------------------------------------- */
+int rmi_gen_q6_k(void* w, size_t nblocks, uint64_t seed, float d_std, void* stream);
+int rmi_gen_q8_0(void* w, size_t nblocks, uint64_t seed, float d_std, void* stream);
+int rmi_gen_normal(float* out, size_t n, uint64_t seed, float mean, float std, void* stream);
+int rmi_gen_normal_f16(uint16_t* out, size_t n, uint64_t seed, float mean, float std, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,28 @@ SIGNATURES = {
     "rmi_native_q6_k_mmvq_res": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_res_n": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_q6_k_block_dots": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "rmi_gen_q6_k": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
+    "rmi_gen_q8_0": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
+    "rmi_gen_normal": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
+    "rmi_gen_normal_f16": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
+    "rmi_rms_quant_apply": (_i, [_vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
+    "rmi_rms_norm_out": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
+    "rmi_row_sum_partials": (_i, [_vp, _vp, _i, _i, _vp]),
+    "rmi_add_partials": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "rmi_swiglu_quant": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_sig_mul_quant": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "rmi_beta_gate": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_argmax_workspace_bytes": (_sz, [_i]),
+    "rmi_argmax": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
+    "rmi_embed_q6_k": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_fused_gdn_conv_l2": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
+    "rmi_fused_gdn_step_norm_silu_q8": (_i, [_vp] * 8 + [_f, _vp, _vp, _i, _i, _vp]),
+    "rmi_gdn_layer_tokens": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _i, _vp,
+                                  _i, _i, _i, _i, _vp]),
+    "rmi_attn_prep": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _f, _i, _i, _vp]),
+    "rmi_gqa_workspace_bytes": (_sz, [_i, _i, _i]),
+    "rmi_gqa_flash_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _f,
+                                  _vp]),
 }
 
 
@@ -124,3 +146,105 @@ def native_q6_k_mmvq_res_n(w, x_q8_1, y, res, partials, n_in: int, n_out: int, n
 
 def q6_k_block_dots(w, x_q8_1, out, n_in: int, n_out: int, stream=None):
     _call("rmi_q6_k_block_dots", _p(w), _p(x_q8_1), _p(out), n_in, n_out, _stream(stream))
+
+
+# ---- seeded synthetic tensors in HBM (random-init stand-in for a GGUF file) -----------------------------------------
+
+def gen_q6_k(w, nblocks: int, seed: int, d_std: float = 1e-3, stream=None):
+    """Fill ``nblocks`` Q6_K blocks: codes U{0..63}, sub-scales U[-32,31], d = fp16(|N(0, d_std)|)."""
+    _call("rmi_gen_q6_k", _p(w), nblocks, seed, d_std, _stream(stream))
+
+
+def gen_q8_0(w, nblocks: int, seed: int, d_std: float = 1e-2, stream=None):
+    _call("rmi_gen_q8_0", _p(w), nblocks, seed, d_std, _stream(stream))
+
+
+def gen_normal(out, n: int, seed: int, mean: float = 0.0, std: float = 1.0, stream=None):
+    _call("rmi_gen_normal", _p(out), n, seed, mean, std, _stream(stream))
+
+
+def gen_normal_f16(out, n: int, seed: int, mean: float = 0.0, std: float = 1.0, stream=None):
+    _call("rmi_gen_normal_f16", _p(out), n, seed, mean, std, _stream(stream))
+
+
+# ---- norm / activation epilogues (qw:602-715) ----------------------------------------------------------------------
+
+def rms_quant_apply(x, w, partials, y_q8_1, cols, eps, ncols=1, stream=None):
+    _call("rmi_rms_quant_apply", _p(x), _p(w), _p(partials), _p(y_q8_1), cols, eps, ncols, _stream(stream))
+
+
+def rms_norm_out(x, w, partials, out, out_partials, cols, eps, ncols=1, stream=None):
+    _call("rmi_rms_norm_out", _p(x), _p(w), _p(partials), _p(out), _p(out_partials), cols, eps, ncols,
+          _stream(stream))
+
+
+def row_sum_partials(x, partials, n, ncols=1, stream=None):
+    _call("rmi_row_sum_partials", _p(x), _p(partials), n, ncols, _stream(stream))
+
+
+def add_partials(x, o, partials, n, ncols=1, stream=None):
+    _call("rmi_add_partials", _p(x), _p(o), _p(partials), n, ncols, _stream(stream))
+
+
+def swiglu_quant(up, gate, y_q8_1, n, ncols=1, col_stride=None, stream=None):
+    _call("rmi_swiglu_quant", _p(up), _p(gate), _p(y_q8_1), n, ncols, n if col_stride is None else col_stride,
+          _stream(stream))
+
+
+def sig_mul_quant(o, g, y_q8_1, n, ncols=1, o_stride=None, g_stride=None, stream=None):
+    _call("rmi_sig_mul_quant", _p(o), _p(g), _p(y_q8_1), n, ncols, n if o_stride is None else o_stride,
+          n if g_stride is None else g_stride, _stream(stream))
+
+
+def beta_gate(beta_alpha, dt, ssm_a, ggate, n, ncols=1, ab_stride=None, stream=None):
+    _call("rmi_beta_gate", _p(beta_alpha), _p(dt), _p(ssm_a), _p(ggate), n, ncols,
+          2 * n if ab_stride is None else ab_stride, _stream(stream))
+
+
+def argmax_workspace_bytes(ncols):
+    return lib().rmi_argmax_workspace_bytes(ncols)
+
+
+def argmax(logits, n, out_idx, workspace, ncols=1, col_stride=None, stream=None):
+    _call("rmi_argmax", _p(logits), n, ncols, n if col_stride is None else col_stride, _p(out_idx), _p(workspace),
+          _stream(stream))
+
+
+def embed_q6_k(emb, tokens, x, partials, n_embd, n_vocab, ncols=1, stream=None):
+    _call("rmi_embed_q6_k", _p(emb), _p(tokens), _p(x), _p(partials), n_embd, n_vocab, ncols, _stream(stream))
+
+
+# ---- Gated DeltaNet (fgdn:40-133) ----------------------------------------------------------------------------------
+
+def fused_gdn_conv_l2(history, qkv, conv_w, h, channels, qk_heads, eps, stream=None):
+    _call("rmi_fused_gdn_conv_l2", _p(history), _p(qkv), _p(conv_w), _p(h), channels, qk_heads, eps, _stream(stream))
+
+
+def fused_gdn_step_norm_silu_q8(state, q, k, v, gate, beta, z, gamma, eps, y, q8, h_k, h_v, stream=None):
+    _call("rmi_fused_gdn_step_norm_silu_q8", _p(state), _p(q), _p(k), _p(v), _p(gate), _p(beta), _p(z), _p(gamma),
+          eps, _p(y), _p(q8), h_k, h_v, _stream(stream))
+
+
+def gdn_layer_tokens(state_a, state_b, hist_a, hist_b, sel, qkvz, qkvz_stride, ab, ab_stride, conv_w, dt, ssm_a,
+                     gamma, eps, y, y_stride, q8, q8_stride, h_k, h_v, ntok, stream=None):
+    _call("rmi_gdn_layer_tokens", _p(state_a), _p(state_b), _p(hist_a), _p(hist_b), _p(sel), _p(qkvz), qkvz_stride,
+          _p(ab), ab_stride, _p(conv_w), _p(dt), _p(ssm_a), _p(gamma), eps, _p(y), y_stride, _p(q8), q8_stride, h_k,
+          h_v, ntok, _stream(stream))
+
+
+# ---- attention --------------------------------------------------------------------------------------------------------
+
+def attn_prep(q3, q3_stride, qn, kn, kcache, vcache, pos, qout, n_head, n_kv, head_dim, n_rot, theta, eps, ntok,
+              max_ctx, stream=None):
+    _call("rmi_attn_prep", _p(q3), q3_stride, _p(qn), _p(kn), _p(kcache), _p(vcache), _p(pos), _p(qout), n_head,
+          n_kv, head_dim, n_rot, theta, eps, ntok, max_ctx, _stream(stream))
+
+
+def gqa_workspace_bytes(max_ctx, n_kv, nsub):
+    return lib().rmi_gqa_workspace_bytes(max_ctx, n_kv, nsub)
+
+
+def gqa_flash_decode(q, kcache, vcache, pos, gate_src, gate_stride, y, y_stride, q8, q8_stride, workspace, n_head,
+                     n_kv, head_dim, ntok, max_ctx, nsub, scale, stream=None):
+    _call("rmi_gqa_flash_decode", _p(q), _p(kcache), _p(vcache), _p(pos), _p(gate_src), gate_stride, _p(y), y_stride,
+          _p(q8), q8_stride, _p(workspace), n_head, n_kv, head_dim, ntok, max_ctx, nsub, scale, _stream(stream))

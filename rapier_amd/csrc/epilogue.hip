@@ -1,0 +1,317 @@
+// epilogue.hip - the small per-token kernels between GEMVs (reference src/qwythos.cpp:602-715, 70-94, 109-115).
+//
+// Every kernel takes `ncols` columns (blockIdx.y) so both verify columns ride one launch; a column's arithmetic is
+// the same as a single-column call, bit for bit.  Row-norm partials follow the GEMV epilogue contract: one slot per
+// 4 rows, partial[g] = fma chain of the 4 rows' squares in row order.
+//
+// Norm reduction (rms_quant_apply / rms_norm_out): 256 lanes; lane t adds partials t, t+256, t+512, ... in order,
+// then a 64-lane xor butterfly, then the 4 wave sums in order.  Every workgroup derives the same bits.
+#include "rmi_common.h"
+
+namespace rmi {
+namespace {
+
+__device__ float block_sum_partials(const float* __restrict__ p, int np) {
+    __shared__ float red[4];
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < np; i += 256) s += p[i];
+    s = group_sum<64>(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+    __syncthreads();
+    return tot;
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+__device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+// Q8_1 of (x * w) * inv, one lane per element (reference rms_quant_apply_kernel, qw:627-655)
+__global__ __launch_bounds__(256) void rms_quant_apply_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                              const float* __restrict__ partials,
+                                                              uint8_t* __restrict__ y, int cols, float eps) {
+    const int c = blockIdx.y;
+    x += static_cast<size_t>(c) * cols;
+    partials += static_cast<size_t>(c) * (cols / 4);
+    y += static_cast<size_t>(c) * (cols / 32) * kQ8_1Bytes;
+    const float ss = block_sum_partials(partials, cols / 4);
+    const float inv = rsqrtf(ss / static_cast<float>(cols) + eps);
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= cols) return;   // cols % 32 == 0: whole 32-lane groups leave together
+    q8_1_store_lane((x[i] * w[i]) * inv, y + static_cast<size_t>(i / 32) * kQ8_1Bytes);
+}
+
+// fp32 out = (x * w) * inv (reference rms_norm_out_kernel, qw:658-672), optionally with the output's own partials
+__global__ __launch_bounds__(256) void rms_norm_out_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                           const float* __restrict__ partials, float* __restrict__ out,
+                                                           float* __restrict__ out_partials, int cols, float eps) {
+    const int c = blockIdx.y;
+    x += static_cast<size_t>(c) * cols;
+    partials += static_cast<size_t>(c) * (cols / 4);
+    out += static_cast<size_t>(c) * cols;
+    const float ss = block_sum_partials(partials, cols / 4);
+    const float inv = rsqrtf(ss / static_cast<float>(cols) + eps);
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    float v = 0.0f;
+    if (i < cols) {
+        v = (x[i] * w[i]) * inv;
+        out[i] = v;
+    }
+    if (out_partials) {
+        // the 4 rows of a partial slot are 4 consecutive lanes: gather them in row order on the first lane
+        const float v0 = __shfl(v, (threadIdx.x & ~3) + 0, 64), v1 = __shfl(v, (threadIdx.x & ~3) + 1, 64);
+        const float v2 = __shfl(v, (threadIdx.x & ~3) + 2, 64), v3 = __shfl(v, (threadIdx.x & ~3) + 3, 64);
+        if ((threadIdx.x & 3) == 0 && i < cols) {
+            float p = 0.0f;
+            p = __builtin_fmaf(v0, v0, p);
+            if (i + 1 < cols) p = __builtin_fmaf(v1, v1, p);
+            if (i + 2 < cols) p = __builtin_fmaf(v2, v2, p);
+            if (i + 3 < cols) p = __builtin_fmaf(v3, v3, p);
+            out_partials[static_cast<size_t>(c) * ((cols + 3) / 4) + i / 4] = p;
+        }
+    }
+}
+
+// partials[g] = sum of squares of rows 4g..4g+3 (reference row_sum_partials_kernel, qw:616-623); optionally x += o
+// first (add_partials_1024_kernel, qw:602-614)
+__global__ __launch_bounds__(256) void add_partials_kernel(float* __restrict__ x, const float* __restrict__ o,
+                                                           float* __restrict__ partials, int n) {
+    const int c = blockIdx.y;
+    const int g = blockIdx.x * 256 + threadIdx.x;
+    const int np = (n + 3) / 4;
+    if (g >= np) return;
+    x += static_cast<size_t>(c) * n;
+    float p = 0.0f;
+    for (int r = 4 * g; r < 4 * g + 4 && r < n; ++r) {
+        float v = x[r];
+        if (o) {
+            v += o[static_cast<size_t>(c) * n + r];
+            x[r] = v;
+        }
+        p = __builtin_fmaf(v, v, p);
+    }
+    partials[static_cast<size_t>(c) * np + g] = p;
+}
+
+// Q8_1 of silu(gate) * up (reference swiglu_quant_kernel, qw:676-689)
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ up, const float* __restrict__ gate,
+                                                           uint8_t* __restrict__ y, int n, int col_stride) {
+    const int c = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const size_t off = static_cast<size_t>(c) * col_stride + i;
+    q8_1_store_lane(silu(gate[off]) * up[off], y + (static_cast<size_t>(c) * (n / 32) + i / 32) * kQ8_1Bytes);
+}
+
+// Q8_1 of o * sigmoid(g) (reference sig_mul_quant_kernel, qw:692-704)
+__global__ __launch_bounds__(256) void sig_mul_quant_kernel(const float* __restrict__ o, const float* __restrict__ g,
+                                                            uint8_t* __restrict__ y, int n, int o_stride,
+                                                            int g_stride) {
+    const int c = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = o[static_cast<size_t>(c) * o_stride + i] * sigmoid(g[static_cast<size_t>(c) * g_stride + i]);
+    q8_1_store_lane(v, y + (static_cast<size_t>(c) * (n / 32) + i / 32) * kQ8_1Bytes);
+}
+
+// beta = sigmoid(beta) in place; gate = softplus(alpha + dt) * ssm_a, softplus linear above 20 (qw:707-715).
+// Layout per column: [beta n | alpha n] at ab + c * ab_stride.
+__global__ __launch_bounds__(64) void beta_gate_kernel(float* __restrict__ ab, const float* __restrict__ dt,
+                                                       const float* __restrict__ ssm_a, float* __restrict__ ggate,
+                                                       int n, int ab_stride) {
+    const int c = blockIdx.y;
+    const int i = blockIdx.x * 64 + threadIdx.x;
+    if (i >= n) return;
+    float* beta = ab + static_cast<size_t>(c) * ab_stride;
+    const float* alpha = beta + n;
+    beta[i] = sigmoid(beta[i]);
+    const float v = alpha[i] + dt[i];
+    ggate[static_cast<size_t>(c) * n + i] = (v > 20.0f ? v : log1pf(expf(v))) * ssm_a[i];
+}
+
+// ---- argmax: lowest index wins ties (qw:70-94: monotonic float bits, n-1-idx packing) -------------------------------
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+    uint32_t b = __float_as_uint(v);
+    b ^= (b >> 31) ? 0xffffffffu : 0x80000000u;
+    return (static_cast<uint64_t>(b) << 32) | static_cast<uint32_t>(0x7fffffff - idx);
+}
+
+__device__ __forceinline__ uint64_t key_max64(uint64_t k) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(k), off, 64);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(k >> 32), off, 64);
+        const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+constexpr int kArgmaxBlocks = 256;
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ l, int n, int col_stride,
+                                                             uint64_t* __restrict__ part) {
+    __shared__ uint64_t red[4];
+    const int c = blockIdx.y;
+    l += static_cast<size_t>(c) * col_stride;
+    uint64_t best = 0;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += kArgmaxBlocks * 256) {
+        const uint64_t k = argmax_key(l[i], i);
+        best = k > best ? k : best;
+    }
+    best = key_max64(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t m = red[0];
+        for (int i = 1; i < 4; ++i) m = red[i] > m ? red[i] : m;
+        part[static_cast<size_t>(c) * kArgmaxBlocks + blockIdx.x] = m;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const uint64_t* __restrict__ part, int* __restrict__ out) {
+    __shared__ uint64_t red[4];
+    const int c = blockIdx.x;
+    uint64_t best = part[static_cast<size_t>(c) * kArgmaxBlocks + threadIdx.x];
+    best = key_max64(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t m = red[0];
+        for (int i = 1; i < 4; ++i) m = red[i] > m ? red[i] : m;
+        out[c] = 0x7fffffff - static_cast<int>(static_cast<uint32_t>(m));
+    }
+}
+
+// ---- token embedding: device dequant of one Q6_K row per token (ggml dequantize_row_q6_K order) ---------------------
+// x[c][e] = (d * sc) * (code - 32); partials of the row for the first norm (row_sum_partials, qw:1426-1430).
+// One workgroup of 256 lanes per 256-element block; lane e dequantizes element e.
+__global__ __launch_bounds__(256) void embed_q6_k_kernel(const uint8_t* __restrict__ emb, const int* __restrict__ tok,
+                                                         float* __restrict__ x, float* __restrict__ partials,
+                                                         int n_embd, int n_vocab) {
+    const int c = blockIdx.y;
+    int t = tok[c];
+    t = t < 0 ? 0 : (t >= n_vocab ? n_vocab - 1 : t);   // an out-of-range id never reads outside the table
+    const int nb = n_embd / 256;
+    const uint8_t* b = emb + (static_cast<size_t>(t) * nb + blockIdx.x) * kQ6KBytes;
+    const int e = threadIdx.x;
+    const int n = e >> 7, k = (e & 127) >> 5, l = e & 31;
+    const uint8_t lo = b[64 * n + 32 * (k & 1) + l];
+    const int nib = (k >> 1) ? (lo >> 4) : (lo & 15);
+    const int hi = (b[128 + 32 * n + l] >> (2 * k)) & 3;
+    const int sc = static_cast<int8_t>(b[192 + 8 * n + l / 16 + 2 * k]);
+    const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b + 208));
+    const float v = (d * static_cast<float>(sc)) * static_cast<float>((nib | (hi << 4)) - 32);
+    const int idx = blockIdx.x * 256 + e;
+    x[static_cast<size_t>(c) * n_embd + idx] = v;
+    const float v0 = __shfl(v, (e & ~3) + 0, 64), v1 = __shfl(v, (e & ~3) + 1, 64);
+    const float v2 = __shfl(v, (e & ~3) + 2, 64), v3 = __shfl(v, (e & ~3) + 3, 64);
+    if ((e & 3) == 0) {
+        float p = 0.0f;
+        p = __builtin_fmaf(v0, v0, p);
+        p = __builtin_fmaf(v1, v1, p);
+        p = __builtin_fmaf(v2, v2, p);
+        p = __builtin_fmaf(v3, v3, p);
+        partials[static_cast<size_t>(c) * (n_embd / 4) + idx / 4] = p;
+    }
+}
+
+bool bad_cols(int ncols) { return ncols < 1 || ncols > kMaxCols; }
+
+}  // namespace
+}  // namespace rmi
+
+using namespace rmi;
+
+extern "C" int rmi_rms_quant_apply(const float* x, const float* w, const float* partials, void* y_q8_1, int cols,
+                                   float eps, int ncols, void* stream) {
+    if (cols <= 0 || cols % 32 != 0 || bad_cols(ncols)) return fail(RMI_ERR_SHAPE, "rms_quant_apply: bad shape");
+    if (!aligned4(x) || !aligned4(w) || !aligned4(partials) || !aligned4(y_q8_1))
+        return fail(RMI_ERR_POINTER, "rms_quant_apply: null or misaligned pointer");
+    hipLaunchKernelGGL(rms_quant_apply_kernel, dim3((cols + 255) / 256, ncols), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, w, partials, static_cast<uint8_t*>(y_q8_1), cols, eps);
+    return launch_status("rms_quant_apply");
+}
+
+extern "C" int rmi_rms_norm_out(const float* x, const float* w, const float* partials, float* out, float* out_partials,
+                                int cols, float eps, int ncols, void* stream) {
+    if (cols <= 0 || cols % 4 != 0 || bad_cols(ncols)) return fail(RMI_ERR_SHAPE, "rms_norm_out: bad shape");
+    if (!aligned4(x) || !aligned4(w) || !aligned4(partials) || !aligned4(out))
+        return fail(RMI_ERR_POINTER, "rms_norm_out: null or misaligned pointer");
+    hipLaunchKernelGGL(rms_norm_out_kernel, dim3((cols + 255) / 256, ncols), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, w, partials, out, out_partials, cols, eps);
+    return launch_status("rms_norm_out");
+}
+
+extern "C" int rmi_row_sum_partials(const float* x, float* partials, int n, int ncols, void* stream) {
+    if (n <= 0 || bad_cols(ncols)) return fail(RMI_ERR_SHAPE, "row_sum_partials: bad shape");
+    if (!aligned4(x) || !aligned4(partials)) return fail(RMI_ERR_POINTER, "row_sum_partials: null pointer");
+    const int np = (n + 3) / 4;
+    hipLaunchKernelGGL(add_partials_kernel, dim3((np + 255) / 256, ncols), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), const_cast<float*>(x), nullptr, partials, n);
+    return launch_status("row_sum_partials");
+}
+
+extern "C" int rmi_add_partials(float* x, const float* o, float* partials, int n, int ncols, void* stream) {
+    if (n <= 0 || bad_cols(ncols)) return fail(RMI_ERR_SHAPE, "add_partials: bad shape");
+    if (!aligned4(x) || !aligned4(o) || !aligned4(partials)) return fail(RMI_ERR_POINTER, "add_partials: null pointer");
+    const int np = (n + 3) / 4;
+    hipLaunchKernelGGL(add_partials_kernel, dim3((np + 255) / 256, ncols), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, o, partials, n);
+    return launch_status("add_partials");
+}
+
+extern "C" int rmi_swiglu_quant(const float* up, const float* gate, void* y_q8_1, int n, int ncols, int col_stride,
+                                void* stream) {
+    if (n <= 0 || n % 32 != 0 || bad_cols(ncols) || col_stride < n) return fail(RMI_ERR_SHAPE, "swiglu_quant: bad shape");
+    if (!aligned4(up) || !aligned4(gate) || !aligned4(y_q8_1)) return fail(RMI_ERR_POINTER, "swiglu_quant: null pointer");
+    hipLaunchKernelGGL(swiglu_quant_kernel, dim3((n + 255) / 256, ncols), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), up, gate, static_cast<uint8_t*>(y_q8_1), n, col_stride);
+    return launch_status("swiglu_quant");
+}
+
+extern "C" int rmi_sig_mul_quant(const float* o, const float* g, void* y_q8_1, int n, int ncols, int o_stride,
+                                 int g_stride, void* stream) {
+    if (n <= 0 || n % 32 != 0 || bad_cols(ncols)) return fail(RMI_ERR_SHAPE, "sig_mul_quant: bad shape");
+    if (!aligned4(o) || !aligned4(g) || !aligned4(y_q8_1)) return fail(RMI_ERR_POINTER, "sig_mul_quant: null pointer");
+    hipLaunchKernelGGL(sig_mul_quant_kernel, dim3((n + 255) / 256, ncols), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), o, g, static_cast<uint8_t*>(y_q8_1), n, o_stride, g_stride);
+    return launch_status("sig_mul_quant");
+}
+
+extern "C" int rmi_beta_gate(float* beta_alpha, const float* dt, const float* ssm_a, float* ggate, int n, int ncols,
+                             int ab_stride, void* stream) {
+    if (n <= 0 || bad_cols(ncols) || ab_stride < 2 * n) return fail(RMI_ERR_SHAPE, "beta_gate: bad shape");
+    if (!aligned4(beta_alpha) || !aligned4(dt) || !aligned4(ssm_a) || !aligned4(ggate))
+        return fail(RMI_ERR_POINTER, "beta_gate: null pointer");
+    hipLaunchKernelGGL(beta_gate_kernel, dim3((n + 63) / 64, ncols), dim3(64), 0, static_cast<hipStream_t>(stream),
+                       beta_alpha, dt, ssm_a, ggate, n, ab_stride);
+    return launch_status("beta_gate");
+}
+
+extern "C" size_t rmi_argmax_workspace_bytes(int ncols) {
+    return static_cast<size_t>(ncols > 0 ? ncols : 1) * kArgmaxBlocks * sizeof(uint64_t);
+}
+
+extern "C" int rmi_argmax(const float* logits, int n, int ncols, int col_stride, int* out_idx, void* workspace,
+                          void* stream) {
+    if (n <= 0 || bad_cols(ncols) || col_stride < n) return fail(RMI_ERR_SHAPE, "argmax: bad shape");
+    if (!aligned4(logits) || !aligned4(out_idx) || !workspace || (reinterpret_cast<uintptr_t>(workspace) & 7u))
+        return fail(RMI_ERR_POINTER, "argmax: null or misaligned pointer");
+    auto* part = static_cast<uint64_t*>(workspace);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxBlocks, ncols), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), logits, n, col_stride, part);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(ncols), dim3(256), 0, static_cast<hipStream_t>(stream), part, out_idx);
+    return launch_status("argmax");
+}
+
+extern "C" int rmi_embed_q6_k(const void* emb, const int* tokens, float* x, float* partials, int n_embd, int n_vocab,
+                              int ncols, void* stream) {
+    if (n_embd <= 0 || n_embd % 256 != 0 || n_vocab <= 0 || bad_cols(ncols))
+        return fail(RMI_ERR_SHAPE, "embed_q6_k: bad shape");
+    if (!emb || (reinterpret_cast<uintptr_t>(emb) & 1u) || !aligned4(tokens) || !aligned4(x) || !aligned4(partials))
+        return fail(RMI_ERR_POINTER, "embed_q6_k: null or misaligned pointer");
+    hipLaunchKernelGGL(embed_q6_k_kernel, dim3(n_embd / 256, ncols), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint8_t*>(emb), tokens, x, partials, n_embd, n_vocab);
+    return launch_status("embed_q6_k");
+}

@@ -1,0 +1,265 @@
+// gdn.hip - Gated DeltaNet decode chain for gfx950 (reference src/fused_gdn.cu:40-133, engine glue
+// src/qwythos.cpp:1101-1127 and the verify pass 1438-1478).
+//
+// Two kernels per layer, for 1 token (the plain decode step) or the 2 verify tokens:
+//   conv:  one lane per channel (8192 = q 2048 | k 2048 | v 4096): causal width-4 conv over [hist(3) | x], SiLU, and
+//          the L2 norm of each 128-channel q/k head.  History is updated in place; with 2 tokens the history after
+//          token 0 also goes to the rollback buffer.
+//   step:  one workgroup per value head (128 columns x 4 row groups, 512 lanes), the head's 128x128 fp32 state held
+//          in registers (32 rows per lane) across both tokens.  Per token: decay g = exp(softplus(a + dt) * ssm_a),
+//          beta = sigmoid(b) (both from the raw beta|alpha GEMV output), kv = S^T k, delta = (v - g kv) beta,
+//          S = g S + k delta^T, o = S^T q / sqrt(128), y = o * rsqrt(mean(o^2) + eps) * gamma * silu(z), Q8_1 of y.
+//          With 2 tokens the state after token 0 is written to the rollback buffer, the final state in place.
+// State layout [128 rows (k index)][h_v][128 cols (v index)], cols fastest (fgdn:60-61).  Conv history [c][3],
+// conv weights [c][4] (fgdn:113-133).
+//
+// Rollback by selector: each GDN layer owns two state buffers and two history buffers; `sel` (device int) names the
+// live one.  A verify writes the after-token-0 state/history into the other buffer, so rejecting the draft is a flip
+// of `sel` (no copy).  A single-token step updates the live buffers in place.
+#include "rmi_common.h"
+
+namespace rmi {
+namespace {
+
+constexpr int S = 128;
+constexpr int RG = 4;
+constexpr int RPG = S / RG;
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+template <typename T>
+__device__ __forceinline__ T* pick(T* a, T* b, const int* sel) {
+    return (sel != nullptr && *sel != 0) ? b : a;
+}
+
+// ---- conv + SiLU + L2 -------------------------------------------------------------------------------------------------
+// 256 lanes per workgroup = two 128-channel heads.  x of token t at x + t * tok_stride, output likewise at h.
+template <int NT>
+__global__ __launch_bounds__(256) void gdn_conv_kernel(float* hist_a, float* hist_b, const int* sel,
+                                                       const float* x, const float* __restrict__ w, float* h,
+                                                       int tok_stride, int qk_heads, float eps) {
+    __shared__ float part[NT][4];
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    float* hist = pick(hist_a, hist_b, sel);
+    float* snap = pick(hist_b, hist_a, sel);
+    const float h0 = hist[3 * c], h1 = hist[3 * c + 1], h2 = hist[3 * c + 2];
+    const float w0 = w[4 * c], w1 = w[4 * c + 1], w2 = w[4 * c + 2], w3 = w[4 * c + 3];
+    const float x0 = x[c];
+    float y[NT];
+    y[0] = silu(__builtin_fmaf(x0, w3, __builtin_fmaf(h2, w2, __builtin_fmaf(h1, w1, h0 * w0))));
+    float x1 = 0.0f;
+    if constexpr (NT == 2) {
+        x1 = x[tok_stride + c];
+        y[1] = silu(__builtin_fmaf(x1, w3, __builtin_fmaf(x0, w2, __builtin_fmaf(h2, w1, h1 * w0))));
+    }
+    const int head = c / S;   // uniform per wave (a head is two waves)
+    if (head < qk_heads) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float sq = group_sum<64>(y[t] * y[t]);
+            if ((threadIdx.x & 63) == 0) part[t][threadIdx.x >> 6] = sq;
+        }
+    }
+    __syncthreads();
+    if (head < qk_heads) {
+        const int pair = (threadIdx.x >> 7) * 2;   // the two waves of this lane's head
+#pragma unroll
+        for (int t = 0; t < NT; ++t) y[t] *= rsqrtf((part[t][pair] + part[t][pair + 1]) + eps);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) h[static_cast<size_t>(t) * tok_stride + c] = y[t];
+    if constexpr (NT == 2) {
+        snap[3 * c] = h1;
+        snap[3 * c + 1] = h2;
+        snap[3 * c + 2] = x0;
+        hist[3 * c] = h2;
+        hist[3 * c + 1] = x0;
+        hist[3 * c + 2] = x1;
+    } else {
+        hist[3 * c] = h1;
+        hist[3 * c + 1] = h2;
+        hist[3 * c + 2] = x0;
+    }
+}
+
+// ---- delta-rule step + RMSNorm * SiLU gate + Q8_1 ----------------------------------------------------------------------
+struct StepArgs {
+    float* state_a;
+    float* state_b;
+    const int* sel;
+    const float* q;        // token t at + t * tok_stride; head qh at + qh * 128
+    const float* k;
+    const float* v;        // head h at + h * 128
+    const float* z;
+    int tok_stride;
+    // gates: RAW = raw beta|alpha GEMV output (beta at ab[h], alpha at ab[h_v + h], token t at + t * ab_stride)
+    const float* ab;
+    int ab_stride;
+    const float* dt;
+    const float* ssm_a;
+    // gates, prepared (the reference API): decay logit gate[h], beta[h] after the sigmoid
+    const float* gate;
+    const float* beta;
+    const float* gamma;
+    float eps;
+    float* y;              // token t at + t * y_stride
+    int y_stride;
+    uint8_t* q8;           // token t at + t * q8_stride bytes (may be null)
+    int q8_stride;
+    int h_k, h_v;
+};
+
+template <int NT, bool RAW>
+__global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
+    __shared__ float sk[S], sq[S];
+    __shared__ float red[RG][S];
+    __shared__ float wsum[2];
+    __shared__ float gb[2];
+    const int head = blockIdx.x;
+    const int col = threadIdx.x & (S - 1);
+    const int rg = threadIdx.x >> 7;
+    const int qh = head % a.h_k;
+    float* state = pick(a.state_a, a.state_b, a.sel);
+    float* snap = pick(a.state_b, a.state_a, a.sel);
+    const size_t row_stride = static_cast<size_t>(a.h_v) * S;
+    const size_t base = (static_cast<size_t>(rg * RPG) * a.h_v + head) * S + col;
+
+    float s[RPG];
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) s[r] = state[base + r * row_stride];
+
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const size_t to = static_cast<size_t>(t) * a.tok_stride;
+        if (threadIdx.x < S) {
+            sk[threadIdx.x] = a.k[to + qh * S + threadIdx.x];
+            sq[threadIdx.x] = a.q[to + qh * S + threadIdx.x];
+        }
+        if (threadIdx.x == 0) {
+            float g, b;
+            if constexpr (RAW) {
+                const float* ab = a.ab + static_cast<size_t>(t) * a.ab_stride;
+                b = 1.0f / (1.0f + expf(-ab[head]));
+                const float vv = ab[a.h_v + head] + a.dt[head];
+                g = expf((vv > 20.0f ? vv : log1pf(expf(vv))) * a.ssm_a[head]);
+            } else {
+                b = a.beta[head];
+                g = expf(a.gate[head]);
+            }
+            gb[0] = g;
+            gb[1] = b;
+        }
+        __syncthreads();
+        const float g = gb[0], beta = gb[1];
+        float kv = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RPG; ++r) kv = __builtin_fmaf(s[r], sk[rg * RPG + r], kv);
+        red[rg][col] = kv;
+        __syncthreads();
+        const float kv_col = ((red[0][col] + red[1][col]) + red[2][col]) + red[3][col];
+        const float delta = (a.v[to + head * S + col] - g * kv_col) * beta;
+        float o = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RPG; ++r) {
+            s[r] = __builtin_fmaf(g, s[r], sk[rg * RPG + r] * delta);
+            o = __builtin_fmaf(s[r], sq[rg * RPG + r], o);
+        }
+        __syncthreads();   // everyone has read red (kv) before it is reused for o
+        red[rg][col] = o;
+        __syncthreads();
+        float oc = 0.0f;
+        if (rg == 0) {
+            oc = (((red[0][col] + red[1][col]) + red[2][col]) + red[3][col]) * 0.08838834764831845f;
+            const float ss = group_sum<64>(oc * oc);
+            if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
+        }
+        if constexpr (NT == 2) {
+            if (t == 0) {
+#pragma unroll
+                for (int r = 0; r < RPG; ++r) snap[base + r * row_stride] = s[r];
+            }
+        }
+        __syncthreads();
+        if (rg == 0) {
+            const float scale = rsqrtf((wsum[0] + wsum[1]) / static_cast<float>(S) + a.eps);
+            const float zz = a.z[to + head * S + col];
+            const float yv = oc * scale * a.gamma[col] * silu(zz);
+            a.y[static_cast<size_t>(t) * a.y_stride + head * S + col] = yv;
+            if (a.q8) q8_1_store_lane(yv, a.q8 + static_cast<size_t>(t) * a.q8_stride + (head * 4 + (col >> 5)) * kQ8_1Bytes);
+        }
+        __syncthreads();   // sk/sq/gb/wsum are rewritten by the next token
+    }
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) state[base + r * row_stride] = s[r];
+}
+
+}  // namespace
+}  // namespace rmi
+
+using namespace rmi;
+
+// ---- reference surface ----------------------------------------------------------------------------------------------
+
+extern "C" int rmi_fused_gdn_conv_l2(float* history, const float* qkv, const float* conv_w, float* h, int channels,
+                                     int qk_heads, float eps, void* stream) {
+    if (channels <= 0 || channels % 256 != 0 || qk_heads < 0 || qk_heads > channels / S)
+        return fail(RMI_ERR_SHAPE, "fused_gdn_conv_l2: invalid arguments");
+    if (!aligned4(history) || !aligned4(qkv) || !aligned4(conv_w) || !aligned4(h))
+        return fail(RMI_ERR_POINTER, "fused_gdn_conv_l2: invalid arguments");
+    hipLaunchKernelGGL(gdn_conv_kernel<1>, dim3(channels / 256), dim3(256), 0, static_cast<hipStream_t>(stream), history,
+                       history, nullptr, qkv, conv_w, h, 0, qk_heads, eps);
+    return launch_status("fused_gdn_conv_l2");
+}
+
+extern "C" int rmi_fused_gdn_step_norm_silu_q8(float* state, const float* q, const float* k, const float* v,
+                                               const float* gate, const float* beta, const float* z,
+                                               const float* gamma, float eps, float* y, uint8_t* q8, int h_k, int h_v,
+                                               void* stream) {
+    if (h_k <= 0 || h_v <= 0 || h_v % h_k) return fail(RMI_ERR_SHAPE, "fused_gdn_step_norm: invalid arguments");
+    if (!aligned4(state) || !aligned4(q) || !aligned4(k) || !aligned4(v) || !aligned4(gate) || !aligned4(beta) ||
+        !aligned4(z) || !aligned4(gamma) || !aligned4(y) || (q8 && (reinterpret_cast<uintptr_t>(q8) & 3u)))
+        return fail(RMI_ERR_POINTER, "fused_gdn_step_norm: invalid arguments");
+    StepArgs a{};
+    a.state_a = a.state_b = state;
+    a.q = q; a.k = k; a.v = v; a.z = z;
+    a.gate = gate; a.beta = beta; a.gamma = gamma; a.eps = eps;
+    a.y = y; a.q8 = q8; a.h_k = h_k; a.h_v = h_v;
+    hipLaunchKernelGGL((gdn_step_kernel<1, false>), dim3(h_v), dim3(S * RG), 0, static_cast<hipStream_t>(stream), a);
+    return launch_status("fused_gdn_step_norm_silu_q8");
+}
+
+// ---- engine surface: qkv|z and beta|alpha GEMV outputs, 1 or 2 tokens, selector-based rollback buffers --------------
+// Per token t: qkvz + t * qkvz_stride holds [q h_k*128 | k h_k*128 | v h_v*128 | z h_v*128]; ab + t * ab_stride holds
+// [beta h_v | alpha h_v].  The conv output overwrites the q|k|v part in place; y + t * y_stride, q8 + t * q8_stride.
+extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_a, float* hist_b, const int* sel,
+                                    float* qkvz, int qkvz_stride, const float* ab, int ab_stride, const float* conv_w,
+                                    const float* dt, const float* ssm_a, const float* gamma, float eps, float* y,
+                                    int y_stride, uint8_t* q8, int q8_stride, int h_k, int h_v, int ntok,
+                                    void* stream) {
+    if (h_k <= 0 || h_v <= 0 || h_v % h_k || ntok < 1 || ntok > 2)
+        return fail(RMI_ERR_SHAPE, "gdn_layer_tokens: invalid arguments");
+    const int channels = 2 * h_k * S + h_v * S;
+    if (channels % 256 != 0 || qkvz_stride < channels + h_v * S)
+        return fail(RMI_ERR_SHAPE, "gdn_layer_tokens: invalid arguments");
+    if (!aligned4(state_a) || !aligned4(state_b) || !aligned4(hist_a) || !aligned4(hist_b) || !aligned4(qkvz) ||
+        !aligned4(ab) || !aligned4(conv_w) || !aligned4(dt) || !aligned4(ssm_a) || !aligned4(gamma) || !aligned4(y))
+        return fail(RMI_ERR_POINTER, "gdn_layer_tokens: invalid arguments");
+    const auto s = static_cast<hipStream_t>(stream);
+    if (ntok == 2)
+        hipLaunchKernelGGL(gdn_conv_kernel<2>, dim3(channels / 256), dim3(256), 0, s, hist_a, hist_b, sel, qkvz, conv_w,
+                           qkvz, qkvz_stride, 2 * h_k, eps);
+    else
+        hipLaunchKernelGGL(gdn_conv_kernel<1>, dim3(channels / 256), dim3(256), 0, s, hist_a, hist_b, sel, qkvz, conv_w,
+                           qkvz, qkvz_stride, 2 * h_k, eps);
+    StepArgs a{};
+    a.state_a = state_a; a.state_b = state_b; a.sel = sel;
+    a.q = qkvz; a.k = qkvz + h_k * S; a.v = qkvz + 2 * h_k * S; a.z = qkvz + channels;
+    a.tok_stride = qkvz_stride;
+    a.ab = ab; a.ab_stride = ab_stride; a.dt = dt; a.ssm_a = ssm_a;
+    a.gamma = gamma; a.eps = eps;
+    a.y = y; a.y_stride = y_stride; a.q8 = q8; a.q8_stride = q8_stride;
+    a.h_k = h_k; a.h_v = h_v;
+    if (ntok == 2) hipLaunchKernelGGL((gdn_step_kernel<2, true>), dim3(h_v), dim3(S * RG), 0, s, a);
+    else hipLaunchKernelGGL((gdn_step_kernel<1, true>), dim3(h_v), dim3(S * RG), 0, s, a);
+    return launch_status("gdn_layer_tokens");
+}

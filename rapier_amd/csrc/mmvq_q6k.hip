@@ -17,6 +17,9 @@
 //    result, and the residual variant is bitwise plain + res.
 #include "rmi_common.h"
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace rmi {
 namespace {
 
@@ -48,7 +51,8 @@ __device__ __forceinline__ int q6_subblock_dot(const int (&v)[8], const int (&u)
     for (int w = 0; w < 4; ++w) d0 = sdot4(v[w], u[w], d0);
 #pragma unroll
     for (int w = 4; w < 8; ++w) d1 = sdot4(v[w], u[w], d1);
-    return sc0 * d0 + sc1 * d1;
+    // |sc| <= 32 and |d| <= 16 * 32 * 127: both fit 24 bits, so the full-rate 24-bit multiplies are exact
+    return __mul24(sc0, d0) + __mul24(sc1, d1);
 }
 
 // 4-byte little-endian word from a 2-byte aligned global address (two u16 loads)
@@ -87,7 +91,10 @@ __device__ __forceinline__ void stage_x_block(const XRegs& r, int col, int j, ui
 }
 
 // ---- the tiled kernel ------------------------------------------------------------------------------------------------
-template <int R, int NCOLS, bool RES>
+// Persistent: workgroup g owns row tiles g, g + G, g + 2G, ... and walks the flat sequence of (tile, chunk) steps with
+// DEPTH chunks of loads in flight in registers, across tile boundaries, so a workgroup never idles on a fresh tile's
+// first load.  Each step: park the oldest chunk in LDS, refill its registers with the chunk DEPTH steps ahead, decode.
+template <int R, int NCOLS, bool RES, int DEPTH>
 __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __restrict__ w,
                                                            const uint8_t* __restrict__ x, float* y,
                                                            const float* res, float* partials, int n_in, int n_out) {
@@ -105,39 +112,39 @@ __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __rest
     __shared__ float vout[NCOLS][R];
 
     const int t = threadIdx.x;
-    const int row0 = blockIdx.x * R;
-    const size_t rowbytes = static_cast<size_t>(n_in / 256) * kQ6KBytes;
-    const int nchunks = n_in / (256 * CB);
+    const uint32_t rowbytes = static_cast<uint32_t>(n_in / 256) * kQ6KBytes;
+    const int nch = n_in / (256 * CB);
+    const int ntiles = (n_out + R - 1) / R;
+    const int G = gridDim.x;
+    const int my_tiles = (ntiles - static_cast<int>(blockIdx.x) + G - 1) / G;
+    const int nsteps = my_tiles * nch;
     const int xcol_blocks = n_in / 32;
 
-    // per-thread load slots (fixed for every chunk): global byte offset in chunk 0 and LDS dword offset
-    uint32_t goff[kLoadsPerThread];
-    int loff[kLoadsPerThread];
-    bool lok[kLoadsPerThread];
-#pragma unroll
-    for (int m = 0; m < kLoadsPerThread; ++m) {
-        const int i = t + kThreads * m;
-        const int tr = i / U, u = i - tr * U;
-        lok[m] = i < kTileVec && row0 + tr < n_out;
-        goff[m] = static_cast<uint32_t>(tr) * static_cast<uint32_t>(rowbytes) + static_cast<uint32_t>(u * 16);
-        loff[m] = tr * ROWW + u * 4;
-    }
-    const uint8_t* wrow0 = w + static_cast<size_t>(row0) * rowbytes;
+    u32x4 wreg[DEPTH][kLoadsPerThread];
+    XRegs xreg[DEPTH][XP];
 
-    u32x4 wreg[kLoadsPerThread];
-    XRegs xreg[XP];
-    auto load_chunk = [&](int c) {
-        const uint8_t* base = wrow0 + static_cast<size_t>(c) * (CB * kQ6KBytes);
+    // step f -> (tile, chunk); loads of 16-byte unit i = t + 256 m: tile row i / U, unit i % U
+    auto issue = [&](int f, u32x4 (&wr)[kLoadsPerThread], XRegs (&xr)[XP]) {
+        const int q = f / nch;
+        const int c = f - q * nch;
+        const int row0 = (static_cast<int>(blockIdx.x) + q * G) * R;
+        const uint8_t* base = w + static_cast<size_t>(row0) * rowbytes + static_cast<size_t>(c) * (CB * kQ6KBytes);
 #pragma unroll
-        for (int m = 0; m < kLoadsPerThread; ++m)
-            if (lok[m]) wreg[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + goff[m]));
+        for (int m = 0; m < kLoadsPerThread; ++m) {
+            const int i = t + kThreads * m;
+            const int tr = i / U, u = i - tr * U;
+            if (i < kTileVec && row0 + tr < n_out)
+                wr[m] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(base + static_cast<uint32_t>(tr) * rowbytes + u * 16));
+        }
 #pragma unroll
         for (int p = 0; p < XP; ++p) {
-            const int s = t + kThreads * p;
-            if (s < XS) {
-                const int col = s / NB, jb = s - col * NB;
-                load_x_block(x + (static_cast<size_t>(col) * xcol_blocks + static_cast<size_t>(c) * NB + jb) * kQ8_1Bytes,
-                             xreg[p]);
+            const int sidx = t + kThreads * p;
+            if (sidx < XS) {
+                const int col = sidx / NB, jb = sidx - col * NB;
+                load_x_block(x + (static_cast<size_t>(col) * xcol_blocks + static_cast<size_t>(c) * NB + jb) *
+                                     kQ8_1Bytes,
+                             xr[p]);
             }
         }
     };
@@ -153,103 +160,130 @@ __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __rest
 #pragma unroll
     for (int c = 0; c < NCOLS; ++c) tot[c] = 0.0f;
 
-    load_chunk(0);
-    for (int c = 0; c < nchunks; ++c) {
-        if (c > 0) __syncthreads();
 #pragma unroll
-        for (int m = 0; m < kLoadsPerThread; ++m)
-            if (lok[m]) {
-                lw[loff[m] + 0] = wreg[m].x;
-                lw[loff[m] + 1] = wreg[m].y;
-                lw[loff[m] + 2] = wreg[m].z;
-                lw[loff[m] + 3] = wreg[m].w;
+    for (int s = 0; s < DEPTH; ++s)
+        if (s < nsteps) issue(s, wreg[s], xreg[s]);
+
+    for (int f0 = 0; f0 < nsteps; f0 += DEPTH) {
+#pragma unroll
+        for (int s = 0; s < DEPTH; ++s) {
+            const int f = f0 + s;
+            if (f >= nsteps) break;   // uniform across the workgroup
+            const int q = f / nch;
+            const int c = f - q * nch;
+            if (f > 0) __syncthreads();
+#pragma unroll
+            for (int m = 0; m < kLoadsPerThread; ++m) {
+                const int i = t + kThreads * m;
+                const int tr = i / U, u = i - tr * U;
+                if (i < kTileVec) {
+                    const int lo = tr * ROWW + u * 4;
+                    lw[lo + 0] = wreg[s][m].x;
+                    lw[lo + 1] = wreg[s][m].y;
+                    lw[lo + 2] = wreg[s][m].z;
+                    lw[lo + 3] = wreg[s][m].w;
+                }
             }
 #pragma unroll
-        for (int p = 0; p < XP; ++p) {
-            const int s = t + kThreads * p;
-            if (s < XS) {
-                const int col = s / NB, jb = s - col * NB;
-                stage_x_block<NB>(xreg[p], col, jb, lq, lrec);
+            for (int p = 0; p < XP; ++p) {
+                const int sidx = t + kThreads * p;
+                if (sidx < XS) {
+                    const int col = sidx / NB, jb = sidx - col * NB;
+                    stage_x_block<NB>(xreg[s][p], col, jb, lq, lrec);
+                }
             }
-        }
-        __syncthreads();
-        if (c + 1 < nchunks) load_chunk(c + 1);
+            __syncthreads();
+            if (f + DEPTH < nsteps) issue(f + DEPTH, wreg[s], xreg[s]);
 
-        // decode the lane's half-block
-        uint32_t ql[16], qh[8], sc[2];
-        {
-            uint32_t tq[17];
+            // decode the lane's half-block: qh and the scales once, ql per nibble pair (sub-blocks k, k + 2)
+            uint32_t qh[8], sc[2];
+            {
+                uint32_t th[9];
 #pragma unroll
-            for (int i = 0; i < 17; ++i) tq[i] = lw[wd + 16 * n + i];
+                for (int i = 0; i < 9; ++i) th[i] = lw[wd + 32 + 8 * n + i];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) ql[i] = __builtin_amdgcn_alignbyte(tq[i + 1], tq[i], mis);
-            uint32_t th[9];
-#pragma unroll
-            for (int i = 0; i < 9; ++i) th[i] = lw[wd + 32 + 8 * n + i];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qh[i] = __builtin_amdgcn_alignbyte(th[i + 1], th[i], mis);
-            const uint32_t s0 = lw[wd + 48 + 2 * n], s1 = lw[wd + 49 + 2 * n], s2 = lw[wd + 50 + 2 * n];
-            sc[0] = __builtin_amdgcn_alignbyte(s1, s0, mis);
-            sc[1] = __builtin_amdgcn_alignbyte(s2, s1, mis);
-        }
-        const float d = half_bits_to_float(lw[wd + 52] >> (8 * mis));
-
-        float acc[NCOLS];
-#pragma unroll
-        for (int col = 0; col < NCOLS; ++col) acc[col] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            int v[8];
-#pragma unroll
-            for (int ww = 0; ww < 8; ++ww) v[ww] = q6_codes4(ql, qh, k, ww);
-            const int sc0 = sc_byte(sc, 2 * k), sc1 = sc_byte(sc, 2 * k + 1);
-            const int j = 8 * b + 4 * n + k;
-#pragma unroll
-            for (int col = 0; col < NCOLS; ++col) {
-                const uint4 qa = lq[col * 2 * NB + swz(2 * j)];
-                const uint4 qb = lq[col * 2 * NB + swz(2 * j + 1)];
-                const uint4 rec = lrec[col * NB + swz(j)];
-                const int u[8] = {static_cast<int>(qa.x), static_cast<int>(qa.y), static_cast<int>(qa.z),
-                                  static_cast<int>(qa.w), static_cast<int>(qb.x), static_cast<int>(qb.y),
-                                  static_cast<int>(qb.z), static_cast<int>(qb.w)};
-                const int s = q6_subblock_dot(v, u, static_cast<int>(rec.x), static_cast<int>(rec.y), sc0, sc1);
-                acc[col] = __builtin_fmaf(__uint_as_float(rec.z), static_cast<float>(s), acc[col]);
+                for (int i = 0; i < 8; ++i) qh[i] = __builtin_amdgcn_alignbyte(th[i + 1], th[i], mis);
+                const uint32_t s0 = lw[wd + 48 + 2 * n], s1 = lw[wd + 49 + 2 * n], s2 = lw[wd + 50 + 2 * n];
+                sc[0] = __builtin_amdgcn_alignbyte(s1, s0, mis);
+                sc[1] = __builtin_amdgcn_alignbyte(s2, s1, mis);
             }
-        }
+            const float d = half_bits_to_float(lw[wd + 52] >> (8 * mis));
+            float acc[NCOLS];
 #pragma unroll
-        for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
-    }
+            for (int col = 0; col < NCOLS; ++col) acc[col] = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                uint32_t ql8[8];
+                {
+                    uint32_t tq[9];
+#pragma unroll
+                    for (int i = 0; i < 9; ++i) tq[i] = lw[wd + 16 * n + 8 * kk + i];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) ql8[i] = __builtin_amdgcn_alignbyte(tq[i + 1], tq[i], mis);
+                }
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh) {
+                    const int k = kk + 2 * kh;
+                    int v[8];
+#pragma unroll
+                    for (int ww = 0; ww < 8; ++ww)
+                        v[ww] = static_cast<int>(((ql8[ww] >> (4 * kh)) & 0x0f0f0f0fu) |
+                                                 (((qh[ww] >> (2 * k)) & 0x03030303u) << 4));
+                    const int sc0 = sc_byte(sc, 2 * k), sc1 = sc_byte(sc, 2 * k + 1);
+                    const int j = 8 * b + 4 * n + k;
+#pragma unroll
+                    for (int col = 0; col < NCOLS; ++col) {
+                        const uint4 qa = lq[col * 2 * NB + swz(2 * j)];
+                        const uint4 qb = lq[col * 2 * NB + swz(2 * j + 1)];
+                        const uint4 rec = lrec[col * NB + swz(j)];
+                        const int u[8] = {static_cast<int>(qa.x), static_cast<int>(qa.y), static_cast<int>(qa.z),
+                                          static_cast<int>(qa.w), static_cast<int>(qb.x), static_cast<int>(qb.y),
+                                          static_cast<int>(qb.z), static_cast<int>(qb.w)};
+                        const int sdot = q6_subblock_dot(v, u, static_cast<int>(rec.x), static_cast<int>(rec.y), sc0, sc1);
+                        acc[col] = __builtin_fmaf(__uint_as_float(rec.z), static_cast<float>(sdot), acc[col]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
 
-    // row reduction over the TPR lanes of the row, then the epilogue
+            if (c == nch - 1) {
+                // the tile's rows are complete: reduce each row's TPR lanes, then the epilogue
+                const int row0 = (static_cast<int>(blockIdx.x) + q * G) * R;
 #pragma unroll
-    for (int col = 0; col < NCOLS; ++col) {
-        const float s = group_sum<TPR>(tot[col]);
-        if (hb == 0) vout[col][ri] = s;
-    }
-    __syncthreads();
-    if (t < NCOLS * R) {
-        const int col = t / R, r = t - col * R;
-        const int row = row0 + r;
-        if (row < n_out) {
-            float v = vout[col][r];
-            if constexpr (RES) v += res[static_cast<size_t>(col) * n_out + row];
-            y[static_cast<size_t>(col) * n_out + row] = v;
-            if constexpr (RES) vout[col][r] = v;
-        }
-    }
-    if constexpr (RES) {
-        __syncthreads();
-        constexpr int G = R / 4;
-        if (t < NCOLS * G) {
-            const int col = t / G, g = t - col * G;
-            const int np = (n_out + 3) / 4;
-            const int grow = row0 / 4 + g;
-            if (grow < np) {
-                float p = 0.0f;
+                for (int col = 0; col < NCOLS; ++col) {
+                    const float sum = group_sum<TPR>(tot[col]);
+                    if (hb == 0) vout[col][ri] = sum;
+                    tot[col] = 0.0f;
+                }
+                __syncthreads();
+                if (t < NCOLS * R) {
+                    const int col = t / R, r = t - col * R;
+                    const int row = row0 + r;
+                    if (row < n_out) {
+                        float v = vout[col][r];
+                        if constexpr (RES) v += res[static_cast<size_t>(col) * n_out + row];
+                        y[static_cast<size_t>(col) * n_out + row] = v;
+                        if constexpr (RES) vout[col][r] = v;
+                    }
+                }
+                if constexpr (RES) {
+                    __syncthreads();
+                    constexpr int GR = R / 4;
+                    if (t < NCOLS * GR) {
+                        const int col = t / GR, g = t - col * GR;
+                        const int np = (n_out + 3) / 4;
+                        const int grow = row0 / 4 + g;
+                        if (grow < np) {
+                            float p = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (row0 + 4 * g + i < n_out) p = __builtin_fmaf(vout[col][4 * g + i], vout[col][4 * g + i], p);
-                partials[static_cast<size_t>(col) * np + grow] = p;
+                            for (int i = 0; i < 4; ++i)
+                                if (row0 + 4 * g + i < n_out)
+                                    p = __builtin_fmaf(vout[col][4 * g + i], vout[col][4 * g + i], p);
+                            partials[static_cast<size_t>(col) * np + grow] = p;
+                        }
+                    }
+                }
             }
         }
     }
@@ -374,16 +408,57 @@ int pick_rows(int n_in, int n_out, const void* w) {
     return 16;
 }
 
+struct TileCfg {
+    int rows;    // 16 or 8 (0: generic kernel)
+    int depth;   // chunks of loads in flight per workgroup
+    int per_cu;  // persistent workgroups per CU (0: one workgroup per tile)
+};
+
+int env_int(const char* name, int def) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : def;
+}
+
+int cu_count() {
+    static int n = [] {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            c = 256;
+        return c > 0 ? c : 256;
+    }();
+    return n;
+}
+
+TileCfg pick_cfg(int n_in, int n_out, const void* w) {
+    static const int depth = env_int("RMI_GEMV_DEPTH", 2);
+    static const int per_cu = env_int("RMI_GEMV_PER_CU", 0);
+    static const int force_rows = env_int("RMI_GEMV_ROWS", 0);
+    TileCfg cfg{pick_rows(n_in, n_out, w), depth == 1 ? 1 : 2, per_cu};
+    if (cfg.rows && (force_rows == 8 || force_rows == 16) && n_in % (256 * (128 / force_rows)) == 0)
+        cfg.rows = force_rows;
+    return cfg;
+}
+
+template <int R, int NCOLS, bool RES, int DEPTH>
+void launch_tiled(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in, int n_out,
+                  int per_cu, hipStream_t s) {
+    const int ntiles = (n_out + R - 1) / R;
+    int grid = ntiles;
+    if (per_cu > 0) grid = std::min(ntiles, per_cu * cu_count());
+    hipLaunchKernelGGL((q6k_gemv_tiled<R, NCOLS, RES, DEPTH>), dim3(grid), dim3(kThreads), 0, s, w, x, y, res, partials,
+                       n_in, n_out);
+}
+
 template <int NCOLS, bool RES>
 void launch_cols(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in, int n_out,
                  hipStream_t s) {
-    const int rows = pick_rows(n_in, n_out, w);
-    if (rows == 16) {
-        hipLaunchKernelGGL((q6k_gemv_tiled<16, NCOLS, RES>), dim3((n_out + 15) / 16), dim3(kThreads), 0, s, w, x, y, res,
-                           partials, n_in, n_out);
-    } else if (rows == 8) {
-        hipLaunchKernelGGL((q6k_gemv_tiled<8, NCOLS, RES>), dim3((n_out + 7) / 8), dim3(kThreads), 0, s, w, x, y, res,
-                           partials, n_in, n_out);
+    const TileCfg cfg = pick_cfg(n_in, n_out, w);
+    if (cfg.rows == 16) {
+        if (cfg.depth == 1) launch_tiled<16, NCOLS, RES, 1>(w, x, y, res, partials, n_in, n_out, cfg.per_cu, s);
+        else launch_tiled<16, NCOLS, RES, 2>(w, x, y, res, partials, n_in, n_out, cfg.per_cu, s);
+    } else if (cfg.rows == 8) {
+        if (cfg.depth == 1) launch_tiled<8, NCOLS, RES, 1>(w, x, y, res, partials, n_in, n_out, cfg.per_cu, s);
+        else launch_tiled<8, NCOLS, RES, 2>(w, x, y, res, partials, n_in, n_out, cfg.per_cu, s);
     } else {
         hipLaunchKernelGGL((q6k_gemv_generic<NCOLS, RES>), dim3((n_out + 3) / 4), dim3(kThreads), 0, s, w, x, y, res,
                            partials, n_in, n_out);

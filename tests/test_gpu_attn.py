@@ -1,0 +1,106 @@
+"""GPU parity of the GQA decode attention (config 4: 16 q heads, 4 KV heads, head_dim 256, 2 query positions, fp16 KV
+cache N(0,1) at contexts 4096 / 32768 / 65536, RoPE'd fp32 queries N(0,1), sigmoid output gate, Q8_1 output).
+
+Bars (written here): gated fp32 output within 1e-3 relative of the oracle's fp64 softmax over the same fp16 K/V;
+Q8_1 within half a quantization step.  Invariants, bit for bit: each column of the 2-query launch equals the
+1-query launch at that position (chunking depends only on the query position).  attn_prep (per-head RMSNorm,
+NEOX RoPE, fp16 store) is checked against the oracle's RMSNorm and complex-form-pinned RoPE.
+"""
+import numpy as np
+import pytest
+
+from tests.gpu_util import assert_close_rel, dev, empty, host, torch
+
+pytestmark = pytest.mark.gpu
+
+NH, NKV, HD = 16, 4, 256
+Q3 = NH * 2 * HD + 2 * NKV * HD     # 10240: [16 x (q | gate) | k | v]
+SCALE = 1.0 / 16.0
+
+
+@pytest.fixture(scope="module")
+def rmi():
+    import rapier_amd
+    rapier_amd.lib()
+    return rapier_amd
+
+
+def kv_cache(orc, ctx, seed):
+    k = orc.normal(ctx * NKV * HD, seed=seed).astype(np.float16).view(np.uint16)
+    v = orc.normal(ctx * NKV * HD, seed=seed + 1).astype(np.float16).view(np.uint16)
+    return k, v
+
+
+def flash(rmi, q, kc, vc, p0, gate, ntok, max_ctx, nsub):
+    ws = empty(rmi.gqa_workspace_bytes(max_ctx, NKV, nsub), "uint8")
+    y = empty(ntok * NH * HD)
+    q8 = empty(ntok * NH * HD // 32 * 36, "uint8")
+    rmi.gqa_flash_decode(q, kc, vc, dev(np.array([p0], np.int32)), gate, Q3, y, NH * HD, q8, NH * HD // 32 * 36, ws,
+                         NH, NKV, HD, ntok, max_ctx, nsub, SCALE)
+    return host(y), host(q8)
+
+
+@pytest.mark.parametrize("ctx,nsub", [(4096, 1), (32768, 4), (65536, 4)])
+def test_flash_decode_matches_oracle(orc, rmi, ctx, nsub):
+    kc, vc = kv_cache(orc, ctx, seed=ctx)
+    q = orc.normal(2 * NH * HD, seed=ctx + 7)
+    g = orc.normal(2 * Q3, seed=ctx + 8)
+    p0 = ctx - 2
+    dk, dv, dq, dg = dev(kc), dev(vc), dev(q), dev(g)
+    y, q8 = flash(rmi, dq, dk, dv, p0, dg, 2, ctx, nsub)
+    for t in range(2):
+        o = orc.gqa_decode(q[t * NH * HD:(t + 1) * NH * HD], kc, vc, NH, NKV, HD, p0 + t + 1, SCALE)
+        gate = np.concatenate([g[t * Q3 + h * 2 * HD + HD:t * Q3 + h * 2 * HD + 2 * HD] for h in range(NH)])
+        ref = o / (1 + np.exp(-gate.astype(np.float64)))
+        assert_close_rel(y[t * NH * HD:(t + 1) * NH * HD], ref, rtol=1e-3, atol_frac=1e-5, what=f"ctx {ctx} t{t}")
+        blk = NH * HD // 32 * 36
+        deq = orc.dequantize_q8_1(q8[t * blk:(t + 1) * blk], NH * HD).reshape(-1, 32).astype(np.float64)
+        r = ref.reshape(-1, 32)
+        amax = np.abs(r).max(1, keepdims=True)
+        assert (np.abs(deq - r) <= 0.5 * amax / 127 * 1.001 + 2e-3 * amax).all(), f"q8 t{t}"
+    # each verify column is bitwise the single-query launch at its position
+    for t in range(2):
+        y1, q81 = flash(rmi, dq[t * NH * HD:], dk, dv, p0 + t, dg[t * Q3:], 1, ctx, nsub)
+        assert np.array_equal(y1.view(np.uint32), y[t * NH * HD:(t + 1) * NH * HD].view(np.uint32))
+
+
+@pytest.mark.parametrize("p0", [0, 1, 63, 64, 200])
+def test_flash_decode_short_contexts(orc, rmi, p0):
+    """edge cases: a single visible position (o = V0), chunk boundaries at 64."""
+    ctx = 320
+    kc, vc = kv_cache(orc, ctx, seed=900 + p0)
+    q = orc.normal(2 * NH * HD, seed=901)
+    g = np.full(2 * Q3, 40.0, np.float32)            # sigmoid(40) == 1: y is the attention output itself
+    y, _ = flash(rmi, dev(q), dev(kc), dev(vc), p0, dev(g), 2, ctx, 1)
+    for t in range(2):
+        o = orc.gqa_decode(q[t * NH * HD:(t + 1) * NH * HD], kc, vc, NH, NKV, HD, p0 + t + 1, SCALE)
+        assert_close_rel(y[t * NH * HD:(t + 1) * NH * HD], o, rtol=1e-3, atol_frac=1e-5, what=f"p0 {p0} t{t}")
+    if p0 == 0:
+        v0 = vc[:NKV * HD].view(np.float16).astype(np.float32).reshape(NKV, HD)
+        assert np.array_equal(y[:NH * HD].reshape(NH, HD), np.repeat(v0, NH // NKV, axis=0))
+
+
+def test_attn_prep_matches_oracle(orc, rmi):
+    t_ = torch()
+    max_ctx, p0, theta, eps = 1024, 777, 1e7, 1e-6
+    q3 = orc.normal(2 * Q3, seed=950)
+    qn = (1 + orc.normal(HD, seed=951, std=0.1)).astype(np.float32)
+    kn = (1 + orc.normal(HD, seed=952, std=0.1)).astype(np.float32)
+    kc = t_.zeros(max_ctx * NKV * HD, dtype=t_.int16, device="cuda:0")
+    vc = t_.zeros(max_ctx * NKV * HD, dtype=t_.int16, device="cuda:0")
+    qo = empty(2 * NH * HD)
+    rmi.attn_prep(dev(q3), Q3, dev(qn), dev(kn), kc, vc, dev(np.array([p0], np.int32)), qo, NH, NKV, HD, 64, theta,
+                  eps, 2, max_ctx)
+    qh, kh, vh = host(qo), host(kc).view(np.float16), host(vc).view(np.float16)
+    for t in range(2):
+        src = q3[t * Q3:(t + 1) * Q3]
+        qx = np.concatenate([src[h * 2 * HD:h * 2 * HD + HD] for h in range(NH)])
+        qref = orc.rope_neox(orc.rms_norm_heads(qx, qn, NH, HD, eps), NH, HD, 64, p0 + t, theta)
+        assert_close_rel(qh[t * NH * HD:(t + 1) * NH * HD], qref, rtol=1e-5, atol_frac=2e-6, what=f"q t{t}")
+        kref = orc.rope_neox(orc.rms_norm_heads(src[NH * 2 * HD:NH * 2 * HD + NKV * HD], kn, NKV, HD, eps),
+                             NKV, HD, 64, p0 + t, theta)
+        kg = kh[(p0 + t) * NKV * HD:(p0 + t + 1) * NKV * HD].astype(np.float64)
+        assert np.abs(kg - kref).max() <= np.abs(kref).max() * 1e-3, f"k t{t}"
+        vref = src[NH * 2 * HD + NKV * HD:].astype(np.float16)
+        assert np.array_equal(vh[(p0 + t) * NKV * HD:(p0 + t + 1) * NKV * HD], vref)
+    assert not host(kc)[:p0 * NKV * HD].any(), "attn_prep wrote outside its positions"

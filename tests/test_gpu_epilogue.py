@@ -1,0 +1,151 @@
+"""GPU parity of the norm / activation epilogues, argmax, the device embedding row and the Q8_0 GEMV.
+
+Bars: Q8_1 outputs of a transcendental epilogue match the oracle's fp64 values within half a quantization step plus the
+fp16 rounding of d and 1e-5 of the block maximum (q may differ by one at a boundary); fp32 outputs within 1e-5 relative; argmax,
+embedding rows and partials of exact inputs bit-exact.
+"""
+import numpy as np
+import pytest
+
+from tests.gpu_util import assert_close_rel, dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def rmi():
+    import rapier_amd
+    rapier_amd.lib()
+    return rapier_amd
+
+
+def check_q8(orc, q8_bytes, ref, what):
+    """Q8_1 bytes vs fp64 reference values, per block: |deq - ref| <= d/2 (rounding of q) + 127 d 2^-11 (the fp16
+    rounding of d that deq multiplies by) + 1e-5 amax (the fp32 value itself)."""
+    deq = orc.dequantize_q8_1(q8_bytes, ref.size).astype(np.float64).reshape(-1, 32)
+    r = np.asarray(ref, np.float64).reshape(-1, 32)
+    amax = np.abs(r).max(1, keepdims=True)
+    d = amax / 127
+    bad = np.abs(deq - r) > 0.5 * d + 127 * d * 2.0 ** -11 + 1e-5 * amax + 1e-30
+    assert not bad.any(), f"{what}: {bad.sum()} elements outside the quantization bound"
+
+
+def test_rms_quant_apply_two_columns(orc, rmi):
+    cols, eps = 4096, 1e-6
+    x = orc.normal(2 * cols, seed=1)
+    w = (1 + orc.normal(cols, seed=2, std=0.1)).astype(np.float32)
+    parts = np.concatenate([orc.row_sum_partials(x[:cols]), orc.row_sum_partials(x[cols:])]).astype(np.float32)
+    y = empty(2 * cols // 32 * 36, "uint8")
+    rmi.rms_quant_apply(dev(x), dev(w), dev(parts), y, cols, eps, ncols=2)
+    yh = host(y)
+    for c in range(2):
+        inv = orc.rms_inv(parts[c * 1024:(c + 1) * 1024].astype(np.float64), cols, eps)
+        ref = orc.rms_norm_out(x[c * cols:(c + 1) * cols], w, inv)
+        check_q8(orc, yh[c * 4608:(c + 1) * 4608], ref, f"rms_quant_apply col {c}")
+    # column 1 of the 2-column launch equals a 1-column launch on that column, bit for bit
+    y1 = empty(4608, "uint8")
+    rmi.rms_quant_apply(dev(x[cols:]), dev(w), dev(parts[1024:]), y1, cols, eps, ncols=1)
+    assert np.array_equal(host(y1), yh[4608:])
+
+
+def test_rms_norm_out_and_partials(orc, rmi):
+    cols, eps = 4096, 1e-6
+    x = orc.normal(cols, seed=3)
+    w = (1 + orc.normal(cols, seed=4, std=0.1)).astype(np.float32)
+    parts = orc.row_sum_partials(x).astype(np.float32)
+    out, op = empty(cols), empty(cols // 4)
+    rmi.rms_norm_out(dev(x), dev(w), dev(parts), out, op, cols, eps)
+    ref = orc.rms_norm_out(x, w, orc.rms_inv(parts.astype(np.float64), cols, eps))
+    assert_close_rel(host(out), ref, rtol=1e-5, atol_frac=1e-6, what="rms_norm_out")
+    o = host(out).astype(np.float64)
+    np.testing.assert_allclose(host(op), (o.reshape(-1, 4) ** 2).sum(1), rtol=1e-6)
+
+
+def test_row_sum_and_add_partials(orc, rmi):
+    n = 4096
+    x, o = orc.normal(2 * n, seed=5), orc.normal(2 * n, seed=6)
+    p = empty(2 * n // 4)
+    rmi.row_sum_partials(dev(x), p, n, ncols=2)
+    np.testing.assert_allclose(host(p), (x.astype(np.float64).reshape(-1, 4) ** 2).sum(1), rtol=1e-6)
+    dx = dev(x)
+    rmi.add_partials(dx, dev(o), p, n, ncols=2)
+    xs = (x + o).astype(np.float32)
+    assert np.array_equal(host(dx), xs)
+    np.testing.assert_allclose(host(p), (xs.astype(np.float64).reshape(-1, 4) ** 2).sum(1), rtol=1e-6)
+
+
+def test_swiglu_and_sig_mul_quant(orc, rmi):
+    n = 12288
+    ug = orc.normal(2 * 2 * n, seed=7)            # two columns of [up n | gate n]
+    y = empty(2 * n // 32 * 36, "uint8")
+    rmi.swiglu_quant(dev(ug), dev(ug[n:]), y, n, ncols=2, col_stride=2 * n)
+    yh = host(y)
+    for c in range(2):
+        up, gate = ug[c * 2 * n:c * 2 * n + n], ug[c * 2 * n + n:(c + 1) * 2 * n]
+        check_q8(orc, yh[c * n // 32 * 36:(c + 1) * n // 32 * 36], orc.swiglu(up, gate), "swiglu")
+    n2 = 4096
+    o, g = orc.normal(n2, seed=8), orc.normal(n2, seed=9)
+    y2 = empty(n2 // 32 * 36, "uint8")
+    rmi.sig_mul_quant(dev(o), dev(g), y2, n2)
+    check_q8(orc, host(y2), orc.sig_mul(o, g), "sig_mul")
+
+
+def test_beta_gate(orc, rmi):
+    n = 32
+    ab = orc.normal(2 * 2 * n, seed=10)
+    ab[2 * n + n:2 * n + n + 4] = 25.0     # softplus linear branch
+    dt = orc.normal(n, seed=11, std=0.1)
+    ssm_a = (-np.exp(orc.normal(n, seed=12, std=0.5))).astype(np.float32)
+    dab, gg = dev(ab), empty(2 * n)
+    rmi.beta_gate(dab, dev(dt), dev(ssm_a), gg, n, ncols=2)
+    abh, ggh = host(dab), host(gg)
+    for c in range(2):
+        b, g = orc.beta_gate(ab[c * 2 * n:c * 2 * n + n], ab[c * 2 * n + n:(c + 1) * 2 * n], dt, ssm_a)
+        assert_close_rel(abh[c * 2 * n:c * 2 * n + n], b, rtol=1e-5, atol_frac=1e-7, what="beta")
+        assert_close_rel(ggh[c * n:(c + 1) * n], g, rtol=1e-5, atol_frac=1e-7, what="gate")
+
+
+@pytest.mark.parametrize("n", [248320, 1000, 1])
+def test_argmax_ties_lowest_index(orc, rmi, n):
+    l = orc.normal(2 * n, seed=n)
+    if n > 10:
+        l[[77, 500, n - 1]] = 9.0           # column 0: a three-way tie -> 77
+        l[n + n - 1] = 9.5                  # column 1: the last element
+        l[n + 3] = 9.5                      # ... tied with an earlier one -> 3
+    ws = empty(rmi.argmax_workspace_bytes(2), "uint8")
+    out = empty(2, "int32")
+    rmi.argmax(dev(l), n, out, ws, ncols=2, col_stride=n)
+    got = host(out)
+    assert got[0] == orc.argmax(l[:n]) and got[1] == orc.argmax(l[n:])
+    if n > 10:
+        assert got[0] == 77 and got[1] == 3
+
+
+def test_embed_q6_k_rows(orc, rmi):
+    n_embd, n_vocab = 4096, 300
+    emb = orc.gen_q6k(n_vocab, n_embd, seed=13)
+    toks = np.array([7, 299], dtype=np.int32)
+    x, p = empty(2 * n_embd), empty(2 * n_embd // 4)
+    rmi.embed_q6_k(dev(emb), dev(toks), x, p, n_embd, n_vocab, ncols=2)
+    deq = orc.q6k_dequant(emb, n_vocab, n_embd)
+    xh = host(x).reshape(2, n_embd)
+    assert np.array_equal(xh[0], deq[7]) and np.array_equal(xh[1], deq[299])
+    np.testing.assert_allclose(host(p), (xh.astype(np.float64).reshape(-1, 4) ** 2).sum(1), rtol=1e-6)
+
+
+@pytest.mark.parametrize("n_in,n_out,ncols", [(4096, 1000, 1), (4096, 257, 2), (1024, 64, 5)])
+def test_q8_0_gemv(orc, rmi, n_in, n_out, ncols):
+    w = orc.gen_q8_0(n_out, n_in, seed=n_out)
+    xq = orc.quantize_q8_1(orc.normal(ncols * n_in, seed=n_in), n_in, ncols)
+    y = empty(ncols * n_out)
+    dw, dxq = dev(w), dev(xq)        # keep the device copies alive until the kernel has run
+    rmi._call("rmi_native_mmvq", 8, rmi._p(dw), rmi._p(dxq), rmi._p(y), n_in, n_out, ncols, rmi._stream(None))
+    assert_close_rel(host(y), orc.q8_0_gemv(w, xq, n_in, n_out, ncols=ncols), what="q8_0")
+    res = orc.normal(n_out, seed=3)
+    yr, pr = dev(res), empty((n_out + 3) // 4)
+    dx1 = dev(xq[:n_in // 32 * 36])
+    rmi._call("rmi_native_q8_0_mmvq_res", rmi._p(dw), rmi._p(dx1), rmi._p(yr), rmi._p(yr), rmi._p(pr), n_in, n_out,
+              rmi._stream(None))
+    ref, pref = orc.q8_0_gemv(w, xq[:n_in // 32 * 36], n_in, n_out, res=res, partials=True)
+    assert_close_rel(host(yr), ref, what="q8_0 res")
+    assert_close_rel(host(pr), pref, rtol=1e-5, atol_frac=1e-6, what="q8_0 partials")

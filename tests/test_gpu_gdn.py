@@ -1,0 +1,126 @@
+"""GPU parity of the Gated DeltaNet chain (config 3: 16 key heads, 32 value heads, head_dim 128, 2 tokens).
+
+Bars (tolerances written here): conv / q / k / v outputs and y within 1e-3 relative of the oracle's fp64 chain; the
+recurrent state within 2e-3 max-abs; Q8_1 within half a quantization step.  Invariants, bit for bit: the 2-token
+call's token 0 and token 1 equal two sequential 1-token calls; the rollback buffer holds exactly the state / history
+after token 0; the reference-surface entry points (conv_l2, step_norm_silu_q8) agree with the fused layer call.
+"""
+import numpy as np
+import pytest
+
+from tests.gpu_util import assert_close_rel, dev, empty, host, torch
+
+pytestmark = pytest.mark.gpu
+
+H_K, H_V, S = 16, 32, 128
+CH = 2 * H_K * S + H_V * S          # 8192 conv channels
+QKVZ = CH + H_V * S                 # 12288 per token: q | k | v | z
+EPS = 1e-6
+
+
+@pytest.fixture(scope="module")
+def rmi():
+    import rapier_amd
+    rapier_amd.lib()
+    return rapier_amd
+
+
+def make_inputs(orc, seed=300):
+    qkvz = orc.normal(2 * QKVZ, seed=seed)
+    qkvz[QKVZ + 2 * H_K * S + 5 * S:QKVZ + 2 * H_K * S + 5 * S + 32] *= 1e4    # token 1: one v block x 1e4
+    qkvz[CH + 7 * S:CH + 7 * S + 32] *= 1e4                                  # token 0: one z block x 1e4 (Q8_1 finite path)
+    ab = orc.normal(2 * 2 * H_V, seed=seed + 1)                               # per token [beta 32 | alpha 32]
+    conv_w = orc.normal(4 * CH, seed=seed + 2, std=0.5)
+    hist = orc.normal(3 * CH, seed=seed + 3, std=0.5)
+    state = orc.normal(S * H_V * S, seed=seed + 4, std=0.05)
+    dt = np.zeros(H_V, np.float32)
+    ssm_a = (-np.exp(orc.normal(H_V, seed=seed + 5, std=0.5))).astype(np.float32)
+    gamma = (1 + orc.normal(S, seed=seed + 6, std=0.1)).astype(np.float32)
+    return qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma
+
+
+def oracle_chain(orc, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok=2):
+    st = state.astype(np.float64)
+    hs = hist.copy()
+    ys, states, hists, convs = [], [], [], []
+    for t in range(ntok):
+        x = qkvz[t * QKVZ:(t + 1) * QKVZ]
+        h, hs = orc.gdn_conv_l2(hs, x[:CH], conv_w, 2 * H_K, EPS)
+        b, g = orc.beta_gate(ab[t * 2 * H_V:t * 2 * H_V + H_V], ab[t * 2 * H_V + H_V:(t + 1) * 2 * H_V], dt, ssm_a)
+        y, st = orc.gdn_step_norm(st, h[:H_K * S], h[H_K * S:2 * H_K * S], h[2 * H_K * S:], g, b, x[CH:], gamma, EPS,
+                                  H_K, H_V)
+        ys.append(y); states.append(st.copy()); hists.append(hs.copy()); convs.append(h)
+    return ys, states, hists, convs
+
+
+def run_layer(rmi, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok, sel_val=0):
+    t = torch()
+    st_live, st_other = dev(state), t.zeros(S * H_V * S, device="cuda:0")
+    hi_live, hi_other = dev(hist), t.zeros(3 * CH, device="cuda:0")
+    sel = dev(np.array([sel_val], np.int32))
+    bufs = (st_live, st_other, hi_live, hi_other) if sel_val == 0 else (st_other, st_live, hi_other, hi_live)
+    dq = dev(qkvz[:ntok * QKVZ])
+    y = empty(ntok * H_V * S)
+    q8 = empty(ntok * H_V * S // 32 * 36, "uint8")
+    rmi.gdn_layer_tokens(bufs[0], bufs[1], bufs[2], bufs[3], sel, dq, QKVZ, dev(ab[:ntok * 2 * H_V]), 2 * H_V,
+                         dev(conv_w), dev(dt), dev(ssm_a), dev(gamma), EPS, y, H_V * S, q8, H_V * S // 32 * 36, H_K,
+                         H_V, ntok)
+    return dict(y=host(y), q8=host(q8), conv=host(dq), state=host(st_live), snap=host(st_other), hist=host(hi_live),
+                hsnap=host(hi_other))
+
+
+def test_gdn_two_tokens_match_oracle(orc, rmi):
+    inp = make_inputs(orc)
+    qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma = inp
+    r = run_layer(rmi, *inp, ntok=2)
+    ys, states, hists, convs = oracle_chain(orc, *inp)
+    for t in range(2):
+        assert_close_rel(r["conv"][t * QKVZ:t * QKVZ + CH], convs[t], rtol=1e-3, atol_frac=1e-6, what=f"conv t{t}")
+        assert_close_rel(r["y"][t * H_V * S:(t + 1) * H_V * S], ys[t], rtol=1e-3, atol_frac=1e-5, what=f"y t{t}")
+        blk = H_V * S // 32 * 36
+        deq = orc.dequantize_q8_1(r["q8"][t * blk:(t + 1) * blk], H_V * S).reshape(-1, 32).astype(np.float64)
+        ref = ys[t].reshape(-1, 32)
+        amax = np.abs(ref).max(1, keepdims=True)
+        assert (np.abs(deq - ref) <= 0.5 * amax / 127 * 1.001 + 1e-3 * amax + 1e-30).all(), f"q8 t{t}"
+        d, s, _ = orc.q8_1_fields(r["q8"][t * blk:(t + 1) * blk])
+        assert np.isfinite(d.view(np.float16)).all() and np.isfinite(s.view(np.float16)).all()
+    assert np.abs(r["snap"] - states[0]).max() < 2e-3, "state after token 0 (rollback buffer)"
+    assert np.abs(r["state"] - states[1]).max() < 2e-3, "state after token 1"
+    assert np.array_equal(r["hsnap"], hists[0].astype(np.float32))
+    assert np.array_equal(r["hist"], hists[1].astype(np.float32))
+
+
+@pytest.mark.parametrize("sel_val", [0, 1])
+def test_gdn_two_tokens_bitwise_equal_sequential(orc, rmi, sel_val):
+    inp = make_inputs(orc, seed=400)
+    qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma = inp
+    r2 = run_layer(rmi, *inp, ntok=2, sel_val=sel_val)
+    a = run_layer(rmi, qkvz[:QKVZ], ab[:2 * H_V], conv_w, hist, state, dt, ssm_a, gamma, ntok=1, sel_val=sel_val)
+    b = run_layer(rmi, qkvz[QKVZ:], ab[2 * H_V:], conv_w, a["hist"], a["state"], dt, ssm_a, gamma, ntok=1,
+                  sel_val=sel_val)
+    u = lambda v: np.asarray(v).view(np.uint32)  # noqa: E731
+    assert np.array_equal(u(r2["y"][:H_V * S]), u(a["y"])) and np.array_equal(u(r2["y"][H_V * S:]), u(b["y"]))
+    blk = H_V * S // 32 * 36
+    assert np.array_equal(r2["q8"][:blk], a["q8"]) and np.array_equal(r2["q8"][blk:], b["q8"])
+    assert np.array_equal(u(r2["snap"]), u(a["state"])), "rollback state != 1-token state"
+    assert np.array_equal(u(r2["state"]), u(b["state"]))
+    assert np.array_equal(u(r2["hsnap"]), u(a["hist"])) and np.array_equal(u(r2["hist"]), u(b["hist"]))
+
+
+def test_reference_surface_entry_points(orc, rmi):
+    """fused_gdn_conv_l2 + beta_gate + fused_gdn_step_norm_silu_q8 (the reference's 3-launch chain) == layer call."""
+    inp = make_inputs(orc, seed=500)
+    qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma = inp
+    ref = run_layer(rmi, qkvz[:QKVZ], ab[:2 * H_V], conv_w, hist, state, dt, ssm_a, gamma, ntok=1)
+    dh, dq = dev(hist), dev(qkvz[:QKVZ])
+    rmi.fused_gdn_conv_l2(dh, dq, dev(conv_w), dq, CH, 2 * H_K, EPS)
+    dab, gg = dev(ab[:2 * H_V]), empty(H_V)
+    rmi.beta_gate(dab, dev(dt), dev(ssm_a), gg, H_V)
+    st, y, q8 = dev(state), empty(H_V * S), empty(H_V * S // 32 * 36, "uint8")
+    rmi.fused_gdn_step_norm_silu_q8(st, dq, dq[H_K * S:], dq[2 * H_K * S:], gg, dab, dq[CH:], dev(gamma), EPS, y, q8,
+                                    H_K, H_V)
+    assert np.array_equal(host(dq)[:CH].view(np.uint32), ref["conv"][:CH].view(np.uint32))
+    assert np.array_equal(host(dh), ref["hist"])
+    # the prepared-gate path computes exp(gate) from a stored logit: same math, last-bit differences allowed
+    assert_close_rel(host(y), ref["y"], rtol=1e-5, atol_frac=1e-6, what="step y")
+    assert np.abs(host(st) - ref["state"]).max() < 1e-5
