@@ -99,6 +99,9 @@ int rmi_rms_quant_apply(const float* x, const float* w, const float* partials, v
  * Replaces rms_norm_out_kernel (qw:658-672) fused with row_sum_partials_kernel (qw:616-623). */
 int rmi_rms_norm_out(const float* x, const float* w, const float* partials, float* out, float* out_partials, int cols,
                      float eps, int ncols, void* stream);
+/* the same with column c of out at out + c * out_stride (the draft's [enorm(emb) | hnorm(h)] concat, qw:1327-1332) */
+int rmi_rms_norm_out_strided(const float* x, const float* w, const float* partials, float* out, int out_stride,
+                             float* out_partials, int cols, float eps, int ncols, void* stream);
 /* partials of x.  Replaces row_sum_partials_kernel (qw:616-623). */
 int rmi_row_sum_partials(const float* x, float* partials, int n, int ncols, void* stream);
 /* x += o, then partials of x.  Replaces add_partials_1024_kernel (qw:602-614). */

@@ -1,0 +1,86 @@
+/*
+ * rapier_mi_engine.h - the decode engine around the kernels of rapier_mi.h: a qwen35 hybrid (Gated-DeltaNet layers,
+ * GQA every 4th layer, one nextn draft block) held in HBM, the single-token greedy forward and the exact-verify MTP
+ * round, each captured as one hipGraph.
+ *
+ * Reference: src/qwythos.cpp - Engine / alloc_primary / load_model (152-281, 1838-2134), forward_token (1773-1824),
+ * draft_predict (1316-1406), launch_token_verify (1412-1618), the MTP accept / rollback loop (3182-3241, serve
+ * 2761-2808) and capture_graph (1757-1771).  Weights are seeded random-init Q6_K of the qwen35 shapes (there is no
+ * GGUF reader); everything else follows the reference's engine.
+ *
+ * Unlike the kernel entry points, the engine owns its memory: rmi_engine_create allocates the model, the caches and
+ * the round buffers once; generation allocates nothing on the device.
+ */
+#ifndef RAPIER_MI_ENGINE_H
+#define RAPIER_MI_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "rapier_mi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct rmi_model_config {
+    int n_embd;        /* 4096 (kEmb, qw:34) */
+    int n_ff;          /* 12288 (kFF) */
+    int n_vocab;       /* 248320 (kVocab) */
+    int n_layer;       /* 32 trunk layers; layer il is attention when (il + 1) % 4 == 0 (qw:2016) */
+    int ssm_h_k;       /* 16 GDN key heads (kHk) */
+    int ssm_h_v;       /* 32 GDN value heads (kHv); state size 128 (kS) */
+    int n_head;        /* 16 attention heads (kHeads) */
+    int n_kv;          /* 4 KV heads (kKv) */
+    int head_dim;      /* 256 (kHd) */
+    int n_rot;         /* 64 rotary dims (kRot) */
+    float rope_theta;  /* 1e7 */
+    float eps;         /* 1e-6 */
+} rmi_model_config;
+
+typedef struct rmi_engine rmi_engine;
+
+typedef struct rmi_engine_info_t {
+    size_t trunk_weight_bytes;   /* all trunk matrices */
+    size_t lm_head_bytes;
+    size_t draft_block_bytes;    /* eh_proj + the draft attention / FFN block */
+    size_t round_weight_bytes;   /* one verify round: trunk + lm_head + draft block + lm_head */
+    size_t token_weight_bytes;   /* one greedy token: trunk + lm_head */
+    size_t kv_bytes_per_pos;     /* fp16 K+V of the trunk attention layers per position */
+    int gdn_layers, attn_layers, max_ctx, attn_chunk;
+} rmi_engine_info_t;
+
+enum { RMI_GEN_GREEDY = 0, RMI_GEN_MTP = 1, RMI_GEN_MTP_FORCED = 2 };
+
+typedef struct rmi_gen_request {
+    int mode;                 /* RMI_GEN_* */
+    int n_gen;                /* tokens to generate after the current token */
+    int use_graph;            /* 1: one hipGraph launch per token / round */
+    const int* ref_tokens;    /* forced mode: the reference stream, ref_tokens[i] at position ref_base + i */
+    int ref_base, ref_len;
+    const uint8_t* pattern;   /* forced mode: round r accepts iff pattern[r % pattern_len] */
+    int pattern_len;
+} rmi_gen_request;
+
+typedef struct rmi_gen_stats {
+    int tokens, emitted, rounds, accepted;
+    float gpu_ms;             /* device time of the whole generation (events on the engine stream) */
+} rmi_gen_stats;
+
+rmi_model_config rmi_qwen35_9b_config(void);
+int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int max_ctx, void* stream, rmi_engine** out);
+int rmi_engine_destroy(rmi_engine* e);
+int rmi_engine_info(const rmi_engine* e, rmi_engine_info_t* info);
+/* prompt of n host tokens from position 0; *first_out = the greedy token after it (the current token) */
+int rmi_engine_prefill(rmi_engine* e, const int* tokens, int n, int* first_out);
+/* seeded synthetic state for positions [0, n_ctx - 1), then one forward of last_token at n_ctx - 1 */
+int rmi_engine_synth_context(rmi_engine* e, int n_ctx, uint64_t seed, int last_token, int* first_out);
+int rmi_engine_save_state(rmi_engine* e);
+int rmi_engine_restore_state(rmi_engine* e, int pos, int cur_token);
+int rmi_engine_state(rmi_engine* e, int* pos, int* cur_token);
+int rmi_engine_generate(rmi_engine* e, const rmi_gen_request* req, int* out_tokens, rmi_gen_stats* stats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,771 @@
+// engine.hip - the qwen35 hybrid decode engine around the kernels: a seeded random-init model in HBM, the
+// single-token forward (non-MTP greedy) and the exact-verify MTP round, each captured as one hipGraph.
+//
+// Reference: src/qwythos.cpp - Engine (152-281), load_model's concatenations (2082-2087, 2125-2128), forward_gdn /
+// forward_attn / ffn (1011-1226), launch_token_gpu (1228-1238), draft_predict (1316-1406), launch_token_verify
+// (1412-1618), the accept / rollback loop (3182-3241) and capture_graph (1757-1771).
+//
+// What differs from the reference, by design:
+//   * every per-round decision lives on the device: token ids, positions, the accept flag, the GDN rollback
+//     selector, the emitted-token ring.  One verify round is one hipGraph launch with no host round trip.
+//   * the verify pass uses the fused residual epilogue at ncols = 2 (the reference runs mm_q2 then add_partials);
+//     each column of every kernel is bitwise the single-column result, so the MTP stream equals the greedy stream.
+//   * GDN rollback flips a selector instead of copying 24 x (2 MiB + 96 KiB) snapshots.
+//   * the draft always runs two columns after a verify: column 0 = (c0, hidden of verify column 0) at pos + 1 and
+//     column 1 = (c1, hidden of column 1) at pos + 2.  On reject column 0 is the reference's corrected draft step; on
+//     accept column 0 is its KV-fill step and column 1 its next-candidate step.  Both weight passes become one.
+//   * the KV cache is fp16; the token embedding is dequantized on the device.
+#include "rmi_common.h"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/rapier_mi_engine.h"
+
+namespace rmi {
+namespace {
+
+constexpr int kS = 128;          // GDN state size
+constexpr int kRingCap = 1 << 16;
+
+#define RMI_TRY(expr)                         \
+    do {                                      \
+        const int rc_ = (expr);               \
+        if (rc_ != RMI_OK) return rc_;        \
+    } while (0)
+
+int hip_check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return RMI_OK;
+    char buf[512];
+    std::snprintf(buf, sizeof buf, "%s: %s", what, hipGetErrorString(e));
+    return fail(RMI_ERR_LAUNCH, buf);
+}
+#define HIP_TRY(expr) RMI_TRY(hip_check((expr), #expr))
+
+size_t q6_bytes(int n_out, int n_in) { return static_cast<size_t>(n_out) * (n_in / 256) * kQ6KBytes; }
+size_t q81_bytes(int n) { return static_cast<size_t>(n / 32) * kQ8_1Bytes; }
+
+struct Mat {
+    uint8_t* w = nullptr;
+    int n_in = 0, n_out = 0;
+};
+
+struct Layer {
+    bool gdn = true;
+    float* attn_norm = nullptr;
+    float* post_norm = nullptr;
+    Mat in_proj;     // GDN: qkv|z|beta|alpha ; attention: wq|wk|wv
+    Mat out_proj;    // GDN: ssm_out ; attention: wo
+    Mat upgate, down;
+    // GDN
+    float *conv_w = nullptr, *dt = nullptr, *ssm_a = nullptr, *ssm_norm = nullptr;
+    float* state[2] = {nullptr, nullptr};
+    float* hist[2] = {nullptr, nullptr};
+    // attention
+    float *qn = nullptr, *kn = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;
+};
+
+// device-side round state: one int block
+enum Slot {
+    kPos = 0,      // position of column 0 (the current token)
+    kTok0, kTok1,  // verify / forward tokens: current token, draft candidate
+    kV0, kV1,      // argmax of the verify (or forward) columns
+    kD0, kD1,      // draft input tokens
+    kDPos,         // draft position of column 0
+    kC0, kC1,      // argmax of the draft columns
+    kSel,          // GDN rollback selector
+    kAccept,       // accept flag of the last verify
+    kNOut,         // tokens emitted into the ring
+    kRound,        // rounds run
+    kNAcc,         // accepted drafts
+    kMode,         // 0 natural draft, 1 forced by pattern
+    kPatLen,
+    kVocab,
+    kMaxPos,       // last usable position
+    kNumSlots
+};
+
+struct Engine {
+    rmi_model_config cfg{};
+    int max_ctx = 0, nsub = 1;
+    hipStream_t s = nullptr;
+    bool own_stream = false;
+    std::vector<void*> allocs;
+
+    Mat lm_head;
+    uint8_t* tok_embd = nullptr;
+    float* out_norm = nullptr;
+    std::vector<Layer> layers;
+    Layer draft;
+    Mat eh_proj;
+    float *enorm = nullptr, *hnorm = nullptr, *shnorm = nullptr;
+
+    // sizes
+    int qkvz_rows = 0, q3_rows = 0, gdn_v = 0, attn_q = 0, max_in = 0;
+
+    int* ints = nullptr;            // kNumSlots
+    int* ring = nullptr;            // emitted tokens
+    int* ref_tok = nullptr;         // forced-acceptance reference stream, indexed by position
+    uint8_t* pattern = nullptr;     // forced-acceptance pattern, indexed by round
+
+    // activations (2 columns)
+    float *x = nullptr, *part = nullptr, *proj = nullptr, *ug = nullptr, *y = nullptr, *logits = nullptr;
+    float *hsave = nullptr, *hpart = nullptr, *hzero = nullptr, *pzero = nullptr, *qbuf = nullptr;
+    float *ex = nullptr, *epart = nullptr, *eh = nullptr, *dx = nullptr, *dpart = nullptr;
+    uint8_t *q8a = nullptr, *q8f = nullptr, *q8y = nullptr;
+    void *attn_ws = nullptr, *argmax_ws = nullptr;
+    // saved GDN state and draft hidden for restore
+    std::vector<float*> saved_state, saved_hist;
+    float *saved_h = nullptr, *saved_hp = nullptr;
+
+    hipGraphExec_t g_single = nullptr, g_round = nullptr, g_draft1 = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+
+    ~Engine() {
+        if (g_single) (void) hipGraphExecDestroy(g_single);
+        if (g_round) (void) hipGraphExecDestroy(g_round);
+        if (g_draft1) (void) hipGraphExecDestroy(g_draft1);
+        if (ev0) (void) hipEventDestroy(ev0);
+        if (ev1) (void) hipEventDestroy(ev1);
+        for (void* p : allocs) (void) hipFree(p);
+        if (own_stream && s) (void) hipStreamDestroy(s);
+    }
+
+    template <typename T>
+    int alloc(T** p, size_t count) {
+        void* v = nullptr;
+        const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+        HIP_TRY(hipMalloc(&v, bytes));
+        allocs.push_back(v);
+        *p = static_cast<T*>(v);
+        return RMI_OK;
+    }
+};
+
+// ---- small device kernels of the round ----------------------------------------------------------------------------
+__global__ void fill_f32_kernel(float* p, size_t n, float v) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+__global__ void fill_i32_kernel(int* p, size_t n, int v) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// after a single-token forward: emit the argmax, feed it back, advance one position
+__global__ void advance_single_kernel(int* st, int* ring) {
+    const int id = st[kV0];
+    const int n = st[kNOut];
+    if (n < kRingCap) ring[n] = id;
+    st[kNOut] = n + 1;
+    st[kTok0] = id;
+    st[kPos] = min(st[kPos] + 1, st[kMaxPos]);
+}
+
+// after the verify: accept c0 == candidate, roll back the GDN state on reject, emit, set up the draft columns
+__global__ void accept_kernel(int* st, int* ring) {
+    const int c0 = st[kV0], c1 = st[kV1];
+    const int accept = c0 == st[kTok1];
+    int n = st[kNOut];
+    if (n < kRingCap) ring[n] = c0;
+    ++n;
+    if (accept) {
+        if (n < kRingCap) ring[n] = c1;
+        ++n;
+        st[kNAcc] += 1;
+    } else {
+        st[kSel] ^= 1;   // the state after column 0 becomes the live one
+    }
+    st[kNOut] = n;
+    st[kAccept] = accept;
+    st[kD0] = c0;
+    st[kD1] = c1;
+    st[kDPos] = st[kPos] + 1;
+}
+
+// after the draft: pick the candidate, advance (1 or 2 positions), apply the forced-acceptance override
+__global__ void finalize_kernel(int* st, const int* ref_tok, const uint8_t* pattern) {
+    const int accept = st[kAccept];
+    const int pos = min(st[kPos] + (accept ? 2 : 1), st[kMaxPos]);
+    const int cur = accept ? st[kV1] : st[kV0];
+    int cand = accept ? st[kC1] : st[kC0];
+    const int round = st[kRound];
+    if (st[kMode] == 1 && st[kPatLen] > 0) {
+        // the candidate for position pos + 1: the reference stream's token (accepted) or another one (rejected)
+        const int truth = ref_tok[min(pos + 1, st[kMaxPos])];
+        cand = pattern[(round + 1) % st[kPatLen]] ? truth : (truth + 1) % st[kVocab];   // for the next round
+    }
+    st[kPos] = pos;
+    st[kTok0] = cur;
+    st[kTok1] = cand;
+    st[kRound] = round + 1;
+}
+
+// initial draft candidate (1-column draft with head): cand = draft argmax, or the forced one
+__global__ void first_candidate_kernel(int* st, const int* ref_tok, const uint8_t* pattern) {
+    int cand = st[kC0];
+    if (st[kMode] == 1 && st[kPatLen] > 0) {
+        const int truth = ref_tok[min(st[kPos] + 1, st[kMaxPos])];
+        cand = pattern[0] ? truth : (truth + 1) % st[kVocab];
+    }
+    st[kTok1] = cand;
+}
+
+unsigned grid1(size_t n) { return static_cast<unsigned>((n + 255) / 256); }
+
+// ---- model construction ------------------------------------------------------------------------------------------
+uint64_t mix_seed(uint64_t seed, int layer, int what) {
+    uint64_t z = seed ^ (0x9E3779B97F4A7C15ULL * static_cast<uint64_t>(layer + 7)) ^
+                 (0xC2B2AE3D27D4EB4FULL * static_cast<uint64_t>(what + 1));
+    z = (z ^ (z >> 31)) * 0xBF58476D1CE4E5B9ULL;
+    return z ^ (z >> 29);
+}
+
+int make_mat(Engine& e, Mat& m, int n_out, int n_in, uint64_t seed) {
+    m.n_in = n_in;
+    m.n_out = n_out;
+    RMI_TRY(e.alloc(&m.w, q6_bytes(n_out, n_in)));
+    return rmi_gen_q6_k(m.w, static_cast<size_t>(n_out) * (n_in / 256), seed, 1e-3f, e.s);
+}
+
+int make_vec(Engine& e, float** p, size_t n, uint64_t seed, float mean, float std) {
+    RMI_TRY(e.alloc(p, n));
+    if (std == 0.0f) {
+        hipLaunchKernelGGL(fill_f32_kernel, dim3(grid1(n)), dim3(256), 0, e.s, *p, n, mean);
+        return launch_status("fill");
+    }
+    return rmi_gen_normal(*p, n, seed, mean, std, e.s);
+}
+
+int zero_f32(Engine& e, float* p, size_t n) {
+    hipLaunchKernelGGL(fill_f32_kernel, dim3(grid1(n)), dim3(256), 0, e.s, p, n, 0.0f);
+    return launch_status("fill");
+}
+
+int make_attn(Engine& e, Layer& L, int li, uint64_t seed) {
+    const auto& c = e.cfg;
+    L.gdn = false;
+    RMI_TRY(make_vec(e, &L.attn_norm, c.n_embd, mix_seed(seed, li, 1), 1.0f, 0.1f));
+    RMI_TRY(make_vec(e, &L.post_norm, c.n_embd, mix_seed(seed, li, 2), 1.0f, 0.1f));
+    RMI_TRY(make_mat(e, L.in_proj, e.q3_rows, c.n_embd, mix_seed(seed, li, 3)));
+    RMI_TRY(make_mat(e, L.out_proj, c.n_embd, e.attn_q, mix_seed(seed, li, 4)));
+    RMI_TRY(make_mat(e, L.upgate, 2 * c.n_ff, c.n_embd, mix_seed(seed, li, 5)));
+    RMI_TRY(make_mat(e, L.down, c.n_embd, c.n_ff, mix_seed(seed, li, 6)));
+    RMI_TRY(make_vec(e, &L.qn, c.head_dim, mix_seed(seed, li, 7), 1.0f, 0.1f));
+    RMI_TRY(make_vec(e, &L.kn, c.head_dim, mix_seed(seed, li, 8), 1.0f, 0.1f));
+    const size_t kv = static_cast<size_t>(e.max_ctx) * c.n_kv * c.head_dim;
+    RMI_TRY(e.alloc(&L.kc, kv));
+    RMI_TRY(e.alloc(&L.vc, kv));
+    HIP_TRY(hipMemsetAsync(L.kc, 0, kv * 2, e.s));
+    HIP_TRY(hipMemsetAsync(L.vc, 0, kv * 2, e.s));
+    return RMI_OK;
+}
+
+int make_gdn(Engine& e, Layer& L, int li, uint64_t seed) {
+    const auto& c = e.cfg;
+    L.gdn = true;
+    RMI_TRY(make_vec(e, &L.attn_norm, c.n_embd, mix_seed(seed, li, 1), 1.0f, 0.1f));
+    RMI_TRY(make_vec(e, &L.post_norm, c.n_embd, mix_seed(seed, li, 2), 1.0f, 0.1f));
+    RMI_TRY(make_mat(e, L.in_proj, e.qkvz_rows, c.n_embd, mix_seed(seed, li, 3)));
+    RMI_TRY(make_mat(e, L.out_proj, c.n_embd, e.gdn_v, mix_seed(seed, li, 4)));
+    RMI_TRY(make_mat(e, L.upgate, 2 * c.n_ff, c.n_embd, mix_seed(seed, li, 5)));
+    RMI_TRY(make_mat(e, L.down, c.n_embd, c.n_ff, mix_seed(seed, li, 6)));
+    const int ch = 2 * c.ssm_h_k * kS + c.ssm_h_v * kS;
+    RMI_TRY(make_vec(e, &L.conv_w, static_cast<size_t>(4) * ch, mix_seed(seed, li, 7), 0.0f, 0.5f));
+    RMI_TRY(make_vec(e, &L.dt, c.ssm_h_v, 0, 0.0f, 0.0f));
+    RMI_TRY(make_vec(e, &L.ssm_a, c.ssm_h_v, mix_seed(seed, li, 8), 0.0f, 0.5f));
+    RMI_TRY(make_vec(e, &L.ssm_norm, kS, mix_seed(seed, li, 9), 1.0f, 0.1f));
+    const size_t st = static_cast<size_t>(kS) * c.ssm_h_v * kS;
+    for (int b = 0; b < 2; ++b) {
+        RMI_TRY(e.alloc(&L.state[b], st));
+        RMI_TRY(e.alloc(&L.hist[b], static_cast<size_t>(3) * ch));
+        RMI_TRY(zero_f32(e, L.state[b], st));
+        RMI_TRY(zero_f32(e, L.hist[b], static_cast<size_t>(3) * ch));
+    }
+    return RMI_OK;
+}
+
+__global__ void neg_exp_kernel(float* p, int n) {   // ssm_a = -exp(N(0, 0.5^2))
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = -expf(p[i]);
+}
+
+// ---- the forward building blocks (ncols = 1 or 2; every kernel is column-invariant) --------------------------------
+int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
+    const auto& c = e.cfg;
+    RMI_TRY(rmi_rms_quant_apply(x, L.post_norm, part, e.q8a, c.n_embd, c.eps, nc, e.s));
+    RMI_TRY(rmi_native_q6_k_mmvq(L.upgate.w, e.q8a, e.ug, c.n_embd, 2 * c.n_ff, nc, e.s));
+    RMI_TRY(rmi_swiglu_quant(e.ug, e.ug + c.n_ff, e.q8f, c.n_ff, nc, 2 * c.n_ff, e.s));
+    return rmi_native_q6_k_mmvq_res_n(L.down.w, e.q8f, x, x, part, c.n_ff, c.n_embd, nc, e.s);
+}
+
+int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc) {
+    const auto& c = e.cfg;
+    RMI_TRY(rmi_rms_quant_apply(x, L.attn_norm, part, e.q8a, c.n_embd, c.eps, nc, e.s));
+    RMI_TRY(rmi_native_q6_k_mmvq(L.in_proj.w, e.q8a, e.proj, c.n_embd, e.q3_rows, nc, e.s));
+    RMI_TRY(rmi_attn_prep(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, e.qbuf, c.n_head, c.n_kv, c.head_dim,
+                          c.n_rot, c.rope_theta, c.eps, nc, e.max_ctx, e.s));
+    RMI_TRY(rmi_gqa_flash_decode(e.qbuf, L.kc, L.vc, pos, e.proj, e.q3_rows, nullptr, 0, e.q8y,
+                                 static_cast<int>(q81_bytes(e.attn_q)), e.attn_ws, c.n_head, c.n_kv, c.head_dim, nc,
+                                 e.max_ctx, e.nsub, 1.0f / sqrtf(static_cast<float>(c.head_dim)), e.s));
+    RMI_TRY(rmi_native_q6_k_mmvq_res_n(L.out_proj.w, e.q8y, x, x, part, e.attn_q, c.n_embd, nc, e.s));
+    return ffn(e, L, x, part, nc);
+}
+
+int gdn_block(Engine& e, Layer& L, int nc) {
+    const auto& c = e.cfg;
+    RMI_TRY(rmi_rms_quant_apply(e.x, L.attn_norm, e.part, e.q8a, c.n_embd, c.eps, nc, e.s));
+    RMI_TRY(rmi_native_q6_k_mmvq(L.in_proj.w, e.q8a, e.proj, c.n_embd, e.qkvz_rows, nc, e.s));
+    const int qkvz = 2 * c.ssm_h_k * kS + 2 * c.ssm_h_v * kS;
+    RMI_TRY(rmi_gdn_layer_tokens(L.state[0], L.state[1], L.hist[0], L.hist[1], e.ints + kSel, e.proj, e.qkvz_rows,
+                                 e.proj + qkvz, e.qkvz_rows, L.conv_w, L.dt, L.ssm_a, L.ssm_norm, c.eps, e.y, e.gdn_v,
+                                 e.q8y, static_cast<int>(q81_bytes(e.gdn_v)), c.ssm_h_k, c.ssm_h_v, nc, e.s));
+    RMI_TRY(rmi_native_q6_k_mmvq_res_n(L.out_proj.w, e.q8y, e.x, e.x, e.part, e.gdn_v, c.n_embd, nc, e.s));
+    return ffn(e, L, e.x, e.part, nc);
+}
+
+// trunk for nc columns: tokens ints[kTok0 + c] at positions ints[kPos] + c.  Leaves argmax in ints[kV0 + c] and the
+// final-normed hidden in hsave/hpart (the draft's input, qw:1235-1237).
+int trunk(Engine& e, int nc) {
+    const auto& c = e.cfg;
+    RMI_TRY(rmi_embed_q6_k(e.tok_embd, e.ints + kTok0, e.x, e.part, c.n_embd, c.n_vocab, nc, e.s));
+    for (auto& L : e.layers) {
+        if (L.gdn) RMI_TRY(gdn_block(e, L, nc));
+        else RMI_TRY(attn_block(e, L, e.x, e.part, e.ints + kPos, nc));
+    }
+    RMI_TRY(rmi_rms_quant_apply(e.x, e.out_norm, e.part, e.q8a, c.n_embd, c.eps, nc, e.s));
+    RMI_TRY(rmi_native_q6_k_mmvq(e.lm_head.w, e.q8a, e.logits, c.n_embd, c.n_vocab, nc, e.s));
+    RMI_TRY(rmi_argmax(e.logits, c.n_vocab, nc, c.n_vocab, e.ints + kV0, e.argmax_ws, e.s));
+    return rmi_rms_norm_out(e.x, e.out_norm, e.part, e.hsave, e.hpart, c.n_embd, c.eps, nc, e.s);
+}
+
+// draft (nextn) block for nc columns: tokens ints[kD0 + c] at positions ints[kDPos] + c, previous hidden h / hp.
+// eh = [enorm(emb) | hnorm(h)] per column (embedding first, qw:1327-1332).  Argmax to ints[kC0 + c] when with_head.
+int draft_block(Engine& e, const float* h, const float* hp, int nc, bool with_head) {
+    const auto& c = e.cfg;
+    RMI_TRY(rmi_embed_q6_k(e.tok_embd, e.ints + kD0, e.ex, e.epart, c.n_embd, c.n_vocab, nc, e.s));
+    RMI_TRY(rmi_rms_norm_out_strided(e.ex, e.enorm, e.epart, e.eh, 2 * c.n_embd, nullptr, c.n_embd, c.eps, nc, e.s));
+    RMI_TRY(rmi_rms_norm_out_strided(h, e.hnorm, hp, e.eh + c.n_embd, 2 * c.n_embd, nullptr, c.n_embd, c.eps, nc,
+                                     e.s));
+    RMI_TRY(rmi_native_quantize_q8_1(e.eh, e.q8f, 2 * c.n_embd, nc, e.s));
+    RMI_TRY(rmi_native_q6_k_mmvq(e.eh_proj.w, e.q8f, e.dx, 2 * c.n_embd, c.n_embd, nc, e.s));
+    RMI_TRY(rmi_row_sum_partials(e.dx, e.dpart, c.n_embd, nc, e.s));
+    RMI_TRY(attn_block(e, e.draft, e.dx, e.dpart, e.ints + kDPos, nc));
+    if (!with_head) return RMI_OK;
+    RMI_TRY(rmi_rms_quant_apply(e.dx, e.shnorm, e.dpart, e.q8a, c.n_embd, c.eps, nc, e.s));
+    RMI_TRY(rmi_native_q6_k_mmvq(e.lm_head.w, e.q8a, e.logits, c.n_embd, c.n_vocab, nc, e.s));
+    return rmi_argmax(e.logits, c.n_vocab, nc, c.n_vocab, e.ints + kC0, e.argmax_ws, e.s);
+}
+
+int single_step(Engine& e) {
+    RMI_TRY(trunk(e, 1));
+    hipLaunchKernelGGL(advance_single_kernel, dim3(1), dim3(1), 0, e.s, e.ints, e.ring);
+    return launch_status("advance_single");
+}
+
+int verify_round(Engine& e) {
+    RMI_TRY(trunk(e, 2));
+    hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(1), 0, e.s, e.ints, e.ring);
+    RMI_TRY(launch_status("accept"));
+    RMI_TRY(draft_block(e, e.hsave, e.hpart, 2, true));
+    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, e.s, e.ints, e.ref_tok, e.pattern);
+    return launch_status("finalize");
+}
+
+// the first candidate: 1-column draft with head of (current token, hidden of the last forward) at the current position
+int first_draft(Engine& e) {
+    HIP_TRY(hipMemcpyAsync(e.ints + kD0, e.ints + kTok0, sizeof(int), hipMemcpyDeviceToDevice, e.s));
+    HIP_TRY(hipMemcpyAsync(e.ints + kDPos, e.ints + kPos, sizeof(int), hipMemcpyDeviceToDevice, e.s));
+    RMI_TRY(draft_block(e, e.hsave, e.hpart, 1, true));
+    hipLaunchKernelGGL(first_candidate_kernel, dim3(1), dim3(1), 0, e.s, e.ints, e.ref_tok, e.pattern);
+    return launch_status("first_candidate");
+}
+
+template <typename F>
+int capture(Engine& e, hipGraphExec_t* out, F&& body) {
+    if (*out) return RMI_OK;
+    HIP_TRY(hipStreamBeginCapture(e.s, hipStreamCaptureModeThreadLocal));
+    const int rc = body();
+    hipGraph_t g = nullptr;
+    const hipError_t ec = hipStreamEndCapture(e.s, &g);
+    if (rc != RMI_OK) {
+        if (g) (void) hipGraphDestroy(g);
+        return rc;
+    }
+    RMI_TRY(hip_check(ec, "hipStreamEndCapture"));
+    const hipError_t ei = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void) hipGraphDestroy(g);
+    return hip_check(ei, "hipGraphInstantiate");
+}
+
+int set_int(Engine& e, int slot, int v) {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(256), 0, e.s, e.ints + slot, static_cast<size_t>(1), v);
+    return launch_status("set_int");
+}
+
+int get_ints(Engine& e, int* host, int n) {
+    HIP_TRY(hipMemcpyAsync(host, e.ints, sizeof(int) * n, hipMemcpyDeviceToHost, e.s));
+    HIP_TRY(hipStreamSynchronize(e.s));
+    return RMI_OK;
+}
+
+}  // namespace
+}  // namespace rmi
+
+using namespace rmi;
+
+struct rmi_engine {
+    Engine e;
+};
+
+extern "C" rmi_model_config rmi_qwen35_9b_config(void) {
+    rmi_model_config c{};
+    c.n_embd = 4096;
+    c.n_ff = 12288;
+    c.n_vocab = 248320;
+    c.n_layer = 32;
+    c.ssm_h_k = 16;
+    c.ssm_h_v = 32;
+    c.n_head = 16;
+    c.n_kv = 4;
+    c.head_dim = 256;
+    c.n_rot = 64;
+    c.rope_theta = 1e7f;
+    c.eps = 1e-6f;
+    return c;
+}
+
+extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int max_ctx, void* stream,
+                                 rmi_engine** out) {
+    if (!cfg || !out) return fail(RMI_ERR_POINTER, "rmi_engine_create: null argument");
+    const rmi_model_config& c = *cfg;
+    if (c.n_embd <= 0 || c.n_embd % 256 || c.n_ff % 256 || c.n_ff <= 0 || c.n_vocab <= 0 || c.n_layer <= 0 ||
+        c.ssm_h_k <= 0 || c.ssm_h_v % c.ssm_h_k || c.head_dim != 256 || c.n_head % c.n_kv || c.n_head <= 0 ||
+        (c.n_head / c.n_kv) * 2 > 16 || (c.ssm_h_v * kS) % 256 || ((2 * c.ssm_h_k + c.ssm_h_v) * kS) % 256 ||
+        (c.n_head * c.head_dim) % 256 || max_ctx < 64)
+        return fail(RMI_ERR_SHAPE, "rmi_engine_create: unsupported model shape");
+    std::unique_ptr<rmi_engine> h(new (std::nothrow) rmi_engine());
+    if (!h) return fail(RMI_ERR_STATE, "rmi_engine_create: out of host memory");
+    Engine& e = h->e;
+    e.cfg = c;
+    e.max_ctx = (max_ctx + 63) / 64 * 64;
+    e.nsub = std::max(1, std::min(8, e.max_ctx / 16384));
+    if (stream) {
+        e.s = static_cast<hipStream_t>(stream);
+    } else {
+        HIP_TRY(hipStreamCreateWithFlags(&e.s, hipStreamNonBlocking));
+        e.own_stream = true;
+    }
+    e.qkvz_rows = 2 * c.ssm_h_k * kS + 2 * c.ssm_h_v * kS + 2 * c.ssm_h_v;   // q|k|v|z|beta|alpha
+    e.gdn_v = c.ssm_h_v * kS;
+    e.attn_q = c.n_head * c.head_dim;
+    e.q3_rows = 2 * e.attn_q + 2 * c.n_kv * c.head_dim;                     // 16 x (q|gate) | k | v
+    e.max_in = std::max({c.n_ff, 2 * c.n_embd, e.gdn_v, e.attn_q});
+
+    // model (all Q6_K matrices random-init as in the benchmark configs)
+    RMI_TRY(e.alloc(&e.tok_embd, q6_bytes(c.n_vocab, c.n_embd)));
+    RMI_TRY(rmi_gen_q6_k(e.tok_embd, static_cast<size_t>(c.n_vocab) * (c.n_embd / 256), mix_seed(seed, -1, 1), 1e-3f,
+                         e.s));
+    RMI_TRY(make_mat(e, e.lm_head, c.n_vocab, c.n_embd, mix_seed(seed, -1, 2)));
+    RMI_TRY(make_vec(e, &e.out_norm, c.n_embd, mix_seed(seed, -1, 3), 1.0f, 0.1f));
+    e.layers.resize(c.n_layer);
+    for (int il = 0; il < c.n_layer; ++il) {
+        const bool gdn = ((il + 1) % 4) != 0;   // qw:2016
+        RMI_TRY(gdn ? make_gdn(e, e.layers[il], il, seed) : make_attn(e, e.layers[il], il, seed));
+        if (gdn) {
+            hipLaunchKernelGGL(neg_exp_kernel, dim3(grid1(c.ssm_h_v)), dim3(256), 0, e.s, e.layers[il].ssm_a, c.ssm_h_v);
+            RMI_TRY(launch_status("ssm_a"));
+        }
+    }
+    RMI_TRY(make_attn(e, e.draft, c.n_layer, seed));
+    RMI_TRY(make_mat(e, e.eh_proj, c.n_embd, 2 * c.n_embd, mix_seed(seed, c.n_layer, 10)));
+    RMI_TRY(make_vec(e, &e.enorm, c.n_embd, mix_seed(seed, c.n_layer, 11), 1.0f, 0.1f));
+    RMI_TRY(make_vec(e, &e.hnorm, c.n_embd, mix_seed(seed, c.n_layer, 12), 1.0f, 0.1f));
+    RMI_TRY(make_vec(e, &e.shnorm, c.n_embd, mix_seed(seed, c.n_layer, 13), 1.0f, 0.1f));
+
+    // round state and activations (two columns)
+    RMI_TRY(e.alloc(&e.ints, 64));
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(256), 0, e.s, e.ints, static_cast<size_t>(64), 0);
+    RMI_TRY(launch_status("fill"));
+    RMI_TRY(set_int(e, kVocab, c.n_vocab));
+    RMI_TRY(set_int(e, kMaxPos, e.max_ctx - 1));
+    RMI_TRY(e.alloc(&e.ring, kRingCap));
+    RMI_TRY(e.alloc(&e.ref_tok, static_cast<size_t>(e.max_ctx) + 1));
+    RMI_TRY(e.alloc(&e.pattern, 4096));
+    const size_t np = c.n_embd / 4;
+    RMI_TRY(e.alloc(&e.x, 2 * static_cast<size_t>(c.n_embd)));
+    RMI_TRY(e.alloc(&e.part, 2 * np));
+    RMI_TRY(e.alloc(&e.proj, 2 * static_cast<size_t>(std::max(e.qkvz_rows, e.q3_rows))));
+    RMI_TRY(e.alloc(&e.ug, 4 * static_cast<size_t>(c.n_ff)));
+    RMI_TRY(e.alloc(&e.y, 2 * static_cast<size_t>(std::max(e.gdn_v, e.attn_q))));
+    RMI_TRY(e.alloc(&e.logits, 2 * static_cast<size_t>(c.n_vocab)));
+    RMI_TRY(e.alloc(&e.hsave, 2 * static_cast<size_t>(c.n_embd)));
+    RMI_TRY(e.alloc(&e.hpart, 2 * np));
+    RMI_TRY(e.alloc(&e.hzero, static_cast<size_t>(c.n_embd)));
+    RMI_TRY(e.alloc(&e.pzero, np));
+    RMI_TRY(zero_f32(e, e.hzero, c.n_embd));
+    RMI_TRY(zero_f32(e, e.pzero, np));
+    RMI_TRY(e.alloc(&e.qbuf, 2 * static_cast<size_t>(e.attn_q)));
+    RMI_TRY(e.alloc(&e.ex, 2 * static_cast<size_t>(c.n_embd)));
+    RMI_TRY(e.alloc(&e.epart, 2 * np));
+    RMI_TRY(e.alloc(&e.eh, 4 * static_cast<size_t>(c.n_embd)));
+    RMI_TRY(e.alloc(&e.dx, 2 * static_cast<size_t>(c.n_embd)));
+    RMI_TRY(e.alloc(&e.dpart, 2 * np));
+    RMI_TRY(e.alloc(&e.q8a, 2 * q81_bytes(c.n_embd)));
+    RMI_TRY(e.alloc(&e.q8f, 2 * q81_bytes(e.max_in)));
+    RMI_TRY(e.alloc(&e.q8y, 2 * q81_bytes(std::max(e.gdn_v, e.attn_q))));
+    uint8_t* ws = nullptr;
+    RMI_TRY(e.alloc(&ws, rmi_gqa_workspace_bytes(e.max_ctx, c.n_kv, e.nsub)));
+    e.attn_ws = ws;
+    uint8_t* aw = nullptr;
+    RMI_TRY(e.alloc(&aw, rmi_argmax_workspace_bytes(2)));
+    e.argmax_ws = aw;
+    for (auto& L : e.layers) {
+        if (!L.gdn) continue;
+        float *s0 = nullptr, *h0 = nullptr;
+        RMI_TRY(e.alloc(&s0, static_cast<size_t>(kS) * c.ssm_h_v * kS));
+        RMI_TRY(e.alloc(&h0, static_cast<size_t>(3) * (2 * c.ssm_h_k + c.ssm_h_v) * kS));
+        e.saved_state.push_back(s0);
+        e.saved_hist.push_back(h0);
+    }
+    RMI_TRY(e.alloc(&e.saved_h, static_cast<size_t>(c.n_embd)));
+    RMI_TRY(e.alloc(&e.saved_hp, np));
+    HIP_TRY(hipEventCreate(&e.ev0));
+    HIP_TRY(hipEventCreate(&e.ev1));
+    HIP_TRY(hipStreamSynchronize(e.s));
+    *out = h.release();
+    return RMI_OK;
+}
+
+extern "C" int rmi_engine_destroy(rmi_engine* h) {
+    if (!h) return RMI_OK;
+    (void) hipStreamSynchronize(h->e.s);
+    delete h;
+    return RMI_OK;
+}
+
+extern "C" int rmi_engine_info(const rmi_engine* h, rmi_engine_info_t* info) {
+    if (!h || !info) return fail(RMI_ERR_POINTER, "rmi_engine_info: null argument");
+    const Engine& e = h->e;
+    const auto& c = e.cfg;
+    size_t trunk = 0;
+    for (const auto& L : e.layers)
+        trunk += q6_bytes(L.in_proj.n_out, L.in_proj.n_in) + q6_bytes(L.out_proj.n_out, L.out_proj.n_in) +
+                 q6_bytes(L.upgate.n_out, L.upgate.n_in) + q6_bytes(L.down.n_out, L.down.n_in);
+    const size_t head = q6_bytes(c.n_vocab, c.n_embd);
+    const size_t dblk = q6_bytes(e.eh_proj.n_out, e.eh_proj.n_in) + q6_bytes(e.draft.in_proj.n_out, e.draft.in_proj.n_in) +
+                        q6_bytes(e.draft.out_proj.n_out, e.draft.out_proj.n_in) +
+                        q6_bytes(e.draft.upgate.n_out, e.draft.upgate.n_in) + q6_bytes(e.draft.down.n_out, e.draft.down.n_in);
+    info->trunk_weight_bytes = trunk;
+    info->lm_head_bytes = head;
+    info->draft_block_bytes = dblk;
+    info->round_weight_bytes = trunk + head + dblk + head;
+    info->token_weight_bytes = trunk + head;
+    int n_attn = 0;
+    for (const auto& L : e.layers) n_attn += L.gdn ? 0 : 1;
+    info->kv_bytes_per_pos = static_cast<size_t>(n_attn) * 2 * c.n_kv * c.head_dim * 2;
+    info->gdn_layers = c.n_layer - n_attn;
+    info->attn_layers = n_attn;
+    info->max_ctx = e.max_ctx;
+    info->attn_chunk = 64 * e.nsub;
+    return RMI_OK;
+}
+
+// Fill the context [0, n_ctx - 1) with seeded synthetic state (fp16 KV N(0,1) for trunk and draft layers, GDN state
+// N(0, 0.05^2), conv history N(0, 0.5^2)), then run one real forward of `last_token` at position n_ctx - 1.
+extern "C" int rmi_engine_synth_context(rmi_engine* h, int n_ctx, uint64_t seed, int last_token, int* first_out) {
+    if (!h) return fail(RMI_ERR_POINTER, "rmi_engine_synth_context: null engine");
+    Engine& e = h->e;
+    const auto& c = e.cfg;
+    if (n_ctx < 1 || n_ctx >= e.max_ctx - 2 || last_token < 0 || last_token >= c.n_vocab)
+        return fail(RMI_ERR_STATE, "rmi_engine_synth_context: context does not fit");
+    const size_t kv = static_cast<size_t>(n_ctx - 1) * c.n_kv * c.head_dim;
+    int il = 0;
+    for (auto& L : e.layers) {
+        if (L.gdn) {
+            const size_t st = static_cast<size_t>(kS) * c.ssm_h_v * kS;
+            const size_t hs = static_cast<size_t>(3) * (2 * c.ssm_h_k + c.ssm_h_v) * kS;
+            RMI_TRY(rmi_gen_normal(L.state[0], st, mix_seed(seed, il, 20), 0.0f, 0.05f, e.s));
+            RMI_TRY(rmi_gen_normal(L.hist[0], hs, mix_seed(seed, il, 21), 0.0f, 0.5f, e.s));
+        } else if (kv) {
+            RMI_TRY(rmi_gen_normal_f16(L.kc, kv, mix_seed(seed, il, 22), 0.0f, 1.0f, e.s));
+            RMI_TRY(rmi_gen_normal_f16(L.vc, kv, mix_seed(seed, il, 23), 0.0f, 1.0f, e.s));
+        }
+        ++il;
+    }
+    if (kv) {
+        RMI_TRY(rmi_gen_normal_f16(e.draft.kc, kv + static_cast<size_t>(c.n_kv) * c.head_dim, mix_seed(seed, il, 22),
+                                   0.0f, 1.0f, e.s));
+        RMI_TRY(rmi_gen_normal_f16(e.draft.vc, kv + static_cast<size_t>(c.n_kv) * c.head_dim, mix_seed(seed, il, 23),
+                                   0.0f, 1.0f, e.s));
+    }
+    RMI_TRY(set_int(e, kSel, 0));
+    RMI_TRY(set_int(e, kPos, n_ctx - 1));
+    RMI_TRY(set_int(e, kTok0, last_token));
+    RMI_TRY(set_int(e, kNOut, 0));
+    RMI_TRY(single_step(e));
+    int st[kNumSlots];
+    RMI_TRY(get_ints(e, st, kNumSlots));
+    if (first_out) *first_out = st[kTok0];
+    return RMI_OK;
+}
+
+// Feed `tokens` one by one from position 0 (zero state), filling the draft's KV as the reference seeds it (slot 0 with a
+// zero hidden, qw:2956-2958) and every later slot with (token, previous final-normed hidden).  *first_out = the
+// greedy token after the prompt.
+extern "C" int rmi_engine_prefill(rmi_engine* h, const int* tokens, int n, int* first_out) {
+    if (!h || !tokens) return fail(RMI_ERR_POINTER, "rmi_engine_prefill: null argument");
+    Engine& e = h->e;
+    const auto& c = e.cfg;
+    if (n < 1 || n >= e.max_ctx - 2) return fail(RMI_ERR_STATE, "rmi_engine_prefill: context does not fit");
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= c.n_vocab) return fail(RMI_ERR_STATE, "rmi_engine_prefill: bad token id");
+    for (auto& L : e.layers)
+        if (L.gdn) {
+            for (int b = 0; b < 2; ++b) {
+                RMI_TRY(zero_f32(e, L.state[b], static_cast<size_t>(kS) * c.ssm_h_v * kS));
+                RMI_TRY(zero_f32(e, L.hist[b], static_cast<size_t>(3) * (2 * c.ssm_h_k + c.ssm_h_v) * kS));
+            }
+        }
+    RMI_TRY(set_int(e, kSel, 0));
+    RMI_TRY(set_int(e, kNOut, 0));
+    for (int i = 0; i < n; ++i) {
+        // draft KV slot i from (token i, hidden of position i - 1) - the zero hidden at slot 0
+        RMI_TRY(set_int(e, kD0, tokens[i]));
+        RMI_TRY(set_int(e, kDPos, i));
+        RMI_TRY(draft_block(e, i == 0 ? e.hzero : e.hsave, i == 0 ? e.pzero : e.hpart, 1, false));
+        RMI_TRY(set_int(e, kTok0, tokens[i]));
+        RMI_TRY(set_int(e, kPos, i));
+        RMI_TRY(single_step(e));
+    }
+    int st[kNumSlots];
+    RMI_TRY(get_ints(e, st, kNumSlots));
+    if (first_out) *first_out = st[kTok0];
+    return RMI_OK;
+}
+
+extern "C" int rmi_engine_save_state(rmi_engine* h) {
+    if (!h) return fail(RMI_ERR_POINTER, "null engine");
+    Engine& e = h->e;
+    const auto& c = e.cfg;
+    int st[kNumSlots];
+    RMI_TRY(get_ints(e, st, kNumSlots));
+    size_t k = 0;
+    for (auto& L : e.layers) {
+        if (!L.gdn) continue;
+        HIP_TRY(hipMemcpyAsync(e.saved_state[k], L.state[st[kSel]], sizeof(float) * kS * c.ssm_h_v * kS,
+                               hipMemcpyDeviceToDevice, e.s));
+        HIP_TRY(hipMemcpyAsync(e.saved_hist[k], L.hist[st[kSel]], sizeof(float) * 3 * (2 * c.ssm_h_k + c.ssm_h_v) * kS,
+                               hipMemcpyDeviceToDevice, e.s));
+        ++k;
+    }
+    HIP_TRY(hipMemcpyAsync(e.saved_h, e.hsave, sizeof(float) * c.n_embd, hipMemcpyDeviceToDevice, e.s));
+    HIP_TRY(hipMemcpyAsync(e.saved_hp, e.hpart, sizeof(float) * (c.n_embd / 4), hipMemcpyDeviceToDevice, e.s));
+    HIP_TRY(hipStreamSynchronize(e.s));
+    return RMI_OK;
+}
+
+// restore the GDN state saved by rmi_engine_save_state and the token / position / hidden it was taken with
+extern "C" int rmi_engine_restore_state(rmi_engine* h, int pos, int cur_token) {
+    if (!h) return fail(RMI_ERR_POINTER, "null engine");
+    Engine& e = h->e;
+    const auto& c = e.cfg;
+    size_t k = 0;
+    for (auto& L : e.layers) {
+        if (!L.gdn) continue;
+        HIP_TRY(hipMemcpyAsync(L.state[0], e.saved_state[k], sizeof(float) * kS * c.ssm_h_v * kS,
+                               hipMemcpyDeviceToDevice, e.s));
+        HIP_TRY(hipMemcpyAsync(L.hist[0], e.saved_hist[k], sizeof(float) * 3 * (2 * c.ssm_h_k + c.ssm_h_v) * kS,
+                               hipMemcpyDeviceToDevice, e.s));
+        ++k;
+    }
+    HIP_TRY(hipMemcpyAsync(e.hsave, e.saved_h, sizeof(float) * c.n_embd, hipMemcpyDeviceToDevice, e.s));
+    HIP_TRY(hipMemcpyAsync(e.hpart, e.saved_hp, sizeof(float) * (c.n_embd / 4), hipMemcpyDeviceToDevice, e.s));
+    RMI_TRY(set_int(e, kSel, 0));
+    RMI_TRY(set_int(e, kPos, pos));
+    RMI_TRY(set_int(e, kTok0, cur_token));
+    HIP_TRY(hipStreamSynchronize(e.s));
+    return RMI_OK;
+}
+
+extern "C" int rmi_engine_state(rmi_engine* h, int* pos, int* cur_token) {
+    if (!h) return fail(RMI_ERR_POINTER, "null engine");
+    int st[kNumSlots];
+    RMI_TRY(get_ints(h->e, st, kNumSlots));
+    if (pos) *pos = st[kPos];
+    if (cur_token) *cur_token = st[kTok0];
+    return RMI_OK;
+}
+
+// Generate n_gen tokens after the current token.  mode RMI_GEN_GREEDY: one forward per token (graph).  RMI_GEN_MTP:
+// draft + 2-column verify rounds (graph).  RMI_GEN_MTP_FORCED: as MTP, but each round's candidate is replaced by
+// ref_tokens[pos + 1 - ref_base] when pattern[round % pattern_len] is 1, and by another token when it is 0.
+// Hidden state for the first draft: the final-normed hidden of the last forward (prefill / synth / previous run).
+extern "C" int rmi_engine_generate(rmi_engine* h, const rmi_gen_request* req, int* out_tokens, rmi_gen_stats* stats) {
+    if (!h || !req || !out_tokens) return fail(RMI_ERR_POINTER, "rmi_engine_generate: null argument");
+    Engine& e = h->e;
+    const int n_gen = req->n_gen;
+    if (n_gen < 1 || n_gen >= kRingCap - 2) return fail(RMI_ERR_STATE, "rmi_engine_generate: bad n_gen");
+    int st[kNumSlots];
+    RMI_TRY(get_ints(e, st, kNumSlots));
+    if (st[kPos] + n_gen + 2 >= e.max_ctx) return fail(RMI_ERR_STATE, "context full");
+    const bool mtp = req->mode != RMI_GEN_GREEDY;
+    if (req->mode == RMI_GEN_MTP_FORCED) {
+        if (!req->ref_tokens || req->ref_len < 1 || !req->pattern || req->pattern_len < 1 || req->pattern_len > 4096)
+            return fail(RMI_ERR_STATE, "rmi_engine_generate: forced mode needs ref_tokens and a pattern");
+        // ref_tokens[i] is the token at position ref_base + i; lay it out by absolute position
+        std::vector<int> byp(static_cast<size_t>(e.max_ctx) + 1, 0);
+        for (int i = 0; i < req->ref_len; ++i) {
+            const int p = req->ref_base + i;
+            if (p >= 0 && p <= e.max_ctx) byp[p] = req->ref_tokens[i];
+        }
+        HIP_TRY(hipMemcpyAsync(e.ref_tok, byp.data(), sizeof(int) * byp.size(), hipMemcpyHostToDevice, e.s));
+        HIP_TRY(hipMemcpyAsync(e.pattern, req->pattern, req->pattern_len, hipMemcpyHostToDevice, e.s));
+        HIP_TRY(hipStreamSynchronize(e.s));
+    }
+    RMI_TRY(set_int(e, kMode, req->mode == RMI_GEN_MTP_FORCED ? 1 : 0));
+    RMI_TRY(set_int(e, kPatLen, req->mode == RMI_GEN_MTP_FORCED ? req->pattern_len : 0));
+    RMI_TRY(set_int(e, kNOut, 0));
+    RMI_TRY(set_int(e, kRound, 0));
+    RMI_TRY(set_int(e, kNAcc, 0));
+    const bool graph = req->use_graph != 0;
+    if (graph) {
+        if (mtp) RMI_TRY(capture(e, &e.g_round, [&] { return verify_round(e); }));
+        else RMI_TRY(capture(e, &e.g_single, [&] { return single_step(e); }));
+    }
+    HIP_TRY(hipStreamSynchronize(e.s));
+    HIP_TRY(hipEventRecord(e.ev0, e.s));
+    if (mtp) RMI_TRY(first_draft(e));
+    int emitted = 0, launched = 0;
+    while (emitted < n_gen) {
+        const int batch = mtp ? std::max(1, (n_gen - emitted + 1) / 2) : n_gen - emitted;
+        for (int i = 0; i < batch; ++i) {
+            if (graph) HIP_TRY(hipGraphLaunch(mtp ? e.g_round : e.g_single, e.s));
+            else RMI_TRY(mtp ? verify_round(e) : single_step(e));
+        }
+        launched += batch;
+        HIP_TRY(hipEventRecord(e.ev1, e.s));
+        RMI_TRY(get_ints(e, st, kNumSlots));
+        emitted = st[kNOut];
+        if (launched > 4 * n_gen + 8) return fail(RMI_ERR_STATE, "rmi_engine_generate: no progress");
+    }
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, e.ev0, e.ev1));
+    std::vector<int> ring(static_cast<size_t>(emitted));
+    HIP_TRY(hipMemcpy(ring.data(), e.ring, sizeof(int) * ring.size(), hipMemcpyDeviceToHost));
+    std::memcpy(out_tokens, ring.data(), sizeof(int) * static_cast<size_t>(n_gen));
+    if (stats) {
+        stats->tokens = n_gen;
+        stats->emitted = emitted;
+        stats->rounds = mtp ? st[kRound] : launched;
+        stats->accepted = st[kNAcc];
+        stats->gpu_ms = ms;
+    }
+    return RMI_OK;
+}

@@ -44,11 +44,12 @@ __global__ __launch_bounds__(256) void rms_quant_apply_kernel(const float* __res
 // fp32 out = (x * w) * inv (reference rms_norm_out_kernel, qw:658-672), optionally with the output's own partials
 __global__ __launch_bounds__(256) void rms_norm_out_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ partials, float* __restrict__ out,
-                                                           float* __restrict__ out_partials, int cols, float eps) {
+                                                           float* __restrict__ out_partials, int cols, float eps,
+                                                           int out_stride) {
     const int c = blockIdx.y;
     x += static_cast<size_t>(c) * cols;
     partials += static_cast<size_t>(c) * (cols / 4);
-    out += static_cast<size_t>(c) * cols;
+    out += static_cast<size_t>(c) * out_stride;
     const float ss = block_sum_partials(partials, cols / 4);
     const float inv = rsqrtf(ss / static_cast<float>(cols) + eps);
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -233,14 +234,21 @@ extern "C" int rmi_rms_quant_apply(const float* x, const float* w, const float* 
     return launch_status("rms_quant_apply");
 }
 
-extern "C" int rmi_rms_norm_out(const float* x, const float* w, const float* partials, float* out, float* out_partials,
-                                int cols, float eps, int ncols, void* stream) {
-    if (cols <= 0 || cols % 4 != 0 || bad_cols(ncols)) return fail(RMI_ERR_SHAPE, "rms_norm_out: bad shape");
+extern "C" int rmi_rms_norm_out_strided(const float* x, const float* w, const float* partials, float* out,
+                                        int out_stride, float* out_partials, int cols, float eps, int ncols,
+                                        void* stream) {
+    if (cols <= 0 || cols % 4 != 0 || bad_cols(ncols) || out_stride < cols)
+        return fail(RMI_ERR_SHAPE, "rms_norm_out: bad shape");
     if (!aligned4(x) || !aligned4(w) || !aligned4(partials) || !aligned4(out))
         return fail(RMI_ERR_POINTER, "rms_norm_out: null or misaligned pointer");
     hipLaunchKernelGGL(rms_norm_out_kernel, dim3((cols + 255) / 256, ncols), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), x, w, partials, out, out_partials, cols, eps);
+                       static_cast<hipStream_t>(stream), x, w, partials, out, out_partials, cols, eps, out_stride);
     return launch_status("rms_norm_out");
+}
+
+extern "C" int rmi_rms_norm_out(const float* x, const float* w, const float* partials, float* out, float* out_partials,
+                                int cols, float eps, int ncols, void* stream) {
+    return rmi_rms_norm_out_strided(x, w, partials, out, cols, out_partials, cols, eps, ncols, stream);
 }
 
 extern "C" int rmi_row_sum_partials(const float* x, float* partials, int n, int ncols, void* stream) {
