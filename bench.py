@@ -1,13 +1,19 @@
 """Benchmark of the exact-verify MTP hot path on one MI355X.
 
-Default workload (``--workload verify_gemv``): the 2-column verify GEMV pair with both fused epilogues -- the
-concatenated up||gate Q6_K matrix (24576 x 4096) at ncols = 2, then the down matrix (4096 x 12288) at ncols = 2
-with the residual add and the per-4-row sum-of-squares partials.  One step = one such pair.  Inputs are resident in
-HBM before timing; >= 1 GiB of distinct weight replicas rotate so no step hits the 256 MB Infinity Cache.
+Default workload (``--workload mtp_round``): the full exact-verify MTP decode round of a random-init 9B-class qwen35
+hybrid (32 layers: 24 Gated-DeltaNet + 8 GQA, hidden 4096, FFN 12288, vocab 248320, nextn draft block; every matrix
+Q6_K with seeded weights) at context 4096 and 65536.  One step = one verify round (draft + 2-column verify + greedy
+acceptance + GDN rollback, one hipGraph launch).  Per context: a non-MTP greedy run (the stream every MTP run must
+reproduce bit for bit), then MTP runs with the draft forced to acceptance 0, 0.5 and 1.0.  The context state is
+synthesized from a seed (KV cache fp16 N(0,1), GDN state N(0,0.05^2)) instead of prefilled.
 
-Prints ONE JSON line.  ``value`` is HBM GB/s of the pair (algorithmic bytes / time); ``roofline`` is the up||gate
-GEMV's algorithmic bytes / its mean launch time from HIP events recorded on the launch stream; ``cpu_baseline`` is the
-oracle's threaded fp32 restatement of the same GEMV pair on this host's cores.
+``--workload verify_gemv``: the 2-column verify GEMV pair with both fused epilogues (up||gate 24576x4096 ncols=2,
+then down 4096x12288 ncols=2 with residual + partials), >= 1 GiB of rotating weight replicas.
+
+Prints ONE JSON line.  For mtp_round, ``value`` is tok/s at context 4096 and acceptance 0.5; ``roofline`` is the
+up||gate verify GEMV's algorithmic bytes / its mean launch time from HIP events on its launch stream (measured in the
+same run); ``cpu_baseline`` is the oracle's threaded fp32 GEMV pair on this host, scaled to a round by its weight
+bytes.
 """
 from __future__ import annotations
 
@@ -56,7 +62,7 @@ def cpu_baseline(budget_s: float = 12.0):
         oracle.q6k_gemv_f32(w_dn, x_dn, DN_IN, DN_ROWS, ncols=2, res=res, threads=threads)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 200:
+        if el >= budget_s or reps >= 5000:
             break
     gbs = reps * PAIR_BYTES / el / 1e9
     del w_ug, w_dn
@@ -160,20 +166,121 @@ def run_verify_gemv(args):
     return out
 
 
+ACCEPT_PATTERNS = {"0": [0], "0.5": [1, 0], "1.0": [1]}
+
+
+def tokens_for_rounds(pattern, rounds):
+    """tokens a forced run emits in exactly `rounds` rounds (2 per accepted round, 1 per rejected)."""
+    return sum(2 if pattern[r % len(pattern)] else 1 for r in range(rounds))
+
+
+def run_mtp_rounds(args, contexts=(4096, 65536)):
+    import torch
+
+    import rapier_amd.engine as E
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream(device=0)
+    torch.cuda.set_stream(stream)
+    K, W = args.steps, args.warmup
+    table, identical, info = {}, True, None
+    for ctx in contexts:
+        n_tok = tokens_for_rounds([1], K)          # greedy reference length covers every forced run
+        eng = E.Engine(E.qwen35_9b_config(), seed=2024, max_ctx=ctx + 2 * (K + W) + 256, stream=stream)
+        info = eng.info()
+        first = eng.synth_context(ctx, seed=ctx, last_token=1000)
+        pos0, cur0 = eng.state()
+        eng.save_state()
+        eng.generate(max(W, 1), mode=E.GREEDY)      # warm the single-token graph
+        eng.restore_state(pos0, cur0)
+        ref, st_g = eng.generate(n_tok, mode=E.GREEDY)
+        row = {"greedy": {"tok_s": round(n_tok / (st_g["gpu_ms"] / 1e3), 2),
+                          "ms_per_token": round(st_g["gpu_ms"] / n_tok, 4), "tokens": n_tok}}
+        for name, pat in ACCEPT_PATTERNS.items():
+            eng.restore_state(pos0, cur0)
+            if W:
+                eng.generate(tokens_for_rounds(pat, W), mode=E.MTP_FORCED, ref_tokens=ref, ref_base=pos0 + 1,
+                             pattern=pat)                                  # untimed warmup rounds (graph capture)
+                eng.restore_state(pos0, cur0)
+            n = tokens_for_rounds(pat, K)
+            toks, st = eng.generate(n, mode=E.MTP_FORCED, ref_tokens=ref, ref_base=pos0 + 1, pattern=pat)
+            same = toks == ref[:n]
+            identical &= same
+            row[name] = {"us_per_round": round(st["gpu_ms"] * 1e3 / st["rounds"], 2),
+                         "tok_s": round(n / (st["gpu_ms"] / 1e3), 2), "rounds": st["rounds"],
+                         "accepted": st["accepted"], "tokens": n, "stream_identical": same}
+        table[str(ctx)] = row
+        eng.close()
+        del eng
+        torch.cuda.synchronize()
+    return table, identical, info
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="verify_gemv", choices=["verify_gemv"])
+    ap.add_argument("--steps", type=int, default=200, help="timed verify rounds per run (mtp_round) or GEMV pairs")
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="mtp_round", choices=["mtp_round", "verify_gemv"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported: the path runs on one GPU "
               f"in this build", file=sys.stderr)
         sys.exit(2)
-    out = run_verify_gemv(args)
-    out["cpu_baseline"] = None if args.no_cpu else cpu_baseline()
+    gemv_args = argparse.Namespace(steps=50 if args.workload == "mtp_round" else args.steps,
+                                   warmup=10 if args.workload == "mtp_round" else args.warmup)
+    gemv = run_verify_gemv(gemv_args)
+    cpu = None if args.no_cpu else cpu_baseline()
+    if args.workload == "verify_gemv":
+        gemv["cpu_baseline"] = cpu
+        print(json.dumps(gemv), flush=True)
+        return
+    table, identical, info = run_mtp_rounds(args)
+    head = table["4096"]["0.5"]
+    out = {
+        "metric": METRIC,
+        "value": head["tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_round"] / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 dot, f32 accumulate (Q6_K x Q8_1 GEMVs); f32 GDN/attention over fp16 KV",
+        "data": "synthetic: seeded random-init Q6_K weights (codes U{0..63}, sc U[-32,31], d=|N(0,1e-3)|); context "
+                "state synthesized from a seed (fp16 KV N(0,1), GDN state N(0,0.05^2)), not prefilled",
+        "config": {
+            "workload": "exact-verify MTP round, random-init 9B-class qwen35 (32 layers: 24 GDN + 8 GQA, hidden 4096, "
+                        "FFN 12288, vocab 248320, nextn draft), one hipGraph per round; value = ctx 4096, forced "
+                        "acceptance 0.5",
+            "model": "qwen35-9B-class random-init Q6_K",
+            "ctx": [4096, 65536],
+            "forced_acceptance": [0, 0.5, 1.0],
+            "runs": table,
+            "mtp_stream_identical_to_greedy": identical,
+            "round_weight_bytes": info["round_weight_bytes"],
+            "token_weight_bytes": info["token_weight_bytes"],
+            "kv_bytes_per_pos": info["kv_bytes_per_pos"],
+            "round_hbm_frac_at_4k_accept05": round(
+                (info["round_weight_bytes"] + info["kv_bytes_per_pos"] * 4096) /
+                (head["us_per_round"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "verify_gemv_pair": {"GB_s": gemv["value"], "us_per_pair": gemv["config"]["us_per_pair"],
+                                 "hbm_frac_of_peak": gemv["config"]["hbm_frac_of_peak"]},
+        },
+        "roofline": gemv["roofline"],
+    }
+    if cpu is not None:
+        # the CPU leg times the same GEMV pair; a round streams round_weight_bytes through the same kind of GEMV
+        s_per_round = info["round_weight_bytes"] / (cpu["value"] * 1e9)
+        tok_round = tokens_for_rounds(ACCEPT_PATTERNS["0.5"], args.steps) / args.steps
+        cpu = dict(cpu, value=round(tok_round / s_per_round, 4), unit="tok/s",
+                   gemv_GB_s=cpu["value"],
+                   sample=cpu["sample"] + "; scaled to one verify round by its weight bytes "
+                          f"({info['round_weight_bytes']} B, GEMVs only: GDN/attention not counted) at "
+                          f"{tok_round:.2f} tokens per round")
+    out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
 
 

@@ -205,15 +205,21 @@ __global__ __launch_bounds__(256) void gqa_partial_kernel(const float* __restric
             o[q][1] *= a;
         }
         const uint32_t* vbase = reinterpret_cast<const uint32_t*>(vc + (static_cast<size_t>(sbase + 32 * ph) * n_kv + kv) * HD) + dp;
-        for (int i = 0; i < pend; ++i) {
-            const uint32_t vw = vbase[static_cast<size_t>(i) * n_kv * (HD / 2)];
-            const float v0 = half_bits_to_float(vw), v1 = half_bits_to_float(vw >> 16);
-            const float* prow = pbuf[32 * ph + i];
+        // all 32 V rows of this half are loaded before the FMA chain (positions past p_last are not read)
+        uint32_t vw[32];
 #pragma unroll
-            for (int q = 0; q < MAXQ; ++q) {
-                if (q < nq) {
-                    o[q][0] = __builtin_fmaf(prow[q], v0, o[q][0]);
-                    o[q][1] = __builtin_fmaf(prow[q], v1, o[q][1]);
+        for (int i = 0; i < 32; ++i) vw[i] = i < pend ? vbase[static_cast<size_t>(i) * n_kv * (HD / 2)] : 0u;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            if (i < pend) {
+                const float v0 = half_bits_to_float(vw[i]), v1 = half_bits_to_float(vw[i] >> 16);
+                const float* prow = pbuf[32 * ph + i];
+#pragma unroll
+                for (int q = 0; q < MAXQ; ++q) {
+                    if (q < nq) {
+                        o[q][0] = __builtin_fmaf(prow[q], v0, o[q][0]);
+                        o[q][1] = __builtin_fmaf(prow[q], v1, o[q][1]);
+                    }
                 }
             }
         }
@@ -243,25 +249,47 @@ __global__ __launch_bounds__(256) void gqa_partial_kernel(const float* __restric
 }
 
 // ---- merge + sigmoid gate + Q8_1 ---------------------------------------------------------------------------------------
+// Two passes over the query's chunks 0..last: (1) the 256 lanes load every chunk's (m, l) in parallel, M = max m,
+// weights w_c = exp(m_c - M) to LDS, L = sum l_c w_c (lane-strided partial sums, butterfly, waves in order);
+// (2) lane d accumulates O = sum_c w_c o_c[d] in chunk order with the loads issued 8 chunks ahead.
+constexpr int kMaxChunks = 2048;
+
 __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__ ws, const float* __restrict__ gsrc,
                                                        int gstride, const int* __restrict__ pos, float* __restrict__ y,
                                                        int y_stride, uint8_t* __restrict__ q8, int q8_stride,
                                                        int n_head, int n_kv, int chunk_len) {
+    __shared__ float wts[kMaxChunks];
+    __shared__ float red[4];
     const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
     const int G = n_head / n_kv;
     const int kv = h / G, qv = t * G + (h - kv * G);
-    const int last = (pos[0] + t) / chunk_len;
-    float M = -INFINITY, L = 0.0f, O = 0.0f;
-    for (int c = 0; c <= last; ++c) {
-        const float* rec = ws + ((static_cast<size_t>(c) * n_kv + kv) * MAXQ + qv) * REC;
-        const float mc = rec[0], lc = rec[1], oc = rec[4 + d];
-        const float Mn = fmaxf(M, mc);
-        const float a = M == -INFINITY ? 0.0f : expf(M - Mn);
-        const float b = mc == -INFINITY ? 0.0f : expf(mc - Mn);
-        L = L * a + lc * b;
-        O = O * a + oc * b;
-        M = Mn;
+    const int nchunk = min((pos[0] + t) / chunk_len + 1, kMaxChunks);
+    const size_t cstride = static_cast<size_t>(n_kv) * MAXQ * REC;
+    const float* base = ws + (static_cast<size_t>(kv) * MAXQ + qv) * REC;
+    float mloc = -INFINITY;
+    for (int c = d; c < nchunk; c += HD) mloc = fmaxf(mloc, base[c * cstride]);
+    mloc = group_max<64>(mloc);
+    if ((d & 63) == 0) red[d >> 6] = mloc;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float lloc = 0.0f;
+    for (int c = d; c < nchunk; c += HD) {
+        const float w = expf(base[c * cstride] - M);
+        wts[c] = w;
+        lloc = __builtin_fmaf(base[c * cstride + 1], w, lloc);
     }
+    const float L = block_sum256(lloc, red);   // includes the barrier that publishes wts
+    float O = 0.0f;
+    int c = 0;
+    for (; c + 8 <= nchunk; c += 8) {
+        float oc[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) oc[k] = base[(c + k) * cstride + 4 + d];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) O = __builtin_fmaf(wts[c + k], oc[k], O);
+    }
+    for (; c < nchunk; ++c) O = __builtin_fmaf(wts[c], base[c * cstride + 4 + d], O);
     const float o = O / L;
     const float g = gsrc[static_cast<size_t>(t) * gstride + h * 2 * HD + HD + d];
     const float v = o * sigmoid(g);
@@ -306,6 +334,7 @@ extern "C" int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, cons
         return fail(RMI_ERR_POINTER, "gqa_flash_decode: invalid arguments");
     const int chunk_len = SUB * nsub;
     const int nchunks = (max_ctx + chunk_len - 1) / chunk_len;
+    if (nchunks > kMaxChunks) return fail(RMI_ERR_SHAPE, "gqa_flash_decode: max_ctx / (64 * nsub) exceeds 2048 chunks");
     const auto s = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(gqa_partial_kernel, dim3(nchunks, n_kv), dim3(256), 0, s, q, kcache, vcache, pos,
                        static_cast<float*>(workspace), n_head, n_kv, ntok, nsub, max_ctx, scale);

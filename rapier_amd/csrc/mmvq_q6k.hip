@@ -102,11 +102,13 @@ __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __rest
     constexpr int TPR = kThreads / R;      // lanes per row = half-blocks per row per chunk
     constexpr int NB = CB * 8;             // Q8_1 blocks per chunk per column
     constexpr int U = CB * kQ6KBytes / 16; // 16-byte units per row per chunk
-    constexpr int ROWW = CB * kQ6KBytes / 4 + 1;   // LDS dwords per tile row (+1 pad: rows land on other banks)
+    // LDS dwords per tile row: 16-byte aligned (the staging stores are 128-bit) and padded so that the decode's
+    // dword reads of the wave's rows spread over the banks (at most 2-way; checked exhaustively for both tiles)
+    constexpr int ROWW = CB * kQ6KBytes / 4 + (R == 16 ? 4 : 12);
     constexpr int XS = NCOLS * NB;         // activation blocks to stage per chunk
     constexpr int XP = (XS + kThreads - 1) / kThreads;
 
-    __shared__ uint32_t lw[R * ROWW];
+    __shared__ __attribute__((aligned(16))) uint32_t lw[R * ROWW];
     __shared__ uint4 lq[NCOLS * 2 * NB];
     __shared__ uint4 lrec[NCOLS * NB];
     __shared__ float vout[NCOLS][R];
@@ -123,20 +125,28 @@ __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __rest
     u32x4 wreg[DEPTH][kLoadsPerThread];
     XRegs xreg[DEPTH][XP];
 
-    // step f -> (tile, chunk); loads of 16-byte unit i = t + 256 m: tile row i / U, unit i % U
+    // per-thread load / store slots, fixed for every step: 16-byte unit i = t + 256 m is tile row i / U, unit i % U
+    uint32_t goff[kLoadsPerThread];   // byte offset from the chunk's first row (UINT32_MAX: slot unused)
+    uint32_t lrow[kLoadsPerThread];   // tile row of the slot
+#pragma unroll
+    for (int m = 0; m < kLoadsPerThread; ++m) {
+        const int i = t + kThreads * m;
+        const int tr = i / U, u = i - tr * U;
+        lrow[m] = static_cast<uint32_t>(tr);
+        goff[m] = i < kTileVec ? static_cast<uint32_t>(tr) * rowbytes + static_cast<uint32_t>(u * 16) : 0xffffffffu;
+    }
+
+    // step f -> (tile, chunk)
     auto issue = [&](int f, u32x4 (&wr)[kLoadsPerThread], XRegs (&xr)[XP]) {
         const int q = f / nch;
         const int c = f - q * nch;
         const int row0 = (static_cast<int>(blockIdx.x) + q * G) * R;
         const uint8_t* base = w + static_cast<size_t>(row0) * rowbytes + static_cast<size_t>(c) * (CB * kQ6KBytes);
+        const uint32_t rows_left = static_cast<uint32_t>(n_out - row0);
 #pragma unroll
-        for (int m = 0; m < kLoadsPerThread; ++m) {
-            const int i = t + kThreads * m;
-            const int tr = i / U, u = i - tr * U;
-            if (i < kTileVec && row0 + tr < n_out)
-                wr[m] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4*>(base + static_cast<uint32_t>(tr) * rowbytes + u * 16));
-        }
+        for (int m = 0; m < kLoadsPerThread; ++m)
+            if (goff[m] != 0xffffffffu && lrow[m] < rows_left)
+                wr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + goff[m]));
 #pragma unroll
         for (int p = 0; p < XP; ++p) {
             const int sidx = t + kThreads * p;
@@ -175,14 +185,8 @@ __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __rest
 #pragma unroll
             for (int m = 0; m < kLoadsPerThread; ++m) {
                 const int i = t + kThreads * m;
-                const int tr = i / U, u = i - tr * U;
-                if (i < kTileVec) {
-                    const int lo = tr * ROWW + u * 4;
-                    lw[lo + 0] = wreg[s][m].x;
-                    lw[lo + 1] = wreg[s][m].y;
-                    lw[lo + 2] = wreg[s][m].z;
-                    lw[lo + 3] = wreg[s][m].w;
-                }
+                const int tr = i / U, u = i - tr * U;   // compile-time U: a multiply-shift, hoisted by the compiler
+                if (i < kTileVec) *reinterpret_cast<u32x4*>(&lw[tr * ROWW + u * 4]) = wreg[s][m];
             }
 #pragma unroll
             for (int p = 0; p < XP; ++p) {
@@ -404,7 +408,8 @@ __global__ __launch_bounds__(kThreads) void q6k_block_dots_kernel(const uint8_t*
 int pick_rows(int n_in, int n_out, const void* w) {
     const bool a16 = (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
     if (!a16 || n_in % 2048 != 0) return 0;
-    if (n_in % 4096 == 0 && (n_out + 15) / 16 < 1024) return 8;
+    // 8-row tiles (16 blocks per chunk) for long rows or too few 16-row tiles to fill the chip (measured on MI355X)
+    if (n_in % 4096 == 0 && (n_in > 4096 || (n_out + 15) / 16 < 512)) return 8;
     return 16;
 }
 
@@ -430,8 +435,8 @@ int cu_count() {
 }
 
 TileCfg pick_cfg(int n_in, int n_out, const void* w) {
-    static const int depth = env_int("RMI_GEMV_DEPTH", 2);
-    static const int per_cu = env_int("RMI_GEMV_PER_CU", 0);
+    static const int depth = env_int("RMI_GEMV_DEPTH", 1);
+    static const int per_cu = env_int("RMI_GEMV_PER_CU", 3);
     static const int force_rows = env_int("RMI_GEMV_ROWS", 0);
     TileCfg cfg{pick_rows(n_in, n_out, w), depth == 1 ? 1 : 2, per_cu};
     if (cfg.rows && (force_rows == 8 || force_rows == 16) && n_in % (256 * (128 / force_rows)) == 0)
