@@ -45,6 +45,14 @@ DN_BYTES = (q6_bytes(DN_ROWS, DN_IN) + 2 * (DN_IN // 32) * 36 + 2 * DN_ROWS * 4 
             + 2 * (DN_ROWS // 4) * 4)                                                       # 41,389,056
 PAIR_BYTES = UG_BYTES + DN_BYTES                                                             # 124,170,240
 
+# HBM traffic of one up||gate ncols=2 launch, from two rocprofv3 --pmc passes over `bench.py --workload
+# traffic_probe` (profiles/gemv_up_gate_traffic.md): FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by
+# what the same counter reads for a copy kernel that reads 256 MiB and writes 256 MiB in the same process.
+PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 41656.4375, 192.0
+PMC_COPY_FETCH_KIB, PMC_COPY_WRITE_KIB, COPY_KIB = 131090.3125, 262144.0, 262144.0
+UG_TRAFFIC_BYTES = round(1024 * (PMC_UG_FETCH_KIB * COPY_KIB / PMC_COPY_FETCH_KIB
+                                 + PMC_UG_WRITE_KIB * COPY_KIB / PMC_COPY_WRITE_KIB))
+
 
 def cpu_baseline(budget_s: float = 12.0):
     """Oracle fp32 GEMV pair (C, OpenMP over rows) on this host: the same shapes, repeated to ~budget_s."""
@@ -113,19 +121,30 @@ def run_verify_gemv(args):
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
     for i in range(args.steps):
-        step(args.warmup + i, evs[i])
+        step(args.warmup + i)
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
     ms_per_step = total_ms / args.steps
-    ug_us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
-    ug_mean_us = sum(ug_us) / len(ug_us)
     value = PAIR_BYTES / (ms_per_step * 1e-3) / 1e9
+
+    # roofline leg: blocks of back-to-back up||gate launches over the rotating replicas, one HIP event pair per
+    # block on the launch stream (per-launch event pairs would add the event's own cost to every launch)
+    blocks, per_block = 5, 2 * reps
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(blocks)]
+    torch.cuda.synchronize()
+    for b in range(blocks):
+        evs[b][0].record(stream)
+        for i in range(per_block):
+            rmi.native_q6_k_mmvq(ug[i % reps], xq_ug, y_ug, UG_IN, UG_ROWS, 2, stream)
+        evs[b][1].record(stream)
+    torch.cuda.synchronize()
+    ug_us = sorted(a.elapsed_time(b) * 1e3 / per_block for a, b in evs)
+    ug_mean_us = sum(ug_us) / len(ug_us)
     achieved = UG_BYTES / (ug_mean_us * 1e-6) / 1e9
     out = {
         "metric": METRIC,
@@ -157,14 +176,50 @@ def run_verify_gemv(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": UG_TRAFFIC_BYTES,
+            "traffic_over_algorithmic": round(UG_TRAFFIC_BYTES / UG_BYTES, 4),
             "algorithmic_bytes_per_launch": UG_BYTES,
             "mean_launch_us": round(ug_mean_us, 3),
-            "median_launch_us": round(ug_us[len(ug_us) // 2], 3),
+            "launches_timed": blocks * per_block,
         },
     }
     return out
 
+
+def run_traffic_probe():
+    """Workload for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: one up||gate ncols=2 launch after a 1 GiB
+    fill has evicted L2 and the Infinity Cache, then a copy-like kernel of known size (reads 256 MiB, writes
+    256 MiB) that calibrates both counters in the same process."""
+    import torch
+
+    import rapier_amd as rmi
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream(device=0)
+    torch.cuda.set_stream(stream)
+    w = torch.empty(q6_bytes(UG_ROWS, UG_IN), dtype=torch.uint8, device="cuda")
+    rmi.gen_q6_k(w, UG_ROWS * UG_IN // 256, seed=1)
+    x = torch.empty(2 * UG_IN, device="cuda")
+    rmi.gen_normal(x, x.numel(), seed=2)
+    xq = torch.empty(rmi.native_q8_1_bytes(UG_IN, 2), dtype=torch.uint8, device="cuda")
+    rmi.native_quantize_q8_1(x, xq, UG_IN, 2)
+    y = torch.empty(2 * UG_ROWS, device="cuda")
+    a = torch.ones(COPY_KIB_ELEMS, device="cuda")
+    b = torch.empty_like(a)
+    junk = torch.empty(256 * 1024 * 1024, device="cuda")
+    torch.cuda.synchronize()
+    junk.fill_(1.0)
+    torch.cuda.synchronize()
+    rmi.native_q6_k_mmvq(w, xq, y, UG_IN, UG_ROWS, 2, stream)
+    torch.cuda.synchronize()
+    junk.fill_(2.0)
+    torch.cuda.synchronize()
+    torch.add(a, 1.0, out=b)
+    torch.cuda.synchronize()
+    print(json.dumps({"workload": "traffic_probe", "gemv_launches": 1, "copy_read_bytes": a.numel() * 4,
+                      "copy_write_bytes": b.numel() * 4}), flush=True)
+
+
+COPY_KIB_ELEMS = int(COPY_KIB * 1024 // 4)
 
 ACCEPT_PATTERNS = {"0": [0], "0.5": [1, 0], "1.0": [1]}
 
@@ -220,14 +275,17 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200, help="timed verify rounds per run (mtp_round) or GEMV pairs")
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="mtp_round", choices=["mtp_round", "verify_gemv"])
+    ap.add_argument("--workload", default="mtp_round", choices=["mtp_round", "verify_gemv", "traffic_probe"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported: the path runs on one GPU "
               f"in this build", file=sys.stderr)
         sys.exit(2)
-    gemv_args = argparse.Namespace(steps=50 if args.workload == "mtp_round" else args.steps,
+    if args.workload == "traffic_probe":
+        run_traffic_probe()
+        return
+    gemv_args =argparse.Namespace(steps=50 if args.workload == "mtp_round" else args.steps,
                                    warmup=10 if args.workload == "mtp_round" else args.warmup)
     gemv = run_verify_gemv(gemv_args)
     cpu = None if args.no_cpu else cpu_baseline()

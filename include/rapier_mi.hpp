@@ -1,0 +1,88 @@
+// rapier_mi.hpp - header-only C++ shim: the reference's strata::kernels launch surface (same names, signatures and
+// error behaviour) implemented over the C ABI of librapier_mi.so (rapier_mi.h).  An engine written against the
+// reference's headers (native_mmvq.hpp, fused_gdn.hpp as used by src/qwythos.cpp) compiles against this file instead.
+//
+// Error behaviour, as in the reference:
+//   MMVQ family (mmvq:2312-2331): std::invalid_argument for shape / ncols / pointer / null-stream errors,
+//   std::runtime_error for a failed launch.
+//   fused_gdn family (fgdn:169-175, 194-204): message on stderr and std::exit(1).
+#pragma once
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <stdexcept>
+#include <string>
+
+#include "rapier_mi.h"
+
+namespace strata::kernels {
+
+namespace rmi_detail {
+inline void check_mmvq(int rc) {
+    if (rc == RMI_OK) return;
+    if (rc == RMI_ERR_LAUNCH || rc == RMI_ERR_STATE) throw std::runtime_error(rmi_last_error());
+    throw std::invalid_argument(rmi_last_error());
+}
+inline void check_exit(int rc) {
+    if (rc == RMI_OK) return;
+    std::fprintf(stderr, "%s\n", rmi_last_error());
+    std::exit(1);
+}
+}  // namespace rmi_detail
+
+// mmvq:3054-3057
+inline std::size_t native_q8_1_bytes(int n_in, int ncols) {
+    const std::size_t n = rmi_native_q8_1_bytes(n_in, ncols);
+    if (n == 0) throw std::invalid_argument(rmi_last_error());
+    return n;
+}
+// mmvq:3059-3071
+inline void native_quantize_q8_1(const float* x, void* x_q8_1, int n_in, int ncols, void* stream) {
+    rmi_detail::check_mmvq(rmi_native_quantize_q8_1(x, x_q8_1, n_in, ncols, stream));
+}
+// mmvq:3627-3660
+inline void native_q6_k_mmvq(const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
+                             void* stream) {
+    rmi_detail::check_mmvq(rmi_native_q6_k_mmvq(w, x_q8_1, y, n_in, n_out, ncols, stream));
+}
+// mmvq:3187-3200 (header patches/0002:9-24)
+inline void native_q6_k_mmvq_res(const void* w, const void* x_q8_1, float* y, const float* res, float* partials,
+                                 int n_in, int n_out, void* stream) {
+    rmi_detail::check_mmvq(rmi_native_q6_k_mmvq_res(w, x_q8_1, y, res, partials, n_in, n_out, stream));
+}
+// mmvq:3732-3736
+inline void native_q8_0_mmvq(const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
+                             void* stream) {
+    rmi_detail::check_mmvq(rmi_native_q8_0_mmvq(w, x_q8_1, y, n_in, n_out, ncols, stream));
+}
+// mmvq:3326-3339
+inline void native_q8_0_mmvq_res(const void* w, const void* x_q8_1, float* y, const float* res, float* partials,
+                                 int n_in, int n_out, void* stream) {
+    rmi_detail::check_mmvq(rmi_native_q8_0_mmvq_res(w, x_q8_1, y, res, partials, n_in, n_out, stream));
+}
+// mmvq:3787-3818
+inline void native_mmvq(int ggml_type, const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
+                        void* stream) {
+    rmi_detail::check_mmvq(rmi_native_mmvq(ggml_type, w, x_q8_1, y, n_in, n_out, ncols, stream));
+}
+inline bool native_mmvq_supported(int ggml_type) noexcept { return rmi_native_mmvq_supported(ggml_type) != 0; }
+inline std::size_t native_mmvq_weight_bytes(int ggml_type, int n_in, int n_out) {
+    const std::size_t n = rmi_native_mmvq_weight_bytes(ggml_type, n_in, n_out);
+    if (n == 0) throw std::invalid_argument(rmi_last_error());
+    return n;
+}
+// fgdn:167-176
+inline void fused_gdn_conv_l2(float* history, const float* qkv, const float* conv_w, float* h, int channels,
+                              int qk_heads, float eps, void* stream) {
+    rmi_detail::check_exit(rmi_fused_gdn_conv_l2(history, qkv, conv_w, h, channels, qk_heads, eps, stream));
+}
+// fgdn:221-225 (header patches/0001:9-15)
+inline void fused_gdn_step_norm_silu_q8(float* state, const float* q, const float* k, const float* v,
+                                        const float* gate, const float* beta, const float* z, const float* gamma,
+                                        float eps, float* y, uint8_t* q8, int h_k, int h_v, void* stream) {
+    rmi_detail::check_exit(
+        rmi_fused_gdn_step_norm_silu_q8(state, q, k, v, gate, beta, z, gamma, eps, y, q8, h_k, h_v, stream));
+}
+
+}  // namespace strata::kernels
