@@ -5,9 +5,9 @@
 //               first n_rot dims -> fp32 q buffer; k heads get RMSNorm (kn) + RoPE and v heads nothing, both stored
 //               as fp16 at cache[pos_t][kv][d].  pos_t = pos[0] + t is read on the device.
 //   partial     split-K flash decode.  Workgroup (chunk, kv head) covers positions [chunk * 64 * nsub, +64 * nsub) for
-//               every query vector of its group (group heads x tokens): QK^T on MFMA 16x16x16 f16 with q split into
-//               fp16 hi + lo (so scores carry ~fp32 precision against the exact fp16 K), online softmax per query,
-//               P V with fp32 FMAs over coalesced fp16 V rows.  Writes (m, l, o[256]) per query vector.
+//               every query vector of its group (group heads x tokens); each of its 4 waves streams a quarter of the
+//               chunk independently: QK^T and P V both on MFMA 16x16x16 f16 with the fp32 operand (q, p) split into
+//               fp16 hi + lo rows of the same MFMA, online softmax per query.  Writes (m, l, o[256]) per query.
 //   merge       one workgroup per (token, head): merges that query's chunks 0..pos_t / chunk in order, divides, gates
 //               with sigmoid(g) and writes fp32 y plus Q8_1 for the wo GEMV.
 // Query t sees positions <= pos[0] + t.  Chunk boundaries depend only on the query's position, so a verify column's
@@ -18,9 +18,9 @@ namespace rmi {
 namespace {
 
 constexpr int HD = 256;
-constexpr int SUB = 64;            // positions per sub-tile (4 waves x 16)
+constexpr int SUB = 64;            // positions per chunk unit (4 waves x 16); a chunk is SUB * nsub positions
 constexpr int REC = HD + 4;        // workspace record: m, l, pad, pad, o[256]
-constexpr int MAXQ = 16;           // query vectors per kv head one launch handles (MFMA N)
+constexpr int SLOTS = 8;           // query vectors per kv head one launch handles (tokens x group heads)
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -83,168 +83,257 @@ __global__ __launch_bounds__(HD) void attn_prep_kernel(const float* __restrict__
 }
 
 // ---- split-K partial ---------------------------------------------------------------------------------------------------
-// Query vector qv = t * G + gh (token t, head kv * G + gh).  MFMA 16x16x16 f16, lane l: A rows (positions) l % 16 with
-// k = 4 (l / 16) .. +3; B cols (query vectors) l % 16, same k; D col l % 16, rows 4 (l / 16) .. +3.  The head
-// dimension is walked in 8 pairs of k-steps: in pair sp, lane group g = l / 16 supplies dims 32 sp + 8 g + 0..3 (first
-// step) and + 4..7 (second step) for both operands, so one 16-byte K load feeds two MFMAs.
-__global__ __launch_bounds__(256) void gqa_partial_kernel(const float* __restrict__ qbuf, const uint16_t* __restrict__ kc,
+// Workgroup (chunk, kv head), 4 waves.  Wave w streams positions [chunk * 64 nsub + w * 16 nsub, +16 nsub) in steps of
+// 16 on its own (no workgroup barrier inside the loop); the 4 waves' (m, l, o) are combined in wave order at the end
+// into one record per query slot.  Query slot q = t * G + gh (token t, head kv * G + gh), q < 8.
+//
+// Both products run on v_mfma_f32_16x16x16f16 (lane l: l16 = l % 16, g4 = l / 16; A rows / B cols / D cols are l16,
+// the k index of A and B is 4 g4 + 0..3, D rows are 4 g4 + 0..3):
+//   scores  D[pos][n] = K[pos][:] . qcol_n, with qcol_n = fp16 hi part of slot n for n < 8 and the fp16 lo part of
+//           slot n - 8 for n >= 8, so one MFMA chain yields both halves and s = D[pos][q] + D[pos][q + 8] carries
+//           ~fp32 precision against the exact fp16 K.  K is loaded coalesced (two 512-byte rows per wave load),
+//           staged through a padded LDS tile and read back in the A layout.
+//   P V     D[m][n] = P'[m][pos] . V[pos][c(n)], with P' rows m < 8 = fp16 hi of p for slot m and rows m >= 8 = fp16
+//           lo of p for slot m - 8.  The score lane (n, g4) already holds p for slot n % 8 at positions 4 g4 + r, which
+//           is exactly the A layout.  V comes straight from coalesced 16-byte loads: lane (l16, g4) loads positions
+//           4 g4 + j, dims 128 dg + 8 l16 + [0, 8); MFMA (dg, e) takes dim c = 128 dg + 8 l16 + e, so its B operand is
+//           the e-th half of the four loads.  hi and lo rows are added once at the end (xor-32 lanes).
+// Rows past the last position re-read the last row (finite data) and are masked to p = 0.
+constexpr int STEP = 16;                 // positions per MFMA step
+constexpr int WAVES = 4;
+constexpr int KROW = 2 * HD + 16;        // bytes per staged K row: 16-byte pad puts consecutive rows 4 banks apart
+constexpr int KTILE = STEP * KROW;       // 8448 bytes per wave; reused for the wave's o[8][256] (8192 bytes)
+
+__device__ __forceinline__ void lds_wave_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+typedef uint32_t u32x32 __attribute__((ext_vector_type(32)));
+
+__device__ __forceinline__ void set_u4(u32x32& v, int j, uint4 w) {
+    v[4 * j] = w.x;
+    v[4 * j + 1] = w.y;
+    v[4 * j + 2] = w.z;
+    v[4 * j + 3] = w.w;
+}
+__device__ __forceinline__ uint4 get_u4(const u32x32& v, int j) {
+    return make_uint4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int w) {
+    return w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w;
+}
+
+__global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __restrict__ qbuf, const uint16_t* __restrict__ kc,
                                                           const uint16_t* __restrict__ vc, const int* __restrict__ pos,
                                                           float* __restrict__ ws, int n_head, int n_kv, int ntok,
                                                           int nsub, int max_ctx, float scale) {
-    __shared__ float pbuf[SUB][MAXQ];
-    __shared__ float red[4][MAXQ];
-    __shared__ float msh[MAXQ];
-    __shared__ float opart[MAXQ][128 * 2];
+    __shared__ __attribute__((aligned(16))) uint8_t tiles[WAVES * KTILE];
+    __shared__ float wstat[WAVES][2][SLOTS];
     const int chunk = blockIdx.x, kv = blockIdx.y;
     const int G = n_head / n_kv;
     const int nq = ntok * G;
     const int p0 = pos[0];
     const int p_last = p0 + ntok - 1;
-    const int cbase = chunk * SUB * nsub;
+    const int wlen = STEP * nsub;
+    const int cbase = chunk * WAVES * wlen;
     if (cbase > p_last || p0 < 0 || p_last >= max_ctx) return;   // uniform: no visible position (or a bad pos)
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int l16 = lane & 15, g4 = lane >> 4;
+    const int slot = l16 & 7;
+    const bool lo_row = l16 >= 8;
+    const int wbase = cbase + wv * wlen;
+    const int nsteps = wbase > p_last ? 0 : min(nsub, (p_last - wbase) / STEP + 1);
+    uint8_t* kt = tiles + wv * KTILE;
 
-    // B operand: q hi/lo for query vector l16
-    half4 qhi[16], qlo[16];
+    // B operand of the score MFMAs: step 2 sp + hlf covers dims 32 sp + 8 g4 + 4 hlf + [0, 4)
+    half4 qb[16];
     {
-        const int qv = l16;
-        const bool ok = qv < nq;
-        const int t = ok ? qv / G : 0, gh = ok ? qv - (qv / G) * G : 0;
+        const bool ok = slot < nq;
+        const int t = ok ? slot / G : 0, gh = ok ? slot - (slot / G) * G : 0;
         const float* q = qbuf + (static_cast<size_t>(t) * n_head + kv * G + gh) * HD;
 #pragma unroll
         for (int sp = 0; sp < 8; ++sp) {
 #pragma unroll
             for (int hlf = 0; hlf < 2; ++hlf) {
-                half4 hi, lo;
+                half4 v;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float x = ok ? q[32 * sp + 8 * g4 + 4 * hlf + e] : 0.0f;
                     const _Float16 h = static_cast<_Float16>(x);
-                    hi[e] = h;
-                    lo[e] = static_cast<_Float16>(x - static_cast<float>(h));
+                    v[e] = lo_row ? static_cast<_Float16>(x - static_cast<float>(h)) : h;
                 }
-                qhi[2 * sp + hlf] = hi;
-                qlo[2 * sp + hlf] = lo;
+                qb[2 * sp + hlf] = v;
             }
         }
     }
+    const int lim = slot < nq ? p0 + slot / G : -1;   // last position slot `slot` may see
 
-    // P V ownership: dims pair dp (2 dims), position half ph of each sub-tile
-    const int dp = threadIdx.x & 127, ph = threadIdx.x >> 7;
-    float o[MAXQ][2];
+    floatx4 oacc[2][8];
 #pragma unroll
-    for (int q = 0; q < MAXQ; ++q) o[q][0] = o[q][1] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;   // for query vector l16 (replicated across lane groups and waves)
+    for (int dg = 0; dg < 2; ++dg)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) oacc[dg][e] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;   // of slot `slot` (same value in every lane of that slot)
 
-    for (int sb = 0; sb < nsub; ++sb) {
-        const int sbase = cbase + sb * SUB;
-        if (sbase > p_last) break;   // uniform
-        // ---- scores: wave wv owns positions sbase + 16 wv + [0, 16)
-        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        {
-            const int prow = sbase + 16 * wv + l16;
-            const uint16_t* krow = kc + (static_cast<size_t>(prow) * n_kv + kv) * HD;
+    const size_t rstride = static_cast<size_t>(n_kv) * HD;   // halves between consecutive positions
+    const uint16_t* kb = kc + static_cast<size_t>(kv) * HD;
+    const uint16_t* vb = vc + static_cast<size_t>(kv) * HD;
+    const int krow = lane >> 5, kcol = lane & 31;
+
+    // rows are clamped to p_last, so every load is in bounds (a wave with no step re-reads row p_last)
+    u32x32 kreg;   // one vector value (an array carried across iterations would live in scratch)
 #pragma unroll
-            for (int sp = 0; sp < 8; ++sp) {
-                const uint4 kw = *reinterpret_cast<const uint4*>(krow + 32 * sp + 8 * g4);
-                half4 k0, k1;
-                k0 = __builtin_bit_cast(half4, make_uint2(kw.x, kw.y));
-                k1 = __builtin_bit_cast(half4, make_uint2(kw.z, kw.w));
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(k0, qhi[2 * sp], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(k0, qlo[2 * sp], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(k1, qhi[2 * sp + 1], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(k1, qlo[2 * sp + 1], acc, 0, 0, 0);
-            }
+    for (int j = 0; j < 8; ++j) {
+        const int p = min(wbase + 2 * j + krow, p_last);
+        set_u4(kreg, j, *reinterpret_cast<const uint4*>(kb + p * rstride + kcol * 8));
+    }
+    // V of a step: [2 j + dg] = position sb + 4 g4 + j, dims 128 dg + 8 l16 + [0, 8); also one step ahead
+    u32x32 vnext;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint16_t* vr = vb + min(wbase + 4 * g4 + j, p_last) * rstride + 8 * l16;
+        set_u4(vnext, 2 * j, *reinterpret_cast<const uint4*>(vr));
+        set_u4(vnext, 2 * j + 1, *reinterpret_cast<const uint4*>(vr + 128));
+    }
+    for (int s = 0; s < nsteps; ++s) {
+        const int sb = wbase + s * STEP;
+        uint4 vreg[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vreg[j] = get_u4(vnext, j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint16_t* vr = vb + min(sb + STEP + 4 * g4 + j, p_last) * rstride + 8 * l16;
+            set_u4(vnext, 2 * j, *reinterpret_cast<const uint4*>(vr));
+            set_u4(vnext, 2 * j + 1, *reinterpret_cast<const uint4*>(vr + 128));
         }
-        // lane holds scores of query l16 at positions sbase + 16 wv + 4 g4 + r
-        const int qv = l16;
-        const int tq = qv < nq ? qv / G : 0;
-        const int lim = qv < nq ? p0 + tq : -1;   // last visible position for this query vector
-        float s[4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) *reinterpret_cast<uint4*>(kt + (2 * j + krow) * KROW + kcol * 16) = get_u4(kreg, j);
+        // next step's K is in flight during this step's math (after the last step: row p_last again, a cache hit)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int p = min(sb + STEP + 2 * j + krow, p_last);
+            set_u4(kreg, j, *reinterpret_cast<const uint4*>(kb + p * rstride + kcol * 8));
+        }
+        lds_wave_sync();
+        floatx4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int sp = 0; sp < 8; ++sp) {
+            const uint4 kw = *reinterpret_cast<const uint4*>(kt + l16 * KROW + 64 * sp + 16 * g4);
+            const half4 k0 = __builtin_bit_cast(half4, make_uint2(kw.x, kw.y));
+            const half4 k1 = __builtin_bit_cast(half4, make_uint2(kw.z, kw.w));
+            sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k0, qb[2 * sp], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k1, qb[2 * sp + 1], sacc, 0, 0, 0);
+        }
+        // lane (l16, g4): s for slot l16 % 8 at positions sb + 4 g4 + r
+        float sc[4];
         float mloc = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int pp = sbase + 16 * wv + 4 * g4 + r;
-            s[r] = pp <= lim ? acc[r] * scale : -INFINITY;
-            mloc = fmaxf(mloc, s[r]);
+            const float v = sacc[r] + __shfl_xor(sacc[r], 8, 64);
+            sc[r] = sb + 4 * g4 + r <= lim ? v * scale : -INFINITY;
+            mloc = fmaxf(mloc, sc[r]);
         }
         mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        if (g4 == 0) red[wv][qv] = mloc;
-        __syncthreads();
-        const float msub = fmaxf(fmaxf(red[0][qv], red[1][qv]), fmaxf(red[2][qv], red[3][qv]));
-        const float m_new = fmaxf(m_run, msub);
-        const float m_ref = m_new == -INFINITY ? 0.0f : m_new;   // all masked so far: exp(-inf) = 0, no NaN
-        float lloc = 0.0f;
+        const float m_new = fmaxf(m_run, mloc);
+        const float m_ref = m_new == -INFINITY ? 0.0f : m_new;   // nothing visible yet: exp(-inf) = 0, no NaN
+        const float alpha = m_run == m_new ? 1.0f : expf(m_run - m_ref);
+        float pr[4], lsum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float pr = expf(s[r] - m_ref);
-            pbuf[16 * wv + 4 * g4 + r][qv] = pr;
-            lloc += pr;
+            pr[r] = expf(sc[r] - m_ref);
+            lsum += pr[r];
         }
-        lloc += __shfl_xor(lloc, 16, 64);
-        lloc += __shfl_xor(lloc, 32, 64);
-        __syncthreads();   // everyone has read red (max) before it holds the sums
-        if (g4 == 0) red[wv][qv] = lloc;
-        __syncthreads();
-        const float lsub = ((red[0][qv] + red[1][qv]) + red[2][qv]) + red[3][qv];
-        const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_ref);
-        l_run = l_run * alpha + lsub;
-        // rescale factor per query vector for the P V owners, via LDS
-        if (threadIdx.x < MAXQ) msh[threadIdx.x] = alpha;
+        lsum += __shfl_xor(lsum, 16, 64);
+        lsum += __shfl_xor(lsum, 32, 64);
+        l_run = l_run * alpha + lsum;
         m_run = m_new;
-        __syncthreads();
-        // ---- P V: positions sbase + 32 ph + [0, 32) that are <= p_last
-        const int pend = min(32, p_last - (sbase + 32 * ph) + 1);
+        if (__ballot(alpha != 1.0f)) {   // wave-uniform: some slot's running max moved
+            float a[4];
 #pragma unroll
-        for (int q = 0; q < MAXQ; ++q) {
-            const float a = msh[q];
-            o[q][0] *= a;
-            o[q][1] *= a;
+            for (int r = 0; r < 4; ++r) a[r] = __shfl(alpha, 4 * (g4 & 1) + r, 64);
+#pragma unroll
+            for (int dg = 0; dg < 2; ++dg)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) oacc[dg][e][r] *= a[r];
         }
-        const uint32_t* vbase = reinterpret_cast<const uint32_t*>(vc + (static_cast<size_t>(sbase + 32 * ph) * n_kv + kv) * HD) + dp;
-        // all 32 V rows of this half are loaded before the FMA chain (positions past p_last are not read)
-        uint32_t vw[32];
+        half4 pa;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) vw[i] = i < pend ? vbase[static_cast<size_t>(i) * n_kv * (HD / 2)] : 0u;
+        for (int r = 0; r < 4; ++r) {
+            const _Float16 h = static_cast<_Float16>(pr[r]);
+            pa[r] = lo_row ? static_cast<_Float16>(pr[r] - static_cast<float>(h)) : h;
+        }
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            if (i < pend) {
-                const float v0 = half_bits_to_float(vw[i]), v1 = half_bits_to_float(vw[i] >> 16);
-                const float* prow = pbuf[32 * ph + i];
+        for (int dg = 0; dg < 2; ++dg) {
 #pragma unroll
-                for (int q = 0; q < MAXQ; ++q) {
-                    if (q < nq) {
-                        o[q][0] = __builtin_fmaf(prow[q], v0, o[q][0]);
-                        o[q][1] = __builtin_fmaf(prow[q], v1, o[q][1]);
-                    }
-                }
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t x0 = word_of(vreg[dg], w), x1 = word_of(vreg[2 + dg], w);
+                const uint32_t x2 = word_of(vreg[4 + dg], w), x3 = word_of(vreg[6 + dg], w);
+                const half4 b_even = __builtin_bit_cast(
+                    half4, make_uint2((x0 & 0xffffu) | (x1 << 16), (x2 & 0xffffu) | (x3 << 16)));
+                const half4 b_odd = __builtin_bit_cast(
+                    half4, make_uint2((x0 >> 16) | (x1 & 0xffff0000u), (x2 >> 16) | (x3 & 0xffff0000u)));
+                oacc[dg][2 * w] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, b_even, oacc[dg][2 * w], 0, 0, 0);
+                oacc[dg][2 * w + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, b_odd, oacc[dg][2 * w + 1], 0, 0, 0);
             }
         }
-        __syncthreads();   // pbuf / msh reused by the next sub-tile
     }
-    // combine the two position halves in order (half 0 + half 1) and write the records
-    if (ph == 1) {
+    // hi rows + lo rows: lanes g4 < 2 end with o[slot 4 g4 + r][128 dg + 8 l16 + e]
 #pragma unroll
-        for (int q = 0; q < MAXQ; ++q) {
-            opart[q][2 * dp] = o[q][0];
-            opart[q][2 * dp + 1] = o[q][1];
-        }
+    for (int dg = 0; dg < 2; ++dg)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) oacc[dg][e][r] += __shfl_xor(oacc[dg][e][r], 32, 64);
+
+    __syncthreads();   // every wave is done with its K tile: reuse it for the wave's o
+    float* ob = reinterpret_cast<float*>(kt);
+    if (g4 < 2) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int dg = 0; dg < 2; ++dg) {
+                float4* dst = reinterpret_cast<float4*>(ob + (4 * g4 + r) * HD + 128 * dg + 8 * l16);
+                dst[0] = make_float4(oacc[dg][0][r], oacc[dg][1][r], oacc[dg][2][r], oacc[dg][3][r]);
+                dst[1] = make_float4(oacc[dg][4][r], oacc[dg][5][r], oacc[dg][6][r], oacc[dg][7][r]);
+            }
+    }
+    if (g4 == 0 && l16 < SLOTS) {
+        wstat[wv][0][l16] = m_run;
+        wstat[wv][1][l16] = l_run;
     }
     __syncthreads();
-    if (ph == 0) {
-        for (int q = 0; q < nq; ++q) {
-            float* rec = ws + ((static_cast<size_t>(chunk) * n_kv + kv) * MAXQ + q) * REC;
-            rec[4 + 2 * dp] = o[q][0] + opart[q][2 * dp];
-            rec[4 + 2 * dp + 1] = o[q][1] + opart[q][2 * dp + 1];
+    // thread: slot q = tid / 32, dims 8 (tid % 32) + [0, 8); waves combined in order 0..3
+    const int q = threadIdx.x >> 5, d0 = 8 * (threadIdx.x & 31);
+    if (q < nq) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, wstat[w][0][q]);
+        const float M_ref = M == -INFINITY ? 0.0f : M;
+        float wt[WAVES], L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            wt[w] = expf(wstat[w][0][q] - M_ref);
+            L = __builtin_fmaf(wstat[w][1][q], wt[w], L);
         }
-    }
-    if (threadIdx.x < nq) {   // lanes 0..15 of wave 0 hold m_run / l_run of query vector threadIdx.x
-        float* rec = ws + ((static_cast<size_t>(chunk) * n_kv + kv) * MAXQ + threadIdx.x) * REC;
-        rec[0] = m_run;
-        rec[1] = l_run;
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float* src = reinterpret_cast<const float*>(tiles + w * KTILE) + q * HD + d0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = __builtin_fmaf(wt[w], src[i], o[i]);
+        }
+        float* rec = ws + ((static_cast<size_t>(chunk) * n_kv + kv) * SLOTS + q) * REC;
+        reinterpret_cast<float4*>(rec + 4 + d0)[0] = make_float4(o[0], o[1], o[2], o[3]);
+        reinterpret_cast<float4*>(rec + 4 + d0)[1] = make_float4(o[4], o[5], o[6], o[7]);
+        if ((threadIdx.x & 31) == 0) {
+            rec[0] = M;
+            rec[1] = L;
+        }
     }
 }
 
@@ -264,8 +353,8 @@ __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__
     const int G = n_head / n_kv;
     const int kv = h / G, qv = t * G + (h - kv * G);
     const int nchunk = min((pos[0] + t) / chunk_len + 1, kMaxChunks);
-    const size_t cstride = static_cast<size_t>(n_kv) * MAXQ * REC;
-    const float* base = ws + (static_cast<size_t>(kv) * MAXQ + qv) * REC;
+    const size_t cstride = static_cast<size_t>(n_kv) * SLOTS * REC;
+    const float* base = ws + (static_cast<size_t>(kv) * SLOTS + qv) * REC;
     float mloc = -INFINITY;
     for (int c = d; c < nchunk; c += HD) mloc = fmaxf(mloc, base[c * cstride]);
     mloc = group_max<64>(mloc);
@@ -319,18 +408,18 @@ extern "C" size_t rmi_gqa_workspace_bytes(int max_ctx, int n_kv, int nsub) {
     if (max_ctx <= 0 || n_kv <= 0 || nsub <= 0) return 0;
     const int chunk_len = SUB * nsub;
     const size_t nchunks = static_cast<size_t>((max_ctx + chunk_len - 1) / chunk_len);
-    return nchunks * static_cast<size_t>(n_kv) * MAXQ * REC * sizeof(float);
+    return nchunks * static_cast<size_t>(n_kv) * SLOTS * REC * sizeof(float);
 }
 
 extern "C" int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* pos,
                                     const float* gate_src, int gate_stride, float* y, int y_stride, uint8_t* q8,
                                     int q8_stride, void* workspace, int n_head, int n_kv, int head_dim, int ntok,
                                     int max_ctx, int nsub, float scale, void* stream) {
-    if (head_dim != HD || n_head <= 0 || n_kv <= 0 || n_head % n_kv || ntok < 1 || ntok * (n_head / n_kv) > MAXQ ||
+    if (head_dim != HD || n_head <= 0 || n_kv <= 0 || n_head % n_kv || ntok < 1 || ntok * (n_head / n_kv) > SLOTS ||
         max_ctx <= 0 || max_ctx % SUB || nsub <= 0)
         return fail(RMI_ERR_SHAPE, "gqa_flash_decode: invalid arguments");
-    if (!aligned4(q) || !aligned4(kcache) || !aligned4(vcache) || !aligned4(pos) || !aligned4(gate_src) ||
-        !aligned4(workspace) || (!y && !q8))
+    if (!aligned4(q) || !aligned16(kcache) || !aligned16(vcache) || !aligned4(pos) || !aligned4(gate_src) ||
+        !aligned16(workspace) || (!y && !q8))
         return fail(RMI_ERR_POINTER, "gqa_flash_decode: invalid arguments");
     const int chunk_len = SUB * nsub;
     const int nchunks = (max_ctx + chunk_len - 1) / chunk_len;

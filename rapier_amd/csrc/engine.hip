@@ -455,7 +455,8 @@ extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int
     Engine& e = h->e;
     e.cfg = c;
     e.max_ctx = (max_ctx + 63) / 64 * 64;
-    e.nsub = std::max(1, std::min(8, e.max_ctx / 16384));
+    // attention chunk = 64 * nsub positions: 128 at 4K-class caches, 512 at 64K (one partial wave per SIMD pair)
+    e.nsub = std::max(2, std::min(16, e.max_ctx / 8192));
     if (stream) {
         e.s = static_cast<hipStream_t>(stream);
     } else {
