@@ -277,6 +277,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="mtp_round", choices=["mtp_round", "verify_gemv", "traffic_probe"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--ctx", default="4096,65536",
+                    help="comma-separated context lengths for mtp_round; value is quoted at the first")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported: the path runs on one GPU "
@@ -293,8 +295,9 @@ def main():
         gemv["cpu_baseline"] = cpu
         print(json.dumps(gemv), flush=True)
         return
-    table, identical, info = run_mtp_rounds(args)
-    head = table["4096"]["0.5"]
+    ctxs = tuple(int(c) for c in args.ctx.split(","))
+    table, identical, info = run_mtp_rounds(args, ctxs)
+    head = table[str(ctxs[0])]["0.5"]
     out = {
         "metric": METRIC,
         "value": head["tok_s"],
@@ -311,18 +314,18 @@ def main():
                 "state synthesized from a seed (fp16 KV N(0,1), GDN state N(0,0.05^2)), not prefilled",
         "config": {
             "workload": "exact-verify MTP round, random-init 9B-class qwen35 (32 layers: 24 GDN + 8 GQA, hidden 4096, "
-                        "FFN 12288, vocab 248320, nextn draft), one hipGraph per round; value = ctx 4096, forced "
-                        "acceptance 0.5",
+                        f"FFN 12288, vocab 248320, nextn draft), one hipGraph per round; value = ctx {ctxs[0]}, "
+                        "forced acceptance 0.5",
             "model": "qwen35-9B-class random-init Q6_K",
-            "ctx": [4096, 65536],
+            "ctx": list(ctxs),
             "forced_acceptance": [0, 0.5, 1.0],
             "runs": table,
             "mtp_stream_identical_to_greedy": identical,
             "round_weight_bytes": info["round_weight_bytes"],
             "token_weight_bytes": info["token_weight_bytes"],
             "kv_bytes_per_pos": info["kv_bytes_per_pos"],
-            "round_hbm_frac_at_4k_accept05": round(
-                (info["round_weight_bytes"] + info["kv_bytes_per_pos"] * 4096) /
+            "round_hbm_frac_at_first_ctx_accept05": round(
+                (info["round_weight_bytes"] + info["kv_bytes_per_pos"] * ctxs[0]) /
                 (head["us_per_round"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "verify_gemv_pair": {"GB_s": gemv["value"], "us_per_pair": gemv["config"]["us_per_pair"],
                                  "hbm_frac_of_peak": gemv["config"]["hbm_frac_of_peak"]},

@@ -7,8 +7,9 @@
 //  * A workgroup of 256 lanes (4 wave64) owns R output rows.  It walks the rows' bytes in chunks of CB Q6_K blocks
 //    (R * CB = 128, so a chunk is always 26880 bytes), loading each chunk with 16-byte fully coalesced loads into
 //    registers one chunk ahead and parking it in LDS.  Rows are 16-byte aligned because n_in % (256 * CB) == 0.
-//  * The chunk's Q8_1 activation blocks are staged in LDS once per workgroup, re-laid as 32 code bytes plus a
-//    record {-32 * sum(q8) per 16 elements, d8}, so the "code - 32" of Q6_K is folded into the dot's accumulator.
+//  * Q8_1 activation blocks are staged in LDS, re-laid as 32 code bytes plus a record {-32 * sum(q8) per 16
+//    elements, d8}, so the "code - 32" of Q6_K is folded into the dot's accumulator.  Rows of at most 4096 elements
+//    are staged whole, once per workgroup, while the first weight chunks are in flight; longer rows chunk by chunk.
 //  * Lane (row, half-block) decodes 128 weights once (aligned LDS dwords + v_alignbyte for the odd blocks' 2-byte
 //    offset) and applies them to every column with v_dot4_i32_i8: an exact int32 per 16 elements, then
 //    acc = fma(d8, float(sc0 * dot0 + sc1 * dot1), acc) per Q8_1 block and tot = fma(d, acc, tot) per half-block.
@@ -76,25 +77,34 @@ __device__ __forceinline__ void load_x_block(const uint8_t* __restrict__ xb, XRe
     for (int i = 0; i < 9; ++i) r.w[i] = p[i];   // re-read by every workgroup: keep it cached
 }
 
-template <int NB>
-__device__ __forceinline__ void stage_x_block(const XRegs& r, int col, int j, uint4* lq, uint4* lrec) {
+// block j of a chunk slice: codes at lq[swz(2j)], lq[swz(2j + 1)], record at lrec[swz(j)]
+__device__ __forceinline__ void stage_codes(const uint32_t (&cw)[8], uint32_t d_bits, int j, uint4* lq, uint4* lrec) {
     int s0 = 0, s1 = 0;
 #pragma unroll
-    for (int i = 1; i <= 4; ++i) s0 = sdot4(static_cast<int>(r.w[i]), 0x01010101, s0);
+    for (int i = 0; i < 4; ++i) s0 = sdot4(static_cast<int>(cw[i]), 0x01010101, s0);
 #pragma unroll
-    for (int i = 5; i <= 8; ++i) s1 = sdot4(static_cast<int>(r.w[i]), 0x01010101, s1);
-    const float d8 = half_bits_to_float(r.w[0]);
-    lq[col * 2 * NB + swz(2 * j)] = make_uint4(r.w[1], r.w[2], r.w[3], r.w[4]);
-    lq[col * 2 * NB + swz(2 * j + 1)] = make_uint4(r.w[5], r.w[6], r.w[7], r.w[8]);
-    lrec[col * NB + swz(j)] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1),
-                                         __float_as_uint(d8), 0u);
+    for (int i = 4; i < 8; ++i) s1 = sdot4(static_cast<int>(cw[i]), 0x01010101, s1);
+    const float d8 = half_bits_to_float(d_bits);
+    lq[swz(2 * j)] = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+    lq[swz(2 * j + 1)] = make_uint4(cw[4], cw[5], cw[6], cw[7]);
+    lrec[swz(j)] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1), __float_as_uint(d8), 0u);
 }
+
+__device__ __forceinline__ void stage_x_block(const XRegs& r, int j, uint4* lq, uint4* lrec) {
+    const uint32_t cw[8] = {r.w[1], r.w[2], r.w[3], r.w[4], r.w[5], r.w[6], r.w[7], r.w[8]};
+    stage_codes(cw, r.w[0], j, lq, lrec);
+}
+
+// Activation staging.  XM 0: a chunk's Q8_1 blocks are loaded one step ahead with the weights and staged per step;
+// XM 1: the whole row (n_in <= kFullMaxIn) is staged once per workgroup, in the same per-chunk layout, while the
+// first weight chunks are in flight.  Same staged values either way.
+constexpr int kFullMaxIn = 4096;
 
 // ---- the tiled kernel ------------------------------------------------------------------------------------------------
 // Persistent: workgroup g owns row tiles g, g + G, g + 2G, ... and walks the flat sequence of (tile, chunk) steps with
 // DEPTH chunks of loads in flight in registers, across tile boundaries, so a workgroup never idles on a fresh tile's
 // first load.  Each step: park the oldest chunk in LDS, refill its registers with the chunk DEPTH steps ahead, decode.
-template <int R, int NCOLS, bool RES, int DEPTH>
+template <int R, int NCOLS, bool RES, int DEPTH, int XM>
 __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __restrict__ w,
                                                            const uint8_t* __restrict__ x, float* y,
                                                            const float* res, float* partials, int n_in, int n_out) {
@@ -105,12 +115,13 @@ __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __rest
     // LDS dwords per tile row: 16-byte aligned (the staging stores are 128-bit) and padded so that the decode's
     // dword reads of the wave's rows spread over the banks (at most 2-way; checked exhaustively for both tiles)
     constexpr int ROWW = CB * kQ6KBytes / 4 + (R == 16 ? 4 : 12);
-    constexpr int XS = NCOLS * NB;         // activation blocks to stage per chunk
-    constexpr int XP = (XS + kThreads - 1) / kThreads;
+    constexpr int XS = XM == 0 ? NCOLS * NB : 0;   // activation blocks to stage per chunk
+    constexpr int XP = XS ? (XS + kThreads - 1) / kThreads : 1;
+    constexpr int XBLK = XM == 0 ? NB : kFullMaxIn / 32;   // staged blocks per column
 
     __shared__ __attribute__((aligned(16))) uint32_t lw[R * ROWW];
-    __shared__ uint4 lq[NCOLS * 2 * NB];
-    __shared__ uint4 lrec[NCOLS * NB];
+    __shared__ uint4 lq[NCOLS * 2 * XBLK];
+    __shared__ uint4 lrec[NCOLS * XBLK];
     __shared__ float vout[NCOLS][R];
 
     const int t = threadIdx.x;
@@ -121,6 +132,7 @@ __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __rest
     const int my_tiles = (ntiles - static_cast<int>(blockIdx.x) + G - 1) / G;
     const int nsteps = my_tiles * nch;
     const int xcol_blocks = n_in / 32;
+    const int xcs = XM == 0 ? NB : nch * NB;   // staged blocks between columns
 
     u32x4 wreg[DEPTH][kLoadsPerThread];
     XRegs xreg[DEPTH][XP];
@@ -174,6 +186,18 @@ __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __rest
     for (int s = 0; s < DEPTH; ++s)
         if (s < nsteps) issue(s, wreg[s], xreg[s]);
 
+    // whole-row activations, staged once while the first weight chunks are in flight (published by the first
+    // step's barrier).  Chunk c of column col occupies blocks [col * xcs + c * NB, + NB) in the per-chunk layout.
+    if constexpr (XM == 1) {
+        for (int J = t; J < NCOLS * xcol_blocks; J += kThreads) {
+            const int col = J / xcol_blocks, jb = J - col * xcol_blocks;
+            const int c = jb / NB, j = jb - c * NB;
+            XRegs r;
+            load_x_block(x + static_cast<size_t>(J) * kQ8_1Bytes, r);
+            stage_x_block(r, j, lq + 2 * (col * xcs + c * NB), lrec + col * xcs + c * NB);
+        }
+    }
+
     for (int f0 = 0; f0 < nsteps; f0 += DEPTH) {
 #pragma unroll
         for (int s = 0; s < DEPTH; ++s) {
@@ -193,9 +217,11 @@ __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __rest
                 const int sidx = t + kThreads * p;
                 if (sidx < XS) {
                     const int col = sidx / NB, jb = sidx - col * NB;
-                    stage_x_block<NB>(xreg[s][p], col, jb, lq, lrec);
+                    stage_x_block(xreg[s][p], jb, lq + 2 * col * NB, lrec + col * NB);
                 }
             }
+            const uint4* lqc = lq + (XM == 0 ? 0 : 2 * c * NB);   // this chunk's slice of every column
+            const uint4* lrc = lrec + (XM == 0 ? 0 : c * NB);
             __syncthreads();
             if (f + DEPTH < nsteps) issue(f + DEPTH, wreg[s], xreg[s]);
 
@@ -237,9 +263,9 @@ __global__ __launch_bounds__(kThreads) void q6k_gemv_tiled(const uint8_t* __rest
                     const int j = 8 * b + 4 * n + k;
 #pragma unroll
                     for (int col = 0; col < NCOLS; ++col) {
-                        const uint4 qa = lq[col * 2 * NB + swz(2 * j)];
-                        const uint4 qb = lq[col * 2 * NB + swz(2 * j + 1)];
-                        const uint4 rec = lrec[col * NB + swz(j)];
+                        const uint4 qa = lqc[2 * col * xcs + swz(2 * j)];
+                        const uint4 qb = lqc[2 * col * xcs + swz(2 * j + 1)];
+                        const uint4 rec = lrc[col * xcs + swz(j)];
                         const int u[8] = {static_cast<int>(qa.x), static_cast<int>(qa.y), static_cast<int>(qa.z),
                                           static_cast<int>(qa.w), static_cast<int>(qb.x), static_cast<int>(qb.y),
                                           static_cast<int>(qb.z), static_cast<int>(qb.w)};
@@ -444,26 +470,40 @@ TileCfg pick_cfg(int n_in, int n_out, const void* w) {
     return cfg;
 }
 
-template <int R, int NCOLS, bool RES, int DEPTH>
+template <int R, int NCOLS, bool RES, int DEPTH, int XM>
 void launch_tiled(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in, int n_out,
                   int per_cu, hipStream_t s) {
     const int ntiles = (n_out + R - 1) / R;
     int grid = ntiles;
     if (per_cu > 0) grid = std::min(ntiles, per_cu * cu_count());
-    hipLaunchKernelGGL((q6k_gemv_tiled<R, NCOLS, RES, DEPTH>), dim3(grid), dim3(kThreads), 0, s, w, x, y, res, partials,
-                       n_in, n_out);
+    hipLaunchKernelGGL((q6k_gemv_tiled<R, NCOLS, RES, DEPTH, XM>), dim3(grid), dim3(kThreads), 0, s, w, x, y, res,
+                       partials, n_in, n_out);
+}
+
+template <int R, int NCOLS, bool RES, int XM>
+void launch_depth(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in, int n_out,
+                  const TileCfg& cfg, hipStream_t s) {
+    if (cfg.depth == 1) launch_tiled<R, NCOLS, RES, 1, XM>(w, x, y, res, partials, n_in, n_out, cfg.per_cu, s);
+    else launch_tiled<R, NCOLS, RES, 2, XM>(w, x, y, res, partials, n_in, n_out, cfg.per_cu, s);
+}
+
+// whole-row staging for rows of at most kFullMaxIn elements (shape-only choice; the staged values are the same)
+bool full_row(int n_in) {
+    static const bool on = env_int("RMI_GEMV_XFULL", 1) != 0;
+    return on && n_in <= kFullMaxIn;
 }
 
 template <int NCOLS, bool RES>
 void launch_cols(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in, int n_out,
                  hipStream_t s) {
     const TileCfg cfg = pick_cfg(n_in, n_out, w);
+    const bool full = full_row(n_in);
     if (cfg.rows == 16) {
-        if (cfg.depth == 1) launch_tiled<16, NCOLS, RES, 1>(w, x, y, res, partials, n_in, n_out, cfg.per_cu, s);
-        else launch_tiled<16, NCOLS, RES, 2>(w, x, y, res, partials, n_in, n_out, cfg.per_cu, s);
+        if (full) launch_depth<16, NCOLS, RES, 1>(w, x, y, res, partials, n_in, n_out, cfg, s);
+        else launch_depth<16, NCOLS, RES, 0>(w, x, y, res, partials, n_in, n_out, cfg, s);
     } else if (cfg.rows == 8) {
-        if (cfg.depth == 1) launch_tiled<8, NCOLS, RES, 1>(w, x, y, res, partials, n_in, n_out, cfg.per_cu, s);
-        else launch_tiled<8, NCOLS, RES, 2>(w, x, y, res, partials, n_in, n_out, cfg.per_cu, s);
+        if (full) launch_depth<8, NCOLS, RES, 1>(w, x, y, res, partials, n_in, n_out, cfg, s);
+        else launch_depth<8, NCOLS, RES, 0>(w, x, y, res, partials, n_in, n_out, cfg, s);
     } else {
         hipLaunchKernelGGL((q6k_gemv_generic<NCOLS, RES>), dim3((n_out + 3) / 4), dim3(kThreads), 0, s, w, x, y, res,
                            partials, n_in, n_out);
@@ -540,3 +580,4 @@ extern "C" int rmi_q6_k_block_dots(const void* w, const void* x_q8_1, int32_t* o
                        static_cast<const uint8_t*>(x_q8_1), out, n_in, n_out);
     return launch_status("q6_k_block_dots");
 }
+
