@@ -66,6 +66,19 @@ int rmi_native_q6_k_mmvq_res(const void* w, const void* x_q8_1, float* y, const 
 int rmi_native_q6_k_mmvq_res_n(const void* w, const void* x_q8_1, float* y, const float* res, float* partials,
                                int n_in, int n_out, int ncols, void* stream);
 
+/* Packed Q6_K: a caller-owned copy of an n_out x n_in Q6_K matrix re-laid in (4-row, 8-block) wave tiles so a
+ * wave loads each lane's half-block with contiguous 1 KB accesses (layout in mmvq_q6k_packed.hip).  Replaces the
+ * reference's registry-owned packed copy (native_q6_k_pack, mmvq:2930-3040; looked up by native_q6_k_mmvq at
+ * mmvq:3629).  n_in a multiple of 2048; packed bytes are 6720 per (4 rows x 2048 elements), the last 4-row group
+ * zero-padded.  The packed GEMVs give, bit for bit, the results of the 16-row tiled kernel (every column of an
+ * ncols >= 2 call equal to the ncols = 1 call; _res_n equal to plain + res with one partial per 4 rows). */
+size_t rmi_q6_k_packed_bytes(int n_in, int n_out);
+int rmi_q6_k_pack(const void* w, void* w_packed, int n_in, int n_out, void* stream);
+int rmi_native_q6_k_mmvq_packed(const void* w_packed, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
+                                void* stream);
+int rmi_native_q6_k_mmvq_packed_res_n(const void* w_packed, const void* x_q8_1, float* y, const float* res,
+                                      float* partials, int n_in, int n_out, int ncols, void* stream);
+
 /* Q8_0 x Q8_1.  Replaces native_q8_0_mmvq (mmvq:3732-3736; dot mmvq:835-847) and native_q8_0_mmvq_res
  * (mmvq:3326-3339, kernel mmvq:3142-3185). */
 int rmi_native_q8_0_mmvq(const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols, void* stream);

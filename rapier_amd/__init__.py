@@ -32,6 +32,10 @@ SIGNATURES = {
     "rmi_native_q6_k_mmvq": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_res": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_res_n": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_q6_k_packed_bytes": (_sz, [_i, _i]),
+    "rmi_q6_k_pack": (_i, [_vp, _vp, _i, _i, _vp]),
+    "rmi_native_q6_k_mmvq_packed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_native_q6_k_mmvq_packed_res_n": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_q6_k_block_dots": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "rmi_gen_q6_k": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
     "rmi_gen_q8_0": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
@@ -142,6 +146,27 @@ def native_q6_k_mmvq_res(w, x_q8_1, y, res, partials, n_in: int, n_out: int, str
 def native_q6_k_mmvq_res_n(w, x_q8_1, y, res, partials, n_in: int, n_out: int, ncols: int, stream=None):
     _call("rmi_native_q6_k_mmvq_res_n", _p(w), _p(x_q8_1), _p(y), _p(res), _p(partials), n_in, n_out, ncols,
           _stream(stream))
+
+
+def q6_k_packed_bytes(n_in: int, n_out: int) -> int:
+    n = lib().rmi_q6_k_packed_bytes(n_in, n_out)
+    if n == 0:
+        raise ValueError(last_error())
+    return n
+
+
+def q6_k_pack(w, w_packed, n_in: int, n_out: int, stream=None):
+    _call("rmi_q6_k_pack", _p(w), _p(w_packed), n_in, n_out, _stream(stream))
+
+
+def native_q6_k_mmvq_packed(w_packed, x_q8_1, y, n_in: int, n_out: int, ncols: int, stream=None):
+    _call("rmi_native_q6_k_mmvq_packed", _p(w_packed), _p(x_q8_1), _p(y), n_in, n_out, ncols, _stream(stream))
+
+
+def native_q6_k_mmvq_packed_res_n(w_packed, x_q8_1, y, res, partials, n_in: int, n_out: int, ncols: int,
+                                  stream=None):
+    _call("rmi_native_q6_k_mmvq_packed_res_n", _p(w_packed), _p(x_q8_1), _p(y), _p(res), _p(partials), n_in, n_out,
+          ncols, _stream(stream))
 
 
 def q6_k_block_dots(w, x_q8_1, out, n_in: int, n_out: int, stream=None):

@@ -17,6 +17,8 @@
 //   * the KV cache is fp16; the token embedding is dequantized on the device.
 #include "rmi_common.h"
 
+#include <cstdlib>
+
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
@@ -50,9 +52,11 @@ int hip_check(hipError_t e, const char* what) {
 size_t q6_bytes(int n_out, int n_in) { return static_cast<size_t>(n_out) * (n_in / 256) * kQ6KBytes; }
 size_t q81_bytes(int n) { return static_cast<size_t>(n / 32) * kQ8_1Bytes; }
 
+// A Q6_K matrix: the packed wave-tiled copy when n_in is a multiple of 2048 (every 9B matrix), else GGUF blocks.
 struct Mat {
     uint8_t* w = nullptr;
     int n_in = 0, n_out = 0;
+    bool packed = false;
 };
 
 struct Layer {
@@ -97,6 +101,8 @@ struct Engine {
     hipStream_t s = nullptr;
     bool own_stream = false;
     std::vector<void*> allocs;
+    uint8_t* gen_tmp = nullptr;   // GGUF staging for the packed matrices, only while the model is created
+    size_t gen_tmp_bytes = 0;
 
     Mat lm_head;
     uint8_t* tok_embd = nullptr;
@@ -134,6 +140,7 @@ struct Engine {
         if (ev0) (void) hipEventDestroy(ev0);
         if (ev1) (void) hipEventDestroy(ev1);
         for (void* p : allocs) (void) hipFree(p);
+        if (gen_tmp) (void) hipFree(gen_tmp);
         if (own_stream && s) (void) hipStreamDestroy(s);
     }
 
@@ -230,8 +237,31 @@ uint64_t mix_seed(uint64_t seed, int layer, int what) {
 int make_mat(Engine& e, Mat& m, int n_out, int n_in, uint64_t seed) {
     m.n_in = n_in;
     m.n_out = n_out;
-    RMI_TRY(e.alloc(&m.w, q6_bytes(n_out, n_in)));
-    return rmi_gen_q6_k(m.w, static_cast<size_t>(n_out) * (n_in / 256), seed, 1e-3f, e.s);
+    static const bool use_packed = [] {
+        const char* v = std::getenv("RMI_ENGINE_PACKED");
+        return !(v && v[0] == '0');
+    }();
+    m.packed = use_packed && n_in % 2048 == 0;
+    if (!m.packed) {
+        RMI_TRY(e.alloc(&m.w, q6_bytes(n_out, n_in)));
+        return rmi_gen_q6_k(m.w, static_cast<size_t>(n_out) * (n_in / 256), seed, 1e-3f, e.s);
+    }
+    // the seeded GGUF blocks go through the engine's staging buffer into the packed copy
+    const size_t gguf = q6_bytes(n_out, n_in);
+    if (gguf > e.gen_tmp_bytes) return fail(RMI_ERR_STATE, "engine: generation buffer too small");
+    RMI_TRY(e.alloc(&m.w, rmi_q6_k_packed_bytes(n_in, n_out)));
+    RMI_TRY(rmi_gen_q6_k(e.gen_tmp, static_cast<size_t>(n_out) * (n_in / 256), seed, 1e-3f, e.s));
+    return rmi_q6_k_pack(e.gen_tmp, m.w, n_in, n_out, e.s);
+}
+
+int gemv(Engine& e, const Mat& m, const uint8_t* xq, float* y, int nc) {
+    if (m.packed) return rmi_native_q6_k_mmvq_packed(m.w, xq, y, m.n_in, m.n_out, nc, e.s);
+    return rmi_native_q6_k_mmvq(m.w, xq, y, m.n_in, m.n_out, nc, e.s);
+}
+
+int gemv_res(Engine& e, const Mat& m, const uint8_t* xq, float* x, float* part, int nc) {
+    if (m.packed) return rmi_native_q6_k_mmvq_packed_res_n(m.w, xq, x, x, part, m.n_in, m.n_out, nc, e.s);
+    return rmi_native_q6_k_mmvq_res_n(m.w, xq, x, x, part, m.n_in, m.n_out, nc, e.s);
 }
 
 int make_vec(Engine& e, float** p, size_t n, uint64_t seed, float mean, float std) {
@@ -300,33 +330,33 @@ __global__ void neg_exp_kernel(float* p, int n) {   // ssm_a = -exp(N(0, 0.5^2))
 int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
     const auto& c = e.cfg;
     RMI_TRY(rmi_rms_quant_apply(x, L.post_norm, part, e.q8a, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(rmi_native_q6_k_mmvq(L.upgate.w, e.q8a, e.ug, c.n_embd, 2 * c.n_ff, nc, e.s));
+    RMI_TRY(gemv(e, L.upgate, e.q8a, e.ug, nc));
     RMI_TRY(rmi_swiglu_quant(e.ug, e.ug + c.n_ff, e.q8f, c.n_ff, nc, 2 * c.n_ff, e.s));
-    return rmi_native_q6_k_mmvq_res_n(L.down.w, e.q8f, x, x, part, c.n_ff, c.n_embd, nc, e.s);
+    return gemv_res(e, L.down, e.q8f, x, part, nc);
 }
 
 int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc) {
     const auto& c = e.cfg;
     RMI_TRY(rmi_rms_quant_apply(x, L.attn_norm, part, e.q8a, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(rmi_native_q6_k_mmvq(L.in_proj.w, e.q8a, e.proj, c.n_embd, e.q3_rows, nc, e.s));
+    RMI_TRY(gemv(e, L.in_proj, e.q8a, e.proj, nc));
     RMI_TRY(rmi_attn_prep(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, e.qbuf, c.n_head, c.n_kv, c.head_dim,
                           c.n_rot, c.rope_theta, c.eps, nc, e.max_ctx, e.s));
     RMI_TRY(rmi_gqa_flash_decode(e.qbuf, L.kc, L.vc, pos, e.proj, e.q3_rows, nullptr, 0, e.q8y,
                                  static_cast<int>(q81_bytes(e.attn_q)), e.attn_ws, c.n_head, c.n_kv, c.head_dim, nc,
                                  e.max_ctx, e.nsub, 1.0f / sqrtf(static_cast<float>(c.head_dim)), e.s));
-    RMI_TRY(rmi_native_q6_k_mmvq_res_n(L.out_proj.w, e.q8y, x, x, part, e.attn_q, c.n_embd, nc, e.s));
+    RMI_TRY(gemv_res(e, L.out_proj, e.q8y, x, part, nc));
     return ffn(e, L, x, part, nc);
 }
 
 int gdn_block(Engine& e, Layer& L, int nc) {
     const auto& c = e.cfg;
     RMI_TRY(rmi_rms_quant_apply(e.x, L.attn_norm, e.part, e.q8a, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(rmi_native_q6_k_mmvq(L.in_proj.w, e.q8a, e.proj, c.n_embd, e.qkvz_rows, nc, e.s));
+    RMI_TRY(gemv(e, L.in_proj, e.q8a, e.proj, nc));
     const int qkvz = 2 * c.ssm_h_k * kS + 2 * c.ssm_h_v * kS;
     RMI_TRY(rmi_gdn_layer_tokens(L.state[0], L.state[1], L.hist[0], L.hist[1], e.ints + kSel, e.proj, e.qkvz_rows,
                                  e.proj + qkvz, e.qkvz_rows, L.conv_w, L.dt, L.ssm_a, L.ssm_norm, c.eps, e.y, e.gdn_v,
                                  e.q8y, static_cast<int>(q81_bytes(e.gdn_v)), c.ssm_h_k, c.ssm_h_v, nc, e.s));
-    RMI_TRY(rmi_native_q6_k_mmvq_res_n(L.out_proj.w, e.q8y, e.x, e.x, e.part, e.gdn_v, c.n_embd, nc, e.s));
+    RMI_TRY(gemv_res(e, L.out_proj, e.q8y, e.x, e.part, nc));
     return ffn(e, L, e.x, e.part, nc);
 }
 
@@ -340,7 +370,7 @@ int trunk(Engine& e, int nc) {
         else RMI_TRY(attn_block(e, L, e.x, e.part, e.ints + kPos, nc));
     }
     RMI_TRY(rmi_rms_quant_apply(e.x, e.out_norm, e.part, e.q8a, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(rmi_native_q6_k_mmvq(e.lm_head.w, e.q8a, e.logits, c.n_embd, c.n_vocab, nc, e.s));
+    RMI_TRY(gemv(e, e.lm_head, e.q8a, e.logits, nc));
     RMI_TRY(rmi_argmax(e.logits, c.n_vocab, nc, c.n_vocab, e.ints + kV0, e.argmax_ws, e.s));
     return rmi_rms_norm_out(e.x, e.out_norm, e.part, e.hsave, e.hpart, c.n_embd, c.eps, nc, e.s);
 }
@@ -354,12 +384,12 @@ int draft_block(Engine& e, const float* h, const float* hp, int nc, bool with_he
     RMI_TRY(rmi_rms_norm_out_strided(h, e.hnorm, hp, e.eh + c.n_embd, 2 * c.n_embd, nullptr, c.n_embd, c.eps, nc,
                                      e.s));
     RMI_TRY(rmi_native_quantize_q8_1(e.eh, e.q8f, 2 * c.n_embd, nc, e.s));
-    RMI_TRY(rmi_native_q6_k_mmvq(e.eh_proj.w, e.q8f, e.dx, 2 * c.n_embd, c.n_embd, nc, e.s));
+    RMI_TRY(gemv(e, e.eh_proj, e.q8f, e.dx, nc));
     RMI_TRY(rmi_row_sum_partials(e.dx, e.dpart, c.n_embd, nc, e.s));
     RMI_TRY(attn_block(e, e.draft, e.dx, e.dpart, e.ints + kDPos, nc));
     if (!with_head) return RMI_OK;
     RMI_TRY(rmi_rms_quant_apply(e.dx, e.shnorm, e.dpart, e.q8a, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(rmi_native_q6_k_mmvq(e.lm_head.w, e.q8a, e.logits, c.n_embd, c.n_vocab, nc, e.s));
+    RMI_TRY(gemv(e, e.lm_head, e.q8a, e.logits, nc));
     return rmi_argmax(e.logits, c.n_vocab, nc, c.n_vocab, e.ints + kC0, e.argmax_ws, e.s);
 }
 
@@ -470,6 +500,10 @@ extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int
     e.max_in = std::max({c.n_ff, 2 * c.n_embd, e.gdn_v, e.attn_q});
 
     // model (all Q6_K matrices random-init as in the benchmark configs)
+    e.gen_tmp_bytes = std::max({q6_bytes(c.n_vocab, c.n_embd), q6_bytes(2 * c.n_ff, c.n_embd), q6_bytes(c.n_embd, c.n_ff),
+                                q6_bytes(std::max(e.qkvz_rows, e.q3_rows), c.n_embd),
+                                q6_bytes(c.n_embd, std::max(e.gdn_v, e.attn_q)), q6_bytes(c.n_embd, 2 * c.n_embd)});
+    HIP_TRY(hipMalloc(&e.gen_tmp, e.gen_tmp_bytes));
     RMI_TRY(e.alloc(&e.tok_embd, q6_bytes(c.n_vocab, c.n_embd)));
     RMI_TRY(rmi_gen_q6_k(e.tok_embd, static_cast<size_t>(c.n_vocab) * (c.n_embd / 256), mix_seed(seed, -1, 1), 1e-3f,
                          e.s));
@@ -489,6 +523,9 @@ extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int
     RMI_TRY(make_vec(e, &e.enorm, c.n_embd, mix_seed(seed, c.n_layer, 11), 1.0f, 0.1f));
     RMI_TRY(make_vec(e, &e.hnorm, c.n_embd, mix_seed(seed, c.n_layer, 12), 1.0f, 0.1f));
     RMI_TRY(make_vec(e, &e.shnorm, c.n_embd, mix_seed(seed, c.n_layer, 13), 1.0f, 0.1f));
+    HIP_TRY(hipStreamSynchronize(e.s));   // every pack has read the staging buffer
+    HIP_TRY(hipFree(e.gen_tmp));
+    e.gen_tmp = nullptr;
 
     // round state and activations (two columns)
     RMI_TRY(e.alloc(&e.ints, 64));

@@ -23,7 +23,6 @@ __device__ float block_sum_partials(const float* __restrict__ p, int np) {
     return tot;
 }
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 __device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
 
 // Q8_1 of (x * w) * inv, one lane per element (reference rms_quant_apply_kernel, qw:627-655)

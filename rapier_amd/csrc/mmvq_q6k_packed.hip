@@ -1,0 +1,363 @@
+// mmvq_q6k_packed.hip - Q6_K x Q8_1 GEMV over a wave-tiled copy of the weights (caller-owned), for gfx950.
+//
+// Reference: the reference keeps an opt-in packed copy of a Q6_K matrix in a registry (native_q6_k_pack,
+// src/native_mmvq.cu:2930-3040; used by native_q6_k_mmvq at mmvq:3629 when STRATA_Q6_PACKED=1).  Here the caller
+// owns the packed buffer (rmi_q6_k_packed_bytes / rmi_q6_k_pack) and calls the packed GEMV on it directly.
+//
+// Packed layout.  Rows are grouped in quads (4 rows; the last quad zero-padded) and each row is cut in chunks of 8
+// Q6_K blocks (2048 elements).  The 6720 bytes of one (quad, chunk) wave tile are re-laid so that lane l = 16 r + hb
+// (row r of the quad, half-block hb: block hb / 2, half hb % 2) finds its half-block in registers after fully
+// coalesced loads:
+//     [    0, 4096)  ql: 16-byte unit u (0..3) of lane l at u * 1024 + 16 l   (ql bytes [64 n + 16 u, +16))
+//     [ 4096, 6144)  qh: unit u (0..1) of lane l at 4096 + u * 1024 + 16 l    (qh bytes [32 n + 16 u, +16))
+//     [ 6144, 6656)  sc: lane l's 8 sub-scales at 6144 + 8 l                  (sc bytes [8 n, +8))
+//     [ 6656, 6720)  d:  block (r, b)'s fp16 scale at 6656 + 2 (8 r + b)
+// Wave tiles are stored quad-major: tile (q, c) at (q * nch + c) * 6720.
+//
+// Kernel: every wave streams its own quads (no workgroup barrier after the activation staging): the (quad, chunk)
+// steps of its quads are loaded D steps ahead straight into registers (8 loads per step per lane, each a contiguous
+// 1 KB / 512 B wave access), decoded as in the tiled kernel (v_dot4 with the "-32" folded into the staged record),
+// and a row's 16 lanes are reduced by the same xor butterfly.  Lane ownership, per-lane accumulation order and the
+// reduction tree are those of the 16-row tiled kernel, so the results are bitwise the same, every column of an
+// ncols >= 2 call is bitwise the ncols = 1 result, and the residual variant is bitwise plain + res.
+#include "rmi_common.h"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace rmi {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kQuad = 4;                                  // rows per wave tile
+constexpr int kChunkBlocks = 8;                           // Q6_K blocks per row per chunk
+constexpr int kChunkElems = kChunkBlocks * 256;           // 2048
+constexpr int kWaveTile = kQuad * kChunkBlocks * kQ6KBytes;   // 6720
+constexpr int kNB = kChunkElems / 32;                     // Q8_1 blocks per chunk per column (64)
+constexpr int kMaxStageBytes = 64 * 1024;                 // activation LDS per workgroup
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int swz(int u) { return u ^ ((u >> 3) & 7); }
+
+__device__ __forceinline__ int sc_byte2(uint32_t s0, uint32_t s1, int i) {
+    const uint32_t w = i < 4 ? s0 : s1;
+    return static_cast<int>(static_cast<int8_t>((w >> (8 * (i & 3))) & 0xffu));
+}
+
+__device__ __forceinline__ int subblock_dot(const int (&v)[8], const int (&u)[8], int corr0, int corr1, int sc0,
+                                            int sc1) {
+    int d0 = corr0, d1 = corr1;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) d0 = sdot4(v[w], u[w], d0);
+#pragma unroll
+    for (int w = 4; w < 8; ++w) d1 = sdot4(v[w], u[w], d1);
+    return __mul24(sc0, d0) + __mul24(sc1, d1);   // |sc|, |d| < 2^23: exact
+}
+
+// ---- pack: one thread per (quad, chunk, lane) --------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void q6k_pack_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ wp,
+                                                            int n_in, int n_out, size_t nslots) {
+    const size_t gid = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (gid >= nslots) return;
+    const int nch = n_in / kChunkElems, nb = n_in / 256;
+    const int l = static_cast<int>(gid & 63);
+    const size_t tile = gid >> 6;                         // q * nch + c
+    const int q = static_cast<int>(tile / nch), c = static_cast<int>(tile - static_cast<size_t>(q) * nch);
+    const int r = l >> 4, hb = l & 15, b = hb >> 1, n = hb & 1;
+    const int row = kQuad * q + r;
+    uint8_t* dst = wp + tile * kWaveTile;
+    const bool live = row < n_out;
+    const uint8_t* src = w + (static_cast<size_t>(row) * nb + static_cast<size_t>(c) * kChunkBlocks + b) * kQ6KBytes;
+    for (int u = 0; u < 4; ++u)
+        for (int i = 0; i < 16; ++i) dst[u * 1024 + 16 * l + i] = live ? src[64 * n + 16 * u + i] : 0;
+    for (int u = 0; u < 2; ++u)
+        for (int i = 0; i < 16; ++i) dst[4096 + u * 1024 + 16 * l + i] = live ? src[128 + 32 * n + 16 * u + i] : 0;
+    for (int i = 0; i < 8; ++i) dst[6144 + 8 * l + i] = live ? src[192 + 8 * n + i] : 0;
+    if (n == 0) {
+        dst[6656 + 2 * (8 * r + b)] = live ? src[208] : 0;
+        dst[6656 + 2 * (8 * r + b) + 1] = live ? src[209] : 0;
+    }
+}
+
+// ---- GEMV ---------------------------------------------------------------------------------------------------------------
+struct WTile {
+    u32x4 ql[4];
+    u32x4 qh[2];
+    uint2 sc;
+    uint32_t d;
+};
+
+// ---- shared pieces -------------------------------------------------------------------------------------------------
+// whole-row activations, staged once per workgroup while the first weight steps are in flight: block J of column
+// col (chunk c = jb / 64, j = jb % 64) -> codes lq[2 (col * nbt + 64 c) + swz(2j), +1], record lrec[...]
+__device__ __forceinline__ void stage_activations(const uint8_t* __restrict__ x, int nblocks, int nbt, uint4* lq,
+                                                  uint4* lrec, int t, int nthreads) {
+    for (int J = t; J < nblocks; J += nthreads) {
+        const int col = J / nbt, jb = J - col * nbt;
+        const int c = jb / kNB, j = jb - c * kNB;
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
+        uint32_t wv[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) wv[i] = p[i];
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 1; i <= 4; ++i) s0 = sdot4(static_cast<int>(wv[i]), 0x01010101, s0);
+#pragma unroll
+        for (int i = 5; i <= 8; ++i) s1 = sdot4(static_cast<int>(wv[i]), 0x01010101, s1);
+        uint4* q = lq + 2 * (col * nbt + c * kNB);
+        q[swz(2 * j)] = make_uint4(wv[1], wv[2], wv[3], wv[4]);
+        q[swz(2 * j + 1)] = make_uint4(wv[5], wv[6], wv[7], wv[8]);
+        lrec[col * nbt + c * kNB + swz(j)] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1),
+                                                        __float_as_uint(half_bits_to_float(wv[0])), 0u);
+    }
+}
+
+// one wave tile step of lane l: its half-block (row l / 16, half-block l % 16) against every column's staged chunk
+template <int NCOLS>
+__device__ __forceinline__ void accumulate_step(const WTile& wt, int lane, const uint4* lqc, const uint4* lrc, int xcs,
+                                                float (&tot)[NCOLS]) {
+    const int hb = lane & 15, b = hb >> 1, n = hb & 1;
+    uint32_t Q[16], H[8];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) Q[i] = wt.ql[i >> 2][i & 3];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) H[i] = wt.qh[i >> 2][i & 3];
+    const uint32_t S0 = wt.sc.x, S1 = wt.sc.y;
+    const float d = half_bits_to_float(wt.d);
+
+    float acc[NCOLS];
+#pragma unroll
+    for (int col = 0; col < NCOLS; ++col) acc[col] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            const int k = kk + 2 * kh;
+            int v[8];
+#pragma unroll
+            for (int ww = 0; ww < 8; ++ww)
+                v[ww] = static_cast<int>(((Q[8 * kk + ww] >> (4 * kh)) & 0x0f0f0f0fu) |
+                                         (((H[ww] >> (2 * k)) & 0x03030303u) << 4));
+            const int sc0 = sc_byte2(S0, S1, 2 * k), sc1 = sc_byte2(S0, S1, 2 * k + 1);
+            const int j = 8 * b + 4 * n + k;
+#pragma unroll
+            for (int col = 0; col < NCOLS; ++col) {
+                const uint4 qa = lqc[2 * col * xcs + swz(2 * j)];
+                const uint4 qb = lqc[2 * col * xcs + swz(2 * j + 1)];
+                const uint4 rec = lrc[col * xcs + swz(j)];
+                const int u[8] = {static_cast<int>(qa.x), static_cast<int>(qa.y), static_cast<int>(qa.z),
+                                  static_cast<int>(qa.w), static_cast<int>(qb.x), static_cast<int>(qb.y),
+                                  static_cast<int>(qb.z), static_cast<int>(qb.w)};
+                const int sd = subblock_dot(v, u, static_cast<int>(rec.x), static_cast<int>(rec.y), sc0, sc1);
+                acc[col] = __builtin_fmaf(__uint_as_float(rec.z), static_cast<float>(sd), acc[col]);
+            }
+        }
+    }
+#pragma unroll
+    for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
+}
+
+template <int NCOLS, bool RES, int D>
+__global__ __launch_bounds__(kThreads) void q6k_packed_gemv(const uint8_t* __restrict__ wp,
+                                                            const uint8_t* __restrict__ x, float* y,
+                                                            const float* res, float* partials, int n_in, int n_out) {
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int nch = n_in / kChunkElems;
+    const int nbt = n_in / 32;                   // Q8_1 blocks per column
+    const int xcs = nch * kNB;                   // staged blocks between columns (= nbt)
+    uint4* lq = smem;                            // codes: 2 units per block
+    uint4* lrec = smem + 2 * NCOLS * nbt;        // records
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    const int GW = static_cast<int>(gridDim.x) * (kThreads / 64);
+    const int gw = static_cast<int>(blockIdx.x) * (kThreads / 64) + (t >> 6);
+    const int my_quads = gw < nq ? (nq - 1 - gw) / GW + 1 : 0;
+    const int nsteps = my_quads * nch;
+
+    WTile buf[D];
+    auto issue = [&](int f, WTile& b) {
+        const int qi = f / nch, c = f - qi * nch;
+        const uint8_t* base = wp + (static_cast<size_t>(gw + qi * GW) * nch + c) * kWaveTile;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            b.ql[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * 1024 + 16 * lane));
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            b.qh[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + 4096 + u * 1024 + 16 * lane));
+        b.sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
+        b.d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (8 * (lane >> 4) + ((lane & 15) >> 1)));
+    };
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+        if (s < nsteps) issue(s, buf[s]);
+
+    stage_activations(x, NCOLS * nbt, nbt, lq, lrec, t, kThreads);
+    __syncthreads();
+
+    const int r = lane >> 4, hb = lane & 15;
+    float tot[NCOLS];
+#pragma unroll
+    for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
+
+    for (int f0 = 0; f0 < nsteps; f0 += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int f = f0 + s;
+            if (f >= nsteps) break;   // uniform across the wave
+            const int qi = f / nch, c = f - qi * nch;
+            const WTile cur = buf[s];
+            if (f + D < nsteps) issue(f + D, buf[s]);
+            accumulate_step<NCOLS>(cur, lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, tot);
+
+            if (c == nch - 1) {   // the quad's rows are complete
+                const int q = gw + qi * GW;
+                const int row = kQuad * q + r;
+                const int np = (n_out + 3) / 4;
+#pragma unroll
+                for (int col = 0; col < NCOLS; ++col) {
+                    float v = group_sum<16>(tot[col]);
+                    tot[col] = 0.0f;
+                    if constexpr (RES) {
+                        if (row < n_out) v += res[static_cast<size_t>(col) * n_out + row];
+                    }
+                    if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v;
+                    if constexpr (RES) {
+                        // partial of the quad: squares of its rows in row order (lanes 0, 16, 32, 48)
+                        const float v0 = __shfl(v, 0, 64), v1 = __shfl(v, 16, 64);
+                        const float v2 = __shfl(v, 32, 64), v3 = __shfl(v, 48, 64);
+                        if (lane == 0) {
+                            const int row0 = kQuad * q;
+                            float p = __builtin_fmaf(v0, v0, 0.0f);
+                            if (row0 + 1 < n_out) p = __builtin_fmaf(v1, v1, p);
+                            if (row0 + 2 < n_out) p = __builtin_fmaf(v2, v2, p);
+                            if (row0 + 3 < n_out) p = __builtin_fmaf(v3, v3, p);
+                            partials[static_cast<size_t>(col) * np + q] = p;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+int env_int(const char* name, int def) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : def;
+}
+
+int cu_count() {
+    static int n = [] {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            c = 256;
+        return c > 0 ? c : 256;
+    }();
+    return n;
+}
+
+// waves: at most per_cu workgroups per CU, and an even split of the quads over them
+int packed_grid(int nq) {
+    static const int per_cu = env_int("RMI_PACKED_PER_CU", 4);
+    const int max_waves = std::max(1, per_cu) * cu_count() * (kThreads / 64);
+    const int qpw = (nq + max_waves - 1) / max_waves;
+    const int waves = (nq + qpw - 1) / qpw;
+    return (waves + 3) / 4;
+}
+
+template <int NCOLS, bool RES>
+void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
+                   int n_out, hipStream_t s) {
+    static const int depth = env_int("RMI_PACKED_DEPTH", 2);
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    const size_t lds = static_cast<size_t>(NCOLS) * (n_in / 32) * 48;
+    const dim3 grid(packed_grid(nq)), block(kThreads);
+    if (depth >= 4)
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+    else if (depth == 3)
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 3>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+    else
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 2>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+}
+
+// columns per pass: at most 4, and the pass's staged activations within kMaxStageBytes
+int cols_per_pass(int n_in) {
+    const int per = kMaxStageBytes / ((n_in / 32) * 48);
+    return std::max(1, std::min(4, per));
+}
+
+template <bool RES>
+int run_packed(const void* wpv, const void* xv, float* y, const float* res, float* partials, int n_in, int n_out,
+               int ncols, hipStream_t s) {
+    const auto* wp = static_cast<const uint8_t*>(wpv);
+    const auto* x = static_cast<const uint8_t*>(xv);
+    const int per = cols_per_pass(n_in);
+    const size_t xcol = static_cast<size_t>(n_in / 32) * kQ8_1Bytes;
+    const size_t pcol = static_cast<size_t>((n_out + 3) / 4);
+    for (int j = 0; j < ncols; j += per) {
+        const int nj = std::min(per, ncols - j);
+        const uint8_t* xj = x + j * xcol;
+        float* yj = y + static_cast<size_t>(j) * n_out;
+        const float* rj = RES ? res + static_cast<size_t>(j) * n_out : nullptr;
+        float* pj = RES ? partials + j * pcol : nullptr;
+        switch (nj) {
+            case 1: launch_packed<1, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
+            case 2: launch_packed<2, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
+            case 3: launch_packed<3, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
+            default: launch_packed<4, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
+        }
+        if (const int rc = launch_status("native_q6_k_mmvq_packed")) return rc;
+    }
+    return RMI_OK;
+}
+
+int validate_packed(const void* wp, const void* x, const float* y, int n_in, int n_out, int ncols, void* stream) {
+    if (n_in <= 0 || n_in % kChunkElems != 0 || (n_in / 32) * 48 > kMaxStageBytes)
+        return fail(RMI_ERR_SHAPE, "packed Q6_K GEMV requires n_in a multiple of 2048 and at most 43690");
+    if (ncols < 1 || ncols > kMaxCols) return fail(RMI_ERR_SHAPE, "native MMVQ requires 1 <= ncols <= 16");
+    if (n_out <= 0) return fail(RMI_ERR_SHAPE, "native MMVQ requires n_out > 0");
+    if (!aligned16(wp) || !aligned4(x) || !aligned4(y))
+        return fail(RMI_ERR_POINTER, "packed Q6_K GEMV requires a 16-byte aligned packed matrix and 4-byte aligned x, y");
+    if (!stream) return fail(RMI_ERR_STREAM, "native MMVQ requires an explicit non-null CUDA stream");
+    return RMI_OK;
+}
+
+}  // namespace
+}  // namespace rmi
+
+using namespace rmi;
+
+extern "C" size_t rmi_q6_k_packed_bytes(int n_in, int n_out) {
+    if (n_in <= 0 || n_in % kChunkElems != 0 || n_out <= 0) {
+        set_error("q6_k_packed_bytes: n_in must be a positive multiple of 2048 and n_out positive");
+        return 0;
+    }
+    return static_cast<size_t>((n_out + kQuad - 1) / kQuad) * (n_in / kChunkElems) * kWaveTile;
+}
+
+extern "C" int rmi_q6_k_pack(const void* w, void* w_packed, int n_in, int n_out, void* stream) {
+    if (n_in <= 0 || n_in % kChunkElems != 0 || n_out <= 0)
+        return fail(RMI_ERR_SHAPE, "q6_k_pack: n_in must be a positive multiple of 2048 and n_out positive");
+    if (!w || !aligned16(w_packed)) return fail(RMI_ERR_POINTER, "q6_k_pack: null weights or misaligned packed buffer");
+    const size_t nslots = static_cast<size_t>((n_out + kQuad - 1) / kQuad) * (n_in / kChunkElems) * 64;
+    hipLaunchKernelGGL(q6k_pack_kernel, dim3(static_cast<unsigned>((nslots + kThreads - 1) / kThreads)), dim3(kThreads),
+                       0, static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(w),
+                       static_cast<uint8_t*>(w_packed), n_in, n_out, nslots);
+    return launch_status("q6_k_pack");
+}
+
+extern "C" int rmi_native_q6_k_mmvq_packed(const void* w_packed, const void* x_q8_1, float* y, int n_in, int n_out,
+                                           int ncols, void* stream) {
+    if (int rc = validate_packed(w_packed, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
+    return run_packed<false>(w_packed, x_q8_1, y, nullptr, nullptr, n_in, n_out, ncols,
+                             static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rmi_native_q6_k_mmvq_packed_res_n(const void* w_packed, const void* x_q8_1, float* y, const float* res,
+                                                 float* partials, int n_in, int n_out, int ncols, void* stream) {
+    if (int rc = validate_packed(w_packed, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
+    if (!aligned4(res) || !aligned4(partials))
+        return fail(RMI_ERR_POINTER, "native MMVQ requires non-null 4-byte aligned device pointers");
+    return run_packed<true>(w_packed, x_q8_1, y, res, partials, n_in, n_out, ncols, static_cast<hipStream_t>(stream));
+}
+

@@ -68,4 +68,6 @@ __device__ __forceinline__ void q8_1_store_lane(float v, uint8_t* block) {
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
 }  // namespace rmi

@@ -1,0 +1,102 @@
+"""GPU parity of the packed Q6_K GEMV (caller-owned wave-tiled copy of the weights).
+
+Bars: within 1e-3 relative of the oracle's fp64 GEMV (|err| <= 1e-3 |ref| + 1e-5 max|ref|); bitwise equal to the
+16-row tiled GEMV on the GGUF layout where the dispatcher picks 16-row tiles (same lane ownership and reduction
+tree); ncols = 2 columns bitwise equal to ncols = 1; residual variant bitwise plain + res with partials = sum of the
+4 rows' squares in row order (src/test_res.cpp:57-112).  Ragged n_out pads the last 4-row group with zeros.
+"""
+import numpy as np
+import pytest
+
+from tests.gpu_util import assert_close_rel, dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def rmi():
+    import rapier_amd
+    rapier_amd.lib()
+    return rapier_amd
+
+
+def packed(rmi, w_dev, n_in, n_out):
+    wp = empty(rmi.q6_k_packed_bytes(n_in, n_out), "uint8")
+    rmi.q6_k_pack(w_dev, wp, n_in, n_out)
+    return wp
+
+
+# (n_in, n_out): config-1 shape, the GDN in-projection, a ragged count, the FFN down projection, the draft eh_proj
+SHAPES = [(4096, 12288), (4096, 12352), (2048, 1001), (12288, 4096), (8192, 4096), (4096, 70)]
+
+
+@pytest.mark.parametrize("n_in,n_out", SHAPES)
+def test_packed_matches_oracle_and_columns(orc, rmi, n_in, n_out):
+    w = orc.gen_q6k(n_out, n_in, seed=n_in + 3 * n_out)
+    x = orc.normal(2 * n_in, seed=n_out + 1)
+    xq = orc.quantize_q8_1(x, n_in, 2)
+    wd, xd = dev(w), dev(xq)
+    wp = packed(rmi, wd, n_in, n_out)
+    y2 = empty(2 * n_out)
+    rmi.native_q6_k_mmvq_packed(wp, xd, y2, n_in, n_out, 2)
+    y2h = host(y2)
+    ref = orc.q6k_gemv(w, xq, n_in, n_out, ncols=2)
+    for c in range(2):
+        assert_close_rel(y2h[c * n_out:(c + 1) * n_out], ref[c * n_out:(c + 1) * n_out], what=f"packed col {c}")
+        y1 = empty(n_out)
+        xc = dev(xq[c * (n_in // 32) * 36:(c + 1) * (n_in // 32) * 36])
+        rmi.native_q6_k_mmvq_packed(wp, xc, y1, n_in, n_out, 1)
+        assert np.array_equal(host(y1).view(np.uint32), y2h[c * n_out:(c + 1) * n_out].view(np.uint32))
+
+
+@pytest.mark.parametrize("n_in,n_out", [(4096, 12352), (2048, 1001), (4096, 24576)])
+def test_packed_bitwise_equals_16_row_tiles(orc, rmi, n_in, n_out):
+    w = orc.gen_q6k(n_out, n_in, seed=7 * n_out)
+    xq = orc.quantize_q8_1(orc.normal(2 * n_in, seed=n_in), n_in, 2)
+    wd, xd = dev(w), dev(xq)
+    wp = packed(rmi, wd, n_in, n_out)
+    yp, yt = empty(2 * n_out), empty(2 * n_out)
+    rmi.native_q6_k_mmvq_packed(wp, xd, yp, n_in, n_out, 2)
+    rmi.native_q6_k_mmvq(wd, xd, yt, n_in, n_out, 2)     # 16-row tiles for these shapes
+    assert np.array_equal(host(yp).view(np.uint32), host(yt).view(np.uint32))
+
+
+@pytest.mark.parametrize("n_in,n_out,ncols", [(12288, 4096, 2), (4096, 4096, 1), (2048, 1001, 3), (4096, 520, 5)])
+def test_packed_residual(orc, rmi, n_in, n_out, ncols):
+    w = orc.gen_q6k(n_out, n_in, seed=n_out + ncols)
+    xq = orc.quantize_q8_1(orc.normal(ncols * n_in, seed=n_in + 2), n_in, ncols)
+    res = orc.normal(ncols * n_out, seed=n_out + 9)
+    wd, xd = dev(w), dev(xq)
+    wp = packed(rmi, wd, n_in, n_out)
+    y0 = empty(ncols * n_out)
+    rmi.native_q6_k_mmvq_packed(wp, xd, y0, n_in, n_out, ncols)
+    y = dev(res.copy())                                   # y aliases res, as the engine calls it
+    np_ = (n_out + 3) // 4
+    part = empty(ncols * np_)
+    rmi.native_q6_k_mmvq_packed_res_n(wp, xd, y, y, part, n_in, n_out, ncols)
+    yh, ph = host(y), host(part)
+    assert np.array_equal(yh.view(np.uint32), (host(y0) + res).view(np.uint32))
+    for c in range(ncols):
+        v = yh[c * n_out:(c + 1) * n_out]
+        vp = np.zeros(4 * np_, np.float64)
+        vp[:n_out] = v
+        want = (vp.reshape(np_, 4) ** 2).sum(1)
+        assert np.allclose(ph[c * np_:(c + 1) * np_], want, rtol=1e-6, atol=0), f"partials col {c}"
+
+
+def test_packed_layout_roundtrip(orc, rmi):
+    """the pack is a permutation of the GGUF bytes (plus zero padding): same multiset of bytes per wave tile set"""
+    n_in, n_out = 2048, 6
+    w = orc.gen_q6k(n_out, n_in, seed=5)
+    wp = host(packed(rmi, dev(w), n_in, n_out))
+    assert wp.size == 2 * 6720
+    tile0 = wp[:6720]
+    rows0 = w.reshape(n_out, -1)[:4].reshape(-1)
+    assert np.array_equal(np.sort(tile0), np.sort(rows0))
+    # lane 0 (row 0, block 0, half 0): ql bytes [0, 16) at offset 0, qh [128, 144) at 4096, sc [192, 200) at 6144
+    blk = w[:210]
+    assert np.array_equal(tile0[0:16], blk[0:16])
+    assert np.array_equal(tile0[4096:4112], blk[128:144])
+    assert np.array_equal(tile0[6144:6152], blk[192:200])
+    assert np.array_equal(tile0[6656:6658], blk[208:210])
+
