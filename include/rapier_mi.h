@@ -151,8 +151,10 @@ int rmi_fused_gdn_conv_l2(float* history, const float* qkv, const float* conv_w,
 int rmi_fused_gdn_step_norm_silu_q8(float* state, const float* q, const float* k, const float* v, const float* gate,
                                     const float* beta, const float* z, const float* gamma, float eps, float* y,
                                     uint8_t* q8, int h_k, int h_v, void* stream);
-/* The whole GDN chain of one layer for ntok = 1 (decode) or 2 (verify) tokens: conv + SiLU + L2, beta/decay from the
- * raw beta|alpha GEMV output, the step with the state in registers across both tokens, norm * silu gate, Q8_1.
+/* The whole GDN chain of one layer for ntok = 1 (decode) or 2 (verify) tokens in one launch: conv + SiLU + L2,
+ * beta/decay from the raw beta|alpha GEMV output, the step with the state in registers across both tokens, norm *
+ * silu gate, Q8_1.  qkvz and ab are read only.  The conv history is kept per value head, [h_v][q 128 | k 128 | v 128][3]
+ * (value head h sees k-head h % h_k), so each of the two value heads of a k-head owns a copy of its q/k history.
  * state_a/state_b and hist_a/hist_b are the two buffers of the selector *sel (live = sel ? b : a).  With ntok = 2
  * the state and history after token 0 go to the non-live buffers, so a rejected draft is rolled back by flipping
  * *sel.  No reference counterpart as one call: replaces beta_gate + fused_gdn_conv_l2 + fused_gdn_step_norm_silu_q8

@@ -51,6 +51,8 @@ int hip_check(hipError_t e, const char* what) {
 
 size_t q6_bytes(int n_out, int n_in) { return static_cast<size_t>(n_out) * (n_in / 256) * kQ6KBytes; }
 size_t q81_bytes(int n) { return static_cast<size_t>(n / 32) * kQ8_1Bytes; }
+// conv history of one GDN layer, per value head: [h_v][q 128 | k 128 | v 128][3]
+size_t hist_floats(const rmi_model_config& c) { return static_cast<size_t>(c.ssm_h_v) * 3 * kS * 3; }
 
 // A Q6_K matrix: the packed wave-tiled copy when n_in is a multiple of 2048 (every 9B matrix), else GGUF blocks.
 struct Mat {
@@ -314,11 +316,21 @@ int make_gdn(Engine& e, Layer& L, int li, uint64_t seed) {
     const size_t st = static_cast<size_t>(kS) * c.ssm_h_v * kS;
     for (int b = 0; b < 2; ++b) {
         RMI_TRY(e.alloc(&L.state[b], st));
-        RMI_TRY(e.alloc(&L.hist[b], static_cast<size_t>(3) * ch));
+        RMI_TRY(e.alloc(&L.hist[b], hist_floats(c)));
         RMI_TRY(zero_f32(e, L.state[b], st));
-        RMI_TRY(zero_f32(e, L.hist[b], static_cast<size_t>(3) * ch));
+        RMI_TRY(zero_f32(e, L.hist[b], hist_floats(c)));
     }
     return RMI_OK;
+}
+
+// per-value-head copy of a [channels][3] conv history: head h takes k-head h % h_k's q and k channels and its v
+__global__ void hist_expand_kernel(const float* __restrict__ std_hist, float* __restrict__ per_head, int h_k, int h_v) {
+    const int i = blockIdx.x * 256 + threadIdx.x;   // (head, kind, j)
+    if (i >= h_v * 3 * kS) return;
+    const int head = i / (3 * kS), kind = (i / kS) % 3, j = i % kS;
+    const int qh = head % h_k;
+    const int c = kind == 0 ? qh * kS + j : kind == 1 ? (h_k + qh) * kS + j : (2 * h_k + head) * kS + j;
+    for (int t = 0; t < 3; ++t) per_head[3 * i + t] = std_hist[3 * c + t];
 }
 
 __global__ void neg_exp_kernel(float* p, int n) {   // ssm_a = -exp(N(0, 0.5^2))
@@ -568,7 +580,7 @@ extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int
         if (!L.gdn) continue;
         float *s0 = nullptr, *h0 = nullptr;
         RMI_TRY(e.alloc(&s0, static_cast<size_t>(kS) * c.ssm_h_v * kS));
-        RMI_TRY(e.alloc(&h0, static_cast<size_t>(3) * (2 * c.ssm_h_k + c.ssm_h_v) * kS));
+        RMI_TRY(e.alloc(&h0, hist_floats(c)));
         e.saved_state.push_back(s0);
         e.saved_hist.push_back(h0);
     }
@@ -628,9 +640,14 @@ extern "C" int rmi_engine_synth_context(rmi_engine* h, int n_ctx, uint64_t seed,
     for (auto& L : e.layers) {
         if (L.gdn) {
             const size_t st = static_cast<size_t>(kS) * c.ssm_h_v * kS;
+            // a [channels][3] history N(0, 0.5^2) (in the non-live buffer, overwritten by the next verify anyway),
+            // expanded to the per-value-head layout of the live one
             const size_t hs = static_cast<size_t>(3) * (2 * c.ssm_h_k + c.ssm_h_v) * kS;
             RMI_TRY(rmi_gen_normal(L.state[0], st, mix_seed(seed, il, 20), 0.0f, 0.05f, e.s));
-            RMI_TRY(rmi_gen_normal(L.hist[0], hs, mix_seed(seed, il, 21), 0.0f, 0.5f, e.s));
+            RMI_TRY(rmi_gen_normal(L.hist[1], hs, mix_seed(seed, il, 21), 0.0f, 0.5f, e.s));
+            hipLaunchKernelGGL(hist_expand_kernel, dim3(grid1(c.ssm_h_v * 3 * kS)), dim3(256), 0, e.s, L.hist[1],
+                               L.hist[0], c.ssm_h_k, c.ssm_h_v);
+            RMI_TRY(launch_status("hist_expand"));
         } else if (kv) {
             RMI_TRY(rmi_gen_normal_f16(L.kc, kv, mix_seed(seed, il, 22), 0.0f, 1.0f, e.s));
             RMI_TRY(rmi_gen_normal_f16(L.vc, kv, mix_seed(seed, il, 23), 0.0f, 1.0f, e.s));
@@ -668,7 +685,7 @@ extern "C" int rmi_engine_prefill(rmi_engine* h, const int* tokens, int n, int* 
         if (L.gdn) {
             for (int b = 0; b < 2; ++b) {
                 RMI_TRY(zero_f32(e, L.state[b], static_cast<size_t>(kS) * c.ssm_h_v * kS));
-                RMI_TRY(zero_f32(e, L.hist[b], static_cast<size_t>(3) * (2 * c.ssm_h_k + c.ssm_h_v) * kS));
+                RMI_TRY(zero_f32(e, L.hist[b], hist_floats(c)));
             }
         }
     RMI_TRY(set_int(e, kSel, 0));
@@ -699,7 +716,7 @@ extern "C" int rmi_engine_save_state(rmi_engine* h) {
         if (!L.gdn) continue;
         HIP_TRY(hipMemcpyAsync(e.saved_state[k], L.state[st[kSel]], sizeof(float) * kS * c.ssm_h_v * kS,
                                hipMemcpyDeviceToDevice, e.s));
-        HIP_TRY(hipMemcpyAsync(e.saved_hist[k], L.hist[st[kSel]], sizeof(float) * 3 * (2 * c.ssm_h_k + c.ssm_h_v) * kS,
+        HIP_TRY(hipMemcpyAsync(e.saved_hist[k], L.hist[st[kSel]], sizeof(float) * hist_floats(c),
                                hipMemcpyDeviceToDevice, e.s));
         ++k;
     }
@@ -719,7 +736,7 @@ extern "C" int rmi_engine_restore_state(rmi_engine* h, int pos, int cur_token) {
         if (!L.gdn) continue;
         HIP_TRY(hipMemcpyAsync(L.state[0], e.saved_state[k], sizeof(float) * kS * c.ssm_h_v * kS,
                                hipMemcpyDeviceToDevice, e.s));
-        HIP_TRY(hipMemcpyAsync(L.hist[0], e.saved_hist[k], sizeof(float) * 3 * (2 * c.ssm_h_k + c.ssm_h_v) * kS,
+        HIP_TRY(hipMemcpyAsync(L.hist[0], e.saved_hist[k], sizeof(float) * hist_floats(c),
                                hipMemcpyDeviceToDevice, e.s));
         ++k;
     }

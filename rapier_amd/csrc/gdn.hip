@@ -1,7 +1,8 @@
 // gdn.hip - Gated DeltaNet decode chain for gfx950 (reference src/fused_gdn.cu:40-133, engine glue
 // src/qwythos.cpp:1101-1127 and the verify pass 1438-1478).
 //
-// Two kernels per layer, for 1 token (the plain decode step) or the 2 verify tokens:
+// Kernels, for 1 token (the plain decode step) or the 2 verify tokens (the engine path runs the conv inside the step
+// kernel's prologue, one launch per layer; the reference surface keeps them apart):
 //   conv:  one lane per channel (8192 = q 2048 | k 2048 | v 4096): causal width-4 conv over [hist(3) | x], SiLU, and
 //          the L2 norm of each 128-channel q/k head.  History is updated in place; with 2 tokens the history after
 //          token 0 also goes to the rollback buffer.
@@ -24,8 +25,6 @@ namespace {
 constexpr int S = 128;
 constexpr int RG = 4;
 constexpr int RPG = S / RG;
-
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
 template <typename T>
 __device__ __forceinline__ T* pick(T* a, T* b, const int* sel) {
@@ -107,14 +106,25 @@ struct StepArgs {
     uint8_t* q8;           // token t at + t * q8_stride bytes (may be null)
     int q8_stride;
     int h_k, h_v;
+    // CONV: the layer's conv + SiLU + L2 runs in the step kernel's prologue on the raw q|k|v rows (q, k, v above)
+    float* hist_a;
+    float* hist_b;
+    const float* conv_w;
 };
 
-template <int NT, bool RAW>
+// CONV (engine path): lanes 0..383 first run the conv of the head's q (k-head qh), k and v channels for all NT
+// tokens with the arithmetic of gdn_conv_kernel (same 64-lane partition of each 128-channel L2 sum) and keep the
+// results in LDS.  The history is per value head, [h_v][q 128 | k 128 | v 128][3]: the heads qh and qh + h_k that
+// share a k-head each carry their own (identical) copy of its q/k history, so no workgroup writes what another reads.
+// The raw q|k|v rows are only read.
+template <int NT, bool RAW, bool CONV>
 __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     __shared__ float sk[S], sq[S];
     __shared__ float red[RG][S];
     __shared__ float wsum[2];
     __shared__ float gb[2];
+    __shared__ float cq[CONV ? NT : 1][S], ck[CONV ? NT : 1][S], cv[CONV ? NT : 1][S];
+    __shared__ float cpart[NT][4];
     const int head = blockIdx.x;
     const int col = threadIdx.x & (S - 1);
     const int rg = threadIdx.x >> 7;
@@ -128,12 +138,70 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
 #pragma unroll
     for (int r = 0; r < RPG; ++r) s[r] = state[base + r * row_stride];
 
+    if constexpr (CONV) {
+        const int kind = threadIdx.x >> 7;   // 0 q, 1 k, 2 v, 3 idle
+        const int j = threadIdx.x & (S - 1);
+        const float* src = kind == 0 ? a.q + qh * S : kind == 1 ? a.k + qh * S : a.v + head * S;
+        const int c = kind == 0 ? qh * S + j : kind == 1 ? (a.h_k + qh) * S + j : (2 * a.h_k + head) * S + j;
+        const int ch = (3 * head + kind) * S + j;   // history slot: this head's own copy of the channel
+        float y[NT];
+        float h0 = 0.0f, h1 = 0.0f, h2 = 0.0f, x0 = 0.0f, x1 = 0.0f;
+        float* hist = pick(a.hist_a, a.hist_b, a.sel);
+        float* hsnap = pick(a.hist_b, a.hist_a, a.sel);
+        if (kind < 3) {
+            h0 = hist[3 * ch];
+            h1 = hist[3 * ch + 1];
+            h2 = hist[3 * ch + 2];
+            const float w0 = a.conv_w[4 * c], w1 = a.conv_w[4 * c + 1], w2 = a.conv_w[4 * c + 2], w3 = a.conv_w[4 * c + 3];
+            x0 = src[j];
+            y[0] = silu(__builtin_fmaf(x0, w3, __builtin_fmaf(h2, w2, __builtin_fmaf(h1, w1, h0 * w0))));
+            if constexpr (NT == 2) {
+                x1 = src[a.tok_stride + j];
+                y[1] = silu(__builtin_fmaf(x1, w3, __builtin_fmaf(x0, w2, __builtin_fmaf(h2, w1, h1 * w0))));
+            }
+        }
+        if (kind < 2) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float sqs = group_sum<64>(y[t] * y[t]);
+                if ((threadIdx.x & 63) == 0) cpart[t][threadIdx.x >> 6] = sqs;
+            }
+        }
+        __syncthreads();
+        if (kind < 3) {
+            if (kind < 2) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) y[t] *= rsqrtf((cpart[t][2 * kind] + cpart[t][2 * kind + 1]) + a.eps);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) (kind == 0 ? cq : kind == 1 ? ck : cv)[t][j] = y[t];
+            if constexpr (NT == 2) {
+                hsnap[3 * ch] = h1;
+                hsnap[3 * ch + 1] = h2;
+                hsnap[3 * ch + 2] = x0;
+                hist[3 * ch] = h2;
+                hist[3 * ch + 1] = x0;
+                hist[3 * ch + 2] = x1;
+            } else {
+                hist[3 * ch] = h1;
+                hist[3 * ch + 1] = h2;
+                hist[3 * ch + 2] = x0;
+            }
+        }
+        __syncthreads();   // cq / ck / cv are read by other lanes at the top of the token loop
+    }
+
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const size_t to = static_cast<size_t>(t) * a.tok_stride;
         if (threadIdx.x < S) {
-            sk[threadIdx.x] = a.k[to + qh * S + threadIdx.x];
-            sq[threadIdx.x] = a.q[to + qh * S + threadIdx.x];
+            if constexpr (CONV) {
+                sk[threadIdx.x] = ck[t][threadIdx.x];
+                sq[threadIdx.x] = cq[t][threadIdx.x];
+            } else {
+                sk[threadIdx.x] = a.k[to + qh * S + threadIdx.x];
+                sq[threadIdx.x] = a.q[to + qh * S + threadIdx.x];
+            }
         }
         if (threadIdx.x == 0) {
             float g, b;
@@ -157,7 +225,8 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
         red[rg][col] = kv;
         __syncthreads();
         const float kv_col = ((red[0][col] + red[1][col]) + red[2][col]) + red[3][col];
-        const float delta = (a.v[to + head * S + col] - g * kv_col) * beta;
+        const float vcol = CONV ? cv[CONV ? t : 0][col] : a.v[to + head * S + col];
+        const float delta = (vcol - g * kv_col) * beta;
         float o = 0.0f;
 #pragma unroll
         for (int r = 0; r < RPG; ++r) {
@@ -224,13 +293,14 @@ extern "C" int rmi_fused_gdn_step_norm_silu_q8(float* state, const float* q, con
     a.q = q; a.k = k; a.v = v; a.z = z;
     a.gate = gate; a.beta = beta; a.gamma = gamma; a.eps = eps;
     a.y = y; a.q8 = q8; a.h_k = h_k; a.h_v = h_v;
-    hipLaunchKernelGGL((gdn_step_kernel<1, false>), dim3(h_v), dim3(S * RG), 0, static_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL((gdn_step_kernel<1, false, false>), dim3(h_v), dim3(S * RG), 0, static_cast<hipStream_t>(stream), a);
     return launch_status("fused_gdn_step_norm_silu_q8");
 }
 
 // ---- engine surface: qkv|z and beta|alpha GEMV outputs, 1 or 2 tokens, selector-based rollback buffers --------------
 // Per token t: qkvz + t * qkvz_stride holds [q h_k*128 | k h_k*128 | v h_v*128 | z h_v*128]; ab + t * ab_stride holds
-// [beta h_v | alpha h_v].  The conv output overwrites the q|k|v part in place; y + t * y_stride, q8 + t * q8_stride.
+// [beta h_v | alpha h_v] (both read only).  History per value head, [h_v][3 * 128][3].  Output y + t * y_stride, q8
+// + t * q8_stride.
 extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_a, float* hist_b, const int* sel,
                                     float* qkvz, int qkvz_stride, const float* ab, int ab_stride, const float* conv_w,
                                     const float* dt, const float* ssm_a, const float* gamma, float eps, float* y,
@@ -245,12 +315,6 @@ extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_
         !aligned4(ab) || !aligned4(conv_w) || !aligned4(dt) || !aligned4(ssm_a) || !aligned4(gamma) || !aligned4(y))
         return fail(RMI_ERR_POINTER, "gdn_layer_tokens: invalid arguments");
     const auto s = static_cast<hipStream_t>(stream);
-    if (ntok == 2)
-        hipLaunchKernelGGL(gdn_conv_kernel<2>, dim3(channels / 256), dim3(256), 0, s, hist_a, hist_b, sel, qkvz, conv_w,
-                           qkvz, qkvz_stride, 2 * h_k, eps);
-    else
-        hipLaunchKernelGGL(gdn_conv_kernel<1>, dim3(channels / 256), dim3(256), 0, s, hist_a, hist_b, sel, qkvz, conv_w,
-                           qkvz, qkvz_stride, 2 * h_k, eps);
     StepArgs a{};
     a.state_a = state_a; a.state_b = state_b; a.sel = sel;
     a.q = qkvz; a.k = qkvz + h_k * S; a.v = qkvz + 2 * h_k * S; a.z = qkvz + channels;
@@ -259,7 +323,8 @@ extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_
     a.gamma = gamma; a.eps = eps;
     a.y = y; a.y_stride = y_stride; a.q8 = q8; a.q8_stride = q8_stride;
     a.h_k = h_k; a.h_v = h_v;
-    if (ntok == 2) hipLaunchKernelGGL((gdn_step_kernel<2, true>), dim3(h_v), dim3(S * RG), 0, s, a);
-    else hipLaunchKernelGGL((gdn_step_kernel<1, true>), dim3(h_v), dim3(S * RG), 0, s, a);
+    a.hist_a = hist_a; a.hist_b = hist_b; a.conv_w = conv_w;
+    if (ntok == 2) hipLaunchKernelGGL((gdn_step_kernel<2, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
+    else hipLaunchKernelGGL((gdn_step_kernel<1, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
     return launch_status("gdn_layer_tokens");
 }

@@ -1,9 +1,11 @@
 """GPU parity of the Gated DeltaNet chain (config 3: 16 key heads, 32 value heads, head_dim 128, 2 tokens).
 
-Bars (tolerances written here): conv / q / k / v outputs and y within 1e-3 relative of the oracle's fp64 chain; the
-recurrent state within 2e-3 max-abs; Q8_1 within half a quantization step.  Invariants, bit for bit: the 2-token
-call's token 0 and token 1 equal two sequential 1-token calls; the rollback buffer holds exactly the state / history
-after token 0; the reference-surface entry points (conv_l2, step_norm_silu_q8) agree with the fused layer call.
+Bars (tolerances written here): conv output and y within 1e-3 relative of the oracle's fp64 chain; the recurrent
+state within 2e-3 max-abs; Q8_1 within half a quantization step; the conv history bit-exact.  Invariants, bit for bit:
+the 2-token call's token 0 and token 1 equal two sequential 1-token calls; the rollback buffer holds exactly the
+state / history after token 0; the reference-surface entry points (conv_l2, step_norm_silu_q8) agree with the layer
+call.  The layer call keeps its conv history per value head ([h_v][q 128 | k 128 | v 128][3], value head h reading
+k-head h % h_k); the tests expand the oracle's [channels][3] history to that layout.
 """
 import numpy as np
 import pytest
@@ -39,6 +41,18 @@ def make_inputs(orc, seed=300):
     return qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma
 
 
+def expand_hist(h):
+    """[channels][3] conv history -> per value head [h_v][q | k | v][128][3] (head h sees k-head h % h_k)"""
+    h = np.asarray(h, np.float32).reshape(CH, 3)
+    out = np.empty((H_V, 3, S, 3), np.float32)
+    for head in range(H_V):
+        qh = head % H_K
+        out[head, 0] = h[qh * S:(qh + 1) * S]
+        out[head, 1] = h[(H_K + qh) * S:(H_K + qh + 1) * S]
+        out[head, 2] = h[(2 * H_K + head) * S:(2 * H_K + head + 1) * S]
+    return out.reshape(-1)
+
+
 def oracle_chain(orc, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok=2):
     st = state.astype(np.float64)
     hs = hist.copy()
@@ -54,9 +68,10 @@ def oracle_chain(orc, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok=2):
 
 
 def run_layer(rmi, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok, sel_val=0):
+    """hist in the per-value-head layout (expand_hist)"""
     t = torch()
     st_live, st_other = dev(state), t.zeros(S * H_V * S, device="cuda:0")
-    hi_live, hi_other = dev(hist), t.zeros(3 * CH, device="cuda:0")
+    hi_live, hi_other = dev(hist), t.zeros(H_V * 3 * S * 3, device="cuda:0")
     sel = dev(np.array([sel_val], np.int32))
     bufs = (st_live, st_other, hi_live, hi_other) if sel_val == 0 else (st_other, st_live, hi_other, hi_live)
     dq = dev(qkvz[:ntok * QKVZ])
@@ -72,10 +87,10 @@ def run_layer(rmi, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok, sel_va
 def test_gdn_two_tokens_match_oracle(orc, rmi):
     inp = make_inputs(orc)
     qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma = inp
-    r = run_layer(rmi, *inp, ntok=2)
+    r = run_layer(rmi, qkvz, ab, conv_w, expand_hist(hist), state, dt, ssm_a, gamma, ntok=2)
+    assert np.array_equal(r["conv"], qkvz[:2 * QKVZ]), "the layer call reads q|k|v|z only"
     ys, states, hists, convs = oracle_chain(orc, *inp)
     for t in range(2):
-        assert_close_rel(r["conv"][t * QKVZ:t * QKVZ + CH], convs[t], rtol=1e-3, atol_frac=1e-6, what=f"conv t{t}")
         assert_close_rel(r["y"][t * H_V * S:(t + 1) * H_V * S], ys[t], rtol=1e-3, atol_frac=1e-5, what=f"y t{t}")
         blk = H_V * S // 32 * 36
         deq = orc.dequantize_q8_1(r["q8"][t * blk:(t + 1) * blk], H_V * S).reshape(-1, 32).astype(np.float64)
@@ -86,15 +101,16 @@ def test_gdn_two_tokens_match_oracle(orc, rmi):
         assert np.isfinite(d.view(np.float16)).all() and np.isfinite(s.view(np.float16)).all()
     assert np.abs(r["snap"] - states[0]).max() < 2e-3, "state after token 0 (rollback buffer)"
     assert np.abs(r["state"] - states[1]).max() < 2e-3, "state after token 1"
-    assert np.array_equal(r["hsnap"], hists[0].astype(np.float32))
-    assert np.array_equal(r["hist"], hists[1].astype(np.float32))
+    assert np.array_equal(r["hsnap"], expand_hist(hists[0]))
+    assert np.array_equal(r["hist"], expand_hist(hists[1]))
 
 
 @pytest.mark.parametrize("sel_val", [0, 1])
 def test_gdn_two_tokens_bitwise_equal_sequential(orc, rmi, sel_val):
     inp = make_inputs(orc, seed=400)
     qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma = inp
-    r2 = run_layer(rmi, *inp, ntok=2, sel_val=sel_val)
+    hist = expand_hist(hist)
+    r2 = run_layer(rmi, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok=2, sel_val=sel_val)
     a = run_layer(rmi, qkvz[:QKVZ], ab[:2 * H_V], conv_w, hist, state, dt, ssm_a, gamma, ntok=1, sel_val=sel_val)
     b = run_layer(rmi, qkvz[QKVZ:], ab[2 * H_V:], conv_w, a["hist"], a["state"], dt, ssm_a, gamma, ntok=1,
                   sel_val=sel_val)
@@ -111,7 +127,8 @@ def test_reference_surface_entry_points(orc, rmi):
     """fused_gdn_conv_l2 + beta_gate + fused_gdn_step_norm_silu_q8 (the reference's 3-launch chain) == layer call."""
     inp = make_inputs(orc, seed=500)
     qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma = inp
-    ref = run_layer(rmi, qkvz[:QKVZ], ab[:2 * H_V], conv_w, hist, state, dt, ssm_a, gamma, ntok=1)
+    ref = run_layer(rmi, qkvz[:QKVZ], ab[:2 * H_V], conv_w, expand_hist(hist), state, dt, ssm_a, gamma, ntok=1)
+    _, _, _, convs = oracle_chain(orc, *inp, ntok=1)
     dh, dq = dev(hist), dev(qkvz[:QKVZ])
     rmi.fused_gdn_conv_l2(dh, dq, dev(conv_w), dq, CH, 2 * H_K, EPS)
     dab, gg = dev(ab[:2 * H_V]), empty(H_V)
@@ -119,8 +136,8 @@ def test_reference_surface_entry_points(orc, rmi):
     st, y, q8 = dev(state), empty(H_V * S), empty(H_V * S // 32 * 36, "uint8")
     rmi.fused_gdn_step_norm_silu_q8(st, dq, dq[H_K * S:], dq[2 * H_K * S:], gg, dab, dq[CH:], dev(gamma), EPS, y, q8,
                                     H_K, H_V)
-    assert np.array_equal(host(dq)[:CH].view(np.uint32), ref["conv"][:CH].view(np.uint32))
-    assert np.array_equal(host(dh), ref["hist"])
+    assert_close_rel(host(dq)[:CH], convs[0], rtol=1e-3, atol_frac=1e-6, what="conv")
+    assert np.array_equal(expand_hist(host(dh)), ref["hist"])
     # the prepared-gate path computes exp(gate) from a stored logit: same math, last-bit differences allowed
     assert_close_rel(host(y), ref["y"], rtol=1e-5, atol_frac=1e-6, what="step y")
     assert np.abs(host(st) - ref["state"]).max() < 1e-5
