@@ -50,16 +50,17 @@ __global__ __launch_bounds__(HD) void attn_prep_kernel(const float* __restrict__
     const int hh = blockIdx.y;   // [0, n_head) q, [n_head, n_head + n_kv) k, then v
     const int d = threadIdx.x;
     const float* src = q3 + static_cast<size_t>(t) * q3_stride;
+    // the row value does not depend on the position: load it in parallel with pos
+    const bool is_v = hh >= n_head + n_kv, is_q = hh < n_head;
+    const float x = is_v ? src[2 * n_head * HD + n_kv * HD + (hh - n_head - n_kv) * HD + d]
+                         : is_q ? src[hh * 2 * HD + d] : src[2 * n_head * HD + (hh - n_head) * HD + d];
     const int p = pos[0] + t;
     if (p < 0 || p >= max_ctx) return;   // uniform: a position outside the cache stores nothing
-    if (hh >= n_head + n_kv) {   // v: straight to the cache
+    if (is_v) {   // v: straight to the cache
         const int kv = hh - n_head - n_kv;
-        const float v = src[2 * n_head * HD + n_kv * HD + kv * HD + d];
-        vc[(static_cast<size_t>(p) * n_kv + kv) * HD + d] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+        vc[(static_cast<size_t>(p) * n_kv + kv) * HD + d] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
         return;
     }
-    const bool is_q = hh < n_head;
-    const float x = is_q ? src[hh * 2 * HD + d] : src[2 * n_head * HD + (hh - n_head) * HD + d];
     const float ss = block_sum256(x * x, red);
     const float inv = rsqrtf(ss / static_cast<float>(HD) + eps);
     float v = x * inv * (is_q ? qn[d] : kn[d]);
@@ -131,41 +132,29 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
     const int chunk = blockIdx.x, kv = blockIdx.y;
     const int G = n_head / n_kv;
     const int nq = ntok * G;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int l16 = lane & 15, g4 = lane >> 4;
+    const int slot = l16 & 7;
+    const bool lo_row = l16 >= 8;
+
+    // the query rows do not depend on the position: their loads go out together with pos[0]
+    float4 qraw[16];   // [2 sp + hlf]: dims 32 sp + 8 g4 + 4 hlf + [0, 4) of query slot `slot`
+    {
+        const bool ok = slot < nq;
+        const int t = ok ? slot / G : 0, gh = ok ? slot - (slot / G) * G : 0;
+        const float4* q = reinterpret_cast<const float4*>(qbuf + (static_cast<size_t>(t) * n_head + kv * G + gh) * HD);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) qraw[i] = ok ? q[8 * (i >> 1) + 2 * g4 + (i & 1)] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     const int p0 = pos[0];
     const int p_last = p0 + ntok - 1;
     const int wlen = STEP * nsub;
     const int cbase = chunk * WAVES * wlen;
     if (cbase > p_last || p0 < 0 || p_last >= max_ctx) return;   // uniform: no visible position (or a bad pos)
 
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int l16 = lane & 15, g4 = lane >> 4;
-    const int slot = l16 & 7;
-    const bool lo_row = l16 >= 8;
     const int wbase = cbase + wv * wlen;
     const int nsteps = wbase > p_last ? 0 : min(nsub, (p_last - wbase) / STEP + 1);
     uint8_t* kt = tiles + wv * KTILE;
-
-    // B operand of the score MFMAs: step 2 sp + hlf covers dims 32 sp + 8 g4 + 4 hlf + [0, 4)
-    half4 qb[16];
-    {
-        const bool ok = slot < nq;
-        const int t = ok ? slot / G : 0, gh = ok ? slot - (slot / G) * G : 0;
-        const float* q = qbuf + (static_cast<size_t>(t) * n_head + kv * G + gh) * HD;
-#pragma unroll
-        for (int sp = 0; sp < 8; ++sp) {
-#pragma unroll
-            for (int hlf = 0; hlf < 2; ++hlf) {
-                half4 v;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float x = ok ? q[32 * sp + 8 * g4 + 4 * hlf + e] : 0.0f;
-                    const _Float16 h = static_cast<_Float16>(x);
-                    v[e] = lo_row ? static_cast<_Float16>(x - static_cast<float>(h)) : h;
-                }
-                qb[2 * sp + hlf] = v;
-            }
-        }
-    }
     const int lim = slot < nq ? p0 + slot / G : -1;   // last position slot `slot` may see
 
     floatx4 oacc[2][8];
@@ -194,6 +183,20 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
         const uint16_t* vr = vb + min(wbase + 4 * g4 + j, p_last) * rstride + 8 * l16;
         set_u4(vnext, 2 * j, *reinterpret_cast<const uint4*>(vr));
         set_u4(vnext, 2 * j + 1, *reinterpret_cast<const uint4*>(vr + 128));
+    }
+    // B operand of the score MFMAs, from the query rows loaded above: step 2 sp + hlf covers dims
+    // 32 sp + 8 g4 + 4 hlf + [0, 4); rows 0-7 the fp16 hi part, rows 8-15 the fp16 lo part of the same slot
+    half4 qb[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float xs[4] = {qraw[i].x, qraw[i].y, qraw[i].z, qraw[i].w};
+        half4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const _Float16 h = static_cast<_Float16>(xs[e]);
+            v[e] = lo_row ? static_cast<_Float16>(xs[e] - static_cast<float>(h)) : h;
+        }
+        qb[i] = v;
     }
     for (int s = 0; s < nsteps; ++s) {
         const int sb = wbase + s * STEP;
@@ -352,6 +355,7 @@ __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__
     const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
     const int G = n_head / n_kv;
     const int kv = h / G, qv = t * G + (h - kv * G);
+    const float g = gsrc[static_cast<size_t>(t) * gstride + h * 2 * HD + HD + d];   // in flight with pos
     const int nchunk = min((pos[0] + t) / chunk_len + 1, kMaxChunks);
     const size_t cstride = static_cast<size_t>(n_kv) * SLOTS * REC;
     const float* base = ws + (static_cast<size_t>(kv) * SLOTS + qv) * REC;
@@ -380,7 +384,6 @@ __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__
     }
     for (; c < nchunk; ++c) O = __builtin_fmaf(wts[c], base[c * cstride + 4 + d], O);
     const float o = O / L;
-    const float g = gsrc[static_cast<size_t>(t) * gstride + h * 2 * HD + HD + d];
     const float v = o * sigmoid(g);
     if (y) y[static_cast<size_t>(t) * y_stride + h * HD + d] = v;
     if (q8) q8_1_store_lane(v, q8 + static_cast<size_t>(t) * q8_stride + (h * (HD / 32) + d / 32) * kQ8_1Bytes);
@@ -418,7 +421,7 @@ extern "C" int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, cons
     if (head_dim != HD || n_head <= 0 || n_kv <= 0 || n_head % n_kv || ntok < 1 || ntok * (n_head / n_kv) > SLOTS ||
         max_ctx <= 0 || max_ctx % SUB || nsub <= 0)
         return fail(RMI_ERR_SHAPE, "gqa_flash_decode: invalid arguments");
-    if (!aligned4(q) || !aligned16(kcache) || !aligned16(vcache) || !aligned4(pos) || !aligned4(gate_src) ||
+    if (!aligned16(q) || !aligned16(kcache) || !aligned16(vcache) || !aligned4(pos) || !aligned4(gate_src) ||
         !aligned16(workspace) || (!y && !q8))
         return fail(RMI_ERR_POINTER, "gqa_flash_decode: invalid arguments");
     const int chunk_len = SUB * nsub;

@@ -33,11 +33,13 @@ __global__ __launch_bounds__(256) void rms_quant_apply_kernel(const float* __res
     x += static_cast<size_t>(c) * cols;
     partials += static_cast<size_t>(c) * (cols / 4);
     y += static_cast<size_t>(c) * (cols / 32) * kQ8_1Bytes;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    // x and w do not depend on the reduction: in flight together with the partials
+    const float xv = i < cols ? x[i] : 0.0f, wv = i < cols ? w[i] : 0.0f;
     const float ss = block_sum_partials(partials, cols / 4);
     const float inv = rsqrtf(ss / static_cast<float>(cols) + eps);
-    const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= cols) return;   // cols % 32 == 0: whole 32-lane groups leave together
-    q8_1_store_lane((x[i] * w[i]) * inv, y + static_cast<size_t>(i / 32) * kQ8_1Bytes);
+    q8_1_store_lane((xv * wv) * inv, y + static_cast<size_t>(i / 32) * kQ8_1Bytes);
 }
 
 // fp32 out = (x * w) * inv (reference rms_norm_out_kernel, qw:658-672), optionally with the output's own partials
@@ -49,12 +51,13 @@ __global__ __launch_bounds__(256) void rms_norm_out_kernel(const float* __restri
     x += static_cast<size_t>(c) * cols;
     partials += static_cast<size_t>(c) * (cols / 4);
     out += static_cast<size_t>(c) * out_stride;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const float xv = i < cols ? x[i] : 0.0f, wv = i < cols ? w[i] : 0.0f;   // in flight with the partials
     const float ss = block_sum_partials(partials, cols / 4);
     const float inv = rsqrtf(ss / static_cast<float>(cols) + eps);
-    const int i = blockIdx.x * 256 + threadIdx.x;
     float v = 0.0f;
     if (i < cols) {
-        v = (x[i] * w[i]) * inv;
+        v = (xv * wv) * inv;
         out[i] = v;
     }
     if (out_partials) {
