@@ -45,11 +45,11 @@ DN_BYTES = (q6_bytes(DN_ROWS, DN_IN) + 2 * (DN_IN // 32) * 36 + 2 * DN_ROWS * 4 
             + 2 * (DN_ROWS // 4) * 4)                                                       # 41,389,056
 PAIR_BYTES = UG_BYTES + DN_BYTES                                                             # 124,170,240
 
-# HBM traffic of one up||gate ncols=2 launch, from two rocprofv3 --pmc passes over `bench.py --workload
+# HBM traffic of one packed up||gate ncols=2 launch, from two rocprofv3 --pmc passes over `bench.py --workload
 # traffic_probe` (profiles/gemv_up_gate_traffic.md): FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by
 # what the same counter reads for a copy kernel that reads 256 MiB and writes 256 MiB in the same process.
-PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 41656.4375, 192.0
-PMC_COPY_FETCH_KIB, PMC_COPY_WRITE_KIB, COPY_KIB = 131090.3125, 262144.0, 262144.0
+PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 40448.0625, 192.0
+PMC_COPY_FETCH_KIB, PMC_COPY_WRITE_KIB, COPY_KIB = 131087.5, 262144.0, 262144.0
 UG_TRAFFIC_BYTES = round(1024 * (PMC_UG_FETCH_KIB * COPY_KIB / PMC_COPY_FETCH_KIB
                                  + PMC_UG_WRITE_KIB * COPY_KIB / PMC_COPY_WRITE_KIB))
 
@@ -132,20 +132,28 @@ def run_verify_gemv(args):
     ms_per_step = total_ms / args.steps
     value = PAIR_BYTES / (ms_per_step * 1e-3) / 1e9
 
-    # roofline leg: blocks of back-to-back up||gate launches over the rotating replicas, one HIP event pair per
-    # block on the launch stream (per-launch event pairs would add the event's own cost to every launch)
+    # roofline leg: the round's GEMV kernel, on the packed (wave-tiled) copies of the up||gate replicas the engine
+    # uses.  Blocks of back-to-back launches over the rotating replicas, one HIP event pair per block on the launch
+    # stream (per-launch event pairs would add the event's own cost to every launch).
+    ugp = [torch.empty(rmi.q6_k_packed_bytes(UG_IN, UG_ROWS), dtype=torch.uint8, device="cuda") for _ in range(reps)]
+    for i in range(reps):
+        rmi.q6_k_pack(ug[i], ugp[i], UG_IN, UG_ROWS, stream)
+    del ug, dn
+    for i in range(reps):
+        rmi.native_q6_k_mmvq_packed(ugp[i], xq_ug, y_ug, UG_IN, UG_ROWS, 2, stream)
     blocks, per_block = 5, 2 * reps
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(blocks)]
     torch.cuda.synchronize()
     for b in range(blocks):
         evs[b][0].record(stream)
         for i in range(per_block):
-            rmi.native_q6_k_mmvq(ug[i % reps], xq_ug, y_ug, UG_IN, UG_ROWS, 2, stream)
+            rmi.native_q6_k_mmvq_packed(ugp[i % reps], xq_ug, y_ug, UG_IN, UG_ROWS, 2, stream)
         evs[b][1].record(stream)
     torch.cuda.synchronize()
     ug_us = sorted(a.elapsed_time(b) * 1e3 / per_block for a, b in evs)
     ug_mean_us = sum(ug_us) / len(ug_us)
     achieved = UG_BYTES / (ug_mean_us * 1e-6) / 1e9
+    del ugp
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -170,7 +178,7 @@ def run_verify_gemv(args):
             "rotated_bytes": reps * (q6_bytes(UG_ROWS, UG_IN) + q6_bytes(DN_ROWS, DN_IN)),
         },
         "roofline": {
-            "kernel": "q6k_gemv_tiled<16,2,false> (up||gate 24576x4096, ncols=2)",
+            "kernel": "q6k_packed_gemv<2,false,2> (up||gate 24576x4096, ncols=2, packed wave-tile layout)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
@@ -187,7 +195,7 @@ def run_verify_gemv(args):
 
 
 def run_traffic_probe():
-    """Workload for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: one up||gate ncols=2 launch after a 1 GiB
+    """Workload for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: one packed up||gate ncols=2 launch after a 1 GiB
     fill has evicted L2 and the Infinity Cache, then a copy-like kernel of known size (reads 256 MiB, writes
     256 MiB) that calibrates both counters in the same process."""
     import torch
@@ -196,8 +204,11 @@ def run_traffic_probe():
     torch.cuda.set_device(0)
     stream = torch.cuda.Stream(device=0)
     torch.cuda.set_stream(stream)
-    w = torch.empty(q6_bytes(UG_ROWS, UG_IN), dtype=torch.uint8, device="cuda")
-    rmi.gen_q6_k(w, UG_ROWS * UG_IN // 256, seed=1)
+    wg = torch.empty(q6_bytes(UG_ROWS, UG_IN), dtype=torch.uint8, device="cuda")
+    rmi.gen_q6_k(wg, UG_ROWS * UG_IN // 256, seed=1)
+    w = torch.empty(rmi.q6_k_packed_bytes(UG_IN, UG_ROWS), dtype=torch.uint8, device="cuda")
+    rmi.q6_k_pack(wg, w, UG_IN, UG_ROWS, stream)
+    del wg
     x = torch.empty(2 * UG_IN, device="cuda")
     rmi.gen_normal(x, x.numel(), seed=2)
     xq = torch.empty(rmi.native_q8_1_bytes(UG_IN, 2), dtype=torch.uint8, device="cuda")
@@ -209,7 +220,7 @@ def run_traffic_probe():
     torch.cuda.synchronize()
     junk.fill_(1.0)
     torch.cuda.synchronize()
-    rmi.native_q6_k_mmvq(w, xq, y, UG_IN, UG_ROWS, 2, stream)
+    rmi.native_q6_k_mmvq_packed(w, xq, y, UG_IN, UG_ROWS, 2, stream)
     torch.cuda.synchronize()
     junk.fill_(2.0)
     torch.cuda.synchronize()

@@ -119,44 +119,77 @@ struct StepArgs {
 // The raw q|k|v rows are only read.
 template <int NT, bool RAW, bool CONV>
 __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
-    __shared__ float sk[S], sq[S];
-    __shared__ float red[RG][S];
-    __shared__ float wsum[2];
-    __shared__ float gb[2];
-    __shared__ float cq[CONV ? NT : 1][S], ck[CONV ? NT : 1][S], cv[CONV ? NT : 1][S];
+    __shared__ float cq[NT][S], ck[NT][S], cv[CONV ? NT : 1][S];   // q, k (and v) of every token
     __shared__ float cpart[NT][4];
+    __shared__ float gbt[NT][2];                                    // decay, beta per token
+    __shared__ float wsum[NT][S * RG / 64];                         // per-wave sums of o^2
+    __shared__ float ybuf[NT][S];
     const int head = blockIdx.x;
-    const int col = threadIdx.x & (S - 1);
-    const int rg = threadIdx.x >> 7;
+    // lane (wave w, lane l): column 16 w + l % 16, row group l / 16 (rows 32 rg .. 32 rg + 31): a column's four row
+    // groups share a wave, so the S^T k and S^T q column sums are two xor shuffles, not LDS round trips
+    const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+    const int col = 16 * wv + (ln & 15);
+    const int rg = ln >> 4;
     const int qh = head % a.h_k;
-    float* state = pick(a.state_a, a.state_b, a.sel);
-    float* snap = pick(a.state_b, a.state_a, a.sel);
     const size_t row_stride = static_cast<size_t>(a.h_v) * S;
     const size_t base = (static_cast<size_t>(rg * RPG) * a.h_v + head) * S + col;
 
+    // everything that does not depend on the selector is loaded first, in flight with *sel: the raw q|k|v rows and
+    // conv taps (CONV), z and gamma (the norm lanes), the gate inputs of every token (lane 0)
+    const int kind = threadIdx.x >> 7;   // CONV prologue: 0 q, 1 k, 2 v, 3 idle
+    const int j = threadIdx.x & (S - 1);
+    const float* src = kind == 0 ? a.q + qh * S : kind == 1 ? a.k + qh * S : a.v + head * S;
+    const int c = kind == 0 ? qh * S + j : kind == 1 ? (a.h_k + qh) * S + j : (2 * a.h_k + head) * S + j;
+    float x0 = 0.0f, x1 = 0.0f, w0 = 0.0f, w1 = 0.0f, w2 = 0.0f, w3 = 0.0f;
+    if (CONV && kind < 3) {
+        x0 = src[j];
+        if (NT == 2) x1 = src[a.tok_stride + j];
+        w0 = a.conv_w[4 * c];
+        w1 = a.conv_w[4 * c + 1];
+        w2 = a.conv_w[4 * c + 2];
+        w3 = a.conv_w[4 * c + 3];
+    }
+    float zz[NT], gam = 0.0f;
+    if (rg == 0) {
+        gam = a.gamma[col];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) zz[t] = a.z[static_cast<size_t>(t) * a.tok_stride + head * S + col];
+    }
+    float gin[NT][4];
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if constexpr (RAW) {
+                const float* ab = a.ab + static_cast<size_t>(t) * a.ab_stride;
+                gin[t][0] = ab[head];
+                gin[t][1] = ab[a.h_v + head];
+                gin[t][2] = a.dt[head];
+                gin[t][3] = a.ssm_a[head];
+            } else {
+                gin[t][0] = a.beta[head];
+                gin[t][1] = a.gate[head];
+            }
+        }
+    }
+
+    float* state = pick(a.state_a, a.state_b, a.sel);
+    float* snap = pick(a.state_b, a.state_a, a.sel);
     float s[RPG];
 #pragma unroll
     for (int r = 0; r < RPG; ++r) s[r] = state[base + r * row_stride];
 
     if constexpr (CONV) {
-        const int kind = threadIdx.x >> 7;   // 0 q, 1 k, 2 v, 3 idle
-        const int j = threadIdx.x & (S - 1);
-        const float* src = kind == 0 ? a.q + qh * S : kind == 1 ? a.k + qh * S : a.v + head * S;
-        const int c = kind == 0 ? qh * S + j : kind == 1 ? (a.h_k + qh) * S + j : (2 * a.h_k + head) * S + j;
         const int ch = (3 * head + kind) * S + j;   // history slot: this head's own copy of the channel
         float y[NT];
-        float h0 = 0.0f, h1 = 0.0f, h2 = 0.0f, x0 = 0.0f, x1 = 0.0f;
+        float h0 = 0.0f, h1 = 0.0f, h2 = 0.0f;
         float* hist = pick(a.hist_a, a.hist_b, a.sel);
         float* hsnap = pick(a.hist_b, a.hist_a, a.sel);
         if (kind < 3) {
             h0 = hist[3 * ch];
             h1 = hist[3 * ch + 1];
             h2 = hist[3 * ch + 2];
-            const float w0 = a.conv_w[4 * c], w1 = a.conv_w[4 * c + 1], w2 = a.conv_w[4 * c + 2], w3 = a.conv_w[4 * c + 3];
-            x0 = src[j];
             y[0] = silu(__builtin_fmaf(x0, w3, __builtin_fmaf(h2, w2, __builtin_fmaf(h1, w1, h0 * w0))));
             if constexpr (NT == 2) {
-                x1 = src[a.tok_stride + j];
                 y[1] = silu(__builtin_fmaf(x1, w3, __builtin_fmaf(x0, w2, __builtin_fmaf(h2, w1, h1 * w0))));
             }
         }
@@ -191,72 +224,81 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
         __syncthreads();   // cq / ck / cv are read by other lanes at the top of the token loop
     }
 
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const size_t to = static_cast<size_t>(t) * a.tok_stride;
+    if constexpr (!CONV) {
         if (threadIdx.x < S) {
-            if constexpr (CONV) {
-                sk[threadIdx.x] = ck[t][threadIdx.x];
-                sq[threadIdx.x] = cq[t][threadIdx.x];
-            } else {
-                sk[threadIdx.x] = a.k[to + qh * S + threadIdx.x];
-                sq[threadIdx.x] = a.q[to + qh * S + threadIdx.x];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                ck[t][threadIdx.x] = a.k[static_cast<size_t>(t) * a.tok_stride + qh * S + threadIdx.x];
+                cq[t][threadIdx.x] = a.q[static_cast<size_t>(t) * a.tok_stride + qh * S + threadIdx.x];
             }
         }
-        if (threadIdx.x == 0) {
+    }
+    float vreg[NT];
+    if constexpr (!CONV) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) vreg[t] = a.v[static_cast<size_t>(t) * a.tok_stride + head * S + col];
+    }
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
             float g, b;
             if constexpr (RAW) {
-                const float* ab = a.ab + static_cast<size_t>(t) * a.ab_stride;
-                b = 1.0f / (1.0f + expf(-ab[head]));
-                const float vv = ab[a.h_v + head] + a.dt[head];
-                g = expf((vv > 20.0f ? vv : log1pf(expf(vv))) * a.ssm_a[head]);
+                b = 1.0f / (1.0f + expf(-gin[t][0]));
+                const float vv = gin[t][1] + gin[t][2];
+                g = expf((vv > 20.0f ? vv : log1pf(expf(vv))) * gin[t][3]);
             } else {
-                b = a.beta[head];
-                g = expf(a.gate[head]);
+                b = gin[t][0];
+                g = expf(gin[t][1]);
             }
-            gb[0] = g;
-            gb[1] = b;
+            gbt[t][0] = g;
+            gbt[t][1] = b;
         }
-        __syncthreads();
-        const float g = gb[0], beta = gb[1];
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float g = gbt[t][0], beta = gbt[t][1];
         float kv = 0.0f;
 #pragma unroll
-        for (int r = 0; r < RPG; ++r) kv = __builtin_fmaf(s[r], sk[rg * RPG + r], kv);
-        red[rg][col] = kv;
-        __syncthreads();
-        const float kv_col = ((red[0][col] + red[1][col]) + red[2][col]) + red[3][col];
-        const float vcol = CONV ? cv[CONV ? t : 0][col] : a.v[to + head * S + col];
-        const float delta = (vcol - g * kv_col) * beta;
+        for (int r = 0; r < RPG; ++r) kv = __builtin_fmaf(s[r], ck[t][rg * RPG + r], kv);
+        kv += __shfl_xor(kv, 16, 64);   // (rg 0 + rg 1) + (rg 2 + rg 3), the same bits in all four lanes
+        kv += __shfl_xor(kv, 32, 64);
+        const float vcol = CONV ? cv[CONV ? t : 0][col] : vreg[t];
+        const float delta = (vcol - g * kv) * beta;
         float o = 0.0f;
 #pragma unroll
         for (int r = 0; r < RPG; ++r) {
-            s[r] = __builtin_fmaf(g, s[r], sk[rg * RPG + r] * delta);
-            o = __builtin_fmaf(s[r], sq[rg * RPG + r], o);
+            s[r] = __builtin_fmaf(g, s[r], ck[t][rg * RPG + r] * delta);
+            o = __builtin_fmaf(s[r], cq[t][rg * RPG + r], o);
         }
-        __syncthreads();   // everyone has read red (kv) before it is reused for o
-        red[rg][col] = o;
-        __syncthreads();
-        float oc = 0.0f;
-        if (rg == 0) {
-            oc = (((red[0][col] + red[1][col]) + red[2][col]) + red[3][col]) * 0.08838834764831845f;
-            const float ss = group_sum<64>(oc * oc);
-            if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
-        }
+        o += __shfl_xor(o, 16, 64);
+        o += __shfl_xor(o, 32, 64);
+        const float oc = o * 0.08838834764831845f;   // 1 / sqrt(128)
         if constexpr (NT == 2) {
             if (t == 0) {
 #pragma unroll
                 for (int r = 0; r < RPG; ++r) snap[base + r * row_stride] = s[r];
             }
         }
+        const float ss = group_sum<16>(oc * oc);   // the wave's 16 columns (row-group 0 lanes carry them)
+        if (ln == 0) wsum[t][wv] = ss;
         __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < S * RG / 64; ++w) tot += wsum[t][w];
         if (rg == 0) {
-            const float scale = rsqrtf((wsum[0] + wsum[1]) / static_cast<float>(S) + a.eps);
-            const float zz = a.z[to + head * S + col];
-            const float yv = oc * scale * a.gamma[col] * silu(zz);
-            a.y[static_cast<size_t>(t) * a.y_stride + head * S + col] = yv;
-            if (a.q8) q8_1_store_lane(yv, a.q8 + static_cast<size_t>(t) * a.q8_stride + (head * 4 + (col >> 5)) * kQ8_1Bytes);
+            const float scale = rsqrtf(tot / static_cast<float>(S) + a.eps);
+            ybuf[t][col] = oc * scale * gam * silu(zz[t]);
         }
-        __syncthreads();   // sk/sq/gb/wsum are rewritten by the next token
+    }
+    __syncthreads();
+    // y and its Q8_1 blocks: lane -> (token, column); 32-lane groups are whole blocks
+    if (threadIdx.x < NT * S) {
+        const int t = threadIdx.x / S, c = threadIdx.x - t * S;
+        const float yv = ybuf[t][c];
+        a.y[static_cast<size_t>(t) * a.y_stride + head * S + c] = yv;
+        if (a.q8) q8_1_store_lane(yv, a.q8 + static_cast<size_t>(t) * a.q8_stride + (head * 4 + (c >> 5)) * kQ8_1Bytes);
     }
 #pragma unroll
     for (int r = 0; r < RPG; ++r) state[base + r * row_stride] = s[r];
