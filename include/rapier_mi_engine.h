@@ -71,14 +71,31 @@ rmi_model_config rmi_qwen35_9b_config(void);
 int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int max_ctx, void* stream, rmi_engine** out);
 int rmi_engine_destroy(rmi_engine* e);
 int rmi_engine_info(const rmi_engine* e, rmi_engine_info_t* info);
-/* prompt of n host tokens from position 0; *first_out = the greedy token after it (the current token) */
+/* prompt of n host tokens from position 0; *first_out = the greedy token after it (the current token).  Ingests in
+ * chunks of 16 tokens (rmi_engine_prefill_batch with batch 16). */
 int rmi_engine_prefill(rmi_engine* e, const int* tokens, int n, int* first_out);
+/* batch 1: token by token (forward_token per prompt token, qw:1773-1824, plus the draft KV row); batch 2..16: chunks
+ * of `batch` tokens, one weight pass per chunk (serve_ingest_kernels, qw:2192-2502, the batch loop qw:2658-2722; the
+ * reference takes 2..8 or 16).  Every batch leaves the same state, bit for bit: GDN state and history, trunk and
+ * draft KV, hidden, position and first token. */
+int rmi_engine_prefill_batch(rmi_engine* e, const int* tokens, int n, int batch, int* first_out);
 /* seeded synthetic state for positions [0, n_ctx - 1), then one forward of last_token at n_ctx - 1 */
 int rmi_engine_synth_context(rmi_engine* e, int n_ctx, uint64_t seed, int last_token, int* first_out);
 int rmi_engine_save_state(rmi_engine* e);
 int rmi_engine_restore_state(rmi_engine* e, int pos, int cur_token);
 int rmi_engine_state(rmi_engine* e, int* pos, int* cur_token);
 int rmi_engine_generate(rmi_engine* e, const rmi_gen_request* req, int* out_tokens, rmi_gen_stats* stats);
+
+/* engine buffers readable with rmi_engine_read (the reference's QWYTHOS_IDUMP probes read the same state) */
+enum {
+    RMI_BUF_GDN_STATE = 0,   /* live GDN state of a GDN layer, fp32 [128][h_v][128] */
+    RMI_BUF_GDN_HIST = 1,    /* live conv history of a GDN layer, fp32 [h_v][3 * 128][3] */
+    RMI_BUF_K_CACHE = 2,     /* K cache of an attention layer (layer n_layer: the draft block), fp16 [pos][n_kv][256] */
+    RMI_BUF_V_CACHE = 3,
+    RMI_BUF_HIDDEN = 4       /* final-normed hidden of the last forward, fp32 [n_embd] (the first draft's input) */
+};
+/* copy bytes [offset, offset + bytes) of an engine buffer to host memory; synchronizes the engine stream */
+int rmi_engine_read(rmi_engine* e, int which, int layer, size_t offset, void* dst, size_t bytes);
 
 #ifdef __cplusplus
 }

@@ -398,7 +398,7 @@ extern "C" int rmi_attn_prep(const float* q3, int q3_stride, const float* qn, co
                              uint16_t* vcache, const int* pos, float* qout, int n_head, int n_kv, int head_dim,
                              int n_rot, float theta, float eps, int ntok, int max_ctx, void* stream) {
     if (head_dim != HD || n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_rot < 0 || n_rot > HD || n_rot % 2 ||
-        ntok < 1 || ntok > 2)
+        ntok < 1 || ntok > kMaxCols)
         return fail(RMI_ERR_SHAPE, "attn_prep: invalid arguments");
     if (!aligned4(q3) || !aligned4(qn) || !aligned4(kn) || !kcache || !vcache || !aligned4(pos) || !aligned4(qout))
         return fail(RMI_ERR_POINTER, "attn_prep: invalid arguments");

@@ -34,6 +34,7 @@ namespace {
 
 constexpr int kS = 128;          // GDN state size
 constexpr int kRingCap = 1 << 16;
+constexpr int kChunk = kMaxCols;  // ingest chunk: prompt tokens per weight pass
 
 #define RMI_TRY(expr)                         \
     do {                                      \
@@ -118,11 +119,14 @@ struct Engine {
     int qkvz_rows = 0, q3_rows = 0, gdn_v = 0, attn_q = 0, max_in = 0;
 
     int* ints = nullptr;            // kNumSlots
+    int* cints = nullptr;           // ingest chunk: trunk tokens [0, 16), positions [16, 32)
+    int* prompt = nullptr;          // ingest: the prompt's token ids, indexed by position
     int* ring = nullptr;            // emitted tokens
     int* ref_tok = nullptr;         // forced-acceptance reference stream, indexed by position
     uint8_t* pattern = nullptr;     // forced-acceptance pattern, indexed by round
 
-    // activations (2 columns)
+    // activations (kChunk columns; decode uses the first two).  hsave / hpart hold kChunk + 1 columns: an ingest chunk
+    // writes its hidden to columns 1..nc, so that column c - 1 is the draft input of column c
     float *x = nullptr, *part = nullptr, *proj = nullptr, *ug = nullptr, *y = nullptr, *logits = nullptr;
     float *hsave = nullptr, *hpart = nullptr, *hzero = nullptr, *pzero = nullptr, *qbuf = nullptr;
     float *ex = nullptr, *epart = nullptr, *eh = nullptr, *dx = nullptr, *dpart = nullptr;
@@ -132,13 +136,14 @@ struct Engine {
     std::vector<float*> saved_state, saved_hist;
     float *saved_h = nullptr, *saved_hp = nullptr;
 
-    hipGraphExec_t g_single = nullptr, g_round = nullptr, g_draft1 = nullptr;
+    hipGraphExec_t g_single = nullptr, g_round = nullptr, g_draft1 = nullptr, g_chunk = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
 
     ~Engine() {
         if (g_single) (void) hipGraphExecDestroy(g_single);
         if (g_round) (void) hipGraphExecDestroy(g_round);
         if (g_draft1) (void) hipGraphExecDestroy(g_draft1);
+        if (g_chunk) (void) hipGraphExecDestroy(g_chunk);
         if (ev0) (void) hipEventDestroy(ev0);
         if (ev1) (void) hipEventDestroy(ev1);
         for (void* p : allocs) (void) hipFree(p);
@@ -224,6 +229,32 @@ __global__ void first_candidate_kernel(int* st, const int* ref_tok, const uint8_
         cand = pattern[0] ? truth : (truth + 1) % st[kVocab];
     }
     st[kTok1] = cand;
+}
+
+// ingest chunk set-up: nc prompt tokens from position st[kPos]; column c is token prompt[pos + c] at pos + c
+__global__ void chunk_setup_kernel(const int* st, const int* prompt, int* cints, int nc) {
+    const int c = threadIdx.x;
+    const int p = st[kPos] + c;
+    if (c < nc) {
+        cints[c] = prompt[p];
+        cints[kChunk + c] = p;
+    }
+}
+
+// after an ingest chunk: advance the position; column nc's hidden becomes column 0 (the next chunk's draft input, and
+// the hidden of the last token for the first draft of generation); with the head, the greedy token is current
+__global__ void chunk_finish_kernel(int* st, float* hsave, float* hpart, int n, int np, int nc, int head) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) hsave[i] = hsave[static_cast<size_t>(nc) * n + i];
+    for (int i = threadIdx.x; i < np; i += blockDim.x) hpart[i] = hpart[static_cast<size_t>(nc) * np + i];
+    if (threadIdx.x == 0) {
+        st[kPos] = st[kPos] + nc;
+        if (head) st[kTok0] = st[kV0];
+    }
+}
+
+__global__ void copy_f32_kernel(float* dst, const float* src, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = src[i];
 }
 
 unsigned grid1(size_t n) { return static_cast<unsigned>((n + 255) / 256); }
@@ -347,15 +378,23 @@ int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
     return gemv_res(e, L.down, e.q8f, x, part, nc);
 }
 
+// pos[0] is the position of column 0; with more than two columns pos is an array, pos[c] = pos[0] + c, and the
+// attention runs on pairs of columns (column 2 p's launch reads pos + 2 p).  Every KV row of the nc columns is stored
+// before any of them attends, and query c sees positions <= pos[0] + c only, as in the per-token path.
 int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc) {
     const auto& c = e.cfg;
     RMI_TRY(rmi_rms_quant_apply(x, L.attn_norm, part, e.q8a, c.n_embd, c.eps, nc, e.s));
     RMI_TRY(gemv(e, L.in_proj, e.q8a, e.proj, nc));
     RMI_TRY(rmi_attn_prep(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, e.qbuf, c.n_head, c.n_kv, c.head_dim,
                           c.n_rot, c.rope_theta, c.eps, nc, e.max_ctx, e.s));
-    RMI_TRY(rmi_gqa_flash_decode(e.qbuf, L.kc, L.vc, pos, e.proj, e.q3_rows, nullptr, 0, e.q8y,
-                                 static_cast<int>(q81_bytes(e.attn_q)), e.attn_ws, c.n_head, c.n_kv, c.head_dim, nc,
-                                 e.max_ctx, e.nsub, 1.0f / sqrtf(static_cast<float>(c.head_dim)), e.s));
+    const size_t q8y_col = q81_bytes(e.attn_q);
+    for (int c0 = 0; c0 < nc; c0 += 2) {
+        RMI_TRY(rmi_gqa_flash_decode(e.qbuf + static_cast<size_t>(c0) * e.attn_q, L.kc, L.vc, pos + c0,
+                                     e.proj + static_cast<size_t>(c0) * e.q3_rows, e.q3_rows, nullptr, 0,
+                                     e.q8y + c0 * q8y_col, static_cast<int>(q8y_col), e.attn_ws, c.n_head, c.n_kv,
+                                     c.head_dim, std::min(2, nc - c0), e.max_ctx, e.nsub,
+                                     1.0f / sqrtf(static_cast<float>(c.head_dim)), e.s));
+    }
     RMI_TRY(gemv_res(e, L.out_proj, e.q8y, x, part, nc));
     return ffn(e, L, x, part, nc);
 }
@@ -372,37 +411,75 @@ int gdn_block(Engine& e, Layer& L, int nc) {
     return ffn(e, L, e.x, e.part, nc);
 }
 
-// trunk for nc columns: tokens ints[kTok0 + c] at positions ints[kPos] + c.  Leaves argmax in ints[kV0 + c] and the
-// final-normed hidden in hsave/hpart (the draft's input, qw:1235-1237).
-int trunk(Engine& e, int nc) {
+enum Head { kHeadAll, kHeadLast, kHeadNone };
+
+// trunk for nc columns: tokens tok[c] at positions pos[0] + c (pos: see attn_block).  The head (output norm, lm_head,
+// argmax to ints[kV0 + c]) runs on every column, on the last one only (as ints[kV0]; an ingest chunk, qw:2700-2722),
+// or not at all.  The final-normed hidden goes to h / hp (the draft's input, qw:1235-1237).
+int trunk_cols(Engine& e, int nc, const int* tok, const int* pos, float* h, float* hp, Head head) {
     const auto& c = e.cfg;
-    RMI_TRY(rmi_embed_q6_k(e.tok_embd, e.ints + kTok0, e.x, e.part, c.n_embd, c.n_vocab, nc, e.s));
+    const size_t np = c.n_embd / 4;
+    RMI_TRY(rmi_embed_q6_k(e.tok_embd, tok, e.x, e.part, c.n_embd, c.n_vocab, nc, e.s));
     for (auto& L : e.layers) {
         if (L.gdn) RMI_TRY(gdn_block(e, L, nc));
-        else RMI_TRY(attn_block(e, L, e.x, e.part, e.ints + kPos, nc));
+        else RMI_TRY(attn_block(e, L, e.x, e.part, pos, nc));
     }
-    RMI_TRY(rmi_rms_quant_apply(e.x, e.out_norm, e.part, e.q8a, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(gemv(e, e.lm_head, e.q8a, e.logits, nc));
-    RMI_TRY(rmi_argmax(e.logits, c.n_vocab, nc, c.n_vocab, e.ints + kV0, e.argmax_ws, e.s));
-    return rmi_rms_norm_out(e.x, e.out_norm, e.part, e.hsave, e.hpart, c.n_embd, c.eps, nc, e.s);
+    if (head != kHeadNone) {
+        const int first = head == kHeadAll ? 0 : nc - 1;
+        const int ncol = nc - first;
+        RMI_TRY(rmi_rms_quant_apply(e.x + static_cast<size_t>(first) * c.n_embd, e.out_norm, e.part + first * np,
+                                    e.q8a, c.n_embd, c.eps, ncol, e.s));
+        RMI_TRY(gemv(e, e.lm_head, e.q8a, e.logits, ncol));
+        RMI_TRY(rmi_argmax(e.logits, c.n_vocab, ncol, c.n_vocab, e.ints + kV0, e.argmax_ws, e.s));
+    }
+    return rmi_rms_norm_out(e.x, e.out_norm, e.part, h, hp, c.n_embd, c.eps, nc, e.s);
 }
 
-// draft (nextn) block for nc columns: tokens ints[kD0 + c] at positions ints[kDPos] + c, previous hidden h / hp.
-// eh = [enorm(emb) | hnorm(h)] per column (embedding first, qw:1327-1332).  Argmax to ints[kC0 + c] when with_head.
-int draft_block(Engine& e, const float* h, const float* hp, int nc, bool with_head) {
+// trunk for the decode columns: tokens ints[kTok0 + c] at positions ints[kPos] + c, head on every column
+int trunk(Engine& e, int nc) {
+    return trunk_cols(e, nc, e.ints + kTok0, e.ints + kPos, e.hsave, e.hpart, kHeadAll);
+}
+
+// draft (nextn) block for nc columns: tokens tok[c] at positions pos[0] + c (pos: see attn_block), previous hidden
+// h / hp.  eh = [enorm(emb) | hnorm(h)] per column (embedding first, qw:1327-1332).  Argmax to ints[kC0 + c] when
+// with_head.
+int draft_cols(Engine& e, const int* tok, const int* pos, const float* h, const float* hp, int nc, bool with_head) {
     const auto& c = e.cfg;
-    RMI_TRY(rmi_embed_q6_k(e.tok_embd, e.ints + kD0, e.ex, e.epart, c.n_embd, c.n_vocab, nc, e.s));
+    RMI_TRY(rmi_embed_q6_k(e.tok_embd, tok, e.ex, e.epart, c.n_embd, c.n_vocab, nc, e.s));
     RMI_TRY(rmi_rms_norm_out_strided(e.ex, e.enorm, e.epart, e.eh, 2 * c.n_embd, nullptr, c.n_embd, c.eps, nc, e.s));
     RMI_TRY(rmi_rms_norm_out_strided(h, e.hnorm, hp, e.eh + c.n_embd, 2 * c.n_embd, nullptr, c.n_embd, c.eps, nc,
                                      e.s));
     RMI_TRY(rmi_native_quantize_q8_1(e.eh, e.q8f, 2 * c.n_embd, nc, e.s));
     RMI_TRY(gemv(e, e.eh_proj, e.q8f, e.dx, nc));
     RMI_TRY(rmi_row_sum_partials(e.dx, e.dpart, c.n_embd, nc, e.s));
-    RMI_TRY(attn_block(e, e.draft, e.dx, e.dpart, e.ints + kDPos, nc));
+    RMI_TRY(attn_block(e, e.draft, e.dx, e.dpart, pos, nc));
     if (!with_head) return RMI_OK;
     RMI_TRY(rmi_rms_quant_apply(e.dx, e.shnorm, e.dpart, e.q8a, c.n_embd, c.eps, nc, e.s));
     RMI_TRY(gemv(e, e.lm_head, e.q8a, e.logits, nc));
     return rmi_argmax(e.logits, c.n_vocab, nc, c.n_vocab, e.ints + kC0, e.argmax_ws, e.s);
+}
+
+// the decode draft: tokens ints[kD0 + c] at positions ints[kDPos] + c
+int draft_block(Engine& e, const float* h, const float* hp, int nc, bool with_head) {
+    return draft_cols(e, e.ints + kD0, e.ints + kDPos, h, hp, nc, with_head);
+}
+
+// One ingest chunk of nc prompt tokens from position ints[kPos] (the row-batched serve_ingest_kernels, qw:2192-2502,
+// plus the draft KV rows of the same positions): the trunk on nc columns, every GEMV one weight pass for all of them,
+// then the draft block on the same tokens with the hidden shifted by one column.  Every kernel computes each column
+// as the single-column call does, so the chunk leaves the state the per-token path leaves.
+int ingest_chunk(Engine& e, int nc, bool head) {
+    const auto& c = e.cfg;
+    const size_t np = c.n_embd / 4;
+    hipLaunchKernelGGL(chunk_setup_kernel, dim3(1), dim3(kChunk), 0, e.s, e.ints, e.prompt, e.cints, nc);
+    RMI_TRY(launch_status("chunk_setup"));
+    const int* tok = e.cints;
+    const int* pos = e.cints + kChunk;
+    RMI_TRY(trunk_cols(e, nc, tok, pos, e.hsave + c.n_embd, e.hpart + np, head ? kHeadLast : kHeadNone));
+    RMI_TRY(draft_cols(e, tok, pos, e.hsave, e.hpart, nc, false));
+    hipLaunchKernelGGL(chunk_finish_kernel, dim3(1), dim3(256), 0, e.s, e.ints, e.hsave, e.hpart, c.n_embd,
+                       static_cast<int>(np), nc, head ? 1 : 0);
+    return launch_status("chunk_finish");
 }
 
 int single_step(Engine& e) {
@@ -549,27 +626,30 @@ extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int
     RMI_TRY(e.alloc(&e.ref_tok, static_cast<size_t>(e.max_ctx) + 1));
     RMI_TRY(e.alloc(&e.pattern, 4096));
     const size_t np = c.n_embd / 4;
-    RMI_TRY(e.alloc(&e.x, 2 * static_cast<size_t>(c.n_embd)));
-    RMI_TRY(e.alloc(&e.part, 2 * np));
-    RMI_TRY(e.alloc(&e.proj, 2 * static_cast<size_t>(std::max(e.qkvz_rows, e.q3_rows))));
-    RMI_TRY(e.alloc(&e.ug, 4 * static_cast<size_t>(c.n_ff)));
-    RMI_TRY(e.alloc(&e.y, 2 * static_cast<size_t>(std::max(e.gdn_v, e.attn_q))));
+    const size_t K = kChunk;
+    RMI_TRY(e.alloc(&e.cints, 2 * K));
+    RMI_TRY(e.alloc(&e.prompt, static_cast<size_t>(e.max_ctx)));
+    RMI_TRY(e.alloc(&e.x, K * c.n_embd));
+    RMI_TRY(e.alloc(&e.part, K * np));
+    RMI_TRY(e.alloc(&e.proj, K * std::max(e.qkvz_rows, e.q3_rows)));
+    RMI_TRY(e.alloc(&e.ug, K * 2 * c.n_ff));
+    RMI_TRY(e.alloc(&e.y, K * std::max(e.gdn_v, e.attn_q)));
     RMI_TRY(e.alloc(&e.logits, 2 * static_cast<size_t>(c.n_vocab)));
-    RMI_TRY(e.alloc(&e.hsave, 2 * static_cast<size_t>(c.n_embd)));
-    RMI_TRY(e.alloc(&e.hpart, 2 * np));
+    RMI_TRY(e.alloc(&e.hsave, (K + 1) * c.n_embd));
+    RMI_TRY(e.alloc(&e.hpart, (K + 1) * np));
     RMI_TRY(e.alloc(&e.hzero, static_cast<size_t>(c.n_embd)));
     RMI_TRY(e.alloc(&e.pzero, np));
     RMI_TRY(zero_f32(e, e.hzero, c.n_embd));
     RMI_TRY(zero_f32(e, e.pzero, np));
-    RMI_TRY(e.alloc(&e.qbuf, 2 * static_cast<size_t>(e.attn_q)));
-    RMI_TRY(e.alloc(&e.ex, 2 * static_cast<size_t>(c.n_embd)));
-    RMI_TRY(e.alloc(&e.epart, 2 * np));
-    RMI_TRY(e.alloc(&e.eh, 4 * static_cast<size_t>(c.n_embd)));
-    RMI_TRY(e.alloc(&e.dx, 2 * static_cast<size_t>(c.n_embd)));
-    RMI_TRY(e.alloc(&e.dpart, 2 * np));
-    RMI_TRY(e.alloc(&e.q8a, 2 * q81_bytes(c.n_embd)));
-    RMI_TRY(e.alloc(&e.q8f, 2 * q81_bytes(e.max_in)));
-    RMI_TRY(e.alloc(&e.q8y, 2 * q81_bytes(std::max(e.gdn_v, e.attn_q))));
+    RMI_TRY(e.alloc(&e.qbuf, K * e.attn_q));
+    RMI_TRY(e.alloc(&e.ex, K * c.n_embd));
+    RMI_TRY(e.alloc(&e.epart, K * np));
+    RMI_TRY(e.alloc(&e.eh, K * 2 * c.n_embd));
+    RMI_TRY(e.alloc(&e.dx, K * c.n_embd));
+    RMI_TRY(e.alloc(&e.dpart, K * np));
+    RMI_TRY(e.alloc(&e.q8a, K * q81_bytes(c.n_embd)));
+    RMI_TRY(e.alloc(&e.q8f, K * q81_bytes(e.max_in)));
+    RMI_TRY(e.alloc(&e.q8y, K * q81_bytes(std::max(e.gdn_v, e.attn_q))));
     uint8_t* ws = nullptr;
     RMI_TRY(e.alloc(&ws, rmi_gqa_workspace_bytes(e.max_ctx, c.n_kv, e.nsub)));
     e.attn_ws = ws;
@@ -671,14 +751,17 @@ extern "C" int rmi_engine_synth_context(rmi_engine* h, int n_ctx, uint64_t seed,
     return RMI_OK;
 }
 
-// Feed `tokens` one by one from position 0 (zero state), filling the draft's KV as the reference seeds it (slot 0 with a
-// zero hidden, qw:2956-2958) and every later slot with (token, previous final-normed hidden).  *first_out = the
-// greedy token after the prompt.
-extern "C" int rmi_engine_prefill(rmi_engine* h, const int* tokens, int n, int* first_out) {
+// Feed the prompt from position 0 (zero state), filling the draft's KV as the reference seeds it (slot 0 with a zero
+// hidden, qw:2956-2958) and every later slot with (token, previous final-normed hidden).  batch 1: one token at a time
+// (the trunk with its head, then the draft row, per token; forward_token, qw:1773-1824).  batch 2..16: chunks of
+// `batch` tokens, each one pass over the weights (the ingest of qw:2658-2722), the head on the last token only; a
+// full chunk is one hipGraph launch.  Both leave the same state.  *first_out = the greedy token after the prompt.
+extern "C" int rmi_engine_prefill_batch(rmi_engine* h, const int* tokens, int n, int batch, int* first_out) {
     if (!h || !tokens) return fail(RMI_ERR_POINTER, "rmi_engine_prefill: null argument");
     Engine& e = h->e;
     const auto& c = e.cfg;
     if (n < 1 || n >= e.max_ctx - 2) return fail(RMI_ERR_STATE, "rmi_engine_prefill: context does not fit");
+    if (batch < 1 || batch > kChunk) return fail(RMI_ERR_SHAPE, "rmi_engine_prefill: batch must be 1..16");
     for (int i = 0; i < n; ++i)
         if (tokens[i] < 0 || tokens[i] >= c.n_vocab) return fail(RMI_ERR_STATE, "rmi_engine_prefill: bad token id");
     for (auto& L : e.layers)
@@ -690,18 +773,78 @@ extern "C" int rmi_engine_prefill(rmi_engine* h, const int* tokens, int n, int* 
         }
     RMI_TRY(set_int(e, kSel, 0));
     RMI_TRY(set_int(e, kNOut, 0));
-    for (int i = 0; i < n; ++i) {
-        // draft KV slot i from (token i, hidden of position i - 1) - the zero hidden at slot 0
-        RMI_TRY(set_int(e, kD0, tokens[i]));
-        RMI_TRY(set_int(e, kDPos, i));
-        RMI_TRY(draft_block(e, i == 0 ? e.hzero : e.hsave, i == 0 ? e.pzero : e.hpart, 1, false));
-        RMI_TRY(set_int(e, kTok0, tokens[i]));
-        RMI_TRY(set_int(e, kPos, i));
-        RMI_TRY(single_step(e));
+    if (batch == 1) {
+        for (int i = 0; i < n; ++i) {
+            // draft KV slot i from (token i, hidden of position i - 1) - the zero hidden at slot 0
+            RMI_TRY(set_int(e, kD0, tokens[i]));
+            RMI_TRY(set_int(e, kDPos, i));
+            RMI_TRY(draft_block(e, i == 0 ? e.hzero : e.hsave, i == 0 ? e.pzero : e.hpart, 1, false));
+            RMI_TRY(set_int(e, kTok0, tokens[i]));
+            RMI_TRY(set_int(e, kPos, i));
+            RMI_TRY(single_step(e));
+        }
+    } else {
+        HIP_TRY(hipMemcpyAsync(e.prompt, tokens, sizeof(int) * static_cast<size_t>(n), hipMemcpyHostToDevice, e.s));
+        hipLaunchKernelGGL(copy_f32_kernel, dim3(grid1(c.n_embd)), dim3(256), 0, e.s, e.hsave, e.hzero, c.n_embd);
+        hipLaunchKernelGGL(copy_f32_kernel, dim3(grid1(c.n_embd / 4)), dim3(256), 0, e.s, e.hpart, e.pzero,
+                           c.n_embd / 4);
+        RMI_TRY(launch_status("copy"));
+        RMI_TRY(set_int(e, kPos, 0));
+        int i = 0;
+        if (batch == kChunk && n > kChunk) {
+            RMI_TRY(capture(e, &e.g_chunk, [&] { return ingest_chunk(e, kChunk, false); }));
+            for (; n - i > kChunk; i += kChunk) HIP_TRY(hipGraphLaunch(e.g_chunk, e.s));
+        }
+        for (; i < n; i += batch) {
+            const int nc = std::min(batch, n - i);
+            RMI_TRY(ingest_chunk(e, nc, i + nc == n));
+        }
     }
     int st[kNumSlots];
     RMI_TRY(get_ints(e, st, kNumSlots));
     if (first_out) *first_out = st[kTok0];
+    return RMI_OK;
+}
+
+extern "C" int rmi_engine_prefill(rmi_engine* h, const int* tokens, int n, int* first_out) {
+    return rmi_engine_prefill_batch(h, tokens, n, kChunk, first_out);
+}
+
+// Copy bytes [offset, offset + bytes) of an engine buffer to host memory (synchronous).  layer indexes the trunk
+// layers; n_layer names the draft block (K/V caches only).  GDN buffers are the live ones.
+extern "C" int rmi_engine_read(rmi_engine* h, int which, int layer, size_t offset, void* dst, size_t bytes) {
+    if (!h || !dst) return fail(RMI_ERR_POINTER, "rmi_engine_read: null argument");
+    Engine& e = h->e;
+    const auto& c = e.cfg;
+    if (layer < 0 || layer > c.n_layer) return fail(RMI_ERR_SHAPE, "rmi_engine_read: bad layer");
+    const Layer& L = layer == c.n_layer ? e.draft : e.layers[layer];
+    int st[kNumSlots];
+    RMI_TRY(get_ints(e, st, kNumSlots));
+    const void* src = nullptr;
+    size_t size = 0;
+    switch (which) {
+        case RMI_BUF_GDN_STATE:
+        case RMI_BUF_GDN_HIST:
+            if (!L.gdn || layer == c.n_layer) return fail(RMI_ERR_SHAPE, "rmi_engine_read: not a GDN layer");
+            src = which == RMI_BUF_GDN_STATE ? static_cast<const void*>(L.state[st[kSel] & 1]) : L.hist[st[kSel] & 1];
+            size = which == RMI_BUF_GDN_STATE ? sizeof(float) * kS * c.ssm_h_v * kS : sizeof(float) * hist_floats(c);
+            break;
+        case RMI_BUF_K_CACHE:
+        case RMI_BUF_V_CACHE:
+            if (L.gdn) return fail(RMI_ERR_SHAPE, "rmi_engine_read: not an attention layer");
+            src = which == RMI_BUF_K_CACHE ? L.kc : L.vc;
+            size = sizeof(uint16_t) * e.max_ctx * c.n_kv * c.head_dim;
+            break;
+        case RMI_BUF_HIDDEN:
+            src = e.hsave;
+            size = sizeof(float) * c.n_embd;
+            break;
+        default:
+            return fail(RMI_ERR_SHAPE, "rmi_engine_read: bad buffer");
+    }
+    if (offset > size || bytes > size - offset) return fail(RMI_ERR_SHAPE, "rmi_engine_read: range outside the buffer");
+    HIP_TRY(hipMemcpyAsync(dst, static_cast<const uint8_t*>(src) + offset, bytes, hipMemcpyDeviceToHost, e.s));
+    HIP_TRY(hipStreamSynchronize(e.s));
     return RMI_OK;
 }
 

@@ -1,8 +1,8 @@
 // gdn.hip - Gated DeltaNet decode chain for gfx950 (reference src/fused_gdn.cu:40-133, engine glue
 // src/qwythos.cpp:1101-1127 and the verify pass 1438-1478).
 //
-// Kernels, for 1 token (the plain decode step) or the 2 verify tokens (the engine path runs the conv inside the step
-// kernel's prologue, one launch per layer; the reference surface keeps them apart):
+// Kernels, for 1 token (the plain decode step), the 2 verify tokens or an ingest chunk of up to 16 tokens (the engine
+// path runs the conv inside the step kernel's prologue, one launch per layer; the reference surface keeps them apart):
 //   conv:  one lane per channel (8192 = q 2048 | k 2048 | v 4096): causal width-4 conv over [hist(3) | x], SiLU, and
 //          the L2 norm of each 128-channel q/k head.  History is updated in place; with 2 tokens the history after
 //          token 0 also goes to the rollback buffer.
@@ -110,20 +110,28 @@ struct StepArgs {
     float* hist_a;
     float* hist_b;
     const float* conv_w;
+    int ntok;              // tokens of this launch (<= the instantiation's NT)
 };
 
-// CONV (engine path): lanes 0..383 first run the conv of the head's q (k-head qh), k and v channels for all NT
-// tokens with the arithmetic of gdn_conv_kernel (same 64-lane partition of each 128-channel L2 sum) and keep the
-// results in LDS.  The history is per value head, [h_v][q 128 | k 128 | v 128][3]: the heads qh and qh + h_k that
-// share a k-head each carry their own (identical) copy of its q/k history, so no workgroup writes what another reads.
-// The raw q|k|v rows are only read.
+// CONV (engine path): lanes 0..383 first run the conv of the head's q (k-head qh), k and v channels for all tokens
+// with the arithmetic of gdn_conv_kernel (same 64-lane partition of each 128-channel L2 sum) and keep the results in
+// LDS.  The history is per value head, [h_v][q 128 | k 128 | v 128][3]: the heads qh and qh + h_k that share a k-head
+// each carry their own (identical) copy of its q/k history, so no workgroup writes what another reads.  The raw
+// q|k|v rows are only read.
+//
+// NT is the largest token count of the instantiation and a.ntok (<= NT) the count of this launch.  NT = 2 is the
+// verify pair: the state and history after token 0 also go to the rollback buffers.  Otherwise (1 token, or an ingest
+// chunk of up to 16) the state and history are updated in place after the last token.  Every token's arithmetic is
+// that of the single-token step in the same order, so a chunk leaves the bits the per-token steps leave.
 template <int NT, bool RAW, bool CONV>
 __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
+    constexpr bool SNAP = NT == 2;
     __shared__ float cq[NT][S], ck[NT][S], cv[CONV ? NT : 1][S];   // q, k (and v) of every token
     __shared__ float cpart[NT][4];
     __shared__ float gbt[NT][2];                                    // decay, beta per token
     __shared__ float wsum[NT][S * RG / 64];                         // per-wave sums of o^2
     __shared__ float ybuf[NT][S];
+    const int ntok = NT <= 2 ? NT : a.ntok;
     const int head = blockIdx.x;
     // lane (wave w, lane l): column 16 w + l % 16, row group l / 16 (rows 32 rg .. 32 rg + 31): a column's four row
     // groups share a wave, so the S^T k and S^T q column sums are two xor shuffles, not LDS round trips
@@ -135,40 +143,44 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     const size_t base = (static_cast<size_t>(rg * RPG) * a.h_v + head) * S + col;
 
     // everything that does not depend on the selector is loaded first, in flight with *sel: the raw q|k|v rows and
-    // conv taps (CONV), z and gamma (the norm lanes), the gate inputs of every token (lane 0)
+    // conv taps (CONV), z and gamma (the norm lanes), the gate inputs (lane t for token t)
     const int kind = threadIdx.x >> 7;   // CONV prologue: 0 q, 1 k, 2 v, 3 idle
     const int j = threadIdx.x & (S - 1);
     const float* src = kind == 0 ? a.q + qh * S : kind == 1 ? a.k + qh * S : a.v + head * S;
     const int c = kind == 0 ? qh * S + j : kind == 1 ? (a.h_k + qh) * S + j : (2 * a.h_k + head) * S + j;
-    float x0 = 0.0f, x1 = 0.0f, w0 = 0.0f, w1 = 0.0f, w2 = 0.0f, w3 = 0.0f;
+    float xr[NT], w0 = 0.0f, w1 = 0.0f, w2 = 0.0f, w3 = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) xr[t] = 0.0f;
     if (CONV && kind < 3) {
-        x0 = src[j];
-        if (NT == 2) x1 = src[a.tok_stride + j];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            if (t < ntok) xr[t] = src[static_cast<size_t>(t) * a.tok_stride + j];
         w0 = a.conv_w[4 * c];
         w1 = a.conv_w[4 * c + 1];
         w2 = a.conv_w[4 * c + 2];
         w3 = a.conv_w[4 * c + 3];
     }
     float zz[NT], gam = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) zz[t] = 0.0f;
     if (rg == 0) {
         gam = a.gamma[col];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) zz[t] = a.z[static_cast<size_t>(t) * a.tok_stride + head * S + col];
+        for (int t = 0; t < NT; ++t)
+            if (t < ntok) zz[t] = a.z[static_cast<size_t>(t) * a.tok_stride + head * S + col];
     }
-    float gin[NT][4];
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if constexpr (RAW) {
-                const float* ab = a.ab + static_cast<size_t>(t) * a.ab_stride;
-                gin[t][0] = ab[head];
-                gin[t][1] = ab[a.h_v + head];
-                gin[t][2] = a.dt[head];
-                gin[t][3] = a.ssm_a[head];
-            } else {
-                gin[t][0] = a.beta[head];
-                gin[t][1] = a.gate[head];
-            }
+    float gin[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int gt = threadIdx.x;   // gate lane: token gt
+    if (gt < ntok) {
+        if constexpr (RAW) {
+            const float* ab = a.ab + static_cast<size_t>(gt) * a.ab_stride;
+            gin[0] = ab[head];
+            gin[1] = ab[a.h_v + head];
+            gin[2] = a.dt[head];
+            gin[3] = a.ssm_a[head];
+        } else {
+            gin[0] = a.beta[head];
+            gin[1] = a.gate[head];
         }
     }
 
@@ -181,44 +193,63 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     if constexpr (CONV) {
         const int ch = (3 * head + kind) * S + j;   // history slot: this head's own copy of the channel
         float y[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) y[t] = 0.0f;
         float h0 = 0.0f, h1 = 0.0f, h2 = 0.0f;
         float* hist = pick(a.hist_a, a.hist_b, a.sel);
         float* hsnap = pick(a.hist_b, a.hist_a, a.sel);
+        // the conv input sequence [h0 h1 h2 | x_0 .. x_ntok-1]; i is a compile-time index after unrolling
+        auto seq = [&](int i) { return i == 0 ? h0 : i == 1 ? h1 : i == 2 ? h2 : xr[i - 3]; };
         if (kind < 3) {
             h0 = hist[3 * ch];
             h1 = hist[3 * ch + 1];
             h2 = hist[3 * ch + 2];
-            y[0] = silu(__builtin_fmaf(x0, w3, __builtin_fmaf(h2, w2, __builtin_fmaf(h1, w1, h0 * w0))));
-            if constexpr (NT == 2) {
-                y[1] = silu(__builtin_fmaf(x1, w3, __builtin_fmaf(x0, w2, __builtin_fmaf(h2, w1, h1 * w0))));
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (t < ntok)
+                    y[t] = silu(__builtin_fmaf(seq(t + 3), w3,
+                                               __builtin_fmaf(seq(t + 2), w2, __builtin_fmaf(seq(t + 1), w1, seq(t) * w0))));
             }
         }
         if (kind < 2) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const float sqs = group_sum<64>(y[t] * y[t]);
-                if ((threadIdx.x & 63) == 0) cpart[t][threadIdx.x >> 6] = sqs;
+                if (t < ntok) {   // uniform
+                    const float sqs = group_sum<64>(y[t] * y[t]);
+                    if ((threadIdx.x & 63) == 0) cpart[t][threadIdx.x >> 6] = sqs;
+                }
             }
         }
         __syncthreads();
         if (kind < 3) {
             if (kind < 2) {
 #pragma unroll
-                for (int t = 0; t < NT; ++t) y[t] *= rsqrtf((cpart[t][2 * kind] + cpart[t][2 * kind + 1]) + a.eps);
+                for (int t = 0; t < NT; ++t)
+                    if (t < ntok) y[t] *= rsqrtf((cpart[t][2 * kind] + cpart[t][2 * kind + 1]) + a.eps);
             }
 #pragma unroll
-            for (int t = 0; t < NT; ++t) (kind == 0 ? cq : kind == 1 ? ck : cv)[t][j] = y[t];
-            if constexpr (NT == 2) {
+            for (int t = 0; t < NT; ++t)
+                if (t < ntok) (kind == 0 ? cq : kind == 1 ? ck : cv)[t][j] = y[t];
+            if constexpr (SNAP) {
                 hsnap[3 * ch] = h1;
                 hsnap[3 * ch + 1] = h2;
-                hsnap[3 * ch + 2] = x0;
+                hsnap[3 * ch + 2] = xr[0];
                 hist[3 * ch] = h2;
-                hist[3 * ch + 1] = x0;
-                hist[3 * ch + 2] = x1;
+                hist[3 * ch + 1] = xr[0];
+                hist[3 * ch + 2] = xr[1];
             } else {
-                hist[3 * ch] = h1;
-                hist[3 * ch + 1] = h2;
-                hist[3 * ch + 2] = x0;
+                float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f;   // the last three inputs
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    if (t == ntok - 1) {
+                        n0 = seq(t + 1);
+                        n1 = seq(t + 2);
+                        n2 = seq(t + 3);
+                    }
+                }
+                hist[3 * ch] = n0;
+                hist[3 * ch + 1] = n1;
+                hist[3 * ch + 2] = n2;
             }
         }
         __syncthreads();   // cq / ck / cv are read by other lanes at the top of the token loop
@@ -228,6 +259,7 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
         if (threadIdx.x < S) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
+                if (t >= ntok) break;
                 ck[t][threadIdx.x] = a.k[static_cast<size_t>(t) * a.tok_stride + qh * S + threadIdx.x];
                 cq[t][threadIdx.x] = a.q[static_cast<size_t>(t) * a.tok_stride + qh * S + threadIdx.x];
             }
@@ -236,69 +268,70 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     float vreg[NT];
     if constexpr (!CONV) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) vreg[t] = a.v[static_cast<size_t>(t) * a.tok_stride + head * S + col];
+        for (int t = 0; t < NT; ++t)
+            vreg[t] = t < ntok ? a.v[static_cast<size_t>(t) * a.tok_stride + head * S + col] : 0.0f;
     }
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float g, b;
-            if constexpr (RAW) {
-                b = 1.0f / (1.0f + expf(-gin[t][0]));
-                const float vv = gin[t][1] + gin[t][2];
-                g = expf((vv > 20.0f ? vv : log1pf(expf(vv))) * gin[t][3]);
-            } else {
-                b = gin[t][0];
-                g = expf(gin[t][1]);
-            }
-            gbt[t][0] = g;
-            gbt[t][1] = b;
+    if (gt < ntok) {
+        float g, b;
+        if constexpr (RAW) {
+            b = 1.0f / (1.0f + expf(-gin[0]));
+            const float vv = gin[1] + gin[2];
+            g = expf((vv > 20.0f ? vv : log1pf(expf(vv))) * gin[3]);
+        } else {
+            b = gin[0];
+            g = expf(gin[1]);
         }
+        gbt[gt][0] = g;
+        gbt[gt][1] = b;
     }
     __syncthreads();
 
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        const float g = gbt[t][0], beta = gbt[t][1];
-        float kv = 0.0f;
+        if (t < ntok) {   // uniform: the barrier below is reached by every lane or none
+            const float g = gbt[t][0], beta = gbt[t][1];
+            float kv = 0.0f;
 #pragma unroll
-        for (int r = 0; r < RPG; ++r) kv = __builtin_fmaf(s[r], ck[t][rg * RPG + r], kv);
-        kv += __shfl_xor(kv, 16, 64);   // (rg 0 + rg 1) + (rg 2 + rg 3), the same bits in all four lanes
-        kv += __shfl_xor(kv, 32, 64);
-        const float vcol = CONV ? cv[CONV ? t : 0][col] : vreg[t];
-        const float delta = (vcol - g * kv) * beta;
-        float o = 0.0f;
+            for (int r = 0; r < RPG; ++r) kv = __builtin_fmaf(s[r], ck[t][rg * RPG + r], kv);
+            kv += __shfl_xor(kv, 16, 64);   // (rg 0 + rg 1) + (rg 2 + rg 3), the same bits in all four lanes
+            kv += __shfl_xor(kv, 32, 64);
+            const float vcol = CONV ? cv[CONV ? t : 0][col] : vreg[t];
+            const float delta = (vcol - g * kv) * beta;
+            float o = 0.0f;
 #pragma unroll
-        for (int r = 0; r < RPG; ++r) {
-            s[r] = __builtin_fmaf(g, s[r], ck[t][rg * RPG + r] * delta);
-            o = __builtin_fmaf(s[r], cq[t][rg * RPG + r], o);
-        }
-        o += __shfl_xor(o, 16, 64);
-        o += __shfl_xor(o, 32, 64);
-        const float oc = o * 0.08838834764831845f;   // 1 / sqrt(128)
-        if constexpr (NT == 2) {
-            if (t == 0) {
-#pragma unroll
-                for (int r = 0; r < RPG; ++r) snap[base + r * row_stride] = s[r];
+            for (int r = 0; r < RPG; ++r) {
+                s[r] = __builtin_fmaf(g, s[r], ck[t][rg * RPG + r] * delta);
+                o = __builtin_fmaf(s[r], cq[t][rg * RPG + r], o);
             }
-        }
-        const float ss = group_sum<16>(oc * oc);   // the wave's 16 columns (row-group 0 lanes carry them)
-        if (ln == 0) wsum[t][wv] = ss;
-        __syncthreads();
-        float tot = 0.0f;
+            o += __shfl_xor(o, 16, 64);
+            o += __shfl_xor(o, 32, 64);
+            const float oc = o * 0.08838834764831845f;   // 1 / sqrt(128)
+            if constexpr (SNAP) {
+                if (t == 0) {
 #pragma unroll
-        for (int w = 0; w < S * RG / 64; ++w) tot += wsum[t][w];
-        if (rg == 0) {
-            const float scale = rsqrtf(tot / static_cast<float>(S) + a.eps);
-            ybuf[t][col] = oc * scale * gam * silu(zz[t]);
+                    for (int r = 0; r < RPG; ++r) snap[base + r * row_stride] = s[r];
+                }
+            }
+            const float ss = group_sum<16>(oc * oc);   // the wave's 16 columns (row-group 0 lanes carry them)
+            if (ln == 0) wsum[t][wv] = ss;
+            __syncthreads();
+            float tot = 0.0f;
+#pragma unroll
+            for (int w = 0; w < S * RG / 64; ++w) tot += wsum[t][w];
+            if (rg == 0) {
+                const float scale = rsqrtf(tot / static_cast<float>(S) + a.eps);
+                ybuf[t][col] = oc * scale * gam * silu(zz[t]);
+            }
         }
     }
     __syncthreads();
-    // y and its Q8_1 blocks: lane -> (token, column); 32-lane groups are whole blocks
-    if (threadIdx.x < NT * S) {
-        const int t = threadIdx.x / S, c = threadIdx.x - t * S;
-        const float yv = ybuf[t][c];
-        a.y[static_cast<size_t>(t) * a.y_stride + head * S + c] = yv;
-        if (a.q8) q8_1_store_lane(yv, a.q8 + static_cast<size_t>(t) * a.q8_stride + (head * 4 + (c >> 5)) * kQ8_1Bytes);
+    // y and its Q8_1 blocks: lane -> (token, column); 32-lane groups are whole blocks, and ntok * 128 is a multiple of
+    // the wave size, so every pass has whole waves active
+    for (int i = threadIdx.x; i < ntok * S; i += S * RG) {
+        const int t = i / S, cc = i - t * S;
+        const float yv = ybuf[t][cc];
+        a.y[static_cast<size_t>(t) * a.y_stride + head * S + cc] = yv;
+        if (a.q8) q8_1_store_lane(yv, a.q8 + static_cast<size_t>(t) * a.q8_stride + (head * 4 + (cc >> 5)) * kQ8_1Bytes);
     }
 #pragma unroll
     for (int r = 0; r < RPG; ++r) state[base + r * row_stride] = s[r];
@@ -339,8 +372,9 @@ extern "C" int rmi_fused_gdn_step_norm_silu_q8(float* state, const float* q, con
     return launch_status("fused_gdn_step_norm_silu_q8");
 }
 
-// ---- engine surface: qkv|z and beta|alpha GEMV outputs, 1 or 2 tokens, selector-based rollback buffers --------------
-// Per token t: qkvz + t * qkvz_stride holds [q h_k*128 | k h_k*128 | v h_v*128 | z h_v*128]; ab + t * ab_stride holds
+// ---- engine surface: qkv|z and beta|alpha GEMV outputs, 1..16 tokens, selector-based rollback buffers --------------
+// ntok = 2 is the verify pair (after-token-0 state and history to the non-live buffers); 1 and 3..16 update the live
+// buffers in place (3..16: an ingest chunk, the row-batched step of src/qwythos_ingest.cu).  Per token t: qkvz + t * qkvz_stride holds [q h_k*128 | k h_k*128 | v h_v*128 | z h_v*128]; ab + t * ab_stride holds
 // [beta h_v | alpha h_v] (both read only).  History per value head, [h_v][3 * 128][3].  Output y + t * y_stride, q8
 // + t * q8_stride.
 extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_a, float* hist_b, const int* sel,
@@ -348,7 +382,7 @@ extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_
                                     const float* dt, const float* ssm_a, const float* gamma, float eps, float* y,
                                     int y_stride, uint8_t* q8, int q8_stride, int h_k, int h_v, int ntok,
                                     void* stream) {
-    if (h_k <= 0 || h_v <= 0 || h_v % h_k || ntok < 1 || ntok > 2)
+    if (h_k <= 0 || h_v <= 0 || h_v % h_k || ntok < 1 || ntok > kMaxCols)
         return fail(RMI_ERR_SHAPE, "gdn_layer_tokens: invalid arguments");
     const int channels = 2 * h_k * S + h_v * S;
     if (channels % 256 != 0 || qkvz_stride < channels + h_v * S)
@@ -366,7 +400,9 @@ extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_
     a.y = y; a.y_stride = y_stride; a.q8 = q8; a.q8_stride = q8_stride;
     a.h_k = h_k; a.h_v = h_v;
     a.hist_a = hist_a; a.hist_b = hist_b; a.conv_w = conv_w;
+    a.ntok = ntok;
     if (ntok == 2) hipLaunchKernelGGL((gdn_step_kernel<2, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
-    else hipLaunchKernelGGL((gdn_step_kernel<1, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
+    else if (ntok == 1) hipLaunchKernelGGL((gdn_step_kernel<1, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
+    else hipLaunchKernelGGL((gdn_step_kernel<kMaxCols, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
     return launch_status("gdn_layer_tokens");
 }

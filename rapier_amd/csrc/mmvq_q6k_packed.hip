@@ -5,19 +5,21 @@
 // owns the packed buffer (rmi_q6_k_packed_bytes / rmi_q6_k_pack) and calls the packed GEMV on it directly.
 //
 // Packed layout.  Rows are grouped in quads (4 rows; the last quad zero-padded) and each row is cut in chunks of 8
-// Q6_K blocks (2048 elements).  The 6720 bytes of one (quad, chunk) wave tile are re-laid so that lane l = 16 r + hb
+// Q6_K blocks (2048 elements).  The 6720 bytes of one (quad, chunk) wave tile are re-laid so that lane l = 4 hb + r
 // (row r of the quad, half-block hb: block hb / 2, half hb % 2) finds its half-block in registers after fully
 // coalesced loads:
 //     [    0, 4096)  ql: 16-byte unit u (0..3) of lane l at u * 1024 + 16 l   (ql bytes [64 n + 16 u, +16))
 //     [ 4096, 6144)  qh: unit u (0..1) of lane l at 4096 + u * 1024 + 16 l    (qh bytes [32 n + 16 u, +16))
 //     [ 6144, 6656)  sc: lane l's 8 sub-scales at 6144 + 8 l                  (sc bytes [8 n, +8))
-//     [ 6656, 6720)  d:  block (r, b)'s fp16 scale at 6656 + 2 (8 r + b)
+//     [ 6656, 6720)  d:  block (r, b)'s fp16 scale at 6656 + 2 (4 b + r)
+// The four rows of a half-block sit in four adjacent lanes: that is the operand layout of the 16-block 4x4x4 int8
+// MFMA (block = half-block, A row = quad row), which the 8 / 16-column ingest kernel runs on.
 // Wave tiles are stored quad-major: tile (q, c) at (q * nch + c) * 6720.
 //
 // Kernel: every wave streams its own quads (no workgroup barrier after the activation staging): the (quad, chunk)
 // steps of its quads are loaded D steps ahead straight into registers (8 loads per step per lane, each a contiguous
 // 1 KB / 512 B wave access), decoded as in the tiled kernel (v_dot4 with the "-32" folded into the staged record),
-// and a row's 16 lanes are reduced by the same xor butterfly.  Lane ownership, per-lane accumulation order and the
+// and a row's 16 lanes are reduced by the same xor butterfly (over hb: lane offsets 32, 16, 8, 4).  Lane ownership, per-lane accumulation order and the
 // reduction tree are those of the 16-row tiled kernel, so the results are bitwise the same, every column of an
 // ncols >= 2 call is bitwise the ncols = 1 result, and the residual variant is bitwise plain + res.
 #include "rmi_common.h"
@@ -34,7 +36,9 @@ constexpr int kChunkBlocks = 8;                           // Q6_K blocks per row
 constexpr int kChunkElems = kChunkBlocks * 256;           // 2048
 constexpr int kWaveTile = kQuad * kChunkBlocks * kQ6KBytes;   // 6720
 constexpr int kNB = kChunkElems / 32;                     // Q8_1 blocks per chunk per column (64)
-constexpr int kMaxStageBytes = 64 * 1024;                 // activation LDS per workgroup
+constexpr int kMaxStageBytes = 64 * 1024;                 // activation LDS per workgroup, up to 4 columns
+constexpr int kWideStageBytes = 160 * 1024;               // 8 / 16 columns: the whole LDS of a CU (gfx950)
+constexpr int kWideWaves = 8;                             // waves per workgroup sharing one wide activation stage
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -55,6 +59,16 @@ __device__ __forceinline__ int subblock_dot(const int (&v)[8], const int (&u)[8]
     return __mul24(sc0, d0) + __mul24(sc1, d1);   // |sc|, |d| < 2^23: exact
 }
 
+// sum over the 16 half-blocks of a row (lanes 4 hb + r): the xor butterfly over hb with offsets 8, 4, 2, 1, the tree
+// of the 16-row tiled kernel's row sum
+__device__ __forceinline__ float hb_sum(float v) {
+    v += __shfl_xor(v, 32, 64);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 4, 64);
+    return v;
+}
+
 // ---- pack: one thread per (quad, chunk, lane) --------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void q6k_pack_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ wp,
                                                             int n_in, int n_out, size_t nslots) {
@@ -64,7 +78,7 @@ __global__ __launch_bounds__(kThreads) void q6k_pack_kernel(const uint8_t* __res
     const int l = static_cast<int>(gid & 63);
     const size_t tile = gid >> 6;                         // q * nch + c
     const int q = static_cast<int>(tile / nch), c = static_cast<int>(tile - static_cast<size_t>(q) * nch);
-    const int r = l >> 4, hb = l & 15, b = hb >> 1, n = hb & 1;
+    const int r = l & 3, hb = l >> 2, b = hb >> 1, n = hb & 1;
     const int row = kQuad * q + r;
     uint8_t* dst = wp + tile * kWaveTile;
     const bool live = row < n_out;
@@ -75,8 +89,8 @@ __global__ __launch_bounds__(kThreads) void q6k_pack_kernel(const uint8_t* __res
         for (int i = 0; i < 16; ++i) dst[4096 + u * 1024 + 16 * l + i] = live ? src[128 + 32 * n + 16 * u + i] : 0;
     for (int i = 0; i < 8; ++i) dst[6144 + 8 * l + i] = live ? src[192 + 8 * n + i] : 0;
     if (n == 0) {
-        dst[6656 + 2 * (8 * r + b)] = live ? src[208] : 0;
-        dst[6656 + 2 * (8 * r + b) + 1] = live ? src[209] : 0;
+        dst[6656 + 2 * (4 * b + r)] = live ? src[208] : 0;
+        dst[6656 + 2 * (4 * b + r) + 1] = live ? src[209] : 0;
     }
 }
 
@@ -117,7 +131,7 @@ __device__ __forceinline__ void stage_activations(const uint8_t* __restrict__ x,
 template <int NCOLS>
 __device__ __forceinline__ void accumulate_step(const WTile& wt, int lane, const uint4* lqc, const uint4* lrc, int xcs,
                                                 float (&tot)[NCOLS]) {
-    const int hb = lane & 15, b = hb >> 1, n = hb & 1;
+    const int hb = lane >> 2, b = hb >> 1, n = hb & 1;
     uint32_t Q[16], H[8];
 #pragma unroll
     for (int i = 0; i < 16; ++i) Q[i] = wt.ql[i >> 2][i & 3];
@@ -158,10 +172,12 @@ __device__ __forceinline__ void accumulate_step(const WTile& wt, int lane, const
     for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
 }
 
-template <int NCOLS, bool RES, int D>
-__global__ __launch_bounds__(kThreads) void q6k_packed_gemv(const uint8_t* __restrict__ wp,
-                                                            const uint8_t* __restrict__ x, float* y,
-                                                            const float* res, float* partials, int n_in, int n_out) {
+// NW waves per workgroup share the staged activations: 4 for up to 4 columns (several workgroups per CU), 8 for the
+// 8 / 16-column ingest passes, whose stage fills most of the CU's LDS (one workgroup per CU)
+template <int NCOLS, bool RES, int D, int NW>
+__global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __restrict__ wp,
+                                                           const uint8_t* __restrict__ x, float* y,
+                                                           const float* res, float* partials, int n_in, int n_out) {
     extern __shared__ uint4 smem[];
     const int t = threadIdx.x, lane = t & 63;
     const int nch = n_in / kChunkElems;
@@ -170,8 +186,8 @@ __global__ __launch_bounds__(kThreads) void q6k_packed_gemv(const uint8_t* __res
     uint4* lq = smem;                            // codes: 2 units per block
     uint4* lrec = smem + 2 * NCOLS * nbt;        // records
     const int nq = (n_out + kQuad - 1) / kQuad;
-    const int GW = static_cast<int>(gridDim.x) * (kThreads / 64);
-    const int gw = static_cast<int>(blockIdx.x) * (kThreads / 64) + (t >> 6);
+    const int GW = static_cast<int>(gridDim.x) * NW;
+    const int gw = static_cast<int>(blockIdx.x) * NW + (t >> 6);
     const int my_quads = gw < nq ? (nq - 1 - gw) / GW + 1 : 0;
     const int nsteps = my_quads * nch;
 
@@ -186,16 +202,16 @@ __global__ __launch_bounds__(kThreads) void q6k_packed_gemv(const uint8_t* __res
         for (int u = 0; u < 2; ++u)
             b.qh[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + 4096 + u * 1024 + 16 * lane));
         b.sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
-        b.d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (8 * (lane >> 4) + ((lane & 15) >> 1)));
+        b.d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (4 * (lane >> 3) + (lane & 3)));
     };
 #pragma unroll
     for (int s = 0; s < D; ++s)
         if (s < nsteps) issue(s, buf[s]);
 
-    stage_activations(x, NCOLS * nbt, nbt, lq, lrec, t, kThreads);
+    stage_activations(x, NCOLS * nbt, nbt, lq, lrec, t, 64 * NW);
     __syncthreads();
 
-    const int r = lane >> 4, hb = lane & 15;
+    const int r = lane & 3, hb = lane >> 2;
     float tot[NCOLS];
 #pragma unroll
     for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
@@ -216,22 +232,227 @@ __global__ __launch_bounds__(kThreads) void q6k_packed_gemv(const uint8_t* __res
                 const int np = (n_out + 3) / 4;
 #pragma unroll
                 for (int col = 0; col < NCOLS; ++col) {
-                    float v = group_sum<16>(tot[col]);
+                    float v = hb_sum(tot[col]);
                     tot[col] = 0.0f;
                     if constexpr (RES) {
                         if (row < n_out) v += res[static_cast<size_t>(col) * n_out + row];
                     }
                     if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v;
                     if constexpr (RES) {
-                        // partial of the quad: squares of its rows in row order (lanes 0, 16, 32, 48)
-                        const float v0 = __shfl(v, 0, 64), v1 = __shfl(v, 16, 64);
-                        const float v2 = __shfl(v, 32, 64), v3 = __shfl(v, 48, 64);
+                        // partial of the quad: squares of its rows in row order (lanes 0, 1, 2, 3)
+                        const float v0 = __shfl(v, 0, 64), v1 = __shfl(v, 1, 64);
+                        const float v2 = __shfl(v, 2, 64), v3 = __shfl(v, 3, 64);
                         if (lane == 0) {
                             const int row0 = kQuad * q;
                             float p = __builtin_fmaf(v0, v0, 0.0f);
                             if (row0 + 1 < n_out) p = __builtin_fmaf(v1, v1, p);
                             if (row0 + 2 < n_out) p = __builtin_fmaf(v2, v2, p);
                             if (row0 + 3 < n_out) p = __builtin_fmaf(v3, v3, p);
+                            partials[static_cast<size_t>(col) * np + q] = p;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---- ingest GEMM: 8 / 16 columns on the 16-block 4x4x4 int8 MFMA -------------------------------------------------
+// Same wave tiles, lane ownership and fp32 arithmetic as q6k_packed_gemv, with the integer dot products on the matrix
+// cores.  MFMA block b = half-block hb (lanes 4 hb .. 4 hb + 3), A row i = quad row i (the lane's own unpacked
+// weights), B column j = activation column 4 cg + j, and D[i][j] lands in lane 4 hb + j, register i (layout of
+// v_mfma_i32_4x4x4_16b_i8).  One 16-element sub-block is four MFMAs over its four K-quads starting from 0: the exact
+// int32 sum the sdot4 chain forms.  The epilogue then repeats the decode kernel's operations in its order - corr + sum,
+// the two sub-scales by __mul24, fma(d8, sd, acc) over k = 0, 2, 1, 3, fma(d, acc, tot) per tile, the hb butterfly -
+// so every column is bitwise the single-column GEMV.  The quad's sub-scales and block scales reach the column lanes by
+// quad broadcasts.
+//
+// Stage: per (column group cg, block jb) 13 uint4 = [codes 0..15 of columns 4 cg + 0..3 | codes 16..31 | records
+// {-32 sum(q[0:16]), -32 sum(q[16:32]), d8, 0} | pad]; the pad makes a half-block step 832 bytes, so the 16 lanes of
+// one LDS pass (4 half-blocks x 4 columns) hit distinct banks.
+constexpr int kMStride = 13;   // uint4 per (cg, block)
+
+__device__ __forceinline__ void stage_activations_mfma(const uint8_t* __restrict__ x, int ncols, int nbt, uint4* st,
+                                                       int t, int nthreads) {
+    for (int J = t; J < ncols * nbt; J += nthreads) {
+        const int col = J / nbt, jb = J - col * nbt;
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
+        uint32_t wv[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) wv[i] = p[i];
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 1; i <= 4; ++i) s0 = sdot4(static_cast<int>(wv[i]), 0x01010101, s0);
+#pragma unroll
+        for (int i = 5; i <= 8; ++i) s1 = sdot4(static_cast<int>(wv[i]), 0x01010101, s1);
+        uint4* q = st + static_cast<size_t>((col >> 2) * nbt + jb) * kMStride + (col & 3);
+        q[0] = make_uint4(wv[1], wv[2], wv[3], wv[4]);
+        q[4] = make_uint4(wv[5], wv[6], wv[7], wv[8]);
+        q[8] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1),
+                          __float_as_uint(half_bits_to_float(wv[0])), 0u);
+    }
+}
+
+// value of lane 4 (l / 4) + i (a broadcast inside each group of four lanes)
+template <int I>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), I | (I << 2) | (I << 4) | (I << 6), 0xf,
+                                                          0xf, false));
+}
+
+template <int NCG, bool RES, int D>
+__global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t* __restrict__ wp,
+                                                                   const uint8_t* __restrict__ x, float* y,
+                                                                   const float* res, float* partials, int n_in,
+                                                                   int n_out) {
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int nch = n_in / kChunkElems;
+    const int nbt = n_in / 32;
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    const int GW = static_cast<int>(gridDim.x) * kWideWaves;
+    const int gw = static_cast<int>(blockIdx.x) * kWideWaves + (t >> 6);
+    const int my_quads = gw < nq ? (nq - 1 - gw) / GW + 1 : 0;
+    const int nsteps = my_quads * nch;
+
+    WTile buf[D];
+    auto issue = [&](int f, WTile& b) {
+        const int qi = f / nch, c = f - qi * nch;
+        const uint8_t* base = wp + (static_cast<size_t>(gw + qi * GW) * nch + c) * kWaveTile;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            b.ql[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * 1024 + 16 * lane));
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            b.qh[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + 4096 + u * 1024 + 16 * lane));
+        b.sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
+        b.d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (4 * (lane >> 3) + (lane & 3)));
+    };
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+        if (s < nsteps) issue(s, buf[s]);
+
+    stage_activations_mfma(x, 4 * NCG, nbt, smem, t, 64 * kWideWaves);
+    __syncthreads();
+
+    const int jj = lane & 3, hb = lane >> 2, b = hb >> 1, n = hb & 1;
+    // stage offsets (uint4 units, 32-bit): column group g at goff[g], the lane's column and half-block at lbase
+    int goff[NCG];
+#pragma unroll
+    for (int g = 0; g < NCG; ++g) goff[g] = g * nbt * kMStride;
+    const int lbase = (8 * b + 4 * n) * kMStride + jj;
+    float tot[4][NCG];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g = 0; g < NCG; ++g) tot[i][g] = 0.0f;
+
+    for (int f0 = 0; f0 < nsteps; f0 += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int f = f0 + s;
+            if (f >= nsteps) break;   // uniform across the wave
+            const int qi = f / nch, c = f - qi * nch;
+            const WTile wt = buf[s];
+            if (f + D < nsteps) issue(f + D, buf[s]);
+
+            uint32_t Q[16], H[8];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) Q[i] = wt.ql[i >> 2][i & 3];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) H[i] = wt.qh[i >> 2][i & 3];
+            // the quad's four rows: sub-scale words and block scales
+            uint32_t S0[4], S1[4];
+            float dr[4];
+            S0[0] = quad_bcast<0>(wt.sc.x); S0[1] = quad_bcast<1>(wt.sc.x);
+            S0[2] = quad_bcast<2>(wt.sc.x); S0[3] = quad_bcast<3>(wt.sc.x);
+            S1[0] = quad_bcast<0>(wt.sc.y); S1[1] = quad_bcast<1>(wt.sc.y);
+            S1[2] = quad_bcast<2>(wt.sc.y); S1[3] = quad_bcast<3>(wt.sc.y);
+            dr[0] = half_bits_to_float(quad_bcast<0>(wt.d)); dr[1] = half_bits_to_float(quad_bcast<1>(wt.d));
+            dr[2] = half_bits_to_float(quad_bcast<2>(wt.d)); dr[3] = half_bits_to_float(quad_bcast<3>(wt.d));
+
+            float acc[4][NCG];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int g = 0; g < NCG; ++g) acc[i][g] = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh) {
+                    const int k = kk + 2 * kh;
+                    int v[8];
+#pragma unroll
+                    for (int ww = 0; ww < 8; ++ww)
+                        v[ww] = static_cast<int>(((Q[8 * kk + ww] >> (4 * kh)) & 0x0f0f0f0fu) |
+                                                 (((H[ww] >> (2 * k)) & 0x03030303u) << 4));
+                    // two column groups at a time: their codes and records first, then the four independent MFMA
+                    // chains interleaved, then the epilogues (no chain waits on its own loads or results)
+                    const int lo = lbase + (c * kNB + k) * kMStride;
+#pragma unroll
+                    for (int g0 = 0; g0 < NCG; g0 += 2) {
+                        uint4 qa[2], qb[2], rec[2];
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            qa[h] = smem[goff[g0 + h] + lo];
+                            qb[h] = smem[goff[g0 + h] + lo + 4];
+                            rec[h] = smem[goff[g0 + h] + lo + 8];
+                        }
+                        i32x4 d0[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}}, d1[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) {
+#pragma unroll
+                            for (int h = 0; h < 2; ++h) {
+                                d0[h] = __builtin_amdgcn_mfma_i32_4x4x4i8(v[qq], static_cast<int>(qa[h][qq]), d0[h], 0,
+                                                                          0, 0);
+                                d1[h] = __builtin_amdgcn_mfma_i32_4x4x4i8(v[4 + qq], static_cast<int>(qb[h][qq]), d1[h],
+                                                                          0, 0, 0);
+                            }
+                        }
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const float d8 = __uint_as_float(rec[h].z);
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const int sc0 = sc_byte2(S0[i], S1[i], 2 * k), sc1 = sc_byte2(S0[i], S1[i], 2 * k + 1);
+                                const int sd = __mul24(sc0, d0[h][i] + static_cast<int>(rec[h].x)) +
+                                               __mul24(sc1, d1[h][i] + static_cast<int>(rec[h].y));
+                                acc[i][g0 + h] = __builtin_fmaf(d8, static_cast<float>(sd), acc[i][g0 + h]);
+                            }
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int g = 0; g < NCG; ++g) tot[i][g] = __builtin_fmaf(dr[i], acc[i][g], tot[i][g]);
+
+            if (c == nch - 1) {   // the quad's rows are complete
+                const int q = gw + qi * GW;
+                const int np = (n_out + 3) / 4;
+#pragma unroll
+                for (int g = 0; g < NCG; ++g) {
+                    const int col = 4 * g + jj;
+                    float v[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        v[i] = hb_sum(tot[i][g]);
+                        tot[i][g] = 0.0f;
+                        const int row = kQuad * q + i;
+                        if constexpr (RES) {
+                            if (row < n_out) v[i] += res[static_cast<size_t>(col) * n_out + row];
+                        }
+                        if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v[i];
+                    }
+                    if constexpr (RES) {
+                        if (hb == 0) {   // squares of the quad's rows in row order
+                            const int row0 = kQuad * q;
+                            float p = __builtin_fmaf(v[0], v[0], 0.0f);
+                            if (row0 + 1 < n_out) p = __builtin_fmaf(v[1], v[1], p);
+                            if (row0 + 2 < n_out) p = __builtin_fmaf(v[2], v[2], p);
+                            if (row0 + 3 < n_out) p = __builtin_fmaf(v[3], v[3], p);
                             partials[static_cast<size_t>(col) * np + q] = p;
                         }
                     }
@@ -273,19 +494,54 @@ void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* r
     const size_t lds = static_cast<size_t>(NCOLS) * (n_in / 32) * 48;
     const dim3 grid(packed_grid(nq)), block(kThreads);
     if (depth >= 4)
-        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 4, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
     else if (depth == 3)
-        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 3>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 3, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
     else
-        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 2>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 2, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
 }
 
-// columns per pass: at most 4, and the pass's staged activations within kMaxStageBytes
+// LDS of the ingest stage: kMStride uint4 per (4-column group, block)
+size_t wide_stage_bytes(int n_in, int ncols) {
+    return static_cast<size_t>(ncols / 4) * (n_in / 32) * kMStride * 16;
+}
+
+// the widest ingest pass (16 or 8 columns) whose stage fits kWideStageBytes, or 0
+int wide_cols(int n_in, int remaining) {
+    if (remaining >= 16 && wide_stage_bytes(n_in, 16) <= kWideStageBytes) return 16;
+    if (remaining >= 8 && wide_stage_bytes(n_in, 8) <= kWideStageBytes) return 8;
+    return 0;
+}
+
+// 8 / 16 columns in one weight pass on the MFMA ingest kernel: one 8-wave workgroup per CU (the stage takes up to
+// 160 KB of LDS), the quads split evenly over the waves
+template <int NCOLS, bool RES>
+int launch_packed_wide(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
+                       int n_out, hipStream_t s) {
+    constexpr int D = 3;
+    auto kern = q6k_packed_mfma<NCOLS / 4, RES, D>;
+    static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 kWideStageBytes) == hipSuccess;
+    if (!attr) return fail(RMI_ERR_LAUNCH, "native_q6_k_mmvq_packed: wide LDS stage not available");
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    const size_t lds = wide_stage_bytes(n_in, NCOLS);
+    const int max_waves = cu_count() * kWideWaves;
+    const int qpw = (nq + max_waves - 1) / max_waves;
+    const int waves = (nq + qpw - 1) / qpw;
+    const dim3 grid((waves + kWideWaves - 1) / kWideWaves), block(64 * kWideWaves);
+    hipLaunchKernelGGL(kern, grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+    return RMI_OK;
+}
+
+// columns per narrow pass: at most 4, and the pass's staged activations within kMaxStageBytes
 int cols_per_pass(int n_in) {
     const int per = kMaxStageBytes / ((n_in / 32) * 48);
     return std::max(1, std::min(4, per));
 }
 
+// Columns are cut into passes (16 or 8 wide, then up to 4); each pass reads the weights once.  The pass width never
+// changes a column's result: lane ownership and reduction order depend on the shape only.
 template <bool RES>
 int run_packed(const void* wpv, const void* xv, float* y, const float* res, float* partials, int n_in, int n_out,
                int ncols, hipStream_t s) {
@@ -294,8 +550,9 @@ int run_packed(const void* wpv, const void* xv, float* y, const float* res, floa
     const int per = cols_per_pass(n_in);
     const size_t xcol = static_cast<size_t>(n_in / 32) * kQ8_1Bytes;
     const size_t pcol = static_cast<size_t>((n_out + 3) / 4);
-    for (int j = 0; j < ncols; j += per) {
-        const int nj = std::min(per, ncols - j);
+    for (int j = 0; j < ncols;) {
+        const int wide = wide_cols(n_in, ncols - j);
+        const int nj = wide ? wide : std::min(per, ncols - j);
         const uint8_t* xj = x + j * xcol;
         float* yj = y + static_cast<size_t>(j) * n_out;
         const float* rj = RES ? res + static_cast<size_t>(j) * n_out : nullptr;
@@ -304,9 +561,16 @@ int run_packed(const void* wpv, const void* xv, float* y, const float* res, floa
             case 1: launch_packed<1, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
             case 2: launch_packed<2, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
             case 3: launch_packed<3, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
-            default: launch_packed<4, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
+            case 4: launch_packed<4, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
+            case 8:
+                if (const int rc = launch_packed_wide<8, RES>(wp, xj, yj, rj, pj, n_in, n_out, s)) return rc;
+                break;
+            default:
+                if (const int rc = launch_packed_wide<16, RES>(wp, xj, yj, rj, pj, n_in, n_out, s)) return rc;
+                break;
         }
         if (const int rc = launch_status("native_q6_k_mmvq_packed")) return rc;
+        j += nj;
     }
     return RMI_OK;
 }

@@ -11,6 +11,7 @@ import ctypes
 from . import _call, _stream, last_error, lib
 
 GREEDY, MTP, MTP_FORCED = 0, 1, 2
+BUF_GDN_STATE, BUF_GDN_HIST, BUF_K_CACHE, BUF_V_CACHE, BUF_HIDDEN = 0, 1, 2, 3, 4
 
 
 class ModelConfig(ctypes.Structure):
@@ -55,6 +56,10 @@ def _bind():
         "rmi_engine_destroy": (ctypes.c_int, [ctypes.c_void_p]),
         "rmi_engine_info": (ctypes.c_int, [ctypes.c_void_p, P(EngineInfo)]),
         "rmi_engine_prefill": (ctypes.c_int, [ctypes.c_void_p, P(ctypes.c_int), ctypes.c_int, P(ctypes.c_int)]),
+        "rmi_engine_prefill_batch": (ctypes.c_int, [ctypes.c_void_p, P(ctypes.c_int), ctypes.c_int, ctypes.c_int,
+                                                    P(ctypes.c_int)]),
+        "rmi_engine_read": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_size_t,
+                                           ctypes.c_void_p, ctypes.c_size_t]),
         "rmi_engine_synth_context": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_int,
                                                     P(ctypes.c_int)]),
         "rmi_engine_save_state": (ctypes.c_int, [ctypes.c_void_p]),
@@ -107,11 +112,19 @@ class Engine:
         _call("rmi_engine_info", self._h, ctypes.byref(i))
         return {k: getattr(i, k) for k, _ in i._fields_}
 
-    def prefill(self, tokens) -> int:
+    def prefill(self, tokens, batch: int = 16) -> int:
+        """Ingest the prompt from position 0; batch 1 is the token-by-token path, 2..16 the chunked one."""
         arr = (ctypes.c_int * len(tokens))(*tokens)
         first = ctypes.c_int()
-        _call("rmi_engine_prefill", self._h, arr, len(tokens), ctypes.byref(first))
+        _call("rmi_engine_prefill_batch", self._h, arr, len(tokens), batch, ctypes.byref(first))
         return first.value
+
+    def read(self, which: int, layer: int, nbytes: int, offset: int = 0):
+        """bytes [offset, offset + nbytes) of an engine buffer (BUF_*) as a uint8 numpy array"""
+        import numpy as np
+        out = np.empty(nbytes, np.uint8)
+        _call("rmi_engine_read", self._h, which, layer, offset, out.ctypes.data_as(ctypes.c_void_p), nbytes)
+        return out
 
     def synth_context(self, n_ctx: int, seed: int, last_token: int) -> int:
         first = ctypes.c_int()

@@ -17,13 +17,13 @@ def rmi():
     return rapier_amd
 
 
-def declared():
-    hdr = open(os.path.join(ROOT, "include", "rapier_mi.h")).read()
+def declared(headers=("rapier_mi.h",)):
+    hdr = "".join(open(os.path.join(ROOT, "include", h)).read() for h in headers)
     return sorted(set(re.findall(r"\b(rmi_\w+)\s*\(", hdr)))
 
 
 def test_every_declared_symbol_is_exported(rmi):
-    names = declared()
+    names = declared(("rapier_mi.h", "rapier_mi_engine.h"))
     assert len(names) >= 30
     missing = [n for n in names if not hasattr(rmi.lib(), n)]
     assert not missing, missing

@@ -80,19 +80,21 @@ def test_flash_decode_short_contexts(orc, rmi, p0):
         assert np.array_equal(y[:NH * HD].reshape(NH, HD), np.repeat(v0, NH // NKV, axis=0))
 
 
-def test_attn_prep_matches_oracle(orc, rmi):
+@pytest.mark.parametrize("ntok", [2, 16])
+def test_attn_prep_matches_oracle(orc, rmi, ntok):
+    """2 tokens (the verify pair) and 16 (an ingest chunk): every token at its own position p0 + t"""
     t_ = torch()
     max_ctx, p0, theta, eps = 1024, 777, 1e7, 1e-6
-    q3 = orc.normal(2 * Q3, seed=950)
+    q3 = orc.normal(ntok * Q3, seed=950)
     qn = (1 + orc.normal(HD, seed=951, std=0.1)).astype(np.float32)
     kn = (1 + orc.normal(HD, seed=952, std=0.1)).astype(np.float32)
     kc = t_.zeros(max_ctx * NKV * HD, dtype=t_.int16, device="cuda:0")
     vc = t_.zeros(max_ctx * NKV * HD, dtype=t_.int16, device="cuda:0")
-    qo = empty(2 * NH * HD)
+    qo = empty(ntok * NH * HD)
     rmi.attn_prep(dev(q3), Q3, dev(qn), dev(kn), kc, vc, dev(np.array([p0], np.int32)), qo, NH, NKV, HD, 64, theta,
-                  eps, 2, max_ctx)
+                  eps, ntok, max_ctx)
     qh, kh, vh = host(qo), host(kc).view(np.float16), host(vc).view(np.float16)
-    for t in range(2):
+    for t in range(ntok):
         src = q3[t * Q3:(t + 1) * Q3]
         qx = np.concatenate([src[h * 2 * HD:h * 2 * HD + HD] for h in range(NH)])
         qref = orc.rope_neox(orc.rms_norm_heads(qx, qn, NH, HD, eps), NH, HD, 64, p0 + t, theta)
@@ -104,3 +106,4 @@ def test_attn_prep_matches_oracle(orc, rmi):
         vref = src[NH * 2 * HD + NKV * HD:].astype(np.float16)
         assert np.array_equal(vh[(p0 + t) * NKV * HD:(p0 + t + 1) * NKV * HD], vref)
     assert not host(kc)[:p0 * NKV * HD].any(), "attn_prep wrote outside its positions"
+    assert not host(kc)[(p0 + ntok) * NKV * HD:].any(), "attn_prep wrote outside its positions"

@@ -141,3 +141,48 @@ def test_reference_surface_entry_points(orc, rmi):
     # the prepared-gate path computes exp(gate) from a stored logit: same math, last-bit differences allowed
     assert_close_rel(host(y), ref["y"], rtol=1e-5, atol_frac=1e-6, what="step y")
     assert np.abs(host(st) - ref["state"]).max() < 1e-5
+
+
+def make_chunk_inputs(orc, ntok, seed):
+    qkvz = orc.normal(ntok * QKVZ, seed=seed)
+    qkvz[CH + 3 * S:CH + 3 * S + 32] *= 1e4                                  # token 0: one z block x 1e4
+    ab = orc.normal(ntok * 2 * H_V, seed=seed + 1)
+    conv_w = orc.normal(4 * CH, seed=seed + 2, std=0.5)
+    hist = orc.normal(3 * CH, seed=seed + 3, std=0.5)
+    state = orc.normal(S * H_V * S, seed=seed + 4, std=0.05)
+    dt = np.zeros(H_V, np.float32)
+    ssm_a = (-np.exp(orc.normal(H_V, seed=seed + 5, std=0.5))).astype(np.float32)
+    gamma = (1 + orc.normal(S, seed=seed + 6, std=0.1)).astype(np.float32)
+    return qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma
+
+
+@pytest.mark.parametrize("ntok", [3, 7, 16])
+def test_gdn_ingest_chunk_bitwise_equal_sequential(orc, rmi, ntok):
+    """an ingest chunk (3..16 tokens in one launch, the row-batched step of src/qwythos_ingest.cu) leaves the state,
+    history, y and Q8_1 of ntok sequential 1-token steps, bit for bit, and updates the live buffers in place"""
+    qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma = make_chunk_inputs(orc, ntok, seed=600 + ntok)
+    hist = expand_hist(hist)
+    r = run_layer(rmi, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok=ntok)
+    assert not r["snap"].any() and not r["hsnap"].any(), "a chunk writes no rollback buffer"
+    u = lambda v: np.asarray(v).view(np.uint32)  # noqa: E731
+    st, hs = state, hist
+    blk = H_V * S // 32 * 36
+    for t in range(ntok):
+        a = run_layer(rmi, qkvz[t * QKVZ:(t + 1) * QKVZ], ab[t * 2 * H_V:(t + 1) * 2 * H_V], conv_w, hs, st, dt, ssm_a,
+                      gamma, ntok=1)
+        assert np.array_equal(u(r["y"][t * H_V * S:(t + 1) * H_V * S]), u(a["y"])), f"y token {t}"
+        assert np.array_equal(r["q8"][t * blk:(t + 1) * blk], a["q8"]), f"q8 token {t}"
+        st, hs = a["state"], a["hist"]
+    assert np.array_equal(u(r["state"]), u(st)) and np.array_equal(u(r["hist"]), u(hs))
+
+
+def test_gdn_ingest_chunk_matches_oracle(orc, rmi):
+    ntok = 16
+    inp = make_chunk_inputs(orc, ntok, seed=700)
+    qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma = inp
+    r = run_layer(rmi, qkvz, ab, conv_w, expand_hist(hist), state, dt, ssm_a, gamma, ntok=ntok)
+    ys, states, hists, _ = oracle_chain(orc, *inp, ntok=ntok)
+    for t in range(ntok):
+        assert_close_rel(r["y"][t * H_V * S:(t + 1) * H_V * S], ys[t], rtol=1e-3, atol_frac=1e-5, what=f"y t{t}")
+    assert np.abs(r["state"] - states[-1]).max() < 2e-3
+    assert np.array_equal(r["hist"], expand_hist(hists[-1]))

@@ -93,10 +93,46 @@ def test_packed_layout_roundtrip(orc, rmi):
     tile0 = wp[:6720]
     rows0 = w.reshape(n_out, -1)[:4].reshape(-1)
     assert np.array_equal(np.sort(tile0), np.sort(rows0))
-    # lane 0 (row 0, block 0, half 0): ql bytes [0, 16) at offset 0, qh [128, 144) at 4096, sc [192, 200) at 6144
-    blk = w[:210]
-    assert np.array_equal(tile0[0:16], blk[0:16])
-    assert np.array_equal(tile0[4096:4112], blk[128:144])
-    assert np.array_equal(tile0[6144:6152], blk[192:200])
-    assert np.array_equal(tile0[6656:6658], blk[208:210])
+    # lane l = 4 hb + r holds row r, half-block hb (block hb // 2, half hb % 2): ql unit u at u * 1024 + 16 l, qh unit
+    # u at 4096 + u * 1024 + 16 l, the 8 sub-scales at 6144 + 8 l; block (r, b)'s d at 6656 + 2 (4 b + r)
+    nb = n_in // 256
+    for lane in (0, 1, 3, 4, 5, 31, 63):
+        r, hb = lane % 4, lane // 4
+        b, n = hb // 2, hb % 2
+        blk = w[(r * nb + b) * 210:(r * nb + b + 1) * 210]
+        for u in range(4):
+            assert np.array_equal(tile0[u * 1024 + 16 * lane:u * 1024 + 16 * lane + 16], blk[64 * n + 16 * u:64 * n + 16 * u + 16])
+        for u in range(2):
+            o = 4096 + u * 1024 + 16 * lane
+            assert np.array_equal(tile0[o:o + 16], blk[128 + 32 * n + 16 * u:128 + 32 * n + 16 * u + 16])
+        assert np.array_equal(tile0[6144 + 8 * lane:6152 + 8 * lane], blk[192 + 8 * n:200 + 8 * n])
+        assert np.array_equal(tile0[6656 + 2 * (4 * b + r):6658 + 2 * (4 * b + r)], blk[208:210])
 
+
+
+@pytest.mark.parametrize("n_in,n_out", [(4096, 12352), (12288, 4096), (8192, 4096), (2048, 1001)])
+@pytest.mark.parametrize("ncols", [16, 13, 8])
+def test_packed_wide_passes_bitwise_equal_single_column(orc, rmi, n_in, n_out, ncols):
+    """ingest widths: 16 / 8 columns in one weight pass (one 8-wave workgroup per CU, up to 160 KB of staged
+    activations), remainders in passes of up to 4; every column bitwise the ncols = 1 result, residual variant
+    bitwise plain + res"""
+    w = orc.gen_q6k(n_out, n_in, seed=n_in + n_out + ncols)
+    xq = orc.quantize_q8_1(orc.normal(ncols * n_in, seed=ncols + n_out), n_in, ncols)
+    wd, xd = dev(w), dev(xq)
+    wp = packed(rmi, wd, n_in, n_out)
+    y = empty(ncols * n_out)
+    rmi.native_q6_k_mmvq_packed(wp, xd, y, n_in, n_out, ncols)
+    yh = host(y)
+    xcol = (n_in // 32) * 36
+    for c in range(ncols):
+        y1 = empty(n_out)
+        rmi.native_q6_k_mmvq_packed(wp, dev(xq[c * xcol:(c + 1) * xcol]), y1, n_in, n_out, 1)
+        assert np.array_equal(host(y1).view(np.uint32), yh[c * n_out:(c + 1) * n_out].view(np.uint32)), f"column {c}"
+    ref = orc.q6k_gemv(w, xq[:xcol], n_in, n_out, ncols=1)
+    assert_close_rel(yh[:n_out], ref, what="wide col 0")
+    res = orc.normal(ncols * n_out, seed=n_out + 5)
+    yr = dev(res.copy())
+    np_ = (n_out + 3) // 4
+    part = empty(ncols * np_)
+    rmi.native_q6_k_mmvq_packed_res_n(wp, xd, yr, yr, part, n_in, n_out, ncols)
+    assert np.array_equal(host(yr).view(np.uint32), (yh + res).view(np.uint32))
