@@ -177,8 +177,10 @@ int rmi_attn_prep(const float* q3, int q3_stride, const float* qn, const float* 
 /* split-K flash decode for ntok query tokens at positions pos[0] + t, sigmoid gate from gate_src (the wq output,
  * gate of head h at + h * 2 * head_dim + head_dim), fp32 y (nullable) and Q8_1 (nullable).  workspace holds
  * rmi_gqa_workspace_bytes(max_ctx, n_kv, nsub) bytes; chunks are 64 * nsub positions.  ntok * (n_head / n_kv)
- * <= 8; q, kcache, vcache and workspace 16-byte aligned.  Replaces gqa_head_kernel (qw:384-442) + sig_mul_quant_kernel
- * (qw:692-704) per column. */
+ * <= 64 (an ingest chunk of 16 tokens at 4 query heads per KV head); q, kcache, vcache and workspace 16-byte
+ * aligned.  Each query's result is bitwise the single-token result at its position.  Replaces gqa_head_kernel
+ * (qw:384-442) + sig_mul_quant_kernel (qw:692-704) per column, and the chunk's shared-K score pass
+ * (gqa_score_chunk_kernel + gqa_from_scores_kernel, qw:444-559). */
 size_t rmi_gqa_workspace_bytes(int max_ctx, int n_kv, int nsub);
 int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* pos,
                          const float* gate_src, int gate_stride, float* y, int y_stride, uint8_t* q8, int q8_stride,

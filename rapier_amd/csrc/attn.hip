@@ -4,10 +4,13 @@
 //   attn_prep   one workgroup per (token, head): q heads get the per-head RMSNorm (weights qn) and NEOX RoPE on the
 //               first n_rot dims -> fp32 q buffer; k heads get RMSNorm (kn) + RoPE and v heads nothing, both stored
 //               as fp16 at cache[pos_t][kv][d].  pos_t = pos[0] + t is read on the device.
-//   partial     split-K flash decode.  Workgroup (chunk, kv head) covers positions [chunk * 64 * nsub, +64 * nsub) for
-//               every query vector of its group (group heads x tokens); each of its 4 waves streams a quarter of the
-//               chunk independently: QK^T and P V both on MFMA 16x16x16 f16 with the fp32 operand (q, p) split into
-//               fp16 hi + lo rows of the same MFMA, online softmax per query.  Writes (m, l, o[256]) per query.
+//   partial     split-K flash decode.  Workgroup (chunk, kv head, slot group) covers positions [chunk * 64 * nsub,
+//               +64 * nsub) for 8 query vectors (slots t * G + gh, group heads x tokens; up to 8 groups, so an ingest
+//               chunk of 16 tokens is one launch); each of its 4 waves streams a quarter of the chunk independently:
+//               QK^T and P V both on MFMA 16x16x16 f16 with the fp32 operand (q, p) split into fp16 hi + lo rows of
+//               the same MFMA, online softmax per query.  Writes (m, l, o[256]) per query.  A slot's arithmetic does
+//               not depend on which group or launch it is in (a wave step past a slot's last position leaves its
+//               running state unchanged), so every query is bitwise its single-token result.
 //   merge       one workgroup per (token, head): merges that query's chunks 0..pos_t / chunk in order, divides, gates
 //               with sigmoid(g) and writes fp32 y plus Q8_1 for the wo GEMV.
 // Query t sees positions <= pos[0] + t.  Chunk boundaries depend only on the query's position, so a verify column's
@@ -20,7 +23,8 @@ namespace {
 constexpr int HD = 256;
 constexpr int SUB = 64;            // positions per chunk unit (4 waves x 16); a chunk is SUB * nsub positions
 constexpr int REC = HD + 4;        // workspace record: m, l, pad, pad, o[256]
-constexpr int SLOTS = 8;           // query vectors per kv head one launch handles (tokens x group heads)
+constexpr int SLOTS = 8;           // query vectors per kv head one partial workgroup handles (tokens x group heads)
+constexpr int kMaxSlots = 64;      // query vectors per kv head one launch handles: SLOTS per slot group, grid.z groups
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -129,12 +133,12 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
                                                           int nsub, int max_ctx, float scale) {
     __shared__ __attribute__((aligned(16))) uint8_t tiles[WAVES * KTILE];
     __shared__ float wstat[WAVES][2][SLOTS];
-    const int chunk = blockIdx.x, kv = blockIdx.y;
+    const int chunk = blockIdx.x, kv = blockIdx.y, s0 = SLOTS * static_cast<int>(blockIdx.z);
     const int G = n_head / n_kv;
     const int nq = ntok * G;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int l16 = lane & 15, g4 = lane >> 4;
-    const int slot = l16 & 7;
+    const int slot = s0 + (l16 & 7);   // query slot t * G + gh of this lane's MFMA column / row
     const bool lo_row = l16 >= 8;
 
     // the query rows do not depend on the position: their loads go out together with pos[0]
@@ -147,7 +151,7 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
         for (int i = 0; i < 16; ++i) qraw[i] = ok ? q[8 * (i >> 1) + 2 * g4 + (i & 1)] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     const int p0 = pos[0];
-    const int p_last = p0 + ntok - 1;
+    const int p_last = p0 + (min(s0 + SLOTS, nq) - 1) / G;   // the last position this group's slots see
     const int wlen = STEP * nsub;
     const int cbase = chunk * WAVES * wlen;
     if (cbase > p_last || p0 < 0 || p_last >= max_ctx) return;   // uniform: no visible position (or a bad pos)
@@ -306,11 +310,11 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
     if (g4 == 0 && l16 < SLOTS) {
         wstat[wv][0][l16] = m_run;
         wstat[wv][1][l16] = l_run;
-    }
+    }   // indexed by the slot within the group
     __syncthreads();
     // thread: slot q = tid / 32, dims 8 (tid % 32) + [0, 8); waves combined in order 0..3
     const int q = threadIdx.x >> 5, d0 = 8 * (threadIdx.x & 31);
-    if (q < nq) {
+    if (s0 + q < nq) {
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) M = fmaxf(M, wstat[w][0][q]);
@@ -330,7 +334,7 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = __builtin_fmaf(wt[w], src[i], o[i]);
         }
-        float* rec = ws + ((static_cast<size_t>(chunk) * n_kv + kv) * SLOTS + q) * REC;
+        float* rec = ws + ((static_cast<size_t>(chunk) * n_kv + kv) * kMaxSlots + s0 + q) * REC;
         reinterpret_cast<float4*>(rec + 4 + d0)[0] = make_float4(o[0], o[1], o[2], o[3]);
         reinterpret_cast<float4*>(rec + 4 + d0)[1] = make_float4(o[4], o[5], o[6], o[7]);
         if ((threadIdx.x & 31) == 0) {
@@ -357,8 +361,8 @@ __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__
     const int kv = h / G, qv = t * G + (h - kv * G);
     const float g = gsrc[static_cast<size_t>(t) * gstride + h * 2 * HD + HD + d];   // in flight with pos
     const int nchunk = min((pos[0] + t) / chunk_len + 1, kMaxChunks);
-    const size_t cstride = static_cast<size_t>(n_kv) * SLOTS * REC;
-    const float* base = ws + (static_cast<size_t>(kv) * SLOTS + qv) * REC;
+    const size_t cstride = static_cast<size_t>(n_kv) * kMaxSlots * REC;
+    const float* base = ws + (static_cast<size_t>(kv) * kMaxSlots + qv) * REC;
     float mloc = -INFINITY;
     for (int c = d; c < nchunk; c += HD) mloc = fmaxf(mloc, base[c * cstride]);
     mloc = group_max<64>(mloc);
@@ -411,14 +415,14 @@ extern "C" size_t rmi_gqa_workspace_bytes(int max_ctx, int n_kv, int nsub) {
     if (max_ctx <= 0 || n_kv <= 0 || nsub <= 0) return 0;
     const int chunk_len = SUB * nsub;
     const size_t nchunks = static_cast<size_t>((max_ctx + chunk_len - 1) / chunk_len);
-    return nchunks * static_cast<size_t>(n_kv) * SLOTS * REC * sizeof(float);
+    return nchunks * static_cast<size_t>(n_kv) * kMaxSlots * REC * sizeof(float);
 }
 
 extern "C" int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* pos,
                                     const float* gate_src, int gate_stride, float* y, int y_stride, uint8_t* q8,
                                     int q8_stride, void* workspace, int n_head, int n_kv, int head_dim, int ntok,
                                     int max_ctx, int nsub, float scale, void* stream) {
-    if (head_dim != HD || n_head <= 0 || n_kv <= 0 || n_head % n_kv || ntok < 1 || ntok * (n_head / n_kv) > SLOTS ||
+    if (head_dim != HD || n_head <= 0 || n_kv <= 0 || n_head % n_kv || ntok < 1 || ntok * (n_head / n_kv) > kMaxSlots ||
         max_ctx <= 0 || max_ctx % SUB || nsub <= 0)
         return fail(RMI_ERR_SHAPE, "gqa_flash_decode: invalid arguments");
     if (!aligned16(q) || !aligned16(kcache) || !aligned16(vcache) || !aligned4(pos) || !aligned4(gate_src) ||
@@ -428,7 +432,8 @@ extern "C" int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, cons
     const int nchunks = (max_ctx + chunk_len - 1) / chunk_len;
     if (nchunks > kMaxChunks) return fail(RMI_ERR_SHAPE, "gqa_flash_decode: max_ctx / (64 * nsub) exceeds 2048 chunks");
     const auto s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(gqa_partial_kernel, dim3(nchunks, n_kv), dim3(256), 0, s, q, kcache, vcache, pos,
+    const int groups = (ntok * (n_head / n_kv) + SLOTS - 1) / SLOTS;
+    hipLaunchKernelGGL(gqa_partial_kernel, dim3(nchunks, n_kv, groups), dim3(256), 0, s, q, kcache, vcache, pos,
                        static_cast<float*>(workspace), n_head, n_kv, ntok, nsub, max_ctx, scale);
     hipLaunchKernelGGL(gqa_merge_kernel, dim3(ntok, n_head), dim3(HD), 0, s, static_cast<const float*>(workspace),
                        gate_src, gate_stride, pos, y, y_stride, q8, q8_stride, n_head, n_kv, chunk_len);

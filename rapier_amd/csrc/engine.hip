@@ -35,6 +35,7 @@ namespace {
 constexpr int kS = 128;          // GDN state size
 constexpr int kRingCap = 1 << 16;
 constexpr int kChunk = kMaxCols;  // ingest chunk: prompt tokens per weight pass
+constexpr int kAttnSlots = 64;    // query vectors per KV head one rmi_gqa_flash_decode launch takes
 
 #define RMI_TRY(expr)                         \
     do {                                      \
@@ -378,9 +379,10 @@ int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
     return gemv_res(e, L.down, e.q8f, x, part, nc);
 }
 
-// pos[0] is the position of column 0; with more than two columns pos is an array, pos[c] = pos[0] + c, and the
-// attention runs on pairs of columns (column 2 p's launch reads pos + 2 p).  Every KV row of the nc columns is stored
-// before any of them attends, and query c sees positions <= pos[0] + c only, as in the per-token path.
+// pos[0] is the position of column 0; with more columns than one attention launch takes (64 query vectors per KV
+// head: 16 tokens at 4 query heads per KV head) pos is an array, pos[c] = pos[0] + c, and the launch for columns
+// c0.. reads pos + c0.  Every KV row of the nc columns is stored before any of them attends, and query c sees
+// positions <= pos[0] + c only, as in the per-token path.
 int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc) {
     const auto& c = e.cfg;
     RMI_TRY(rmi_rms_quant_apply(x, L.attn_norm, part, e.q8a, c.n_embd, c.eps, nc, e.s));
@@ -388,11 +390,12 @@ int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int n
     RMI_TRY(rmi_attn_prep(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, e.qbuf, c.n_head, c.n_kv, c.head_dim,
                           c.n_rot, c.rope_theta, c.eps, nc, e.max_ctx, e.s));
     const size_t q8y_col = q81_bytes(e.attn_q);
-    for (int c0 = 0; c0 < nc; c0 += 2) {
+    const int per = std::max(1, kAttnSlots / (c.n_head / c.n_kv));   // tokens per attention launch
+    for (int c0 = 0; c0 < nc; c0 += per) {
         RMI_TRY(rmi_gqa_flash_decode(e.qbuf + static_cast<size_t>(c0) * e.attn_q, L.kc, L.vc, pos + c0,
                                      e.proj + static_cast<size_t>(c0) * e.q3_rows, e.q3_rows, nullptr, 0,
                                      e.q8y + c0 * q8y_col, static_cast<int>(q8y_col), e.attn_ws, c.n_head, c.n_kv,
-                                     c.head_dim, std::min(2, nc - c0), e.max_ctx, e.nsub,
+                                     c.head_dim, std::min(per, nc - c0), e.max_ctx, e.nsub,
                                      1.0f / sqrtf(static_cast<float>(c.head_dim)), e.s));
     }
     RMI_TRY(gemv_res(e, L.out_proj, e.q8y, x, part, nc));

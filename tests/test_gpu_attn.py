@@ -107,3 +107,23 @@ def test_attn_prep_matches_oracle(orc, rmi, ntok):
         assert np.array_equal(vh[(p0 + t) * NKV * HD:(p0 + t + 1) * NKV * HD], vref)
     assert not host(kc)[:p0 * NKV * HD].any(), "attn_prep wrote outside its positions"
     assert not host(kc)[(p0 + ntok) * NKV * HD:].any(), "attn_prep wrote outside its positions"
+
+
+@pytest.mark.parametrize("ctx,nsub,ntok", [(4096, 2, 16), (2048, 1, 13), (65536, 8, 16)])
+def test_flash_decode_chunk_bitwise_equals_single_queries(orc, rmi, ctx, nsub, ntok):
+    """an ingest chunk: ntok query tokens (ntok * 4 = up to 64 query vectors per KV head, 8 slot groups) in one launch;
+    each token's y and Q8_1 are bitwise the 1-token launch at its position; token 0 within 1e-3 of the oracle"""
+    kc, vc = kv_cache(orc, ctx, seed=ctx + ntok)
+    q = orc.normal(ntok * NH * HD, seed=ctx + 17)
+    g = orc.normal(ntok * Q3, seed=ctx + 18)
+    p0 = ctx - ntok - 3
+    dk, dv, dq, dg = dev(kc), dev(vc), dev(q), dev(g)
+    y, q8 = flash(rmi, dq, dk, dv, p0, dg, ntok, ctx, nsub)
+    blk = NH * HD // 32 * 36
+    for t in range(ntok):
+        y1, q81 = flash(rmi, dq[t * NH * HD:], dk, dv, p0 + t, dg[t * Q3:], 1, ctx, nsub)
+        assert np.array_equal(y1.view(np.uint32), y[t * NH * HD:(t + 1) * NH * HD].view(np.uint32)), f"token {t}"
+        assert np.array_equal(q81, q8[t * blk:(t + 1) * blk]), f"q8 token {t}"
+    o = orc.gqa_decode(q[:NH * HD], kc, vc, NH, NKV, HD, p0 + 1, SCALE)
+    gate = np.concatenate([g[h * 2 * HD + HD:h * 2 * HD + 2 * HD] for h in range(NH)])
+    assert_close_rel(y[:NH * HD], o / (1 + np.exp(-gate.astype(np.float64))), rtol=1e-3, atol_frac=1e-5, what="t0")
