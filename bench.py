@@ -313,12 +313,132 @@ def run_ingest(n_prompt=4096, batch=16, n_check=64):
                     f"{n_check} tokens; identical = first token and final hidden bit-equal after {n_check} tokens"}
 
 
+def qwen35_9b_tensors():
+    """(name, ggml type, dims) of a 9B-class qwen35 GGUF with the reference's tensor names (qw:2003-2127)"""
+    E, F, V, NL, HK, HV, NH, NKV, HD = 4096, 12288, 248320, 32, 16, 32, 16, 4, 256
+    ch = (2 * HK + HV) * 128
+    t = [("token_embd.weight", 14, (E, V)), ("output.weight", 14, (E, V)), ("output_norm.weight", 0, (E,))]
+
+    def attn(il):
+        p = f"blk.{il}."
+        return [(p + "attn_norm.weight", 0, (E,)), (p + "post_attention_norm.weight", 0, (E,)),
+                (p + "attn_q.weight", 14, (E, 2 * NH * HD)), (p + "attn_k.weight", 14, (E, NKV * HD)),
+                (p + "attn_v.weight", 14, (E, NKV * HD)), (p + "attn_output.weight", 14, (NH * HD, E)),
+                (p + "attn_q_norm.weight", 0, (HD,)), (p + "attn_k_norm.weight", 0, (HD,))]
+
+    def ffn(il):
+        p = f"blk.{il}."
+        return [(p + "ffn_up.weight", 14, (E, F)), (p + "ffn_gate.weight", 14, (E, F)), (p + "ffn_down.weight", 14, (F, E))]
+
+    for il in range(NL):
+        p = f"blk.{il}."
+        if (il + 1) % 4 == 0:
+            t += attn(il)
+        else:
+            t += [(p + "attn_norm.weight", 0, (E,)), (p + "post_attention_norm.weight", 0, (E,)),
+                  (p + "attn_qkv.weight", 14, (E, ch)), (p + "attn_gate.weight", 14, (E, HV * 128)),
+                  (p + "ssm_beta.weight", 14, (E, HV)), (p + "ssm_alpha.weight", 14, (E, HV)),
+                  (p + "ssm_out.weight", 14, (HV * 128, E)), (p + "ssm_conv1d.weight", 0, (4, ch)),
+                  (p + "ssm_dt.bias", 0, (HV,)), (p + "ssm_a", 0, (HV,)), (p + "ssm_norm.weight", 0, (128,))]
+        t += ffn(il)
+    t += attn(NL) + ffn(NL) + [(f"blk.{NL}.nextn.eh_proj.weight", 14, (2 * E, E))]
+    t += [(f"blk.{NL}.nextn.{w}.weight", 0, (E,)) for w in ("enorm", "hnorm", "shared_head_norm")]
+    meta = [("general.architecture", 8, "qwen35"), ("qwen35.block_count", 4, NL + 1),
+            ("qwen35.nextn_predict_layers", 4, 1), ("qwen35.attention.layer_norm_rms_epsilon", 6, 1e-6),
+            ("qwen35.rope.freq_base", 6, 1e7), ("qwen35.rope.dimension_count", 4, 64)]
+    return t, meta
+
+
+def write_synthetic_gguf(path, tensors, meta, seed=7):
+    """Stream a GGUF v3 file (the published layout: header, key/values, tensor infos, data aligned to 32): random
+    Q6_K blocks with a valid fp16 scale, unit norms, ssm_a = -1, small conv taps.  Returns the file size."""
+    import struct
+
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    s = lambda x: struct.pack("<Q", len(x.encode())) + x.encode()   # noqa: E731
+    fmt = {4: "<I", 6: "<f"}
+    kv = b"".join(s(k) + struct.pack("<I", t) + (s(v) if t == 8 else struct.pack(fmt[t], v)) for k, t, v in meta)
+    sizes = [(n, tp, d, (int(np.prod(d)) // 256 * 210) if tp == 14 else int(np.prod(d)) * 4) for n, tp, d in tensors]
+    infos, off, offs = b"", 0, []
+    for n, tp, d, nb in sizes:
+        infos += s(n) + struct.pack("<I", len(d)) + b"".join(struct.pack("<Q", x) for x in d) + struct.pack("<IQ", tp, off)
+        offs.append(off)
+        off = (off + nb + 31) // 32 * 32
+    head = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(meta)) + kv + infos
+    with open(path, "wb") as f:
+        f.write(head + b"\0" * ((-len(head)) % 32))
+        pos = 0
+        for (n, tp, d, nb), o in zip(sizes, offs):
+            f.write(b"\0" * (o - pos))
+            if tp == 14:
+                for r0 in range(0, nb, 210 << 16):          # 65536 blocks at a time
+                    blk = rng.integers(0, 256, min(210 << 16, nb - r0), dtype=np.uint8).reshape(-1, 210)
+                    blk[:, 208:210] = np.frombuffer(np.float16(1e-3).tobytes(), np.uint8)
+                    f.write(blk.tobytes())
+            else:
+                v = np.ones(nb // 4, np.float32)
+                if n.endswith("ssm_a"):
+                    v[:] = -1.0
+                elif n.endswith("conv1d.weight") or n.endswith("dt.bias"):
+                    v = (0.1 * rng.standard_normal(nb // 4)).astype(np.float32)
+                f.write(v.tobytes())
+            pos = o + nb
+    return os.path.getsize(path)
+
+
+def run_gguf_load(args):
+    """Load a 9B-class qwen35 GGUF (written to local disk first, so the load reads the page cache) through
+    rmi_engine_create_gguf and decode from it."""
+    import tempfile
+
+    import torch
+
+    import rapier_amd.engine as E
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream(device=0)
+    torch.cuda.set_stream(stream)
+    import shutil
+    tensors, meta = qwen35_9b_tensors()
+    tmp = os.environ.get("TMPDIR", "/tmp")
+    if shutil.disk_usage(tmp).free < 16e9:
+        print(json.dumps({"workload": "gguf_load", "skipped": f"less than 16 GB free under {tmp}"}), flush=True)
+        return
+    with tempfile.TemporaryDirectory(dir=tmp) as d:
+        path = os.path.join(d, "qwen35-9b-synthetic.gguf")
+        t0 = time.perf_counter()
+        size = write_synthetic_gguf(path, tensors, meta)
+        t_write = time.perf_counter() - t0
+        print(f"gguf written: {size / 1e9:.2f} GB in {t_write:.1f} s", file=sys.stderr, flush=True)
+        t0 = time.perf_counter()
+        eng = E.Engine.from_gguf(path, max_ctx=4096 + 512, stream=stream)
+        t_load = time.perf_counter() - t0
+    info = eng.info()
+    first = eng.prefill(list(range(1000, 1064)), batch=16)
+    pos0, cur0 = eng.state()
+    eng.save_state()
+    n = args.steps
+    ref, st_g = eng.generate(n, mode=E.GREEDY)
+    eng.restore_state(pos0, cur0)
+    toks, st_m = eng.generate(n, mode=E.MTP)
+    eng.close()
+    print(json.dumps({"workload": "gguf_load", "file_bytes": size, "load_s": round(t_load, 3),
+                      "load_GB_s": round(size / t_load / 1e9, 2), "write_s": round(t_write, 2),
+                      "round_weight_bytes": info["round_weight_bytes"], "first_token": first,
+                      "greedy_tok_s": round(n / (st_g["gpu_ms"] / 1e3), 1),
+                      "mtp_tok_s_natural": round(n / (st_m["gpu_ms"] / 1e3), 1), "mtp_identical": toks == ref,
+                      "note": "random Q6_K blocks (fp16 scale 1e-3), unit norms: a load and shape check, not a "
+                              "trained model; the file is read from the page cache right after it was written"}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200, help="timed verify rounds per run (mtp_round) or GEMV pairs")
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="mtp_round", choices=["mtp_round", "verify_gemv", "traffic_probe"])
+    ap.add_argument("--workload", default="mtp_round",
+                    choices=["mtp_round", "verify_gemv", "traffic_probe", "gguf_load"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--ctx", default="4096,65536",
                     help="comma-separated context lengths for mtp_round; value is quoted at the first")
@@ -329,6 +449,9 @@ def main():
         sys.exit(2)
     if args.workload == "traffic_probe":
         run_traffic_probe()
+        return
+    if args.workload == "gguf_load":
+        run_gguf_load(args)
         return
     gemv_args =argparse.Namespace(steps=50 if args.workload == "mtp_round" else args.steps,
                                    warmup=10 if args.workload == "mtp_round" else args.warmup)

@@ -132,8 +132,12 @@ int rmi_beta_gate(float* beta_alpha, const float* dt, const float* ssm_a, float*
  * Replaces argmax_kernel / serve_argmax_dev (qw:70-94) and the host scan (qw:3199-3205), without the memset. */
 size_t rmi_argmax_workspace_bytes(int ncols);
 int rmi_argmax(const float* logits, int n, int ncols, int col_stride, int* out_idx, void* workspace, void* stream);
-/* Device-resident token embedding: x[c] = dequant(Q6_K row tokens[c]), partials of each row.  Replaces the host
- * dequant + H2D copy of emb_dequant_block (qw:109-115, 1418-1430). */
+/* Device-resident token embedding: x[c] = dequant(row tokens[c]) of a GGUF type 14 (Q6_K), 13 (Q5_K) or 12 (Q4_K)
+ * table, partials of each row (4 elements per slot).  Replaces the host dequant + H2D copy of emb_dequant_block
+ * (qw:109-115, 1418-1430); Q3_K and IQ4_XS tables are RMI_ERR_UNSUPPORTED. */
+int rmi_embed(int type, const void* emb, const int* tokens, float* x, float* partials, int n_embd, int n_vocab,
+              int ncols, void* stream);
+/* rmi_embed with type 14 */
 int rmi_embed_q6_k(const void* emb, const int* tokens, float* x, float* partials, int n_embd, int n_vocab, int ncols,
                    void* stream);
 
@@ -174,6 +178,16 @@ int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_a, float* h
 int rmi_attn_prep(const float* q3, int q3_stride, const float* qn, const float* kn, uint16_t* kcache, uint16_t* vcache,
                   const int* pos, float* qout, int n_head, int n_kv, int head_dim, int n_rot, float theta, float eps,
                   int ntok, int max_ctx, void* stream);
+/* RoPE parameters as the reference sets them for qwen35 (qw:1991-1999): YaRN with freq_base, factor (the GGUF's
+ * rope.scaling.factor; <= 1 is plain NEOX RoPE) and orig_ctx (rope.scaling.original_context_length), ext_factor 1,
+ * attn_factor 1, beta_fast 32, beta_slow 1. */
+typedef struct rmi_rope_params {
+    float freq_base, factor, orig_ctx, ext_factor, attn_factor, beta_fast, beta_slow;
+} rmi_rope_params;
+/* rmi_attn_prep with YaRN scaling (native_rope_apply with RopeScalingType::YaRN, qw:1991-1999, 1540-1546) */
+int rmi_attn_prep_rope(const float* q3, int q3_stride, const float* qn, const float* kn, uint16_t* kcache,
+                       uint16_t* vcache, const int* pos, float* qout, int n_head, int n_kv, int head_dim, int n_rot,
+                       const rmi_rope_params* rope, float eps, int ntok, int max_ctx, void* stream);
 /* split-K flash decode for ntok query tokens at positions pos[0] + t, sigmoid gate from gate_src (the wq output,
  * gate of head h at + h * 2 * head_dim + head_dim), fp32 y (nullable) and Q8_1 (nullable).  workspace holds
  * rmi_gqa_workspace_bytes(max_ctx, n_kv, nsub) bytes; chunks are 64 * nsub positions.  ntok * (n_head / n_kv)

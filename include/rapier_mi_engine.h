@@ -36,6 +36,8 @@ typedef struct rmi_model_config {
     int n_rot;         /* 64 rotary dims (kRot) */
     float rope_theta;  /* 1e7 */
     float eps;         /* 1e-6 */
+    float rope_factor; /* qwen35.rope.scaling.factor: YaRN when > 1, plain RoPE otherwise (qw:1991-1999) */
+    float rope_orig_ctx; /* qwen35.rope.scaling.original_context_length (262144) */
 } rmi_model_config;
 
 typedef struct rmi_engine rmi_engine;
@@ -86,13 +88,40 @@ int rmi_engine_restore_state(rmi_engine* e, int pos, int cur_token);
 int rmi_engine_state(rmi_engine* e, int* pos, int* cur_token);
 int rmi_engine_generate(rmi_engine* e, const rmi_gen_request* req, int* out_tokens, rmi_gen_stats* stats);
 
+/* ---- GGUF (v2 / v3) files: the reader the engine loads through (the role of strata::GgufFile, qw:945-957,
+ * 1978-2134).  Tensors are memory-mapped; dims[0] is the innermost dimension (n_in of a matrix). ---- */
+typedef struct rmi_gguf rmi_gguf;
+int rmi_gguf_open(const char* path, rmi_gguf** out);
+void rmi_gguf_close(rmi_gguf* g);
+int64_t rmi_gguf_tensor_count(const rmi_gguf* g);
+int64_t rmi_gguf_find(const rmi_gguf* g, const char* name);      /* tensor index or -1 */
+/* GGML type, rank, dims[4] (unused dims 1), data bytes (0 for a type the reader does not size) and data pointer */
+int rmi_gguf_tensor_info(const rmi_gguf* g, int64_t i, const char** name, int* type, int* n_dims, int64_t* dims,
+                         size_t* bytes, const void** data);
+int rmi_gguf_get_num(const rmi_gguf* g, const char* key, double* out);       /* any numeric scalar */
+int rmi_gguf_get_str(const rmi_gguf* g, const char* key, const char** out);
+int64_t rmi_gguf_array_len(const rmi_gguf* g, const char* key);             /* -1 if not an array */
+int rmi_gguf_array_str(const rmi_gguf* g, const char* key, int64_t i, const char** out);
+int rmi_gguf_array_num(const rmi_gguf* g, const char* key, int64_t i, double* out);
+
+/* Create the engine from a qwen35 GGUF (load_model, qw:1978-2134): general.architecture "qwen35", trunk layers =
+ * block_count - nextn_predict_layers, layer il attention when blk.il.attn_q.weight exists, the draft block at
+ * blk.<n_layer> with its nextn tensors; shapes from the tensors, eps / RoPE / YaRN from the metadata.  Matrices are
+ * Q6_K (concatenated as the reference's try_cat groups: attn_qkv | attn_gate | ssm_beta | ssm_alpha, attn_q | attn_k |
+ * attn_v, ffn_up | ffn_gate), token_embd Q6_K / Q5_K / Q4_K, norms and GDN vectors F32.  Other matrix types are
+ * RMI_ERR_UNSUPPORTED. */
+int rmi_engine_create_gguf(const char* path, int max_ctx, void* stream, rmi_engine** out);
+/* the model configuration the engine runs (from the file for a GGUF engine) */
+int rmi_engine_config(const rmi_engine* e, rmi_model_config* out);
+
 /* engine buffers readable with rmi_engine_read (the reference's QWYTHOS_IDUMP probes read the same state) */
 enum {
     RMI_BUF_GDN_STATE = 0,   /* live GDN state of a GDN layer, fp32 [128][h_v][128] */
     RMI_BUF_GDN_HIST = 1,    /* live conv history of a GDN layer, fp32 [h_v][3 * 128][3] */
     RMI_BUF_K_CACHE = 2,     /* K cache of an attention layer (layer n_layer: the draft block), fp16 [pos][n_kv][256] */
     RMI_BUF_V_CACHE = 3,
-    RMI_BUF_HIDDEN = 4       /* final-normed hidden of the last forward, fp32 [n_embd] (the first draft's input) */
+    RMI_BUF_HIDDEN = 4,      /* final-normed hidden of the last forward, fp32 [n_embd] (the first draft's input) */
+    RMI_BUF_LOGITS = 5       /* logits of the last head pass, fp32 [2][n_vocab] (column 0: the last forward) */
 };
 /* copy bytes [offset, offset + bytes) of an engine buffer to host memory; synchronizes the engine stream */
 int rmi_engine_read(rmi_engine* e, int which, int layer, size_t offset, void* dst, size_t bytes);

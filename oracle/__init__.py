@@ -17,6 +17,8 @@ _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 Q6K_BYTES = 210
+Q4K_BYTES = 144
+Q5K_BYTES = 176
 Q8_0_BYTES = 34
 Q8_1_BYTES = 36
 
@@ -39,6 +41,8 @@ _SIGS = {
     "orc_dequantize_q8_1": (None, [_u8p, _f32p, _c.c_int]),
     "orc_q6k_code": (_c.c_int, [_u8p, _c.c_int]),
     "orc_q6k_dequant_row": (None, [_u8p, _f32p, _c.c_int]),
+    "orc_q4k_dequant_row": (None, [_u8p, _f32p, _c.c_int]),
+    "orc_q5k_dequant_row": (None, [_u8p, _f32p, _c.c_int]),
     "orc_q6k_block_dots": (None, [_u8p, _u8p, _i32p, _c.c_int, _c.c_int]),
     "orc_q6k_block_dots_lanes": (None, [_u8p, _u8p, _i32p, _c.c_int, _c.c_int]),
     "orc_q8_0_block_dots": (None, [_u8p, _u8p, _i32p, _c.c_int, _c.c_int]),
@@ -58,6 +62,7 @@ _SIGS = {
     "orc_gqa_decode": (None, [_f32p, _u16p, _u16p, _f64p, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_double]),
     "orc_rms_norm_heads": (None, [_f32p, _f32p, _f64p, _c.c_int, _c.c_int, _c.c_double]),
     "orc_rope_neox": (None, [_f64p, _f64p, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_double]),
+    "orc_rope_yarn": (None, [_f64p, _f64p, _c.c_int, _c.c_int, _c.c_int, _c.c_int] + [_c.c_double] * 7),
     "orc_argmax": (_c.c_int, [_f32p, _c.c_int]),
 }
 
@@ -144,6 +149,20 @@ def q6k_dequant(w: np.ndarray, n_out: int, n_in: int) -> np.ndarray:
     for r in range(n_out):
         lib().orc_q6k_dequant_row(np.ascontiguousarray(w[r * row:(r + 1) * row]), out[r], n_in)
     return out
+
+
+def q4k_dequant(w: np.ndarray, n_out: int, n_in: int) -> np.ndarray:
+    """ggml dequantize_row_q4_K (token_embd of Q5_K_M files, qw:109-115) -> float32 [n_out * n_in]"""
+    y = np.empty(n_out * n_in, np.float32)
+    lib().orc_q4k_dequant_row(np.ascontiguousarray(w, np.uint8), y, n_out * n_in)
+    return y
+
+
+def q5k_dequant(w: np.ndarray, n_out: int, n_in: int) -> np.ndarray:
+    """ggml dequantize_row_q5_K -> float32 [n_out * n_in]"""
+    y = np.empty(n_out * n_in, np.float32)
+    lib().orc_q5k_dequant_row(np.ascontiguousarray(w, np.uint8), y, n_out * n_in)
+    return y
 
 
 def q6k_block_dots(w, xq, n_in, n_out, lanes=False):
@@ -267,6 +286,15 @@ def rope_neox(x, heads, hd, n_rot, pos, theta):
     x = np.ascontiguousarray(x, dtype=np.float64).reshape(-1)
     out = np.empty_like(x)
     lib().orc_rope_neox(x, out, heads, hd, n_rot, pos, theta)
+    return out
+
+
+def rope_yarn(x, heads, hd, n_rot, pos, base, factor, orig_ctx, ext_factor=1.0, attn_factor=1.0, beta_fast=32.0,
+              beta_slow=1.0):
+    """YaRN NEOX RoPE with the reference's parameters (qw:1991-1999) -> float64"""
+    out = np.empty(heads * hd, np.float64)
+    lib().orc_rope_yarn(np.ascontiguousarray(x, np.float64), out, heads, hd, n_rot, pos, base, factor, orig_ctx,
+                        ext_factor, attn_factor, beta_fast, beta_slow)
     return out
 
 

@@ -234,6 +234,71 @@ void orc_q6k_dequant_row(const uint8_t* w, float* y, int n) {
     }
 }
 
+/* ------------------------------------------------------------------------------------------------------------ */
+/* Q4_K / Q5_K (token_embd of Q5_K_M files; dequantized by strata::dequantize_q4_K / q5_K at qw:109-115, a      */
+/* dependency absent from the reference tree: restated from ggml's published dequantize_row_q4_K / q5_K).       */
+/* A 256-block is 8 sub-blocks of 32 with a 6-bit scale and a 6-bit min each, packed in 12 bytes: for j < 4     */
+/* scale = s[j] & 63, min = s[j+4] & 63; for j >= 4 scale = (s[j+4] & 15) | (s[j-4] >> 6) << 4,                  */
+/* min = (s[j+4] >> 4) | (s[j] >> 6) << 4.  weight = d * scale * q - dmin * min.                                */
+/* Q4_K (144 B): d, dmin (fp16), scales[12], qs[128]; sub-block 2c takes the low nibbles of qs[32c .. 32c+31],   */
+/* sub-block 2c+1 their high nibbles.  Q5_K (176 B): d, dmin, scales[12], qh[32], qs[128]; element l of          */
+/* sub-block j gains bit j of qh[l] as its fifth bit (16).                                                      */
+
+static void k4_scale_min(const uint8_t* s, int j, int* sc, int* m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+        *m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+static float f16_at(const uint8_t* p) {
+    uint16_t h;
+    memcpy(&h, p, 2);
+    return orc_f16_to_f32(h);
+}
+
+void orc_q4k_dequant_row(const uint8_t* w, float* y, int n) {
+    for (int bi = 0; bi < n / 256; ++bi) {
+        const uint8_t* b = w + (size_t) bi * ORC_Q4K_BYTES;
+        const float d = f16_at(b), dmin = f16_at(b + 2);
+        const uint8_t* qs = b + 16;
+        for (int c = 0; c < 4; ++c) {
+            int s0, m0, s1, m1;
+            k4_scale_min(b + 4, 2 * c, &s0, &m0);
+            k4_scale_min(b + 4, 2 * c + 1, &s1, &m1);
+            const float d0 = d * (float) s0, mm0 = dmin * (float) m0, d1 = d * (float) s1, mm1 = dmin * (float) m1;
+            for (int l = 0; l < 32; ++l) {
+                y[256 * bi + 64 * c + l] = d0 * (float) (qs[32 * c + l] & 15) - mm0;
+                y[256 * bi + 64 * c + 32 + l] = d1 * (float) (qs[32 * c + l] >> 4) - mm1;
+            }
+        }
+    }
+}
+
+void orc_q5k_dequant_row(const uint8_t* w, float* y, int n) {
+    for (int bi = 0; bi < n / 256; ++bi) {
+        const uint8_t* b = w + (size_t) bi * ORC_Q5K_BYTES;
+        const float d = f16_at(b), dmin = f16_at(b + 2);
+        const uint8_t* qh = b + 16;
+        const uint8_t* qs = b + 48;
+        for (int c = 0; c < 4; ++c) {
+            int s0, m0, s1, m1;
+            k4_scale_min(b + 4, 2 * c, &s0, &m0);
+            k4_scale_min(b + 4, 2 * c + 1, &s1, &m1);
+            const float d0 = d * (float) s0, mm0 = dmin * (float) m0, d1 = d * (float) s1, mm1 = dmin * (float) m1;
+            for (int l = 0; l < 32; ++l) {
+                const int q0 = (qs[32 * c + l] & 15) | (((qh[l] >> (2 * c)) & 1) << 4);
+                const int q1 = (qs[32 * c + l] >> 4) | (((qh[l] >> (2 * c + 1)) & 1) << 4);
+                y[256 * bi + 64 * c + l] = d0 * (float) q0 - mm0;
+                y[256 * bi + 64 * c + 32 + l] = d1 * (float) q1 - mm1;
+            }
+        }
+    }
+}
+
 static const int8_t* q81_qs(const uint8_t* xq, int j) { return (const int8_t*) (xq + (size_t) ORC_Q8_1_BYTES * j + 4); }
 static float q81_d(const uint8_t* xq, int j) {
     uint16_t h;
@@ -570,6 +635,39 @@ void orc_rope_neox(const double* x, double* out, int heads, int hd, int n_rot, i
         for (int i = 0; i < half; ++i) {
             const double ang = (double) pos * pow(theta, -2.0 * i / (double) n_rot);
             const double c = cos(ang), s = sin(ang);
+            yo[i] = xi[i] * c - xi[i + half] * s;
+            yo[i + half] = xi[i] * s + xi[i + half] * c;
+        }
+    }
+}
+
+/* YaRN RoPE as the reference configures it (qw:1991-1999: freq_base, factor, original context, ext_factor 1,
+ * attn_factor 1, beta_fast 32, beta_slow 1), applied by strata's native_rope_apply (absent from the reference tree):
+ * restated from the published YaRN algorithm as ggml implements it (rope_yarn, ggml_rope_yarn_corr_dims).  For pair i
+ * (rotary dims i and i + n_rot/2): theta_extrap = pos * base^(-2i/n_rot), theta_interp = theta_extrap / factor,
+ * ramp = 1 - clamp((i - low) / max(0.001, high - low), 0, 1) with low = max(0, floor(corr(beta_fast))),
+ * high = min(n_rot - 1, ceil(corr(beta_slow))), corr(b) = n_rot ln(orig_ctx / (2 pi b)) / (2 ln base);
+ * theta = theta_interp (1 - ramp ext) + theta_extrap ramp ext; cos, sin scaled by
+ * attn_factor (1 + 0.1 ln factor) when ext != 0.  factor 1 is plain NEOX RoPE. */
+void orc_rope_yarn(const double* x, double* out, int heads, int hd, int n_rot, int pos, double base, double factor,
+                   double orig_ctx, double ext_factor, double attn_factor, double beta_fast, double beta_slow) {
+    const int half = n_rot / 2;
+    const double pi = 3.14159265358979323846;
+    const double cf = n_rot * log(orig_ctx / (beta_fast * 2.0 * pi)) / (2.0 * log(base));
+    const double cs = n_rot * log(orig_ctx / (beta_slow * 2.0 * pi)) / (2.0 * log(base));
+    const double low = fmax(0.0, floor(cf)), high = fmin((double) (n_rot - 1), ceil(cs));
+    const double mscale = ext_factor != 0.0 ? attn_factor * (1.0 + 0.1 * log(factor)) : attn_factor;
+    for (int h = 0; h < heads; ++h) {
+        const double* xi = x + (size_t) h * hd;
+        double* yo = out + (size_t) h * hd;
+        for (int d = 0; d < hd; ++d) yo[d] = xi[d];
+        for (int i = 0; i < half; ++i) {
+            const double te = (double) pos * pow(base, -2.0 * i / (double) n_rot);
+            const double ti = te / factor;
+            const double y = ((double) i - low) / fmax(0.001, high - low);
+            const double ramp = (1.0 - fmin(1.0, fmax(0.0, y))) * ext_factor;
+            const double th = ti * (1.0 - ramp) + te * ramp;
+            const double c = cos(th) * mscale, s = sin(th) * mscale;
             yo[i] = xi[i] * c - xi[i + half] * s;
             yo[i + half] = xi[i] * s + xi[i + half] * c;
         }

@@ -22,6 +22,7 @@ extern "C" {
 
 /* ---- block formats (mmvq:98-103 Q8_1, 113-116 Q8_0, 121-140 Q6_K) ---- */
 enum { ORC_Q6K_BYTES = 210, ORC_Q6K_ELEMS = 256, ORC_Q8_0_BYTES = 34, ORC_Q8_1_BYTES = 36, ORC_QK8 = 32 };
+enum { ORC_Q4K_BYTES = 144, ORC_Q5K_BYTES = 176 };   /* token_embd of Q5_K_M files (qw:109-115) */
 
 /* ---- seeded counter-based generators (same stream on every platform: splitmix64 + Box-Muller in fp64) ---- */
 uint64_t orc_rand_u64(uint64_t seed, uint64_t index);
@@ -43,6 +44,8 @@ void orc_dequantize_q8_1(const uint8_t* y, float* x, int n);
 /* ---- Q6_K helpers ---- */
 int orc_q6k_code(const uint8_t* block, int e);                       /* 6-bit code of element e, 0..63 */
 void orc_q6k_dequant_row(const uint8_t* w, float* y, int n);          /* ggml dequantize_row_q6_K order */
+void orc_q4k_dequant_row(const uint8_t* w, float* y, int n);          /* ggml dequantize_row_q4_K */
+void orc_q5k_dequant_row(const uint8_t* w, float* y, int n);          /* ggml dequantize_row_q5_K */
 
 /* ---- integer block dots (mmvq:642-655, 733-748 restated in closed form) ---- */
 /* out[r * (n_in/32) + j] = sum over the 32 elements of Q8_1 block j of sc(e) * (q6(e) - 32) * q8(e), exact int32 */
@@ -81,6 +84,9 @@ void orc_gqa_decode(const float* q, const uint16_t* kc, const uint16_t* vc, doub
                     int n_tok, double scale);
 void orc_rms_norm_heads(const float* x, const float* w, double* out, int rows, int cols, double eps);
 void orc_rope_neox(const double* x, double* out, int heads, int hd, int n_rot, int pos, double theta);
+/* YaRN (qw:1991-1999 parameters; ggml's rope_yarn restated) */
+void orc_rope_yarn(const double* x, double* out, int heads, int hd, int n_rot, int pos, double base, double factor,
+                   double orig_ctx, double ext_factor, double attn_factor, double beta_fast, double beta_slow);
 
 /* ---- argmax, lowest index wins ties (qw:70-94) ---- */
 int orc_argmax(const float* l, int n);

@@ -51,11 +51,13 @@ SIGNATURES = {
     "rmi_argmax_workspace_bytes": (_sz, [_i]),
     "rmi_argmax": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "rmi_embed_q6_k": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_embed": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_fused_gdn_conv_l2": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
     "rmi_fused_gdn_step_norm_silu_q8": (_i, [_vp] * 8 + [_f, _vp, _vp, _i, _i, _vp]),
     "rmi_gdn_layer_tokens": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _i, _vp,
                                   _i, _i, _i, _i, _vp]),
     "rmi_attn_prep": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _f, _i, _i, _vp]),
+    "rmi_attn_prep_rope": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _f, _i, _i, _vp]),
     "rmi_gqa_workspace_bytes": (_sz, [_i, _i, _i]),
     "rmi_gqa_flash_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _f,
                                   _vp]),
@@ -239,6 +241,11 @@ def embed_q6_k(emb, tokens, x, partials, n_embd, n_vocab, ncols=1, stream=None):
     _call("rmi_embed_q6_k", _p(emb), _p(tokens), _p(x), _p(partials), n_embd, n_vocab, ncols, _stream(stream))
 
 
+def embed(ggml_type, emb, tokens, x, partials, n_embd, n_vocab, ncols=1, stream=None):
+    """token rows of a GGUF type 14 (Q6_K) / 13 (Q5_K) / 12 (Q4_K) table, dequantized on the device"""
+    _call("rmi_embed", ggml_type, _p(emb), _p(tokens), _p(x), _p(partials), n_embd, n_vocab, ncols, _stream(stream))
+
+
 # ---- Gated DeltaNet (fgdn:40-133) ----------------------------------------------------------------------------------
 
 def fused_gdn_conv_l2(history, qkv, conv_w, h, channels, qk_heads, eps, stream=None):
@@ -263,6 +270,20 @@ def attn_prep(q3, q3_stride, qn, kn, kcache, vcache, pos, qout, n_head, n_kv, he
               max_ctx, stream=None):
     _call("rmi_attn_prep", _p(q3), q3_stride, _p(qn), _p(kn), _p(kcache), _p(vcache), _p(pos), _p(qout), n_head,
           n_kv, head_dim, n_rot, theta, eps, ntok, max_ctx, _stream(stream))
+
+
+class RopeParams(ctypes.Structure):
+    """rmi_rope_params: YaRN as the reference configures it (qw:1991-1999)"""
+    _fields_ = [(n, ctypes.c_float) for n in ("freq_base", "factor", "orig_ctx", "ext_factor", "attn_factor",
+                                              "beta_fast", "beta_slow")]
+
+
+def attn_prep_rope(q3, q3_stride, qn, kn, kcache, vcache, pos, qout, n_head, n_kv, head_dim, n_rot, freq_base, factor,
+                   orig_ctx, eps, ntok, max_ctx, ext_factor=1.0, attn_factor=1.0, beta_fast=32.0, beta_slow=1.0,
+                   stream=None):
+    rope = RopeParams(freq_base, factor, orig_ctx, ext_factor, attn_factor, beta_fast, beta_slow)
+    _call("rmi_attn_prep_rope", _p(q3), q3_stride, _p(qn), _p(kn), _p(kcache), _p(vcache), _p(pos), _p(qout), n_head,
+          n_kv, head_dim, n_rot, ctypes.byref(rope), eps, ntok, max_ctx, _stream(stream))
 
 
 def gqa_workspace_bytes(max_ctx, n_kv, nsub):

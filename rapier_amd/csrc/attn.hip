@@ -17,6 +17,8 @@
 // result is bitwise the single-token result at the same position.
 #include "rmi_common.h"
 
+#include <cmath>
+
 namespace rmi {
 namespace {
 
@@ -41,13 +43,21 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 }
 
 // ---- attn_prep -------------------------------------------------------------------------------------------------------
+// YaRN (the reference's rope configuration, qw:1991-1999): per rotary pair i, theta = theta_extrap (pos base^(-2i/n_rot))
+// mixed with theta_extrap / factor by ramp(i) ext_factor, ramp = 1 - clamp((i - low) / max(0.001, high - low), 0, 1);
+// cos and sin scaled by mscale.  low, high and mscale come from the host in fp64.  yarn = 0: plain NEOX RoPE.
+struct Yarn {
+    int on;
+    double factor, low, high, ext, mscale;
+};
+
 // q3 per token: [n_head x (q HD | gate HD) | k n_kv*HD | v n_kv*HD] at q3 + t * q3_stride.
 __global__ __launch_bounds__(HD) void attn_prep_kernel(const float* __restrict__ q3, int q3_stride,
                                                        const float* __restrict__ qn, const float* __restrict__ kn,
                                                        uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
                                                        const int* __restrict__ pos, float* __restrict__ qout,
                                                        int n_head, int n_kv, int n_rot, int max_ctx, float theta,
-                                                       float eps) {
+                                                       float eps, Yarn yarn) {
     __shared__ float red[4];
     __shared__ float xs[HD];
     const int t = blockIdx.x;
@@ -73,9 +83,18 @@ __global__ __launch_bounds__(HD) void attn_prep_kernel(const float* __restrict__
     const int half = n_rot / 2;
     if (d < n_rot) {
         const int i = d < half ? d : d - half;
-        const double ang = static_cast<double>(p) * pow(static_cast<double>(theta), -2.0 * i / static_cast<double>(n_rot));
+        double ang = static_cast<double>(p) * pow(static_cast<double>(theta), -2.0 * i / static_cast<double>(n_rot));
         double sn, cs;
-        sincos(ang, &sn, &cs);
+        if (yarn.on) {
+            const double y = (static_cast<double>(i) - yarn.low) / fmax(0.001, yarn.high - yarn.low);
+            const double ramp = (1.0 - fmin(1.0, fmax(0.0, y))) * yarn.ext;
+            ang = (ang / yarn.factor) * (1.0 - ramp) + ang * ramp;
+            sincos(ang, &sn, &cs);
+            sn *= yarn.mscale;
+            cs *= yarn.mscale;
+        } else {
+            sincos(ang, &sn, &cs);
+        }
         const float c = static_cast<float>(cs), s = static_cast<float>(sn);
         v = d < half ? xs[d] * c - xs[d + half] * s : xs[d - half] * s + xs[d] * c;
     }
@@ -398,17 +417,42 @@ __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__
 
 using namespace rmi;
 
-extern "C" int rmi_attn_prep(const float* q3, int q3_stride, const float* qn, const float* kn, uint16_t* kcache,
-                             uint16_t* vcache, const int* pos, float* qout, int n_head, int n_kv, int head_dim,
-                             int n_rot, float theta, float eps, int ntok, int max_ctx, void* stream) {
+extern "C" int rmi_attn_prep_rope(const float* q3, int q3_stride, const float* qn, const float* kn,
+                                  uint16_t* kcache, uint16_t* vcache, const int* pos, float* qout, int n_head,
+                                  int n_kv, int head_dim, int n_rot, const rmi_rope_params* rope, float eps, int ntok,
+                                  int max_ctx, void* stream) {
     if (head_dim != HD || n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_rot < 0 || n_rot > HD || n_rot % 2 ||
-        ntok < 1 || ntok > kMaxCols)
+        ntok < 1 || ntok > kMaxCols || !rope || !(rope->freq_base > 1.0f))
         return fail(RMI_ERR_SHAPE, "attn_prep: invalid arguments");
     if (!aligned4(q3) || !aligned4(qn) || !aligned4(kn) || !kcache || !vcache || !aligned4(pos) || !aligned4(qout))
         return fail(RMI_ERR_POINTER, "attn_prep: invalid arguments");
+    Yarn y{};
+    if (rope->factor > 1.0f) {   // scaling on: the corr dims and magnitude scale of the YaRN ramp (fp64, once per call)
+        if (!(rope->orig_ctx > 0.0f) || !(rope->beta_fast > 0.0f) || !(rope->beta_slow > 0.0f))
+            return fail(RMI_ERR_SHAPE, "attn_prep: invalid YaRN parameters");
+        const double pi = 3.14159265358979323846, base = rope->freq_base;
+        const double cf = n_rot * std::log(rope->orig_ctx / (rope->beta_fast * 2.0 * pi)) / (2.0 * std::log(base));
+        const double cs = n_rot * std::log(rope->orig_ctx / (rope->beta_slow * 2.0 * pi)) / (2.0 * std::log(base));
+        y.on = 1;
+        y.factor = rope->factor;
+        y.low = std::fmax(0.0, std::floor(cf));
+        y.high = std::fmin(static_cast<double>(n_rot - 1), std::ceil(cs));
+        y.ext = rope->ext_factor;
+        y.mscale = rope->ext_factor != 0.0f ? rope->attn_factor * (1.0 + 0.1 * std::log(static_cast<double>(rope->factor)))
+                                            : rope->attn_factor;
+    }
     hipLaunchKernelGGL(attn_prep_kernel, dim3(ntok, n_head + 2 * n_kv), dim3(HD), 0, static_cast<hipStream_t>(stream),
-                       q3, q3_stride, qn, kn, kcache, vcache, pos, qout, n_head, n_kv, n_rot, max_ctx, theta, eps);
+                       q3, q3_stride, qn, kn, kcache, vcache, pos, qout, n_head, n_kv, n_rot, max_ctx, rope->freq_base,
+                       eps, y);
     return launch_status("attn_prep");
+}
+
+extern "C" int rmi_attn_prep(const float* q3, int q3_stride, const float* qn, const float* kn, uint16_t* kcache,
+                             uint16_t* vcache, const int* pos, float* qout, int n_head, int n_kv, int head_dim,
+                             int n_rot, float theta, float eps, int ntok, int max_ctx, void* stream) {
+    const rmi_rope_params rope{theta, 1.0f, 0.0f, 1.0f, 1.0f, 32.0f, 1.0f};
+    return rmi_attn_prep_rope(q3, q3_stride, qn, kn, kcache, vcache, pos, qout, n_head, n_kv, head_dim, n_rot, &rope,
+                              eps, ntok, max_ctx, stream);
 }
 
 extern "C" size_t rmi_gqa_workspace_bytes(int max_ctx, int n_kv, int nsub) {

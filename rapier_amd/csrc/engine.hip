@@ -110,6 +110,8 @@ struct Engine {
 
     Mat lm_head;
     uint8_t* tok_embd = nullptr;
+    int emb_type = 14;              // GGML type of the token embedding table (Q6_K, Q5_K or Q4_K)
+    rmi_rope_params rope{};
     float* out_norm = nullptr;
     std::vector<Layer> layers;
     Layer draft;
@@ -312,6 +314,30 @@ int zero_f32(Engine& e, float* p, size_t n) {
     return launch_status("fill");
 }
 
+// fp16 K/V caches of an attention layer, zeroed
+int alloc_attn_state(Engine& e, Layer& L) {
+    const auto& c = e.cfg;
+    const size_t kv = static_cast<size_t>(e.max_ctx) * c.n_kv * c.head_dim;
+    RMI_TRY(e.alloc(&L.kc, kv));
+    RMI_TRY(e.alloc(&L.vc, kv));
+    HIP_TRY(hipMemsetAsync(L.kc, 0, kv * 2, e.s));
+    HIP_TRY(hipMemsetAsync(L.vc, 0, kv * 2, e.s));
+    return RMI_OK;
+}
+
+// the two GDN state and history buffers of a layer, zeroed
+int alloc_gdn_state(Engine& e, Layer& L) {
+    const auto& c = e.cfg;
+    const size_t st = static_cast<size_t>(kS) * c.ssm_h_v * kS;
+    for (int b = 0; b < 2; ++b) {
+        RMI_TRY(e.alloc(&L.state[b], st));
+        RMI_TRY(e.alloc(&L.hist[b], hist_floats(c)));
+        RMI_TRY(zero_f32(e, L.state[b], st));
+        RMI_TRY(zero_f32(e, L.hist[b], hist_floats(c)));
+    }
+    return RMI_OK;
+}
+
 int make_attn(Engine& e, Layer& L, int li, uint64_t seed) {
     const auto& c = e.cfg;
     L.gdn = false;
@@ -323,12 +349,7 @@ int make_attn(Engine& e, Layer& L, int li, uint64_t seed) {
     RMI_TRY(make_mat(e, L.down, c.n_embd, c.n_ff, mix_seed(seed, li, 6)));
     RMI_TRY(make_vec(e, &L.qn, c.head_dim, mix_seed(seed, li, 7), 1.0f, 0.1f));
     RMI_TRY(make_vec(e, &L.kn, c.head_dim, mix_seed(seed, li, 8), 1.0f, 0.1f));
-    const size_t kv = static_cast<size_t>(e.max_ctx) * c.n_kv * c.head_dim;
-    RMI_TRY(e.alloc(&L.kc, kv));
-    RMI_TRY(e.alloc(&L.vc, kv));
-    HIP_TRY(hipMemsetAsync(L.kc, 0, kv * 2, e.s));
-    HIP_TRY(hipMemsetAsync(L.vc, 0, kv * 2, e.s));
-    return RMI_OK;
+    return alloc_attn_state(e, L);
 }
 
 int make_gdn(Engine& e, Layer& L, int li, uint64_t seed) {
@@ -345,14 +366,7 @@ int make_gdn(Engine& e, Layer& L, int li, uint64_t seed) {
     RMI_TRY(make_vec(e, &L.dt, c.ssm_h_v, 0, 0.0f, 0.0f));
     RMI_TRY(make_vec(e, &L.ssm_a, c.ssm_h_v, mix_seed(seed, li, 8), 0.0f, 0.5f));
     RMI_TRY(make_vec(e, &L.ssm_norm, kS, mix_seed(seed, li, 9), 1.0f, 0.1f));
-    const size_t st = static_cast<size_t>(kS) * c.ssm_h_v * kS;
-    for (int b = 0; b < 2; ++b) {
-        RMI_TRY(e.alloc(&L.state[b], st));
-        RMI_TRY(e.alloc(&L.hist[b], hist_floats(c)));
-        RMI_TRY(zero_f32(e, L.state[b], st));
-        RMI_TRY(zero_f32(e, L.hist[b], hist_floats(c)));
-    }
-    return RMI_OK;
+    return alloc_gdn_state(e, L);
 }
 
 // per-value-head copy of a [channels][3] conv history: head h takes k-head h % h_k's q and k channels and its v
@@ -387,8 +401,8 @@ int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int n
     const auto& c = e.cfg;
     RMI_TRY(rmi_rms_quant_apply(x, L.attn_norm, part, e.q8a, c.n_embd, c.eps, nc, e.s));
     RMI_TRY(gemv(e, L.in_proj, e.q8a, e.proj, nc));
-    RMI_TRY(rmi_attn_prep(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, e.qbuf, c.n_head, c.n_kv, c.head_dim,
-                          c.n_rot, c.rope_theta, c.eps, nc, e.max_ctx, e.s));
+    RMI_TRY(rmi_attn_prep_rope(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, e.qbuf, c.n_head, c.n_kv, c.head_dim,
+                               c.n_rot, &e.rope, c.eps, nc, e.max_ctx, e.s));
     const size_t q8y_col = q81_bytes(e.attn_q);
     const int per = std::max(1, kAttnSlots / (c.n_head / c.n_kv));   // tokens per attention launch
     for (int c0 = 0; c0 < nc; c0 += per) {
@@ -422,7 +436,7 @@ enum Head { kHeadAll, kHeadLast, kHeadNone };
 int trunk_cols(Engine& e, int nc, const int* tok, const int* pos, float* h, float* hp, Head head) {
     const auto& c = e.cfg;
     const size_t np = c.n_embd / 4;
-    RMI_TRY(rmi_embed_q6_k(e.tok_embd, tok, e.x, e.part, c.n_embd, c.n_vocab, nc, e.s));
+    RMI_TRY(rmi_embed(e.emb_type, e.tok_embd, tok, e.x, e.part, c.n_embd, c.n_vocab, nc, e.s));
     for (auto& L : e.layers) {
         if (L.gdn) RMI_TRY(gdn_block(e, L, nc));
         else RMI_TRY(attn_block(e, L, e.x, e.part, pos, nc));
@@ -448,7 +462,7 @@ int trunk(Engine& e, int nc) {
 // with_head.
 int draft_cols(Engine& e, const int* tok, const int* pos, const float* h, const float* hp, int nc, bool with_head) {
     const auto& c = e.cfg;
-    RMI_TRY(rmi_embed_q6_k(e.tok_embd, tok, e.ex, e.epart, c.n_embd, c.n_vocab, nc, e.s));
+    RMI_TRY(rmi_embed(e.emb_type, e.tok_embd, tok, e.ex, e.epart, c.n_embd, c.n_vocab, nc, e.s));
     RMI_TRY(rmi_rms_norm_out_strided(e.ex, e.enorm, e.epart, e.eh, 2 * c.n_embd, nullptr, c.n_embd, c.eps, nc, e.s));
     RMI_TRY(rmi_rms_norm_out_strided(h, e.hnorm, hp, e.eh + c.n_embd, 2 * c.n_embd, nullptr, c.n_embd, c.eps, nc,
                                      e.s));
@@ -560,21 +574,26 @@ extern "C" rmi_model_config rmi_qwen35_9b_config(void) {
     c.n_rot = 64;
     c.rope_theta = 1e7f;
     c.eps = 1e-6f;
+    c.rope_factor = 1.0f;
+    c.rope_orig_ctx = 262144.0f;
     return c;
 }
 
-extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int max_ctx, void* stream,
-                                 rmi_engine** out) {
-    if (!cfg || !out) return fail(RMI_ERR_POINTER, "rmi_engine_create: null argument");
-    const rmi_model_config& c = *cfg;
+namespace rmi {
+namespace {
+
+int validate_config(const rmi_model_config& c, int max_ctx) {
     if (c.n_embd <= 0 || c.n_embd % 256 || c.n_ff % 256 || c.n_ff <= 0 || c.n_vocab <= 0 || c.n_layer <= 0 ||
-        c.ssm_h_k <= 0 || c.ssm_h_v % c.ssm_h_k || c.head_dim != 256 || c.n_head % c.n_kv || c.n_head <= 0 ||
-        (c.n_head / c.n_kv) * 2 > 16 || (c.ssm_h_v * kS) % 256 || ((2 * c.ssm_h_k + c.ssm_h_v) * kS) % 256 ||
-        (c.n_head * c.head_dim) % 256 || max_ctx < 64)
+        c.ssm_h_k <= 0 || c.ssm_h_v % c.ssm_h_k || c.head_dim != 256 || c.n_kv <= 0 || c.n_head % c.n_kv ||
+        c.n_head <= 0 || (c.n_head / c.n_kv) * 2 > 16 || (c.ssm_h_v * kS) % 256 ||
+        ((2 * c.ssm_h_k + c.ssm_h_v) * kS) % 256 || (c.n_head * c.head_dim) % 256 || c.n_rot < 0 || c.n_rot > 256 ||
+        c.n_rot % 2 || !(c.rope_theta > 1.0f) || max_ctx < 64)
         return fail(RMI_ERR_SHAPE, "rmi_engine_create: unsupported model shape");
-    std::unique_ptr<rmi_engine> h(new (std::nothrow) rmi_engine());
-    if (!h) return fail(RMI_ERR_STATE, "rmi_engine_create: out of host memory");
-    Engine& e = h->e;
+    return RMI_OK;
+}
+
+// configuration, stream, derived sizes and RoPE parameters
+int setup(Engine& e, const rmi_model_config& c, int max_ctx, void* stream) {
     e.cfg = c;
     e.max_ctx = (max_ctx + 63) / 64 * 64;
     // attention chunk = 64 * nsub positions: 128 at 4K-class caches, 512 at 64K (one partial wave per SIMD pair)
@@ -590,12 +609,19 @@ extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int
     e.attn_q = c.n_head * c.head_dim;
     e.q3_rows = 2 * e.attn_q + 2 * c.n_kv * c.head_dim;                     // 16 x (q|gate) | k | v
     e.max_in = std::max({c.n_ff, 2 * c.n_embd, e.gdn_v, e.attn_q});
-
-    // model (all Q6_K matrices random-init as in the benchmark configs)
+    // qw:1991-1999: YaRN with ext_factor 1, attn_factor 1, beta_fast 32, beta_slow 1
+    e.rope = rmi_rope_params{c.rope_theta, c.rope_factor > 1.0f ? c.rope_factor : 1.0f,
+                             c.rope_orig_ctx > 0.0f ? c.rope_orig_ctx : 262144.0f, 1.0f, 1.0f, 32.0f, 1.0f};
     e.gen_tmp_bytes = std::max({q6_bytes(c.n_vocab, c.n_embd), q6_bytes(2 * c.n_ff, c.n_embd), q6_bytes(c.n_embd, c.n_ff),
                                 q6_bytes(std::max(e.qkvz_rows, e.q3_rows), c.n_embd),
                                 q6_bytes(c.n_embd, std::max(e.gdn_v, e.attn_q)), q6_bytes(c.n_embd, 2 * c.n_embd)});
     HIP_TRY(hipMalloc(&e.gen_tmp, e.gen_tmp_bytes));
+    return RMI_OK;
+}
+
+// seeded random-init Q6_K model of the configured shapes (the benchmark configs)
+int weights_synthetic(Engine& e, uint64_t seed) {
+    const auto& c = e.cfg;
     RMI_TRY(e.alloc(&e.tok_embd, q6_bytes(c.n_vocab, c.n_embd)));
     RMI_TRY(rmi_gen_q6_k(e.tok_embd, static_cast<size_t>(c.n_vocab) * (c.n_embd / 256), mix_seed(seed, -1, 1), 1e-3f,
                          e.s));
@@ -614,12 +640,251 @@ extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int
     RMI_TRY(make_mat(e, e.eh_proj, c.n_embd, 2 * c.n_embd, mix_seed(seed, c.n_layer, 10)));
     RMI_TRY(make_vec(e, &e.enorm, c.n_embd, mix_seed(seed, c.n_layer, 11), 1.0f, 0.1f));
     RMI_TRY(make_vec(e, &e.hnorm, c.n_embd, mix_seed(seed, c.n_layer, 12), 1.0f, 0.1f));
-    RMI_TRY(make_vec(e, &e.shnorm, c.n_embd, mix_seed(seed, c.n_layer, 13), 1.0f, 0.1f));
+    return make_vec(e, &e.shnorm, c.n_embd, mix_seed(seed, c.n_layer, 13), 1.0f, 0.1f);
+}
+
+// ---- GGUF weights -------------------------------------------------------------------------------------------------
+struct GTensor {
+    const char* name = nullptr;
+    int type = -1, n_dims = 0;
+    int64_t dims[4] = {1, 1, 1, 1};
+    size_t bytes = 0;
+    const void* data = nullptr;
+};
+
+bool find_tensor(const rmi_gguf* g, const std::string& name, GTensor* t) {
+    const int64_t i = rmi_gguf_find(g, name.c_str());
+    if (i < 0) return false;
+    if (t) (void) rmi_gguf_tensor_info(g, i, &t->name, &t->type, &t->n_dims, t->dims, &t->bytes, &t->data);
+    return true;
+}
+
+int need_tensor(const rmi_gguf* g, const std::string& name, GTensor* t) {
+    if (!find_tensor(g, name, t)) return fail(RMI_ERR_SHAPE, ("gguf: missing tensor " + name).c_str());
+    if (!t->data) return fail(RMI_ERR_UNSUPPORTED, ("gguf: unsupported tensor type for " + name).c_str());
+    return RMI_OK;
+}
+
+std::string blk(int il, const char* what) { return "blk." + std::to_string(il) + "." + what; }
+
+// host -> device through two pinned staging buffers (hipHostMalloc), copies of one overlapping the fill of the other
+struct Uploader {
+    static constexpr size_t kBuf = 32u << 20;
+    uint8_t* pin[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    int next = 0;
+    ~Uploader() {
+        for (int i = 0; i < 2; ++i) {
+            if (ev[i]) (void) hipEventDestroy(ev[i]);
+            if (pin[i]) (void) hipHostFree(pin[i]);
+        }
+    }
+    int init() {
+        for (int i = 0; i < 2; ++i) {
+            HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&pin[i]), kBuf, hipHostMallocDefault));
+            HIP_TRY(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
+        }
+        return RMI_OK;
+    }
+    int put(void* dst, const void* src, size_t n, hipStream_t s) {
+        const auto* h = static_cast<const uint8_t*>(src);
+        auto* d = static_cast<uint8_t*>(dst);
+        for (size_t off = 0; off < n;) {
+            const size_t len = std::min(kBuf, n - off);
+            HIP_TRY(hipEventSynchronize(ev[next]));   // the copy that last used this buffer is done
+            std::memcpy(pin[next], h + off, len);
+            HIP_TRY(hipMemcpyAsync(d + off, pin[next], len, hipMemcpyHostToDevice, s));
+            HIP_TRY(hipEventRecord(ev[next], s));
+            next ^= 1;
+            off += len;
+        }
+        return RMI_OK;
+    }
+};
+
+// rows of the named Q6_K tensors, concatenated in order (the reference's try_cat groups, qw:2082-2087), into one engine
+// matrix: packed when n_in % 2048 == 0, else kept in GGUF blocks
+int load_mat(Engine& e, Uploader& up, const rmi_gguf* g, Mat& m, std::initializer_list<std::string> names) {
+    int n_in = -1, n_out = 0;
+    std::vector<GTensor> parts;
+    for (const auto& nm : names) {
+        GTensor t;
+        RMI_TRY(need_tensor(g, nm, &t));
+        if (t.type != 14 || t.n_dims != 2) return fail(RMI_ERR_UNSUPPORTED, ("gguf: " + nm + " is not a Q6_K matrix").c_str());
+        if (n_in >= 0 && t.dims[0] != n_in) return fail(RMI_ERR_SHAPE, ("gguf: " + nm + " has another row length").c_str());
+        n_in = static_cast<int>(t.dims[0]);
+        n_out += static_cast<int>(t.dims[1]);
+        parts.push_back(t);
+    }
+    m.n_in = n_in;
+    m.n_out = n_out;
+    static const bool use_packed = [] {
+        const char* v = std::getenv("RMI_ENGINE_PACKED");
+        return !(v && v[0] == '0');
+    }();
+    m.packed = use_packed && n_in % 2048 == 0;
+    const size_t gguf = q6_bytes(n_out, n_in);
+    uint8_t* dst = nullptr;
+    if (m.packed) {
+        if (gguf > e.gen_tmp_bytes) return fail(RMI_ERR_STATE, "engine: generation buffer too small");
+        dst = e.gen_tmp;
+    } else {
+        RMI_TRY(e.alloc(&m.w, gguf));
+        dst = m.w;
+    }
+    size_t off = 0;
+    for (const auto& t : parts) {
+        RMI_TRY(up.put(dst + off, t.data, t.bytes, e.s));
+        off += t.bytes;
+    }
+    if (!m.packed) return RMI_OK;
+    RMI_TRY(e.alloc(&m.w, rmi_q6_k_packed_bytes(n_in, n_out)));
+    RMI_TRY(rmi_q6_k_pack(e.gen_tmp, m.w, n_in, n_out, e.s));
+    HIP_TRY(hipStreamSynchronize(e.s));   // the next matrix reuses the staging buffer
+    return RMI_OK;
+}
+
+int load_f32(Engine& e, Uploader& up, const rmi_gguf* g, float** p, const std::string& name, size_t n) {
+    GTensor t;
+    RMI_TRY(need_tensor(g, name, &t));
+    size_t elems = 1;
+    for (int d = 0; d < t.n_dims; ++d) elems *= static_cast<size_t>(t.dims[d]);
+    if (t.type != 0 || elems != n) return fail(RMI_ERR_SHAPE, ("gguf: " + name + " is not an F32 vector of the expected size").c_str());
+    RMI_TRY(e.alloc(p, n));
+    return up.put(*p, t.data, n * sizeof(float), e.s);
+}
+
+int load_attn(Engine& e, Uploader& up, const rmi_gguf* g, Layer& L, int il) {
+    const auto& c = e.cfg;
+    L.gdn = false;
+    RMI_TRY(load_f32(e, up, g, &L.attn_norm, blk(il, "attn_norm.weight"), c.n_embd));
+    RMI_TRY(load_f32(e, up, g, &L.post_norm, blk(il, "post_attention_norm.weight"), c.n_embd));
+    RMI_TRY(load_mat(e, up, g, L.in_proj, {blk(il, "attn_q.weight"), blk(il, "attn_k.weight"), blk(il, "attn_v.weight")}));
+    RMI_TRY(load_mat(e, up, g, L.out_proj, {blk(il, "attn_output.weight")}));
+    RMI_TRY(load_mat(e, up, g, L.upgate, {blk(il, "ffn_up.weight"), blk(il, "ffn_gate.weight")}));
+    RMI_TRY(load_mat(e, up, g, L.down, {blk(il, "ffn_down.weight")}));
+    RMI_TRY(load_f32(e, up, g, &L.qn, blk(il, "attn_q_norm.weight"), c.head_dim));
+    RMI_TRY(load_f32(e, up, g, &L.kn, blk(il, "attn_k_norm.weight"), c.head_dim));
+    if (L.in_proj.n_out != e.q3_rows || L.out_proj.n_in != e.attn_q || L.upgate.n_out != 2 * c.n_ff ||
+        L.down.n_in != c.n_ff || L.in_proj.n_in != c.n_embd)
+        return fail(RMI_ERR_SHAPE, ("gguf: attention layer " + std::to_string(il) + " has unexpected shapes").c_str());
+    return alloc_attn_state(e, L);
+}
+
+int load_gdn(Engine& e, Uploader& up, const rmi_gguf* g, Layer& L, int il) {
+    const auto& c = e.cfg;
+    L.gdn = true;
+    RMI_TRY(load_f32(e, up, g, &L.attn_norm, blk(il, "attn_norm.weight"), c.n_embd));
+    RMI_TRY(load_f32(e, up, g, &L.post_norm, blk(il, "post_attention_norm.weight"), c.n_embd));
+    // qkv | z | beta | alpha: the reference's qkvz and ab groups (beta before alpha, qw:2085) as one GEMV
+    RMI_TRY(load_mat(e, up, g, L.in_proj, {blk(il, "attn_qkv.weight"), blk(il, "attn_gate.weight"),
+                                           blk(il, "ssm_beta.weight"), blk(il, "ssm_alpha.weight")}));
+    RMI_TRY(load_mat(e, up, g, L.out_proj, {blk(il, "ssm_out.weight")}));
+    RMI_TRY(load_mat(e, up, g, L.upgate, {blk(il, "ffn_up.weight"), blk(il, "ffn_gate.weight")}));
+    RMI_TRY(load_mat(e, up, g, L.down, {blk(il, "ffn_down.weight")}));
+    const int ch = 2 * c.ssm_h_k * kS + c.ssm_h_v * kS;
+    RMI_TRY(load_f32(e, up, g, &L.conv_w, blk(il, "ssm_conv1d.weight"), static_cast<size_t>(4) * ch));
+    RMI_TRY(load_f32(e, up, g, &L.dt, blk(il, "ssm_dt.bias"), c.ssm_h_v));
+    RMI_TRY(load_f32(e, up, g, &L.ssm_a, blk(il, "ssm_a"), c.ssm_h_v));
+    RMI_TRY(load_f32(e, up, g, &L.ssm_norm, blk(il, "ssm_norm.weight"), kS));
+    if (L.in_proj.n_out != e.qkvz_rows || L.out_proj.n_in != e.gdn_v || L.upgate.n_out != 2 * c.n_ff ||
+        L.down.n_in != c.n_ff || L.in_proj.n_in != c.n_embd)
+        return fail(RMI_ERR_SHAPE, ("gguf: GDN layer " + std::to_string(il) + " has unexpected shapes").c_str());
+    return alloc_gdn_state(e, L);
+}
+
+double meta_num(const rmi_gguf* g, const char* key, double def) {
+    double v = def;
+    return rmi_gguf_get_num(g, key, &v) == RMI_OK ? v : def;
+}
+
+// the model configuration from a qwen35 file: shapes from the tensors, eps / RoPE / YaRN from the metadata
+int gguf_config(const rmi_gguf* g, rmi_model_config* c) {
+    const char* arch = nullptr;
+    if (rmi_gguf_get_str(g, "general.architecture", &arch) != RMI_OK || std::string(arch) != "qwen35")
+        return fail(RMI_ERR_UNSUPPORTED, "gguf: not a qwen35 GGUF");
+    double blocks = 0, nextn = 0;
+    if (rmi_gguf_get_num(g, "qwen35.block_count", &blocks) != RMI_OK ||
+        rmi_gguf_get_num(g, "qwen35.nextn_predict_layers", &nextn) != RMI_OK || nextn != 1)
+        return fail(RMI_ERR_SHAPE, "gguf: qwen35 file without block_count / one nextn layer");
+    *c = rmi_model_config{};
+    c->n_layer = static_cast<int>(blocks - nextn);
+    GTensor emb, up, qkv, ssma, qn, aq, ak, snorm;
+    RMI_TRY(need_tensor(g, "token_embd.weight", &emb));
+    c->n_embd = static_cast<int>(emb.dims[0]);
+    c->n_vocab = static_cast<int>(emb.dims[1]);
+    RMI_TRY(need_tensor(g, blk(0, "ffn_up.weight"), &up));
+    c->n_ff = static_cast<int>(up.dims[1]);
+    int first_attn = -1, first_gdn = -1;
+    for (int il = 0; il < c->n_layer; ++il) {
+        const bool a = find_tensor(g, blk(il, "attn_q.weight"), nullptr);
+        const bool d = find_tensor(g, blk(il, "attn_qkv.weight"), nullptr);
+        if (a == d) return fail(RMI_ERR_SHAPE, ("gguf: layer " + std::to_string(il) + " is neither GDN nor attention").c_str());
+        if (a && first_attn < 0) first_attn = il;
+        if (d && first_gdn < 0) first_gdn = il;
+    }
+    const int ai = first_attn >= 0 ? first_attn : c->n_layer;   // the draft block is an attention layer
+    RMI_TRY(need_tensor(g, blk(ai, "attn_q_norm.weight"), &qn));
+    RMI_TRY(need_tensor(g, blk(ai, "attn_q.weight"), &aq));
+    RMI_TRY(need_tensor(g, blk(ai, "attn_k.weight"), &ak));
+    c->head_dim = static_cast<int>(qn.dims[0]);
+    c->n_head = static_cast<int>(aq.dims[1] / (2 * c->head_dim));
+    c->n_kv = static_cast<int>(ak.dims[1] / c->head_dim);
+    if (first_gdn >= 0) {
+        RMI_TRY(need_tensor(g, blk(first_gdn, "ssm_a"), &ssma));
+        RMI_TRY(need_tensor(g, blk(first_gdn, "attn_qkv.weight"), &qkv));
+        RMI_TRY(need_tensor(g, blk(first_gdn, "ssm_norm.weight"), &snorm));
+        if (snorm.dims[0] != kS) return fail(RMI_ERR_SHAPE, "gguf: GDN state size must be 128");
+        c->ssm_h_v = static_cast<int>(ssma.dims[0]);
+        c->ssm_h_k = static_cast<int>((qkv.dims[1] - static_cast<int64_t>(kS) * c->ssm_h_v) / (2 * kS));
+    } else {
+        c->ssm_h_k = 1;
+        c->ssm_h_v = 2;
+    }
+    c->n_rot = static_cast<int>(meta_num(g, "qwen35.rope.dimension_count", 64));
+    c->rope_theta = static_cast<float>(meta_num(g, "qwen35.rope.freq_base", 1e7));
+    c->eps = static_cast<float>(meta_num(g, "qwen35.attention.layer_norm_rms_epsilon", 1e-6));
+    c->rope_factor = static_cast<float>(meta_num(g, "qwen35.rope.scaling.factor", 1.0));
+    c->rope_orig_ctx = static_cast<float>(meta_num(g, "qwen35.rope.scaling.original_context_length", 262144.0));
+    return RMI_OK;
+}
+
+int weights_gguf(Engine& e, const rmi_gguf* g) {
+    const auto& c = e.cfg;
+    Uploader up;
+    RMI_TRY(up.init());
+    GTensor emb;
+    RMI_TRY(need_tensor(g, "token_embd.weight", &emb));
+    if (emb.type != 14 && emb.type != 13 && emb.type != 12)
+        return fail(RMI_ERR_UNSUPPORTED, "gguf: token_embd must be Q6_K, Q5_K or Q4_K");
+    e.emb_type = emb.type;
+    RMI_TRY(e.alloc(&e.tok_embd, emb.bytes));
+    RMI_TRY(up.put(e.tok_embd, emb.data, emb.bytes, e.s));
+    RMI_TRY(load_mat(e, up, g, e.lm_head, {"output.weight"}));
+    RMI_TRY(load_f32(e, up, g, &e.out_norm, "output_norm.weight", c.n_embd));
+    if (e.lm_head.n_out != c.n_vocab || e.lm_head.n_in != c.n_embd) return fail(RMI_ERR_SHAPE, "gguf: bad output.weight");
+    e.layers.resize(c.n_layer);
+    for (int il = 0; il < c.n_layer; ++il) {
+        if (find_tensor(g, blk(il, "attn_qkv.weight"), nullptr)) RMI_TRY(load_gdn(e, up, g, e.layers[il], il));
+        else RMI_TRY(load_attn(e, up, g, e.layers[il], il));
+    }
+    const int d = c.n_layer;   // the nextn draft block (qw:2096-2126)
+    RMI_TRY(load_attn(e, up, g, e.draft, d));
+    RMI_TRY(load_mat(e, up, g, e.eh_proj, {blk(d, "nextn.eh_proj.weight")}));
+    if (e.eh_proj.n_in != 2 * c.n_embd || e.eh_proj.n_out != c.n_embd) return fail(RMI_ERR_SHAPE, "gguf: bad eh_proj");
+    RMI_TRY(load_f32(e, up, g, &e.hnorm, blk(d, "nextn.hnorm.weight"), c.n_embd));
+    RMI_TRY(load_f32(e, up, g, &e.enorm, blk(d, "nextn.enorm.weight"), c.n_embd));
+    RMI_TRY(load_f32(e, up, g, &e.shnorm, blk(d, "nextn.shared_head_norm.weight"), c.n_embd));
+    HIP_TRY(hipStreamSynchronize(e.s));   // the staging buffers are freed on return
+    return RMI_OK;
+}
+
+// round state and activations (kChunk columns), after the weights
+int alloc_runtime(Engine& e) {
+    const auto& c = e.cfg;
     HIP_TRY(hipStreamSynchronize(e.s));   // every pack has read the staging buffer
     HIP_TRY(hipFree(e.gen_tmp));
     e.gen_tmp = nullptr;
-
-    // round state and activations (two columns)
     RMI_TRY(e.alloc(&e.ints, 64));
     hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(256), 0, e.s, e.ints, static_cast<size_t>(64), 0);
     RMI_TRY(launch_status("fill"));
@@ -672,7 +937,45 @@ extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int
     HIP_TRY(hipEventCreate(&e.ev0));
     HIP_TRY(hipEventCreate(&e.ev1));
     HIP_TRY(hipStreamSynchronize(e.s));
+    return RMI_OK;
+}
+
+}  // namespace
+}  // namespace rmi
+
+extern "C" int rmi_engine_create(const rmi_model_config* cfg, uint64_t seed, int max_ctx, void* stream,
+                                 rmi_engine** out) {
+    if (!cfg || !out) return fail(RMI_ERR_POINTER, "rmi_engine_create: null argument");
+    RMI_TRY(validate_config(*cfg, max_ctx));
+    std::unique_ptr<rmi_engine> h(new (std::nothrow) rmi_engine());
+    if (!h) return fail(RMI_ERR_STATE, "rmi_engine_create: out of host memory");
+    RMI_TRY(setup(h->e, *cfg, max_ctx, stream));
+    RMI_TRY(weights_synthetic(h->e, seed));
+    RMI_TRY(alloc_runtime(h->e));
     *out = h.release();
+    return RMI_OK;
+}
+
+extern "C" int rmi_engine_create_gguf(const char* path, int max_ctx, void* stream, rmi_engine** out) {
+    if (!path || !out) return fail(RMI_ERR_POINTER, "rmi_engine_create_gguf: null argument");
+    rmi_gguf* g = nullptr;
+    RMI_TRY(rmi_gguf_open(path, &g));
+    std::unique_ptr<rmi_gguf, void (*)(rmi_gguf*)> file(g, rmi_gguf_close);
+    rmi_model_config c{};
+    RMI_TRY(gguf_config(g, &c));
+    RMI_TRY(validate_config(c, max_ctx));
+    std::unique_ptr<rmi_engine> h(new (std::nothrow) rmi_engine());
+    if (!h) return fail(RMI_ERR_STATE, "rmi_engine_create_gguf: out of host memory");
+    RMI_TRY(setup(h->e, c, max_ctx, stream));
+    RMI_TRY(weights_gguf(h->e, g));
+    RMI_TRY(alloc_runtime(h->e));
+    *out = h.release();
+    return RMI_OK;
+}
+
+extern "C" int rmi_engine_config(const rmi_engine* h, rmi_model_config* out) {
+    if (!h || !out) return fail(RMI_ERR_POINTER, "rmi_engine_config: null argument");
+    *out = h->e.cfg;
     return RMI_OK;
 }
 
@@ -841,6 +1144,10 @@ extern "C" int rmi_engine_read(rmi_engine* h, int which, int layer, size_t offse
         case RMI_BUF_HIDDEN:
             src = e.hsave;
             size = sizeof(float) * c.n_embd;
+            break;
+        case RMI_BUF_LOGITS:
+            src = e.logits;
+            size = sizeof(float) * 2 * static_cast<size_t>(c.n_vocab);
             break;
         default:
             return fail(RMI_ERR_SHAPE, "rmi_engine_read: bad buffer");

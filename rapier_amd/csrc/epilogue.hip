@@ -186,25 +186,55 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const uint64_t* __res
     }
 }
 
-// ---- token embedding: device dequant of one Q6_K row per token (ggml dequantize_row_q6_K order) ---------------------
-// x[c][e] = (d * sc) * (code - 32); partials of the row for the first norm (row_sum_partials, qw:1426-1430).
-// One workgroup of 256 lanes per 256-element block; lane e dequantizes element e.
-__global__ __launch_bounds__(256) void embed_q6_k_kernel(const uint8_t* __restrict__ emb, const int* __restrict__ tok,
-                                                         float* __restrict__ x, float* __restrict__ partials,
-                                                         int n_embd, int n_vocab) {
+// ---- token embedding: device dequant of one row per token ---------------------------------------------------------
+// GGUF types 14 (Q6_K, ggml dequantize_row_q6_K order), 13 (Q5_K) and 12 (Q4_K) (ggml dequantize_row_q5_K / q4_K):
+// every weight is d * sc * q (- dmin * m), whose products are exact in fp32, so one rounding at most.  One lane per
+// element of a 256-block; partials of 4 consecutive elements in order.
+__device__ __forceinline__ void k4_scale_min(const uint8_t* s, int j, int& sc, int& m) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        m = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ float embed_value(const uint8_t* b, int e) {
+    if constexpr (TYPE == 14) {
+        const int n = e >> 7, k = (e & 127) >> 5, l = e & 31;
+        const uint8_t lo = b[64 * n + 32 * (k & 1) + l];
+        const int nib = (k >> 1) ? (lo >> 4) : (lo & 15);
+        const int hi = (b[128 + 32 * n + l] >> (2 * k)) & 3;
+        const int sc = static_cast<int8_t>(b[192 + 8 * n + l / 16 + 2 * k]);
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b + 208));
+        return (d * static_cast<float>(sc)) * static_cast<float>((nib | (hi << 4)) - 32);
+    } else {
+        const int j = e >> 5, c = j >> 1, h = j & 1, l = e & 31;
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b));
+        const float dmin = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b + 2));
+        int sc, m;
+        k4_scale_min(b + 4, j, sc, m);
+        int q;
+        if constexpr (TYPE == 13) q = ((b[48 + 32 * c + l] >> (4 * h)) & 15) | (((b[16 + l] >> j) & 1) << 4);
+        else q = (b[16 + 32 * c + l] >> (4 * h)) & 15;
+        return (d * static_cast<float>(sc)) * static_cast<float>(q) - dmin * static_cast<float>(m);
+    }
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ emb, const int* __restrict__ tok,
+                                                    float* __restrict__ x, float* __restrict__ partials, int n_embd,
+                                                    int n_vocab) {
+    constexpr int kBytes = TYPE == 14 ? kQ6KBytes : TYPE == 13 ? 176 : 144;
     const int c = blockIdx.y;
     int t = tok[c];
     t = t < 0 ? 0 : (t >= n_vocab ? n_vocab - 1 : t);   // an out-of-range id never reads outside the table
     const int nb = n_embd / 256;
-    const uint8_t* b = emb + (static_cast<size_t>(t) * nb + blockIdx.x) * kQ6KBytes;
+    const uint8_t* b = emb + (static_cast<size_t>(t) * nb + blockIdx.x) * kBytes;
     const int e = threadIdx.x;
-    const int n = e >> 7, k = (e & 127) >> 5, l = e & 31;
-    const uint8_t lo = b[64 * n + 32 * (k & 1) + l];
-    const int nib = (k >> 1) ? (lo >> 4) : (lo & 15);
-    const int hi = (b[128 + 32 * n + l] >> (2 * k)) & 3;
-    const int sc = static_cast<int8_t>(b[192 + 8 * n + l / 16 + 2 * k]);
-    const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b + 208));
-    const float v = (d * static_cast<float>(sc)) * static_cast<float>((nib | (hi << 4)) - 32);
+    const float v = embed_value<TYPE>(b, e);
     const int idx = blockIdx.x * 256 + e;
     x[static_cast<size_t>(c) * n_embd + idx] = v;
     const float v0 = __shfl(v, (e & ~3) + 0, 64), v1 = __shfl(v, (e & ~3) + 1, 64);
@@ -315,13 +345,23 @@ extern "C" int rmi_argmax(const float* logits, int n, int ncols, int col_stride,
     return launch_status("argmax");
 }
 
+extern "C" int rmi_embed(int type, const void* emb, const int* tokens, float* x, float* partials, int n_embd,
+                         int n_vocab, int ncols, void* stream) {
+    if (n_embd <= 0 || n_embd % 256 != 0 || n_vocab <= 0 || bad_cols(ncols))
+        return fail(RMI_ERR_SHAPE, "embed: bad shape");
+    if (type != 14 && type != 13 && type != 12) return fail(RMI_ERR_UNSUPPORTED, "embed: token_embd type must be Q6_K, Q5_K or Q4_K");
+    if (!emb || !aligned4(tokens) || !aligned4(x) || !aligned4(partials))
+        return fail(RMI_ERR_POINTER, "embed: null or misaligned pointer");
+    const auto s = static_cast<hipStream_t>(stream);
+    const dim3 grid(n_embd / 256, ncols), block(256);
+    const auto* e = static_cast<const uint8_t*>(emb);
+    if (type == 14) hipLaunchKernelGGL(embed_kernel<14>, grid, block, 0, s, e, tokens, x, partials, n_embd, n_vocab);
+    else if (type == 13) hipLaunchKernelGGL(embed_kernel<13>, grid, block, 0, s, e, tokens, x, partials, n_embd, n_vocab);
+    else hipLaunchKernelGGL(embed_kernel<12>, grid, block, 0, s, e, tokens, x, partials, n_embd, n_vocab);
+    return launch_status("embed");
+}
+
 extern "C" int rmi_embed_q6_k(const void* emb, const int* tokens, float* x, float* partials, int n_embd, int n_vocab,
                               int ncols, void* stream) {
-    if (n_embd <= 0 || n_embd % 256 != 0 || n_vocab <= 0 || bad_cols(ncols))
-        return fail(RMI_ERR_SHAPE, "embed_q6_k: bad shape");
-    if (!emb || (reinterpret_cast<uintptr_t>(emb) & 1u) || !aligned4(tokens) || !aligned4(x) || !aligned4(partials))
-        return fail(RMI_ERR_POINTER, "embed_q6_k: null or misaligned pointer");
-    hipLaunchKernelGGL(embed_q6_k_kernel, dim3(n_embd / 256, ncols), dim3(256), 0, static_cast<hipStream_t>(stream),
-                       static_cast<const uint8_t*>(emb), tokens, x, partials, n_embd, n_vocab);
-    return launch_status("embed_q6_k");
+    return rmi_embed(14, emb, tokens, x, partials, n_embd, n_vocab, ncols, stream);
 }

@@ -7,17 +7,19 @@ moves token ids in and out.
 from __future__ import annotations
 
 import ctypes
+import os
 
 from . import _call, _stream, last_error, lib
 
 GREEDY, MTP, MTP_FORCED = 0, 1, 2
-BUF_GDN_STATE, BUF_GDN_HIST, BUF_K_CACHE, BUF_V_CACHE, BUF_HIDDEN = 0, 1, 2, 3, 4
+BUF_GDN_STATE, BUF_GDN_HIST, BUF_K_CACHE, BUF_V_CACHE, BUF_HIDDEN, BUF_LOGITS = 0, 1, 2, 3, 4, 5
 
 
 class ModelConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("n_embd", "n_ff", "n_vocab", "n_layer", "ssm_h_k", "ssm_h_v", "n_head",
                                             "n_kv", "head_dim", "n_rot")] + \
-               [("rope_theta", ctypes.c_float), ("eps", ctypes.c_float)]
+               [("rope_theta", ctypes.c_float), ("eps", ctypes.c_float), ("rope_factor", ctypes.c_float),
+                ("rope_orig_ctx", ctypes.c_float)]
 
 
 class EngineInfo(ctypes.Structure):
@@ -60,6 +62,20 @@ def _bind():
                                                     P(ctypes.c_int)]),
         "rmi_engine_read": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_size_t,
                                            ctypes.c_void_p, ctypes.c_size_t]),
+        "rmi_engine_create_gguf": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.c_void_p, P(ctypes.c_void_p)]),
+        "rmi_engine_config": (ctypes.c_int, [ctypes.c_void_p, P(ModelConfig)]),
+        "rmi_gguf_open": (ctypes.c_int, [ctypes.c_char_p, P(ctypes.c_void_p)]),
+        "rmi_gguf_close": (None, [ctypes.c_void_p]),
+        "rmi_gguf_tensor_count": (ctypes.c_int64, [ctypes.c_void_p]),
+        "rmi_gguf_find": (ctypes.c_int64, [ctypes.c_void_p, ctypes.c_char_p]),
+        "rmi_gguf_tensor_info": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, P(ctypes.c_char_p), P(ctypes.c_int),
+                                                P(ctypes.c_int), P(ctypes.c_int64), P(ctypes.c_size_t),
+                                                P(ctypes.c_void_p)]),
+        "rmi_gguf_get_num": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, P(ctypes.c_double)]),
+        "rmi_gguf_get_str": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, P(ctypes.c_char_p)]),
+        "rmi_gguf_array_len": (ctypes.c_int64, [ctypes.c_void_p, ctypes.c_char_p]),
+        "rmi_gguf_array_str": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64, P(ctypes.c_char_p)]),
+        "rmi_gguf_array_num": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64, P(ctypes.c_double)]),
         "rmi_engine_synth_context": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_int,
                                                     P(ctypes.c_int)]),
         "rmi_engine_save_state": (ctypes.c_int, [ctypes.c_void_p]),
@@ -88,13 +104,88 @@ def small_config(**kw) -> ModelConfig:
     return c
 
 
-class Engine:
-    def __init__(self, cfg: ModelConfig, seed: int = 1234, max_ctx: int = 4096, stream=None):
+class GgufFile:
+    """A memory-mapped GGUF file (the engine's reader, rmi_gguf_*): metadata and tensor table."""
+
+    def __init__(self, path: str):
         _bind()
+        h = ctypes.c_void_p()
+        _call("rmi_gguf_open", os.fsencode(path), ctypes.byref(h))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().rmi_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self):
+        return lib().rmi_gguf_tensor_count(self._h)
+
+    def find(self, name: str) -> int:
+        return lib().rmi_gguf_find(self._h, name.encode())
+
+    def tensor(self, i: int):
+        """(name, ggml type, dims tuple, data bytes as a uint8 array or None)"""
+        import numpy as np
+        name, t, nd = ctypes.c_char_p(), ctypes.c_int(), ctypes.c_int()
+        dims, nbytes, data = (ctypes.c_int64 * 4)(), ctypes.c_size_t(), ctypes.c_void_p()
+        _call("rmi_gguf_tensor_info", self._h, i, ctypes.byref(name), ctypes.byref(t), ctypes.byref(nd), dims,
+              ctypes.byref(nbytes), ctypes.byref(data))
+        arr = None
+        if data.value:
+            arr = np.ctypeslib.as_array((ctypes.c_uint8 * nbytes.value).from_address(data.value)).copy()
+        return name.value.decode(), t.value, tuple(dims[:nd.value]), arr
+
+    def num(self, key: str):
+        v = ctypes.c_double()
+        return v.value if lib().rmi_gguf_get_num(self._h, key.encode(), ctypes.byref(v)) == 0 else None
+
+    def str(self, key: str):
+        v = ctypes.c_char_p()
+        return v.value.decode() if lib().rmi_gguf_get_str(self._h, key.encode(), ctypes.byref(v)) == 0 else None
+
+    def array(self, key: str):
+        n = lib().rmi_gguf_array_len(self._h, key.encode())
+        if n < 0:
+            return None
+        out = []
+        for i in range(n):
+            sv, dv = ctypes.c_char_p(), ctypes.c_double()
+            if lib().rmi_gguf_array_str(self._h, key.encode(), i, ctypes.byref(sv)) == 0:
+                out.append(sv.value.decode())
+            else:
+                _call("rmi_gguf_array_num", self._h, key.encode(), i, ctypes.byref(dv))
+                out.append(dv.value)
+        return out
+
+
+class Engine:
+    def __init__(self, cfg: ModelConfig, seed: int = 1234, max_ctx: int = 4096, stream=None, _handle=None):
+        _bind()
+        if _handle is not None:
+            self._h = _handle
+            c = ModelConfig()
+            _call("rmi_engine_config", self._h, ctypes.byref(c))
+            self.cfg = c
+            return
         self.cfg = cfg
         h = ctypes.c_void_p()
         _call("rmi_engine_create", ctypes.byref(cfg), seed, max_ctx, _stream(stream), ctypes.byref(h))
         self._h = h
+
+    @classmethod
+    def from_gguf(cls, path: str, max_ctx: int = 4096, stream=None) -> "Engine":
+        """a qwen35 GGUF (load_model, qw:1978-2134)"""
+        _bind()
+        h = ctypes.c_void_p()
+        _call("rmi_engine_create_gguf", os.fsencode(path), max_ctx, _stream(stream), ctypes.byref(h))
+        return cls(None, _handle=h)
 
     def close(self):
         if self._h:

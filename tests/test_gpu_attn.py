@@ -127,3 +127,30 @@ def test_flash_decode_chunk_bitwise_equals_single_queries(orc, rmi, ctx, nsub, n
     o = orc.gqa_decode(q[:NH * HD], kc, vc, NH, NKV, HD, p0 + 1, SCALE)
     gate = np.concatenate([g[h * 2 * HD + HD:h * 2 * HD + 2 * HD] for h in range(NH)])
     assert_close_rel(y[:NH * HD], o / (1 + np.exp(-gate.astype(np.float64))), rtol=1e-3, atol_frac=1e-5, what="t0")
+
+
+@pytest.mark.parametrize("factor,ntok", [(4.0, 3), (1.0, 2)])
+def test_attn_prep_yarn_matches_oracle(orc, rmi, factor, ntok):
+    """YaRN RoPE (rope.scaling.factor 4, original context 65536, the reference's ext 1 / attn 1 / beta 32, 1):
+    q within 1e-5 of the oracle's fp64 YaRN; factor 1 is bitwise the plain-RoPE entry point"""
+    t_ = torch()
+    max_ctx, p0, base, eps, orig = 1 << 18, 150001, 1e7, 1e-6, 65536.0
+    q3 = orc.normal(ntok * Q3, seed=960)
+    qn = (1 + orc.normal(HD, seed=961, std=0.1)).astype(np.float32)
+    kn = (1 + orc.normal(HD, seed=962, std=0.1)).astype(np.float32)
+    kc = t_.zeros(max_ctx * NKV * HD, dtype=t_.int16, device="cuda:0")
+    vc = t_.zeros(max_ctx * NKV * HD, dtype=t_.int16, device="cuda:0")
+    qo = empty(ntok * NH * HD)
+    dpos = dev(np.array([p0], np.int32))
+    rmi.attn_prep_rope(dev(q3), Q3, dev(qn), dev(kn), kc, vc, dpos, qo, NH, NKV, HD, 64, base, factor, orig, eps, ntok,
+                       max_ctx)
+    qh = host(qo)
+    for t in range(ntok):
+        src = q3[t * Q3:(t + 1) * Q3]
+        qx = np.concatenate([src[h * 2 * HD:h * 2 * HD + HD] for h in range(NH)])
+        qref = orc.rope_yarn(orc.rms_norm_heads(qx, qn, NH, HD, eps), NH, HD, 64, p0 + t, base, factor, orig)
+        assert_close_rel(qh[t * NH * HD:(t + 1) * NH * HD], qref, rtol=1e-5, atol_frac=2e-6, what=f"q t{t}")
+    if factor == 1.0:
+        qo2 = empty(ntok * NH * HD)
+        rmi.attn_prep(dev(q3), Q3, dev(qn), dev(kn), kc, vc, dpos, qo2, NH, NKV, HD, 64, base, eps, ntok, max_ctx)
+        assert np.array_equal(host(qo2).view(np.uint32), qh.view(np.uint32))

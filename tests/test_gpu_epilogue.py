@@ -133,6 +133,22 @@ def test_embed_q6_k_rows(orc, rmi):
     np.testing.assert_allclose(host(p), (xh.astype(np.float64).reshape(-1, 4) ** 2).sum(1), rtol=1e-6)
 
 
+@pytest.mark.parametrize("ggml_type", [13, 12])
+def test_embed_k_quant_rows(orc, rmi, ggml_type):
+    """Q5_K / Q4_K token_embd tables (Q5_K_M files): rows bit-exact vs the oracle's ggml dequant, ids clamped"""
+    from tests.kquant import k_blocks
+    n_embd, n_vocab = 1024, 40
+    emb, _ = k_blocks(np.random.default_rng(ggml_type), n_vocab * n_embd // 256, ggml_type == 13)
+    toks = np.array([0, 39, 17, 1000], dtype=np.int32)          # 1000 is clamped to the last row
+    x, p = empty(4 * n_embd), empty(4 * n_embd // 4)
+    rmi.embed(ggml_type, dev(emb), dev(toks), x, p, n_embd, n_vocab, ncols=4)
+    deq = (orc.q5k_dequant if ggml_type == 13 else orc.q4k_dequant)(emb, n_vocab, n_embd).reshape(n_vocab, n_embd)
+    xh = host(x).reshape(4, n_embd)
+    for c, t in enumerate([0, 39, 17, 39]):
+        assert np.array_equal(xh[c], deq[t]), f"column {c}"
+    np.testing.assert_allclose(host(p), (xh.astype(np.float64).reshape(-1, 4) ** 2).sum(1), rtol=1e-6)
+
+
 @pytest.mark.parametrize("n_in,n_out,ncols", [(4096, 1000, 1), (4096, 257, 2), (1024, 64, 5)])
 def test_q8_0_gemv(orc, rmi, n_in, n_out, ncols):
     w = orc.gen_q8_0(n_out, n_in, seed=n_out)

@@ -1,0 +1,204 @@
+"""A qwen35 GGUF through rmi_engine_create_gguf (load_model, qw:1978-2134) against the CPU oracle of the whole model
+(oracle/model.py: forward_token qw:1773-1824 and draft_predict qw:1316-1406 composed from the pinned oracle pieces,
+every matrix applied on its own, no concatenation).
+
+The files are small members of the family (the nextn draft block always present) written with the reference's tensor
+names and metadata keys.  Without Q8_1 rounding differences the engine and the oracle agree to ~1e-7 (fp32 against
+fp64 inside the ops; observed on one-layer models).  But a ~1e-7 difference ahead of a Q8_1 quantization rounds an
+activation to the neighbouring code now and then (~1e-5 per element here), which moves every output of the next GEMV
+by about (amax / 127) / (sqrt(n) rms), ~1e-3 of their scale, and later tokens and layers carry it.  So the bars
+(written here) admit such flips and still catch any systematic error, which would touch every row:
+- K/V cache rows (trunk attention layers and the draft block): with one trunk layer at least 80% within fp16 rounding
+  of the oracle's row (2e-3 of its max|.|) and every row within 3e-2; with four layers every row within 6e-2 (a flip
+  perturbs the GDN state, and every later position carries it);
+- logits and the final-normed hidden within 1e-2 (one layer) or 5e-2 (four layers) of max|.|, correlation > 0.9999 /
+  0.999; GDN states within the same bound;
+- the first greedy token equal to the oracle's argmax wherever the oracle's top-2 margin exceeds twice the bound; along
+  a greedy stream (the oracle fed the engine's tokens) every token whose oracle margin exceeds 3e-2 of max|logit|
+  (3x the observed error) equal to the oracle's argmax; MTP after a GGUF load bit-identical to greedy."""
+import numpy as np
+import pytest
+
+from tests.gguf_writer import STR, U32, F32 as GF32, write_gguf
+
+pytestmark = pytest.mark.gpu
+
+N_EMBD, N_FF, N_VOCAB, N_LAYER = 2048, 4096, 5000, 4
+H_K, H_V, N_HEAD, N_KV, HD = 4, 8, 8, 2, 256
+
+
+@pytest.fixture(scope="module")
+def E():
+    import rapier_amd.engine as eng
+    from tests.gpu_util import torch
+    torch()
+    return eng
+
+
+def build_model(orc, seed=1, emb_type="Q6_K", rope_factor=None, pattern=(0, 0, 0, 1)):
+    """tensors name -> (ggml type, dims, data) with the reference's names (qw:2003-2127); pattern[il] = 1 for an
+    attention layer"""
+    from tests.kquant import k_blocks
+    rng = np.random.default_rng(seed)
+    t = {}
+    cnt = [0]
+
+    def q6(name, n_in, n_out):
+        cnt[0] += 1
+        t[name] = (14, (n_in, n_out), orc.gen_q6k(n_out, n_in, seed=seed * 1000 + cnt[0]))
+
+    def vec(name, n, mean=1.0, std=0.1):
+        t[name] = (0, (n,), (mean + std * rng.standard_normal(n)).astype(np.float32))
+
+    if emb_type == "Q6_K":
+        q6("token_embd.weight", N_EMBD, N_VOCAB)
+    else:
+        five = emb_type == "Q5_K"
+        data, _ = k_blocks(rng, N_VOCAB * N_EMBD // 256, five)
+        t["token_embd.weight"] = (13 if five else 12, (N_EMBD, N_VOCAB), data)
+    q6("output.weight", N_EMBD, N_VOCAB)
+    vec("output_norm.weight", N_EMBD)
+
+    def attn(il):
+        p = f"blk.{il}."
+        vec(p + "attn_norm.weight", N_EMBD)
+        vec(p + "post_attention_norm.weight", N_EMBD)
+        q6(p + "attn_q.weight", N_EMBD, 2 * N_HEAD * HD)
+        q6(p + "attn_k.weight", N_EMBD, N_KV * HD)
+        q6(p + "attn_v.weight", N_EMBD, N_KV * HD)
+        q6(p + "attn_output.weight", N_HEAD * HD, N_EMBD)
+        vec(p + "attn_q_norm.weight", HD)
+        vec(p + "attn_k_norm.weight", HD)
+
+    def ffn(il):
+        p = f"blk.{il}."
+        q6(p + "ffn_up.weight", N_EMBD, N_FF)
+        q6(p + "ffn_gate.weight", N_EMBD, N_FF)
+        q6(p + "ffn_down.weight", N_FF, N_EMBD)
+
+    ch = (2 * H_K + H_V) * 128
+    n_layer = len(pattern)
+    for il in range(n_layer):
+        p = f"blk.{il}."
+        if pattern[il]:
+            attn(il)
+        else:
+            vec(p + "attn_norm.weight", N_EMBD)
+            vec(p + "post_attention_norm.weight", N_EMBD)
+            q6(p + "attn_qkv.weight", N_EMBD, ch)
+            q6(p + "attn_gate.weight", N_EMBD, H_V * 128)
+            q6(p + "ssm_beta.weight", N_EMBD, H_V)
+            q6(p + "ssm_alpha.weight", N_EMBD, H_V)
+            q6(p + "ssm_out.weight", H_V * 128, N_EMBD)
+            t[p + "ssm_conv1d.weight"] = (0, (4, ch), (0.5 * rng.standard_normal(4 * ch)).astype(np.float32))
+            vec(p + "ssm_dt.bias", H_V, 0.0, 0.3)
+            t[p + "ssm_a"] = (0, (H_V,), (-np.exp(0.5 * rng.standard_normal(H_V))).astype(np.float32))
+            vec(p + "ssm_norm.weight", 128)
+        ffn(il)
+    d = n_layer
+    attn(d)
+    ffn(d)
+    q6(f"blk.{d}.nextn.eh_proj.weight", 2 * N_EMBD, N_EMBD)
+    for w in ("enorm", "hnorm", "shared_head_norm"):
+        vec(f"blk.{d}.nextn.{w}.weight", N_EMBD)
+    meta = [("general.architecture", STR, "qwen35"), ("qwen35.block_count", U32, n_layer + 1),
+            ("qwen35.nextn_predict_layers", U32, 1), ("qwen35.attention.layer_norm_rms_epsilon", GF32, 1e-6),
+            ("qwen35.rope.freq_base", GF32, 1e7), ("qwen35.rope.dimension_count", U32, 64),
+            ("qwen35.embedding_length", U32, N_EMBD)]
+    if rope_factor:
+        meta += [("qwen35.rope.scaling.factor", GF32, rope_factor),
+                 ("qwen35.rope.scaling.original_context_length", U32, 4096)]
+    return t, meta
+
+
+def write(t, meta, path):
+    names = {0: "F32", 14: "Q6_K", 13: "Q5_K", 12: "Q4_K"}
+    return write_gguf(str(path), meta, [(n, names[tp], dims, data) for n, (tp, dims, data) in t.items()])
+
+
+def close(a, b, frac, what):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    err, scale = np.abs(a - b).max(), np.abs(b).max()
+    assert err <= frac * scale, f"{what}: max err {err:.3e} vs {frac} x {scale:.3e}"
+    return err
+
+
+def oracle_model(orc, t, n_layer, **kw):
+    import oracle.model as om
+    return om.Qwen35(t, n_layer, **kw)
+
+
+def check_rows(got, ref, row, exact_frac, bound, what):
+    """K/V rows: a fraction exact_frac within fp16 rounding (2e-3), every one within bound (relative to max|row|)"""
+    got, ref = got.reshape(-1, row), ref.reshape(-1, row)
+    rel = np.abs(got - ref).max(1) / np.maximum(np.abs(ref).max(1), 1e-30)
+    assert rel.max() <= bound, f"{what}: row errors {np.round(rel, 5)}"
+    assert (rel <= 2e-3).mean() >= exact_frac, f"{what}: row errors {np.round(rel, 5)}"
+
+
+@pytest.mark.parametrize("pattern,emb_type,rope_factor", [
+    ((0,), "Q6_K", None), ((1,), "Q5_K", 4.0), ((0,), "Q4_K", None), ((0, 0, 0, 1), "Q6_K", None)])
+def test_gguf_engine_matches_oracle_model(orc, E, tmp_path, pattern, emb_type, rope_factor):
+    n_layer = len(pattern)
+    bound, corr, row_bound, exact_frac = (1e-2, 0.9999, 3e-2, 0.8) if n_layer == 1 else (5e-2, 0.999, 6e-2, 0.0)
+    t, meta = build_model(orc, seed=3, emb_type=emb_type, rope_factor=rope_factor, pattern=pattern)
+    eng = E.Engine.from_gguf(write(t, meta, tmp_path / "m.gguf"), max_ctx=512)
+    c = eng.cfg
+    assert (c.n_embd, c.n_ff, c.n_vocab, c.n_layer, c.n_head, c.n_kv, c.head_dim, c.n_rot) == \
+        (N_EMBD, N_FF, N_VOCAB, n_layer, N_HEAD, N_KV, HD, 64)
+    if not all(pattern):
+        assert (c.ssm_h_k, c.ssm_h_v) == (H_K, H_V)
+    assert c.rope_factor == (rope_factor or 1.0)
+    m = oracle_model(orc, t, n_layer, rope_factor=rope_factor or 1.0, rope_orig_ctx=4096.0)
+    prompt = [int(x) for x in np.random.default_rng(9).integers(0, N_VOCAB, 7)]
+    first = eng.prefill(prompt, batch=1)
+    lo, h = m.prefill(prompt)
+    logits = eng.read(E.BUF_LOGITS, 0, 4 * N_VOCAB).view(np.float32)
+    close(logits, lo, bound, "logits")
+    assert np.corrcoef(logits, lo)[0, 1] > corr
+    close(eng.read(E.BUF_HIDDEN, 0, 4 * N_EMBD).view(np.float32), h, bound, "hidden")
+    top = np.sort(lo)[-2:]
+    if top[1] - top[0] > 2 * bound * np.abs(lo).max():
+        assert first == int(np.argmax(lo))
+    for il in range(n_layer):
+        if not pattern[il]:
+            st = eng.read(E.BUF_GDN_STATE, il, 4 * 128 * H_V * 128).view(np.float32)
+            close(st, m.state[il], bound, f"GDN state of layer {il}")
+    n = len(prompt) * N_KV * HD
+    for il in [i for i in range(n_layer) if pattern[i]] + [n_layer]:   # trunk attention layers and the draft block
+        for which, ref in ((E.BUF_K_CACHE, m.kc[il]), (E.BUF_V_CACHE, m.vc[il])):
+            got = eng.read(which, il, 2 * n).view(np.float16).astype(np.float64)
+            check_rows(got, ref[:n].view(np.float16).astype(np.float64), N_KV * HD, exact_frac, row_bound,
+                       f"cache {which} layer {il}")
+    # the chunked ingest of the same file leaves the same state
+    h1 = eng.read(E.BUF_HIDDEN, 0, 4 * N_EMBD)
+    assert eng.prefill(prompt, batch=16) == first
+    assert np.array_equal(eng.read(E.BUF_HIDDEN, 0, 4 * N_EMBD), h1)
+    eng.close()
+
+
+def test_gguf_engine_greedy_and_mtp_streams(orc, E, tmp_path):
+    """greedy tokens after the prompt follow the oracle model (while its top-2 margin is clear of the bound), and MTP
+    on the loaded model reproduces the greedy stream"""
+    t, meta = build_model(orc, seed=5)
+    eng = E.Engine.from_gguf(write(t, meta, tmp_path / "g.gguf"), max_ctx=512)
+    m = oracle_model(orc, t, N_LAYER)
+    prompt = [11, 222, 3333, 44]
+    first = eng.prefill(prompt, batch=4)
+    lo, h = m.prefill(prompt)
+    pos0, cur0 = eng.state()
+    eng.save_state()
+    toks, _ = eng.generate(12, mode=E.GREEDY)
+    stream = [first] + toks
+    checked = 0
+    for i in range(len(toks)):   # the oracle follows the engine's tokens; each clear-margin step must agree
+        lo, h = m.forward(stream[i], len(prompt) + i)
+        top = np.sort(lo)[-2:]
+        if top[1] - top[0] > 3e-2 * np.abs(lo).max():
+            assert stream[i + 1] == int(np.argmax(lo)), f"greedy token {i}"
+            checked += 1
+    assert checked >= 4, "too few tokens with a clear margin"
+    eng.restore_state(pos0, cur0)
+    mtp, st = eng.generate(12, mode=E.MTP)
+    assert mtp == toks
+    eng.close()

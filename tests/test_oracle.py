@@ -359,3 +359,72 @@ def test_beta_gate_and_norms(orc):
     p = orc.row_sum_partials(x)
     inv = orc.rms_inv(p, 4096, 1e-6)
     np.testing.assert_allclose(inv, 1 / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6), rtol=1e-13)
+
+
+# ---- K-quant token-embedding formats (qw:109-115; ggml dequantize_row_q4_K / q5_K) -------------------------------
+from tests.kquant import k_blocks, pack_k_scales  # noqa: E402
+
+@pytest.mark.parametrize("five_bit", [False, True])
+def test_k_quant_dequant_from_fields(orc, five_bit):
+    """every element = d * scale_j * q - dmin * min_j (both products exact in fp32, one rounding), for blocks packed
+    from their fields with ggml's packing rule: pins the 12-byte scale/min unpacking (including the high bits of
+    sub-blocks 4..7), the nibble order and, for Q5_K, the qh bit of each sub-block"""
+    rng = np.random.default_rng(11 + five_bit)
+    w, fields = k_blocks(rng, 6, five_bit)
+    assert w.size == 6 * (orc.Q5K_BYTES if five_bit else orc.Q4K_BYTES)
+    y = (orc.q5k_dequant if five_bit else orc.q4k_dequant)(w, 1, 6 * 256)
+    for b, (d, dmin, sc, mn, q) in enumerate(fields):
+        j = np.arange(256) // 32
+        want = (np.float64(d) * sc[j] * q - np.float64(dmin) * mn[j]).astype(np.float32)
+        assert np.array_equal(y[256 * b:256 * (b + 1)], want), f"block {b}"
+
+
+def test_k_quant_scale_unpacking_extremes(orc):
+    """all 6-bit scales / mins 63 (every high bit set) and 0, Q4_K: the unpacked values reach 63 in every slot"""
+    for val in (0, 63):
+        sc = np.full(8, val)
+        blk = np.concatenate([np.array([1.0, 1.0], np.float16).view(np.uint8), pack_k_scales(sc, sc),
+                              np.full(128, 0x11, np.uint8)])
+        y = orc.q4k_dequant(blk, 1, 256)
+        assert np.array_equal(y, np.full(256, val * 1.0 - val * 1.0, np.float32))
+        blk2 = blk.copy()
+        blk2[16:] = 0x32                                 # low nibble 2, high nibble 3
+        y2 = orc.q4k_dequant(blk2, 1, 256).reshape(4, 2, 32)
+        assert np.all(y2[:, 0] == 2 * val - val) and np.all(y2[:, 1] == 3 * val - val)
+
+
+# ---- YaRN RoPE (qw:1991-1999 parameters) ----------------------------------------------------------------------
+def test_rope_yarn_factor_one_is_plain_rope(orc):
+    x = orc.normal(4 * 256, seed=71).astype(np.float64)
+    for pos in (0, 1, 777, 200000):
+        a = orc.rope_yarn(x, 4, 256, 64, pos, 1e7, 1.0, 262144.0)
+        b = orc.rope_neox(x, 4, 256, 64, pos, 1e7)
+        assert np.allclose(a, b, rtol=0, atol=1e-12)
+
+
+def test_rope_yarn_limits(orc):
+    """ext_factor 0 is linear position interpolation (plain RoPE at pos / factor, unit magnitude); with ext_factor 1
+    the fastest-rotating pairs (i <= low) keep the extrapolated angle and the slowest (i >= high) take the interpolated
+    one, both scaled by 1 + 0.1 ln(factor)"""
+    hd, n_rot, base, factor, orig = 256, 64, 1e7, 4.0, 65536.0
+    x = orc.normal(hd, seed=72).astype(np.float64)
+    pos = 4 * 9001
+    pi_ = orc.rope_yarn(x, 1, hd, n_rot, pos, base, factor, orig, ext_factor=0.0)
+    assert np.allclose(pi_, orc.rope_neox(x, 1, hd, n_rot, pos // 4, base), rtol=0, atol=1e-10)
+    y = orc.rope_yarn(x, 1, hd, n_rot, pos, base, factor, orig)
+    m = 1 + 0.1 * np.log(factor)
+    corr = lambda b: n_rot * np.log(orig / (b * 2 * np.pi)) / (2 * np.log(base))  # noqa: E731
+    low, high = max(0, np.floor(corr(32.0))), min(n_rot - 1, np.ceil(corr(1.0)))
+    half = n_rot // 2
+    ext = orc.rope_neox(x, 1, hd, n_rot, pos, base)
+    interp = orc.rope_neox(x, 1, hd, n_rot, pos // 4, base)
+    for i in range(half):
+        pair = [i, i + half]
+        if i <= low:
+            assert np.allclose(y[pair], m * ext[pair], rtol=0, atol=1e-10), i
+        elif i >= high:
+            assert np.allclose(y[pair], m * interp[pair], rtol=0, atol=1e-10), i
+        # every pair is a rotation scaled by m
+        assert np.isclose(np.hypot(*y[pair]), m * np.hypot(*x[pair]), rtol=1e-12)
+    assert np.array_equal(y[n_rot:], x[n_rot:])
+    assert 0 < low < high < half, "the ramp covers interior dims for these parameters"
