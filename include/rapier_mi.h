@@ -87,8 +87,23 @@ int rmi_native_q8_0_mmvq_res(const void* w, const void* x_q8_1, float* y, const 
 int rmi_native_q8_0_mmvq_res_n(const void* w, const void* x_q8_1, float* y, const float* res, float* partials,
                                int n_in, int n_out, int ncols, void* stream);
 
-/* Type-dispatched GEMV (GGML type 14 = Q6_K, 8 = Q8_0; others RMI_ERR_UNSUPPORTED).  Replaces native_mmvq
- * (mmvq:3787-3818), including its split of more than 16 columns into passes. */
+/* Q4_K / Q5_K x Q8_1 GEMV, ncols 1..16, plain and with the residual + partials epilogue (the matrices of Q5_K_M
+ * files).  Replace native_q4_k_mmvq / native_q5_k_mmvq (mmvq:562-640, 185-300, 3587-3624, 3341-3379) and
+ * native_q4_k_mmvq_res / native_q5_k_mmvq_res (mmvq:3202-3324); the _res_n forms take ncols columns in one call.
+ * The matrix is 16-byte aligned (every GGUF row is: 144 and 176 bytes per block); n_in <= 52224. */
+int rmi_native_q4_k_mmvq(const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols, void* stream);
+int rmi_native_q5_k_mmvq(const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols, void* stream);
+int rmi_native_q4_k_mmvq_res(const void* w, const void* x_q8_1, float* y, const float* res, float* partials, int n_in,
+                             int n_out, void* stream);
+int rmi_native_q5_k_mmvq_res(const void* w, const void* x_q8_1, float* y, const float* res, float* partials, int n_in,
+                             int n_out, void* stream);
+int rmi_native_q4_k_mmvq_res_n(const void* w, const void* x_q8_1, float* y, const float* res, float* partials,
+                               int n_in, int n_out, int ncols, void* stream);
+int rmi_native_q5_k_mmvq_res_n(const void* w, const void* x_q8_1, float* y, const float* res, float* partials,
+                               int n_in, int n_out, int ncols, void* stream);
+
+/* Type-dispatched GEMV (GGML type 14 = Q6_K, 13 = Q5_K, 12 = Q4_K, 8 = Q8_0; others RMI_ERR_UNSUPPORTED).
+ * Replaces native_mmvq (mmvq:3787-3818), including its split of more than 16 columns into passes. */
 int rmi_native_mmvq(int ggml_type, const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                     void* stream);
 int rmi_native_mmvq_supported(int ggml_type);

@@ -61,6 +61,24 @@ inline void native_q8_0_mmvq_res(const void* w, const void* x_q8_1, float* y, co
                                  int n_in, int n_out, void* stream) {
     rmi_detail::check_mmvq(rmi_native_q8_0_mmvq_res(w, x_q8_1, y, res, partials, n_in, n_out, stream));
 }
+// mmvq:3587-3612, 3341-3366 (Q5_K_M matrices)
+inline void native_q4_k_mmvq(const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
+                             void* stream) {
+    rmi_detail::check_mmvq(rmi_native_q4_k_mmvq(w, x_q8_1, y, n_in, n_out, ncols, stream));
+}
+inline void native_q5_k_mmvq(const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
+                             void* stream) {
+    rmi_detail::check_mmvq(rmi_native_q5_k_mmvq(w, x_q8_1, y, n_in, n_out, ncols, stream));
+}
+// mmvq:3296-3324
+inline void native_q4_k_mmvq_res(const void* w, const void* x_q8_1, float* y, const float* res, float* partials,
+                                 int n_in, int n_out, void* stream) {
+    rmi_detail::check_mmvq(rmi_native_q4_k_mmvq_res(w, x_q8_1, y, res, partials, n_in, n_out, stream));
+}
+inline void native_q5_k_mmvq_res(const void* w, const void* x_q8_1, float* y, const float* res, float* partials,
+                                 int n_in, int n_out, void* stream) {
+    rmi_detail::check_mmvq(rmi_native_q5_k_mmvq_res(w, x_q8_1, y, res, partials, n_in, n_out, stream));
+}
 // mmvq:3787-3818
 inline void native_mmvq(int ggml_type, const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                         void* stream) {

@@ -48,6 +48,8 @@ _SIGS = {
     "orc_q8_0_block_dots": (None, [_u8p, _u8p, _i32p, _c.c_int, _c.c_int]),
     "orc_q6k_gemv": (None, [_u8p, _u8p, _c.c_void_p, _f64p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_int]),
     "orc_q8_0_gemv": (None, [_u8p, _u8p, _c.c_void_p, _f64p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_int]),
+    "orc_q4k_gemv": (None, [_u8p, _u8p, _c.c_void_p, _f64p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_int]),
+    "orc_q5k_gemv": (None, [_u8p, _u8p, _c.c_void_p, _f64p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_int]),
     "orc_q6k_gemv_f32_omp": (None, [_u8p, _u8p, _c.c_void_p, _f32p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_int,
                                      _c.c_int]),
     "orc_row_sum_partials": (None, [_f32p, _f64p, _c.c_int]),
@@ -190,6 +192,16 @@ def _gemv(fn, w, xq, n_in, n_out, ncols, res, want_partials):
 def q6k_gemv(w, xq, n_in, n_out, ncols=1, res=None, partials=False):
     """fp64 y = W x (+ res), per column; partials = sum of squares of each 4-row group."""
     return _gemv(lib().orc_q6k_gemv, w, xq, n_in, n_out, ncols, res, partials)
+
+
+def q4k_gemv(w, xq, n_in, n_out, ncols=1, res=None, partials=False):
+    """Q4_K x Q8_1 GEMV (mmvq:562-640) in exact integers + fp64"""
+    return _gemv(lib().orc_q4k_gemv, w, xq, n_in, n_out, ncols, res, partials)
+
+
+def q5k_gemv(w, xq, n_in, n_out, ncols=1, res=None, partials=False):
+    """Q5_K x Q8_1 GEMV (mmvq:185-300) in exact integers + fp64"""
+    return _gemv(lib().orc_q5k_gemv, w, xq, n_in, n_out, ncols, res, partials)
 
 
 def q8_0_gemv(w, xq, n_in, n_out, ncols=1, res=None, partials=False):

@@ -67,8 +67,8 @@ class Qwen35:
 
     def gemv(self, name, xq, res=None):
         tp, dims, data = self.t[name]
-        assert tp == 14, f"{name}: the oracle model applies Q6_K matrices"
-        y = orc.q6k_gemv(data, xq, dims[0], dims[1])
+        fn = {14: orc.q6k_gemv, 13: orc.q5k_gemv, 12: orc.q4k_gemv, 8: orc.q8_0_gemv}[tp]
+        y = fn(data, xq, dims[0], dims[1])
         return f32(y if res is None else y + res)
 
     def embed(self, tok):

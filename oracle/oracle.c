@@ -449,6 +449,54 @@ void orc_q8_0_gemv(const uint8_t* w, const uint8_t* xq, const float* res, double
     gemv_epilogue(res, y, partials, n_out, ncols);
 }
 
+/* Q4_K / Q5_K x Q8_1 GEMV (native_q4_k_mmvq / native_q5_k_mmvq, mmvq:562-640 and 185-300, with the residual
+ * epilogue of mmvq:3202-3294): per weight block and Q8_1 block j (32 elements, sub-block j of the 256-block), the
+ * exact integer dot sum(q u) and code sum sum(u) (vec_dot_q4_K/q5_K_q8_1_impl_vmmq's dot1 / dot2), then
+ * d * sc_j * d8_j * dot1 - dmin * m_j * d8_j * dot2, accumulated in fp64. */
+static void kquant_gemv(int five, const uint8_t* w, const uint8_t* xq, const float* res, double* y, double* partials,
+                        int n_in, int n_out, int ncols) {
+    const int nb = n_in / 256, bytes = five ? ORC_Q5K_BYTES : ORC_Q4K_BYTES;
+    for (int c = 0; c < ncols; ++c) {
+        const uint8_t* xc = xq + (size_t) c * (n_in / 32) * ORC_Q8_1_BYTES;
+#pragma omp parallel for schedule(static)
+        for (int r = 0; r < n_out; ++r) {
+            double acc = 0.0;
+            for (int bi = 0; bi < nb; ++bi) {
+                const uint8_t* b = w + ((size_t) r * nb + bi) * bytes;
+                const double d = f16_at(b), dmin = f16_at(b + 2);
+                const uint8_t* qh = b + 16;
+                const uint8_t* qs = b + (five ? 48 : 16);
+                for (int j = 0; j < 8; ++j) {
+                    int sc, m;
+                    k4_scale_min(b + 4, j, &sc, &m);
+                    const int8_t* u = q81_qs(xc, 8 * bi + j);
+                    int32_t dot = 0, su = 0;
+                    for (int l = 0; l < 32; ++l) {
+                        int q = (qs[32 * (j / 2) + l] >> (4 * (j & 1))) & 15;
+                        if (five) q |= ((qh[l] >> j) & 1) << 4;
+                        dot += q * (int) u[l];
+                        su += (int) u[l];
+                    }
+                    const double d8 = q81_d(xc, 8 * bi + j);
+                    acc += d * sc * d8 * (double) dot - dmin * m * d8 * (double) su;
+                }
+            }
+            y[(size_t) c * n_out + r] = acc;
+        }
+    }
+    gemv_epilogue(res, y, partials, n_out, ncols);
+}
+
+void orc_q4k_gemv(const uint8_t* w, const uint8_t* xq, const float* res, double* y, double* partials, int n_in,
+                  int n_out, int ncols) {
+    kquant_gemv(0, w, xq, res, y, partials, n_in, n_out, ncols);
+}
+
+void orc_q5k_gemv(const uint8_t* w, const uint8_t* xq, const float* res, double* y, double* partials, int n_in,
+                  int n_out, int ncols) {
+    kquant_gemv(1, w, xq, res, y, partials, n_in, n_out, ncols);
+}
+
 /* fp32 timing build of the same GEMV: per 256-block, decode to int8, integer dots per 16 elements, then the
  * fp32 accumulation d8 * (sc * dot) as in mmvq:642-655.  Threaded over rows. */
 void orc_q6k_gemv_f32_omp(const uint8_t* w, const uint8_t* xq, const float* res, float* y, float* partials,

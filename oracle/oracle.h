@@ -60,6 +60,12 @@ void orc_q6k_gemv(const uint8_t* w, const uint8_t* xq, const float* res, double*
                   int n_out, int ncols);
 void orc_q8_0_gemv(const uint8_t* w, const uint8_t* xq, const float* res, double* y, double* partials, int n_in,
                    int n_out, int ncols);
+/* Q4_K / Q5_K x Q8_1 GEMV (mmvq:185-300, 562-640, residual 3202-3294): exact integer sub-block dots and code sums,
+ * d*sc*d8*dot - dmin*m*d8*sum(u) in fp64 */
+void orc_q4k_gemv(const uint8_t* w, const uint8_t* xq, const float* res, double* y, double* partials, int n_in,
+                  int n_out, int ncols);
+void orc_q5k_gemv(const uint8_t* w, const uint8_t* xq, const float* res, double* y, double* partials, int n_in,
+                  int n_out, int ncols);
 /* same math in fp32, threaded (OpenMP), for the CPU timing baseline */
 void orc_q6k_gemv_f32_omp(const uint8_t* w, const uint8_t* xq, const float* res, float* y, float* partials,
                           int n_in, int n_out, int ncols, int threads);

@@ -32,6 +32,12 @@ SIGNATURES = {
     "rmi_native_q6_k_mmvq": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_res": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_res_n": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_native_q4_k_mmvq": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_native_q5_k_mmvq": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_native_q4_k_mmvq_res_n": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_native_q5_k_mmvq_res_n": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_native_q4_k_mmvq_res": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "rmi_native_q5_k_mmvq_res": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
     "rmi_q6_k_packed_bytes": (_sz, [_i, _i]),
     "rmi_q6_k_pack": (_i, [_vp, _vp, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_packed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
@@ -148,6 +154,18 @@ def native_q6_k_mmvq_res(w, x_q8_1, y, res, partials, n_in: int, n_out: int, str
 def native_q6_k_mmvq_res_n(w, x_q8_1, y, res, partials, n_in: int, n_out: int, ncols: int, stream=None):
     _call("rmi_native_q6_k_mmvq_res_n", _p(w), _p(x_q8_1), _p(y), _p(res), _p(partials), n_in, n_out, ncols,
           _stream(stream))
+
+
+def native_kquant_mmvq(ggml_type, w, x_q8_1, y, n_in: int, n_out: int, ncols: int = 1, stream=None):
+    """Q4_K (12) / Q5_K (13) x Q8_1 GEMV"""
+    name = {12: "rmi_native_q4_k_mmvq", 13: "rmi_native_q5_k_mmvq"}[ggml_type]
+    _call(name, _p(w), _p(x_q8_1), _p(y), n_in, n_out, ncols, _stream(stream))
+
+
+def native_kquant_mmvq_res_n(ggml_type, w, x_q8_1, y, res, partials, n_in: int, n_out: int, ncols: int = 1,
+                             stream=None):
+    name = {12: "rmi_native_q4_k_mmvq_res_n", 13: "rmi_native_q5_k_mmvq_res_n"}[ggml_type]
+    _call(name, _p(w), _p(x_q8_1), _p(y), _p(res), _p(partials), n_in, n_out, ncols, _stream(stream))
 
 
 def q6_k_packed_bytes(n_in: int, n_out: int) -> int:

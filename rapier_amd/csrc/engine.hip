@@ -56,11 +56,17 @@ size_t q81_bytes(int n) { return static_cast<size_t>(n / 32) * kQ8_1Bytes; }
 // conv history of one GDN layer, per value head: [h_v][q 128 | k 128 | v 128][3]
 size_t hist_floats(const rmi_model_config& c) { return static_cast<size_t>(c.ssm_h_v) * 3 * kS * 3; }
 
-// A Q6_K matrix: the packed wave-tiled copy when n_in is a multiple of 2048 (every 9B matrix), else GGUF blocks.
+// A matrix of GGML type 14 (Q6_K: the packed wave-tiled copy when n_in is a multiple of 2048, every 9B matrix, else
+// GGUF blocks), 13 (Q5_K), 12 (Q4_K) or 8 (Q8_0), in GGUF blocks.  A group whose parts differ in type (a Q5_K_M file's
+// qkv | z | beta | alpha, say) keeps its parts: the GEMV then runs per part and per column into the group's rows, the
+// reference's mm_q2_group fallback (qw:1284-1309).
 struct Mat {
     uint8_t* w = nullptr;
     int n_in = 0, n_out = 0;
+    int type = 14;
     bool packed = false;
+    size_t bytes = 0;            // GGUF bytes of the matrix (the weight pass it costs)
+    std::vector<Mat> parts;      // non-empty: a mixed-type group
 };
 
 struct Layer {
@@ -278,6 +284,8 @@ int make_mat(Engine& e, Mat& m, int n_out, int n_in, uint64_t seed) {
         return !(v && v[0] == '0');
     }();
     m.packed = use_packed && n_in % 2048 == 0;
+    m.type = 14;
+    m.bytes = q6_bytes(n_out, n_in);
     if (!m.packed) {
         RMI_TRY(e.alloc(&m.w, q6_bytes(n_out, n_in)));
         return rmi_gen_q6_k(m.w, static_cast<size_t>(n_out) * (n_in / 256), seed, 1e-3f, e.s);
@@ -291,13 +299,30 @@ int make_mat(Engine& e, Mat& m, int n_out, int n_in, uint64_t seed) {
 }
 
 int gemv(Engine& e, const Mat& m, const uint8_t* xq, float* y, int nc) {
+    if (!m.parts.empty()) {   // mixed-type group: each part, each column, into its rows (qw:1296-1308)
+        const size_t xcol = q81_bytes(m.n_in);
+        for (int c = 0; c < nc; ++c) {
+            int off = 0;
+            for (const Mat& p : m.parts) {
+                RMI_TRY(gemv(e, p, xq + c * xcol, y + static_cast<size_t>(c) * m.n_out + off, 1));
+                off += p.n_out;
+            }
+        }
+        return RMI_OK;
+    }
     if (m.packed) return rmi_native_q6_k_mmvq_packed(m.w, xq, y, m.n_in, m.n_out, nc, e.s);
-    return rmi_native_q6_k_mmvq(m.w, xq, y, m.n_in, m.n_out, nc, e.s);
+    return rmi_native_mmvq(m.type, m.w, xq, y, m.n_in, m.n_out, nc, e.s);
 }
 
 int gemv_res(Engine& e, const Mat& m, const uint8_t* xq, float* x, float* part, int nc) {
     if (m.packed) return rmi_native_q6_k_mmvq_packed_res_n(m.w, xq, x, x, part, m.n_in, m.n_out, nc, e.s);
-    return rmi_native_q6_k_mmvq_res_n(m.w, xq, x, x, part, m.n_in, m.n_out, nc, e.s);
+    switch (m.type) {
+        case 14: return rmi_native_q6_k_mmvq_res_n(m.w, xq, x, x, part, m.n_in, m.n_out, nc, e.s);
+        case 13: return rmi_native_q5_k_mmvq_res_n(m.w, xq, x, x, part, m.n_in, m.n_out, nc, e.s);
+        case 12: return rmi_native_q4_k_mmvq_res_n(m.w, xq, x, x, part, m.n_in, m.n_out, nc, e.s);
+        case 8: return rmi_native_q8_0_mmvq_res_n(m.w, xq, x, x, part, m.n_in, m.n_out, nc, e.s);
+        default: return fail(RMI_ERR_UNSUPPORTED, "engine: residual GEMV of an unsupported type");
+    }
 }
 
 int make_vec(Engine& e, float** p, size_t n, uint64_t seed, float mean, float std) {
@@ -702,34 +727,49 @@ struct Uploader {
     }
 };
 
-// rows of the named Q6_K tensors, concatenated in order (the reference's try_cat groups, qw:2082-2087), into one engine
-// matrix: packed when n_in % 2048 == 0, else kept in GGUF blocks
+// rows of the named tensors, concatenated in order (the reference's try_cat groups, qw:2082-2087), into one engine
+// matrix when every part has the same type (Q6_K packed when n_in % 2048 == 0, else GGUF blocks); a group whose parts
+// differ in type keeps them as parts (try_cat leaves such a group unfused, qw:1284-1288)
 int load_mat(Engine& e, Uploader& up, const rmi_gguf* g, Mat& m, std::initializer_list<std::string> names) {
-    int n_in = -1, n_out = 0;
+    int n_in = -1, n_out = 0, type = -1;
+    bool mixed = false;
     std::vector<GTensor> parts;
     for (const auto& nm : names) {
         GTensor t;
         RMI_TRY(need_tensor(g, nm, &t));
-        if (t.type != 14 || t.n_dims != 2) return fail(RMI_ERR_UNSUPPORTED, ("gguf: " + nm + " is not a Q6_K matrix").c_str());
+        if (t.n_dims != 2 || !rmi_native_mmvq_supported(t.type))
+            return fail(RMI_ERR_UNSUPPORTED, ("gguf: " + nm + " is not a Q6_K / Q5_K / Q4_K / Q8_0 matrix").c_str());
         if (n_in >= 0 && t.dims[0] != n_in) return fail(RMI_ERR_SHAPE, ("gguf: " + nm + " has another row length").c_str());
+        if (type >= 0 && t.type != type) mixed = true;
         n_in = static_cast<int>(t.dims[0]);
         n_out += static_cast<int>(t.dims[1]);
+        type = t.type;
         parts.push_back(t);
     }
     m.n_in = n_in;
     m.n_out = n_out;
+    m.bytes = 0;
+    for (const auto& t : parts) m.bytes += t.bytes;
+    if (mixed) {
+        for (const auto& nm : names) {
+            Mat p;
+            RMI_TRY(load_mat(e, up, g, p, {nm}));
+            m.parts.push_back(std::move(p));
+        }
+        return RMI_OK;
+    }
+    m.type = type;
     static const bool use_packed = [] {
         const char* v = std::getenv("RMI_ENGINE_PACKED");
         return !(v && v[0] == '0');
     }();
-    m.packed = use_packed && n_in % 2048 == 0;
-    const size_t gguf = q6_bytes(n_out, n_in);
+    m.packed = type == 14 && use_packed && n_in % 2048 == 0;
     uint8_t* dst = nullptr;
     if (m.packed) {
-        if (gguf > e.gen_tmp_bytes) return fail(RMI_ERR_STATE, "engine: generation buffer too small");
+        if (m.bytes > e.gen_tmp_bytes) return fail(RMI_ERR_STATE, "engine: generation buffer too small");
         dst = e.gen_tmp;
     } else {
-        RMI_TRY(e.alloc(&m.w, gguf));
+        RMI_TRY(e.alloc(&m.w, m.bytes));
         dst = m.w;
     }
     size_t off = 0;
@@ -991,13 +1031,10 @@ extern "C" int rmi_engine_info(const rmi_engine* h, rmi_engine_info_t* info) {
     const Engine& e = h->e;
     const auto& c = e.cfg;
     size_t trunk = 0;
-    for (const auto& L : e.layers)
-        trunk += q6_bytes(L.in_proj.n_out, L.in_proj.n_in) + q6_bytes(L.out_proj.n_out, L.out_proj.n_in) +
-                 q6_bytes(L.upgate.n_out, L.upgate.n_in) + q6_bytes(L.down.n_out, L.down.n_in);
-    const size_t head = q6_bytes(c.n_vocab, c.n_embd);
-    const size_t dblk = q6_bytes(e.eh_proj.n_out, e.eh_proj.n_in) + q6_bytes(e.draft.in_proj.n_out, e.draft.in_proj.n_in) +
-                        q6_bytes(e.draft.out_proj.n_out, e.draft.out_proj.n_in) +
-                        q6_bytes(e.draft.upgate.n_out, e.draft.upgate.n_in) + q6_bytes(e.draft.down.n_out, e.draft.down.n_in);
+    for (const auto& L : e.layers) trunk += L.in_proj.bytes + L.out_proj.bytes + L.upgate.bytes + L.down.bytes;
+    const size_t head = e.lm_head.bytes;
+    const size_t dblk = e.eh_proj.bytes + e.draft.in_proj.bytes + e.draft.out_proj.bytes + e.draft.upgate.bytes +
+                        e.draft.down.bytes;
     info->trunk_weight_bytes = trunk;
     info->lm_head_bytes = head;
     info->draft_block_bytes = dblk;

@@ -128,11 +128,15 @@ extern "C" int rmi_native_q8_0_mmvq_res(const void* w, const void* x_q8_1, float
     return rmi_native_q8_0_mmvq_res_n(w, x_q8_1, y, res, partials, n_in, n_out, 1, stream);
 }
 
-extern "C" int rmi_native_mmvq_supported(int ggml_type) { return ggml_type == 14 || ggml_type == 8; }
+extern "C" int rmi_native_mmvq_supported(int ggml_type) {
+    return ggml_type == 14 || ggml_type == 13 || ggml_type == 12 || ggml_type == 8;
+}
 
 extern "C" size_t rmi_native_mmvq_weight_bytes(int ggml_type, int n_in, int n_out) {
     int elems, bytes;
     if (ggml_type == 14) { elems = 256; bytes = kQ6KBytes; }
+    else if (ggml_type == 13) { elems = 256; bytes = 176; }
+    else if (ggml_type == 12) { elems = 256; bytes = 144; }
     else if (ggml_type == 8) { elems = 32; bytes = kQ8_0Bytes; }
     else { set_error("unsupported native MMVQ GGML type"); return 0; }
     if (n_in <= 0 || n_in % elems != 0 || n_out <= 0) {
@@ -143,6 +147,8 @@ extern "C" size_t rmi_native_mmvq_weight_bytes(int ggml_type, int n_in, int n_ou
 }
 
 extern "C" int rmi_native_q6_k_mmvq(const void*, const void*, float*, int, int, int, void*);
+extern "C" int rmi_native_q5_k_mmvq(const void*, const void*, float*, int, int, int, void*);
+extern "C" int rmi_native_q4_k_mmvq(const void*, const void*, float*, int, int, int, void*);
 
 extern "C" int rmi_native_mmvq(int ggml_type, const void* w, const void* x_q8_1, float* y, int n_in, int n_out,
                                int ncols, void* stream) {
@@ -158,6 +164,8 @@ extern "C" int rmi_native_mmvq(int ggml_type, const void* w, const void* x_q8_1,
         return RMI_OK;
     }
     if (ggml_type == 14) return rmi_native_q6_k_mmvq(w, x_q8_1, y, n_in, n_out, ncols, stream);
+    if (ggml_type == 13) return rmi_native_q5_k_mmvq(w, x_q8_1, y, n_in, n_out, ncols, stream);
+    if (ggml_type == 12) return rmi_native_q4_k_mmvq(w, x_q8_1, y, n_in, n_out, ncols, stream);
     if (ggml_type == 8) return rmi_native_q8_0_mmvq(w, x_q8_1, y, n_in, n_out, ncols, stream);
     return fail(RMI_ERR_UNSUPPORTED, "unsupported native MMVQ GGML type");
 }

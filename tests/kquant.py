@@ -18,12 +18,12 @@ def pack_k_scales(sc, mn):
     return s
 
 
-def k_blocks(rng, nblocks, five_bit):
+def k_blocks(rng, nblocks, five_bit, d_std=1e-2):
     """random K-quant blocks from their fields, and the fields"""
     out, fields = [], []
     for _ in range(nblocks):
-        d = np.float16(rng.normal(0, 1e-2))
-        dmin = np.float16(abs(rng.normal(0, 1e-2)))
+        d = np.float16(rng.normal(0, d_std))
+        dmin = np.float16(abs(rng.normal(0, d_std)))
         sc = rng.integers(0, 64, 8)
         mn = rng.integers(0, 64, 8)
         q = rng.integers(0, 32 if five_bit else 16, 256)                 # element e -> code

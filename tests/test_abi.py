@@ -58,14 +58,17 @@ def test_gemv_pointer_and_stream_validation(rmi):
 
 def test_type_dispatch(rmi):
     L = rmi.lib()
-    assert L.rmi_native_mmvq_supported(14) and L.rmi_native_mmvq_supported(8)
-    assert not L.rmi_native_mmvq_supported(12)
+    for t in (14, 13, 12, 8):
+        assert L.rmi_native_mmvq_supported(t)
+    assert not L.rmi_native_mmvq_supported(11) and not L.rmi_native_mmvq_supported(23)   # Q3_K, IQ4_XS
     with pytest.raises(ValueError, match="unsupported"):
-        rmi._call("rmi_native_mmvq", 12, FAKE, FAKE, FAKE, 256, 4, 1, FAKE)
+        rmi._call("rmi_native_mmvq", 11, FAKE, FAKE, FAKE, 256, 4, 1, FAKE)
     L.rmi_native_mmvq_weight_bytes.restype = ctypes.c_size_t
     L.rmi_native_mmvq_weight_bytes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
     assert L.rmi_native_mmvq_weight_bytes(14, 4096, 12288) == 41_287_680
     assert L.rmi_native_mmvq_weight_bytes(8, 4096, 10) == 10 * 128 * 34
+    assert L.rmi_native_mmvq_weight_bytes(13, 4096, 10) == 10 * 16 * 176
+    assert L.rmi_native_mmvq_weight_bytes(12, 4096, 10) == 10 * 16 * 144
     assert L.rmi_native_mmvq_weight_bytes(14, 100, 10) == 0
 
 

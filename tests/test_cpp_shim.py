@@ -22,15 +22,17 @@ PROGRAM = textwrap.dedent(r"""
         catch (const std::invalid_argument& e) { caught += std::strstr(e.what(), "divisible") != nullptr; }
         try { strata::kernels::native_q6_k_mmvq(fake, fake, (float*) fake, 256, 4, 1, nullptr); }
         catch (const std::invalid_argument& e) { caught += std::strstr(e.what(), "stream") != nullptr; }
-        try { strata::kernels::native_mmvq(12, fake, fake, (float*) fake, 256, 4, 1, fake); }
+        try { strata::kernels::native_mmvq(11, fake, fake, (float*) fake, 256, 4, 1, fake); }
         catch (const std::invalid_argument& e) { caught += std::strstr(e.what(), "unsupported") != nullptr; }
         try { (void) strata::kernels::native_q8_1_bytes(31, 1); }
         catch (const std::invalid_argument&) { caught += 1; }
+        try { strata::kernels::native_q5_k_mmvq(fake, fake, (float*) fake, 100, 4, 1, fake); }
+        catch (const std::invalid_argument& e) { caught += std::strstr(e.what(), "divisible") != nullptr; }
         const bool ok = strata::kernels::native_q8_1_bytes(4096, 2) == 9216 &&
                         strata::kernels::native_mmvq_weight_bytes(14, 4096, 12288) == 41287680u &&
                         rmi_qwen35_9b_config().n_vocab == 248320;
         std::printf("%d %d\n", caught, ok ? 1 : 0);
-        return caught == 4 && ok ? 0 : 1;
+        return caught == 5 && ok ? 0 : 1;
     }
 """)
 
@@ -47,4 +49,4 @@ def test_cpp_shim_compiles_and_throws(tmp_path):
                     f"-Wl,-rpath,{os.path.dirname(lib)}", "-o", str(exe)], check=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert r.stdout.split() == ["4", "1"]
+    assert r.stdout.split() == ["5", "1"]

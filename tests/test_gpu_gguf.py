@@ -35,9 +35,17 @@ def E():
     return eng
 
 
-def build_model(orc, seed=1, emb_type="Q6_K", rope_factor=None, pattern=(0, 0, 0, 1)):
+# a Q5_K_M-like type plan: matrix name suffix -> GGML type (others Q6_K).  qkv | gate | beta | alpha and q | k | v mix
+# types (the per-part fallback), up | gate share Q5_K (one concatenated K-quant GEMV), ssm_out / attn_output / down
+# are K-quant and Q8_0 residual GEMVs
+MIXED = {"attn_qkv.weight": 13, "ssm_beta.weight": 8, "ssm_alpha.weight": 8, "ssm_out.weight": 12,
+         "attn_q.weight": 13, "attn_k.weight": 13, "attn_output.weight": 12, "ffn_up.weight": 13,
+         "ffn_gate.weight": 13, "ffn_down.weight": 8, "nextn.eh_proj.weight": 12}
+
+
+def build_model(orc, seed=1, emb_type="Q6_K", rope_factor=None, pattern=(0, 0, 0, 1), mixed=False):
     """tensors name -> (ggml type, dims, data) with the reference's names (qw:2003-2127); pattern[il] = 1 for an
-    attention layer"""
+    attention layer; mixed: the MIXED type plan"""
     from tests.kquant import k_blocks
     rng = np.random.default_rng(seed)
     t = {}
@@ -45,7 +53,14 @@ def build_model(orc, seed=1, emb_type="Q6_K", rope_factor=None, pattern=(0, 0, 0
 
     def q6(name, n_in, n_out):
         cnt[0] += 1
-        t[name] = (14, (n_in, n_out), orc.gen_q6k(n_out, n_in, seed=seed * 1000 + cnt[0]))
+        tp = next((v for k, v in MIXED.items() if name.endswith(k)), 14) if mixed else 14
+        if tp == 14:
+            data = orc.gen_q6k(n_out, n_in, seed=seed * 1000 + cnt[0])
+        elif tp == 8:
+            data = orc.gen_q8_0(n_out, n_in, seed=seed * 1000 + cnt[0], d_std=3e-3)
+        else:
+            data, _ = k_blocks(np.random.default_rng(seed * 1000 + cnt[0]), n_out * n_in // 256, tp == 13, d_std=2e-3)
+        t[name] = (tp, (n_in, n_out), data)
 
     def vec(name, n, mean=1.0, std=0.1):
         t[name] = (0, (n,), (mean + std * rng.standard_normal(n)).astype(np.float32))
@@ -112,7 +127,7 @@ def build_model(orc, seed=1, emb_type="Q6_K", rope_factor=None, pattern=(0, 0, 0
 
 
 def write(t, meta, path):
-    names = {0: "F32", 14: "Q6_K", 13: "Q5_K", 12: "Q4_K"}
+    names = {0: "F32", 14: "Q6_K", 13: "Q5_K", 12: "Q4_K", 8: "Q8_0"}
     return write_gguf(str(path), meta, [(n, names[tp], dims, data) for n, (tp, dims, data) in t.items()])
 
 
@@ -136,12 +151,15 @@ def check_rows(got, ref, row, exact_frac, bound, what):
     assert (rel <= 2e-3).mean() >= exact_frac, f"{what}: row errors {np.round(rel, 5)}"
 
 
-@pytest.mark.parametrize("pattern,emb_type,rope_factor", [
-    ((0,), "Q6_K", None), ((1,), "Q5_K", 4.0), ((0,), "Q4_K", None), ((0, 0, 0, 1), "Q6_K", None)])
-def test_gguf_engine_matches_oracle_model(orc, E, tmp_path, pattern, emb_type, rope_factor):
+@pytest.mark.parametrize("pattern,emb_type,rope_factor,mixed", [
+    ((0,), "Q6_K", None, False), ((1,), "Q5_K", 4.0, False), ((0,), "Q4_K", None, False),
+    ((0, 0, 0, 1), "Q6_K", None, False), ((0,), "Q5_K", None, True), ((1,), "Q6_K", None, True),
+    ((0, 0, 0, 1), "Q5_K", None, True)])
+def test_gguf_engine_matches_oracle_model(orc, E, tmp_path, pattern, emb_type, rope_factor, mixed):
+    """mixed: a Q5_K_M-like file - Q5_K / Q4_K / Q8_0 / Q6_K matrices, groups of mixed type on the per-part fallback"""
     n_layer = len(pattern)
     bound, corr, row_bound, exact_frac = (1e-2, 0.9999, 3e-2, 0.8) if n_layer == 1 else (5e-2, 0.999, 6e-2, 0.0)
-    t, meta = build_model(orc, seed=3, emb_type=emb_type, rope_factor=rope_factor, pattern=pattern)
+    t, meta = build_model(orc, seed=3, emb_type=emb_type, rope_factor=rope_factor, pattern=pattern, mixed=mixed)
     eng = E.Engine.from_gguf(write(t, meta, tmp_path / "m.gguf"), max_ctx=512)
     c = eng.cfg
     assert (c.n_embd, c.n_ff, c.n_vocab, c.n_layer, c.n_head, c.n_kv, c.head_dim, c.n_rot) == \

@@ -428,3 +428,20 @@ def test_rope_yarn_limits(orc):
         assert np.isclose(np.hypot(*y[pair]), m * np.hypot(*x[pair]), rtol=1e-12)
     assert np.array_equal(y[n_rot:], x[n_rot:])
     assert 0 < low < high < half, "the ramp covers interior dims for these parameters"
+
+
+@pytest.mark.parametrize("five_bit", [False, True])
+def test_k_quant_gemv_matches_dequant_matmul(orc, five_bit):
+    """the integer-dot GEMV equals the fp64 product of the dequantized weights (pinned above) and the dequantized
+    Q8_1 activations: the min term must use the code sum of exactly the sub-block's 32 activations.  Each dequantized
+    weight is one fp32 rounding of its exact value, so the bound is 2^-24 of sum |w x| per output."""
+    from tests.kquant import k_blocks
+    n_in, n_out, ncols = 768, 9, 2
+    w, _ = k_blocks(np.random.default_rng(31 + five_bit), n_out * n_in // 256, five_bit)
+    xq = orc.quantize_q8_1(orc.normal(ncols * n_in, seed=32), n_in, ncols)
+    y = (orc.q5k_gemv if five_bit else orc.q4k_gemv)(w, xq, n_in, n_out, ncols=ncols)
+    wd = (orc.q5k_dequant if five_bit else orc.q4k_dequant)(w, n_out, n_in).reshape(n_out, n_in).astype(np.float64)
+    xd = orc.dequantize_q8_1(xq, ncols * n_in).reshape(ncols, n_in).astype(np.float64)
+    bound = 2.0 ** -24 * (np.abs(xd) @ np.abs(wd).T) * 1.01
+    assert np.all(np.abs(y.reshape(ncols, n_out) - xd @ wd.T) <= bound)
+    assert np.abs(y).max() > 1e3 * bound.max(), "a nontrivial product"
