@@ -147,6 +147,11 @@ int rmi_beta_gate(float* beta_alpha, const float* dt, const float* ssm_a, float*
  * Replaces argmax_kernel / serve_argmax_dev (qw:70-94) and the host scan (qw:3199-3205), without the memset. */
 size_t rmi_argmax_workspace_bytes(int ncols);
 int rmi_argmax(const float* logits, int n, int ncols, int col_stride, int* out_idx, void* workspace, void* stream);
+/* the k largest of n logits (k <= 64, n <= 1048576) with their ids, logit descending, lower id first among equal
+ * logits (-0 equals +0): out_idx[k] and out_val[k] on the device; workspace of rmi_topk_workspace_bytes(n) bytes.
+ * Replaces topk_out's host scan (qw:2513-2531) and the 1 MB logits copy before it (qw:1800-1803). */
+size_t rmi_topk_workspace_bytes(int n);
+int rmi_topk(const float* logits, int n, int k, int* out_idx, float* out_val, void* workspace, void* stream);
 /* Device-resident token embedding: x[c] = dequant(row tokens[c]) of a GGUF type 14 (Q6_K), 13 (Q5_K) or 12 (Q4_K)
  * table, partials of each row (4 elements per slot).  Replaces the host dequant + H2D copy of emb_dequant_block
  * (qw:109-115, 1418-1430); Q3_K and IQ4_XS tables are RMI_ERR_UNSUPPORTED. */

@@ -88,6 +88,47 @@ int rmi_engine_restore_state(rmi_engine* e, int pos, int cur_token);
 int rmi_engine_state(rmi_engine* e, int* pos, int* cur_token);
 int rmi_engine_generate(rmi_engine* e, const rmi_gen_request* req, int* out_tokens, rmi_gen_stats* stats);
 
+/* ---- serving: the context continues across calls (serve_loop, qw:2593-2813) ---- */
+/* empty context at position 0 (the serve reset, qw:2533-2549) */
+int rmi_engine_reset(rmi_engine* e);
+/* feed n tokens at the current position (batch as in rmi_engine_prefill_batch; the same state bit for bit);
+ * *first_out = the greedy token after them (the current token).  rmi_engine_prefill_batch = reset + ingest. */
+int rmi_engine_ingest(rmi_engine* e, const int* tokens, int n, int batch, int* first_out);
+/* token-at-a-time generation from the current token: gen_begin(RMI_GEN_GREEDY or RMI_GEN_MTP), then each gen_step
+ * runs one greedy forward (out[0] = the next token; the current one is fed) or one verify round (out[0] = c0, and
+ * out[1] = c1 when the draft was accepted; *n_out = 1 or 2).  Any call that replaces the context ends the stream. */
+int rmi_engine_gen_begin(rmi_engine* e, int mode);
+int rmi_engine_gen_step(rmi_engine* e, int* out_tokens, int* n_out);
+/* the k (1..64) largest logits of column col (0 or 1) of the last head pass, with their ids (rmi_topk order).  Column 0
+ * after an ingest or a greedy step: the logits that chose the current token (topk_out, qw:2513-2531). */
+int rmi_engine_topk(rmi_engine* e, int col, int k, int* ids, float* logits);
+
+/* The --serve JSON-lines protocol (qw:2139-2148, serve_loop qw:2593-2813): reads requests from in_fd until end of input,
+ * writes one response line each to out_fd.  Requests: {"op":"reset"}, {"op":"run","tokens":[..],"gen":N,"mtp":B}
+ * (optional "topk":K, 0..64).  Responses: {"ok":true,"op":"reset"}; per generated token {"id":I,"top":[[id,logit],..]}
+ * (%.5f logits; with mtp only the first token carries its list); {"done":true,"pos":P}; {"error":"..."}.
+ * Returns RMI_OK at end of input, or the code of a device failure after its error line. */
+typedef struct rmi_serve_options {
+    int eos;     /* generation stops after this id: 248046, the qwen35 end-of-turn id the reference compares */
+    int batch;   /* ingest chunk, 1..16 (16) */
+    int topk;    /* list length when a request names none (40) */
+} rmi_serve_options;
+/* the engine behind the protocol, as function pointers (a test can drive the loop with its own backend) */
+typedef struct rmi_serve_backend {
+    void* user;
+    int max_ctx;
+    int (*reset)(void* user);
+    int (*ingest)(void* user, const int* tokens, int n, int batch, int* first);
+    int (*topk)(void* user, int k, int* ids, float* logits);
+    int (*gen_begin)(void* user, int mode);
+    int (*gen_step)(void* user, int* out_tokens, int* n_out);
+    int (*position)(void* user, int* pos);
+    const char* (*error)(void* user);   /* message of the last failure (may be NULL) */
+} rmi_serve_backend;
+rmi_serve_options rmi_serve_default_options(void);
+int rmi_serve_fd(const rmi_serve_backend* b, const rmi_serve_options* o, int in_fd, int out_fd);
+int rmi_serve_engine(rmi_engine* e, const rmi_serve_options* o, int in_fd, int out_fd);
+
 /* ---- GGUF (v2 / v3) files: the reader the engine loads through (the role of strata::GgufFile, qw:945-957,
  * 1978-2134).  Tensors are memory-mapped; dims[0] is the innermost dimension (n_in of a matrix). ---- */
 typedef struct rmi_gguf rmi_gguf;

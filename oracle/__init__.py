@@ -66,6 +66,7 @@ _SIGS = {
     "orc_rope_neox": (None, [_f64p, _f64p, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_double]),
     "orc_rope_yarn": (None, [_f64p, _f64p, _c.c_int, _c.c_int, _c.c_int, _c.c_int] + [_c.c_double] * 7),
     "orc_argmax": (_c.c_int, [_f32p, _c.c_int]),
+    "orc_topk": (_c.c_int, [_f32p, _c.c_int, _c.c_int, _i32p, _f32p]),
 }
 
 
@@ -313,3 +314,19 @@ def rope_yarn(x, heads, hd, n_rot, pos, base, factor, orig_ctx, ext_factor=1.0, 
 def argmax(l):
     l = np.ascontiguousarray(l, dtype=np.float32)
     return lib().orc_argmax(l, l.size)
+
+
+def topk(l, k):
+    """topk_out (qw:2513-2531) restated in C: [(id, logit)] of the k largest logits, descending"""
+    l = np.ascontiguousarray(l, dtype=np.float32)
+    ids = np.zeros(k, np.int32)
+    vals = np.zeros(k, np.float32)
+    m = lib().orc_topk(l, l.size, k, ids, vals)
+    return list(zip(ids[:m].tolist(), vals[:m].tolist()))
+
+
+def topk_sorted(l, k):
+    """the same list by a full sort: logit descending, then id ascending (-0 equal to +0)"""
+    l = np.asarray(l, dtype=np.float32)
+    order = np.lexsort((np.arange(l.size), -(l.astype(np.float64) + 0.0)))[:k]
+    return [(int(i), float(l[i])) for i in order]

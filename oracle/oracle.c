@@ -728,3 +728,46 @@ int orc_argmax(const float* l, int n) {
         if (l[i] > l[best]) best = i;
     return best;
 }
+
+/* topk_out (qw:2513-2531) restated: scan the logits once; the first k fill the list, which is then sorted by logit,
+ * descending; afterwards a logit strictly greater than the list's last replaces it and moves up past every strictly
+ * smaller entry.  The reference sorts the first k with std::sort, which leaves the order of equal logits among them
+ * unspecified; this restatement sorts them stably (lower id first), the order the rest of the scan gives equal logits.
+ * With n < k the list is never sorted (as in the reference) and holds the n logits in id order. */
+int orc_topk(const float* l, int n, int k, int* ids, float* vals) {
+    int m = 0;
+    for (int i = 0; i < n; ++i) {
+        if (m < k) {
+            ids[m] = i;
+            vals[m] = l[i];
+            ++m;
+            if (m == k) {   /* stable insertion sort, descending */
+                for (int a = 1; a < k; ++a) {
+                    const int id = ids[a];
+                    const float v = vals[a];
+                    int b = a;
+                    while (b > 0 && v > vals[b - 1]) {
+                        ids[b] = ids[b - 1];
+                        vals[b] = vals[b - 1];
+                        --b;
+                    }
+                    ids[b] = id;
+                    vals[b] = v;
+                }
+            }
+        } else if (l[i] > vals[k - 1]) {
+            int j = k - 1;
+            ids[j] = i;
+            vals[j] = l[i];
+            for (; j > 0 && vals[j] > vals[j - 1]; --j) {
+                const int ti = ids[j];
+                const float tv = vals[j];
+                ids[j] = ids[j - 1];
+                vals[j] = vals[j - 1];
+                ids[j - 1] = ti;
+                vals[j - 1] = tv;
+            }
+        }
+    }
+    return m;
+}

@@ -97,6 +97,9 @@ void orc_rope_yarn(const double* x, double* out, int heads, int hd, int n_rot, i
 /* ---- argmax, lowest index wins ties (qw:70-94) ---- */
 int orc_argmax(const float* l, int n);
 
+/* ---- top-k list of the serve protocol (topk_out, qw:2513-2531): returns the entries written (min(n, k)) ---- */
+int orc_topk(const float* l, int n, int k, int* ids, float* vals);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,8 @@ SIGNATURES = {
     "rmi_beta_gate": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_argmax_workspace_bytes": (_sz, [_i]),
     "rmi_argmax": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
+    "rmi_topk_workspace_bytes": (_sz, [_i]),
+    "rmi_topk": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
     "rmi_embed_q6_k": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_embed": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_fused_gdn_conv_l2": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
@@ -253,6 +255,15 @@ def argmax_workspace_bytes(ncols):
 def argmax(logits, n, out_idx, workspace, ncols=1, col_stride=None, stream=None):
     _call("rmi_argmax", _p(logits), n, ncols, n if col_stride is None else col_stride, _p(out_idx), _p(workspace),
           _stream(stream))
+
+
+def topk_workspace_bytes(n):
+    return lib().rmi_topk_workspace_bytes(n)
+
+
+def topk(logits, n, k, out_idx, out_val, workspace, stream=None):
+    """the k largest of n logits: out_idx (int32) and out_val (fp32), logit descending, lower id first on ties"""
+    _call("rmi_topk", _p(logits), n, k, _p(out_idx), _p(out_val), _p(workspace), _stream(stream))
 
 
 def embed_q6_k(emb, tokens, x, partials, n_embd, n_vocab, ncols=1, stream=None):

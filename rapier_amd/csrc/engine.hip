@@ -140,7 +140,9 @@ struct Engine {
     float *hsave = nullptr, *hpart = nullptr, *hzero = nullptr, *pzero = nullptr, *qbuf = nullptr;
     float *ex = nullptr, *epart = nullptr, *eh = nullptr, *dx = nullptr, *dpart = nullptr;
     uint8_t *q8a = nullptr, *q8f = nullptr, *q8y = nullptr;
-    void *attn_ws = nullptr, *argmax_ws = nullptr;
+    void *attn_ws = nullptr, *argmax_ws = nullptr, *topk_ws = nullptr;
+    int* topk_out = nullptr;        // top-k ids [0, 64) and logits (as float) [64, 128)
+    int stream_mode = -1;           // rmi_engine_gen_begin's mode, -1 before it
     // saved GDN state and draft hidden for restore
     std::vector<float*> saved_state, saved_hist;
     float *saved_h = nullptr, *saved_hp = nullptr;
@@ -212,9 +214,17 @@ __global__ void accept_kernel(int* st, int* ring) {
     st[kDPos] = st[kPos] + 1;
 }
 
-// after the draft: pick the candidate, advance (1 or 2 positions), apply the forced-acceptance override
-__global__ void finalize_kernel(int* st, const int* ref_tok, const uint8_t* pattern) {
+// after the draft: pick the candidate, advance (1 or 2 positions), apply the forced-acceptance override.  On accept the
+// last fed token is column 1, whose hidden moves to column 0, so that column 0 always holds the hidden of the token
+// before the current one (the input of a later first draft or ingest chunk).
+__global__ void finalize_kernel(int* st, const int* ref_tok, const uint8_t* pattern, float* hsave, float* hpart, int n,
+                                int np) {
     const int accept = st[kAccept];
+    if (accept) {
+        for (int i = threadIdx.x; i < n; i += blockDim.x) hsave[i] = hsave[n + i];
+        for (int i = threadIdx.x; i < np; i += blockDim.x) hpart[i] = hpart[np + i];
+    }
+    if (threadIdx.x != 0) return;
     const int pos = min(st[kPos] + (accept ? 2 : 1), st[kMaxPos]);
     const int cur = accept ? st[kV1] : st[kV0];
     int cand = accept ? st[kC1] : st[kC0];
@@ -259,11 +269,6 @@ __global__ void chunk_finish_kernel(int* st, float* hsave, float* hpart, int n, 
         st[kPos] = st[kPos] + nc;
         if (head) st[kTok0] = st[kV0];
     }
-}
-
-__global__ void copy_f32_kernel(float* dst, const float* src, int n) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) dst[i] = src[i];
 }
 
 unsigned grid1(size_t n) { return static_cast<unsigned>((n + 255) / 256); }
@@ -535,7 +540,8 @@ int verify_round(Engine& e) {
     hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(1), 0, e.s, e.ints, e.ring);
     RMI_TRY(launch_status("accept"));
     RMI_TRY(draft_block(e, e.hsave, e.hpart, 2, true));
-    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, e.s, e.ints, e.ref_tok, e.pattern);
+    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(256), 0, e.s, e.ints, e.ref_tok, e.pattern, e.hsave, e.hpart,
+                       e.cfg.n_embd, e.cfg.n_embd / 4);
     return launch_status("finalize");
 }
 
@@ -964,6 +970,10 @@ int alloc_runtime(Engine& e) {
     uint8_t* aw = nullptr;
     RMI_TRY(e.alloc(&aw, rmi_argmax_workspace_bytes(2)));
     e.argmax_ws = aw;
+    uint8_t* tw = nullptr;
+    RMI_TRY(e.alloc(&tw, rmi_topk_workspace_bytes(c.n_vocab)));
+    e.topk_ws = tw;
+    RMI_TRY(e.alloc(&e.topk_out, 128));
     for (auto& L : e.layers) {
         if (!L.gdn) continue;
         float *s0 = nullptr, *h0 = nullptr;
@@ -1055,6 +1065,7 @@ extern "C" int rmi_engine_info(const rmi_engine* h, rmi_engine_info_t* info) {
 extern "C" int rmi_engine_synth_context(rmi_engine* h, int n_ctx, uint64_t seed, int last_token, int* first_out) {
     if (!h) return fail(RMI_ERR_POINTER, "rmi_engine_synth_context: null engine");
     Engine& e = h->e;
+    e.stream_mode = -1;
     const auto& c = e.cfg;
     if (n_ctx < 1 || n_ctx >= e.max_ctx - 2 || last_token < 0 || last_token >= c.n_vocab)
         return fail(RMI_ERR_STATE, "rmi_engine_synth_context: context does not fit");
@@ -1094,19 +1105,13 @@ extern "C" int rmi_engine_synth_context(rmi_engine* h, int n_ctx, uint64_t seed,
     return RMI_OK;
 }
 
-// Feed the prompt from position 0 (zero state), filling the draft's KV as the reference seeds it (slot 0 with a zero
-// hidden, qw:2956-2958) and every later slot with (token, previous final-normed hidden).  batch 1: one token at a time
-// (the trunk with its head, then the draft row, per token; forward_token, qw:1773-1824).  batch 2..16: chunks of
-// `batch` tokens, each one pass over the weights (the ingest of qw:2658-2722), the head on the last token only; a
-// full chunk is one hipGraph launch.  Both leave the same state.  *first_out = the greedy token after the prompt.
-extern "C" int rmi_engine_prefill_batch(rmi_engine* h, const int* tokens, int n, int batch, int* first_out) {
-    if (!h || !tokens) return fail(RMI_ERR_POINTER, "rmi_engine_prefill: null argument");
+// Empty context: zero GDN state and history (both buffers), selector 0, position 0, and a zero hidden as the input of
+// the first draft row (the reference's serve reset, qw:2533-2549; KV rows need no clearing, attention reads only rows
+// below the position it writes).
+extern "C" int rmi_engine_reset(rmi_engine* h) {
+    if (!h) return fail(RMI_ERR_POINTER, "rmi_engine_reset: null engine");
     Engine& e = h->e;
     const auto& c = e.cfg;
-    if (n < 1 || n >= e.max_ctx - 2) return fail(RMI_ERR_STATE, "rmi_engine_prefill: context does not fit");
-    if (batch < 1 || batch > kChunk) return fail(RMI_ERR_SHAPE, "rmi_engine_prefill: batch must be 1..16");
-    for (int i = 0; i < n; ++i)
-        if (tokens[i] < 0 || tokens[i] >= c.n_vocab) return fail(RMI_ERR_STATE, "rmi_engine_prefill: bad token id");
     for (auto& L : e.layers)
         if (L.gdn) {
             for (int b = 0; b < 2; ++b) {
@@ -1114,25 +1119,52 @@ extern "C" int rmi_engine_prefill_batch(rmi_engine* h, const int* tokens, int n,
                 RMI_TRY(zero_f32(e, L.hist[b], hist_floats(c)));
             }
         }
+    RMI_TRY(zero_f32(e, e.hsave, c.n_embd));
+    RMI_TRY(zero_f32(e, e.hpart, c.n_embd / 4));
     RMI_TRY(set_int(e, kSel, 0));
+    RMI_TRY(set_int(e, kPos, 0));
+    RMI_TRY(set_int(e, kTok0, 0));
     RMI_TRY(set_int(e, kNOut, 0));
+    e.stream_mode = -1;
+    HIP_TRY(hipStreamSynchronize(e.s));
+    return RMI_OK;
+}
+
+// Feed n tokens from the current position, filling the draft's KV as the reference seeds it (slot 0 with a zero hidden,
+// qw:2956-2958) and every later slot with (token, previous final-normed hidden).  batch 1: one token at a time (the
+// trunk with its head, then the draft row, per token; forward_token, qw:1773-1824).  batch 2..16: chunks of `batch`
+// tokens, each one pass over the weights (the ingest of qw:2658-2722), the head on the last token only; a full chunk is
+// one hipGraph launch.  Both leave the same state.  *first_out = the greedy token after the last one fed (the current
+// token).  After a generation the context continues at its position, as the reference's serve loop does.
+extern "C" int rmi_engine_ingest(rmi_engine* h, const int* tokens, int n, int batch, int* first_out) {
+    if (!h || !tokens) return fail(RMI_ERR_POINTER, "rmi_engine_ingest: null argument");
+    Engine& e = h->e;
+    const auto& c = e.cfg;
+    if (batch < 1 || batch > kChunk) return fail(RMI_ERR_SHAPE, "rmi_engine_ingest: batch must be 1..16");
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= c.n_vocab) return fail(RMI_ERR_STATE, "rmi_engine_ingest: bad token id");
+    int st[kNumSlots];
+    RMI_TRY(get_ints(e, st, kNumSlots));
+    const int pos0 = st[kPos];
+    if (n < 1 || pos0 + n >= e.max_ctx - 2) return fail(RMI_ERR_STATE, "rmi_engine_ingest: context does not fit");
+    RMI_TRY(set_int(e, kNOut, 0));
+    e.stream_mode = -1;
     if (batch == 1) {
         for (int i = 0; i < n; ++i) {
-            // draft KV slot i from (token i, hidden of position i - 1) - the zero hidden at slot 0
+            // draft KV slot p from (token, hidden of position p - 1) - the zero hidden at slot 0
+            const int p = pos0 + i;
             RMI_TRY(set_int(e, kD0, tokens[i]));
-            RMI_TRY(set_int(e, kDPos, i));
-            RMI_TRY(draft_block(e, i == 0 ? e.hzero : e.hsave, i == 0 ? e.pzero : e.hpart, 1, false));
+            RMI_TRY(set_int(e, kDPos, p));
+            RMI_TRY(draft_block(e, p == 0 ? e.hzero : e.hsave, p == 0 ? e.pzero : e.hpart, 1, false));
             RMI_TRY(set_int(e, kTok0, tokens[i]));
-            RMI_TRY(set_int(e, kPos, i));
+            RMI_TRY(set_int(e, kPos, p));
             RMI_TRY(single_step(e));
         }
     } else {
-        HIP_TRY(hipMemcpyAsync(e.prompt, tokens, sizeof(int) * static_cast<size_t>(n), hipMemcpyHostToDevice, e.s));
-        hipLaunchKernelGGL(copy_f32_kernel, dim3(grid1(c.n_embd)), dim3(256), 0, e.s, e.hsave, e.hzero, c.n_embd);
-        hipLaunchKernelGGL(copy_f32_kernel, dim3(grid1(c.n_embd / 4)), dim3(256), 0, e.s, e.hpart, e.pzero,
-                           c.n_embd / 4);
-        RMI_TRY(launch_status("copy"));
-        RMI_TRY(set_int(e, kPos, 0));
+        // the chunk kernels read the tokens by position; hidden column 0 holds the hidden of position pos0 - 1 (zero
+        // after a reset)
+        HIP_TRY(hipMemcpyAsync(e.prompt + pos0, tokens, sizeof(int) * static_cast<size_t>(n), hipMemcpyHostToDevice,
+                               e.s));
         int i = 0;
         if (batch == kChunk && n > kChunk) {
             RMI_TRY(capture(e, &e.g_chunk, [&] { return ingest_chunk(e, kChunk, false); }));
@@ -1143,10 +1175,18 @@ extern "C" int rmi_engine_prefill_batch(rmi_engine* h, const int* tokens, int n,
             RMI_TRY(ingest_chunk(e, nc, i + nc == n));
         }
     }
-    int st[kNumSlots];
-    RMI_TRY(get_ints(e, st, kNumSlots));
+    RMI_TRY(get_ints(e, st, kNumSlots));   // synchronizes: the host tokens are no longer read
     if (first_out) *first_out = st[kTok0];
     return RMI_OK;
+}
+
+// the prompt from position 0: reset, then ingest
+extern "C" int rmi_engine_prefill_batch(rmi_engine* h, const int* tokens, int n, int batch, int* first_out) {
+    if (!h || !tokens) return fail(RMI_ERR_POINTER, "rmi_engine_prefill: null argument");
+    if (n < 1 || n >= h->e.max_ctx - 2) return fail(RMI_ERR_STATE, "rmi_engine_prefill: context does not fit");
+    if (batch < 1 || batch > kChunk) return fail(RMI_ERR_SHAPE, "rmi_engine_prefill: batch must be 1..16");
+    RMI_TRY(rmi_engine_reset(h));
+    return rmi_engine_ingest(h, tokens, n, batch, first_out);
 }
 
 extern "C" int rmi_engine_prefill(rmi_engine* h, const int* tokens, int n, int* first_out) {
@@ -1220,6 +1260,7 @@ extern "C" int rmi_engine_save_state(rmi_engine* h) {
 extern "C" int rmi_engine_restore_state(rmi_engine* h, int pos, int cur_token) {
     if (!h) return fail(RMI_ERR_POINTER, "null engine");
     Engine& e = h->e;
+    e.stream_mode = -1;
     const auto& c = e.cfg;
     size_t k = 0;
     for (auto& L : e.layers) {
@@ -1255,6 +1296,7 @@ extern "C" int rmi_engine_state(rmi_engine* h, int* pos, int* cur_token) {
 extern "C" int rmi_engine_generate(rmi_engine* h, const rmi_gen_request* req, int* out_tokens, rmi_gen_stats* stats) {
     if (!h || !req || !out_tokens) return fail(RMI_ERR_POINTER, "rmi_engine_generate: null argument");
     Engine& e = h->e;
+    e.stream_mode = -1;
     const int n_gen = req->n_gen;
     if (n_gen < 1 || n_gen >= kRingCap - 2) return fail(RMI_ERR_STATE, "rmi_engine_generate: bad n_gen");
     int st[kNumSlots];
@@ -1312,5 +1354,67 @@ extern "C" int rmi_engine_generate(rmi_engine* h, const rmi_gen_request* req, in
         stats->accepted = st[kNAcc];
         stats->gpu_ms = ms;
     }
+    return RMI_OK;
+}
+
+// Token-at-a-time generation for a serving loop (the reference's serve_loop, qw:2740-2808): gen_begin prepares the
+// mode (the captured graph; for MTP the first draft candidate of the current token), then each gen_step runs one
+// greedy forward (1 token: the greedy token after the current one, which it feeds) or one verify round (c0, and c1
+// when the candidate was accepted) and returns the emitted tokens.
+extern "C" int rmi_engine_gen_begin(rmi_engine* h, int mode) {
+    if (!h) return fail(RMI_ERR_POINTER, "rmi_engine_gen_begin: null engine");
+    Engine& e = h->e;
+    if (mode != RMI_GEN_GREEDY && mode != RMI_GEN_MTP) return fail(RMI_ERR_STATE, "rmi_engine_gen_begin: bad mode");
+    RMI_TRY(set_int(e, kMode, 0));
+    RMI_TRY(set_int(e, kPatLen, 0));
+    RMI_TRY(set_int(e, kNOut, 0));
+    RMI_TRY(set_int(e, kRound, 0));
+    RMI_TRY(set_int(e, kNAcc, 0));
+    if (mode == RMI_GEN_MTP) {
+        RMI_TRY(capture(e, &e.g_round, [&] { return verify_round(e); }));
+        RMI_TRY(first_draft(e));
+    } else {
+        RMI_TRY(capture(e, &e.g_single, [&] { return single_step(e); }));
+    }
+    HIP_TRY(hipStreamSynchronize(e.s));
+    e.stream_mode = mode;
+    return RMI_OK;
+}
+
+extern "C" int rmi_engine_gen_step(rmi_engine* h, int* out_tokens, int* n_out) {
+    if (!h || !out_tokens || !n_out) return fail(RMI_ERR_POINTER, "rmi_engine_gen_step: null argument");
+    Engine& e = h->e;
+    if (e.stream_mode < 0) return fail(RMI_ERR_STATE, "rmi_engine_gen_step: no rmi_engine_gen_begin since the context changed");
+    int st[kNumSlots];
+    RMI_TRY(get_ints(e, st, kNumSlots));
+    if (st[kPos] + 3 >= e.max_ctx) return fail(RMI_ERR_STATE, "context full");
+    const bool mtp = e.stream_mode == RMI_GEN_MTP;
+    HIP_TRY(hipGraphLaunch(mtp ? e.g_round : e.g_single, e.s));
+    RMI_TRY(get_ints(e, st, kNumSlots));
+    out_tokens[0] = st[kV0];
+    *n_out = 1;
+    if (mtp && st[kAccept]) {
+        out_tokens[1] = st[kV1];
+        *n_out = 2;
+    }
+    return RMI_OK;
+}
+
+// The k largest logits of column col of the last head pass (column 0: the last forward or ingest, before any draft of
+// a gen_begin / gen_step overwrites it) with their ids, logit descending, lower id first among equal logits
+// (topk_out, qw:2513-2531).
+extern "C" int rmi_engine_topk(rmi_engine* h, int col, int k, int* ids, float* logits) {
+    if (!h || !ids || !logits) return fail(RMI_ERR_POINTER, "rmi_engine_topk: null argument");
+    Engine& e = h->e;
+    const int n = e.cfg.n_vocab;
+    if (col < 0 || col > 1) return fail(RMI_ERR_SHAPE, "rmi_engine_topk: column must be 0 or 1");
+    if (k < 1 || k > 64 || k > n) return fail(RMI_ERR_SHAPE, "rmi_engine_topk: k must be 1..min(64, n_vocab)");
+    RMI_TRY(rmi_topk(e.logits + static_cast<size_t>(col) * n, n, k, e.topk_out,
+                     reinterpret_cast<float*>(e.topk_out + 64), e.topk_ws, e.s));
+    int buf[128];
+    HIP_TRY(hipMemcpyAsync(buf, e.topk_out, sizeof buf, hipMemcpyDeviceToHost, e.s));
+    HIP_TRY(hipStreamSynchronize(e.s));
+    std::memcpy(ids, buf, sizeof(int) * k);
+    std::memcpy(logits, buf + 64, sizeof(float) * k);
     return RMI_OK;
 }

@@ -1,0 +1,164 @@
+// topk.hip - the k largest logits (k <= 64) with their token ids, on the device: the per-token list the serve protocol
+// prints (reference qw:2513-2531, topk_out: a host scan over all n logits keeping the k largest in descending order; an
+// incoming logit must be strictly greater than the current k-th to displace it, so among equal logits the lower id
+// ranks first and is kept).  Here each logit becomes a 64-bit key (order-preserving float bits with -0 folded into +0,
+// then the inverted id), all keys are distinct, and the list is the k largest keys in descending order: the same
+// (logit descending, id ascending) order.
+//
+// Two launches.  topk_lists: one wave per 64*E consecutive logits; each lane sorts its E keys in registers (a bitonic
+// network, compile-time indices), then k rounds of a wave max over the lanes' heads pop the wave's k largest into a
+// sorted list.  topk_merge: one 512-lane workgroup, lane t owns list t; k rounds of a workgroup max over the heads (a
+// wave butterfly, one LDS exchange and one barrier per round) pop the global k largest.  The winning lane refills its
+// head from a four-entry register cache, which it tops up from its list with a load that has four pops to land.
+#include "rmi_common.h"
+
+namespace rmi {
+namespace {
+
+constexpr int kTopkMax = 64;       // largest k
+constexpr int kListStride = 64;    // keys per list in the workspace
+constexpr int kMergeLanes = 512;   // lists the merge workgroup can own
+
+__device__ __forceinline__ uint64_t topk_key(float v, uint32_t idx) {
+    uint32_t b = __float_as_uint(v);
+    if (b == 0x80000000u) b = 0u;   // -0 compares equal to +0
+    b ^= (b >> 31) ? 0xffffffffu : 0x80000000u;
+    return (static_cast<uint64_t>(b) << 32) | (0xffffffffu - idx);   // > 0 for every real key; 0 = no entry
+}
+
+__device__ __forceinline__ uint64_t wave_max64(uint64_t k) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(k), off, 64);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(k >> 32), off, 64);
+        const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+template <int E>
+__global__ __launch_bounds__(256) void topk_lists_kernel(const float* __restrict__ x, int n, int k,
+                                                         uint64_t* __restrict__ lists) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t base = static_cast<int64_t>(wave) * 64 * E;
+    uint64_t v[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int64_t i = base + lane + 64 * j;
+        v[j] = i < n ? topk_key(x[i], static_cast<uint32_t>(i)) : 0ull;
+    }
+    // bitonic sort of the lane's E keys, descending
+#pragma unroll
+    for (int size = 2; size <= E; size <<= 1) {
+#pragma unroll
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const uint64_t a = v[i], b = v[j];
+                    const bool swap = (i & size) == 0 ? a < b : a > b;
+                    v[i] = swap ? b : a;
+                    v[j] = swap ? a : b;
+                }
+            }
+        }
+    }
+    uint64_t mine = 0;
+    for (int it = 0; it < k; ++it) {
+        const uint64_t m = wave_max64(v[0]);
+        if (m == 0) break;              // the slice has fewer than k logits (uniform across the wave)
+        if (lane == it) mine = m;
+        if (v[0] == m) {                // keys are distinct: exactly one lane pops
+#pragma unroll
+            for (int j = 0; j + 1 < E; ++j) v[j] = v[j + 1];
+            v[E - 1] = 0;
+        }
+    }
+    if (lane < k) lists[static_cast<size_t>(wave) * kListStride + lane] = mine;
+}
+
+__global__ __launch_bounds__(kMergeLanes) void topk_merge_kernel(const float* __restrict__ x,
+                                                                 const uint64_t* __restrict__ lists, int nlists, int k,
+                                                                 int* __restrict__ out_idx, float* __restrict__ out_val) {
+    __shared__ uint64_t wmax[2][kMergeLanes / 64];
+    __shared__ uint64_t picked[kTopkMax];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const uint64_t* list = lists + static_cast<size_t>(t) * kListStride;
+    const bool own = t < nlists;
+    uint64_t h = own ? list[0] : 0;
+    uint64_t c0 = own && k > 1 ? list[1] : 0, c1 = own && k > 2 ? list[2] : 0;
+    uint64_t c2 = own && k > 3 ? list[3] : 0, c3 = own && k > 4 ? list[4] : 0;
+    int next = 5;
+    for (int it = 0; it < k; ++it) {
+        // the two LDS rows alternate: a row is rewritten two rounds later, after every lane has passed the barrier of
+        // the round in between, i.e. after every lane has read it
+        const uint64_t m = wave_max64(h);
+        if (lane == 0) wmax[it & 1][w] = m;
+        __syncthreads();
+        uint64_t g = wmax[it & 1][0];
+#pragma unroll
+        for (int i = 1; i < kMergeLanes / 64; ++i) g = wmax[it & 1][i] > g ? wmax[it & 1][i] : g;
+        if (t == 0) picked[it] = g;
+        if (g != 0 && h == g) {         // only an owned list holds a nonzero key
+            h = c0;
+            c0 = c1;
+            c1 = c2;
+            c2 = c3;
+            c3 = next < k ? list[next] : 0;
+            ++next;
+        }
+    }
+    __syncthreads();
+    if (t < k) {
+        const uint64_t key = picked[t];
+        const int idx = key ? static_cast<int>(0xffffffffu - static_cast<uint32_t>(key)) : -1;
+        out_idx[t] = idx;
+        out_val[t] = idx >= 0 ? x[idx] : 0.0f;
+    }
+}
+
+// logits per lane of the list pass: the smallest of 8, 16, 32 that keeps the lists within one merge workgroup
+int lane_elems(int n) {
+    for (int e = 8; e <= 32; e *= 2) {
+        const int64_t waves = (static_cast<int64_t>(n) + 64 * e - 1) / (64 * e);
+        if ((waves + 3) / 4 * 4 <= kMergeLanes) return e;
+    }
+    return 0;
+}
+
+}  // namespace
+}  // namespace rmi
+
+using namespace rmi;
+
+extern "C" size_t rmi_topk_workspace_bytes(int n) {
+    const int e = lane_elems(n);
+    if (n <= 0 || e == 0) return 0;
+    const int64_t waves = (static_cast<int64_t>(n) + 64 * e - 1) / (64 * e);
+    return static_cast<size_t>((waves + 3) / 4 * 4) * kListStride * sizeof(uint64_t);
+}
+
+extern "C" int rmi_topk(const float* logits, int n, int k, int* out_idx, float* out_val, void* workspace,
+                        void* stream) {
+    const int e = lane_elems(n);
+    if (n <= 0 || e == 0) return fail(RMI_ERR_SHAPE, "topk: n must be 1..1048576");
+    if (k < 1 || k > kTopkMax || k > n) return fail(RMI_ERR_SHAPE, "topk: k must be 1..min(64, n)");
+    if (!aligned4(logits) || !aligned4(out_idx) || !aligned4(out_val) || !workspace ||
+        (reinterpret_cast<uintptr_t>(workspace) & 7u) != 0)
+        return fail(RMI_ERR_POINTER, "topk: null or misaligned pointer");
+    const int64_t waves = (static_cast<int64_t>(n) + 64 * e - 1) / (64 * e);
+    const int blocks = static_cast<int>((waves + 3) / 4);
+    auto* lists = static_cast<uint64_t*>(workspace);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (e == 8) hipLaunchKernelGGL(topk_lists_kernel<8>, dim3(blocks), dim3(256), 0, s, logits, n, k, lists);
+    else if (e == 16) hipLaunchKernelGGL(topk_lists_kernel<16>, dim3(blocks), dim3(256), 0, s, logits, n, k, lists);
+    else hipLaunchKernelGGL(topk_lists_kernel<32>, dim3(blocks), dim3(256), 0, s, logits, n, k, lists);
+    const int rc = launch_status("topk_lists");
+    if (rc != RMI_OK) return rc;
+    hipLaunchKernelGGL(topk_merge_kernel, dim3(1), dim3(kMergeLanes), 0, s, logits, lists, blocks * 4, k, out_idx,
+                       out_val);
+    return launch_status("topk_merge");
+}

@@ -34,6 +34,28 @@ class GenRequest(ctypes.Structure):
                 ("pattern", ctypes.POINTER(ctypes.c_uint8)), ("pattern_len", ctypes.c_int)]
 
 
+class ServeOptions(ctypes.Structure):
+    _fields_ = [("eos", ctypes.c_int), ("batch", ctypes.c_int), ("topk", ctypes.c_int)]
+
+
+_CB = ctypes.CFUNCTYPE
+SERVE_RESET = _CB(ctypes.c_int, ctypes.c_void_p)
+SERVE_INGEST = _CB(ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int,
+                   ctypes.POINTER(ctypes.c_int))
+SERVE_TOPK = _CB(ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                 ctypes.POINTER(ctypes.c_float))
+SERVE_GEN_BEGIN = _CB(ctypes.c_int, ctypes.c_void_p, ctypes.c_int)
+SERVE_GEN_STEP = _CB(ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int))
+SERVE_POSITION = _CB(ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int))
+SERVE_ERROR = _CB(ctypes.c_void_p, ctypes.c_void_p)   # returns a char* the backend keeps alive
+
+
+class ServeBackend(ctypes.Structure):
+    _fields_ = [("user", ctypes.c_void_p), ("max_ctx", ctypes.c_int), ("reset", SERVE_RESET),
+                ("ingest", SERVE_INGEST), ("topk", SERVE_TOPK), ("gen_begin", SERVE_GEN_BEGIN),
+                ("gen_step", SERVE_GEN_STEP), ("position", SERVE_POSITION), ("error", SERVE_ERROR)]
+
+
 class GenStats(ctypes.Structure):
     _fields_ = [("tokens", ctypes.c_int), ("emitted", ctypes.c_int), ("rounds", ctypes.c_int),
                 ("accepted", ctypes.c_int), ("gpu_ms", ctypes.c_float)]
@@ -82,6 +104,16 @@ def _bind():
         "rmi_engine_restore_state": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
         "rmi_engine_state": (ctypes.c_int, [ctypes.c_void_p, P(ctypes.c_int), P(ctypes.c_int)]),
         "rmi_engine_generate": (ctypes.c_int, [ctypes.c_void_p, P(GenRequest), P(ctypes.c_int), P(GenStats)]),
+        "rmi_engine_reset": (ctypes.c_int, [ctypes.c_void_p]),
+        "rmi_engine_ingest": (ctypes.c_int, [ctypes.c_void_p, P(ctypes.c_int), ctypes.c_int, ctypes.c_int,
+                                             P(ctypes.c_int)]),
+        "rmi_engine_gen_begin": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+        "rmi_engine_gen_step": (ctypes.c_int, [ctypes.c_void_p, P(ctypes.c_int), P(ctypes.c_int)]),
+        "rmi_engine_topk": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, P(ctypes.c_int),
+                                           P(ctypes.c_float)]),
+        "rmi_serve_default_options": (ServeOptions, []),
+        "rmi_serve_fd": (ctypes.c_int, [P(ServeBackend), P(ServeOptions), ctypes.c_int, ctypes.c_int]),
+        "rmi_serve_engine": (ctypes.c_int, [ctypes.c_void_p, P(ServeOptions), ctypes.c_int, ctypes.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -210,6 +242,39 @@ class Engine:
         _call("rmi_engine_prefill_batch", self._h, arr, len(tokens), batch, ctypes.byref(first))
         return first.value
 
+    def reset(self):
+        """empty context at position 0"""
+        _call("rmi_engine_reset", self._h)
+
+    def ingest(self, tokens, batch: int = 16) -> int:
+        """feed tokens at the current position; returns the greedy token after them"""
+        arr = (ctypes.c_int * len(tokens))(*tokens)
+        first = ctypes.c_int()
+        _call("rmi_engine_ingest", self._h, arr, len(tokens), batch, ctypes.byref(first))
+        return first.value
+
+    def gen_begin(self, mode: int = GREEDY):
+        _call("rmi_engine_gen_begin", self._h, mode)
+
+    def gen_step(self):
+        """one greedy forward ([next]) or one verify round ([c0] or [c0, c1])"""
+        out = (ctypes.c_int * 2)()
+        n = ctypes.c_int()
+        _call("rmi_engine_gen_step", self._h, out, ctypes.byref(n))
+        return list(out)[:n.value]
+
+    def topk(self, k: int = 40, col: int = 0):
+        """[(id, logit)] of the k largest logits of the last head pass, logit descending, lower id first on ties"""
+        ids = (ctypes.c_int * k)()
+        vals = (ctypes.c_float * k)()
+        _call("rmi_engine_topk", self._h, col, k, ids, vals)
+        return list(zip(list(ids), list(vals)))
+
+    def serve_fd(self, in_fd: int, out_fd: int, eos: int = 248046, batch: int = 16, topk: int = 40):
+        """the --serve protocol over two file descriptors (rmi_serve_engine), until end of input"""
+        o = ServeOptions(eos=eos, batch=batch, topk=topk)
+        _call("rmi_serve_engine", self._h, ctypes.byref(o), in_fd, out_fd)
+
     def read(self, which: int, layer: int, nbytes: int, offset: int = 0):
         """bytes [offset, offset + nbytes) of an engine buffer (BUF_*) as a uint8 numpy array"""
         import numpy as np
@@ -252,6 +317,13 @@ class Engine:
         st = GenStats()
         _call("rmi_engine_generate", self._h, ctypes.byref(req), out, ctypes.byref(st))
         return list(out), st.as_dict()
+
+
+def serve_fd(backend: ServeBackend, in_fd: int, out_fd: int, eos: int = 248046, batch: int = 16, topk: int = 40):
+    """the --serve protocol loop over any backend (rmi_serve_fd); returns its status code"""
+    _bind()
+    o = ServeOptions(eos=eos, batch=batch, topk=topk)
+    return lib().rmi_serve_fd(ctypes.byref(backend), ctypes.byref(o), in_fd, out_fd)
 
 
 __all__ = ["Engine", "ModelConfig", "qwen35_9b_config", "small_config", "GREEDY", "MTP", "MTP_FORCED", "last_error"]
