@@ -313,22 +313,34 @@ def run_ingest(n_prompt=4096, batch=16, n_check=64):
                     f"{n_check} tokens; identical = first token and final hidden bit-equal after {n_check} tokens"}
 
 
-def qwen35_9b_tensors():
-    """(name, ggml type, dims) of a 9B-class qwen35 GGUF with the reference's tensor names (qw:2003-2127)"""
+def qwen35_9b_tensors(plan="q6_k"):
+    """(name, ggml type, dims) of a 9B-class qwen35 GGUF with the reference's tensor names (qw:2003-2127).
+    plan "q6_k": every matrix Q6_K.  plan "q5_k_m": a Q5_K_M-like mix (llama.cpp's rule for that file type): Q5_K
+    matrices and token table, Q6_K output, attn_v and ffn_down Q6_K in the first and last eighth of the layers and in
+    every third layer between, Q5_K elsewhere - so q|k|v groups mix types in those layers."""
     E, F, V, NL, HK, HV, NH, NKV, HD = 4096, 12288, 248320, 32, 16, 32, 16, 4, 256
     ch = (2 * HK + HV) * 128
-    t = [("token_embd.weight", 14, (E, V)), ("output.weight", 14, (E, V)), ("output_norm.weight", 0, (E,))]
+    mixed = plan == "q5_k_m"
+    mat = 13 if mixed else 14
+
+    def more_bits(il):
+        return il < NL // 8 or il >= 7 * NL // 8 or (il - NL // 8) % 3 == 2
+
+    t = [("token_embd.weight", mat, (E, V)), ("output.weight", 14, (E, V)), ("output_norm.weight", 0, (E,))]
 
     def attn(il):
         p = f"blk.{il}."
+        vt = 14 if not mixed or more_bits(il) else 13
         return [(p + "attn_norm.weight", 0, (E,)), (p + "post_attention_norm.weight", 0, (E,)),
-                (p + "attn_q.weight", 14, (E, 2 * NH * HD)), (p + "attn_k.weight", 14, (E, NKV * HD)),
-                (p + "attn_v.weight", 14, (E, NKV * HD)), (p + "attn_output.weight", 14, (NH * HD, E)),
+                (p + "attn_q.weight", mat, (E, 2 * NH * HD)), (p + "attn_k.weight", mat, (E, NKV * HD)),
+                (p + "attn_v.weight", vt, (E, NKV * HD)), (p + "attn_output.weight", mat, (NH * HD, E)),
                 (p + "attn_q_norm.weight", 0, (HD,)), (p + "attn_k_norm.weight", 0, (HD,))]
 
     def ffn(il):
         p = f"blk.{il}."
-        return [(p + "ffn_up.weight", 14, (E, F)), (p + "ffn_gate.weight", 14, (E, F)), (p + "ffn_down.weight", 14, (F, E))]
+        dt = 14 if not mixed or more_bits(il) else 13
+        return [(p + "ffn_up.weight", mat, (E, F)), (p + "ffn_gate.weight", mat, (E, F)),
+                (p + "ffn_down.weight", dt, (F, E))]
 
     for il in range(NL):
         p = f"blk.{il}."
@@ -336,12 +348,12 @@ def qwen35_9b_tensors():
             t += attn(il)
         else:
             t += [(p + "attn_norm.weight", 0, (E,)), (p + "post_attention_norm.weight", 0, (E,)),
-                  (p + "attn_qkv.weight", 14, (E, ch)), (p + "attn_gate.weight", 14, (E, HV * 128)),
-                  (p + "ssm_beta.weight", 14, (E, HV)), (p + "ssm_alpha.weight", 14, (E, HV)),
-                  (p + "ssm_out.weight", 14, (HV * 128, E)), (p + "ssm_conv1d.weight", 0, (4, ch)),
+                  (p + "attn_qkv.weight", mat, (E, ch)), (p + "attn_gate.weight", mat, (E, HV * 128)),
+                  (p + "ssm_beta.weight", mat, (E, HV)), (p + "ssm_alpha.weight", mat, (E, HV)),
+                  (p + "ssm_out.weight", mat, (HV * 128, E)), (p + "ssm_conv1d.weight", 0, (4, ch)),
                   (p + "ssm_dt.bias", 0, (HV,)), (p + "ssm_a", 0, (HV,)), (p + "ssm_norm.weight", 0, (128,))]
         t += ffn(il)
-    t += attn(NL) + ffn(NL) + [(f"blk.{NL}.nextn.eh_proj.weight", 14, (2 * E, E))]
+    t += attn(NL) + ffn(NL) + [(f"blk.{NL}.nextn.eh_proj.weight", mat, (2 * E, E))]
     t += [(f"blk.{NL}.nextn.{w}.weight", 0, (E,)) for w in ("enorm", "hnorm", "shared_head_norm")]
     meta = [("general.architecture", 8, "qwen35"), ("qwen35.block_count", 4, NL + 1),
             ("qwen35.nextn_predict_layers", 4, 1), ("qwen35.attention.layer_norm_rms_epsilon", 6, 1e-6),
@@ -349,9 +361,13 @@ def qwen35_9b_tensors():
     return t, meta
 
 
+BLOCK = {14: 210, 13: 176, 12: 144}   # bytes per 256 weights of Q6_K, Q5_K, Q4_K
+
+
 def write_synthetic_gguf(path, tensors, meta, seed=7):
     """Stream a GGUF v3 file (the published layout: header, key/values, tensor infos, data aligned to 32): random
-    Q6_K blocks with a valid fp16 scale, unit norms, ssm_a = -1, small conv taps.  Returns the file size."""
+    Q6_K / Q5_K / Q4_K blocks with valid fp16 scales, unit norms, ssm_a = -1, small conv taps.  Returns the file
+    size."""
     import struct
 
     import numpy as np
@@ -359,7 +375,8 @@ def write_synthetic_gguf(path, tensors, meta, seed=7):
     s = lambda x: struct.pack("<Q", len(x.encode())) + x.encode()   # noqa: E731
     fmt = {4: "<I", 6: "<f"}
     kv = b"".join(s(k) + struct.pack("<I", t) + (s(v) if t == 8 else struct.pack(fmt[t], v)) for k, t, v in meta)
-    sizes = [(n, tp, d, (int(np.prod(d)) // 256 * 210) if tp == 14 else int(np.prod(d)) * 4) for n, tp, d in tensors]
+    sizes = [(n, tp, d, (int(np.prod(d)) // 256 * BLOCK[tp]) if tp in BLOCK else int(np.prod(d)) * 4)
+             for n, tp, d in tensors]
     infos, off, offs = b"", 0, []
     for n, tp, d, nb in sizes:
         infos += s(n) + struct.pack("<I", len(d)) + b"".join(struct.pack("<Q", x) for x in d) + struct.pack("<IQ", tp, off)
@@ -371,10 +388,15 @@ def write_synthetic_gguf(path, tensors, meta, seed=7):
         pos = 0
         for (n, tp, d, nb), o in zip(sizes, offs):
             f.write(b"\0" * (o - pos))
-            if tp == 14:
-                for r0 in range(0, nb, 210 << 16):          # 65536 blocks at a time
-                    blk = rng.integers(0, 256, min(210 << 16, nb - r0), dtype=np.uint8).reshape(-1, 210)
-                    blk[:, 208:210] = np.frombuffer(np.float16(1e-3).tobytes(), np.uint8)
+            if tp in BLOCK:
+                bb = BLOCK[tp]
+                for r0 in range(0, nb, bb << 16):           # 65536 blocks at a time
+                    blk = rng.integers(0, 256, min(bb << 16, nb - r0), dtype=np.uint8).reshape(-1, bb)
+                    if tp == 14:
+                        blk[:, 208:210] = np.frombuffer(np.float16(1e-3).tobytes(), np.uint8)
+                    else:                                   # d, dmin at the block head
+                        blk[:, 0:2] = np.frombuffer(np.float16(2e-3).tobytes(), np.uint8)
+                        blk[:, 2:4] = np.frombuffer(np.float16(1e-3).tobytes(), np.uint8)
                     f.write(blk.tobytes())
             else:
                 v = np.ones(nb // 4, np.float32)
@@ -387,9 +409,64 @@ def write_synthetic_gguf(path, tensors, meta, seed=7):
     return os.path.getsize(path)
 
 
+def serve_leg(path, n_gen):
+    """The --serve protocol through the engine executable on the same file: JSON lines over pipes, the way the
+    reference's server drives its engine.  Times a 4096-token ingest (gen 1), then greedy (top-40 list per token) and
+    MTP runs of n_gen tokens from a 64-token prompt, each from the request write to its done line."""
+    import subprocess
+
+    import numpy as np
+    exe = os.path.join(ROOT, "rapier_amd", "rmi_engine")
+    if not os.path.exists(exe):
+        return {"skipped": "the engine executable is not built"}
+    env = dict(os.environ, QWYTHOS_MAXCTX="8192")
+    p = subprocess.Popen([exe, "--model", path, "--serve"], stdin=subprocess.PIPE, stdout=subprocess.PIPE,
+                         stderr=subprocess.PIPE, text=True, bufsize=1, env=env)
+    try:
+        seen = []
+        for line in p.stderr:                                # the runtime may print notices first
+            seen.append(line.strip())
+            if "ready" in line or len(seen) > 50:
+                break
+        if not seen or "ready" not in seen[-1]:
+            return {"error": " | ".join(seen)[-300:]}
+        rng = np.random.default_rng(3)
+
+        def run(req):
+            t0 = time.perf_counter()
+            p.stdin.write(json.dumps(req, separators=(",", ":")) + "\n")
+            p.stdin.flush()
+            ids, t_first = [], None
+            while True:
+                o = json.loads(p.stdout.readline())
+                if "id" in o:
+                    ids.append(o["id"])
+                    if t_first is None:
+                        t_first = time.perf_counter()
+                elif "done" in o or "error" in o or "ok" in o:
+                    return ids, t_first - t0 if t_first else None, time.perf_counter() - t0, o
+
+        run({"op": "reset"})
+        prompt = rng.integers(0, 248320, 4096).tolist()
+        _, t_first, _, _ = run({"op": "run", "tokens": prompt, "gen": 1, "mtp": False})
+        out = {"ingest_tokens": 4096, "ingest_tok_s": round(4096 / t_first, 1)}
+        short = rng.integers(0, 248320, 64).tolist()
+        for mtp in (False, True):
+            run({"op": "reset"})
+            ids, t_first, t_all, done = run({"op": "run", "tokens": short, "gen": n_gen, "mtp": mtp})
+            key = "mtp" if mtp else "greedy"
+            out[key + "_tok_s"] = round((len(ids) - 1) / (t_all - t_first), 1)
+            out[key + "_ids"] = ids
+        out["mtp_identical"] = out.pop("mtp_ids") == out.pop("greedy_ids")
+        return out
+    finally:
+        p.stdin.close()
+        p.wait(timeout=120)
+
+
 def run_gguf_load(args):
     """Load a 9B-class qwen35 GGUF (written to local disk first, so the load reads the page cache) through
-    rmi_engine_create_gguf and decode from it."""
+    rmi_engine_create_gguf and decode from it; then serve from the same file through the engine executable."""
     import tempfile
 
     import torch
@@ -399,7 +476,7 @@ def run_gguf_load(args):
     stream = torch.cuda.Stream(device=0)
     torch.cuda.set_stream(stream)
     import shutil
-    tensors, meta = qwen35_9b_tensors()
+    tensors, meta = qwen35_9b_tensors(args.plan)
     tmp = os.environ.get("TMPDIR", "/tmp")
     if shutil.disk_usage(tmp).free < 16e9:
         print(json.dumps({"workload": "gguf_load", "skipped": f"less than 16 GB free under {tmp}"}), flush=True)
@@ -413,22 +490,27 @@ def run_gguf_load(args):
         t0 = time.perf_counter()
         eng = E.Engine.from_gguf(path, max_ctx=4096 + 512, stream=stream)
         t_load = time.perf_counter() - t0
-    info = eng.info()
-    first = eng.prefill(list(range(1000, 1064)), batch=16)
-    pos0, cur0 = eng.state()
-    eng.save_state()
-    n = args.steps
-    ref, st_g = eng.generate(n, mode=E.GREEDY)
-    eng.restore_state(pos0, cur0)
-    toks, st_m = eng.generate(n, mode=E.MTP)
-    eng.close()
-    print(json.dumps({"workload": "gguf_load", "file_bytes": size, "load_s": round(t_load, 3),
+        info = eng.info()
+        first = eng.prefill(list(range(1000, 1064)), batch=16)
+        pos0, cur0 = eng.state()
+        eng.save_state()
+        n = args.steps
+        ref, st_g = eng.generate(n, mode=E.GREEDY)
+        eng.restore_state(pos0, cur0)
+        toks, st_m = eng.generate(n, mode=E.MTP)
+        eng.close()
+        torch.cuda.synchronize()
+        print(f"in-process decode done; serving from the file", file=sys.stderr, flush=True)
+        serve = serve_leg(path, n)
+    print(json.dumps({"workload": "gguf_load", "plan": args.plan, "file_bytes": size, "load_s": round(t_load, 3),
                       "load_GB_s": round(size / t_load / 1e9, 2), "write_s": round(t_write, 2),
                       "round_weight_bytes": info["round_weight_bytes"], "first_token": first,
                       "greedy_tok_s": round(n / (st_g["gpu_ms"] / 1e3), 1),
                       "mtp_tok_s_natural": round(n / (st_m["gpu_ms"] / 1e3), 1), "mtp_identical": toks == ref,
-                      "note": "random Q6_K blocks (fp16 scale 1e-3), unit norms: a load and shape check, not a "
-                              "trained model; the file is read from the page cache right after it was written"}),
+                      "serve": serve,
+                      "note": "random K-quant blocks, unit norms: a load and shape check, not a trained model (draft "
+                              "acceptance near 0); the file is read from the page cache right after it was written; "
+                              "serve rates are wall-clock over pipes, from the first token line to the done line"}),
           flush=True)
 
 
@@ -440,6 +522,7 @@ def main():
     ap.add_argument("--workload", default="mtp_round",
                     choices=["mtp_round", "verify_gemv", "traffic_probe", "gguf_load"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--plan", default="q6_k", choices=["q6_k", "q5_k_m"], help="gguf_load: the file's type plan")
     ap.add_argument("--ctx", default="4096,65536",
                     help="comma-separated context lengths for mtp_round; value is quoted at the first")
     args = ap.parse_args()

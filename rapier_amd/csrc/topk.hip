@@ -8,7 +8,7 @@
 // Two launches.  topk_lists: one wave per 64*E consecutive logits; each lane sorts its E keys in registers (a bitonic
 // network, compile-time indices), then k rounds of a wave max over the lanes' heads pop the wave's k largest into a
 // sorted list.  topk_merge: one 512-lane workgroup, lane t owns list t; k rounds of a workgroup max over the heads (a
-// wave butterfly, one LDS exchange and one barrier per round) pop the global k largest.  The winning lane refills its
+// DPP wave max, one LDS exchange and one barrier per round) pop the global k largest.  The winning lane refills its
 // head from a four-entry register cache, which it tops up from its list with a load that has four pops to land.
 #include "rmi_common.h"
 
@@ -26,15 +26,33 @@ __device__ __forceinline__ uint64_t topk_key(float v, uint32_t idx) {
     return (static_cast<uint64_t>(b) << 32) | (0xffffffffu - idx);   // > 0 for every real key; 0 = no entry
 }
 
+__device__ __forceinline__ uint64_t max64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// lane exchange by a DPP pattern (every lane active)
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v)), CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v >> 32)), CTRL, 0xf, 0xf,
+                                               false);
+    return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+}
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), lane));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)),
+                                                                        lane));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// wave-uniform max of a 64-bit key: DPP within each row of 16 lanes (xor 1, xor 2, half-row mirror, row mirror; max
+// is symmetric, so a mirror partner serves as well as an xor one), then the four row maxima read into scalars.
+// Called with every lane of the wave active.
 __device__ __forceinline__ uint64_t wave_max64(uint64_t k) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(k), off, 64);
-        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(k >> 32), off, 64);
-        const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
-        k = o > k ? o : k;
-    }
-    return k;
+    k = max64(k, dpp64<0xb1>(k));    // quad_perm [1,0,3,2]
+    k = max64(k, dpp64<0x4e>(k));    // quad_perm [2,3,0,1]
+    k = max64(k, dpp64<0x141>(k));   // row_half_mirror
+    k = max64(k, dpp64<0x140>(k));   // row_mirror
+    return max64(max64(readlane64(k, 0), readlane64(k, 16)), max64(readlane64(k, 32), readlane64(k, 48)));
 }
 
 template <int E>
