@@ -477,9 +477,11 @@ int cu_count() {
     return n;
 }
 
-// waves: at most per_cu workgroups per CU, and an even split of the quads over them
+// waves: at most per_cu workgroups per CU, and an even split of the quads over them.  32 gives every matrix up to
+// 32768 quads one quad per wave (all its tiles in flight from the start; the lm_head gets two): measured in the 9B
+// round, 4 -> 8 -> 32 workgroups per CU took it from 2758 to 2727 to 2712 us.
 int packed_grid(int nq) {
-    static const int per_cu = env_int("RMI_PACKED_PER_CU", 4);
+    static const int per_cu = env_int("RMI_PACKED_PER_CU", 32);
     const int max_waves = std::max(1, per_cu) * cu_count() * (kThreads / 64);
     const int qpw = (nq + max_waves - 1) / max_waves;
     const int waves = (nq + qpw - 1) / qpw;
