@@ -130,6 +130,13 @@ constexpr int KTILE = STEP * KROW;       // 8448 bytes per wave; reused for the 
 
 __device__ __forceinline__ void lds_wave_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+// K / V rows are streamed once per step: nontemporal loads, as the GEMVs stream their weights
+__device__ __forceinline__ uint4 load_kv(const uint16_t* p) {
+    const u32x4v v = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 typedef uint32_t u32x32 __attribute__((ext_vector_type(32)));
 
 __device__ __forceinline__ void set_u4(u32x32& v, int j, uint4 w) {
@@ -197,15 +204,15 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int p = min(wbase + 2 * j + krow, p_last);
-        set_u4(kreg, j, *reinterpret_cast<const uint4*>(kb + p * rstride + kcol * 8));
+        set_u4(kreg, j, load_kv(kb + p * rstride + kcol * 8));
     }
     // V of a step: [2 j + dg] = position sb + 4 g4 + j, dims 128 dg + 8 l16 + [0, 8); also one step ahead
     u32x32 vnext;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint16_t* vr = vb + min(wbase + 4 * g4 + j, p_last) * rstride + 8 * l16;
-        set_u4(vnext, 2 * j, *reinterpret_cast<const uint4*>(vr));
-        set_u4(vnext, 2 * j + 1, *reinterpret_cast<const uint4*>(vr + 128));
+        set_u4(vnext, 2 * j, load_kv(vr));
+        set_u4(vnext, 2 * j + 1, load_kv(vr + 128));
     }
     // B operand of the score MFMAs, from the query rows loaded above: step 2 sp + hlf covers dims
     // 32 sp + 8 g4 + 4 hlf + [0, 4); rows 0-7 the fp16 hi part, rows 8-15 the fp16 lo part of the same slot
@@ -229,8 +236,8 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint16_t* vr = vb + min(sb + STEP + 4 * g4 + j, p_last) * rstride + 8 * l16;
-            set_u4(vnext, 2 * j, *reinterpret_cast<const uint4*>(vr));
-            set_u4(vnext, 2 * j + 1, *reinterpret_cast<const uint4*>(vr + 128));
+            set_u4(vnext, 2 * j, load_kv(vr));
+            set_u4(vnext, 2 * j + 1, load_kv(vr + 128));
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) *reinterpret_cast<uint4*>(kt + (2 * j + krow) * KROW + kcol * 16) = get_u4(kreg, j);
@@ -238,7 +245,7 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int p = min(sb + STEP + 2 * j + krow, p_last);
-            set_u4(kreg, j, *reinterpret_cast<const uint4*>(kb + p * rstride + kcol * 8));
+            set_u4(kreg, j, load_kv(kb + p * rstride + kcol * 8));
         }
         lds_wave_sync();
         floatx4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
