@@ -123,6 +123,17 @@ struct StepArgs {
 // verify pair: the state and history after token 0 also go to the rollback buffers.  Otherwise (1 token, or an ingest
 // chunk of up to 16) the state and history are updated in place after the last token.  Every token's arithmetic is
 // that of the single-token step in the same order, so a chunk leaves the bits the per-token steps leave.
+// v[l] + v[l ^ 16], then that plus its value in lane l ^ 32: the sum over a column's four row groups, in every lane of
+// the column.  gfx950's lane swaps (v_permlane16_swap / v_permlane32_swap: each returns a half's even / odd rows, or
+// the two 32-lane halves, side by side) keep it on the VALU; the sums are those of the xor-16 / xor-32 butterfly
+// (the two addends of each lane are the same, in either order).
+__device__ __forceinline__ float sum_row_groups(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int NT, bool RAW, bool CONV>
 __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     constexpr bool SNAP = NT == 2;
@@ -286,15 +297,20 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     }
     __syncthreads();
 
+    // The recurrence runs through all tokens without a workgroup barrier: the output norm of token t (a sum over the
+    // head's 128 columns, across waves) feeds only y, so each token's o and per-wave sum of squares are kept and the
+    // norms are taken after the loop, with the same operations in the same order.
+    float occ[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) occ[t] = 0.0f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        if (t < ntok) {   // uniform: the barrier below is reached by every lane or none
+        if (t < ntok) {   // uniform
             const float g = gbt[t][0], beta = gbt[t][1];
             float kv = 0.0f;
 #pragma unroll
             for (int r = 0; r < RPG; ++r) kv = __builtin_fmaf(s[r], ck[t][rg * RPG + r], kv);
-            kv += __shfl_xor(kv, 16, 64);   // (rg 0 + rg 1) + (rg 2 + rg 3), the same bits in all four lanes
-            kv += __shfl_xor(kv, 32, 64);
+            kv = sum_row_groups(kv);   // (rg 0 + rg 1) + (rg 2 + rg 3), the same bits in all four lanes
             const float vcol = CONV ? cv[CONV ? t : 0][col] : vreg[t];
             const float delta = (vcol - g * kv) * beta;
             float o = 0.0f;
@@ -303,8 +319,7 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
                 s[r] = __builtin_fmaf(g, s[r], ck[t][rg * RPG + r] * delta);
                 o = __builtin_fmaf(s[r], cq[t][rg * RPG + r], o);
             }
-            o += __shfl_xor(o, 16, 64);
-            o += __shfl_xor(o, 32, 64);
+            o = sum_row_groups(o);
             const float oc = o * 0.08838834764831845f;   // 1 / sqrt(128)
             if constexpr (SNAP) {
                 if (t == 0) {
@@ -314,13 +329,19 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
             }
             const float ss = group_sum<16>(oc * oc);   // the wave's 16 columns (row-group 0 lanes carry them)
             if (ln == 0) wsum[t][wv] = ss;
-            __syncthreads();
+            occ[t] = oc;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        if (t < ntok) {
             float tot = 0.0f;
 #pragma unroll
             for (int w = 0; w < S * RG / 64; ++w) tot += wsum[t][w];
             if (rg == 0) {
                 const float scale = rsqrtf(tot / static_cast<float>(S) + a.eps);
-                ybuf[t][col] = oc * scale * gam * silu(zz[t]);
+                ybuf[t][col] = occ[t] * scale * gam * silu(zz[t]);
             }
         }
     }
