@@ -262,12 +262,12 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
         float mloc = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float v = sacc[r] + __shfl_xor(sacc[r], 8, 64);
+            const float v = sacc[r] + xor_lane<8>(sacc[r]);
             sc[r] = sb + 4 * g4 + r <= lim ? v * scale : -INFINITY;
             mloc = fmaxf(mloc, sc[r]);
         }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        mloc = fmaxf(mloc, xor_lane<16>(mloc));
+        mloc = fmaxf(mloc, xor_lane<32>(mloc));
         const float m_new = fmaxf(m_run, mloc);
         const float m_ref = m_new == -INFINITY ? 0.0f : m_new;   // nothing visible yet: exp(-inf) = 0, no NaN
         const float alpha = m_run == m_new ? 1.0f : expf(m_run - m_ref);
@@ -277,8 +277,8 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
             pr[r] = expf(sc[r] - m_ref);
             lsum += pr[r];
         }
-        lsum += __shfl_xor(lsum, 16, 64);
-        lsum += __shfl_xor(lsum, 32, 64);
+        lsum += xor_lane<16>(lsum);
+        lsum += xor_lane<32>(lsum);
         l_run = l_run * alpha + lsum;
         m_run = m_new;
         if (__ballot(alpha != 1.0f)) {   // wave-uniform: some slot's running max moved
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
 #pragma unroll
         for (int e = 0; e < 8; ++e)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) oacc[dg][e][r] += __shfl_xor(oacc[dg][e][r], 32, 64);
+            for (int r = 0; r < 4; ++r) oacc[dg][e][r] += xor_lane<32>(oacc[dg][e][r]);
 
     __syncthreads();   // every wave is done with its K tile: reuse it for the wave's o
     float* ob = reinterpret_cast<float*>(kt);

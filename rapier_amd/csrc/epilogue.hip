@@ -140,13 +140,16 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
 }
 
 __device__ __forceinline__ uint64_t key_max64(uint64_t k) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(k), off, 64);
-        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(k >> 32), off, 64);
+    auto step = [&](uint32_t lo, uint32_t hi) {
         const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
         k = o > k ? o : k;
-    }
+    };
+    step(xor_lane<32>(static_cast<uint32_t>(k)), xor_lane<32>(static_cast<uint32_t>(k >> 32)));
+    step(xor_lane<16>(static_cast<uint32_t>(k)), xor_lane<16>(static_cast<uint32_t>(k >> 32)));
+    step(xor_lane<8>(static_cast<uint32_t>(k)), xor_lane<8>(static_cast<uint32_t>(k >> 32)));
+    step(xor_lane<4>(static_cast<uint32_t>(k)), xor_lane<4>(static_cast<uint32_t>(k >> 32)));
+    step(xor_lane<2>(static_cast<uint32_t>(k)), xor_lane<2>(static_cast<uint32_t>(k >> 32)));
+    step(xor_lane<1>(static_cast<uint32_t>(k)), xor_lane<1>(static_cast<uint32_t>(k >> 32)));
     return k;
 }
 

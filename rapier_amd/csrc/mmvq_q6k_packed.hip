@@ -62,10 +62,10 @@ __device__ __forceinline__ int subblock_dot(const int (&v)[8], const int (&u)[8]
 // sum over the 16 half-blocks of a row (lanes 4 hb + r): the xor butterfly over hb with offsets 8, 4, 2, 1, the tree
 // of the 16-row tiled kernel's row sum
 __device__ __forceinline__ float hb_sum(float v) {
-    v += __shfl_xor(v, 32, 64);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 8, 64);
-    v += __shfl_xor(v, 4, 64);
+    v += xor_lane<32>(v);
+    v += xor_lane<16>(v);
+    v += xor_lane<8>(v);
+    v += xor_lane<4>(v);
     return v;
 }
 

@@ -37,17 +37,56 @@ __device__ __forceinline__ uint32_t float_to_half_sat(float v) {
     return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v)));
 }
 
-// xor butterfly over groups of W lanes; every lane of a group ends with the same value
+// The value of lane l ^ K (K = 1, 2, 4, 8, 16, 32) on the VALU, the partner __shfl_xor would fetch through the LDS
+// unit: DPP within a row of 16 lanes (quad permutes; row shifts by 4 picked by lane bit 2, since a row shift reads
+// lane l + 4 / l - 4; a row rotation by 8), and gfx950's lane swaps across rows (v_permlane16_swap pairs rows 0-1 and
+// 2-3, v_permlane32_swap the two halves; each returns both rows side by side).  The partner lane must be active.
+template <int K>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    const int x = static_cast<int>(v);
+    if constexpr (K == 1) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0xb1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+    } else if constexpr (K == 2) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x4e, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+    } else if constexpr (K == 4) {
+        const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xf, 0xf, false);   // row_shl:4 - lane l + 4
+        const int dn = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);   // row_shr:4 - lane l - 4
+        return static_cast<uint32_t>((__lane_id() & 4) ? dn : up);
+    } else if constexpr (K == 8) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, false));  // row_ror:8
+    } else if constexpr (K == 16) {
+        const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (__lane_id() & 16) ? a[0] : a[1];
+    } else {
+        static_assert(K == 32, "xor_lane: K must be 1, 2, 4, 8, 16 or 32");
+        const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (__lane_id() & 32) ? a[0] : a[1];
+    }
+}
+template <int K>
+__device__ __forceinline__ float xor_lane(float v) {
+    return __uint_as_float(xor_lane<K>(__float_as_uint(v)));
+}
+
+// xor butterfly over groups of W lanes (offsets W / 2 .. 1); every lane of a group ends with the same value
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, W);
+    if constexpr (W >= 64) v += xor_lane<32>(v);
+    if constexpr (W >= 32) v += xor_lane<16>(v);
+    if constexpr (W >= 16) v += xor_lane<8>(v);
+    if constexpr (W >= 8) v += xor_lane<4>(v);
+    if constexpr (W >= 4) v += xor_lane<2>(v);
+    if constexpr (W >= 2) v += xor_lane<1>(v);
     return v;
 }
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int off = W / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, W));
+    if constexpr (W >= 64) v = fmaxf(v, xor_lane<32>(v));
+    if constexpr (W >= 32) v = fmaxf(v, xor_lane<16>(v));
+    if constexpr (W >= 16) v = fmaxf(v, xor_lane<8>(v));
+    if constexpr (W >= 8) v = fmaxf(v, xor_lane<4>(v));
+    if constexpr (W >= 4) v = fmaxf(v, xor_lane<2>(v));
+    if constexpr (W >= 2) v = fmaxf(v, xor_lane<1>(v));
     return v;
 }
 
