@@ -62,8 +62,7 @@ __global__ __launch_bounds__(256) void rms_norm_out_kernel(const float* __restri
     }
     if (out_partials) {
         // the 4 rows of a partial slot are 4 consecutive lanes: gather them in row order on the first lane
-        const float v0 = __shfl(v, (threadIdx.x & ~3) + 0, 64), v1 = __shfl(v, (threadIdx.x & ~3) + 1, 64);
-        const float v2 = __shfl(v, (threadIdx.x & ~3) + 2, 64), v3 = __shfl(v, (threadIdx.x & ~3) + 3, 64);
+        const float v0 = quad_lane<0>(v), v1 = quad_lane<1>(v), v2 = quad_lane<2>(v), v3 = quad_lane<3>(v);
         if ((threadIdx.x & 3) == 0 && i < cols) {
             float p = 0.0f;
             p = __builtin_fmaf(v0, v0, p);
@@ -240,8 +239,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ 
     const float v = embed_value<TYPE>(b, e);
     const int idx = blockIdx.x * 256 + e;
     x[static_cast<size_t>(c) * n_embd + idx] = v;
-    const float v0 = __shfl(v, (e & ~3) + 0, 64), v1 = __shfl(v, (e & ~3) + 1, 64);
-    const float v2 = __shfl(v, (e & ~3) + 2, 64), v3 = __shfl(v, (e & ~3) + 3, 64);
+    const float v0 = quad_lane<0>(v), v1 = quad_lane<1>(v), v2 = quad_lane<2>(v), v3 = quad_lane<3>(v);
     if ((e & 3) == 0) {
         float p = 0.0f;
         p = __builtin_fmaf(v0, v0, p);

@@ -240,8 +240,10 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
                     if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v;
                     if constexpr (RES) {
                         // partial of the quad: squares of its rows in row order (lanes 0, 1, 2, 3)
-                        const float v0 = __shfl(v, 0, 64), v1 = __shfl(v, 1, 64);
-                        const float v2 = __shfl(v, 2, 64), v3 = __shfl(v, 3, 64);
+                        const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+                        const float v1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 1));
+                        const float v2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 2));
+                        const float v3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 3));
                         if (lane == 0) {
                             const int row0 = kQuad * q;
                             float p = __builtin_fmaf(v0, v0, 0.0f);

@@ -68,6 +68,12 @@ __device__ __forceinline__ float xor_lane(float v) {
     return __uint_as_float(xor_lane<K>(__float_as_uint(v)));
 }
 
+// member K of the lane's quad (lanes 4 (l / 4) + K), by a DPP quad broadcast
+template <int K>
+__device__ __forceinline__ float quad_lane(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), K * 0x55, 0xf, 0xf, false));
+}
+
 // xor butterfly over groups of W lanes (offsets W / 2 .. 1); every lane of a group ends with the same value
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
