@@ -105,25 +105,43 @@ struct WTile {
 // ---- shared pieces -------------------------------------------------------------------------------------------------
 // whole-row activations, staged once per workgroup while the first weight steps are in flight: block J of column
 // col (chunk c = jb / 64, j = jb % 64) -> codes lq[2 (col * nbt + 64 c) + swz(2j), +1], record lrec[...]
+__device__ __forceinline__ void stage_one(const uint32_t (&wv)[9], int J, int nbt, uint4* lq, uint4* lrec) {
+    const int col = J / nbt, jb = J - col * nbt;
+    const int c = jb / kNB, j = jb - c * kNB;
+    int s0 = 0, s1 = 0;
+#pragma unroll
+    for (int i = 1; i <= 4; ++i) s0 = sdot4(static_cast<int>(wv[i]), 0x01010101, s0);
+#pragma unroll
+    for (int i = 5; i <= 8; ++i) s1 = sdot4(static_cast<int>(wv[i]), 0x01010101, s1);
+    uint4* q = lq + 2 * (col * nbt + c * kNB);
+    q[swz(2 * j)] = make_uint4(wv[1], wv[2], wv[3], wv[4]);
+    q[swz(2 * j + 1)] = make_uint4(wv[5], wv[6], wv[7], wv[8]);
+    lrec[col * nbt + c * kNB + swz(j)] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1),
+                                                    __float_as_uint(half_bits_to_float(wv[0])), 0u);
+}
+
+// Blocks are taken up to 4 per lane at a time, every load of a batch issued before the first is used (768 blocks of a
+// 12288-row at two columns: one batch per lane).  Measured against one block per iteration: 12288 x 4096 residual
+// 12.1 -> 12.0 us, 4096 x 4096 residual 7.1 -> 6.9 us (the weight loads issued before the staging hide most of it).
 __device__ __forceinline__ void stage_activations(const uint8_t* __restrict__ x, int nblocks, int nbt, uint4* lq,
                                                   uint4* lrec, int t, int nthreads) {
-    for (int J = t; J < nblocks; J += nthreads) {
-        const int col = J / nbt, jb = J - col * nbt;
-        const int c = jb / kNB, j = jb - c * kNB;
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
-        uint32_t wv[9];
+    constexpr int B = 4;
+    for (int J0 = t; J0 < nblocks; J0 += B * nthreads) {
+        uint32_t wv[B][9];
 #pragma unroll
-        for (int i = 0; i < 9; ++i) wv[i] = p[i];
-        int s0 = 0, s1 = 0;
+        for (int b = 0; b < B; ++b) {
+            const int J = J0 + b * nthreads;
+            if (J < nblocks) {
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
 #pragma unroll
-        for (int i = 1; i <= 4; ++i) s0 = sdot4(static_cast<int>(wv[i]), 0x01010101, s0);
+                for (int i = 0; i < 9; ++i) wv[b][i] = p[i];
+            }
+        }
 #pragma unroll
-        for (int i = 5; i <= 8; ++i) s1 = sdot4(static_cast<int>(wv[i]), 0x01010101, s1);
-        uint4* q = lq + 2 * (col * nbt + c * kNB);
-        q[swz(2 * j)] = make_uint4(wv[1], wv[2], wv[3], wv[4]);
-        q[swz(2 * j + 1)] = make_uint4(wv[5], wv[6], wv[7], wv[8]);
-        lrec[col * nbt + c * kNB + swz(j)] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1),
-                                                        __float_as_uint(half_bits_to_float(wv[0])), 0u);
+        for (int b = 0; b < B; ++b) {
+            const int J = J0 + b * nthreads;
+            if (J < nblocks) stage_one(wv[b], J, nbt, lq, lrec);
+        }
     }
 }
 
