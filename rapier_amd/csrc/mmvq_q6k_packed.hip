@@ -22,6 +22,10 @@
 // and a row's 16 lanes are reduced by the same xor butterfly (over hb: lane offsets 32, 16, 8, 4).  Lane ownership, per-lane accumulation order and the
 // reduction tree are those of the 16-row tiled kernel, so the results are bitwise the same, every column of an
 // ncols >= 2 call is bitwise the ncols = 1 result, and the residual variant is bitwise plain + res.
+//
+// Rows of 4096 (two chunks) with up to 4096 quads run a split-chunk variant: a quad's two chunks go to two waves of
+// one workgroup, the second hands its per-lane (scale, sum) pairs to the first through LDS, and the first continues
+// the same fma chain - the same bits with twice the waves in flight on grids that otherwise give a SIMD one wave.
 #include "rmi_common.h"
 
 #include <algorithm>
@@ -146,9 +150,10 @@ __device__ __forceinline__ void stage_activations(const uint8_t* __restrict__ x,
 }
 
 // one wave tile step of lane l: its half-block (row l / 16, half-block l % 16) against every column's staged chunk
+// (the tile's block scale d, the lane's sum acc[col]) of one step; the step adds fma(d, acc[col], tot[col])
 template <int NCOLS>
-__device__ __forceinline__ void accumulate_step(const WTile& wt, int lane, const uint4* lqc, const uint4* lrc, int xcs,
-                                                float (&tot)[NCOLS]) {
+__device__ __forceinline__ float step_acc(const WTile& wt, int lane, const uint4* lqc, const uint4* lrc, int xcs,
+                                          float (&acc)[NCOLS]) {
     const int hb = lane >> 2, b = hb >> 1, n = hb & 1;
     uint32_t Q[16], H[8];
 #pragma unroll
@@ -156,9 +161,7 @@ __device__ __forceinline__ void accumulate_step(const WTile& wt, int lane, const
 #pragma unroll
     for (int i = 0; i < 8; ++i) H[i] = wt.qh[i >> 2][i & 3];
     const uint32_t S0 = wt.sc.x, S1 = wt.sc.y;
-    const float d = half_bits_to_float(wt.d);
 
-    float acc[NCOLS];
 #pragma unroll
     for (int col = 0; col < NCOLS; ++col) acc[col] = 0.0f;
 #pragma unroll
@@ -186,8 +189,50 @@ __device__ __forceinline__ void accumulate_step(const WTile& wt, int lane, const
             }
         }
     }
+    return half_bits_to_float(wt.d);
+}
+
+template <int NCOLS>
+__device__ __forceinline__ void accumulate_step(const WTile& wt, int lane, const uint4* lqc, const uint4* lrc, int xcs,
+                                                float (&tot)[NCOLS]) {
+    float acc[NCOLS];
+    const float d = step_acc<NCOLS>(wt, lane, lqc, lrc, xcs, acc);
 #pragma unroll
     for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
+}
+
+// the finished quad q (lane 4 hb + r holds row 4 q + r's half-block sums): row sums, the residual, y and the quad's
+// sum of squares
+template <int NCOLS, bool RES>
+__device__ __forceinline__ void quad_epilogue(float (&tot)[NCOLS], int lane, int q, float* y, const float* res,
+                                              float* partials, int n_out) {
+    const int r = lane & 3, hb = lane >> 2;
+    const int row = kQuad * q + r;
+    const int np = (n_out + 3) / 4;
+#pragma unroll
+    for (int col = 0; col < NCOLS; ++col) {
+        float v = hb_sum(tot[col]);
+        tot[col] = 0.0f;
+        if constexpr (RES) {
+            if (row < n_out) v += res[static_cast<size_t>(col) * n_out + row];
+        }
+        if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v;
+        if constexpr (RES) {
+            // partial of the quad: squares of its rows in row order (lanes 0, 1, 2, 3)
+            const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+            const float v1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 1));
+            const float v2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 2));
+            const float v3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 3));
+            if (lane == 0) {
+                const int row0 = kQuad * q;
+                float p = __builtin_fmaf(v0, v0, 0.0f);
+                if (row0 + 1 < n_out) p = __builtin_fmaf(v1, v1, p);
+                if (row0 + 2 < n_out) p = __builtin_fmaf(v2, v2, p);
+                if (row0 + 3 < n_out) p = __builtin_fmaf(v3, v3, p);
+                partials[static_cast<size_t>(col) * np + q] = p;
+            }
+        }
+    }
 }
 
 // NW waves per workgroup share the staged activations: 4 for up to 4 columns (several workgroups per CU), 8 for the
@@ -229,7 +274,6 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
     stage_activations(x, NCOLS * nbt, nbt, lq, lrec, t, 64 * NW);
     __syncthreads();
 
-    const int r = lane & 3, hb = lane >> 2;
     float tot[NCOLS];
 #pragma unroll
     for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
@@ -244,37 +288,88 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
             if (f + D < nsteps) issue(f + D, buf[s]);
             accumulate_step<NCOLS>(cur, lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, tot);
 
-            if (c == nch - 1) {   // the quad's rows are complete
-                const int q = gw + qi * GW;
-                const int row = kQuad * q + r;
-                const int np = (n_out + 3) / 4;
+            if (c == nch - 1) quad_epilogue<NCOLS, RES>(tot, lane, gw + qi * GW, y, res, partials, n_out);
+        }
+    }
+}
+
+// Split-chunk variant for grids with few quads per CU: the S = nch / CS waves of a quad each take CS consecutive
+// chunks, every tile issued at the start, and hand their per-lane (d, acc) pairs through LDS to the quad's first
+// wave, which continues the fma chain over the chunks in order.  The operations and their order are those of one wave
+// walking every chunk, so the result is bitwise that of q6k_packed_gemv.  NW waves per workgroup = QW quads x S.
+template <int NCOLS, bool RES, int CS, int NW>
+__global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* __restrict__ wp,
+                                                                 const uint8_t* __restrict__ x, float* y,
+                                                                 const float* res, float* partials, int n_in,
+                                                                 int n_out) {
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
+    const int nbt = n_in / 32, xcs = nch * kNB;
+    uint4* lq = smem;
+    uint4* lrec = smem + 2 * NCOLS * nbt;
+    float* lx = reinterpret_cast<float*>(lrec + NCOLS * nbt);   // [wave][chunk][d, acc[0..NCOLS)][lane]
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    const int qg = w / S, sp = w - qg * S;
+    const int q = static_cast<int>(blockIdx.x) * QW + qg;
+    const bool live = qg < QW && q < nq;   // uniform across the wave
+
+    WTile buf[CS];
+    if (live) {
 #pragma unroll
-                for (int col = 0; col < NCOLS; ++col) {
-                    float v = hb_sum(tot[col]);
-                    tot[col] = 0.0f;
-                    if constexpr (RES) {
-                        if (row < n_out) v += res[static_cast<size_t>(col) * n_out + row];
-                    }
-                    if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v;
-                    if constexpr (RES) {
-                        // partial of the quad: squares of its rows in row order (lanes 0, 1, 2, 3)
-                        const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-                        const float v1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 1));
-                        const float v2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 2));
-                        const float v3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 3));
-                        if (lane == 0) {
-                            const int row0 = kQuad * q;
-                            float p = __builtin_fmaf(v0, v0, 0.0f);
-                            if (row0 + 1 < n_out) p = __builtin_fmaf(v1, v1, p);
-                            if (row0 + 2 < n_out) p = __builtin_fmaf(v2, v2, p);
-                            if (row0 + 3 < n_out) p = __builtin_fmaf(v3, v3, p);
-                            partials[static_cast<size_t>(col) * np + q] = p;
-                        }
-                    }
-                }
+        for (int c = 0; c < CS; ++c) {
+            const uint8_t* base = wp + (static_cast<size_t>(q) * nch + sp * CS + c) * kWaveTile;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                buf[c].ql[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * 1024 + 16 * lane));
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+                buf[c].qh[u] =
+                    __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + 4096 + u * 1024 + 16 * lane));
+            buf[c].sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
+            buf[c].d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (4 * (lane >> 3) + (lane & 3)));
+        }
+    }
+    stage_activations(x, NCOLS * nbt, nbt, lq, lrec, t, 64 * NW);
+    __syncthreads();
+
+    float acc[CS][NCOLS], dd[CS];
+    if (live) {
+#pragma unroll
+        for (int c = 0; c < CS; ++c) {
+            const int ch = sp * CS + c;
+            dd[c] = step_acc<NCOLS>(buf[c], lane, lq + 2 * ch * kNB, lrec + ch * kNB, xcs, acc[c]);
+        }
+        if (sp != 0) {
+#pragma unroll
+            for (int c = 0; c < CS; ++c) {
+                float* o = lx + (w * CS + c) * (NCOLS + 1) * 64 + lane;
+                o[0] = dd[c];
+#pragma unroll
+                for (int col = 0; col < NCOLS; ++col) o[(col + 1) * 64] = acc[c][col];
             }
         }
     }
+    __syncthreads();
+    if (!live || sp != 0) return;
+
+    float tot[NCOLS];
+#pragma unroll
+    for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CS; ++c)
+#pragma unroll
+        for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(dd[c], acc[c][col], tot[col]);
+    for (int s2 = 1; s2 < S; ++s2) {
+#pragma unroll
+        for (int c = 0; c < CS; ++c) {
+            const float* o = lx + ((w + s2) * CS + c) * (NCOLS + 1) * 64 + lane;
+            const float d = o[0];
+#pragma unroll
+            for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, o[(col + 1) * 64], tot[col]);
+        }
+    }
+    quad_epilogue<NCOLS, RES>(tot, lane, q, y, res, partials, n_out);
 }
 
 // ---- ingest GEMM: 8 / 16 columns on the 16-block 4x4x4 int8 MFMA -------------------------------------------------
@@ -508,10 +603,53 @@ int packed_grid(int nq) {
     return (waves + 3) / 4;
 }
 
+// split-chunk launch of one or two columns: chunks per wave (cs) and waves per workgroup (nw), or cs = 0 for the
+// one-wave-per-quad kernel
+struct SplitCfg {
+    int cs, nw;
+};
+
+size_t split_lds(int n_in, int ncols, SplitCfg c) {
+    return static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(c.nw) * c.cs * (ncols + 1) * 64 * 4;
+}
+
+// Measured per launch at n_in = 4096 (two columns; one column in brackets), one-wave-per-quad -> split:
+//   4096 rows   6.80 -> 6.12 us (5.98 -> 5.44) with 8 waves per workgroup (4 quads)
+//   10240 rows  9.99 -> 8.98 us (9.43 -> 9.05), 12352 rows 11.57 -> 10.31 us (10.4 -> 10.3) with 4 waves (2 quads)
+//   24576 rows 16.48 -> 16.54 us (15.97 -> 16.38), 248320 rows 122.5 -> 131.9 us, 12288 -> 4096 rows at n_in = 12288
+//   11.80 -> 12.3-13.4 us: these keep one wave per quad.
+// RMI_SPLIT_CS (0 = off, 1) and RMI_SPLIT_NW (4, 8) override the choice for every shape with n_in = 4096.
+SplitCfg split_cfg(int n_in, int n_out, int ncols) {
+    static const int env_cs = env_int("RMI_SPLIT_CS", -1), env_nw = env_int("RMI_SPLIT_NW", 0);
+    const int nch = n_in / kChunkElems, nq = (n_out + kQuad - 1) / kQuad;
+    if (ncols > 2 || nch != 2) return {0, 0};
+    if (env_cs >= 0) return env_cs == 1 && (env_nw == 4 || env_nw == 8) ? SplitCfg{1, env_nw} : SplitCfg{0, 0};
+    if (nq <= 1024) return {1, 8};
+    if (nq <= 4096) return {1, 4};
+    return {0, 0};
+}
+
+template <int NCOLS, bool RES, int CS, int NW>
+void launch_split_k(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
+                    int n_out, hipStream_t s) {
+    const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    const dim3 grid((nq + QW - 1) / QW), block(64 * NW);
+    hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW>), grid, block, split_lds(n_in, NCOLS, {CS, NW}), s,
+                       wp, x, y, res, partials, n_in, n_out);
+}
+
 template <int NCOLS, bool RES>
 void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
                    int n_out, hipStream_t s) {
     static const int depth = env_int("RMI_PACKED_DEPTH", 2);
+    if constexpr (NCOLS <= 2) {
+        const SplitCfg sc = split_cfg(n_in, n_out, NCOLS);
+        if (sc.cs) {
+            if (sc.nw == 8) return launch_split_k<NCOLS, RES, 1, 8>(wp, x, y, res, partials, n_in, n_out, s);
+            return launch_split_k<NCOLS, RES, 1, 4>(wp, x, y, res, partials, n_in, n_out, s);
+        }
+    }
     const int nq = (n_out + kQuad - 1) / kQuad;
     const size_t lds = static_cast<size_t>(NCOLS) * (n_in / 32) * 48;
     const dim3 grid(packed_grid(nq)), block(kThreads);
