@@ -389,30 +389,59 @@ __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__
     const int nchunk = min((pos[0] + t) / chunk_len + 1, kMaxChunks);
     const size_t cstride = static_cast<size_t>(n_kv) * kMaxSlots * REC;
     const float* base = ws + (static_cast<size_t>(kv) * kMaxSlots + qv) * REC;
+    // in flight together before the first barrier: the lane's first (m, l) record and the first 8 chunks' o values
+    float m0 = 0.0f, l0 = 0.0f;
+    if (d < nchunk) {
+        m0 = base[d * cstride];
+        l0 = base[d * cstride + 1];
+    }
+    float oa[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) oa[k] = k < nchunk ? base[k * cstride + 4 + d] : 0.0f;
     float mloc = -INFINITY;
-    for (int c = d; c < nchunk; c += HD) mloc = fmaxf(mloc, base[c * cstride]);
+    if (d < nchunk) mloc = fmaxf(mloc, m0);
+    for (int c = d + HD; c < nchunk; c += HD) mloc = fmaxf(mloc, base[c * cstride]);
     mloc = group_max<64>(mloc);
     if ((d & 63) == 0) red[d >> 6] = mloc;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     float lloc = 0.0f;
-    for (int c = d; c < nchunk; c += HD) {
+    if (d < nchunk) {
+        const float w = expf(m0 - M);
+        wts[d] = w;
+        lloc = __builtin_fmaf(l0, w, lloc);
+    }
+    for (int c = d + HD; c < nchunk; c += HD) {
         const float w = expf(base[c * cstride] - M);
         wts[c] = w;
         lloc = __builtin_fmaf(base[c * cstride + 1], w, lloc);
     }
     const float L = block_sum256(lloc, red);   // includes the barrier that publishes wts
+    // O over the chunks in order; each block of 8 o values is loaded while the previous block is summed
     float O = 0.0f;
-    int c = 0;
-    for (; c + 8 <= nchunk; c += 8) {
-        float oc[8];
+    if (nchunk < 8) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) oc[k] = base[(c + k) * cstride + 4 + d];
+        for (int k = 0; k < 8; ++k)
+            if (k < nchunk) O = __builtin_fmaf(wts[k], oa[k], O);
+    } else {
+        int c = 0;
+        for (; c + 8 <= nchunk; c += 8) {
+            const bool more = c + 16 <= nchunk;
+            float nx[8];
+            if (more) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) O = __builtin_fmaf(wts[c + k], oc[k], O);
+                for (int k = 0; k < 8; ++k) nx[k] = base[(c + 8 + k) * cstride + 4 + d];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) O = __builtin_fmaf(wts[c + k], oa[k], O);
+            if (more) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) oa[k] = nx[k];
+            }
+        }
+        for (; c < nchunk; ++c) O = __builtin_fmaf(wts[c], base[c * cstride + 4 + d], O);
     }
-    for (; c < nchunk; ++c) O = __builtin_fmaf(wts[c], base[c * cstride + 4 + d], O);
     const float o = O / L;
     const float v = o * sigmoid(g);
     if (y) y[static_cast<size_t>(t) * y_stride + h * HD + d] = v;

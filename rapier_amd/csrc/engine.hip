@@ -214,6 +214,21 @@ __global__ void accept_kernel(int* st, int* ring) {
     st[kDPos] = st[kPos] + 1;
 }
 
+// dst[i] = src[i], i < n, by one workgroup (dst and src do not overlap): every load of a lane's pass is issued before
+// its first store, where a strided loop would wait on each load in turn
+__device__ void wg_copy(float* __restrict__ dst, const float* __restrict__ src, int n) {
+    constexpr int kPer = 16;
+    const int nt = static_cast<int>(blockDim.x);
+    for (int b = static_cast<int>(threadIdx.x); b < n; b += kPer * nt) {
+        float v[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) v[k] = b + k * nt < n ? src[b + k * nt] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
+            if (b + k * nt < n) dst[b + k * nt] = v[k];
+    }
+}
+
 // after the draft: pick the candidate, advance (1 or 2 positions), apply the forced-acceptance override.  On accept the
 // last fed token is column 1, whose hidden moves to column 0, so that column 0 always holds the hidden of the token
 // before the current one (the input of a later first draft or ingest chunk).
@@ -221,8 +236,8 @@ __global__ void finalize_kernel(int* st, const int* ref_tok, const uint8_t* patt
                                 int np) {
     const int accept = st[kAccept];
     if (accept) {
-        for (int i = threadIdx.x; i < n; i += blockDim.x) hsave[i] = hsave[n + i];
-        for (int i = threadIdx.x; i < np; i += blockDim.x) hpart[i] = hpart[np + i];
+        wg_copy(hsave, hsave + n, n);
+        wg_copy(hpart, hpart + np, np);
     }
     if (threadIdx.x != 0) return;
     const int pos = min(st[kPos] + (accept ? 2 : 1), st[kMaxPos]);
@@ -263,8 +278,8 @@ __global__ void chunk_setup_kernel(const int* st, const int* prompt, int* cints,
 // after an ingest chunk: advance the position; column nc's hidden becomes column 0 (the next chunk's draft input, and
 // the hidden of the last token for the first draft of generation); with the head, the greedy token is current
 __global__ void chunk_finish_kernel(int* st, float* hsave, float* hpart, int n, int np, int nc, int head) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) hsave[i] = hsave[static_cast<size_t>(nc) * n + i];
-    for (int i = threadIdx.x; i < np; i += blockDim.x) hpart[i] = hpart[static_cast<size_t>(nc) * np + i];
+    wg_copy(hsave, hsave + static_cast<size_t>(nc) * n, n);
+    wg_copy(hpart, hpart + static_cast<size_t>(nc) * np, np);
     if (threadIdx.x == 0) {
         st[kPos] = st[kPos] + nc;
         if (head) st[kTok0] = st[kV0];

@@ -11,10 +11,23 @@
 namespace rmi {
 namespace {
 
+// A lane's first kPartialLoads partials are loaded before the first add (a strided loop waits on each load in turn);
+// the adds keep their order.
+constexpr int kPartialLoads = 8;
+
 __device__ float block_sum_partials(const float* __restrict__ p, int np) {
     __shared__ float red[4];
+    float pv[kPartialLoads];
+#pragma unroll
+    for (int k = 0; k < kPartialLoads; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        pv[k] = i < np ? p[i] : 0.0f;
+    }
     float s = 0.0f;
-    for (int i = threadIdx.x; i < np; i += 256) s += p[i];
+#pragma unroll
+    for (int k = 0; k < kPartialLoads; ++k)
+        if (threadIdx.x + 256 * k < np) s += pv[k];
+    for (int i = threadIdx.x + 256 * kPartialLoads; i < np; i += 256) s += p[i];
     s = group_sum<64>(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
@@ -159,10 +172,20 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
     __shared__ uint64_t red[4];
     const int c = blockIdx.y;
     l += static_cast<size_t>(c) * col_stride;
+    // four logits per lane per pass, loaded before the first compare (the max does not depend on the order)
+    constexpr int kPer = 4, kStride = kArgmaxBlocks * 256;
     uint64_t best = 0;
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += kArgmaxBlocks * 256) {
-        const uint64_t k = argmax_key(l[i], i);
-        best = k > best ? k : best;
+    for (int i0 = blockIdx.x * 256 + threadIdx.x; i0 < n; i0 += kPer * kStride) {
+        float v[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) v[k] = i0 + k * kStride < n ? l[i0 + k * kStride] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            if (i0 + k * kStride < n) {
+                const uint64_t key = argmax_key(v[k], i0 + k * kStride);
+                best = key > best ? key : best;
+            }
+        }
     }
     best = key_max64(best);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
