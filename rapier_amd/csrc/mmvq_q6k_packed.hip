@@ -23,9 +23,9 @@
 // reduction tree are those of the 16-row tiled kernel, so the results are bitwise the same, every column of an
 // ncols >= 2 call is bitwise the ncols = 1 result, and the residual variant is bitwise plain + res.
 //
-// Rows of 4096 (two chunks) with up to 4096 quads run a split-chunk variant: a quad's two chunks go to two waves of
-// one workgroup, the second hands its per-lane (scale, sum) pairs to the first through LDS, and the first continues
-// the same fma chain - the same bits with twice the waves in flight on grids that otherwise give a SIMD one wave.
+// Rows of 4096 and 8192 (two and four chunks) run a split-chunk variant: a quad's chunks go to one or two waves of one
+// workgroup, every tile issued at the start behind the activation loads; a second wave hands its per-lane (scale,
+// sum) pairs to the first through LDS, which continues the same fma chain - the same bits, more waves in flight.
 #include "rmi_common.h"
 
 #include <algorithm>
@@ -314,11 +314,27 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
     const int q = static_cast<int>(blockIdx.x) * QW + qg;
     const bool live = qg < QW && q < nq;   // uniform across the wave
 
+    // the activation loads go first: a wave's loads return in issue order, so a stage issued after the weight tiles
+    // would wait for all of them before the first step could start
+    constexpr int SB = 4;
+    const int nblocks = NCOLS * nbt;
+    uint32_t sv[SB][9];
+#pragma unroll
+    for (int b = 0; b < SB; ++b) {   // unconditional (clamped) loads: no branch for the compiler to wait inside
+        const int J = min(t + b * 64 * NW, nblocks - 1);
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) sv[b][i] = p[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // the stage's loads stay ahead of the weight tiles
+    // unconditional loads (a wave past the last quad reads the last quad's tiles and discards them): with the loads in
+    // a branch the compiler waits for the stage as if no tile had been issued after it
     WTile buf[CS];
-    if (live) {
+    const int qld = min(q, nq - 1);
+    {
 #pragma unroll
         for (int c = 0; c < CS; ++c) {
-            const uint8_t* base = wp + (static_cast<size_t>(q) * nch + sp * CS + c) * kWaveTile;
+            const uint8_t* base = wp + (static_cast<size_t>(qld) * nch + sp * CS + c) * kWaveTile;
 #pragma unroll
             for (int u = 0; u < 4; ++u)
                 buf[c].ql[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * 1024 + 16 * lane));
@@ -330,7 +346,23 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
             buf[c].d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (4 * (lane >> 3) + (lane & 3)));
         }
     }
-    stage_activations(x, NCOLS * nbt, nbt, lq, lrec, t, 64 * NW);
+    // Every load above is issued before any loaded value is used: the tiles' fp16 scales are or-ed with a zero that
+    // only exists after this point (the compiler otherwise converts each scale right after its load, and the wait for
+    // it stalls the remaining loads)
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+#pragma unroll
+    for (int b = 0; b < SB; ++b) {
+        const int J = t + b * 64 * NW;
+        if (J < nblocks) stage_one(sv[b], J, nbt, lq, lrec);
+    }
+    for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
+        uint32_t wv[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) wv[i] = p[i];
+        stage_one(wv, J, nbt, lq, lrec);
+    }
     __syncthreads();
 
     float acc[CS][NCOLS], dd[CS];
@@ -338,6 +370,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
 #pragma unroll
         for (int c = 0; c < CS; ++c) {
             const int ch = sp * CS + c;
+            buf[c].d |= static_cast<uint32_t>(zero);
             dd[c] = step_acc<NCOLS>(buf[c], lane, lq + 2 * ch * kNB, lrec + ch * kNB, xcs, acc[c]);
         }
         if (sp != 0) {
@@ -613,20 +646,28 @@ size_t split_lds(int n_in, int ncols, SplitCfg c) {
     return static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(c.nw) * c.cs * (ncols + 1) * 64 * 4;
 }
 
-// Measured per launch at n_in = 4096 (two columns; one column in brackets), one-wave-per-quad -> split:
-//   4096 rows   6.80 -> 6.12 us (5.98 -> 5.44) with 8 waves per workgroup (4 quads)
-//   10240 rows  9.99 -> 8.98 us (9.43 -> 9.05), 12352 rows 11.57 -> 10.31 us (10.4 -> 10.3) with 4 waves (2 quads)
-//   24576 rows 16.48 -> 16.54 us (15.97 -> 16.38), 248320 rows 122.5 -> 131.9 us, 12288 -> 4096 rows at n_in = 12288
-//   11.80 -> 12.3-13.4 us: these keep one wave per quad.
-// RMI_SPLIT_CS (0 = off, 1) and RMI_SPLIT_NW (4, 8) override the choice for every shape with n_in = 4096.
+// Measured per launch (two columns; one column in brackets), one-wave-per-quad kernel -> split:
+//   n_in 4096:  4096 rows 6.80 -> 5.71 us (8 waves per workgroup), 10240 rows 9.92 -> 8.98 us (9.0 -> 8.2),
+//               12352 rows 11.35 -> 10.23 us (10.3 -> 9.4), 24576 rows 16.58 -> 16.58 us (15.5 -> 15.1) with one
+//               chunk per wave; the 248320-row lm_head 123.9 -> 120.7 us (118.7 -> 115.1) with one quad per wave
+//   n_in 8192:  4096 rows 9.15 -> 8.64 us (8.10 -> 7.78), one quad (four chunks) per two waves
+//   n_in 12288: 4096 rows 11.6 -> 11.8-13.3 us for every split tried, so these keep one wave per quad
+// RMI_SPLIT_CS / RMI_SPLIT_NW override the choice (CS 0 = off; CS 1 or 2 with NW 4, or CS 1 with NW 8).
 SplitCfg split_cfg(int n_in, int n_out, int ncols) {
     static const int env_cs = env_int("RMI_SPLIT_CS", -1), env_nw = env_int("RMI_SPLIT_NW", 0);
     const int nch = n_in / kChunkElems, nq = (n_out + kQuad - 1) / kQuad;
-    if (ncols > 2 || nch != 2) return {0, 0};
-    if (env_cs >= 0) return env_cs == 1 && (env_nw == 4 || env_nw == 8) ? SplitCfg{1, env_nw} : SplitCfg{0, 0};
-    if (nq <= 1024) return {1, 8};
-    if (nq <= 4096) return {1, 4};
-    return {0, 0};
+    if (ncols > 2) return {0, 0};
+    SplitCfg c{0, 0};
+    if (nch == 2) c = nq <= 1024 ? SplitCfg{1, 8} : nq <= 8192 ? SplitCfg{1, 4} : SplitCfg{2, 4};
+    else if (nch == 4) c = {2, 4};
+    if (env_cs >= 0) {
+        const bool known = (env_cs == 1 && (env_nw == 4 || env_nw == 8)) || (env_cs == 2 && env_nw == 4);
+        c = known ? SplitCfg{env_cs, env_nw} : SplitCfg{0, 0};
+    }
+    if (c.cs == 0 || nch % c.cs != 0) return {0, 0};
+    const int S = nch / c.cs;
+    if (S > c.nw || c.nw % S != 0 || split_lds(n_in, ncols, c) > kMaxStageBytes) return {0, 0};
+    return c;
 }
 
 template <int NCOLS, bool RES, int CS, int NW>
@@ -646,6 +687,7 @@ void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* r
     if constexpr (NCOLS <= 2) {
         const SplitCfg sc = split_cfg(n_in, n_out, NCOLS);
         if (sc.cs) {
+            if (sc.cs == 2) return launch_split_k<NCOLS, RES, 2, 4>(wp, x, y, res, partials, n_in, n_out, s);
             if (sc.nw == 8) return launch_split_k<NCOLS, RES, 1, 8>(wp, x, y, res, partials, n_in, n_out, s);
             return launch_split_k<NCOLS, RES, 1, 4>(wp, x, y, res, partials, n_in, n_out, s);
         }
