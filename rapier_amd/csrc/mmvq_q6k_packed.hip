@@ -23,9 +23,10 @@
 // reduction tree are those of the 16-row tiled kernel, so the results are bitwise the same, every column of an
 // ncols >= 2 call is bitwise the ncols = 1 result, and the residual variant is bitwise plain + res.
 //
-// Rows of 4096 and 8192 (two and four chunks) run a split-chunk variant: a quad's chunks go to one or two waves of one
-// workgroup, every tile issued at the start behind the activation loads; a second wave hands its per-lane (scale,
-// sum) pairs to the first through LDS, which continues the same fma chain - the same bits, more waves in flight.
+// Rows of 4096, 8192 and 12288 (two, four and six chunks) run a split-chunk variant: a quad's chunks go to one or two
+// waves of one workgroup, in straight-line code with the tiles issued behind the activation loads (all at once, or two
+// ahead of the step for six chunks); a second wave hands its per-lane (scale, sum) pairs to the first through LDS,
+// which continues the same fma chain - the same bits, more loads in flight.
 #include "rmi_common.h"
 
 #include <algorithm>
@@ -103,7 +104,7 @@ struct WTile {
     u32x4 ql[4];
     u32x4 qh[2];
     uint2 sc;
-    uint32_t d;
+    uint32_t d;   // the dword holding the lane's fp16 block scale (half lane & 1)
 };
 
 // ---- shared pieces -------------------------------------------------------------------------------------------------
@@ -149,6 +150,14 @@ __device__ __forceinline__ void stage_activations(const uint8_t* __restrict__ x,
     }
 }
 
+// Marks the point where a tile's registers are first used: no computation on them moves above it and no load moves
+// across it, so the wait placed here covers this tile and the loads issued before it only (loads complete in issue
+// order).  Without it the compiler converts a tile's scale right after its load and the wait stalls later loads.
+__device__ __forceinline__ void pin_tile(WTile& w) {
+    asm volatile("" : "+v"(w.ql[0]), "+v"(w.ql[1]), "+v"(w.ql[2]), "+v"(w.ql[3]), "+v"(w.qh[0]), "+v"(w.qh[1]),
+                 "+v"(w.sc), "+v"(w.d)::"memory");
+}
+
 // one wave tile step of lane l: its half-block (row l / 16, half-block l % 16) against every column's staged chunk
 // (the tile's block scale d, the lane's sum acc[col]) of one step; the step adds fma(d, acc[col], tot[col])
 template <int NCOLS>
@@ -189,7 +198,7 @@ __device__ __forceinline__ float step_acc(const WTile& wt, int lane, const uint4
             }
         }
     }
-    return half_bits_to_float(wt.d);
+    return half_bits_to_float((lane & 1) ? wt.d >> 16 : wt.d & 0xffffu);
 }
 
 template <int NCOLS>
@@ -265,7 +274,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
         for (int u = 0; u < 2; ++u)
             b.qh[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + 4096 + u * 1024 + 16 * lane));
         b.sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
-        b.d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (4 * (lane >> 3) + (lane & 3)));
+        b.d = *reinterpret_cast<const uint32_t*>(base + 6656 + 4 * (2 * (lane >> 3) + ((lane & 3) >> 1)));
     };
 #pragma unroll
     for (int s = 0; s < D; ++s)
@@ -297,7 +306,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
 // chunks, every tile issued at the start, and hand their per-lane (d, acc) pairs through LDS to the quad's first
 // wave, which continues the fma chain over the chunks in order.  The operations and their order are those of one wave
 // walking every chunk, so the result is bitwise that of q6k_packed_gemv.  NW waves per workgroup = QW quads x S.
-template <int NCOLS, bool RES, int CS, int NW>
+template <int NCOLS, bool RES, int CS, int NW, int PD = CS>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* __restrict__ wp,
                                                                  const uint8_t* __restrict__ x, float* y,
                                                                  const float* res, float* partials, int n_in,
@@ -328,29 +337,26 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
     }
     __builtin_amdgcn_sched_barrier(0);   // the stage's loads stay ahead of the weight tiles
     // unconditional loads (a wave past the last quad reads the last quad's tiles and discards them): with the loads in
-    // a branch the compiler waits for the stage as if no tile had been issued after it
+    // a branch the compiler waits for the stage as if no tile had been issued after it.  PD tiles are in flight ahead
+    // of the step that uses them, issued tile by tile in order.
     WTile buf[CS];
     const int qld = min(q, nq - 1);
-    {
+    auto issue = [&](int c) {
+        const uint8_t* base = wp + (static_cast<size_t>(qld) * nch + sp * CS + c) * kWaveTile;
 #pragma unroll
-        for (int c = 0; c < CS; ++c) {
-            const uint8_t* base = wp + (static_cast<size_t>(qld) * nch + sp * CS + c) * kWaveTile;
+        for (int u = 0; u < 4; ++u)
+            buf[c].ql[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * 1024 + 16 * lane));
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                buf[c].ql[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * 1024 + 16 * lane));
+        for (int u = 0; u < 2; ++u)
+            buf[c].qh[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + 4096 + u * 1024 + 16 * lane));
+        buf[c].sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
+        buf[c].d = *reinterpret_cast<const uint32_t*>(base + 6656 + 4 * (2 * (lane >> 3) + ((lane & 3) >> 1)));
+    };
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
-                buf[c].qh[u] =
-                    __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + 4096 + u * 1024 + 16 * lane));
-            buf[c].sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
-            buf[c].d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (4 * (lane >> 3) + (lane & 3)));
-        }
+    for (int c = 0; c < PD && c < CS; ++c) {
+        issue(c);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    // Every load above is issued before any loaded value is used: the tiles' fp16 scales are or-ed with a zero that
-    // only exists after this point (the compiler otherwise converts each scale right after its load, and the wait for
-    // it stalls the remaining loads)
-    int zero;
-    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
 #pragma unroll
     for (int b = 0; b < SB; ++b) {
         const int J = t + b * 64 * NW;
@@ -370,8 +376,13 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
 #pragma unroll
         for (int c = 0; c < CS; ++c) {
             const int ch = sp * CS + c;
-            buf[c].d |= static_cast<uint32_t>(zero);
+            pin_tile(buf[c]);
             dd[c] = step_acc<NCOLS>(buf[c], lane, lq + 2 * ch * kNB, lrec + ch * kNB, xcs, acc[c]);
+            if (c + PD < CS) {
+                __builtin_amdgcn_sched_barrier(0);
+                issue(c + PD);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         if (sp != 0) {
 #pragma unroll
@@ -642,8 +653,11 @@ struct SplitCfg {
     int cs, nw;
 };
 
+// the stage, plus the (scale, sum) hand-over when a quad has more than one wave
 size_t split_lds(int n_in, int ncols, SplitCfg c) {
-    return static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(c.nw) * c.cs * (ncols + 1) * 64 * 4;
+    const bool handover = n_in / kChunkElems > c.cs;
+    return static_cast<size_t>(ncols) * (n_in / 32) * 48 +
+           (handover ? static_cast<size_t>(c.nw) * c.cs * (ncols + 1) * 64 * 4 : 0);
 }
 
 // Measured per launch (two columns; one column in brackets), one-wave-per-quad kernel -> split:
@@ -651,7 +665,8 @@ size_t split_lds(int n_in, int ncols, SplitCfg c) {
 //               12352 rows 11.35 -> 10.23 us (10.3 -> 9.4), 24576 rows 16.58 -> 16.58 us (15.5 -> 15.1) with one
 //               chunk per wave; the 248320-row lm_head 123.9 -> 120.7 us (118.7 -> 115.1) with one quad per wave
 //   n_in 8192:  4096 rows 9.15 -> 8.64 us (8.10 -> 7.78), one quad (four chunks) per two waves
-//   n_in 12288: 4096 rows 11.6 -> 11.8-13.3 us for every split tried, so these keep one wave per quad
+//   n_in 12288: 4096 rows 11.8 -> 11.0 us (10.5 -> 9.9) with one quad (six chunks) per wave and two tiles in flight
+//               ahead of the step (three: 11.4 us, all six: 13.2 us; two waves per quad: 11.2 us)
 // RMI_SPLIT_CS / RMI_SPLIT_NW override the choice (CS 0 = off; CS 1 or 2 with NW 4, or CS 1 with NW 8).
 SplitCfg split_cfg(int n_in, int n_out, int ncols) {
     static const int env_cs = env_int("RMI_SPLIT_CS", -1), env_nw = env_int("RMI_SPLIT_NW", 0);
@@ -660,6 +675,7 @@ SplitCfg split_cfg(int n_in, int n_out, int ncols) {
     SplitCfg c{0, 0};
     if (nch == 2) c = nq <= 1024 ? SplitCfg{1, 8} : nq <= 8192 ? SplitCfg{1, 4} : SplitCfg{2, 4};
     else if (nch == 4) c = {2, 4};
+    else if (nch == 6) c = {6, 4};
     if (env_cs >= 0) {
         const bool known = (env_cs == 1 && (env_nw == 4 || env_nw == 8)) || (env_cs == 2 && env_nw == 4);
         c = known ? SplitCfg{env_cs, env_nw} : SplitCfg{0, 0};
@@ -670,13 +686,13 @@ SplitCfg split_cfg(int n_in, int n_out, int ncols) {
     return c;
 }
 
-template <int NCOLS, bool RES, int CS, int NW>
+template <int NCOLS, bool RES, int CS, int NW, int PD = CS>
 void launch_split_k(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
                     int n_out, hipStream_t s) {
     const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
     const int nq = (n_out + kQuad - 1) / kQuad;
     const dim3 grid((nq + QW - 1) / QW), block(64 * NW);
-    hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW>), grid, block, split_lds(n_in, NCOLS, {CS, NW}), s,
+    hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW, PD>), grid, block, split_lds(n_in, NCOLS, {CS, NW}), s,
                        wp, x, y, res, partials, n_in, n_out);
 }
 
@@ -687,6 +703,7 @@ void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* r
     if constexpr (NCOLS <= 2) {
         const SplitCfg sc = split_cfg(n_in, n_out, NCOLS);
         if (sc.cs) {
+            if (sc.cs == 6) return launch_split_k<NCOLS, RES, 6, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
             if (sc.cs == 2) return launch_split_k<NCOLS, RES, 2, 4>(wp, x, y, res, partials, n_in, n_out, s);
             if (sc.nw == 8) return launch_split_k<NCOLS, RES, 1, 8>(wp, x, y, res, partials, n_in, n_out, s);
             return launch_split_k<NCOLS, RES, 1, 4>(wp, x, y, res, partials, n_in, n_out, s);

@@ -65,8 +65,8 @@ def test_packed_bitwise_equals_16_row_tiles(orc, rmi, n_in, n_out):
     assert np.array_equal(host(yp).view(np.uint32), host(yt).view(np.uint32))
 
 
-@pytest.mark.parametrize("n_in,n_out,ncols", [(12288, 4096, 2), (4096, 4096, 1), (4096, 4096, 2), (8192, 1001, 2),
-                                              (2048, 1001, 3), (4096, 520, 5)])
+@pytest.mark.parametrize("n_in,n_out,ncols", [(12288, 4096, 2), (12288, 1001, 1), (4096, 4096, 1), (4096, 4096, 2),
+                                              (8192, 1001, 2), (2048, 1001, 3), (4096, 520, 5)])
 def test_packed_residual(orc, rmi, n_in, n_out, ncols):
     w = orc.gen_q6k(n_out, n_in, seed=n_out + ncols)
     xq = orc.quantize_q8_1(orc.normal(ncols * n_in, seed=n_in + 2), n_in, ncols)
