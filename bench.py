@@ -178,7 +178,7 @@ def run_verify_gemv(args):
             "rotated_bytes": reps * (q6_bytes(UG_ROWS, UG_IN) + q6_bytes(DN_ROWS, DN_IN)),
         },
         "roofline": {
-            "kernel": "q6k_packed_gemv_split<2,false,1,4> (up||gate 24576x4096, ncols=2, packed wave-tile layout)",
+            "kernel": "q6k_packed_gemv_stream<2,false,2,2,4,2> (up||gate 24576x4096, ncols=2, packed wave-tile layout)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

@@ -31,6 +31,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <string>
 
 namespace rmi {
 namespace {
@@ -156,6 +157,19 @@ __device__ __forceinline__ void stage_activations(const uint8_t* __restrict__ x,
 __device__ __forceinline__ void pin_tile(WTile& w) {
     asm volatile("" : "+v"(w.ql[0]), "+v"(w.ql[1]), "+v"(w.ql[2]), "+v"(w.ql[3]), "+v"(w.qh[0]), "+v"(w.qh[1]),
                  "+v"(w.sc), "+v"(w.d)::"memory");
+}
+
+// pin_tile that also keeps the previous step's arithmetic above it (the running sums pass through the asm): without it
+// the compiler may hoist this pin, and the wait for this tile, above the previous step's compute
+template <int NCOLS>
+__device__ __forceinline__ void pin_tile_after(WTile& w, float (&tot)[NCOLS]) {
+    static_assert(NCOLS == 1 || NCOLS == 2, "one or two columns");
+    if constexpr (NCOLS == 1)
+        asm volatile("" : "+v"(w.ql[0]), "+v"(w.ql[1]), "+v"(w.ql[2]), "+v"(w.ql[3]), "+v"(w.qh[0]), "+v"(w.qh[1]),
+                     "+v"(w.sc), "+v"(w.d), "+v"(tot[0])::"memory");
+    else
+        asm volatile("" : "+v"(w.ql[0]), "+v"(w.ql[1]), "+v"(w.ql[2]), "+v"(w.ql[3]), "+v"(w.qh[0]), "+v"(w.qh[1]),
+                     "+v"(w.sc), "+v"(w.d), "+v"(tot[0]), "+v"(tot[1])::"memory");
 }
 
 // one wave tile step of lane l: its half-block (row l / 16, half-block l % 16) against every column's staged chunk
@@ -306,7 +320,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
 // chunks, every tile issued at the start, and hand their per-lane (d, acc) pairs through LDS to the quad's first
 // wave, which continues the fma chain over the chunks in order.  The operations and their order are those of one wave
 // walking every chunk, so the result is bitwise that of q6k_packed_gemv.  NW waves per workgroup = QW quads x S.
-template <int NCOLS, bool RES, int CS, int NW, int PD = CS>
+template <int NCOLS, bool RES, int CS, int NW>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* __restrict__ wp,
                                                                  const uint8_t* __restrict__ x, float* y,
                                                                  const float* res, float* partials, int n_in,
@@ -337,8 +351,8 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
     }
     __builtin_amdgcn_sched_barrier(0);   // the stage's loads stay ahead of the weight tiles
     // unconditional loads (a wave past the last quad reads the last quad's tiles and discards them): with the loads in
-    // a branch the compiler waits for the stage as if no tile had been issued after it.  PD tiles are in flight ahead
-    // of the step that uses them, issued tile by tile in order.
+    // a branch the compiler waits for the stage as if no tile had been issued after it.  Every tile is issued here,
+    // tile by tile in order.
     WTile buf[CS];
     const int qld = min(q, nq - 1);
     auto issue = [&](int c) {
@@ -353,7 +367,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
         buf[c].d = *reinterpret_cast<const uint32_t*>(base + 6656 + 4 * (2 * (lane >> 3) + ((lane & 3) >> 1)));
     };
 #pragma unroll
-    for (int c = 0; c < PD && c < CS; ++c) {
+    for (int c = 0; c < CS; ++c) {
         issue(c);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -378,11 +392,6 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
             const int ch = sp * CS + c;
             pin_tile(buf[c]);
             dd[c] = step_acc<NCOLS>(buf[c], lane, lq + 2 * ch * kNB, lrec + ch * kNB, xcs, acc[c]);
-            if (c + PD < CS) {
-                __builtin_amdgcn_sched_barrier(0);
-                issue(c + PD);
-                __builtin_amdgcn_sched_barrier(0);
-            }
         }
         if (sp != 0) {
 #pragma unroll
@@ -414,6 +423,92 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
         }
     }
     quad_epilogue<NCOLS, RES>(tot, lane, q, y, res, partials, n_out);
+}
+
+// Stream variant: one wave per quad and QPW quads per wave (quads q, q + G, q + 2G, ... with G the grid's wave count),
+// all in straight-line code with PD tiles in flight ahead of the step that uses them.  Every wave is resident from the
+// start (a wave per quad would leave a tail of waves waiting for slots), and the per-quad arithmetic is that of
+// q6k_packed_gemv: the same bits.
+template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD>
+__global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t* __restrict__ wp,
+                                                                  const uint8_t* __restrict__ x, float* y,
+                                                                  const float* res, float* partials, int n_in,
+                                                                  int n_out) {
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int nbt = n_in / 32, xcs = NCH * kNB;
+    uint4* lq = smem;
+    uint4* lrec = smem + 2 * NCOLS * nbt;
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    const int G = static_cast<int>(gridDim.x) * NW;
+    const int q0 = static_cast<int>(blockIdx.x) * NW + (t >> 6);
+
+    // activation loads first (a wave's loads return in issue order), clamped so that none sits in a branch
+    constexpr int SB = 4;
+    const int nblocks = NCOLS * nbt;
+    uint32_t sv[SB][9];
+#pragma unroll
+    for (int b = 0; b < SB; ++b) {
+        const int J = min(t + b * 64 * NW, nblocks - 1);
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) sv[b][i] = p[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // tile i = (quad j = i / NCH, chunk i % NCH); a quad past the last reads the last quad's tiles and discards them
+    constexpr int T = QPW * NCH;
+    WTile buf[T];
+    auto issue = [&](int i) {
+        const int j = i / NCH, c = i - j * NCH;
+        const int qq = min(q0 + j * G, nq - 1);
+        const uint8_t* base = wp + (static_cast<size_t>(qq) * NCH + c) * kWaveTile;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            buf[i].ql[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * 1024 + 16 * lane));
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            buf[i].qh[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + 4096 + u * 1024 + 16 * lane));
+        buf[i].sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
+        buf[i].d = *reinterpret_cast<const uint32_t*>(base + 6656 + 4 * (2 * (lane >> 3) + ((lane & 3) >> 1)));
+    };
+#pragma unroll
+    for (int i = 0; i < PD && i < T; ++i) {
+        issue(i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int b = 0; b < SB; ++b) {
+        const int J = t + b * 64 * NW;
+        if (J < nblocks) stage_one(sv[b], J, nbt, lq, lrec);
+    }
+    for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
+        uint32_t wv[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) wv[i] = p[i];
+        stage_one(wv, J, nbt, lq, lrec);
+    }
+    __syncthreads();
+
+    float tot[NCOLS];
+#pragma unroll
+    for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+        const int j = i / NCH, c = i - (i / NCH) * NCH;
+        pin_tile_after<NCOLS>(buf[i], tot);
+        float acc[NCOLS];
+        const float d = step_acc<NCOLS>(buf[i], lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, acc);
+#pragma unroll
+        for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
+        if (i + PD < T) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(i + PD);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (c == NCH - 1 && q0 + j * G < nq) quad_epilogue<NCOLS, RES>(tot, lane, q0 + j * G, y, res, partials, n_out);
+    }
 }
 
 // ---- ingest GEMM: 8 / 16 columns on the 16-block 4x4x4 int8 MFMA -------------------------------------------------
@@ -647,53 +742,60 @@ int packed_grid(int nq) {
     return (waves + 3) / 4;
 }
 
-// split-chunk launch of one or two columns: chunks per wave (cs) and waves per workgroup (nw), or cs = 0 for the
-// one-wave-per-quad kernel
-struct SplitCfg {
-    int cs, nw;
+// Kernel choice for one or two columns (more columns, and shapes without an entry, run the pipelined loop kernel).
+// Measured per launch at two columns (one column in brackets) against the loop kernel:
+//   n_in 4096:  4096 rows 6.80 -> 5.71 us (split, 8 waves per workgroup), 10240 rows 9.92 -> 8.98 us (9.0 -> 8.2),
+//               12352 rows 11.35 -> 10.23 us (10.3 -> 9.4) (split, 4 waves); 24576 rows 16.6 -> 16.1 us
+//               (15.5 -> 14.8) and the 248320-row lm_head 123.9 -> 117.7 us (stream, two quads per wave, both tiles
+//               of the next quad issued while the current one is summed; three quads per wave: 16.2 us)
+//   n_in 8192:  4096 rows 9.15 -> 8.64 us (8.10 -> 7.78) (split, a quad's four chunks on two waves)
+//   n_in 12288: 4096 rows 11.8 -> 10.4 us (10.5 -> 9.6) (stream, one quad per wave, two tiles ahead; three ahead
+//               10.8 us, all six 13.2 us, two quads per wave 13.8 us, a quad on two waves 11.2 us)
+// RMI_PACKED_KERNEL=loop runs the loop kernel for every shape.
+struct PackedCfg {
+    enum Kind { kLoop, kSplit, kStream } kind;
+    int cs, nw;   // split: chunks per wave, waves per workgroup
 };
 
-// the stage, plus the (scale, sum) hand-over when a quad has more than one wave
-size_t split_lds(int n_in, int ncols, SplitCfg c) {
-    const bool handover = n_in / kChunkElems > c.cs;
-    return static_cast<size_t>(ncols) * (n_in / 32) * 48 +
-           (handover ? static_cast<size_t>(c.nw) * c.cs * (ncols + 1) * 64 * 4 : 0);
-}
-
-// Measured per launch (two columns; one column in brackets), one-wave-per-quad kernel -> split:
-//   n_in 4096:  4096 rows 6.80 -> 5.71 us (8 waves per workgroup), 10240 rows 9.92 -> 8.98 us (9.0 -> 8.2),
-//               12352 rows 11.35 -> 10.23 us (10.3 -> 9.4), 24576 rows 16.58 -> 16.58 us (15.5 -> 15.1) with one
-//               chunk per wave; the 248320-row lm_head 123.9 -> 120.7 us (118.7 -> 115.1) with one quad per wave
-//   n_in 8192:  4096 rows 9.15 -> 8.64 us (8.10 -> 7.78), one quad (four chunks) per two waves
-//   n_in 12288: 4096 rows 11.8 -> 11.0 us (10.5 -> 9.9) with one quad (six chunks) per wave and two tiles in flight
-//               ahead of the step (three: 11.4 us, all six: 13.2 us; two waves per quad: 11.2 us)
-// RMI_SPLIT_CS / RMI_SPLIT_NW override the choice (CS 0 = off; CS 1 or 2 with NW 4, or CS 1 with NW 8).
-SplitCfg split_cfg(int n_in, int n_out, int ncols) {
-    static const int env_cs = env_int("RMI_SPLIT_CS", -1), env_nw = env_int("RMI_SPLIT_NW", 0);
+PackedCfg packed_cfg(int n_in, int n_out, int ncols) {
+    static const bool loop_only = [] {
+        const char* v = std::getenv("RMI_PACKED_KERNEL");
+        return v && std::string(v) == "loop";
+    }();
     const int nch = n_in / kChunkElems, nq = (n_out + kQuad - 1) / kQuad;
-    if (ncols > 2) return {0, 0};
-    SplitCfg c{0, 0};
-    if (nch == 2) c = nq <= 1024 ? SplitCfg{1, 8} : nq <= 8192 ? SplitCfg{1, 4} : SplitCfg{2, 4};
-    else if (nch == 4) c = {2, 4};
-    else if (nch == 6) c = {6, 4};
-    if (env_cs >= 0) {
-        const bool known = (env_cs == 1 && (env_nw == 4 || env_nw == 8)) || (env_cs == 2 && env_nw == 4);
-        c = known ? SplitCfg{env_cs, env_nw} : SplitCfg{0, 0};
+    if (loop_only || ncols > 2) return {PackedCfg::kLoop, 0, 0};
+    if (nch == 2) {
+        if (nq <= 1024) return {PackedCfg::kSplit, 1, 8};
+        if (nq <= 4096) return {PackedCfg::kSplit, 1, 4};
+        return {PackedCfg::kStream, 0, 0};
     }
-    if (c.cs == 0 || nch % c.cs != 0) return {0, 0};
-    const int S = nch / c.cs;
-    if (S > c.nw || c.nw % S != 0 || split_lds(n_in, ncols, c) > kMaxStageBytes) return {0, 0};
-    return c;
+    if (nch == 4) return {PackedCfg::kSplit, 2, 4};
+    if (nch == 6) return {PackedCfg::kStream, 0, 0};
+    return {PackedCfg::kLoop, 0, 0};
 }
 
-template <int NCOLS, bool RES, int CS, int NW, int PD = CS>
-void launch_split_k(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                    int n_out, hipStream_t s) {
+// the stage plus the (scale, sum) hand-over of the quads' second waves
+size_t split_lds(int n_in, int ncols, int cs, int nw) {
+    return static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(nw) * cs * (ncols + 1) * 64 * 4;
+}
+
+template <int NCOLS, bool RES, int CS, int NW>
+void launch_split(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
+                  int n_out, hipStream_t s) {
     const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
     const int nq = (n_out + kQuad - 1) / kQuad;
     const dim3 grid((nq + QW - 1) / QW), block(64 * NW);
-    hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW, PD>), grid, block, split_lds(n_in, NCOLS, {CS, NW}), s,
+    hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW>), grid, block, split_lds(n_in, NCOLS, CS, NW), s,
                        wp, x, y, res, partials, n_in, n_out);
+}
+
+template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD>
+void launch_stream(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
+                   int n_out, hipStream_t s) {
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    const dim3 grid((nq + NW * QPW - 1) / (NW * QPW)), block(64 * NW);
+    hipLaunchKernelGGL((q6k_packed_gemv_stream<NCOLS, RES, NCH, QPW, NW, PD>), grid, block,
+                       static_cast<size_t>(NCOLS) * (n_in / 32) * 48, s, wp, x, y, res, partials, n_in, n_out);
 }
 
 template <int NCOLS, bool RES>
@@ -701,12 +803,15 @@ void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* r
                    int n_out, hipStream_t s) {
     static const int depth = env_int("RMI_PACKED_DEPTH", 2);
     if constexpr (NCOLS <= 2) {
-        const SplitCfg sc = split_cfg(n_in, n_out, NCOLS);
-        if (sc.cs) {
-            if (sc.cs == 6) return launch_split_k<NCOLS, RES, 6, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
-            if (sc.cs == 2) return launch_split_k<NCOLS, RES, 2, 4>(wp, x, y, res, partials, n_in, n_out, s);
-            if (sc.nw == 8) return launch_split_k<NCOLS, RES, 1, 8>(wp, x, y, res, partials, n_in, n_out, s);
-            return launch_split_k<NCOLS, RES, 1, 4>(wp, x, y, res, partials, n_in, n_out, s);
+        const PackedCfg c = packed_cfg(n_in, n_out, NCOLS);
+        if (c.kind == PackedCfg::kStream) {
+            if (n_in / kChunkElems == 2) return launch_stream<NCOLS, RES, 2, 2, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
+            return launch_stream<NCOLS, RES, 6, 1, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
+        }
+        if (c.kind == PackedCfg::kSplit) {
+            if (c.cs == 2) return launch_split<NCOLS, RES, 2, 4>(wp, x, y, res, partials, n_in, n_out, s);
+            if (c.nw == 8) return launch_split<NCOLS, RES, 1, 8>(wp, x, y, res, partials, n_in, n_out, s);
+            return launch_split<NCOLS, RES, 1, 4>(wp, x, y, res, partials, n_in, n_out, s);
         }
     }
     const int nq = (n_out + kQuad - 1) / kQuad;

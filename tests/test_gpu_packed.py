@@ -4,8 +4,8 @@ Bars: within 1e-3 relative of the oracle's fp64 GEMV (|err| <= 1e-3 |ref| + 1e-5
 16-row tiled GEMV on the GGUF layout where the dispatcher picks 16-row tiles (same lane ownership and reduction
 tree); ncols = 2 columns bitwise equal to ncols = 1; residual variant bitwise plain + res with partials = sum of the
 4 rows' squares in row order (src/test_res.cpp:57-112).  Ragged n_out pads the last 4-row group with zeros.
-Shapes with n_in = 4096 or 8192 (one or two columns) run the split-chunk kernel, the others the pipelined
-one-wave-per-quad kernel; both must give the same bits.
+At one or two columns, n_in = 4096 and 8192 run the split kernel (up to 16384 rows at 4096) or the stream kernel
+(more rows, and n_in = 12288); the other shapes the pipelined loop kernel.  All must give the same bits.
 """
 import numpy as np
 import pytest
@@ -51,8 +51,8 @@ def test_packed_matches_oracle_and_columns(orc, rmi, n_in, n_out):
         assert np.array_equal(host(y1).view(np.uint32), y2h[c * n_out:(c + 1) * n_out].view(np.uint32))
 
 
-# n_in 4096 runs the split-chunk kernel: two waves per quad up to 32768 rows, one wave per quad (all tiles in flight)
-# above; (2048, 1001) the one-wave-per-quad pipelined kernel
+# n_in 4096: the split kernel (a quad's two chunks on two waves) up to 16384 rows, the stream kernel (two quads per
+# wave) above, ragged at 33001; (2048, 1001) the pipelined loop kernel
 @pytest.mark.parametrize("n_in,n_out", [(4096, 12352), (4096, 10240), (2048, 1001), (4096, 24576), (4096, 33001)])
 def test_packed_bitwise_equals_16_row_tiles(orc, rmi, n_in, n_out):
     w = orc.gen_q6k(n_out, n_in, seed=7 * n_out)
