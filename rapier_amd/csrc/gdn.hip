@@ -195,26 +195,34 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
         }
     }
 
-    float* state = pick(a.state_a, a.state_b, a.sel);
-    float* snap = pick(a.state_b, a.state_a, a.sel);
+    // the selector is read once; the conv history loads go ahead of the state's 32 loads, so the conv (which needs
+    // only the history) does not wait for the state (a wave's loads complete in issue order)
+    const bool sel_b = a.sel != nullptr && *a.sel != 0;
+    float* state = sel_b ? a.state_b : a.state_a;
+    float* snap = sel_b ? a.state_a : a.state_b;
+    float* hist = sel_b ? a.hist_b : a.hist_a;
+    float* hsnap = sel_b ? a.hist_a : a.hist_b;
+    // CONV history slot: this head's own copy of the channel (the idle lanes read the q slot and ignore it: no branch
+    // around the loads, so the compiler's wait for them counts the state loads issued after)
+    const int ch = (3 * head + (kind < 3 ? kind : 0)) * S + j;
+    float h0 = 0.0f, h1 = 0.0f, h2 = 0.0f;
+    if constexpr (CONV) {
+        h0 = hist[3 * ch];
+        h1 = hist[3 * ch + 1];
+        h2 = hist[3 * ch + 2];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float s[RPG];
 #pragma unroll
     for (int r = 0; r < RPG; ++r) s[r] = state[base + r * row_stride];
 
     if constexpr (CONV) {
-        const int ch = (3 * head + kind) * S + j;   // history slot: this head's own copy of the channel
         float y[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) y[t] = 0.0f;
-        float h0 = 0.0f, h1 = 0.0f, h2 = 0.0f;
-        float* hist = pick(a.hist_a, a.hist_b, a.sel);
-        float* hsnap = pick(a.hist_b, a.hist_a, a.sel);
         // the conv input sequence [h0 h1 h2 | x_0 .. x_ntok-1]; i is a compile-time index after unrolling
         auto seq = [&](int i) { return i == 0 ? h0 : i == 1 ? h1 : i == 2 ? h2 : xr[i - 3]; };
         if (kind < 3) {
-            h0 = hist[3 * ch];
-            h1 = hist[3 * ch + 1];
-            h2 = hist[3 * ch + 2];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 if (t < ntok)
