@@ -11,18 +11,15 @@
 namespace rmi {
 namespace {
 
-// A lane's first kPartialLoads partials are loaded before the first add (a strided loop waits on each load in turn);
-// the adds keep their order.
+// A lane's first kPartialLoads partials are loaded before the first add (a strided loop waits on each load in turn),
+// unconditionally from clamped indices (a load under a branch gets a wait of its own); the adds keep their order.
 constexpr int kPartialLoads = 8;
 
 __device__ float block_sum_partials(const float* __restrict__ p, int np) {
     __shared__ float red[4];
     float pv[kPartialLoads];
 #pragma unroll
-    for (int k = 0; k < kPartialLoads; ++k) {
-        const int i = threadIdx.x + 256 * k;
-        pv[k] = i < np ? p[i] : 0.0f;
-    }
+    for (int k = 0; k < kPartialLoads; ++k) pv[k] = p[min(static_cast<int>(threadIdx.x) + 256 * k, np - 1)];
     float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < kPartialLoads; ++k)
@@ -47,8 +44,8 @@ __global__ __launch_bounds__(256) void rms_quant_apply_kernel(const float* __res
     partials += static_cast<size_t>(c) * (cols / 4);
     y += static_cast<size_t>(c) * (cols / 32) * kQ8_1Bytes;
     const int i = blockIdx.x * 256 + threadIdx.x;
-    // x and w do not depend on the reduction: in flight together with the partials
-    const float xv = i < cols ? x[i] : 0.0f, wv = i < cols ? w[i] : 0.0f;
+    // x and w do not depend on the reduction: in flight together with the partials (clamped, unconditional)
+    const float xv = x[min(i, cols - 1)], wv = w[min(i, cols - 1)];
     const float ss = block_sum_partials(partials, cols / 4);
     const float inv = rsqrtf(ss / static_cast<float>(cols) + eps);
     if (i >= cols) return;   // cols % 32 == 0: whole 32-lane groups leave together
@@ -65,7 +62,7 @@ __global__ __launch_bounds__(256) void rms_norm_out_kernel(const float* __restri
     partials += static_cast<size_t>(c) * (cols / 4);
     out += static_cast<size_t>(c) * out_stride;
     const int i = blockIdx.x * 256 + threadIdx.x;
-    const float xv = i < cols ? x[i] : 0.0f, wv = i < cols ? w[i] : 0.0f;   // in flight with the partials
+    const float xv = x[min(i, cols - 1)], wv = w[min(i, cols - 1)];   // in flight with the partials
     const float ss = block_sum_partials(partials, cols / 4);
     const float inv = rsqrtf(ss / static_cast<float>(cols) + eps);
     float v = 0.0f;
@@ -113,9 +110,13 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
                                                            uint8_t* __restrict__ y, int n, int col_stride) {
     const int c = blockIdx.y;
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const size_t off = static_cast<size_t>(c) * col_stride + i;
-    q8_1_store_lane(silu(gate[off]) * up[off], y + (static_cast<size_t>(c) * (n / 32) + i / 32) * kQ8_1Bytes);
+    // loads from a clamped index ahead of the range check, held there by the asm: with the check first, the pointer
+    // arguments are fetched only after it, one more round trip before the data loads
+    const size_t off = static_cast<size_t>(c) * col_stride + min(i, n - 1);
+    float g = gate[off], u = up[off];
+    asm volatile("" : "+v"(g), "+v"(u));
+    if (i >= n) return;   // n % 32 == 0: whole 32-lane groups leave together
+    q8_1_store_lane(silu(g) * u, y + (static_cast<size_t>(c) * (n / 32) + i / 32) * kQ8_1Bytes);
 }
 
 // Q8_1 of o * sigmoid(g) (reference sig_mul_quant_kernel, qw:692-704)
