@@ -226,9 +226,18 @@ __device__ __forceinline__ void accumulate_step(const WTile& wt, int lane, const
 
 // the finished quad q (lane 4 hb + r holds row 4 q + r's half-block sums): row sums, the residual, y and the quad's
 // sum of squares
+// the residual of quad q's rows for this lane (row 4 q + lane % 4), loaded from a clamped row so that the load can go
+// out with the kernel's first loads (in the epilogue it would wait behind every tile issued before it)
+template <int NCOLS>
+__device__ __forceinline__ void load_residual(float (&rv)[NCOLS], const float* res, int lane, int q, int n_out) {
+    const int row = min(kQuad * q + (lane & 3), n_out - 1);
+#pragma unroll
+    for (int col = 0; col < NCOLS; ++col) rv[col] = res[static_cast<size_t>(col) * n_out + row];
+}
+
 template <int NCOLS, bool RES>
 __device__ __forceinline__ void quad_epilogue(float (&tot)[NCOLS], int lane, int q, float* y, const float* res,
-                                              float* partials, int n_out) {
+                                              float* partials, int n_out, const float* rv = nullptr) {
     const int r = lane & 3, hb = lane >> 2;
     const int row = kQuad * q + r;
     const int np = (n_out + 3) / 4;
@@ -237,7 +246,7 @@ __device__ __forceinline__ void quad_epilogue(float (&tot)[NCOLS], int lane, int
         float v = hb_sum(tot[col]);
         tot[col] = 0.0f;
         if constexpr (RES) {
-            if (row < n_out) v += res[static_cast<size_t>(col) * n_out + row];
+            if (row < n_out) v += rv ? rv[col] : res[static_cast<size_t>(col) * n_out + row];
         }
         if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v;
         if constexpr (RES) {
@@ -349,6 +358,8 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
 #pragma unroll
         for (int i = 0; i < 9; ++i) sv[b][i] = p[i];
     }
+    float rv[NCOLS];
+    if constexpr (RES) load_residual<NCOLS>(rv, res, lane, min(q, nq - 1), n_out);
     __builtin_amdgcn_sched_barrier(0);   // the stage's loads stay ahead of the weight tiles
     // unconditional loads (a wave past the last quad reads the last quad's tiles and discards them): with the loads in
     // a branch the compiler waits for the stage as if no tile had been issued after it.  Every tile is issued here,
@@ -422,7 +433,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
             for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, o[(col + 1) * 64], tot[col]);
         }
     }
-    quad_epilogue<NCOLS, RES>(tot, lane, q, y, res, partials, n_out);
+    quad_epilogue<NCOLS, RES>(tot, lane, q, y, res, partials, n_out, rv);
 }
 
 // Stream variant: one wave per quad and QPW quads per wave (quads q, q + G, q + 2G, ... with G the grid's wave count),
@@ -453,6 +464,11 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
         const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
 #pragma unroll
         for (int i = 0; i < 9; ++i) sv[b][i] = p[i];
+    }
+    float rv[QPW][NCOLS];
+    if constexpr (RES) {
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) load_residual<NCOLS>(rv[j], res, lane, min(q0 + j * G, nq - 1), n_out);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -507,7 +523,8 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
             issue(i + PD);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (c == NCH - 1 && q0 + j * G < nq) quad_epilogue<NCOLS, RES>(tot, lane, q0 + j * G, y, res, partials, n_out);
+        if (c == NCH - 1 && q0 + j * G < nq)
+            quad_epilogue<NCOLS, RES>(tot, lane, q0 + j * G, y, res, partials, n_out, rv[j]);
     }
 }
 
