@@ -66,9 +66,12 @@ __global__ __launch_bounds__(HD) void attn_prep_kernel(const float* __restrict__
     const float* src = q3 + static_cast<size_t>(t) * q3_stride;
     // the row value does not depend on the position: load it in parallel with pos
     const bool is_v = hh >= n_head + n_kv, is_q = hh < n_head;
-    const float x = is_v ? src[2 * n_head * HD + n_kv * HD + (hh - n_head - n_kv) * HD + d]
-                         : is_q ? src[hh * 2 * HD + d] : src[2 * n_head * HD + (hh - n_head) * HD + d];
+    float x = is_v ? src[2 * n_head * HD + n_kv * HD + (hh - n_head - n_kv) * HD + d]
+                   : is_q ? src[hh * 2 * HD + d] : src[2 * n_head * HD + (hh - n_head) * HD + d];
+    float wn = is_q ? qn[d] : kn[d];   // the norm weight too (unused for v): not a round trip after the sum
     const int p = pos[0] + t;
+    // held here: the compiler would otherwise sink both loads below the position check, one round trip after it
+    asm volatile("" : "+v"(x), "+v"(wn));
     if (p < 0 || p >= max_ctx) return;   // uniform: a position outside the cache stores nothing
     if (is_v) {   // v: straight to the cache
         const int kv = hh - n_head - n_kv;
@@ -77,7 +80,7 @@ __global__ __launch_bounds__(HD) void attn_prep_kernel(const float* __restrict__
     }
     const float ss = block_sum256(x * x, red);
     const float inv = rsqrtf(ss / static_cast<float>(HD) + eps);
-    float v = x * inv * (is_q ? qn[d] : kn[d]);
+    float v = x * inv * wn;
     xs[d] = v;
     __syncthreads();
     const int half = n_rot / 2;
@@ -395,9 +398,9 @@ __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__
         m0 = base[d * cstride];
         l0 = base[d * cstride + 1];
     }
-    float oa[8];
+    float oa[8];   // from clamped chunks (unconditional: a load under a branch gets a wait of its own); k < nchunk used
 #pragma unroll
-    for (int k = 0; k < 8; ++k) oa[k] = k < nchunk ? base[k * cstride + 4 + d] : 0.0f;
+    for (int k = 0; k < 8; ++k) oa[k] = base[min(k, nchunk - 1) * cstride + 4 + d];
     float mloc = -INFINITY;
     if (d < nchunk) mloc = fmaxf(mloc, m0);
     for (int c = d + HD; c < nchunk; c += HD) mloc = fmaxf(mloc, base[c * cstride]);
