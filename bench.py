@@ -48,8 +48,8 @@ PAIR_BYTES = UG_BYTES + DN_BYTES                                                
 # HBM traffic of one packed up||gate ncols=2 launch, from two rocprofv3 --pmc passes over `bench.py --workload
 # traffic_probe` (profiles/gemv_up_gate_traffic.md): FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by
 # what the same counter reads for a copy kernel that reads 256 MiB and writes 256 MiB in the same process.
-PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 40444.75, 192.0
-PMC_COPY_FETCH_KIB, PMC_COPY_WRITE_KIB, COPY_KIB = 131090.1875, 262144.0, 262144.0
+PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 40478.5, 192.0625
+PMC_COPY_FETCH_KIB, PMC_COPY_WRITE_KIB, COPY_KIB = 131091.625, 262144.0, 262144.0
 UG_TRAFFIC_BYTES = round(1024 * (PMC_UG_FETCH_KIB * COPY_KIB / PMC_COPY_FETCH_KIB
                                  + PMC_UG_WRITE_KIB * COPY_KIB / PMC_COPY_WRITE_KIB))
 
