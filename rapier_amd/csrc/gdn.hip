@@ -212,9 +212,12 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
         h2 = hist[3 * ch + 2];
     }
     __builtin_amdgcn_sched_barrier(0);
+    // The state is read once and written once per launch (2 MiB per layer, 4 MiB with the rollback copy):
+    // nontemporal loads and stores keep it from filling the L2 that the end of the kernel writes back
+    // (measured: 2447 -> 2376 us per 4K round over 24 layers).
     float s[RPG];
 #pragma unroll
-    for (int r = 0; r < RPG; ++r) s[r] = state[base + r * row_stride];
+    for (int r = 0; r < RPG; ++r) s[r] = __builtin_nontemporal_load(state + base + r * row_stride);
 
     if constexpr (CONV) {
         float y[NT];
@@ -332,7 +335,7 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
             if constexpr (SNAP) {
                 if (t == 0) {
 #pragma unroll
-                    for (int r = 0; r < RPG; ++r) snap[base + r * row_stride] = s[r];
+                    for (int r = 0; r < RPG; ++r) __builtin_nontemporal_store(s[r], snap + base + r * row_stride);
                 }
             }
             const float ss = group_sum<16>(oc * oc);   // the wave's 16 columns (row-group 0 lanes carry them)
@@ -363,7 +366,7 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
         if (a.q8) q8_1_store_lane(yv, a.q8 + static_cast<size_t>(t) * a.q8_stride + (head * 4 + (cc >> 5)) * kQ8_1Bytes);
     }
 #pragma unroll
-    for (int r = 0; r < RPG; ++r) state[base + r * row_stride] = s[r];
+    for (int r = 0; r < RPG; ++r) __builtin_nontemporal_store(s[r], state + base + r * row_stride);
 }
 
 }  // namespace
