@@ -74,6 +74,17 @@ int rmi_native_q6_k_mmvq_res_n(const void* w, const void* x_q8_1, float* y, cons
  * ncols >= 2 call equal to the ncols = 1 call; _res_n equal to plain + res with one partial per 4 rows). */
 size_t rmi_q6_k_packed_bytes(int n_in, int n_out);
 int rmi_q6_k_pack(const void* w, void* w_packed, int n_in, int n_out, void* stream);
+/* No counterpart in the reference (a fusion of its up/gate GEMVs, mmvq:1261-1356, with swiglu_quant_kernel,
+ * qw:676-689).  Packs an up||gate Q6_K matrix (2 n_ff rows: up rows, then gate rows) in the SwiGLU row order:
+ * packed rows 64 G .. 64 G + 31 are gate rows 32 G .., rows 64 G + 32 .. 64 G + 63 up rows 32 G ...  n_ff a multiple
+ * of 32; the buffer is rmi_q6_k_packed_bytes(n_in, 2 n_ff).  A plain packed GEMV over it returns the rows in that
+ * order (rmi_swiglu_quant_interleaved takes them). */
+int rmi_q6_k_pack_swiglu(const void* w, void* w_packed, int n_in, int n_ff, void* stream);
+/* No counterpart in the reference (see rmi_q6_k_pack_swiglu).  Q8_1 of silu(gate) * up for 1 or 2 columns straight
+ * from the SwiGLU-packed up||gate matrix, n_in = 4096: bitwise the packed GEMV followed by rmi_swiglu_quant, in one
+ * launch and with no fp32 up / gate rows in memory. */
+int rmi_native_q6_k_swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_in, int n_ff,
+                                  int ncols, void* stream);
 int rmi_native_q6_k_mmvq_packed(const void* w_packed, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                                 void* stream);
 int rmi_native_q6_k_mmvq_packed_res_n(const void* w_packed, const void* x_q8_1, float* y, const float* res,
@@ -136,6 +147,9 @@ int rmi_row_sum_partials(const float* x, float* partials, int n, int ncols, void
 int rmi_add_partials(float* x, const float* o, float* partials, int n, int ncols, void* stream);
 /* Q8_1 of silu(gate) * up; column c reads up/gate at + c * col_stride.  Replaces swiglu_quant_kernel (qw:676-689). */
 int rmi_swiglu_quant(const float* up, const float* gate, void* y_q8_1, int n, int ncols, int col_stride, void* stream);
+/* rmi_swiglu_quant over up||gate rows in the SwiGLU order of rmi_q6_k_pack_swiglu (column c at up_gate + c col_stride,
+ * col_stride >= 2 n).  No counterpart in the reference (its rows are never interleaved). */
+int rmi_swiglu_quant_interleaved(const float* up_gate, void* y_q8_1, int n, int ncols, int col_stride, void* stream);
 /* Q8_1 of o * sigmoid(g).  Replaces sig_mul_quant_kernel (qw:692-704). */
 int rmi_sig_mul_quant(const float* o, const float* g, void* y_q8_1, int n, int ncols, int o_stride, int g_stride,
                       void* stream);

@@ -40,6 +40,8 @@ SIGNATURES = {
     "rmi_native_q5_k_mmvq_res": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
     "rmi_q6_k_packed_bytes": (_sz, [_i, _i]),
     "rmi_q6_k_pack": (_i, [_vp, _vp, _i, _i, _vp]),
+    "rmi_q6_k_pack_swiglu": (_i, [_vp, _vp, _i, _i, _vp]),
+    "rmi_native_q6_k_swiglu_packed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_packed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_packed_res_n": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_q6_k_block_dots": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
@@ -52,6 +54,7 @@ SIGNATURES = {
     "rmi_row_sum_partials": (_i, [_vp, _vp, _i, _i, _vp]),
     "rmi_add_partials": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "rmi_swiglu_quant": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_swiglu_quant_interleaved": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "rmi_sig_mul_quant": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rmi_beta_gate": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_argmax_workspace_bytes": (_sz, [_i]),
@@ -181,6 +184,16 @@ def q6_k_pack(w, w_packed, n_in: int, n_out: int, stream=None):
     _call("rmi_q6_k_pack", _p(w), _p(w_packed), n_in, n_out, _stream(stream))
 
 
+def q6_k_pack_swiglu(w, w_packed, n_in: int, n_ff: int, stream=None):
+    """pack an up||gate Q6_K matrix ([up n_ff rows | gate n_ff rows]) in the SwiGLU row order"""
+    _call("rmi_q6_k_pack_swiglu", _p(w), _p(w_packed), n_in, n_ff, _stream(stream))
+
+
+def native_q6_k_swiglu_packed(w_packed, x_q8_1, y_q8_1, n_in: int, n_ff: int, ncols: int, stream=None):
+    """Q8_1 of silu(gate) * up from an up||gate matrix packed by q6_k_pack_swiglu (one launch)"""
+    _call("rmi_native_q6_k_swiglu_packed", _p(w_packed), _p(x_q8_1), _p(y_q8_1), n_in, n_ff, ncols, _stream(stream))
+
+
 def native_q6_k_mmvq_packed(w_packed, x_q8_1, y, n_in: int, n_out: int, ncols: int, stream=None):
     _call("rmi_native_q6_k_mmvq_packed", _p(w_packed), _p(x_q8_1), _p(y), n_in, n_out, ncols, _stream(stream))
 
@@ -235,6 +248,11 @@ def add_partials(x, o, partials, n, ncols=1, stream=None):
 
 def swiglu_quant(up, gate, y_q8_1, n, ncols=1, col_stride=None, stream=None):
     _call("rmi_swiglu_quant", _p(up), _p(gate), _p(y_q8_1), n, ncols, n if col_stride is None else col_stride,
+          _stream(stream))
+
+
+def swiglu_quant_interleaved(up_gate, y_q8_1, n, ncols=1, col_stride=None, stream=None):
+    _call("rmi_swiglu_quant_interleaved", _p(up_gate), _p(y_q8_1), n, ncols, 2 * n if col_stride is None else col_stride,
           _stream(stream))
 
 

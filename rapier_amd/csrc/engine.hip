@@ -65,6 +65,7 @@ struct Mat {
     int n_in = 0, n_out = 0;
     int type = 14;
     bool packed = false;
+    int swiglu_ff = 0;           // > 0: an up||gate matrix packed in the SwiGLU row order (ff rows each)
     size_t bytes = 0;            // GGUF bytes of the matrix (the weight pass it costs)
     std::vector<Mat> parts;      // non-empty: a mixed-type group
 };
@@ -296,7 +297,19 @@ uint64_t mix_seed(uint64_t seed, int layer, int what) {
     return z ^ (z >> 29);
 }
 
-int make_mat(Engine& e, Mat& m, int n_out, int n_in, uint64_t seed) {
+// an up||gate matrix ([up | gate], swiglu) of 4096-wide rows is packed in the SwiGLU row order, for the fused
+// up||gate + SwiGLU kernel
+bool swiglu_packing(const Mat& m, bool swiglu) { return swiglu && m.packed && m.n_in == 4096 && (m.n_out / 2) % 32 == 0; }
+
+int pack_mat(Engine& e, Mat& m, bool swiglu) {
+    if (swiglu_packing(m, swiglu)) {
+        m.swiglu_ff = m.n_out / 2;
+        return rmi_q6_k_pack_swiglu(e.gen_tmp, m.w, m.n_in, m.swiglu_ff, e.s);
+    }
+    return rmi_q6_k_pack(e.gen_tmp, m.w, m.n_in, m.n_out, e.s);
+}
+
+int make_mat(Engine& e, Mat& m, int n_out, int n_in, uint64_t seed, bool swiglu = false) {
     m.n_in = n_in;
     m.n_out = n_out;
     static const bool use_packed = [] {
@@ -315,7 +328,7 @@ int make_mat(Engine& e, Mat& m, int n_out, int n_in, uint64_t seed) {
     if (gguf > e.gen_tmp_bytes) return fail(RMI_ERR_STATE, "engine: generation buffer too small");
     RMI_TRY(e.alloc(&m.w, rmi_q6_k_packed_bytes(n_in, n_out)));
     RMI_TRY(rmi_gen_q6_k(e.gen_tmp, static_cast<size_t>(n_out) * (n_in / 256), seed, 1e-3f, e.s));
-    return rmi_q6_k_pack(e.gen_tmp, m.w, n_in, n_out, e.s);
+    return pack_mat(e, m, swiglu);
 }
 
 int gemv(Engine& e, const Mat& m, const uint8_t* xq, float* y, int nc) {
@@ -390,7 +403,7 @@ int make_attn(Engine& e, Layer& L, int li, uint64_t seed) {
     RMI_TRY(make_vec(e, &L.post_norm, c.n_embd, mix_seed(seed, li, 2), 1.0f, 0.1f));
     RMI_TRY(make_mat(e, L.in_proj, e.q3_rows, c.n_embd, mix_seed(seed, li, 3)));
     RMI_TRY(make_mat(e, L.out_proj, c.n_embd, e.attn_q, mix_seed(seed, li, 4)));
-    RMI_TRY(make_mat(e, L.upgate, 2 * c.n_ff, c.n_embd, mix_seed(seed, li, 5)));
+    RMI_TRY(make_mat(e, L.upgate, 2 * c.n_ff, c.n_embd, mix_seed(seed, li, 5), true));
     RMI_TRY(make_mat(e, L.down, c.n_embd, c.n_ff, mix_seed(seed, li, 6)));
     RMI_TRY(make_vec(e, &L.qn, c.head_dim, mix_seed(seed, li, 7), 1.0f, 0.1f));
     RMI_TRY(make_vec(e, &L.kn, c.head_dim, mix_seed(seed, li, 8), 1.0f, 0.1f));
@@ -404,7 +417,7 @@ int make_gdn(Engine& e, Layer& L, int li, uint64_t seed) {
     RMI_TRY(make_vec(e, &L.post_norm, c.n_embd, mix_seed(seed, li, 2), 1.0f, 0.1f));
     RMI_TRY(make_mat(e, L.in_proj, e.qkvz_rows, c.n_embd, mix_seed(seed, li, 3)));
     RMI_TRY(make_mat(e, L.out_proj, c.n_embd, e.gdn_v, mix_seed(seed, li, 4)));
-    RMI_TRY(make_mat(e, L.upgate, 2 * c.n_ff, c.n_embd, mix_seed(seed, li, 5)));
+    RMI_TRY(make_mat(e, L.upgate, 2 * c.n_ff, c.n_embd, mix_seed(seed, li, 5), true));
     RMI_TRY(make_mat(e, L.down, c.n_embd, c.n_ff, mix_seed(seed, li, 6)));
     const int ch = 2 * c.ssm_h_k * kS + c.ssm_h_v * kS;
     RMI_TRY(make_vec(e, &L.conv_w, static_cast<size_t>(4) * ch, mix_seed(seed, li, 7), 0.0f, 0.5f));
@@ -433,8 +446,15 @@ __global__ void neg_exp_kernel(float* p, int n) {   // ssm_a = -exp(N(0, 0.5^2))
 int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
     const auto& c = e.cfg;
     RMI_TRY(rmi_rms_quant_apply(x, L.post_norm, part, e.q8a, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(gemv(e, L.upgate, e.q8a, e.ug, nc));
-    RMI_TRY(rmi_swiglu_quant(e.ug, e.ug + c.n_ff, e.q8f, c.n_ff, nc, 2 * c.n_ff, e.s));
+    if (L.upgate.swiglu_ff && nc <= 2) {   // up||gate GEMV + SwiGLU + Q8_1 in one launch
+        RMI_TRY(rmi_native_q6_k_swiglu_packed(L.upgate.w, e.q8a, e.q8f, c.n_embd, c.n_ff, nc, e.s));
+    } else {
+        RMI_TRY(gemv(e, L.upgate, e.q8a, e.ug, nc));
+        if (L.upgate.swiglu_ff)
+            RMI_TRY(rmi_swiglu_quant_interleaved(e.ug, e.q8f, c.n_ff, nc, 2 * c.n_ff, e.s));
+        else
+            RMI_TRY(rmi_swiglu_quant(e.ug, e.ug + c.n_ff, e.q8f, c.n_ff, nc, 2 * c.n_ff, e.s));
+    }
     return gemv_res(e, L.down, e.q8f, x, part, nc);
 }
 
@@ -751,7 +771,8 @@ struct Uploader {
 // rows of the named tensors, concatenated in order (the reference's try_cat groups, qw:2082-2087), into one engine
 // matrix when every part has the same type (Q6_K packed when n_in % 2048 == 0, else GGUF blocks); a group whose parts
 // differ in type keeps them as parts (try_cat leaves such a group unfused, qw:1284-1288)
-int load_mat(Engine& e, Uploader& up, const rmi_gguf* g, Mat& m, std::initializer_list<std::string> names) {
+int load_mat(Engine& e, Uploader& up, const rmi_gguf* g, Mat& m, std::initializer_list<std::string> names,
+             bool swiglu = false) {
     int n_in = -1, n_out = 0, type = -1;
     bool mixed = false;
     std::vector<GTensor> parts;
@@ -800,7 +821,7 @@ int load_mat(Engine& e, Uploader& up, const rmi_gguf* g, Mat& m, std::initialize
     }
     if (!m.packed) return RMI_OK;
     RMI_TRY(e.alloc(&m.w, rmi_q6_k_packed_bytes(n_in, n_out)));
-    RMI_TRY(rmi_q6_k_pack(e.gen_tmp, m.w, n_in, n_out, e.s));
+    RMI_TRY(pack_mat(e, m, swiglu));
     HIP_TRY(hipStreamSynchronize(e.s));   // the next matrix reuses the staging buffer
     return RMI_OK;
 }
@@ -822,7 +843,7 @@ int load_attn(Engine& e, Uploader& up, const rmi_gguf* g, Layer& L, int il) {
     RMI_TRY(load_f32(e, up, g, &L.post_norm, blk(il, "post_attention_norm.weight"), c.n_embd));
     RMI_TRY(load_mat(e, up, g, L.in_proj, {blk(il, "attn_q.weight"), blk(il, "attn_k.weight"), blk(il, "attn_v.weight")}));
     RMI_TRY(load_mat(e, up, g, L.out_proj, {blk(il, "attn_output.weight")}));
-    RMI_TRY(load_mat(e, up, g, L.upgate, {blk(il, "ffn_up.weight"), blk(il, "ffn_gate.weight")}));
+    RMI_TRY(load_mat(e, up, g, L.upgate, {blk(il, "ffn_up.weight"), blk(il, "ffn_gate.weight")}, true));
     RMI_TRY(load_mat(e, up, g, L.down, {blk(il, "ffn_down.weight")}));
     RMI_TRY(load_f32(e, up, g, &L.qn, blk(il, "attn_q_norm.weight"), c.head_dim));
     RMI_TRY(load_f32(e, up, g, &L.kn, blk(il, "attn_k_norm.weight"), c.head_dim));
@@ -841,7 +862,7 @@ int load_gdn(Engine& e, Uploader& up, const rmi_gguf* g, Layer& L, int il) {
     RMI_TRY(load_mat(e, up, g, L.in_proj, {blk(il, "attn_qkv.weight"), blk(il, "attn_gate.weight"),
                                            blk(il, "ssm_beta.weight"), blk(il, "ssm_alpha.weight")}));
     RMI_TRY(load_mat(e, up, g, L.out_proj, {blk(il, "ssm_out.weight")}));
-    RMI_TRY(load_mat(e, up, g, L.upgate, {blk(il, "ffn_up.weight"), blk(il, "ffn_gate.weight")}));
+    RMI_TRY(load_mat(e, up, g, L.upgate, {blk(il, "ffn_up.weight"), blk(il, "ffn_gate.weight")}, true));
     RMI_TRY(load_mat(e, up, g, L.down, {blk(il, "ffn_down.weight")}));
     const int ch = 2 * c.ssm_h_k * kS + c.ssm_h_v * kS;
     RMI_TRY(load_f32(e, up, g, &L.conv_w, blk(il, "ssm_conv1d.weight"), static_cast<size_t>(4) * ch));

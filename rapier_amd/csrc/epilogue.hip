@@ -119,6 +119,20 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
     q8_1_store_lane(silu(g) * u, y + (static_cast<size_t>(c) * (n / 32) + i / 32) * kQ8_1Bytes);
 }
 
+// the same over an up||gate output in the SwiGLU row order (64-row groups [gate 32 | up 32]): output i reads gate at
+// 64 (i / 32) + i % 32 and up 32 rows later
+__global__ __launch_bounds__(256) void swiglu_quant_interleaved_kernel(const float* __restrict__ ug,
+                                                                       uint8_t* __restrict__ y, int n, int col_stride) {
+    const int c = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int ic = min(i, n - 1);
+    const size_t off = static_cast<size_t>(c) * col_stride + 64 * (ic / 32) + ic % 32;
+    float g = ug[off], u = ug[off + 32];
+    asm volatile("" : "+v"(g), "+v"(u));   // loads ahead of the range check (see swiglu_quant_kernel)
+    if (i >= n) return;
+    q8_1_store_lane(silu(g) * u, y + (static_cast<size_t>(c) * (n / 32) + i / 32) * kQ8_1Bytes);
+}
+
 // Q8_1 of o * sigmoid(g) (reference sig_mul_quant_kernel, qw:692-704)
 __global__ __launch_bounds__(256) void sig_mul_quant_kernel(const float* __restrict__ o, const float* __restrict__ g,
                                                             uint8_t* __restrict__ y, int n, int o_stride,
@@ -324,6 +338,16 @@ extern "C" int rmi_add_partials(float* x, const float* o, float* partials, int n
     hipLaunchKernelGGL(add_partials_kernel, dim3((np + 255) / 256, ncols), dim3(256), 0,
                        static_cast<hipStream_t>(stream), x, o, partials, n);
     return launch_status("add_partials");
+}
+
+extern "C" int rmi_swiglu_quant_interleaved(const float* up_gate, void* y_q8_1, int n, int ncols, int col_stride,
+                                            void* stream) {
+    if (n <= 0 || n % 32 != 0 || bad_cols(ncols) || col_stride < 2 * n)
+        return fail(RMI_ERR_SHAPE, "swiglu_quant_interleaved: bad shape");
+    if (!aligned4(up_gate) || !aligned4(y_q8_1)) return fail(RMI_ERR_POINTER, "swiglu_quant_interleaved: bad pointer");
+    hipLaunchKernelGGL(swiglu_quant_interleaved_kernel, dim3((n + 255) / 256, ncols), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), up_gate, static_cast<uint8_t*>(y_q8_1), n, col_stride);
+    return launch_status("swiglu_quant_interleaved");
 }
 
 extern "C" int rmi_swiglu_quant(const float* up, const float* gate, void* y_q8_1, int n, int ncols, int col_stride,

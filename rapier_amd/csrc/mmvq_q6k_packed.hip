@@ -76,8 +76,16 @@ __device__ __forceinline__ float hb_sum(float v) {
 }
 
 // ---- pack: one thread per (quad, chunk, lane) --------------------------------------------------------------------------
+// SwiGLU row order of an up||gate matrix ([up ff rows | gate ff rows] in the source): packed rows 64 G .. 64 G + 31 are
+// gate rows 32 G .., rows 64 G + 32 .. 64 G + 63 up rows 32 G .., so a 16-quad group holds both inputs of 32 outputs
+__host__ __device__ __forceinline__ int swiglu_src_row(int p, int ff) {
+    const int g = p >> 6, j = p & 63;
+    return j < 32 ? ff + 32 * g + j : 32 * g + j - 32;
+}
+
+// ff = 0: rows in source order; ff > 0: the SwiGLU order above (n_out = 2 ff, ff % 32 == 0)
 __global__ __launch_bounds__(kThreads) void q6k_pack_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ wp,
-                                                            int n_in, int n_out, size_t nslots) {
+                                                            int n_in, int n_out, size_t nslots, int ff) {
     const size_t gid = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
     if (gid >= nslots) return;
     const int nch = n_in / kChunkElems, nb = n_in / 256;
@@ -88,7 +96,8 @@ __global__ __launch_bounds__(kThreads) void q6k_pack_kernel(const uint8_t* __res
     const int row = kQuad * q + r;
     uint8_t* dst = wp + tile * kWaveTile;
     const bool live = row < n_out;
-    const uint8_t* src = w + (static_cast<size_t>(row) * nb + static_cast<size_t>(c) * kChunkBlocks + b) * kQ6KBytes;
+    const int srow = ff > 0 && live ? swiglu_src_row(row, ff) : row;
+    const uint8_t* src = w + (static_cast<size_t>(srow) * nb + static_cast<size_t>(c) * kChunkBlocks + b) * kQ6KBytes;
     for (int u = 0; u < 4; ++u)
         for (int i = 0; i < 16; ++i) dst[u * 1024 + 16 * l + i] = live ? src[64 * n + 16 * u + i] : 0;
     for (int u = 0; u < 2; ++u)
@@ -528,6 +537,86 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
     }
 }
 
+// up||gate GEMV with the SwiGLU + Q8_1 epilogue, over a matrix packed in the SwiGLU row order (rows of 4096: two
+// chunks).  Workgroup g (8 waves) owns quads 16 g .. 16 g + 15 = gate and up rows of outputs 32 g .. 32 g + 31; wave w
+// takes quads 16 g + 2 w and + 1 as the stream kernel takes its quads (same per-row arithmetic, so the same row sums
+// as the plain GEMV), parks the row sums in LDS, and one 32-lane group per column forms silu(gate) * up and its Q8_1
+// block with the quantizer of swiglu_quant: bitwise the GEMV + swiglu_quant pair, one launch and no fp32 round trip.
+template <int NCOLS>
+__global__ __launch_bounds__(512) void q6k_packed_swiglu(const uint8_t* __restrict__ wp, const uint8_t* __restrict__ x,
+                                                         uint8_t* __restrict__ out, int n_in, int ff) {
+    constexpr int NW = 8, NCH = 2, T = 2 * NCH, PD = 2;
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int nbt = n_in / 32, xcs = NCH * kNB;
+    uint4* lq = smem;
+    uint4* lrec = smem + 2 * NCOLS * nbt;
+    float* lrow = reinterpret_cast<float*>(lrec + NCOLS * nbt);   // [col][64 rows of the group]
+    const int q0 = static_cast<int>(blockIdx.x) * 16 + 2 * w;
+
+    const int nblocks = NCOLS * nbt;   // <= 2 x 128: one block per lane at most
+    uint32_t sv[9];
+    {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(min(t, nblocks - 1)) * kQ8_1Bytes);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) sv[i] = p[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    WTile buf[T];
+    auto issue = [&](int i) {
+        const int j = i / NCH, c = i - j * NCH;
+        const uint8_t* base = wp + (static_cast<size_t>(q0 + j) * NCH + c) * kWaveTile;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            buf[i].ql[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * 1024 + 16 * lane));
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            buf[i].qh[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + 4096 + u * 1024 + 16 * lane));
+        buf[i].sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
+        buf[i].d = *reinterpret_cast<const uint32_t*>(base + 6656 + 4 * (2 * (lane >> 3) + ((lane & 3) >> 1)));
+    };
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+        issue(i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (t < nblocks) stage_one(sv, t, nbt, lq, lrec);
+    __syncthreads();
+
+    float tot[NCOLS];
+#pragma unroll
+    for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+        const int j = i / NCH, c = i - (i / NCH) * NCH;
+        pin_tile_after<NCOLS>(buf[i], tot);
+        float acc[NCOLS];
+        const float d = step_acc<NCOLS>(buf[i], lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, acc);
+#pragma unroll
+        for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
+        if (i + PD < T) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(i + PD);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (c == NCH - 1) {
+#pragma unroll
+            for (int col = 0; col < NCOLS; ++col) {
+                const float v = hb_sum(tot[col]);
+                tot[col] = 0.0f;
+                if (lane < kQuad) lrow[col * 64 + 4 * (2 * w + j) + lane] = v;
+            }
+        }
+    }
+    __syncthreads();
+    // wave 0: lanes 32 c .. 32 c + 31 quantize column c's 32 outputs of this group
+    if (w == 0 && (lane >> 5) < NCOLS) {
+        const int col = lane >> 5, i = lane & 31;
+        const float a = silu(lrow[col * 64 + i]) * lrow[col * 64 + 32 + i];
+        q8_1_store_lane(a, out + (static_cast<size_t>(col) * (ff / 32) + blockIdx.x) * kQ8_1Bytes);
+    }
+}
+
 // ---- ingest GEMM: 8 / 16 columns on the 16-block 4x4x4 int8 MFMA -------------------------------------------------
 // Same wave tiles, lane ownership and fp32 arithmetic as q6k_packed_gemv, with the integer dot products on the matrix
 // cores.  MFMA block b = half-block hb (lanes 4 hb .. 4 hb + 3), A row i = quad row i (the lane's own unpacked
@@ -940,15 +1029,51 @@ extern "C" size_t rmi_q6_k_packed_bytes(int n_in, int n_out) {
     return static_cast<size_t>((n_out + kQuad - 1) / kQuad) * (n_in / kChunkElems) * kWaveTile;
 }
 
+namespace rmi {
+namespace {
+int pack(const void* w, void* w_packed, int n_in, int n_out, int ff, void* stream) {
+    const size_t nslots = static_cast<size_t>((n_out + kQuad - 1) / kQuad) * (n_in / kChunkElems) * 64;
+    hipLaunchKernelGGL(q6k_pack_kernel, dim3(static_cast<unsigned>((nslots + kThreads - 1) / kThreads)), dim3(kThreads),
+                       0, static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(w),
+                       static_cast<uint8_t*>(w_packed), n_in, n_out, nslots, ff);
+    return launch_status("q6_k_pack");
+}
+}  // namespace
+}  // namespace rmi
+
 extern "C" int rmi_q6_k_pack(const void* w, void* w_packed, int n_in, int n_out, void* stream) {
     if (n_in <= 0 || n_in % kChunkElems != 0 || n_out <= 0)
         return fail(RMI_ERR_SHAPE, "q6_k_pack: n_in must be a positive multiple of 2048 and n_out positive");
     if (!w || !aligned16(w_packed)) return fail(RMI_ERR_POINTER, "q6_k_pack: null weights or misaligned packed buffer");
-    const size_t nslots = static_cast<size_t>((n_out + kQuad - 1) / kQuad) * (n_in / kChunkElems) * 64;
-    hipLaunchKernelGGL(q6k_pack_kernel, dim3(static_cast<unsigned>((nslots + kThreads - 1) / kThreads)), dim3(kThreads),
-                       0, static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(w),
-                       static_cast<uint8_t*>(w_packed), n_in, n_out, nslots);
-    return launch_status("q6_k_pack");
+    return pack(w, w_packed, n_in, n_out, 0, stream);
+}
+
+extern "C" int rmi_q6_k_pack_swiglu(const void* w, void* w_packed, int n_in, int n_ff, void* stream) {
+    if (n_in <= 0 || n_in % kChunkElems != 0 || n_ff <= 0 || n_ff % 32 != 0)
+        return fail(RMI_ERR_SHAPE, "q6_k_pack_swiglu: n_in must be a positive multiple of 2048, n_ff of 32");
+    if (!w || !aligned16(w_packed))
+        return fail(RMI_ERR_POINTER, "q6_k_pack_swiglu: null weights or misaligned packed buffer");
+    return pack(w, w_packed, n_in, 2 * n_ff, n_ff, stream);
+}
+
+extern "C" int rmi_native_q6_k_swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_in, int n_ff,
+                                             int ncols, void* stream) {
+    if (n_in != 2 * kChunkElems || n_ff <= 0 || n_ff % 32 != 0 || ncols < 1 || ncols > 2)
+        return fail(RMI_ERR_SHAPE, "q6_k_swiglu_packed: n_in must be 4096, n_ff a positive multiple of 32, ncols 1 or 2");
+    if (!aligned16(w_packed) || !aligned4(x_q8_1) || !aligned4(y_q8_1))
+        return fail(RMI_ERR_POINTER, "q6_k_swiglu_packed: null or misaligned pointer");
+    if (!stream) return fail(RMI_ERR_STREAM, "native MMVQ requires an explicit non-null CUDA stream");
+    const auto* wp = static_cast<const uint8_t*>(w_packed);
+    const auto* x = static_cast<const uint8_t*>(x_q8_1);
+    auto* y = static_cast<uint8_t*>(y_q8_1);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t lds = static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(ncols) * 64 * 4;
+    const dim3 grid(n_ff / 32), block(512);
+    if (ncols == 1)
+        hipLaunchKernelGGL((q6k_packed_swiglu<1>), grid, block, lds, s, wp, x, y, n_in, n_ff);
+    else
+        hipLaunchKernelGGL((q6k_packed_swiglu<2>), grid, block, lds, s, wp, x, y, n_in, n_ff);
+    return launch_status("q6_k_swiglu_packed");
 }
 
 extern "C" int rmi_native_q6_k_mmvq_packed(const void* w_packed, const void* x_q8_1, float* y, int n_in, int n_out,

@@ -141,3 +141,62 @@ def test_packed_wide_passes_bitwise_equal_single_column(orc, rmi, n_in, n_out, n
     part = empty(ncols * np_)
     rmi.native_q6_k_mmvq_packed_res_n(wp, xd, yr, yr, part, n_in, n_out, ncols)
     assert np.array_equal(host(yr).view(np.uint32), (yh + res).view(np.uint32))
+
+
+def swiglu_perm(ff):
+    """packed row p of the SwiGLU order -> source row of [up ff | gate ff]"""
+    p = np.arange(2 * ff)
+    g, j = p // 64, p % 64
+    return np.where(j < 32, ff + 32 * g + j, 32 * g + j - 32)
+
+
+@pytest.mark.parametrize("ff", [12288, 320])
+def test_swiglu_pack_is_a_row_permutation(orc, rmi, ff):
+    """a plain packed GEMV over the SwiGLU packing returns the natural rows in the SwiGLU order, bit for bit"""
+    n_in = 4096
+    w = orc.gen_q6k(2 * ff, n_in, seed=ff + 1)
+    xq = orc.quantize_q8_1(orc.normal(3 * n_in, seed=5), n_in, 3)
+    wd, xd = dev(w), dev(xq)
+    wn = packed(rmi, wd, n_in, 2 * ff)
+    ws = empty(rmi.q6_k_packed_bytes(n_in, 2 * ff), "uint8")
+    rmi.q6_k_pack_swiglu(wd, ws, n_in, ff)
+    yn, ys = empty(3 * 2 * ff), empty(3 * 2 * ff)
+    rmi.native_q6_k_mmvq_packed(wn, xd, yn, n_in, 2 * ff, 3)
+    rmi.native_q6_k_mmvq_packed(ws, xd, ys, n_in, 2 * ff, 3)
+    yn, ys = host(yn).reshape(3, 2 * ff), host(ys).reshape(3, 2 * ff)
+    assert np.array_equal(ys.view(np.uint32), yn[:, swiglu_perm(ff)].view(np.uint32))
+
+
+@pytest.mark.parametrize("ff", [12288, 320])
+@pytest.mark.parametrize("ncols", [1, 2])
+def test_fused_swiglu_gemv_bitwise_equals_gemv_then_swiglu(orc, rmi, ff, ncols):
+    """rmi_native_q6_k_swiglu_packed == packed GEMV + swiglu_quant (Q8_1 bytes), and the interleaved SwiGLU over the
+    SwiGLU-order rows gives the same bytes"""
+    n_in = 4096
+    w = orc.gen_q6k(2 * ff, n_in, seed=7 * ff + ncols)
+    xq = orc.quantize_q8_1(orc.normal(ncols * n_in, seed=ff), n_in, ncols)
+    wd, xd = dev(w), dev(xq)
+    wn = packed(rmi, wd, n_in, 2 * ff)
+    ws = empty(rmi.q6_k_packed_bytes(n_in, 2 * ff), "uint8")
+    rmi.q6_k_pack_swiglu(wd, ws, n_in, ff)
+    ug = empty(ncols * 2 * ff)
+    rmi.native_q6_k_mmvq_packed(wn, xd, ug, n_in, 2 * ff, ncols)
+    qbytes = rmi.native_q8_1_bytes(ff, ncols)
+    ref = empty(qbytes, "uint8")
+    rmi.swiglu_quant(ug, ug[ff:], ref, ff, ncols, 2 * ff)
+    fused = empty(qbytes, "uint8")
+    rmi.native_q6_k_swiglu_packed(ws, xd, fused, n_in, ff, ncols)
+    assert np.array_equal(host(fused), host(ref))
+    ugs = empty(ncols * 2 * ff)
+    rmi.native_q6_k_mmvq_packed(ws, xd, ugs, n_in, 2 * ff, ncols)
+    inter = empty(qbytes, "uint8")
+    rmi.swiglu_quant_interleaved(ugs, inter, ff, ncols)
+    assert np.array_equal(host(inter), host(ref))
+    # and the Q8_1 blocks hold silu(gate) * up of the oracle's GEMV within the quantizer's step
+    yo = orc.q6k_gemv(w, xq, n_in, 2 * ff, ncols=ncols).reshape(ncols, 2 * ff).astype(np.float64)
+    a = yo[:, ff:] / (1.0 + np.exp(-yo[:, ff:])) * yo[:, :ff]
+    blk = host(fused).reshape(ncols, ff // 32, 36)
+    d = blk[:, :, 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
+    q = blk[:, :, 4:].view(np.int8).astype(np.float64)
+    deq = (q * d[..., None]).reshape(ncols, ff)
+    assert np.all(np.abs(deq - a) <= 0.51 * np.repeat(d, 32, axis=1) + 1e-3 * np.abs(a) + 1e-6)
