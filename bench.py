@@ -44,8 +44,10 @@ UG_BYTES = q6_bytes(UG_ROWS, UG_IN) + 2 * (UG_IN // 32) * 36 + 2 * UG_ROWS * 4  
 DN_BYTES = (q6_bytes(DN_ROWS, DN_IN) + 2 * (DN_IN // 32) * 36 + 2 * DN_ROWS * 4 * 2
             + 2 * (DN_ROWS // 4) * 4)                                                       # 41,389,056
 PAIR_BYTES = UG_BYTES + DN_BYTES                                                             # 124,170,240
+# the round's up||gate kernel: GEMV + SwiGLU + Q8_1 in one launch (weights, Q8_1 in, Q8_1 out of the 12288 products)
+UGS_BYTES = q6_bytes(UG_ROWS, UG_IN) + 2 * (UG_IN // 32) * 36 + 2 * (UG_ROWS // 2 // 32) * 36  # 82,612,224
 
-# HBM traffic of one packed up||gate ncols=2 launch, from two rocprofv3 --pmc passes over `bench.py --workload
+# HBM traffic of one fused up||gate + SwiGLU ncols=2 launch, from two rocprofv3 --pmc passes over `bench.py --workload
 # traffic_probe` (profiles/gemv_up_gate_traffic.md): FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by
 # what the same counter reads for a copy kernel that reads 256 MiB and writes 256 MiB in the same process.
 PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 40478.5, 192.0625
@@ -132,27 +134,29 @@ def run_verify_gemv(args):
     ms_per_step = total_ms / args.steps
     value = PAIR_BYTES / (ms_per_step * 1e-3) / 1e9
 
-    # roofline leg: the round's GEMV kernel, on the packed (wave-tiled) copies of the up||gate replicas the engine
-    # uses.  Blocks of back-to-back launches over the rotating replicas, one HIP event pair per block on the launch
-    # stream (per-launch event pairs would add the event's own cost to every launch).
+    # roofline leg: the round's up||gate kernel (GEMV + SwiGLU + Q8_1, one launch) on SwiGLU-packed (wave-tiled)
+    # copies of the up||gate replicas, as the engine packs them.  Blocks of back-to-back launches over the rotating
+    # replicas, one HIP event pair per block on the launch stream (per-launch event pairs would add the event's own
+    # cost to every launch).
     ugp = [torch.empty(rmi.q6_k_packed_bytes(UG_IN, UG_ROWS), dtype=torch.uint8, device="cuda") for _ in range(reps)]
     for i in range(reps):
-        rmi.q6_k_pack(ug[i], ugp[i], UG_IN, UG_ROWS, stream)
+        rmi.q6_k_pack_swiglu(ug[i], ugp[i], UG_IN, UG_ROWS // 2, stream)
     del ug, dn
+    q_ug = torch.empty(rmi.native_q8_1_bytes(UG_ROWS // 2, 2), dtype=torch.uint8, device="cuda")
     for i in range(reps):
-        rmi.native_q6_k_mmvq_packed(ugp[i], xq_ug, y_ug, UG_IN, UG_ROWS, 2, stream)
+        rmi.native_q6_k_swiglu_packed(ugp[i], xq_ug, q_ug, UG_IN, UG_ROWS // 2, 2, stream)
     blocks, per_block = 5, 2 * reps
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(blocks)]
     torch.cuda.synchronize()
     for b in range(blocks):
         evs[b][0].record(stream)
         for i in range(per_block):
-            rmi.native_q6_k_mmvq_packed(ugp[i % reps], xq_ug, y_ug, UG_IN, UG_ROWS, 2, stream)
+            rmi.native_q6_k_swiglu_packed(ugp[i % reps], xq_ug, q_ug, UG_IN, UG_ROWS // 2, 2, stream)
         evs[b][1].record(stream)
     torch.cuda.synchronize()
     ug_us = sorted(a.elapsed_time(b) * 1e3 / per_block for a, b in evs)
     ug_mean_us = sum(ug_us) / len(ug_us)
-    achieved = UG_BYTES / (ug_mean_us * 1e-6) / 1e9
+    achieved = UGS_BYTES / (ug_mean_us * 1e-6) / 1e9
     del ugp
     out = {
         "metric": METRIC,
@@ -178,15 +182,16 @@ def run_verify_gemv(args):
             "rotated_bytes": reps * (q6_bytes(UG_ROWS, UG_IN) + q6_bytes(DN_ROWS, DN_IN)),
         },
         "roofline": {
-            "kernel": "q6k_packed_gemv_stream<2,false,2,2,4,2> (up||gate 24576x4096, ncols=2, packed wave-tile layout)",
+            "kernel": "q6k_packed_swiglu<2> (up||gate 24576x4096 GEMV + SwiGLU + Q8_1, ncols=2, SwiGLU-packed "
+                      "wave-tile layout)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": UG_TRAFFIC_BYTES,
-            "traffic_over_algorithmic": round(UG_TRAFFIC_BYTES / UG_BYTES, 4),
-            "algorithmic_bytes_per_launch": UG_BYTES,
+            "traffic_over_algorithmic": round(UG_TRAFFIC_BYTES / UGS_BYTES, 4),
+            "algorithmic_bytes_per_launch": UGS_BYTES,
             "mean_launch_us": round(ug_mean_us, 3),
             "launches_timed": blocks * per_block,
         },
@@ -195,7 +200,8 @@ def run_verify_gemv(args):
 
 
 def run_traffic_probe():
-    """Workload for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: one packed up||gate ncols=2 launch after a 1 GiB
+    """Workload for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: one fused up||gate + SwiGLU ncols=2 launch
+    (SwiGLU-packed weights) after a 1 GiB
     fill has evicted L2 and the Infinity Cache, then a copy-like kernel of known size (reads 256 MiB, writes
     256 MiB) that calibrates both counters in the same process."""
     import torch
@@ -207,20 +213,20 @@ def run_traffic_probe():
     wg = torch.empty(q6_bytes(UG_ROWS, UG_IN), dtype=torch.uint8, device="cuda")
     rmi.gen_q6_k(wg, UG_ROWS * UG_IN // 256, seed=1)
     w = torch.empty(rmi.q6_k_packed_bytes(UG_IN, UG_ROWS), dtype=torch.uint8, device="cuda")
-    rmi.q6_k_pack(wg, w, UG_IN, UG_ROWS, stream)
+    rmi.q6_k_pack_swiglu(wg, w, UG_IN, UG_ROWS // 2, stream)
     del wg
     x = torch.empty(2 * UG_IN, device="cuda")
     rmi.gen_normal(x, x.numel(), seed=2)
     xq = torch.empty(rmi.native_q8_1_bytes(UG_IN, 2), dtype=torch.uint8, device="cuda")
     rmi.native_quantize_q8_1(x, xq, UG_IN, 2)
-    y = torch.empty(2 * UG_ROWS, device="cuda")
+    y = torch.empty(rmi.native_q8_1_bytes(UG_ROWS // 2, 2), dtype=torch.uint8, device="cuda")
     a = torch.ones(COPY_KIB_ELEMS, device="cuda")
     b = torch.empty_like(a)
     junk = torch.empty(256 * 1024 * 1024, device="cuda")
     torch.cuda.synchronize()
     junk.fill_(1.0)
     torch.cuda.synchronize()
-    rmi.native_q6_k_mmvq_packed(w, xq, y, UG_IN, UG_ROWS, 2, stream)
+    rmi.native_q6_k_swiglu_packed(w, xq, y, UG_IN, UG_ROWS // 2, 2, stream)
     torch.cuda.synchronize()
     junk.fill_(2.0)
     torch.cuda.synchronize()
