@@ -48,10 +48,10 @@ PAIR_BYTES = UG_BYTES + DN_BYTES                                                
 UGS_BYTES = q6_bytes(UG_ROWS, UG_IN) + 2 * (UG_IN // 32) * 36 + 2 * (UG_ROWS // 2 // 32) * 36  # 82,612,224
 
 # HBM traffic of one fused up||gate + SwiGLU ncols=2 launch, from two rocprofv3 --pmc passes over `bench.py --workload
-# traffic_probe` (profiles/gemv_up_gate_traffic.md): FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by
+# traffic_probe` (profiles/gemv_up_gate_swiglu_traffic.md): FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by
 # what the same counter reads for a copy kernel that reads 256 MiB and writes 256 MiB in the same process.
-PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 40478.5, 192.0625
-PMC_COPY_FETCH_KIB, PMC_COPY_WRITE_KIB, COPY_KIB = 131091.625, 262144.0, 262144.0
+PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 40500.4375, 48.0
+PMC_COPY_FETCH_KIB, PMC_COPY_WRITE_KIB, COPY_KIB = 131087.8125, 262144.0, 262144.0
 UG_TRAFFIC_BYTES = round(1024 * (PMC_UG_FETCH_KIB * COPY_KIB / PMC_COPY_FETCH_KIB
                                  + PMC_UG_WRITE_KIB * COPY_KIB / PMC_COPY_WRITE_KIB))
 
