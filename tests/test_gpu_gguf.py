@@ -220,3 +220,24 @@ def test_gguf_engine_greedy_and_mtp_streams(orc, E, tmp_path):
     mtp, st = eng.generate(12, mode=E.MTP)
     assert mtp == toks
     eng.close()
+
+
+def test_gguf_engine_swiglu_packing_at_4096(orc, E, tmp_path, monkeypatch):
+    """at 4096-wide rows the loader packs up||gate in the SwiGLU row order: the fused up||gate + SwiGLU kernel (decode)
+    and the interleaved SwiGLU (ingest chunks) must still follow the oracle model, and agree bit for bit"""
+    import sys
+    mod = sys.modules[__name__]
+    monkeypatch.setattr(mod, "N_EMBD", 4096)
+    t, meta = build_model(orc, seed=4, pattern=(0,))
+    eng = E.Engine.from_gguf(write(t, meta, tmp_path / "w.gguf"), max_ctx=512)
+    assert eng.cfg.n_embd == 4096
+    m = oracle_model(orc, t, 1, rope_factor=1.0, rope_orig_ctx=4096.0)
+    prompt = [int(x) for x in np.random.default_rng(13).integers(0, N_VOCAB, 7)]
+    first = eng.prefill(prompt, batch=1)
+    lo, h = m.prefill(prompt)
+    close(eng.read(E.BUF_LOGITS, 0, 4 * N_VOCAB).view(np.float32), lo, 1e-2, "logits")
+    close(eng.read(E.BUF_HIDDEN, 0, 4 * 4096).view(np.float32), h, 1e-2, "hidden")
+    h1 = eng.read(E.BUF_HIDDEN, 0, 4 * 4096)
+    assert eng.prefill(prompt, batch=16) == first
+    assert np.array_equal(eng.read(E.BUF_HIDDEN, 0, 4 * 4096), h1)
+    eng.close()
