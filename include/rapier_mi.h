@@ -134,6 +134,12 @@ int rmi_q6_k_block_dots(const void* w, const void* x_q8_1, int32_t* out, int n_i
 /* Q8_1 of (x * w) * rsqrt(sum(partials) / cols + eps).  Replaces rms_quant_apply_kernel (qw:627-655). */
 int rmi_rms_quant_apply(const float* x, const float* w, const float* partials, void* y_q8_1, int cols, float eps,
                         int ncols, void* stream);
+/* Two rmi_rms_quant_apply results of cols each into the two halves of one 2 cols Q8_1 row per column (x0 -> blocks
+ * [0, cols/32), x1 -> [cols/32, cols/16)).  No counterpart in the reference: it replaces its two rms_norm_out calls
+ * and the quantize of their concatenation in the draft's input (qw:1327-1332), with the same bits. */
+int rmi_rms_quant_apply_pair(const float* x0, const float* w0, const float* partials0, const float* x1,
+                             const float* w1, const float* partials1, void* y_q8_1, int cols, float eps, int ncols,
+                             void* stream);
 /* fp32 out = (x * w) * rsqrt(...); out_partials (nullable) gets the output's own 4-row partials.
  * Replaces rms_norm_out_kernel (qw:658-672) fused with row_sum_partials_kernel (qw:616-623). */
 int rmi_rms_norm_out(const float* x, const float* w, const float* partials, float* out, float* out_partials, int cols,

@@ -139,7 +139,7 @@ struct Engine {
     // writes its hidden to columns 1..nc, so that column c - 1 is the draft input of column c
     float *x = nullptr, *part = nullptr, *proj = nullptr, *ug = nullptr, *y = nullptr, *logits = nullptr;
     float *hsave = nullptr, *hpart = nullptr, *hzero = nullptr, *pzero = nullptr, *qbuf = nullptr;
-    float *ex = nullptr, *epart = nullptr, *eh = nullptr, *dx = nullptr, *dpart = nullptr;
+    float *ex = nullptr, *epart = nullptr, *dx = nullptr, *dpart = nullptr;
     uint8_t *q8a = nullptr, *q8f = nullptr, *q8y = nullptr;
     void *attn_ws = nullptr, *argmax_ws = nullptr, *topk_ws = nullptr;
     int* topk_out = nullptr;        // top-k ids [0, 64) and logits (as float) [64, 128)
@@ -523,15 +523,13 @@ int trunk(Engine& e, int nc) {
 }
 
 // draft (nextn) block for nc columns: tokens tok[c] at positions pos[0] + c (pos: see attn_block), previous hidden
-// h / hp.  eh = [enorm(emb) | hnorm(h)] per column (embedding first, qw:1327-1332).  Argmax to ints[kC0 + c] when
-// with_head.
+// h / hp.  eh_proj's input = [enorm(emb) | hnorm(h)] per column (embedding first, qw:1327-1332).  Argmax to
+// ints[kC0 + c] when with_head.
 int draft_cols(Engine& e, const int* tok, const int* pos, const float* h, const float* hp, int nc, bool with_head) {
     const auto& c = e.cfg;
     RMI_TRY(rmi_embed(e.emb_type, e.tok_embd, tok, e.ex, e.epart, c.n_embd, c.n_vocab, nc, e.s));
-    RMI_TRY(rmi_rms_norm_out_strided(e.ex, e.enorm, e.epart, e.eh, 2 * c.n_embd, nullptr, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(rmi_rms_norm_out_strided(h, e.hnorm, hp, e.eh + c.n_embd, 2 * c.n_embd, nullptr, c.n_embd, c.eps, nc,
-                                     e.s));
-    RMI_TRY(rmi_native_quantize_q8_1(e.eh, e.q8f, 2 * c.n_embd, nc, e.s));
+    // [enorm(emb) | hnorm(h)] straight into the Q8_1 row of eh_proj's input: the bits of norm, norm, quantize
+    RMI_TRY(rmi_rms_quant_apply_pair(e.ex, e.enorm, e.epart, h, e.hnorm, hp, e.q8f, c.n_embd, c.eps, nc, e.s));
     RMI_TRY(gemv(e, e.eh_proj, e.q8f, e.dx, nc));
     RMI_TRY(rmi_row_sum_partials(e.dx, e.dpart, c.n_embd, nc, e.s));
     RMI_TRY(attn_block(e, e.draft, e.dx, e.dpart, pos, nc));
@@ -994,7 +992,6 @@ int alloc_runtime(Engine& e) {
     RMI_TRY(e.alloc(&e.qbuf, K * e.attn_q));
     RMI_TRY(e.alloc(&e.ex, K * c.n_embd));
     RMI_TRY(e.alloc(&e.epart, K * np));
-    RMI_TRY(e.alloc(&e.eh, K * 2 * c.n_embd));
     RMI_TRY(e.alloc(&e.dx, K * c.n_embd));
     RMI_TRY(e.alloc(&e.dpart, K * np));
     RMI_TRY(e.alloc(&e.q8a, K * q81_bytes(c.n_embd)));

@@ -35,14 +35,11 @@ __device__ float block_sum_partials(const float* __restrict__ p, int np) {
 
 __device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
 
-// Q8_1 of (x * w) * inv, one lane per element (reference rms_quant_apply_kernel, qw:627-655)
-__global__ __launch_bounds__(256) void rms_quant_apply_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                              const float* __restrict__ partials,
-                                                              uint8_t* __restrict__ y, int cols, float eps) {
-    const int c = blockIdx.y;
-    x += static_cast<size_t>(c) * cols;
-    partials += static_cast<size_t>(c) * (cols / 4);
-    y += static_cast<size_t>(c) * (cols / 32) * kQ8_1Bytes;
+// Q8_1 of (x * w) * inv of one column, one lane per element (reference rms_quant_apply_kernel, qw:627-655); y is the
+// column's first Q8_1 block
+__device__ __forceinline__ void rms_quant_column(const float* __restrict__ x, const float* __restrict__ w,
+                                                 const float* __restrict__ partials, uint8_t* __restrict__ y, int cols,
+                                                 float eps) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     // x and w do not depend on the reduction: in flight together with the partials (clamped, unconditional)
     const float xv = x[min(i, cols - 1)], wv = w[min(i, cols - 1)];
@@ -50,6 +47,29 @@ __global__ __launch_bounds__(256) void rms_quant_apply_kernel(const float* __res
     const float inv = rsqrtf(ss / static_cast<float>(cols) + eps);
     if (i >= cols) return;   // cols % 32 == 0: whole 32-lane groups leave together
     q8_1_store_lane((xv * wv) * inv, y + static_cast<size_t>(i / 32) * kQ8_1Bytes);
+}
+
+__global__ __launch_bounds__(256) void rms_quant_apply_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                              const float* __restrict__ partials,
+                                                              uint8_t* __restrict__ y, int cols, float eps) {
+    const int c = blockIdx.y;
+    rms_quant_column(x + static_cast<size_t>(c) * cols, w, partials + static_cast<size_t>(c) * (cols / 4),
+                     y + static_cast<size_t>(c) * (cols / 32) * kQ8_1Bytes, cols, eps);
+}
+
+// two normed vectors of a column into the two halves of one Q8_1 row of 2 cols (blockIdx.z = half)
+struct NormInput {
+    const float* x;
+    const float* w;
+    const float* partials;
+};
+
+__global__ __launch_bounds__(256) void rms_quant_pair_kernel(NormInput a, NormInput b, uint8_t* __restrict__ y,
+                                                             int cols, float eps) {
+    const int c = blockIdx.y;
+    const NormInput& in = blockIdx.z ? b : a;
+    rms_quant_column(in.x + static_cast<size_t>(c) * cols, in.w, in.partials + static_cast<size_t>(c) * (cols / 4),
+                     y + (static_cast<size_t>(c) * 2 + blockIdx.z) * (cols / 32) * kQ8_1Bytes, cols, eps);
 }
 
 // fp32 out = (x * w) * inv (reference rms_norm_out_kernel, qw:658-672), optionally with the output's own partials
@@ -303,6 +323,19 @@ extern "C" int rmi_rms_quant_apply(const float* x, const float* w, const float* 
     hipLaunchKernelGGL(rms_quant_apply_kernel, dim3((cols + 255) / 256, ncols), dim3(256), 0,
                        static_cast<hipStream_t>(stream), x, w, partials, static_cast<uint8_t*>(y_q8_1), cols, eps);
     return launch_status("rms_quant_apply");
+}
+
+extern "C" int rmi_rms_quant_apply_pair(const float* x0, const float* w0, const float* partials0, const float* x1,
+                                        const float* w1, const float* partials1, void* y_q8_1, int cols, float eps,
+                                        int ncols, void* stream) {
+    if (cols <= 0 || cols % 32 != 0 || bad_cols(ncols)) return fail(RMI_ERR_SHAPE, "rms_quant_apply_pair: bad shape");
+    if (!aligned4(x0) || !aligned4(w0) || !aligned4(partials0) || !aligned4(x1) || !aligned4(w1) ||
+        !aligned4(partials1) || !aligned4(y_q8_1))
+        return fail(RMI_ERR_POINTER, "rms_quant_apply_pair: null or misaligned pointer");
+    hipLaunchKernelGGL(rms_quant_pair_kernel, dim3((cols + 255) / 256, ncols, 2), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), NormInput{x0, w0, partials0}, NormInput{x1, w1, partials1},
+                       static_cast<uint8_t*>(y_q8_1), cols, eps);
+    return launch_status("rms_quant_apply_pair");
 }
 
 extern "C" int rmi_rms_norm_out_strided(const float* x, const float* w, const float* partials, float* out,
