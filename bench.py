@@ -50,8 +50,8 @@ UGS_BYTES = q6_bytes(UG_ROWS, UG_IN) + 2 * (UG_IN // 32) * 36 + 2 * (UG_ROWS // 
 # HBM traffic of one fused up||gate + SwiGLU ncols=2 launch, from two rocprofv3 --pmc passes over `bench.py --workload
 # traffic_probe` (profiles/gemv_up_gate_swiglu_traffic.md): FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by
 # what the same counter reads for a copy kernel that reads 256 MiB and writes 256 MiB in the same process.
-PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 40500.4375, 48.0
-PMC_COPY_FETCH_KIB, PMC_COPY_WRITE_KIB, COPY_KIB = 131087.8125, 262144.0, 262144.0
+PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 40505.75, 48.0
+PMC_COPY_FETCH_KIB, PMC_COPY_WRITE_KIB, COPY_KIB = 131087.625, 262144.0, 262144.0
 UG_TRAFFIC_BYTES = round(1024 * (PMC_UG_FETCH_KIB * COPY_KIB / PMC_COPY_FETCH_KIB
                                  + PMC_UG_WRITE_KIB * COPY_KIB / PMC_COPY_WRITE_KIB))
 

@@ -50,7 +50,9 @@ SIGNATURES = {
     "rmi_gen_normal": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
     "rmi_gen_normal_f16": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
     "rmi_rms_quant_apply": (_i, [_vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
+    "rmi_rms_quant_apply_pair": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
     "rmi_rms_norm_out": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
+    "rmi_rms_norm_out_strided": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _f, _i, _vp]),
     "rmi_row_sum_partials": (_i, [_vp, _vp, _i, _i, _vp]),
     "rmi_add_partials": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "rmi_swiglu_quant": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
@@ -233,9 +235,19 @@ def rms_quant_apply(x, w, partials, y_q8_1, cols, eps, ncols=1, stream=None):
     _call("rmi_rms_quant_apply", _p(x), _p(w), _p(partials), _p(y_q8_1), cols, eps, ncols, _stream(stream))
 
 
+def rms_quant_apply_pair(x0, w0, partials0, x1, w1, partials1, y_q8_1, cols, eps, ncols=1, stream=None):
+    _call("rmi_rms_quant_apply_pair", _p(x0), _p(w0), _p(partials0), _p(x1), _p(w1), _p(partials1), _p(y_q8_1), cols,
+          eps, ncols, _stream(stream))
+
+
 def rms_norm_out(x, w, partials, out, out_partials, cols, eps, ncols=1, stream=None):
     _call("rmi_rms_norm_out", _p(x), _p(w), _p(partials), _p(out), _p(out_partials), cols, eps, ncols,
           _stream(stream))
+
+
+def rms_norm_out_strided(x, w, partials, out, out_stride, out_partials, cols, eps, ncols=1, stream=None):
+    _call("rmi_rms_norm_out_strided", _p(x), _p(w), _p(partials), _p(out), out_stride, _p(out_partials), cols, eps,
+          ncols, _stream(stream))
 
 
 def row_sum_partials(x, partials, n, ncols=1, stream=None):

@@ -48,6 +48,34 @@ def test_rms_quant_apply_two_columns(orc, rmi):
     assert np.array_equal(host(y1), yh[4608:])
 
 
+def test_rms_quant_apply_pair_equals_two_norms_then_quantize(orc, rmi):
+    """The draft's input (qwythos.cpp:1327-1332): [enorm(emb) | hnorm(h)] per column as one Q8_1 row of 2 cols, in
+    one launch; bitwise the reference's two rms_norm_out calls into eh_cat and the quantize of eh_cat."""
+    cols, eps, nc = 4096, 1e-6, 2
+    e = orc.normal(nc * cols, seed=11)
+    h = orc.normal(nc * cols, seed=12, std=3.0)
+    we = (1 + orc.normal(cols, seed=13, std=0.1)).astype(np.float32)
+    wh = (1 + orc.normal(cols, seed=14, std=0.1)).astype(np.float32)
+    pe = np.concatenate([orc.row_sum_partials(e[c * cols:(c + 1) * cols]) for c in range(nc)]).astype(np.float32)
+    ph = np.concatenate([orc.row_sum_partials(h[c * cols:(c + 1) * cols]) for c in range(nc)]).astype(np.float32)
+    row = 2 * cols // 32 * 36
+    y = empty(nc * row, "uint8")
+    rmi.rms_quant_apply_pair(dev(e), dev(we), dev(pe), dev(h), dev(wh), dev(ph), y, cols, eps, ncols=nc)
+    yh = host(y)
+    cat = empty(nc * 2 * cols)
+    rmi.rms_norm_out_strided(dev(e), dev(we), dev(pe), cat, 2 * cols, None, cols, eps, ncols=nc)
+    rmi.rms_norm_out_strided(dev(h), dev(wh), dev(ph), cat[cols:], 2 * cols, None, cols, eps, ncols=nc)
+    yq = empty(nc * row, "uint8")
+    rmi.native_quantize_q8_1(cat, yq, 2 * cols, nc)
+    assert np.array_equal(yh, host(yq))
+    for c in range(nc):
+        ref = np.concatenate([
+            orc.rms_norm_out(x[c * cols:(c + 1) * cols], w, orc.rms_inv(p[c * 1024:(c + 1) * 1024].astype(np.float64),
+                                                                        cols, eps))
+            for x, w, p in ((e, we, pe), (h, wh, ph))])
+        check_q8(orc, yh[c * row:(c + 1) * row], ref, f"rms_quant_apply_pair col {c}")
+
+
 def test_rms_norm_out_and_partials(orc, rmi):
     cols, eps = 4096, 1e-6
     x = orc.normal(cols, seed=3)
