@@ -228,6 +228,20 @@ typedef struct rmi_rope_params {
 int rmi_attn_prep_rope(const float* q3, int q3_stride, const float* qn, const float* kn, uint16_t* kcache,
                        uint16_t* vcache, const int* pos, float* qout, int n_head, int n_kv, int head_dim, int n_rot,
                        const rmi_rope_params* rope, float eps, int ntok, int max_ctx, void* stream);
+/* Per-row RMSNorm in place: x[r][c] = x[r][c] * rsqrt(mean_c(x[r][:]^2) + eps) * w[c], rows x cols, cols <= 8192.
+ * Replaces strata::kernels::rms_norm_weighted (qw:971-975; the q / k per-head norms, rows = heads, cols = 256).  At
+ * cols = 256 the bits equal rmi_attn_prep's fused norm. */
+int rmi_rms_norm_weighted(float* x, const float* w, int rows, int cols, float eps, void* stream);
+/* NEOX RoPE (YaRN ramp when rope->factor > 1) on the first n_rot dims of each of `heads` rows of head_dim floats,
+ * head h at position pos[h] (device), dims >= n_rot copied; x may equal y.  Replaces strata::kernels::native_rope_apply
+ * (qw:1165-1166, 1357-1358, 1542-1544, 2380-2407; parameters qw:1991-1999).  Norm + rope equals rmi_attn_prep's q. */
+int rmi_native_rope_apply(const float* x, float* y, int heads, int head_dim, int n_rot, const rmi_rope_params* rope,
+                          const int* pos, void* stream);
+/* x += y; x *= s; x = silu(x) over n floats.  Replace strata::kernels::add_inplace / scale_inplace / silu_inplace
+ * (qw:1002, 1053, 1059, 1068, 1178: the reference's --split and old-GDN paths). */
+int rmi_add_inplace(float* x, const float* y, int n, void* stream);
+int rmi_scale_inplace(float* x, int n, float s, void* stream);
+int rmi_silu_inplace(float* x, int n, void* stream);
 /* split-K flash decode for ntok query tokens at positions pos[0] + t, sigmoid gate from gate_src (the wq output,
  * gate of head h at + h * 2 * head_dim + head_dim), fp32 y (nullable) and Q8_1 (nullable).  workspace holds
  * rmi_gqa_workspace_bytes(max_ctx, n_kv, nsub) bytes; chunks are 64 * nsub positions.  ntok * (n_head / n_kv)

@@ -6,6 +6,10 @@
 //   MMVQ family (mmvq:2312-2331): std::invalid_argument for shape / ncols / pointer / null-stream errors,
 //   std::runtime_error for a failed launch.
 //   fused_gdn family (fgdn:169-175, 194-204): message on stderr and std::exit(1).
+//   RoPE, per-row norm and elementwise calls: as the MMVQ family (their strata definitions are absent from the
+//   reference tree).
+// The device-side Q8_1 helpers the reference's own kernels call (q8_1_finite / q8_1_quant / q8_1_ds, qw:10-13) are in
+// rapier_mi_q8_1.hpp (HIP device code).
 #pragma once
 
 #include <cstdint>
@@ -102,5 +106,39 @@ inline void fused_gdn_step_norm_silu_q8(float* state, const float* q, const floa
     rmi_detail::check_exit(
         rmi_fused_gdn_step_norm_silu_q8(state, q, k, v, gate, beta, z, gamma, eps, y, q8, h_k, h_v, stream));
 }
+
+// RoPE configuration as the reference fills it for qwen35 (qw:280, 1991-1999).  strata's own definition is absent
+// from the reference tree: these are the members the reference sets; RopeScalingType::None is plain NEOX RoPE.
+enum class RopeScalingType { None, YaRN };
+struct RopeScaling {
+    RopeScalingType type = RopeScalingType::None;
+    float freq_base = 10000.0f;
+    float factor = 1.0f;
+    float orig_ctx = 0.0f;
+    float ext_factor = 0.0f;
+    float attn_factor = 1.0f;
+    float beta_fast = 32.0f;
+    float beta_slow = 1.0f;
+};
+// qw:1165-1166, 1357-1358, 1542-1544, 2380-2407: heads rows of head_dim, head h at position pos[h] (device)
+inline void native_rope_apply(const float* x, float* y, int heads, int head_dim, int n_rot, const RopeScaling& rope,
+                              const int* pos, void* stream) {
+    const bool yarn = rope.type == RopeScalingType::YaRN;
+    const rmi_rope_params p{rope.freq_base, yarn ? rope.factor : 1.0f, rope.orig_ctx, rope.ext_factor,
+                            rope.attn_factor, rope.beta_fast, rope.beta_slow};
+    rmi_detail::check_mmvq(rmi_native_rope_apply(x, y, heads, head_dim, n_rot, &p, pos, stream));
+}
+// qw:971-975
+inline void rms_norm_weighted(float* x, const float* w, int rows, int cols, float eps, void* stream) {
+    rmi_detail::check_mmvq(rmi_rms_norm_weighted(x, w, rows, cols, eps, stream));
+}
+// qw:1002, 1068, 1178 (x += y), 1059 (x *= s), 1053 (x = silu(x))
+inline void add_inplace(float* x, const float* y, int n, void* stream) {
+    rmi_detail::check_mmvq(rmi_add_inplace(x, y, n, stream));
+}
+inline void scale_inplace(float* x, int n, float s, void* stream) {
+    rmi_detail::check_mmvq(rmi_scale_inplace(x, n, s, stream));
+}
+inline void silu_inplace(float* x, int n, void* stream) { rmi_detail::check_mmvq(rmi_silu_inplace(x, n, stream)); }
 
 }  // namespace strata::kernels

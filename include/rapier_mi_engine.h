@@ -162,7 +162,10 @@ enum {
     RMI_BUF_K_CACHE = 2,     /* K cache of an attention layer (layer n_layer: the draft block), fp16 [pos][n_kv][256] */
     RMI_BUF_V_CACHE = 3,
     RMI_BUF_HIDDEN = 4,      /* final-normed hidden of the last forward, fp32 [n_embd] (the first draft's input) */
-    RMI_BUF_LOGITS = 5       /* logits of the last head pass, fp32 [2][n_vocab] (column 0: the last forward) */
+    RMI_BUF_LOGITS = 5,      /* logits of the last head pass, fp32 [2][n_vocab] (column 0: the last forward) */
+    RMI_BUF_ROUND = 6        /* the round's token slots, int32 [8] (layer ignored): position of the current token,
+                                current token, draft candidate for the next verify, verify argmax of columns 0 / 1,
+                                draft argmax of columns 0 / 1, accept flag of the last verify */
 };
 /* copy bytes [offset, offset + bytes) of an engine buffer to host memory; synchronizes the engine stream */
 int rmi_engine_read(rmi_engine* e, int which, int layer, size_t offset, void* dst, size_t bytes);

@@ -71,6 +71,11 @@ SIGNATURES = {
                                   _i, _i, _i, _i, _vp]),
     "rmi_attn_prep": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _f, _i, _i, _vp]),
     "rmi_attn_prep_rope": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _f, _i, _i, _vp]),
+    "rmi_rms_norm_weighted": (_i, [_vp, _vp, _i, _i, _f, _vp]),
+    "rmi_native_rope_apply": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "rmi_add_inplace": (_i, [_vp, _vp, _i, _vp]),
+    "rmi_scale_inplace": (_i, [_vp, _i, _f, _vp]),
+    "rmi_silu_inplace": (_i, [_vp, _i, _vp]),
     "rmi_gqa_workspace_bytes": (_sz, [_i, _i, _i]),
     "rmi_gqa_flash_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _f,
                                   _vp]),
@@ -343,6 +348,30 @@ def attn_prep_rope(q3, q3_stride, qn, kn, kcache, vcache, pos, qout, n_head, n_k
     rope = RopeParams(freq_base, factor, orig_ctx, ext_factor, attn_factor, beta_fast, beta_slow)
     _call("rmi_attn_prep_rope", _p(q3), q3_stride, _p(qn), _p(kn), _p(kcache), _p(vcache), _p(pos), _p(qout), n_head,
           n_kv, head_dim, n_rot, ctypes.byref(rope), eps, ntok, max_ctx, _stream(stream))
+
+
+def rms_norm_weighted(x, w, rows, cols, eps, stream=None):
+    """per-row RMSNorm in place (strata::kernels::rms_norm_weighted, qw:971-975)"""
+    _call("rmi_rms_norm_weighted", _p(x), _p(w), rows, cols, eps, _stream(stream))
+
+
+def native_rope_apply(x, y, heads, head_dim, n_rot, pos, freq_base, factor=1.0, orig_ctx=0.0, ext_factor=1.0,
+                      attn_factor=1.0, beta_fast=32.0, beta_slow=1.0, stream=None):
+    """NEOX / YaRN RoPE of each head at its device position pos[h] (strata::kernels::native_rope_apply)"""
+    rope = RopeParams(freq_base, factor, orig_ctx, ext_factor, attn_factor, beta_fast, beta_slow)
+    _call("rmi_native_rope_apply", _p(x), _p(y), heads, head_dim, n_rot, ctypes.byref(rope), _p(pos), _stream(stream))
+
+
+def add_inplace(x, y, n, stream=None):
+    _call("rmi_add_inplace", _p(x), _p(y), n, _stream(stream))
+
+
+def scale_inplace(x, n, s, stream=None):
+    _call("rmi_scale_inplace", _p(x), n, s, _stream(stream))
+
+
+def silu_inplace(x, n, stream=None):
+    _call("rmi_silu_inplace", _p(x), n, _stream(stream))
 
 
 def gqa_workspace_bytes(max_ctx, n_kv, nsub):

@@ -16,6 +16,7 @@
 // Query t sees positions <= pos[0] + t.  Chunk boundaries depend only on the query's position, so a verify column's
 // result is bitwise the single-token result at the same position.
 #include "rmi_common.h"
+#include "rope.h"
 
 #include <cmath>
 
@@ -43,13 +44,7 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 }
 
 // ---- attn_prep -------------------------------------------------------------------------------------------------------
-// YaRN (the reference's rope configuration, qw:1991-1999): per rotary pair i, theta = theta_extrap (pos base^(-2i/n_rot))
-// mixed with theta_extrap / factor by ramp(i) ext_factor, ramp = 1 - clamp((i - low) / max(0.001, high - low), 0, 1);
-// cos and sin scaled by mscale.  low, high and mscale come from the host in fp64.  yarn = 0: plain NEOX RoPE.
-struct Yarn {
-    int on;
-    double factor, low, high, ext, mscale;
-};
+// RoPE: rope.h (NEOX pairs with the YaRN ramp; plain NEOX when yarn.on == 0).
 
 // q3 per token: [n_head x (q HD | gate HD) | k n_kv*HD | v n_kv*HD] at q3 + t * q3_stride.
 __global__ __launch_bounds__(HD) void attn_prep_kernel(const float* __restrict__ q3, int q3_stride,
@@ -86,20 +81,9 @@ __global__ __launch_bounds__(HD) void attn_prep_kernel(const float* __restrict__
     const int half = n_rot / 2;
     if (d < n_rot) {
         const int i = d < half ? d : d - half;
-        double ang = static_cast<double>(p) * pow(static_cast<double>(theta), -2.0 * i / static_cast<double>(n_rot));
-        double sn, cs;
-        if (yarn.on) {
-            const double y = (static_cast<double>(i) - yarn.low) / fmax(0.001, yarn.high - yarn.low);
-            const double ramp = (1.0 - fmin(1.0, fmax(0.0, y))) * yarn.ext;
-            ang = (ang / yarn.factor) * (1.0 - ramp) + ang * ramp;
-            sincos(ang, &sn, &cs);
-            sn *= yarn.mscale;
-            cs *= yarn.mscale;
-        } else {
-            sincos(ang, &sn, &cs);
-        }
-        const float c = static_cast<float>(cs), s = static_cast<float>(sn);
-        v = d < half ? xs[d] * c - xs[d + half] * s : xs[d - half] * s + xs[d] * c;
+        float c, s;
+        rope_cos_sin(p, i, n_rot, theta, yarn, &c, &s);
+        v = d < half ? rope_lo(xs[d], xs[d + half], c, s) : rope_hi(xs[d - half], xs[d], c, s);
     }
     if (is_q) {
         qout[(static_cast<size_t>(t) * n_head + hh) * HD + d] = v;
@@ -466,20 +450,7 @@ extern "C" int rmi_attn_prep_rope(const float* q3, int q3_stride, const float* q
     if (!aligned4(q3) || !aligned4(qn) || !aligned4(kn) || !kcache || !vcache || !aligned4(pos) || !aligned4(qout))
         return fail(RMI_ERR_POINTER, "attn_prep: invalid arguments");
     Yarn y{};
-    if (rope->factor > 1.0f) {   // scaling on: the corr dims and magnitude scale of the YaRN ramp (fp64, once per call)
-        if (!(rope->orig_ctx > 0.0f) || !(rope->beta_fast > 0.0f) || !(rope->beta_slow > 0.0f))
-            return fail(RMI_ERR_SHAPE, "attn_prep: invalid YaRN parameters");
-        const double pi = 3.14159265358979323846, base = rope->freq_base;
-        const double cf = n_rot * std::log(rope->orig_ctx / (rope->beta_fast * 2.0 * pi)) / (2.0 * std::log(base));
-        const double cs = n_rot * std::log(rope->orig_ctx / (rope->beta_slow * 2.0 * pi)) / (2.0 * std::log(base));
-        y.on = 1;
-        y.factor = rope->factor;
-        y.low = std::fmax(0.0, std::floor(cf));
-        y.high = std::fmin(static_cast<double>(n_rot - 1), std::ceil(cs));
-        y.ext = rope->ext_factor;
-        y.mscale = rope->ext_factor != 0.0f ? rope->attn_factor * (1.0 + 0.1 * std::log(static_cast<double>(rope->factor)))
-                                            : rope->attn_factor;
-    }
+    if (!yarn_setup(*rope, n_rot, &y)) return fail(RMI_ERR_SHAPE, "attn_prep: invalid YaRN parameters");
     hipLaunchKernelGGL(attn_prep_kernel, dim3(ntok, n_head + 2 * n_kv), dim3(HD), 0, static_cast<hipStream_t>(stream),
                        q3, q3_stride, qn, kn, kcache, vcache, pos, qout, n_head, n_kv, n_rot, max_ctx, rope->freq_base,
                        eps, y);

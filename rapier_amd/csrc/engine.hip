@@ -1259,6 +1259,13 @@ extern "C" int rmi_engine_read(rmi_engine* h, int which, int layer, size_t offse
             src = e.logits;
             size = sizeof(float) * 2 * static_cast<size_t>(c.n_vocab);
             break;
+        case RMI_BUF_ROUND: {
+            const int slots[8] = {st[kPos], st[kTok0], st[kTok1], st[kV0], st[kV1], st[kC0], st[kC1], st[kAccept]};
+            if (offset > sizeof(slots) || bytes > sizeof(slots) - offset)
+                return fail(RMI_ERR_SHAPE, "rmi_engine_read: range outside the buffer");
+            std::memcpy(dst, reinterpret_cast<const uint8_t*>(slots) + offset, bytes);
+            return RMI_OK;
+        }
         default:
             return fail(RMI_ERR_SHAPE, "rmi_engine_read: bad buffer");
     }

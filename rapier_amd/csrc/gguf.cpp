@@ -165,6 +165,10 @@ int parse(rmi_gguf& g) {
     }
     if (!r.ok) return fail(RMI_ERR_SHAPE, "gguf: truncated metadata");
     if (g.alignment == 0 || (g.alignment & (g.alignment - 1))) return fail(RMI_ERR_SHAPE, "gguf: bad alignment");
+    // A tensor record is at least a name length (8), a rank (4), one dimension (8), a type (4) and an offset (8):
+    // a count the remaining bytes cannot hold is rejected before anything is sized by it.
+    constexpr size_t kMinTensorRecord = 8 + 4 + 8 + 4 + 8;
+    if (n_tensors > (r.size - r.at) / kMinTensorRecord) return fail(RMI_ERR_SHAPE, "gguf: truncated tensor table");
     g.tensors.resize(n_tensors);
     for (uint64_t i = 0; i < n_tensors && r.ok; ++i) {
         rmi_gguf::Tensor& t = g.tensors[i];
@@ -219,7 +223,15 @@ extern "C" int rmi_gguf_open(const char* path, rmi_gguf** out) {
         return fail(RMI_ERR_STATE, "gguf: mmap failed");
     }
     g->map = static_cast<const uint8_t*>(m);
-    if (const int rc = parse(*g)) {
+    int rc = RMI_OK;
+    try {
+        rc = parse(*g);
+    } catch (const std::bad_alloc&) {
+        rc = fail(RMI_ERR_SHAPE, "gguf: metadata too large for host memory");
+    } catch (const std::length_error&) {
+        rc = fail(RMI_ERR_SHAPE, "gguf: metadata too large");
+    }
+    if (rc != RMI_OK) {
         delete g;
         return rc;
     }

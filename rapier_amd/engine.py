@@ -12,7 +12,7 @@ import os
 from . import _call, _stream, last_error, lib
 
 GREEDY, MTP, MTP_FORCED = 0, 1, 2
-BUF_GDN_STATE, BUF_GDN_HIST, BUF_K_CACHE, BUF_V_CACHE, BUF_HIDDEN, BUF_LOGITS = 0, 1, 2, 3, 4, 5
+BUF_GDN_STATE, BUF_GDN_HIST, BUF_K_CACHE, BUF_V_CACHE, BUF_HIDDEN, BUF_LOGITS, BUF_ROUND = 0, 1, 2, 3, 4, 5, 6
 
 
 class ModelConfig(ctypes.Structure):
@@ -281,6 +281,12 @@ class Engine:
         out = np.empty(nbytes, np.uint8)
         _call("rmi_engine_read", self._h, which, layer, offset, out.ctypes.data_as(ctypes.c_void_p), nbytes)
         return out
+
+    def round_slots(self) -> dict:
+        """the round's token slots (BUF_ROUND): position, current token, candidate, verify / draft argmaxes, accept"""
+        v = self.read(BUF_ROUND, 0, 32).view("<i4")
+        keys = ("pos", "cur", "cand", "v0", "v1", "c0", "c1", "accept")
+        return {k: int(x) for k, x in zip(keys, v)}
 
     def synth_context(self, n_ctx: int, seed: int, last_token: int) -> int:
         first = ctypes.c_int()

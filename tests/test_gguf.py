@@ -60,7 +60,9 @@ def test_reader_rejects_malformed(E, tmp_path):
     path, _, _ = sample(tmp_path)
     blob = open(path, "rb").read()
     cases = {"magic": b"GGUX" + blob[4:], "version": blob[:4] + b"\x07\0\0\0" + blob[8:],
-             "truncated meta": blob[:60], "truncated data": blob[:-100], "empty": b""}
+             "truncated meta": blob[:60], "truncated data": blob[:-100], "empty": b"",
+             # a 16M tensor count in a file of a few hundred bytes: rejected before the table is sized by it
+             "tensor count": blob[:8] + (1 << 24).to_bytes(8, "little") + blob[16:]}
     for what, data in cases.items():
         p = tmp_path / f"bad_{what.replace(' ', '_')}.gguf"
         p.write_bytes(data)

@@ -154,3 +154,56 @@ def test_attn_prep_yarn_matches_oracle(orc, rmi, factor, ntok):
         qo2 = empty(ntok * NH * HD)
         rmi.attn_prep(dev(q3), Q3, dev(qn), dev(kn), kc, vc, dpos, qo2, NH, NKV, HD, 64, base, eps, ntok, max_ctx)
         assert np.array_equal(host(qo2).view(np.uint32), qh.view(np.uint32))
+
+
+@pytest.mark.parametrize("factor", [1.0, 4.0])
+def test_standalone_norm_and_rope_match_oracle_and_attn_prep(orc, rmi, factor):
+    """the reference's separate calls (rms_norm_weighted qw:971-975, then native_rope_apply in place qw:1542-1544, each
+    head at its own device position, as dpos_b holds per-head positions at qw:2380): within 1e-5 of the oracle's
+    RMSNorm + RoPE / YaRN, and bitwise attn_prep's fused q (same norm tree, same rotation)"""
+    max_ctx, p0, base, eps, orig, ntok = 1 << 18, 150001, 1e7, 1e-6, 65536.0, 2
+    q3 = orc.normal(ntok * Q3, seed=970)
+    qn = (1 + orc.normal(HD, seed=971, std=0.1)).astype(np.float32)
+    kn = (1 + orc.normal(HD, seed=972, std=0.1)).astype(np.float32)
+    qx = np.concatenate([q3[t * Q3 + h * 2 * HD:t * Q3 + h * 2 * HD + HD] for t in range(ntok) for h in range(NH)])
+    x = dev(qx)
+    rmi.rms_norm_weighted(x, dev(qn), ntok * NH, HD, eps)
+    normed = host(x).copy()
+    pos = dev(np.repeat(np.arange(p0, p0 + ntok, dtype=np.int32), NH))
+    rmi.native_rope_apply(x, x, ntok * NH, HD, 64, pos, base, factor, orig)
+    got = host(x)
+    for t in range(ntok):
+        sl = slice(t * NH * HD, (t + 1) * NH * HD)
+        nref = orc.rms_norm_heads(qx[sl], qn, NH, HD, eps)
+        assert_close_rel(normed[sl], nref, rtol=1e-6, atol_frac=1e-7, what=f"norm t{t}")
+        rope = (orc.rope_yarn(nref, NH, HD, 64, p0 + t, base, factor, orig) if factor > 1 else
+                orc.rope_neox(nref, NH, HD, 64, p0 + t, base))
+        assert_close_rel(got[sl], rope, rtol=1e-5, atol_frac=2e-6, what=f"rope t{t}")
+    t_ = torch()
+    kc = t_.zeros(max_ctx * NKV * HD, dtype=t_.int16, device="cuda:0")
+    vc = t_.zeros(max_ctx * NKV * HD, dtype=t_.int16, device="cuda:0")
+    qo = empty(ntok * NH * HD)
+    rmi.attn_prep_rope(dev(q3), Q3, dev(qn), dev(kn), kc, vc, dev(np.array([p0], np.int32)), qo, NH, NKV, HD, 64, base,
+                       factor, orig, eps, ntok, max_ctx)
+    assert np.array_equal(host(qo).view(np.uint32), got.view(np.uint32))
+    # out of place: y gets the rotation, dims past n_rot copied, x untouched
+    y = empty(ntok * NH * HD)
+    xin = dev(normed)
+    rmi.native_rope_apply(xin, y, ntok * NH, HD, 64, pos, base, factor, orig)
+    assert np.array_equal(host(y).view(np.uint32), got.view(np.uint32))
+    assert np.array_equal(host(xin).view(np.uint32), normed.view(np.uint32))
+
+
+def test_elementwise_inplace(orc, rmi):
+    """add_inplace (x += y), scale_inplace (x *= s), silu_inplace against numpy fp32 (the --split path's glue)"""
+    n = 4096 + 37
+    a, b = orc.normal(n, seed=980), orc.normal(n, seed=981)
+    x = dev(a)
+    rmi.add_inplace(x, dev(b), n)
+    assert np.array_equal(host(x), a + b)
+    rmi.scale_inplace(x, n, 0.0883883476)
+    assert np.array_equal(host(x), (a + b) * np.float32(0.0883883476))
+    x = dev(a)
+    rmi.silu_inplace(x, n)
+    ref = a.astype(np.float64) / (1 + np.exp(-a.astype(np.float64)))
+    assert_close_rel(host(x), ref, rtol=1e-6, atol_frac=1e-7, what="silu")

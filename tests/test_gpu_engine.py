@@ -87,3 +87,47 @@ def test_qwen35_9b_mtp_stream_bit_identical_at_4k(eng_mod):
     ref, res = streams_agree(E, eng, pos0, cur0, 64, natural=False)
     assert res["accept1"]["rounds"] == 32 and res["accept0"]["rounds"] == 64
     eng.close()
+
+
+@pytest.fixture(scope="module")
+def engine_64k(eng_mod):
+    E = eng_mod
+    eng = E.Engine(E.qwen35_9b_config(), seed=2025, max_ctx=65536)
+    yield eng
+    eng.close()
+
+
+def test_qwen35_9b_mtp_stream_bit_identical_at_64k(eng_mod, engine_64k):
+    """config 5 at ctx 65536: synthetic context of 64K positions (attention over 512-position chunks, 128 of them per
+    query), greedy vs MTP at forced acceptance 0 / 0.5 / 1.0 for 64 tokens, then the config's 400 generated tokens at
+    acceptance 0.5 and with the natural draft."""
+    E, eng = eng_mod, engine_64k
+    ctx = 65536 - 512
+    first = eng.synth_context(ctx, seed=13, last_token=4321)
+    pos0, cur0 = eng.state()
+    assert pos0 == ctx and cur0 == first
+    ref, res = streams_agree(E, eng, pos0, cur0, 64, natural=False)
+    assert res["accept1"]["rounds"] == 32 and res["accept0"]["rounds"] == 64
+    # 400 generated tokens (bench/RESULTS.md:81-82 diff the 400-token stream against greedy)
+    eng.restore_state(pos0, cur0)
+    long_ref, _ = eng.generate(400, mode=E.GREEDY)
+    assert long_ref[:64] == ref
+    eng.restore_state(pos0, cur0)
+    toks, st = eng.generate(400, mode=E.MTP_FORCED, ref_tokens=long_ref, ref_base=pos0 + 1, pattern=[1, 0])
+    assert toks == long_ref, f"400-token MTP stream differs at {next(i for i in range(400) if toks[i] != long_ref[i])}"
+    assert st["accepted"] == (st["rounds"] + 1) // 2
+    eng.restore_state(pos0, cur0)
+    toks, _ = eng.generate(400, mode=E.MTP)
+    assert toks == long_ref, "400-token MTP stream (natural draft) differs from greedy"
+
+
+def test_qwen35_9b_mtp_after_ingest_past_32k(eng_mod, engine_64k):
+    """a random prompt of 33,000 tokens ingested in 16-token chunks (every GEMV, GDN step and attention chunk of the
+    batched path, the context past 32K), then MTP at forced acceptance 0 / 0.5 / 1.0 equals greedy"""
+    E, eng = eng_mod, engine_64k
+    prompt = [int(t) for t in np.random.default_rng(17).integers(0, 248320, size=33000)]
+    first = eng.prefill(prompt, batch=16)
+    pos0, cur0 = eng.state()
+    assert pos0 == len(prompt) and cur0 == first
+    ref, _ = streams_agree(E, eng, pos0, cur0, 48, natural=True)
+    assert len(set(ref)) > 3, "degenerate stream"

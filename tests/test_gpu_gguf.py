@@ -241,3 +241,66 @@ def test_gguf_engine_swiglu_packing_at_4096(orc, E, tmp_path, monkeypatch):
     assert eng.prefill(prompt, batch=16) == first
     assert np.array_equal(eng.read(E.BUF_HIDDEN, 0, 4 * 4096), h1)
     eng.close()
+
+
+def clear_margin(lo, bound):
+    top = np.sort(lo)[-2:]
+    return top[1] - top[0] > 2 * bound * np.abs(lo).max()
+
+
+@pytest.mark.parametrize("pattern,emb_type", [((0,), "Q6_K"), ((1,), "Q5_K"), ((0, 0, 0, 1), "Q6_K")])
+def test_gguf_draft_head_matches_oracle(orc, E, tmp_path, pattern, emb_type):
+    """the draft head (draft_predict with_head, qw:1316-1406: [enorm(emb) | hnorm(h)] -> eh_proj -> blk.<n_layer> ->
+    shared_head_norm -> lm_head -> argmax) against Qwen35.draft(with_head=True): the 1-column first draft after the
+    prompt, then the 2-column draft of one verify round (column 0 = (c0, hidden of verify column 0) at pos + 1,
+    column 1 = (c1, hidden of column 1) at pos + 2).  Logits within the module's flip-tolerant bars, the candidate the
+    engine keeps equal to the argmax of its own draft logits, and to the oracle's wherever its top-2 margin is clear."""
+    n_layer = len(pattern)
+    bound, corr = (1e-2, 0.9999) if n_layer == 1 else (5e-2, 0.999)
+    t, meta = build_model(orc, seed=7, emb_type=emb_type, pattern=pattern)
+    eng = E.Engine.from_gguf(write(t, meta, tmp_path / "d.gguf"), max_ctx=512)
+    m = oracle_model(orc, t, n_layer)
+    prompt = [int(x) for x in np.random.default_rng(21).integers(0, N_VOCAB, 6)]
+    n = len(prompt)
+    first = eng.prefill(prompt, batch=1)
+    lo, h = m.prefill(prompt)
+    V = N_VOCAB
+
+    def logits(col):
+        return eng.read(E.BUF_LOGITS, 0, 4 * V, offset=4 * V * col).view(np.float32)
+
+    checked = 0
+    # first draft: (current token, hidden of the last forward) at the current position
+    eng.gen_begin(E.MTP)
+    s = eng.round_slots()
+    assert (s["pos"], s["cur"]) == (n, first)
+    d = m.draft(first, n, h, with_head=True)
+    got = logits(0)
+    close(got, d, bound, "first draft logits")
+    assert np.corrcoef(got, d)[0, 1] > corr
+    assert s["c0"] == int(np.argmax(got)) == s["cand"]
+    if clear_margin(d, bound):
+        assert s["cand"] == int(np.argmax(d))
+        checked += 1
+    # one verify round: the oracle runs both verify columns, then both draft columns on the engine's tokens
+    cand = s["cand"]
+    emitted = eng.gen_step()
+    s = eng.round_slots()
+    lo0, h0 = m.forward(first, n)
+    lo1, h1 = m.forward(cand, n + 1)
+    assert emitted[0] == s["v0"]
+    if clear_margin(lo0, bound):
+        assert s["v0"] == int(np.argmax(lo0))
+    d0 = m.draft(s["v0"], n + 1, h0, with_head=True)
+    d1 = m.draft(s["v1"], n + 2, h1, with_head=True)
+    for col, ref in ((0, d0), (1, d1)):
+        got = logits(col)
+        close(got, ref, bound, f"draft column {col} logits")
+        assert np.corrcoef(got, ref)[0, 1] > corr
+        assert s[f"c{col}"] == int(np.argmax(got))
+        if clear_margin(ref, bound):
+            assert s[f"c{col}"] == int(np.argmax(ref)), f"draft column {col} argmax"
+            checked += 1
+    assert s["cand"] == (s["c1"] if s["accept"] else s["c0"])
+    assert checked >= 1, "no draft step with a clear oracle margin"
+    eng.close()

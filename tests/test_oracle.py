@@ -361,6 +361,68 @@ def test_beta_gate_and_norms(orc):
     np.testing.assert_allclose(inv, 1 / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6), rtol=1e-13)
 
 
+def _rms_norm_def(x, w, eps):
+    """RMSNorm from its definition, rowwise in fp64: x * w / sqrt(mean(x^2) + eps)."""
+    x = np.asarray(x, dtype=np.float64)
+    return x * np.asarray(w, dtype=np.float64) / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+
+
+def _norm_out(orc, x, w, eps):
+    """The engine's output-norm chain (qw:602-623, 658-672): 4-row partials, their sum, inverse RMS, (x*w)*inv."""
+    return orc.rms_norm_out(x, w, orc.rms_inv(orc.row_sum_partials(x), x.size, eps))
+
+
+def test_rms_norm_out_matches_definition(orc):
+    for n, seed in ((4096, 150), (12288, 151), (8, 152)):
+        x = orc.normal(n, seed=seed, std=3.0)
+        w = orc.normal(n, seed=seed + 10, mean=1.0, std=0.1)
+        np.testing.assert_allclose(_norm_out(orc, x, w, 1e-6), _rms_norm_def(x, w, 1e-6), rtol=1e-13, atol=0)
+
+
+def test_rms_norm_out_hand_worked_row(orc):
+    # sum of squares 1 + 4 + 4 + 16 = 25, mean 6.25, rms 2.5 (eps 0): inv = 0.4 exactly in the chain's arithmetic
+    x = np.array([1.0, -2.0, 2.0, 4.0], np.float32)
+    w = np.array([1.0, 1.0, 0.5, 2.0], np.float32)
+    np.testing.assert_allclose(_norm_out(orc, x, w, 0.0), [0.4, -0.8, 0.4, 3.2], rtol=1e-15, atol=0)
+    # w is applied elementwise: swapping two weights swaps exactly those two outputs
+    out = _norm_out(orc, x, w[[0, 1, 3, 2]], 0.0)
+    np.testing.assert_allclose(out, [0.4, -0.8, 1.6, 0.8], rtol=1e-15, atol=0)
+
+
+def test_rms_norm_out_scale_invariance_and_unit_rms(orc):
+    x = orc.normal(4096, seed=153)
+    w = orc.normal(4096, seed=154, mean=1.0, std=0.1)
+    base = _norm_out(orc, x, w, 0.0)
+    for c in (0.25, 8.0, 1024.0):   # powers of two: every step of the chain scales exactly, so the output is equal
+        assert np.array_equal(_norm_out(orc, (x * np.float32(c)).astype(np.float32), w, 0.0), base)
+    c = np.float32(3.7)              # any other factor: equal up to the fp32 rounding of c*x
+    np.testing.assert_allclose(_norm_out(orc, (x * c).astype(np.float32), w, 0.0), base, rtol=2e-7, atol=0)
+    ones = np.ones(4096, np.float32)
+    for eps in (0.0, 1e-6, 1e-2):    # w = 1: mean(out^2) = ms / (ms + eps)
+        out = _norm_out(orc, x, ones, eps)
+        ms = np.mean(x.astype(np.float64) ** 2)
+        np.testing.assert_allclose(np.mean(out * out), ms / (ms + eps), rtol=1e-12)
+
+
+def test_rms_norm_heads_matches_definition(orc):
+    rows, cols = 16, 256
+    x = orc.normal(rows * cols, seed=155, std=2.0).reshape(rows, cols)
+    x[3] *= np.float32(100.0)        # rows are normed independently: one loud head changes no other row
+    w = orc.normal(cols, seed=156, mean=1.0, std=0.1)
+    out = orc.rms_norm_heads(x, w, rows, cols, 1e-6).reshape(rows, cols)
+    np.testing.assert_allclose(out, _rms_norm_def(x, w, 1e-6), rtol=1e-13, atol=0)
+    quiet = orc.rms_norm_heads(np.delete(x, 3, axis=0), w, rows - 1, cols, 1e-6).reshape(rows - 1, cols)
+    assert np.array_equal(np.delete(out, 3, axis=0), quiet)
+    # hand-worked: two 4-wide heads, weights shared by every head (indexed by column)
+    hx = np.array([[1, -2, 2, 4], [3, 0, 0, 4]], np.float32)
+    hw = np.array([1.0, 1.0, 0.5, 2.0], np.float32)
+    ref = [[0.4, -0.8, 0.4, 3.2], [3 / 2.5, 0.0, 0.0, 2 * 4 / 2.5]]   # rms 2.5 for both rows
+    np.testing.assert_allclose(orc.rms_norm_heads(hx, hw, 2, 4, 0.0).reshape(2, 4), ref, rtol=1e-15, atol=0)
+    for c in (0.5, 64.0):            # per-row scale invariance, exact for powers of two at eps 0
+        assert np.array_equal(orc.rms_norm_heads((x * np.float32(c)).astype(np.float32), w, rows, cols, 0.0),
+                              orc.rms_norm_heads(x, w, rows, cols, 0.0))
+
+
 # ---- K-quant token-embedding formats (qw:109-115; ggml dequantize_row_q4_K / q5_K) -------------------------------
 from tests.kquant import k_blocks, pack_k_scales  # noqa: E402
 
