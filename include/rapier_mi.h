@@ -255,6 +255,20 @@ int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, const uint16_t*
                          void* workspace, int n_head, int n_kv, int head_dim, int ntok, int max_ctx, int nsub,
                          float scale, void* stream);
 
+/* rmi_gqa_flash_decode without the workspace argument, for callers that cannot allocate (code under HIP graph
+ * capture, serving loops that forbid hipMalloc).  No counterpart in the reference.  The split-K records go to the
+ * library's own scratch array on the stream's GPU (rmi_gqa_noalloc_scratch_max() = 16 MiB, held until the process
+ * ends); the call allocates and frees nothing.  Needs rmi_gqa_noalloc_scratch_bytes(max_ctx, n_kv, nsub,
+ * ntok * n_head / n_kv) <= that maximum (decode at ctx 65536 with nsub >= 4 fits), else RMI_ERR_SHAPE.  Every call on
+ * one GPU shares the array: calls that overlap on one GPU (two streams) race.  Results equal rmi_gqa_flash_decode's
+ * bit for bit. */
+size_t rmi_gqa_noalloc_scratch_bytes(int max_ctx, int n_kv, int nsub, int slots);
+size_t rmi_gqa_noalloc_scratch_max(void);
+int rmi_gqa_flash_decode_noalloc(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* pos,
+                                 const float* gate_src, int gate_stride, float* y, int y_stride, uint8_t* q8,
+                                 int q8_stride, int n_head, int n_kv, int head_dim, int ntok, int max_ctx, int nsub,
+                                 float scale, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------------
  * Seeded synthetic tensors in HBM (stand-in for a GGUF file: random-init weights; no reference counterpart)
  * ------------------------------------------------------------------------------------------------------------- */

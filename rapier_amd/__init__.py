@@ -77,6 +77,10 @@ SIGNATURES = {
     "rmi_scale_inplace": (_i, [_vp, _i, _f, _vp]),
     "rmi_silu_inplace": (_i, [_vp, _i, _vp]),
     "rmi_gqa_workspace_bytes": (_sz, [_i, _i, _i]),
+    "rmi_gqa_noalloc_scratch_bytes": (_sz, [_i, _i, _i, _i]),
+    "rmi_gqa_noalloc_scratch_max": (_sz, []),
+    "rmi_gqa_flash_decode_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _f,
+                                          _vp]),
     "rmi_gqa_flash_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _f,
                                   _vp]),
 }
@@ -382,3 +386,11 @@ def gqa_flash_decode(q, kcache, vcache, pos, gate_src, gate_stride, y, y_stride,
                      n_kv, head_dim, ntok, max_ctx, nsub, scale, stream=None):
     _call("rmi_gqa_flash_decode", _p(q), _p(kcache), _p(vcache), _p(pos), _p(gate_src), gate_stride, _p(y), y_stride,
           _p(q8), q8_stride, _p(workspace), n_head, n_kv, head_dim, ntok, max_ctx, nsub, scale, _stream(stream))
+
+
+def gqa_flash_decode_noalloc(q, kcache, vcache, pos, gate_src, gate_stride, y, y_stride, q8, q8_stride, n_head, n_kv,
+                             head_dim, ntok, max_ctx, nsub, scale, stream=None):
+    """rmi_gqa_flash_decode without a workspace argument: the split-K records live in the library's own per-GPU
+    scratch array (rmi_gqa_noalloc_scratch_max() bytes); no allocation.  Calls that overlap on one GPU race."""
+    _call("rmi_gqa_flash_decode_noalloc", _p(q), _p(kcache), _p(vcache), _p(pos), _p(gate_src), gate_stride, _p(y),
+          y_stride, _p(q8), q8_stride, n_head, n_kv, head_dim, ntok, max_ctx, nsub, scale, _stream(stream))

@@ -19,6 +19,7 @@
 #include "rope.h"
 
 #include <cmath>
+#include <mutex>
 
 namespace rmi {
 namespace {
@@ -142,8 +143,8 @@ __device__ __forceinline__ uint32_t word_of(const uint4& v, int w) {
 
 __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __restrict__ qbuf, const uint16_t* __restrict__ kc,
                                                           const uint16_t* __restrict__ vc, const int* __restrict__ pos,
-                                                          float* __restrict__ ws, int n_head, int n_kv, int ntok,
-                                                          int nsub, int max_ctx, float scale) {
+                                                          float* __restrict__ ws, int slot_stride, int n_head,
+                                                          int n_kv, int ntok, int nsub, int max_ctx, float scale) {
     __shared__ __attribute__((aligned(16))) uint8_t tiles[WAVES * KTILE];
     __shared__ float wstat[WAVES][2][SLOTS];
     const int chunk = blockIdx.x, kv = blockIdx.y, s0 = SLOTS * static_cast<int>(blockIdx.z);
@@ -347,7 +348,7 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = __builtin_fmaf(wt[w], src[i], o[i]);
         }
-        float* rec = ws + ((static_cast<size_t>(chunk) * n_kv + kv) * kMaxSlots + s0 + q) * REC;
+        float* rec = ws + ((static_cast<size_t>(chunk) * n_kv + kv) * slot_stride + s0 + q) * REC;
         reinterpret_cast<float4*>(rec + 4 + d0)[0] = make_float4(o[0], o[1], o[2], o[3]);
         reinterpret_cast<float4*>(rec + 4 + d0)[1] = make_float4(o[4], o[5], o[6], o[7]);
         if ((threadIdx.x & 31) == 0) {
@@ -363,8 +364,9 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
 // (2) lane d accumulates O = sum_c w_c o_c[d] in chunk order with the loads issued 8 chunks ahead.
 constexpr int kMaxChunks = 2048;
 
-__global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__ ws, const float* __restrict__ gsrc,
-                                                       int gstride, const int* __restrict__ pos, float* __restrict__ y,
+__global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__ ws, int slot_stride,
+                                                       const float* __restrict__ gsrc, int gstride,
+                                                       const int* __restrict__ pos, float* __restrict__ y,
                                                        int y_stride, uint8_t* __restrict__ q8, int q8_stride,
                                                        int n_head, int n_kv, int chunk_len) {
     __shared__ float wts[kMaxChunks];
@@ -374,8 +376,8 @@ __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__
     const int kv = h / G, qv = t * G + (h - kv * G);
     const float g = gsrc[static_cast<size_t>(t) * gstride + h * 2 * HD + HD + d];   // in flight with pos
     const int nchunk = min((pos[0] + t) / chunk_len + 1, kMaxChunks);
-    const size_t cstride = static_cast<size_t>(n_kv) * kMaxSlots * REC;
-    const float* base = ws + (static_cast<size_t>(kv) * kMaxSlots + qv) * REC;
+    const size_t cstride = static_cast<size_t>(n_kv) * slot_stride * REC;
+    const float* base = ws + (static_cast<size_t>(kv) * slot_stride + qv) * REC;
     // in flight together before the first barrier: the lane's first (m, l) record and the first 8 chunks' o values
     float m0 = 0.0f, l0 = 0.0f;
     if (d < nchunk) {
@@ -472,24 +474,111 @@ extern "C" size_t rmi_gqa_workspace_bytes(int max_ctx, int n_kv, int nsub) {
     return nchunks * static_cast<size_t>(n_kv) * kMaxSlots * REC * sizeof(float);
 }
 
-extern "C" int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* pos,
-                                    const float* gate_src, int gate_stride, float* y, int y_stride, uint8_t* q8,
-                                    int q8_stride, void* workspace, int n_head, int n_kv, int head_dim, int ntok,
-                                    int max_ctx, int nsub, float scale, void* stream) {
+namespace rmi {
+namespace {
+
+// Workspace records: [chunk][kv head][slot_stride][REC] floats.  Every record the merge reads (chunks 0 .. pos_t /
+// chunk_len of its query) is written by the partial launch of the same call, so nothing needs to start at zero.
+int flash_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* pos, const float* gate_src,
+                 int gate_stride, float* y, int y_stride, uint8_t* q8, int q8_stride, float* ws, int slot_stride,
+                 int n_head, int n_kv, int ntok, int nchunks, int nsub, int max_ctx, float scale, hipStream_t s) {
+    const int groups = (ntok * (n_head / n_kv) + SLOTS - 1) / SLOTS;
+    hipLaunchKernelGGL(gqa_partial_kernel, dim3(nchunks, n_kv, groups), dim3(256), 0, s, q, kcache, vcache, pos, ws,
+                       slot_stride, n_head, n_kv, ntok, nsub, max_ctx, scale);
+    hipLaunchKernelGGL(gqa_merge_kernel, dim3(ntok, n_head), dim3(HD), 0, s, ws, slot_stride, gate_src, gate_stride,
+                       pos, y, y_stride, q8, q8_stride, n_head, n_kv, SUB * nsub);
+    return launch_status("gqa_flash_decode");
+}
+
+int flash_decode_check(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* pos,
+                       const float* gate_src, float* y, uint8_t* q8, int n_head, int n_kv, int head_dim, int ntok,
+                       int max_ctx, int nsub, int* nchunks) {
     if (head_dim != HD || n_head <= 0 || n_kv <= 0 || n_head % n_kv || ntok < 1 || ntok * (n_head / n_kv) > kMaxSlots ||
         max_ctx <= 0 || max_ctx % SUB || nsub <= 0)
         return fail(RMI_ERR_SHAPE, "gqa_flash_decode: invalid arguments");
     if (!aligned16(q) || !aligned16(kcache) || !aligned16(vcache) || !aligned4(pos) || !aligned4(gate_src) ||
-        !aligned16(workspace) || (!y && !q8))
+        (!y && !q8))
         return fail(RMI_ERR_POINTER, "gqa_flash_decode: invalid arguments");
     const int chunk_len = SUB * nsub;
-    const int nchunks = (max_ctx + chunk_len - 1) / chunk_len;
-    if (nchunks > kMaxChunks) return fail(RMI_ERR_SHAPE, "gqa_flash_decode: max_ctx / (64 * nsub) exceeds 2048 chunks");
+    *nchunks = (max_ctx + chunk_len - 1) / chunk_len;
+    if (*nchunks > kMaxChunks) return fail(RMI_ERR_SHAPE, "gqa_flash_decode: max_ctx / (64 * nsub) exceeds 2048 chunks");
+    return RMI_OK;
+}
+
+// ---- the allocation-free variant's scratch ----------------------------------------------------------------------------
+// One array per GPU, in the library's code object, held until the process ends.  In host code `scratch` names a
+// host-side stand-in, not the device array: its device address comes from hipGetSymbolAddress, once per device with
+// that device current, and only that address reaches a kernel.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// the device address of `scratch` on the device that owns `stream` (the current device for the null stream)
+int scratch_address(hipStream_t stream, float** out) {
+    int dev = -1, cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return fail(RMI_ERR_LAUNCH, "gqa_flash_decode_noalloc: no current device");
+    if (!stream) dev = cur;
+    else if (hipStreamGetDevice(stream, &dev) != hipSuccess)
+        return fail(RMI_ERR_STREAM, "gqa_flash_decode_noalloc: cannot query the stream's device");
+    if (dev < 0 || dev >= kMaxDevices) return fail(RMI_ERR_STATE, "gqa_flash_decode_noalloc: device ordinal too large");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        if (dev != cur && hipSetDevice(dev) != hipSuccess)
+            return fail(RMI_ERR_LAUNCH, "gqa_flash_decode_noalloc: cannot select the stream's device");
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (dev != cur) (void) hipSetDevice(cur);
+        if (e != hipSuccess || !p) return fail(RMI_ERR_LAUNCH, "gqa_flash_decode_noalloc: hipGetSymbolAddress failed");
+        g_scratch_dev[dev] = p;
+    }
+    *out = static_cast<float*>(g_scratch_dev[dev]);
+    return RMI_OK;
+}
+
+}  // namespace
+}  // namespace rmi
+
+extern "C" int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* pos,
+                                    const float* gate_src, int gate_stride, float* y, int y_stride, uint8_t* q8,
+                                    int q8_stride, void* workspace, int n_head, int n_kv, int head_dim, int ntok,
+                                    int max_ctx, int nsub, float scale, void* stream) {
+    int nchunks = 0;
+    RMI_TRY(flash_decode_check(q, kcache, vcache, pos, gate_src, y, q8, n_head, n_kv, head_dim, ntok, max_ctx, nsub,
+                               &nchunks));
+    if (!aligned16(workspace)) return fail(RMI_ERR_POINTER, "gqa_flash_decode: invalid arguments");
+    return flash_decode(q, kcache, vcache, pos, gate_src, gate_stride, y, y_stride, q8, q8_stride,
+                        static_cast<float*>(workspace), kMaxSlots, n_head, n_kv, ntok, nchunks, nsub, max_ctx, scale,
+                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t rmi_gqa_noalloc_scratch_bytes(int max_ctx, int n_kv, int nsub, int slots) {
+    if (max_ctx <= 0 || n_kv <= 0 || nsub <= 0 || slots <= 0) return 0;
+    const int chunk_len = SUB * nsub;
+    const size_t nchunks = static_cast<size_t>((max_ctx + chunk_len - 1) / chunk_len);
+    const size_t stride = static_cast<size_t>((slots + SLOTS - 1) / SLOTS) * SLOTS;
+    return nchunks * static_cast<size_t>(n_kv) * stride * REC * sizeof(float);
+}
+
+extern "C" size_t rmi_gqa_noalloc_scratch_max(void) { return kScratchBytes; }
+
+extern "C" int rmi_gqa_flash_decode_noalloc(const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                                            const int* pos, const float* gate_src, int gate_stride, float* y,
+                                            int y_stride, uint8_t* q8, int q8_stride, int n_head, int n_kv,
+                                            int head_dim, int ntok, int max_ctx, int nsub, float scale, void* stream) {
+    int nchunks = 0;
+    RMI_TRY(flash_decode_check(q, kcache, vcache, pos, gate_src, y, q8, n_head, n_kv, head_dim, ntok, max_ctx, nsub,
+                               &nchunks));
+    const int slots = ntok * (n_head / n_kv);
+    const int slot_stride = (slots + SLOTS - 1) / SLOTS * SLOTS;
+    if (rmi_gqa_noalloc_scratch_bytes(max_ctx, n_kv, nsub, slots) > kScratchBytes)
+        return fail(RMI_ERR_SHAPE, "gqa_flash_decode_noalloc: the split-K records exceed the 16 MiB scratch "
+                                   "(chunks x kv heads x query slots; use a larger nsub or rmi_gqa_flash_decode)");
+    float* ws = nullptr;
     const auto s = static_cast<hipStream_t>(stream);
-    const int groups = (ntok * (n_head / n_kv) + SLOTS - 1) / SLOTS;
-    hipLaunchKernelGGL(gqa_partial_kernel, dim3(nchunks, n_kv, groups), dim3(256), 0, s, q, kcache, vcache, pos,
-                       static_cast<float*>(workspace), n_head, n_kv, ntok, nsub, max_ctx, scale);
-    hipLaunchKernelGGL(gqa_merge_kernel, dim3(ntok, n_head), dim3(HD), 0, s, static_cast<const float*>(workspace),
-                       gate_src, gate_stride, pos, y, y_stride, q8, q8_stride, n_head, n_kv, chunk_len);
-    return launch_status("gqa_flash_decode");
+    RMI_TRY(scratch_address(s, &ws));
+    return flash_decode(q, kcache, vcache, pos, gate_src, gate_stride, y, y_stride, q8, q8_stride, ws, slot_stride,
+                        n_head, n_kv, ntok, nchunks, nsub, max_ctx, scale, s);
 }

@@ -37,12 +37,6 @@ constexpr int kRingCap = 1 << 16;
 constexpr int kChunk = kMaxCols;  // ingest chunk: prompt tokens per weight pass
 constexpr int kAttnSlots = 64;    // query vectors per KV head one rmi_gqa_flash_decode launch takes
 
-#define RMI_TRY(expr)                         \
-    do {                                      \
-        const int rc_ = (expr);               \
-        if (rc_ != RMI_OK) return rc_;        \
-    } while (0)
-
 int hip_check(hipError_t e, const char* what) {
     if (e == hipSuccess) return RMI_OK;
     char buf[512];

@@ -23,6 +23,13 @@ void set_error(const char* msg);
 int fail(int code, const char* msg);
 int launch_status(const char* what);   // hipGetLastError after a launch -> RMI_ERR_LAUNCH with the HIP message
 
+// return the status of a call that failed
+#define RMI_TRY(expr)                  \
+    do {                               \
+        const int rc_ = (expr);        \
+        if (rc_ != RMI_OK) return rc_; \
+    } while (0)
+
 inline bool aligned4(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 inline bool aligned16(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
