@@ -12,8 +12,8 @@ then down 4096x12288 ncols=2 with residual + partials), >= 1 GiB of rotating wei
 
 Prints ONE JSON line.  For mtp_round, ``value`` is tok/s at context 4096 and acceptance 0.5; ``roofline`` is the
 up||gate verify GEMV's algorithmic bytes / its mean launch time from HIP events on its launch stream (measured in the
-same run); ``cpu_baseline`` is the oracle's threaded fp32 GEMV pair on this host, scaled to a round by its weight
-bytes.
+same run); ``cpu_baseline`` is one verify round on this host's cores: the reference's CPU arithmetic as a SIMD
+timing build (oracle/cpu_round.c), every GEMV shape, GDN layer and attention of the round timed as a leg and summed.
 """
 from __future__ import annotations
 
@@ -56,30 +56,100 @@ UG_TRAFFIC_BYTES = round(1024 * (PMC_UG_FETCH_KIB * COPY_KIB / PMC_COPY_FETCH_KI
                                  + PMC_UG_WRITE_KIB * COPY_KIB / PMC_COPY_WRITE_KIB))
 
 
-def cpu_baseline(budget_s: float = 12.0):
-    """Oracle fp32 GEMV pair (C, OpenMP over rows) on this host: the same shapes, repeated to ~budget_s."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# the 9B verify round's work at two columns: (n_in, n_out, residual, launches per round); the draft block adds one
+# attention layer (qkv, out_proj, FFN), eh_proj and a second lm_head pass
+ROUND_GEMVS = [(4096, 12352, False, 24), (4096, 10240, False, 9), (4096, 4096, True, 33), (4096, 24576, False, 33),
+               (12288, 4096, True, 33), (8192, 4096, False, 1)]
+LM_HEAD_ROWS, LM_HEAD_PASSES = 248320, 2
+ROUND_GDN, ROUND_ATTN = 24, 9
+
+
+def cpu_baseline(ctx: int = 4096, leg_s: float = 0.6):
+    """The reference's CPU path for one verify round, restated as a SIMD timing build (oracle/cpu_round.c: AVX2 /
+    AVX-512 VNNI integer dots, OpenMP), timed leg by leg on this host: each distinct GEMV shape of the round at two
+    columns (the lm_head on a 24576-row slice, scaled by rows), the 2-token GDN layer and the 2-query attention at ctx,
+    each repeated for ~leg_s; the round is the sum of legs times their launches per round.  Config 1 (Q6_K 12288x4096
+    GEMV, one column, residual) is timed on all the threads and on one."""
+    import numpy as np
+
     import oracle
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(threads, 16))
-    w_ug = oracle.gen_q6k(UG_ROWS, UG_IN, seed=101)
-    w_dn = oracle.gen_q6k(DN_ROWS, DN_IN, seed=102)
-    x_ug = oracle.quantize_q8_1(oracle.normal(2 * UG_IN, seed=103), UG_IN, 2)
-    x_dn = oracle.quantize_q8_1(oracle.normal(2 * DN_IN, seed=104), DN_IN, 2)
-    res = oracle.normal(2 * DN_ROWS, seed=105)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        oracle.q6k_gemv_f32(w_ug, x_ug, UG_IN, UG_ROWS, ncols=2, threads=threads)
-        oracle.q6k_gemv_f32(w_dn, x_dn, DN_IN, DN_ROWS, ncols=2, res=res, threads=threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 5000:
-            break
-    gbs = reps * PAIR_BYTES / el / 1e9
-    del w_ug, w_dn
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} full verify GEMV pairs (up||gate 24576x4096 + down 4096x12288 res, 2 columns) in "
-                      f"{el:.1f} s, oracle fp32 C restatement, OpenMP over rows",
-            "ms_per_pair": round(el / reps * 1e3, 3)}
+    threads = max(1, min(threads, 16))   # a one-GPU box's CPU share
+    simd = oracle.cpr().cpr_simd_level()
+
+    def timed(fn):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= leg_s and n >= 2:
+                return el / n
+
+    t_start = time.perf_counter()
+    legs, round_s = {}, 0.0
+    for n_in, n_out, res, count in ROUND_GEMVS:
+        w = oracle.gen_q6k(n_out, n_in, seed=n_in + n_out)
+        xq = oracle.quantize_q8_1(oracle.normal(2 * n_in, seed=7), n_in, 2)
+        r = oracle.normal(2 * n_out, seed=8) if res else None
+        t = timed(lambda: oracle.cpr_q6k_gemv(w, xq, n_in, n_out, ncols=2, res=r, partials=res, threads=threads))
+        legs[f"gemv {n_out}x{n_in}{' res' if res else ''} x{count}"] = round(t * 1e6, 1)
+        round_s += count * t
+        if (n_in, n_out) == (4096, 24576):   # the lm_head: the same rows of 4096, scaled to its 248320 rows
+            t_head = t * LM_HEAD_ROWS / n_out
+            legs[f"lm_head {LM_HEAD_ROWS}x4096 x{LM_HEAD_PASSES} (scaled from 24576 rows)"] = round(t_head * 1e6, 1)
+            round_s += LM_HEAD_PASSES * t_head
+        del w
+    h_k, h_v, S = 16, 32, 128
+    ch = (2 * h_k + h_v) * S
+    stride = ch + h_v * S
+    g = dict(qkvz=oracle.normal(2 * stride, seed=11), ab=oracle.normal(4 * h_v, seed=12),
+             conv_w=oracle.normal(4 * ch, seed=13, std=0.5), dt=np.zeros(h_v, np.float32),
+             ssm_a=(-np.exp(oracle.normal(h_v, seed=14, std=0.5))).astype(np.float32),
+             gamma=(1 + oracle.normal(S, seed=15, std=0.1)).astype(np.float32),
+             hist=oracle.normal(3 * ch, seed=16, std=0.5), state=oracle.normal(S * h_v * S, seed=17, std=0.05))
+    t = timed(lambda: oracle.cpr_gdn_layer(g["qkvz"], stride, g["ab"], g["conv_w"], g["dt"], g["ssm_a"], g["gamma"],
+                                           1e-6, g["hist"], g["state"], h_k, h_v, 2, threads=threads))
+    legs[f"gdn layer 2 tokens x{ROUND_GDN}"] = round(t * 1e6, 1)
+    round_s += ROUND_GDN * t
+    kc = oracle.normal(ctx * 4 * 256, seed=18).astype(np.float16).view(np.uint16)
+    vc = oracle.normal(ctx * 4 * 256, seed=19).astype(np.float16).view(np.uint16)
+    q = oracle.normal(2 * 16 * 256, seed=20)
+    t = timed(lambda: oracle.cpr_gqa_decode(q, kc, vc, 16, 4, 256, ctx - 2, 2, 1 / 16, threads=threads))
+    legs[f"attention 2 queries ctx {ctx} x{ROUND_ATTN}"] = round(t * 1e6, 1)
+    round_s += ROUND_ATTN * t
+    # config 1: one column with the residual, all threads and one
+    w = oracle.gen_q6k(12288, 4096, seed=21)
+    xq = oracle.quantize_q8_1(oracle.normal(4096, seed=22), 4096, 1)
+    r = oracle.normal(12288, seed=23)
+    c1 = timed(lambda: oracle.cpr_q6k_gemv(w, xq, 4096, 12288, ncols=1, res=r, partials=True, threads=threads))
+    c1_one = timed(lambda: oracle.cpr_q6k_gemv(w, xq, 4096, 12288, ncols=1, res=r, partials=True, threads=1))
+    tok_round = tokens_for_rounds(ACCEPT_PATTERNS["0.5"], 20) / 20
+    return {"value": round(tok_round / round_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"one verify round of the 9B-class model at ctx {ctx}, acceptance 0.5 ({tok_round:.2f} tokens per "
+                      "round), summed from legs timed on this host: every distinct GEMV shape at two columns, the GDN "
+                      "layer and the attention, each repeated ~%.1f s (%.1f s in all)"
+                      % (leg_s, time.perf_counter() - t_start),
+            "us_per_round": round(round_s * 1e6, 1),
+            "legs_us": legs,
+            "cpu_model": cpu_model(),
+            "simd": "avx512-vnni" if simd >= 2 else "avx2",
+            "config1": {"workload": "Q6_K 12288x4096 GEMV, ncols=1, residual + partials",
+                        "us": round(c1 * 1e6, 1), "GB_s": round(q6_bytes(12288, 4096) / c1 / 1e9, 2),
+                        "us_1thread": round(c1_one * 1e6, 1),
+                        "GB_s_1thread": round(q6_bytes(12288, 4096) / c1_one / 1e9, 2)}}
 
 
 def run_verify_gemv(args):
@@ -158,6 +228,7 @@ def run_verify_gemv(args):
     ug_mean_us = sum(ug_us) / len(ug_us)
     achieved = UGS_BYTES / (ug_mean_us * 1e-6) / 1e9
     del ugp
+    c1 = run_config1(stream, blocks=5)
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -180,6 +251,7 @@ def run_verify_gemv(args):
             "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
             "weight_replicas": reps,
             "rotated_bytes": reps * (q6_bytes(UG_ROWS, UG_IN) + q6_bytes(DN_ROWS, DN_IN)),
+            "config1": c1,
         },
         "roofline": {
             "kernel": "q6k_packed_swiglu<2> (up||gate 24576x4096 GEMV + SwiGLU + Q8_1, ncols=2, SwiGLU-packed "
@@ -197,6 +269,56 @@ def run_verify_gemv(args):
         },
     }
     return out
+
+
+# config 1: Q6_K 12288 x 4096, one column, residual + partials; algorithmic bytes = weights + Q8_1 x + res read +
+# y write + partials
+C1_ROWS, C1_IN = 12288, 4096
+C1_BYTES = q6_bytes(C1_ROWS, C1_IN) + (C1_IN // 32) * 36 + 2 * C1_ROWS * 4 + (C1_ROWS // 4) * 4   # 41,402,880
+
+
+def run_config1(stream, blocks=5):
+    """config 1 on the GPU: the drop-in residual GEMV on GGUF blocks (rmi_native_q6_k_mmvq_res, the reference's call)
+    and on the engine's packed copy, over >= 1.2 GB of rotating replicas, one HIP event pair per block of launches"""
+    import torch
+
+    import rapier_amd as rmi
+    reps = max(2, -(-1_200_000_000 // q6_bytes(C1_ROWS, C1_IN)))
+    ws = [torch.empty(q6_bytes(C1_ROWS, C1_IN), dtype=torch.uint8, device="cuda") for _ in range(reps)]
+    for i in range(reps):
+        rmi.gen_q6_k(ws[i], C1_ROWS * C1_IN // 256, seed=4000 + i)
+    x = torch.empty(C1_IN, device="cuda")
+    rmi.gen_normal(x, C1_IN, seed=41)
+    xq = torch.empty(rmi.native_q8_1_bytes(C1_IN, 1), dtype=torch.uint8, device="cuda")
+    rmi.native_quantize_q8_1(x, xq, C1_IN, 1)
+    y = torch.empty(C1_ROWS, device="cuda")
+    rmi.gen_normal(y, C1_ROWS, seed=42)
+    part = torch.empty(C1_ROWS // 4, device="cuda")
+
+    def time_it(fn):
+        for i in range(reps):
+            fn(i)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(blocks)]
+        torch.cuda.synchronize()
+        for b in range(blocks):
+            evs[b][0].record(stream)
+            for i in range(2 * reps):
+                fn(i % reps)
+            evs[b][1].record(stream)
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) * 1e3 / (2 * reps) for a, b in evs) / blocks
+
+    gguf_us = time_it(lambda i: rmi.native_q6_k_mmvq_res(ws[i], xq, y, y, part, C1_IN, C1_ROWS, stream))
+    wp = [torch.empty(rmi.q6_k_packed_bytes(C1_IN, C1_ROWS), dtype=torch.uint8, device="cuda") for _ in range(reps)]
+    for i in range(reps):
+        rmi.q6_k_pack(ws[i], wp[i], C1_IN, C1_ROWS, stream)
+    del ws
+    packed_us = time_it(lambda i: rmi.native_q6_k_mmvq_packed_res_n(wp[i], xq, y, y, part, C1_IN, C1_ROWS, 1, stream))
+    del wp
+    return {"workload": "config 1: Q6_K 12288x4096 GEMV, ncols=1, residual + partials (y aliases res)",
+            "algorithmic_bytes": C1_BYTES,
+            "gguf_layout_us": round(gguf_us, 2), "gguf_layout_GB_s": round(C1_BYTES / gguf_us / 1e3, 1),
+            "packed_us": round(packed_us, 2), "packed_GB_s": round(C1_BYTES / packed_us / 1e3, 1)}
 
 
 def run_traffic_probe():
@@ -545,7 +667,7 @@ def main():
     gemv_args =argparse.Namespace(steps=50 if args.workload == "mtp_round" else args.steps,
                                    warmup=10 if args.workload == "mtp_round" else args.warmup)
     gemv = run_verify_gemv(gemv_args)
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None if args.no_cpu else cpu_baseline(int(args.ctx.split(",")[0]))
     if args.workload == "verify_gemv":
         gemv["cpu_baseline"] = cpu
         print(json.dumps(gemv), flush=True)
@@ -589,15 +711,6 @@ def main():
         },
         "roofline": gemv["roofline"],
     }
-    if cpu is not None:
-        # the CPU leg times the same GEMV pair; a round streams round_weight_bytes through the same kind of GEMV
-        s_per_round = info["round_weight_bytes"] / (cpu["value"] * 1e9)
-        tok_round = tokens_for_rounds(ACCEPT_PATTERNS["0.5"], args.steps) / args.steps
-        cpu = dict(cpu, value=round(tok_round / s_per_round, 4), unit="tok/s",
-                   gemv_GB_s=cpu["value"],
-                   sample=cpu["sample"] + "; scaled to one verify round by its weight bytes "
-                          f"({info['round_weight_bytes']} B, GEMVs only: GDN/attention not counted) at "
-                          f"{tok_round:.2f} tokens per round")
     out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
 

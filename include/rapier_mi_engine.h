@@ -50,6 +50,9 @@ typedef struct rmi_engine_info_t {
     size_t token_weight_bytes;   /* one greedy token: trunk + lm_head */
     size_t kv_bytes_per_pos;     /* fp16 K+V of the trunk attention layers per position */
     int gdn_layers, attn_layers, max_ctx, attn_chunk;
+    int norm_fold;               /* 1 (RMI_NORM_FOLD=1 at creation): the norms before the in-projections, the FFNs
+                                    and the heads are folded into their GEMVs (rmi_native_q6_k_mmvq_packed_res_fold /
+                                    _scaled), on every path; 0: rms_quant_apply, the reference's order */
 } rmi_engine_info_t;
 
 enum { RMI_GEN_GREEDY = 0, RMI_GEN_MTP = 1, RMI_GEN_MTP_FORCED = 2 };

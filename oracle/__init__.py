@@ -330,3 +330,57 @@ def topk_sorted(l, k):
     l = np.asarray(l, dtype=np.float32)
     order = np.lexsort((np.arange(l.size), -(l.astype(np.float64) + 0.0)))[:k]
     return [(int(i), float(l[i])) for i in order]
+
+
+# ---- the CPU baseline's SIMD timing build (cpu_round.c) --------------------------------------------------------------
+_CPR_PATH = os.path.join(_HERE, "libcpu_round.so")
+_cpr = None
+_CPR_SIGS = {
+    "cpr_simd_level": (_c.c_int, []),
+    "cpr_q6k_gemv": (None, [_u8p, _u8p, _c.c_void_p, _f32p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
+                            _c.c_int]),
+    "cpr_gdn_layer": (None, [_f32p, _c.c_int, _f32p, _f32p, _f32p, _f32p, _f32p, _c.c_float, _f32p, _f32p, _f32p,
+                             _c.c_int, _c.c_int, _c.c_int, _c.c_int]),
+    "cpr_gqa_decode": (None, [_f32p, _u16p, _u16p, _f32p, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
+                              _c.c_float, _c.c_int]),
+}
+
+
+def cpr():
+    """the timing build (libcpu_round.so): the reported CPU baseline's kernels, checked against the oracle"""
+    global _cpr
+    if _cpr is None:
+        if not os.path.exists(_CPR_PATH):
+            subprocess.run(["make", "-s", "libcpu_round.so"], cwd=_HERE, check=True)
+        _cpr = ctypes.CDLL(_CPR_PATH)
+        for name, (res, args) in _CPR_SIGS.items():
+            fn = getattr(_cpr, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _cpr
+
+
+def cpr_q6k_gemv(w, xq, n_in, n_out, ncols=1, res=None, partials=False, threads=1, simd=2):
+    """timing-build Q6_K x Q8_1 GEMV (fp32): y, and the 4-row partials when res and partials"""
+    y = np.empty(ncols * n_out, np.float32)
+    part = np.empty(ncols * ((n_out + 3) // 4), np.float32) if (partials and res is not None) else None
+    res_a = None if res is None else np.ascontiguousarray(res, dtype=np.float32).reshape(-1)
+    cpr().cpr_q6k_gemv(w, xq, _ptr(res_a), y, _ptr(part), n_in, n_out, ncols, threads, simd)
+    return (y, part) if part is not None else y
+
+
+def cpr_gdn_layer(qkvz, stride, ab, conv_w, dt, ssm_a, gamma, eps, hist, state, h_k, h_v, ntok, threads=1):
+    """timing-build GDN layer for ntok tokens: returns (y, new history, new state); inputs are not modified"""
+    f = lambda a: np.ascontiguousarray(a, dtype=np.float32).reshape(-1)  # noqa: E731
+    hist, state = f(hist).copy(), f(state).copy()
+    y = np.empty(ntok * h_v * 128, np.float32)
+    cpr().cpr_gdn_layer(f(qkvz), stride, f(ab), f(conv_w), f(dt), f(ssm_a), f(gamma), eps, hist, state, y, h_k, h_v,
+                        ntok, threads)
+    return y, hist, state
+
+
+def cpr_gqa_decode(q, kc, vc, n_head, n_kv, hd, pos0, ntok, scale, threads=1):
+    o = np.empty(ntok * n_head * hd, np.float32)
+    cpr().cpr_gqa_decode(np.ascontiguousarray(q, np.float32).reshape(-1), np.ascontiguousarray(kc, np.uint16),
+                         np.ascontiguousarray(vc, np.uint16), o, n_head, n_kv, hd, pos0, ntok, scale, threads)
+    return o

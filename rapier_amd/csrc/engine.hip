@@ -103,6 +103,11 @@ enum Slot {
 struct Engine {
     rmi_model_config cfg{};
     int max_ctx = 0, nsub = 1;
+    // Folded norms (every path of the engine, so decode, verify and ingest stay bitwise equal): a norm's GEMV reads
+    // Q8_1(x * w) and scales its rows by inv.  q8a_norm: the norm weights whose Q8_1(x * w) the last residual GEMV's
+    // epilogue left in q8a (columns 0..), so the norm site skips its quantize launch.
+    bool fold = false;
+    const float* q8a_norm = nullptr;
     hipStream_t s = nullptr;
     bool own_stream = false;
     std::vector<void*> allocs;
@@ -437,29 +442,71 @@ __global__ void neg_exp_kernel(float* p, int n) {   // ssm_a = -exp(N(0, 0.5^2))
 }
 
 // ---- the forward building blocks (ncols = 1 or 2; every kernel is column-invariant) --------------------------------
-int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
+// A norm feeds its GEMV through q8a.  Unfolded: q8a = Q8_1((x * w) * inv) (rms_quant_apply, qw:627-655) and a plain
+// GEMV.  Folded (e.fold): q8a = Q8_1(x * w) - left by the residual GEMV that produced x when its epilogue could
+// (q8a_norm == w), else one quantize launch - and the GEMV multiplies its rows by inv, derived from x's partials.
+// Returns the Q8_1 of columns col0 .. col0 + nc - 1 (an epilogue wrote every column of its launch).
+int norm_input(Engine& e, const float* x, const float* part, const float* w, int col0, int nc, const uint8_t** xq) {
     const auto& c = e.cfg;
-    RMI_TRY(rmi_rms_quant_apply(x, L.post_norm, part, e.q8a, c.n_embd, c.eps, nc, e.s));
+    const size_t xs = static_cast<size_t>(col0) * c.n_embd, ps = static_cast<size_t>(col0) * (c.n_embd / 4);
+    const bool left = e.fold && e.q8a_norm == w;
+    e.q8a_norm = nullptr;
+    if (left) {
+        *xq = e.q8a + col0 * q81_bytes(c.n_embd);
+        return RMI_OK;
+    }
+    *xq = e.q8a;
+    if (e.fold) return rmi_quantize_q8_1_weighted(x + xs, w, e.q8a, c.n_embd, nc, e.s);
+    return rmi_rms_quant_apply(x + xs, w, part + ps, e.q8a, c.n_embd, c.eps, nc, e.s);
+}
+
+// the GEMV behind a norm: part = the normed vector's partials (columns as xq's)
+int norm_gemv(Engine& e, const Mat& m, const uint8_t* xq, const float* part, float* y, int nc) {
+    if (!e.fold) return gemv(e, m, xq, y, nc);
+    return rmi_native_q6_k_mmvq_packed_scaled(m.w, xq, part, e.cfg.eps, y, m.n_in, m.n_out, nc, e.s);
+}
+
+// residual GEMV x += W xq; folded, with the next norm's weights w_next and a shape its epilogue takes, it also leaves
+// Q8_1(x * w_next) in q8a
+int res_gemv(Engine& e, const Mat& m, const uint8_t* xq, float* x, float* part, int nc, const float* w_next) {
+    if (e.fold && w_next && m.packed && rmi_q6_k_packed_fold_supported(m.n_in, m.n_out, nc)) {
+        RMI_TRY(rmi_native_q6_k_mmvq_packed_res_fold(m.w, xq, x, x, part, w_next, e.q8a, m.n_in, m.n_out, nc, e.s));
+        e.q8a_norm = w_next;
+        return RMI_OK;
+    }
+    e.q8a_norm = nullptr;
+    return gemv_res(e, m, xq, x, part, nc);
+}
+
+// post-attention norm, up||gate + SwiGLU, down with the residual; w_next: the norm after the layer (for the fold)
+int ffn(Engine& e, Layer& L, float* x, float* part, int nc, const float* w_next) {
+    const auto& c = e.cfg;
+    const uint8_t* xq = nullptr;
+    RMI_TRY(norm_input(e, x, part, L.post_norm, 0, nc, &xq));
     if (L.upgate.swiglu_ff && nc <= 2) {   // up||gate GEMV + SwiGLU + Q8_1 in one launch
-        RMI_TRY(rmi_native_q6_k_swiglu_packed(L.upgate.w, e.q8a, e.q8f, c.n_embd, c.n_ff, nc, e.s));
+        if (e.fold)
+            RMI_TRY(rmi_native_q6_k_swiglu_packed_scaled(L.upgate.w, xq, part, c.eps, e.q8f, c.n_embd, c.n_ff, nc, e.s));
+        else
+            RMI_TRY(rmi_native_q6_k_swiglu_packed(L.upgate.w, xq, e.q8f, c.n_embd, c.n_ff, nc, e.s));
     } else {
-        RMI_TRY(gemv(e, L.upgate, e.q8a, e.ug, nc));
+        RMI_TRY(norm_gemv(e, L.upgate, xq, part, e.ug, nc));
         if (L.upgate.swiglu_ff)
             RMI_TRY(rmi_swiglu_quant_interleaved(e.ug, e.q8f, c.n_ff, nc, 2 * c.n_ff, e.s));
         else
             RMI_TRY(rmi_swiglu_quant(e.ug, e.ug + c.n_ff, e.q8f, c.n_ff, nc, 2 * c.n_ff, e.s));
     }
-    return gemv_res(e, L.down, e.q8f, x, part, nc);
+    return res_gemv(e, L.down, e.q8f, x, part, nc, w_next);
 }
 
 // pos[0] is the position of column 0; with more columns than one attention launch takes (64 query vectors per KV
 // head: 16 tokens at 4 query heads per KV head) pos is an array, pos[c] = pos[0] + c, and the launch for columns
 // c0.. reads pos + c0.  Every KV row of the nc columns is stored before any of them attends, and query c sees
 // positions <= pos[0] + c only, as in the per-token path.
-int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc) {
+int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc, const float* w_next) {
     const auto& c = e.cfg;
-    RMI_TRY(rmi_rms_quant_apply(x, L.attn_norm, part, e.q8a, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(gemv(e, L.in_proj, e.q8a, e.proj, nc));
+    const uint8_t* xq = nullptr;
+    RMI_TRY(norm_input(e, x, part, L.attn_norm, 0, nc, &xq));
+    RMI_TRY(norm_gemv(e, L.in_proj, xq, part, e.proj, nc));
     RMI_TRY(rmi_attn_prep_rope(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, e.qbuf, c.n_head, c.n_kv, c.head_dim,
                                c.n_rot, &e.rope, c.eps, nc, e.max_ctx, e.s));
     const size_t q8y_col = q81_bytes(e.attn_q);
@@ -471,20 +518,21 @@ int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int n
                                      c.head_dim, std::min(per, nc - c0), e.max_ctx, e.nsub,
                                      1.0f / sqrtf(static_cast<float>(c.head_dim)), e.s));
     }
-    RMI_TRY(gemv_res(e, L.out_proj, e.q8y, x, part, nc));
-    return ffn(e, L, x, part, nc);
+    RMI_TRY(res_gemv(e, L.out_proj, e.q8y, x, part, nc, L.post_norm));
+    return ffn(e, L, x, part, nc, w_next);
 }
 
-int gdn_block(Engine& e, Layer& L, int nc) {
+int gdn_block(Engine& e, Layer& L, int nc, const float* w_next) {
     const auto& c = e.cfg;
-    RMI_TRY(rmi_rms_quant_apply(e.x, L.attn_norm, e.part, e.q8a, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(gemv(e, L.in_proj, e.q8a, e.proj, nc));
+    const uint8_t* xq = nullptr;
+    RMI_TRY(norm_input(e, e.x, e.part, L.attn_norm, 0, nc, &xq));
+    RMI_TRY(norm_gemv(e, L.in_proj, xq, e.part, e.proj, nc));
     const int qkvz = 2 * c.ssm_h_k * kS + 2 * c.ssm_h_v * kS;
     RMI_TRY(rmi_gdn_layer_tokens(L.state[0], L.state[1], L.hist[0], L.hist[1], e.ints + kSel, e.proj, e.qkvz_rows,
                                  e.proj + qkvz, e.qkvz_rows, L.conv_w, L.dt, L.ssm_a, L.ssm_norm, c.eps, e.y, e.gdn_v,
                                  e.q8y, static_cast<int>(q81_bytes(e.gdn_v)), c.ssm_h_k, c.ssm_h_v, nc, e.s));
-    RMI_TRY(gemv_res(e, L.out_proj, e.q8y, e.x, e.part, nc));
-    return ffn(e, L, e.x, e.part, nc);
+    RMI_TRY(res_gemv(e, L.out_proj, e.q8y, e.x, e.part, nc, L.post_norm));
+    return ffn(e, L, e.x, e.part, nc, w_next);
 }
 
 enum Head { kHeadAll, kHeadLast, kHeadNone };
@@ -495,17 +543,21 @@ enum Head { kHeadAll, kHeadLast, kHeadNone };
 int trunk_cols(Engine& e, int nc, const int* tok, const int* pos, float* h, float* hp, Head head) {
     const auto& c = e.cfg;
     const size_t np = c.n_embd / 4;
+    e.q8a_norm = nullptr;
     RMI_TRY(rmi_embed(e.emb_type, e.tok_embd, tok, e.x, e.part, c.n_embd, c.n_vocab, nc, e.s));
-    for (auto& L : e.layers) {
-        if (L.gdn) RMI_TRY(gdn_block(e, L, nc));
-        else RMI_TRY(attn_block(e, L, e.x, e.part, pos, nc));
+    const int nl = static_cast<int>(e.layers.size());
+    for (int il = 0; il < nl; ++il) {
+        Layer& L = e.layers[il];
+        const float* w_next = il + 1 < nl ? e.layers[il + 1].attn_norm : head != kHeadNone ? e.out_norm : nullptr;
+        if (L.gdn) RMI_TRY(gdn_block(e, L, nc, w_next));
+        else RMI_TRY(attn_block(e, L, e.x, e.part, pos, nc, w_next));
     }
     if (head != kHeadNone) {
         const int first = head == kHeadAll ? 0 : nc - 1;
         const int ncol = nc - first;
-        RMI_TRY(rmi_rms_quant_apply(e.x + static_cast<size_t>(first) * c.n_embd, e.out_norm, e.part + first * np,
-                                    e.q8a, c.n_embd, c.eps, ncol, e.s));
-        RMI_TRY(gemv(e, e.lm_head, e.q8a, e.logits, ncol));
+        const uint8_t* xq = nullptr;
+        RMI_TRY(norm_input(e, e.x, e.part, e.out_norm, first, ncol, &xq));
+        RMI_TRY(norm_gemv(e, e.lm_head, xq, e.part + first * np, e.logits, ncol));
         RMI_TRY(rmi_argmax(e.logits, c.n_vocab, ncol, c.n_vocab, e.ints + kV0, e.argmax_ws, e.s));
     }
     return rmi_rms_norm_out(e.x, e.out_norm, e.part, h, hp, c.n_embd, c.eps, nc, e.s);
@@ -521,15 +573,17 @@ int trunk(Engine& e, int nc) {
 // ints[kC0 + c] when with_head.
 int draft_cols(Engine& e, const int* tok, const int* pos, const float* h, const float* hp, int nc, bool with_head) {
     const auto& c = e.cfg;
+    e.q8a_norm = nullptr;
     RMI_TRY(rmi_embed(e.emb_type, e.tok_embd, tok, e.ex, e.epart, c.n_embd, c.n_vocab, nc, e.s));
     // [enorm(emb) | hnorm(h)] straight into the Q8_1 row of eh_proj's input: the bits of norm, norm, quantize
     RMI_TRY(rmi_rms_quant_apply_pair(e.ex, e.enorm, e.epart, h, e.hnorm, hp, e.q8f, c.n_embd, c.eps, nc, e.s));
     RMI_TRY(gemv(e, e.eh_proj, e.q8f, e.dx, nc));
     RMI_TRY(rmi_row_sum_partials(e.dx, e.dpart, c.n_embd, nc, e.s));
-    RMI_TRY(attn_block(e, e.draft, e.dx, e.dpart, pos, nc));
+    RMI_TRY(attn_block(e, e.draft, e.dx, e.dpart, pos, nc, with_head ? e.shnorm : nullptr));
     if (!with_head) return RMI_OK;
-    RMI_TRY(rmi_rms_quant_apply(e.dx, e.shnorm, e.dpart, e.q8a, c.n_embd, c.eps, nc, e.s));
-    RMI_TRY(gemv(e, e.lm_head, e.q8a, e.logits, nc));
+    const uint8_t* xq = nullptr;
+    RMI_TRY(norm_input(e, e.dx, e.dpart, e.shnorm, 0, nc, &xq));
+    RMI_TRY(norm_gemv(e, e.lm_head, xq, e.dpart, e.logits, nc));
     return rmi_argmax(e.logits, c.n_vocab, nc, c.n_vocab, e.ints + kC0, e.argmax_ws, e.s);
 }
 
@@ -1014,6 +1068,17 @@ int alloc_runtime(Engine& e) {
     HIP_TRY(hipEventCreate(&e.ev0));
     HIP_TRY(hipEventCreate(&e.ev1));
     HIP_TRY(hipStreamSynchronize(e.s));
+    // RMI_NORM_FOLD=1 folds the norms (every GEMV behind a norm a packed Q6_K matrix, n_embd <= 4096 for the
+    // 16-column ingest kernel).  Off by default: measured on the 9B round it is slower (the 32-row producer grid
+    // halves the CUs its residual GEMVs use, the scaled GEMVs lose a wave of occupancy) and it moves Q8_1's fp16 d
+    // rounding away from the reference's order.  Read per engine, so one process can hold both kinds.
+    const char* fold_var = std::getenv("RMI_NORM_FOLD");
+    const bool fold_env = fold_var && fold_var[0] == '1';
+    auto scaled_ok = [](const Mat& m) { return m.packed && m.parts.empty(); };
+    bool ok = fold_env && c.n_embd <= 4096 && scaled_ok(e.lm_head) && scaled_ok(e.draft.in_proj) &&
+              scaled_ok(e.draft.upgate);
+    for (const auto& L : e.layers) ok = ok && scaled_ok(L.in_proj) && scaled_ok(L.upgate);
+    e.fold = ok;
     return RMI_OK;
 }
 
@@ -1084,6 +1149,7 @@ extern "C" int rmi_engine_info(const rmi_engine* h, rmi_engine_info_t* info) {
     info->attn_layers = n_attn;
     info->max_ctx = e.max_ctx;
     info->attn_chunk = 64 * e.nsub;
+    info->norm_fold = e.fold ? 1 : 0;
     return RMI_OK;
 }
 

@@ -11,21 +11,12 @@
 namespace rmi {
 namespace {
 
-// A lane's first kPartialLoads partials are loaded before the first add (a strided loop waits on each load in turn),
-// unconditionally from clamped indices (a load under a branch gets a wait of its own); the adds keep their order.
-constexpr int kPartialLoads = 8;
-
+// sum of a vector's 4-row partials, by the tree of rmi_common.h (norm_load / norm_wave_sum / norm_inv)
 __device__ float block_sum_partials(const float* __restrict__ p, int np) {
     __shared__ float red[4];
-    float pv[kPartialLoads];
-#pragma unroll
-    for (int k = 0; k < kPartialLoads; ++k) pv[k] = p[min(static_cast<int>(threadIdx.x) + 256 * k, np - 1)];
-    float s = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kPartialLoads; ++k)
-        if (threadIdx.x + 256 * k < np) s += pv[k];
-    for (int i = threadIdx.x + 256 * kPartialLoads; i < np; i += 256) s += p[i];
-    s = group_sum<64>(s);
+    NormLoads pv;
+    norm_load(pv, p, np, static_cast<int>(threadIdx.x));
+    const float s = norm_wave_sum(pv, p, np, static_cast<int>(threadIdx.x));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
     const float tot = ((red[0] + red[1]) + red[2]) + red[3];
@@ -55,6 +46,17 @@ __global__ __launch_bounds__(256) void rms_quant_apply_kernel(const float* __res
     const int c = blockIdx.y;
     rms_quant_column(x + static_cast<size_t>(c) * cols, w, partials + static_cast<size_t>(c) * (cols / 4),
                      y + static_cast<size_t>(c) * (cols / 32) * kQ8_1Bytes, cols, eps);
+}
+
+// Q8_1 of x * w, no inv: a folded norm's GEMV input where no residual GEMV epilogue makes it (the same fp32 product and
+// quantizer as that epilogue, so the same bytes); the GEMV scales its rows by inv
+__global__ __launch_bounds__(256) void quant_weighted_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                             uint8_t* __restrict__ y, int cols) {
+    const int c = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= cols) return;   // cols % 32 == 0: whole 32-lane groups leave together
+    q8_1_store_lane(x[static_cast<size_t>(c) * cols + i] * w[i],
+                    y + (static_cast<size_t>(c) * (cols / 32) + i / 32) * kQ8_1Bytes);
 }
 
 // two normed vectors of a column into the two halves of one Q8_1 row of 2 cols (blockIdx.z = half)
@@ -323,6 +325,16 @@ extern "C" int rmi_rms_quant_apply(const float* x, const float* w, const float* 
     hipLaunchKernelGGL(rms_quant_apply_kernel, dim3((cols + 255) / 256, ncols), dim3(256), 0,
                        static_cast<hipStream_t>(stream), x, w, partials, static_cast<uint8_t*>(y_q8_1), cols, eps);
     return launch_status("rms_quant_apply");
+}
+
+extern "C" int rmi_quantize_q8_1_weighted(const float* x, const float* w, void* y_q8_1, int cols, int ncols,
+                                          void* stream) {
+    if (cols <= 0 || cols % 32 != 0 || bad_cols(ncols)) return fail(RMI_ERR_SHAPE, "quantize_q8_1_weighted: bad shape");
+    if (!aligned4(x) || !aligned4(w) || !aligned4(y_q8_1))
+        return fail(RMI_ERR_POINTER, "quantize_q8_1_weighted: null or misaligned pointer");
+    hipLaunchKernelGGL(quant_weighted_kernel, dim3((cols + 255) / 256, ncols), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, w, static_cast<uint8_t*>(y_q8_1), cols);
+    return launch_status("quantize_q8_1_weighted");
 }
 
 extern "C" int rmi_rms_quant_apply_pair(const float* x0, const float* w0, const float* partials0, const float* x1,

@@ -244,9 +244,10 @@ __device__ __forceinline__ void load_residual(float (&rv)[NCOLS], const float* r
     for (int col = 0; col < NCOLS; ++col) rv[col] = res[static_cast<size_t>(col) * n_out + row];
 }
 
-template <int NCOLS, bool RES>
+template <int NCOLS, bool RES, bool INV = false>
 __device__ __forceinline__ void quad_epilogue(float (&tot)[NCOLS], int lane, int q, float* y, const float* res,
-                                              float* partials, int n_out, const float* rv = nullptr) {
+                                              float* partials, int n_out, const float* rv = nullptr,
+                                              const float* inv = nullptr, float* vout = nullptr) {
     const int r = lane & 3, hb = lane >> 2;
     const int row = kQuad * q + r;
     const int np = (n_out + 3) / 4;
@@ -254,9 +255,11 @@ __device__ __forceinline__ void quad_epilogue(float (&tot)[NCOLS], int lane, int
     for (int col = 0; col < NCOLS; ++col) {
         float v = hb_sum(tot[col]);
         tot[col] = 0.0f;
+        if constexpr (INV) v *= inv[col];   // a folded norm: the row sum of Q8_1(x * w), times inv
         if constexpr (RES) {
             if (row < n_out) v += rv ? rv[col] : res[static_cast<size_t>(col) * n_out + row];
         }
+        if (vout) vout[col] = v;
         if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v;
         if constexpr (RES) {
             // partial of the quad: squares of its rows in row order (lanes 0, 1, 2, 3)
@@ -276,13 +279,69 @@ __device__ __forceinline__ void quad_epilogue(float (&tot)[NCOLS], int lane, int
     }
 }
 
+// ---- folded RMSNorm ---------------------------------------------------------------------------------------------------
+// The input of a normed GEMV is Q8_1((x * w) * inv) when rms_quant_apply makes it.  Folded, the GEMV before it (a
+// residual GEMV, whose workgroups own whole 32-row groups: FOLD) writes Q8_1(x * w) straight from its output rows, and
+// the normed GEMV (INV) scales every row sum by inv, which it derives from x's 4-row partials with the tree every norm
+// kernel uses (rmi_common.h): the same inv bits as rms_quant_apply, the quantization rounding moved (Q8_1 of x * w
+// instead of (x * w) * inv).  That removes the norm launch between them.
+struct Fold {
+    const float* part;    // INV: the input vector's 4-row partials, column col at + col * (n_in / 4)
+    float eps;
+    const float* w_next;  // FOLD: the next norm's weights over this GEMV's rows
+    uint8_t* q8_next;     // FOLD: Q8_1(y * w_next), column col at + col * (n_out / 32) blocks
+};
+
+// waves 0..3 (whole waves) reduce each column's partials to its four wave sums in red[col]; the caller's next barrier
+// publishes them, then inv[col] = norm_inv(red[col], n_in, eps)
+template <int NCOLS>
+__device__ __forceinline__ void inv_issue(NormLoads (&pv)[NCOLS], const Fold& f, int n_in, int t) {
+    const int np = n_in / 4;
+#pragma unroll
+    for (int col = 0; col < NCOLS; ++col) norm_load(pv[col], f.part + static_cast<size_t>(col) * np, np, t);
+}
+
+template <int NCOLS>
+__device__ __forceinline__ void inv_reduce(const NormLoads (&pv)[NCOLS], const Fold& f, int n_in, int t,
+                                           float (*red)[4]) {
+    const int np = n_in / 4;
+    if (t < 256) {
+#pragma unroll
+        for (int col = 0; col < NCOLS; ++col) {
+            const float s = norm_wave_sum(pv[col], f.part + static_cast<size_t>(col) * np, np, t);
+            if ((t & 63) == 0) red[col][t >> 6] = s;
+        }
+    }
+}
+
+// FOLD tail: the workgroup's 32 rows (rows[col][i] = y of row 32 blockIdx.x + i) into column col's Q8_1 block of
+// y * w_next, by wave 0 (lanes 32 col + i), with the quantizer of rms_quant_apply.  wn = w_next[32 blockIdx.x + t % 32],
+// loaded by the caller with its first loads.
+template <int NCOLS>
+__device__ __forceinline__ float fold_weight(const Fold& f, int t) {
+    return f.w_next[32 * static_cast<int>(blockIdx.x) + (t & 31)];
+}
+
+template <int NCOLS>
+__device__ __forceinline__ void fold_quantize(const float (*rows)[32], float wn, const Fold& f, int n_out, int t) {
+    static_assert(NCOLS <= 2, "one wave quantizes up to two columns");
+    if (t < 32 * NCOLS) {
+        const int col = t >> 5, i = t & 31;
+        q8_1_store_lane(rows[col][i] * wn,
+                        f.q8_next + (static_cast<size_t>(col) * (n_out / 32) + blockIdx.x) * kQ8_1Bytes);
+    }
+}
+
 // NW waves per workgroup share the staged activations: 4 for up to 4 columns (several workgroups per CU), 8 for the
 // 8 / 16-column ingest passes, whose stage fills most of the CU's LDS (one workgroup per CU)
-template <int NCOLS, bool RES, int D, int NW>
+template <int NCOLS, bool RES, int D, int NW, bool INV = false>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __restrict__ wp,
                                                            const uint8_t* __restrict__ x, float* y,
-                                                           const float* res, float* partials, int n_in, int n_out) {
+                                                           const float* res, float* partials, int n_in, int n_out,
+                                                           Fold fold) {
+    static_assert(!INV || NW >= 4, "the norm tree takes four waves");
     extern __shared__ uint4 smem[];
+    __shared__ float inv_red[INV ? NCOLS : 1][4];
     const int t = threadIdx.x, lane = t & 63;
     const int nch = n_in / kChunkElems;
     const int nbt = n_in / 32;                   // Q8_1 blocks per column
@@ -308,12 +367,20 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
         b.sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
         b.d = *reinterpret_cast<const uint32_t*>(base + 6656 + 4 * (2 * (lane >> 3) + ((lane & 3) >> 1)));
     };
+    NormLoads pv[INV ? NCOLS : 1];
+    if constexpr (INV) inv_issue<NCOLS>(pv, fold, n_in, t);
 #pragma unroll
     for (int s = 0; s < D; ++s)
         if (s < nsteps) issue(s, buf[s]);
 
     stage_activations(x, NCOLS * nbt, nbt, lq, lrec, t, 64 * NW);
+    if constexpr (INV) inv_reduce<NCOLS>(pv, fold, n_in, t, inv_red);
     __syncthreads();
+    float inv[NCOLS];
+    if constexpr (INV) {
+#pragma unroll
+        for (int col = 0; col < NCOLS; ++col) inv[col] = norm_inv(inv_red[col], n_in, fold.eps);
+    }
 
     float tot[NCOLS];
 #pragma unroll
@@ -329,7 +396,8 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
             if (f + D < nsteps) issue(f + D, buf[s]);
             accumulate_step<NCOLS>(cur, lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, tot);
 
-            if (c == nch - 1) quad_epilogue<NCOLS, RES>(tot, lane, gw + qi * GW, y, res, partials, n_out);
+            if (c == nch - 1)
+                quad_epilogue<NCOLS, RES, INV>(tot, lane, gw + qi * GW, y, res, partials, n_out, nullptr, inv);
         }
     }
 }
@@ -338,12 +406,17 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
 // chunks, every tile issued at the start, and hand their per-lane (d, acc) pairs through LDS to the quad's first
 // wave, which continues the fma chain over the chunks in order.  The operations and their order are those of one wave
 // walking every chunk, so the result is bitwise that of q6k_packed_gemv.  NW waves per workgroup = QW quads x S.
-template <int NCOLS, bool RES, int CS, int NW>
+// INV: the input is a folded norm's Q8_1(x * w) (row sums times inv).  FOLD (with RES, QW = 8: the workgroup owns 32
+// rows): also Q8_1(y * w_next) of its rows, the next GEMV's folded input.
+template <int NCOLS, bool RES, int CS, int NW, bool INV = false, bool FOLD = false>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* __restrict__ wp,
                                                                  const uint8_t* __restrict__ x, float* y,
                                                                  const float* res, float* partials, int n_in,
-                                                                 int n_out) {
+                                                                 int n_out, Fold fold) {
+    static_assert(!FOLD || RES, "the folded norm's producer is a residual GEMV");
     extern __shared__ uint4 smem[];
+    __shared__ float inv_red[INV ? NCOLS : 1][4];
+    __shared__ float frows[FOLD ? NCOLS : 1][32];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
     const int nbt = n_in / 32, xcs = nch * kNB;
@@ -369,6 +442,10 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
     }
     float rv[NCOLS];
     if constexpr (RES) load_residual<NCOLS>(rv, res, lane, min(q, nq - 1), n_out);
+    NormLoads pv[INV ? NCOLS : 1];
+    if constexpr (INV) inv_issue<NCOLS>(pv, fold, n_in, t);
+    float wn = 0.0f;
+    if constexpr (FOLD) wn = fold_weight<NCOLS>(fold, t);
     __builtin_amdgcn_sched_barrier(0);   // the stage's loads stay ahead of the weight tiles
     // unconditional loads (a wave past the last quad reads the last quad's tiles and discards them): with the loads in
     // a branch the compiler waits for the stage as if no tile had been issued after it.  Every tile is issued here,
@@ -403,7 +480,13 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
         for (int i = 0; i < 9; ++i) wv[i] = p[i];
         stage_one(wv, J, nbt, lq, lrec);
     }
+    if constexpr (INV) inv_reduce<NCOLS>(pv, fold, n_in, t, inv_red);
     __syncthreads();
+    float inv[NCOLS];
+    if constexpr (INV) {
+#pragma unroll
+        for (int col = 0; col < NCOLS; ++col) inv[col] = norm_inv(inv_red[col], n_in, fold.eps);
+    }
 
     float acc[CS][NCOLS], dd[CS];
     if (live) {
@@ -424,37 +507,55 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
         }
     }
     __syncthreads();
-    if (!live || sp != 0) return;
-
-    float tot[NCOLS];
+    if constexpr (!FOLD) {
+        if (!live || sp != 0) return;
+    }
+    if (live && sp == 0) {   // with FOLD every wave goes on to the barrier below
+        float tot[NCOLS];
 #pragma unroll
-    for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
+        for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
 #pragma unroll
-    for (int c = 0; c < CS; ++c)
+        for (int c = 0; c < CS; ++c)
 #pragma unroll
-        for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(dd[c], acc[c][col], tot[col]);
-    for (int s2 = 1; s2 < S; ++s2) {
+            for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(dd[c], acc[c][col], tot[col]);
+        for (int s2 = 1; s2 < S; ++s2) {
 #pragma unroll
-        for (int c = 0; c < CS; ++c) {
-            const float* o = lx + ((w + s2) * CS + c) * (NCOLS + 1) * 64 + lane;
-            const float d = o[0];
+            for (int c = 0; c < CS; ++c) {
+                const float* o = lx + ((w + s2) * CS + c) * (NCOLS + 1) * 64 + lane;
+                const float d = o[0];
 #pragma unroll
-            for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, o[(col + 1) * 64], tot[col]);
+                for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, o[(col + 1) * 64], tot[col]);
+            }
+        }
+        float v[NCOLS];
+        quad_epilogue<NCOLS, RES, INV>(tot, lane, q, y, res, partials, n_out, rv, inv, v);
+        if constexpr (FOLD) {
+            if (lane < kQuad) {
+#pragma unroll
+                for (int col = 0; col < NCOLS; ++col) frows[col][kQuad * qg + lane] = v[col];
+            }
         }
     }
-    quad_epilogue<NCOLS, RES>(tot, lane, q, y, res, partials, n_out, rv);
+    if constexpr (FOLD) {
+        __syncthreads();
+        fold_quantize<NCOLS>(frows, wn, fold, n_out, t);
+    }
 }
 
 // Stream variant: one wave per quad and QPW quads per wave (quads q, q + G, q + 2G, ... with G the grid's wave count),
 // all in straight-line code with PD tiles in flight ahead of the step that uses them.  Every wave is resident from the
 // start (a wave per quad would leave a tail of waves waiting for slots), and the per-quad arithmetic is that of
-// q6k_packed_gemv: the same bits.
-template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD>
+// q6k_packed_gemv: the same bits.  INV / FOLD: the folded norm, as in the split variant (FOLD: QPW = 1, NW = 8, so
+// the workgroup's waves hold its 32 rows).
+template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD, bool INV = false, bool FOLD = false>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t* __restrict__ wp,
                                                                   const uint8_t* __restrict__ x, float* y,
                                                                   const float* res, float* partials, int n_in,
-                                                                  int n_out) {
+                                                                  int n_out, Fold fold) {
+    static_assert(!FOLD || (RES && QPW == 1 && NW == 8), "FOLD: a residual GEMV whose 8 waves own 32 rows");
     extern __shared__ uint4 smem[];
+    __shared__ float inv_red[INV ? NCOLS : 1][4];
+    __shared__ float frows[FOLD ? NCOLS : 1][32];
     const int t = threadIdx.x, lane = t & 63;
     const int nbt = n_in / 32, xcs = NCH * kNB;
     uint4* lq = smem;
@@ -479,6 +580,10 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
 #pragma unroll
         for (int j = 0; j < QPW; ++j) load_residual<NCOLS>(rv[j], res, lane, min(q0 + j * G, nq - 1), n_out);
     }
+    NormLoads pv[INV ? NCOLS : 1];
+    if constexpr (INV) inv_issue<NCOLS>(pv, fold, n_in, t);
+    float wn = 0.0f;
+    if constexpr (FOLD) wn = fold_weight<NCOLS>(fold, t);
     __builtin_amdgcn_sched_barrier(0);
 
     // tile i = (quad j = i / NCH, chunk i % NCH); a quad past the last reads the last quad's tiles and discards them
@@ -514,7 +619,13 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
         for (int i = 0; i < 9; ++i) wv[i] = p[i];
         stage_one(wv, J, nbt, lq, lrec);
     }
+    if constexpr (INV) inv_reduce<NCOLS>(pv, fold, n_in, t, inv_red);
     __syncthreads();
+    float inv[NCOLS];
+    if constexpr (INV) {
+#pragma unroll
+        for (int col = 0; col < NCOLS; ++col) inv[col] = norm_inv(inv_red[col], n_in, fold.eps);
+    }
 
     float tot[NCOLS];
 #pragma unroll
@@ -532,8 +643,20 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
             issue(i + PD);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (c == NCH - 1 && q0 + j * G < nq)
-            quad_epilogue<NCOLS, RES>(tot, lane, q0 + j * G, y, res, partials, n_out, rv[j]);
+        if (c == NCH - 1 && q0 + j * G < nq) {
+            float v[NCOLS];
+            quad_epilogue<NCOLS, RES, INV>(tot, lane, q0 + j * G, y, res, partials, n_out, rv[j], inv, v);
+            if constexpr (FOLD) {
+                if (lane < kQuad) {
+#pragma unroll
+                    for (int col = 0; col < NCOLS; ++col) frows[col][kQuad * (t >> 6) + lane] = v[col];
+                }
+            }
+        }
+    }
+    if constexpr (FOLD) {
+        __syncthreads();
+        fold_quantize<NCOLS>(frows, wn, fold, n_out, t);
     }
 }
 
@@ -544,11 +667,13 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
 // and its Q8_1 block with the quantizer of swiglu_quant: bitwise the GEMV + swiglu_quant pair, one launch and no fp32
 // round trip.  Per launch at 24576 x 4096: 18.2 -> 16.5 us at two columns, 17.4 -> 15.5 us at one (8 waves of two
 // quads each: 17.4 us at two columns, one workgroup per CU at their register count).
-template <int NCOLS>
+// INV: the input is a folded norm's Q8_1(x * w); the gate and up row sums are scaled by inv before the SwiGLU.
+template <int NCOLS, bool INV = false>
 __global__ __launch_bounds__(256) void q6k_packed_swiglu(const uint8_t* __restrict__ wp, const uint8_t* __restrict__ x,
-                                                         uint8_t* __restrict__ out, int n_in, int ff) {
+                                                         uint8_t* __restrict__ out, int n_in, int ff, Fold fold) {
     constexpr int NW = 4, QPW = 4, NCH = 2, T = QPW * NCH, PD = 2;
     extern __shared__ uint4 smem[];
+    __shared__ float inv_red[INV ? NCOLS : 1][4];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int nbt = n_in / 32, xcs = NCH * kNB;
     uint4* lq = smem;
@@ -564,6 +689,8 @@ __global__ __launch_bounds__(256) void q6k_packed_swiglu(const uint8_t* __restri
 #pragma unroll
         for (int i = 0; i < 9; ++i) sv[i] = p[i];
     }
+    NormLoads pv[INV ? NCOLS : 1];
+    if constexpr (INV) inv_issue<NCOLS>(pv, fold, n_in, t);
     __builtin_amdgcn_sched_barrier(0);
     WTile buf[T];
     auto issue = [&](int i) {
@@ -584,7 +711,13 @@ __global__ __launch_bounds__(256) void q6k_packed_swiglu(const uint8_t* __restri
         __builtin_amdgcn_sched_barrier(0);
     }
     if (t < nblocks) stage_one(sv, t, nbt, lq, lrec);
+    if constexpr (INV) inv_reduce<NCOLS>(pv, fold, n_in, t, inv_red);
     __syncthreads();
+    float inv[NCOLS];
+    if constexpr (INV) {
+#pragma unroll
+        for (int col = 0; col < NCOLS; ++col) inv[col] = norm_inv(inv_red[col], n_in, fold.eps);
+    }
 
     float tot[NCOLS];
 #pragma unroll
@@ -605,7 +738,8 @@ __global__ __launch_bounds__(256) void q6k_packed_swiglu(const uint8_t* __restri
         if (c == NCH - 1) {
 #pragma unroll
             for (int col = 0; col < NCOLS; ++col) {
-                const float v = hb_sum(tot[col]);
+                float v = hb_sum(tot[col]);
+                if constexpr (INV) v *= inv[col];
                 tot[col] = 0.0f;
                 if (lane < kQuad) lrow[col * 64 + 4 * (QPW * w + j) + lane] = v;
             }
@@ -663,13 +797,21 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
                                                           0xf, false));
 }
 
-template <int NCG, bool RES, int D>
+// INV: the folded norm (n_in <= 4096: at most four partial slots per lane and column).  The 8 waves split the columns:
+// waves 0..3 reduce the even ones and waves 4..7 the odd ones, each group as the 256 lanes of the norm tree.
+constexpr int kMfmaNormLoads = 4;
+
+template <int NCG, bool RES, int D, bool INV = false>
 __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t* __restrict__ wp,
                                                                    const uint8_t* __restrict__ x, float* y,
                                                                    const float* res, float* partials, int n_in,
-                                                                   int n_out) {
+                                                                   int n_out, Fold fold) {
     typedef int i32x4 __attribute__((ext_vector_type(4)));
+    static_assert(kWideWaves == 8, "two 256-lane norm trees");
     extern __shared__ uint4 smem[];
+    // INV: the columns' four wave sums after the stage (the stage may take all 160 KB of the CU's LDS otherwise, so
+    // the kernel has no static LDS)
+    float(*inv_red)[4] = reinterpret_cast<float(*)[4]>(smem + static_cast<size_t>(NCG) * (n_in / 32) * kMStride);
     const int t = threadIdx.x, lane = t & 63;
     const int nch = n_in / kChunkElems;
     const int nbt = n_in / 32;
@@ -692,14 +834,40 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
         b.sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
         b.d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (4 * (lane >> 3) + (lane & 3)));
     };
+    constexpr int NH = INV ? 2 * NCG : 1;   // columns per lane group
+    float pvm[NH][kMfmaNormLoads];
+    const int np = n_in / 4, nu = t & 255, par = t >> 8;
+    if constexpr (INV) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int k = 0; k < kMfmaNormLoads; ++k)
+                pvm[h][k] = fold.part[static_cast<size_t>(2 * h + par) * np + min(nu + 256 * k, np - 1)];
+    }
 #pragma unroll
     for (int s = 0; s < D; ++s)
         if (s < nsteps) issue(s, buf[s]);
 
     stage_activations_mfma(x, 4 * NCG, nbt, smem, t, 64 * kWideWaves);
+    if constexpr (INV) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kMfmaNormLoads; ++k)
+                if (nu + 256 * k < np) sum += pvm[h][k];
+            sum = group_sum<64>(sum);
+            if ((t & 63) == 0) inv_red[2 * h + par][(t >> 6) & 3] = sum;
+        }
+    }
     __syncthreads();
 
     const int jj = lane & 3, hb = lane >> 2, b = hb >> 1, n = hb & 1;
+    float invc[NCG];   // inv of the lane's column 4 g + jj
+    if constexpr (INV) {
+#pragma unroll
+        for (int g = 0; g < NCG; ++g) invc[g] = norm_inv(inv_red[4 * g + jj], n_in, fold.eps);
+    }
     // stage offsets (uint4 units, 32-bit): column group g at goff[g], the lane's column and half-block at lbase
     int goff[NCG];
 #pragma unroll
@@ -802,6 +970,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         v[i] = hb_sum(tot[i][g]);
+                        if constexpr (INV) v[i] *= invc[g];
                         tot[i][g] = 0.0f;
                         const int row = kQuad * q + i;
                         if constexpr (RES) {
@@ -888,50 +1057,54 @@ size_t split_lds(int n_in, int ncols, int cs, int nw) {
     return static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(nw) * cs * (ncols + 1) * 64 * 4;
 }
 
-template <int NCOLS, bool RES, int CS, int NW>
+template <int NCOLS, bool RES, int CS, int NW, bool INV = false, bool FOLD = false>
 void launch_split(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                  int n_out, hipStream_t s) {
+                  int n_out, const Fold& f, hipStream_t s) {
     const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
     const int nq = (n_out + kQuad - 1) / kQuad;
     const dim3 grid((nq + QW - 1) / QW), block(64 * NW);
-    hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW>), grid, block, split_lds(n_in, NCOLS, CS, NW), s,
-                       wp, x, y, res, partials, n_in, n_out);
+    hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW, INV, FOLD>), grid, block,
+                       split_lds(n_in, NCOLS, CS, NW), s, wp, x, y, res, partials, n_in, n_out, f);
 }
 
-template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD>
+template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD, bool INV = false, bool FOLD = false>
 void launch_stream(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                   int n_out, hipStream_t s) {
+                   int n_out, const Fold& f, hipStream_t s) {
     const int nq = (n_out + kQuad - 1) / kQuad;
     const dim3 grid((nq + NW * QPW - 1) / (NW * QPW)), block(64 * NW);
-    hipLaunchKernelGGL((q6k_packed_gemv_stream<NCOLS, RES, NCH, QPW, NW, PD>), grid, block,
-                       static_cast<size_t>(NCOLS) * (n_in / 32) * 48, s, wp, x, y, res, partials, n_in, n_out);
+    hipLaunchKernelGGL((q6k_packed_gemv_stream<NCOLS, RES, NCH, QPW, NW, PD, INV, FOLD>), grid, block,
+                       static_cast<size_t>(NCOLS) * (n_in / 32) * 48, s, wp, x, y, res, partials, n_in, n_out, f);
 }
 
-template <int NCOLS, bool RES>
+template <int NCOLS, bool RES, bool INV = false>
 void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                   int n_out, hipStream_t s) {
+                   int n_out, const Fold& f, hipStream_t s) {
     static const int depth = env_int("RMI_PACKED_DEPTH", 2);
     if constexpr (NCOLS <= 2) {
         const PackedCfg c = packed_cfg(n_in, n_out, NCOLS);
         if (c.kind == PackedCfg::kStream) {
-            if (n_in / kChunkElems == 2) return launch_stream<NCOLS, RES, 2, 2, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
-            return launch_stream<NCOLS, RES, 6, 1, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
+            if (n_in / kChunkElems == 2)
+                return launch_stream<NCOLS, RES, 2, 2, 4, 2, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
+            return launch_stream<NCOLS, RES, 6, 1, 4, 2, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
         }
         if (c.kind == PackedCfg::kSplit) {
-            if (c.cs == 2) return launch_split<NCOLS, RES, 2, 4>(wp, x, y, res, partials, n_in, n_out, s);
-            if (c.nw == 8) return launch_split<NCOLS, RES, 1, 8>(wp, x, y, res, partials, n_in, n_out, s);
-            return launch_split<NCOLS, RES, 1, 4>(wp, x, y, res, partials, n_in, n_out, s);
+            if (c.cs == 2) return launch_split<NCOLS, RES, 2, 4, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
+            if (c.nw == 8) return launch_split<NCOLS, RES, 1, 8, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
+            return launch_split<NCOLS, RES, 1, 4, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
         }
     }
     const int nq = (n_out + kQuad - 1) / kQuad;
     const size_t lds = static_cast<size_t>(NCOLS) * (n_in / 32) * 48;
     const dim3 grid(packed_grid(nq)), block(kThreads);
     if (depth >= 4)
-        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 4, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 4, 4, INV>), grid, block, lds, s, wp, x, y, res, partials, n_in,
+                           n_out, f);
     else if (depth == 3)
-        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 3, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 3, 4, INV>), grid, block, lds, s, wp, x, y, res, partials, n_in,
+                           n_out, f);
     else
-        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 2, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 2, 4, INV>), grid, block, lds, s, wp, x, y, res, partials, n_in,
+                           n_out, f);
 }
 
 // LDS of the ingest stage: kMStride uint4 per (4-column group, block)
@@ -948,22 +1121,23 @@ int wide_cols(int n_in, int remaining) {
 
 // 8 / 16 columns in one weight pass on the MFMA ingest kernel: one 8-wave workgroup per CU (the stage takes up to
 // 160 KB of LDS), the quads split evenly over the waves
-template <int NCOLS, bool RES>
+template <int NCOLS, bool RES, bool INV = false>
 int launch_packed_wide(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                       int n_out, hipStream_t s) {
+                       int n_out, const Fold& f, hipStream_t s) {
     constexpr int D = 3;
-    auto kern = q6k_packed_mfma<NCOLS / 4, RES, D>;
+    auto kern = q6k_packed_mfma<NCOLS / 4, RES, D, INV>;
     static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  kWideStageBytes) == hipSuccess;
     if (!attr) return fail(RMI_ERR_LAUNCH, "native_q6_k_mmvq_packed: wide LDS stage not available");
     const int nq = (n_out + kQuad - 1) / kQuad;
-    const size_t lds = wide_stage_bytes(n_in, NCOLS);
+    const size_t lds = wide_stage_bytes(n_in, NCOLS) + (INV ? NCOLS * 4 * sizeof(float) : 0);
+    if (lds > kWideStageBytes) return fail(RMI_ERR_SHAPE, "native_q6_k_mmvq_packed: wide stage exceeds the LDS");
     const int max_waves = cu_count() * kWideWaves;
     const int qpw = (nq + max_waves - 1) / max_waves;
     const int waves = (nq + qpw - 1) / qpw;
     const dim3 grid((waves + kWideWaves - 1) / kWideWaves), block(64 * kWideWaves);
-    hipLaunchKernelGGL(kern, grid, block, lds, s, wp, x, y, res, partials, n_in, n_out);
+    hipLaunchKernelGGL(kern, grid, block, lds, s, wp, x, y, res, partials, n_in, n_out, f);
     return RMI_OK;
 }
 
@@ -974,10 +1148,11 @@ int cols_per_pass(int n_in) {
 }
 
 // Columns are cut into passes (16 or 8 wide, then up to 4); each pass reads the weights once.  The pass width never
-// changes a column's result: lane ownership and reduction order depend on the shape only.
-template <bool RES>
+// changes a column's result: lane ownership and reduction order depend on the shape only.  INV: the input columns are
+// a folded norm's Q8_1(x * w); f.part holds x's partials, column j at + j * n_in / 4.
+template <bool RES, bool INV = false>
 int run_packed(const void* wpv, const void* xv, float* y, const float* res, float* partials, int n_in, int n_out,
-               int ncols, hipStream_t s) {
+               int ncols, const Fold& fold, hipStream_t s) {
     const auto* wp = static_cast<const uint8_t*>(wpv);
     const auto* x = static_cast<const uint8_t*>(xv);
     const int per = cols_per_pass(n_in);
@@ -990,16 +1165,18 @@ int run_packed(const void* wpv, const void* xv, float* y, const float* res, floa
         float* yj = y + static_cast<size_t>(j) * n_out;
         const float* rj = RES ? res + static_cast<size_t>(j) * n_out : nullptr;
         float* pj = RES ? partials + j * pcol : nullptr;
+        Fold fj = fold;
+        if (INV) fj.part = fold.part + static_cast<size_t>(j) * (n_in / 4);
         switch (nj) {
-            case 1: launch_packed<1, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
-            case 2: launch_packed<2, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
-            case 3: launch_packed<3, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
-            case 4: launch_packed<4, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
+            case 1: launch_packed<1, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s); break;
+            case 2: launch_packed<2, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s); break;
+            case 3: launch_packed<3, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s); break;
+            case 4: launch_packed<4, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s); break;
             case 8:
-                if (const int rc = launch_packed_wide<8, RES>(wp, xj, yj, rj, pj, n_in, n_out, s)) return rc;
+                if (const int rc = launch_packed_wide<8, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s)) return rc;
                 break;
             default:
-                if (const int rc = launch_packed_wide<16, RES>(wp, xj, yj, rj, pj, n_in, n_out, s)) return rc;
+                if (const int rc = launch_packed_wide<16, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s)) return rc;
                 break;
         }
         if (const int rc = launch_status("native_q6_k_mmvq_packed")) return rc;
@@ -1059,11 +1236,13 @@ extern "C" int rmi_q6_k_pack_swiglu(const void* w, void* w_packed, int n_in, int
     return pack(w, w_packed, n_in, 2 * n_ff, n_ff, stream);
 }
 
-extern "C" int rmi_native_q6_k_swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_in, int n_ff,
-                                             int ncols, void* stream) {
+namespace rmi {
+namespace {
+int swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_in, int n_ff, int ncols,
+                  const Fold* fold, void* stream) {
     if (n_in != 2 * kChunkElems || n_ff <= 0 || n_ff % 32 != 0 || ncols < 1 || ncols > 2)
         return fail(RMI_ERR_SHAPE, "q6_k_swiglu_packed: n_in must be 4096, n_ff a positive multiple of 32, ncols 1 or 2");
-    if (!aligned16(w_packed) || !aligned4(x_q8_1) || !aligned4(y_q8_1))
+    if (!aligned16(w_packed) || !aligned4(x_q8_1) || !aligned4(y_q8_1) || (fold && !aligned4(fold->part)))
         return fail(RMI_ERR_POINTER, "q6_k_swiglu_packed: null or misaligned pointer");
     if (!stream) return fail(RMI_ERR_STREAM, "native MMVQ requires an explicit non-null CUDA stream");
     const auto* wp = static_cast<const uint8_t*>(w_packed);
@@ -1072,18 +1251,64 @@ extern "C" int rmi_native_q6_k_swiglu_packed(const void* w_packed, const void* x
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const size_t lds = static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(ncols) * 64 * 4;
     const dim3 grid(n_ff / 32), block(256);
-    if (ncols == 1)
-        hipLaunchKernelGGL((q6k_packed_swiglu<1>), grid, block, lds, s, wp, x, y, n_in, n_ff);
-    else
-        hipLaunchKernelGGL((q6k_packed_swiglu<2>), grid, block, lds, s, wp, x, y, n_in, n_ff);
+    const Fold f = fold ? *fold : Fold{};
+    if (ncols == 1) {
+        if (fold) hipLaunchKernelGGL((q6k_packed_swiglu<1, true>), grid, block, lds, s, wp, x, y, n_in, n_ff, f);
+        else hipLaunchKernelGGL((q6k_packed_swiglu<1>), grid, block, lds, s, wp, x, y, n_in, n_ff, f);
+    } else {
+        if (fold) hipLaunchKernelGGL((q6k_packed_swiglu<2, true>), grid, block, lds, s, wp, x, y, n_in, n_ff, f);
+        else hipLaunchKernelGGL((q6k_packed_swiglu<2>), grid, block, lds, s, wp, x, y, n_in, n_ff, f);
+    }
     return launch_status("q6_k_swiglu_packed");
+}
+
+// the residual GEMVs that carry the next norm's Q8_1 in their epilogue: rows of 4096 (split, 8 quads per workgroup)
+// and of 12288 (stream, 8 waves of one quad), 1 or 2 columns, n_out a multiple of 32
+bool fold_shape(int n_in, int n_out, int ncols) {
+    return (n_in == 2 * kChunkElems || n_in == 6 * kChunkElems) && n_out > 0 && n_out % 32 == 0 && ncols >= 1 &&
+           ncols <= 2;
+}
+
+template <int NCOLS>
+void launch_res_fold(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
+                     int n_out, const Fold& f, hipStream_t s) {
+    static const int split_waves = env_int("RMI_FOLD_SPLIT_WAVES", 16);
+    if (n_in == 6 * kChunkElems)
+        return launch_stream<NCOLS, true, 6, 1, 8, 2, false, true>(wp, x, y, res, partials, n_in, n_out, f, s);
+    if (split_waves == 8)   // a quad's two chunks on one wave
+        return launch_split<NCOLS, true, 2, 8, false, true>(wp, x, y, res, partials, n_in, n_out, f, s);
+    return launch_split<NCOLS, true, 1, 16, false, true>(wp, x, y, res, partials, n_in, n_out, f, s);
+}
+}  // namespace
+}  // namespace rmi
+
+extern "C" int rmi_native_q6_k_swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_in, int n_ff,
+                                             int ncols, void* stream) {
+    return swiglu_packed(w_packed, x_q8_1, y_q8_1, n_in, n_ff, ncols, nullptr, stream);
+}
+
+extern "C" int rmi_native_q6_k_swiglu_packed_scaled(const void* w_packed, const void* x_q8_1, const float* partials,
+                                                    float eps, void* y_q8_1, int n_in, int n_ff, int ncols,
+                                                    void* stream) {
+    const Fold f{partials, eps, nullptr, nullptr};
+    return swiglu_packed(w_packed, x_q8_1, y_q8_1, n_in, n_ff, ncols, &f, stream);
 }
 
 extern "C" int rmi_native_q6_k_mmvq_packed(const void* w_packed, const void* x_q8_1, float* y, int n_in, int n_out,
                                            int ncols, void* stream) {
     if (int rc = validate_packed(w_packed, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
-    return run_packed<false>(w_packed, x_q8_1, y, nullptr, nullptr, n_in, n_out, ncols,
+    return run_packed<false>(w_packed, x_q8_1, y, nullptr, nullptr, n_in, n_out, ncols, Fold{},
                              static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rmi_native_q6_k_mmvq_packed_scaled(const void* w_packed, const void* x_q8_1, const float* partials,
+                                                  float eps, float* y, int n_in, int n_out, int ncols, void* stream) {
+    if (int rc = validate_packed(w_packed, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
+    if (!aligned4(partials)) return fail(RMI_ERR_POINTER, "packed scaled GEMV: null or misaligned partials");
+    if (n_in > 4 * 1024 && ncols >= 8)
+        return fail(RMI_ERR_SHAPE, "packed scaled GEMV: 8 or more columns need n_in <= 4096");
+    return run_packed<false, true>(w_packed, x_q8_1, y, nullptr, nullptr, n_in, n_out, ncols,
+                                   Fold{partials, eps, nullptr, nullptr}, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int rmi_native_q6_k_mmvq_packed_res_n(const void* w_packed, const void* x_q8_1, float* y, const float* res,
@@ -1091,6 +1316,28 @@ extern "C" int rmi_native_q6_k_mmvq_packed_res_n(const void* w_packed, const voi
     if (int rc = validate_packed(w_packed, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
     if (!aligned4(res) || !aligned4(partials))
         return fail(RMI_ERR_POINTER, "native MMVQ requires non-null 4-byte aligned device pointers");
-    return run_packed<true>(w_packed, x_q8_1, y, res, partials, n_in, n_out, ncols, static_cast<hipStream_t>(stream));
+    return run_packed<true>(w_packed, x_q8_1, y, res, partials, n_in, n_out, ncols, Fold{},
+                            static_cast<hipStream_t>(stream));
 }
 
+extern "C" int rmi_q6_k_packed_fold_supported(int n_in, int n_out, int ncols) {
+    return fold_shape(n_in, n_out, ncols) ? 1 : 0;
+}
+
+extern "C" int rmi_native_q6_k_mmvq_packed_res_fold(const void* w_packed, const void* x_q8_1, float* y,
+                                                    const float* res, float* partials, const float* w_next,
+                                                    void* y_q8_1_next, int n_in, int n_out, int ncols, void* stream) {
+    if (int rc = validate_packed(w_packed, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
+    if (!fold_shape(n_in, n_out, ncols))
+        return fail(RMI_ERR_UNSUPPORTED, "packed residual GEMV with the next norm: n_in 4096 or 12288, n_out a "
+                                         "multiple of 32, 1 or 2 columns");
+    if (!aligned4(res) || !aligned4(partials) || !aligned4(w_next) || !aligned4(y_q8_1_next))
+        return fail(RMI_ERR_POINTER, "native MMVQ requires non-null 4-byte aligned device pointers");
+    const Fold f{nullptr, 0.0f, w_next, static_cast<uint8_t*>(y_q8_1_next)};
+    const auto* wp = static_cast<const uint8_t*>(w_packed);
+    const auto* x = static_cast<const uint8_t*>(x_q8_1);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (ncols == 1) launch_res_fold<1>(wp, x, y, res, partials, n_in, n_out, f, s);
+    else launch_res_fold<2>(wp, x, y, res, partials, n_in, n_out, f, s);
+    return launch_status("native_q6_k_mmvq_packed_res_fold");
+}

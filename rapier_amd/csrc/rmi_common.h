@@ -118,6 +118,38 @@ __device__ __forceinline__ void q8_1_store_lane(float v, uint8_t* block) {
     }
 }
 
+// ---- the row-norm reduction over 4-row partials ------------------------------------------------------------------
+// One tree for every kernel that derives a norm's inv = rsqrt(sum / cols + eps) from a vector's 4-row partials
+// (rms_quant_apply, rms_norm_out, and the GEMVs that take a folded norm), so they all get the same bits: 256 lanes
+// (waves 0..3); lane t adds slots t, t + 256, t + 512, ... in order starting from 0, a 64-lane xor butterfly, then the
+// four wave sums in wave order.  A lane's first kNormLoads slots are loaded before the first add (clamped,
+// unconditional: a strided loop or a load under a branch waits on each load in turn).
+constexpr int kNormLoads = 8;
+
+struct NormLoads {
+    float v[kNormLoads];
+};
+
+__device__ __forceinline__ void norm_load(NormLoads& pv, const float* __restrict__ p, int np, int t) {
+#pragma unroll
+    for (int k = 0; k < kNormLoads; ++k) pv.v[k] = p[min(t + 256 * k, np - 1)];
+}
+
+// the lane's ordered sum and the wave's butterfly; every lane of the wave ends with the wave sum
+__device__ __forceinline__ float norm_wave_sum(const NormLoads& pv, const float* __restrict__ p, int np, int t) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormLoads; ++k)
+        if (t + 256 * k < np) s += pv.v[k];
+    for (int i = t + 256 * kNormLoads; i < np; i += 256) s += p[i];
+    return group_sum<64>(s);
+}
+
+__device__ __forceinline__ float norm_inv(const float* red, int cols, float eps) {
+    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+    return rsqrtf(tot / static_cast<float>(cols) + eps);
+}
+
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }

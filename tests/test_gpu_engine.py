@@ -78,6 +78,7 @@ def test_qwen35_9b_mtp_stream_bit_identical_at_4k(eng_mod):
     eng = E.Engine(E.qwen35_9b_config(), seed=2024, max_ctx=4096 + 256)
     info = eng.info()
     assert info["gdn_layers"] == 24 and info["attn_layers"] == 8
+    assert info["norm_fold"] == 0   # the reference's norm order (RMI_NORM_FOLD=1 folds them)
     # one weight pass per round: trunk 5,675,335,680 + lm_head 834,355,200 + draft block 199,557,120 + lm_head
     assert info["trunk_weight_bytes"] == 5_675_335_680 and info["lm_head_bytes"] == 834_355_200
     assert info["round_weight_bytes"] == 7_543_603_200
@@ -131,3 +132,35 @@ def test_qwen35_9b_mtp_after_ingest_past_32k(eng_mod, engine_64k):
     assert pos0 == len(prompt) and cur0 == first
     ref, _ = streams_agree(E, eng, pos0, cur0, 48, natural=True)
     assert len(set(ref)) > 3, "degenerate stream"
+
+
+def test_small_model_folded_norms_follow_the_unfolded_engine(eng_mod, monkeypatch):
+    """the folded norms (RMI_NORM_FOLD=1: Q8_1(x * w) into a GEMV that scales by inv) against the same seeded model
+    with the default rms_quant_apply (the reference's rounding order).  The two round a few activations to
+    neighbouring Q8_1 codes, and the GDN state carries each such flip to later tokens, so the bar is the multi-layer one
+    of tests/test_gpu_gguf.py: after a 7-token prompt through 4 layers, logits and hidden within 5e-2 of max|.| and
+    correlated > 0.999.  The folded engine's MTP stream equals its own greedy stream."""
+    E = eng_mod
+    monkeypatch.delenv("RMI_NORM_FOLD", raising=False)
+    ref = E.Engine(E.small_config(), seed=21, max_ctx=256)
+    monkeypatch.setenv("RMI_NORM_FOLD", "1")
+    fold = E.Engine(E.small_config(), seed=21, max_ctx=256)
+    monkeypatch.delenv("RMI_NORM_FOLD")
+    assert ref.info()["norm_fold"] == 0 and fold.info()["norm_fold"] == 1
+    prompt = [int(t) for t in np.random.default_rng(8).integers(0, 5000, size=7)]
+    f_ref, f_fold = ref.prefill(prompt, batch=1), fold.prefill(prompt, batch=16)
+    n_v, n_e = 5000, 2048
+    lr = ref.read(E.BUF_LOGITS, 0, 4 * n_v).view(np.float32).astype(np.float64)
+    lf = fold.read(E.BUF_LOGITS, 0, 4 * n_v).view(np.float32).astype(np.float64)
+    assert np.abs(lf - lr).max() <= 5e-2 * np.abs(lr).max()
+    assert np.corrcoef(lf, lr)[0, 1] > 0.999
+    hr = ref.read(E.BUF_HIDDEN, 0, 4 * n_e).view(np.float32).astype(np.float64)
+    hf = fold.read(E.BUF_HIDDEN, 0, 4 * n_e).view(np.float32).astype(np.float64)
+    assert np.abs(hf - hr).max() <= 5e-2 * np.abs(hr).max()
+    top = np.sort(lr)[-2:]
+    if top[1] - top[0] > 1e-1 * np.abs(lr).max():
+        assert f_fold == f_ref
+    pos0, cur0 = fold.state()
+    streams_agree(E, fold, pos0, cur0, 24)
+    ref.close()
+    fold.close()

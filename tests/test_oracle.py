@@ -507,3 +507,60 @@ def test_k_quant_gemv_matches_dequant_matmul(orc, five_bit):
     bound = 2.0 ** -24 * (np.abs(xd) @ np.abs(wd).T) * 1.01
     assert np.all(np.abs(y.reshape(ncols, n_out) - xd @ wd.T) <= bound)
     assert np.abs(y).max() > 1e3 * bound.max(), "a nontrivial product"
+
+
+# ---- the CPU baseline's SIMD timing build (oracle/cpu_round.c) against the oracle --------------------------------
+
+@pytest.mark.parametrize("simd", [1, 2])
+def test_timing_gemv_close_to_fp64(orc, simd):
+    """AVX2 (simd 1) and, where the CPU has it, AVX-512 VNNI (simd 2) Q6_K x Q8_1 GEMV: 1 and 2 columns, residual and
+    partials, within 1e-4 of the fp64 oracle (fp32 lane sums in another order)"""
+    n_in, n_out = 4096, 96
+    w = orc.gen_q6k(n_out, n_in, seed=171)
+    xq = orc.quantize_q8_1(orc.normal(2 * n_in, seed=172), n_in, 2)
+    res = orc.normal(2 * n_out, seed=173)
+    y64, p64 = orc.q6k_gemv(w, xq, n_in, n_out, ncols=2, res=res, partials=True)
+    y32, p32 = orc.cpr_q6k_gemv(w, xq, n_in, n_out, ncols=2, res=res, partials=True, threads=3, simd=simd)
+    np.testing.assert_allclose(y32, y64, rtol=1e-4, atol=1e-4 * np.abs(y64).max())
+    np.testing.assert_allclose(p32, p64, rtol=1e-4, atol=1e-4 * np.abs(p64).max())
+    y1 = orc.cpr_q6k_gemv(w, xq[:n_in // 32 * 36], n_in, n_out, ncols=1, threads=1, simd=simd)
+    np.testing.assert_allclose(y1, orc.q6k_gemv(w, xq, n_in, n_out, ncols=1), rtol=1e-4,
+                               atol=1e-4 * np.abs(y64).max())
+
+
+def test_timing_gdn_layer_close_to_oracle(orc):
+    h_k, h_v, S, ntok = 2, 4, 128, 2
+    ch = (2 * h_k + h_v) * S
+    stride = ch + h_v * S
+    qkvz = orc.normal(ntok * stride, seed=181)
+    ab = orc.normal(ntok * 2 * h_v, seed=182)
+    conv_w = orc.normal(4 * ch, seed=183, std=0.5)
+    hist = orc.normal(3 * ch, seed=184, std=0.5)
+    state = orc.normal(S * h_v * S, seed=185, std=0.05)
+    dt = np.zeros(h_v, np.float32)
+    ssm_a = (-np.exp(orc.normal(h_v, seed=186, std=0.5))).astype(np.float32)
+    gamma = (1 + orc.normal(S, seed=187, std=0.1)).astype(np.float32)
+    y, hist2, st2 = orc.cpr_gdn_layer(qkvz, stride, ab, conv_w, dt, ssm_a, gamma, 1e-6, hist, state, h_k, h_v, ntok,
+                                      threads=2)
+    st, hs = state.astype(np.float64), hist.copy()
+    for t in range(ntok):
+        x = qkvz[t * stride:(t + 1) * stride]
+        h, hs = orc.gdn_conv_l2(hs, x[:ch], conv_w, 2 * h_k, 1e-6)
+        b, g = orc.beta_gate(ab[t * 2 * h_v:t * 2 * h_v + h_v], ab[t * 2 * h_v + h_v:(t + 1) * 2 * h_v], dt, ssm_a)
+        yr, st = orc.gdn_step_norm(st, h[:h_k * S], h[h_k * S:2 * h_k * S], h[2 * h_k * S:], g, b, x[ch:], gamma,
+                                   1e-6, h_k, h_v)
+        np.testing.assert_allclose(y[t * h_v * S:(t + 1) * h_v * S], yr, rtol=1e-4, atol=1e-5 * np.abs(yr).max())
+    assert np.array_equal(hist2, hs)
+    assert np.abs(st2 - st).max() < 1e-5
+
+
+def test_timing_gqa_decode_close_to_oracle(orc):
+    nh, nkv, hd, ctx, ntok = 16, 4, 256, 700, 2
+    k = orc.normal(ctx * nkv * hd, seed=191).astype(np.float16).view(np.uint16)
+    v = orc.normal(ctx * nkv * hd, seed=192).astype(np.float16).view(np.uint16)
+    q = orc.normal(ntok * nh * hd, seed=193)
+    p0 = ctx - ntok - 5
+    o = orc.cpr_gqa_decode(q, k, v, nh, nkv, hd, p0, ntok, 1 / 16, threads=4)
+    for t in range(ntok):
+        ref = orc.gqa_decode(q[t * nh * hd:(t + 1) * nh * hd], k, v, nh, nkv, hd, p0 + t + 1, 1 / 16)
+        np.testing.assert_allclose(o[t * nh * hd:(t + 1) * nh * hd], ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
