@@ -360,6 +360,205 @@ def run_traffic_probe():
 
 COPY_KIB_ELEMS = int(COPY_KIB * 1024 // 4)
 
+# the round's Q6_K GEMVs at two columns, as the engine launches them on its packed copies: (name, n_in, n_out, kind,
+# launches per round); kind "res" = residual + partials epilogue, "swiglu" = up||gate + SwiGLU + Q8_1 (n_out = 2 ff)
+ROUND_KERNEL_GEMVS = [
+    ("gdn in_proj qkv|z|beta|alpha", 4096, 12352, "plain", 24),
+    ("attn qkv", 4096, 10240, "plain", 9),
+    ("out_proj (ssm_out / wo)", 4096, 4096, "res", 33),
+    ("up||gate + SwiGLU", 4096, 24576, "swiglu", 33),
+    ("ffn down", 12288, 4096, "res", 33),
+    ("draft eh_proj", 8192, 4096, "plain", 1),
+    ("lm_head", 4096, 248320, "plain", 2),
+]
+
+
+def gemv_algorithmic_bytes(n_in, n_out, kind, ncols=2):
+    """weights once + Q8_1 inputs + outputs (fp32 rows, or the Q8_1 of the ff SwiGLU products) + the residual read
+    and 4-row partials of a residual GEMV"""
+    b = q6_bytes(n_out, n_in) + ncols * (n_in // 32) * 36
+    if kind == "swiglu":
+        return b + ncols * (n_out // 2 // 32) * 36
+    b += ncols * n_out * 4
+    if kind == "res":
+        b += ncols * n_out * 4 + ncols * (n_out // 4) * 4
+    return b
+
+
+def time_blocks(stream, launch, nrot, blocks=5, per_block=None):
+    """mean launch time (us) from HIP events around blocks of back-to-back launches over nrot rotating buffer sets"""
+    import torch
+    per_block = per_block or max(2 * nrot, 20)
+    for r in range(nrot):
+        launch(r)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(blocks)]
+    torch.cuda.synchronize()
+    for b in range(blocks):
+        evs[b][0].record(stream)
+        for i in range(per_block):
+            launch(i % nrot)
+        evs[b][1].record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) * 1e3 / per_block for a, b in evs) / blocks, blocks * per_block
+
+
+def time_gdn_layer(stream):
+    """the verify round's GDN layer launch (rmi_gdn_layer_tokens, 2 tokens: conv + SiLU + L2, delta-rule step, RMSNorm
+    * SiLU gate, Q8_1; after-token-0 state to the rollback buffer) at the 9B shapes, rotating over 80 layers' state
+    (320 MB, above the Infinity Cache).  Algorithmic bytes: state read + state written twice + history and conv taps
+    + inputs + y and its Q8_1."""
+    import torch
+
+    import rapier_amd as rmi
+    h_k, h_v, S = 16, 32, 128
+    ch = 2 * h_k * S + h_v * S
+    stride = ch + h_v * S + 2 * h_v                    # the engine's in_proj rows: q|k|v|z|beta|alpha
+    nrot = 80
+    st = torch.empty(nrot, 2, S * h_v * S, device="cuda")
+    rmi.gen_normal(st, st.numel(), seed=31, std=0.05)
+    hist = torch.empty(nrot, 2, h_v * 3 * S * 3, device="cuda")
+    rmi.gen_normal(hist, hist.numel(), seed=32, std=0.5)
+    proj = torch.empty(2 * stride, device="cuda")
+    rmi.gen_normal(proj, proj.numel(), seed=33)
+    conv_w = torch.empty(4 * ch, device="cuda")
+    rmi.gen_normal(conv_w, conv_w.numel(), seed=34, std=0.5)
+    dt = torch.zeros(h_v, device="cuda")
+    ssm_a = -torch.ones(h_v, device="cuda")
+    gamma = torch.ones(S, device="cuda")
+    sel = torch.zeros(1, dtype=torch.int32, device="cuda")
+    y = torch.empty(2 * h_v * S, device="cuda")
+    q8b = rmi.native_q8_1_bytes(h_v * S, 1)
+    q8 = torch.empty(2 * q8b, dtype=torch.uint8, device="cuda")
+
+    def launch(r):
+        rmi.gdn_layer_tokens(st[r, 0], st[r, 1], hist[r, 0], hist[r, 1], sel, proj, stride, proj[ch + h_v * S:],
+                             stride, conv_w, dt, ssm_a, gamma, 1e-6, y, h_v * S, q8, q8b, h_k, h_v, 2, stream)
+
+    us, n = time_blocks(stream, launch, nrot)
+    state = S * h_v * S * 4
+    nbytes = 3 * state + 2 * 2 * h_v * 3 * S * 3 * 4 + 4 * ch * 4 + 2 * stride * 4 + 2 * (h_v * S * 4 + q8b)
+    return {"kernel": "gdn layer, 2 tokens (rmi_gdn_layer_tokens)", "per_round": ROUND_GDN, "algorithmic_bytes": nbytes,
+            "us": round(us, 3), "GB_s": round(nbytes / us / 1e3, 1), "launches_timed": n}
+
+
+def time_attention(stream, ctx):
+    """the verify round's attention launch pair (rmi_gqa_flash_decode: split-K partial + merge with the sigmoid gate
+    and Q8_1) for 2 queries at positions ctx - 2, ctx - 1 over a fp16 KV cache of the 9B shapes (4 KV heads x 256),
+    rotating over enough caches to exceed the Infinity Cache.  Algorithmic bytes: K + V rows read once."""
+    import torch
+
+    import rapier_amd as rmi
+    n_head, n_kv, hd = 16, 4, 256
+    max_ctx = ctx + 512
+    nsub = max(2, min(16, max_ctx // 8192))
+    row = n_kv * hd
+    nrot = max(2, -(-400_000_000 // (2 * max_ctx * row * 2)))
+    kv = torch.empty(nrot, 2, max_ctx * row, dtype=torch.float16, device="cuda")
+    rmi.gen_normal_f16(kv, kv.numel(), seed=41)
+    q = torch.empty(2 * n_head * hd, device="cuda")
+    rmi.gen_normal(q, q.numel(), seed=42)
+    gstride = 2 * n_head * hd + 2 * row
+    gate = torch.empty(2 * gstride, device="cuda")
+    rmi.gen_normal(gate, gate.numel(), seed=43)
+    pos = torch.tensor([ctx - 2], dtype=torch.int32, device="cuda")
+    q8b = rmi.native_q8_1_bytes(n_head * hd, 1)
+    q8 = torch.empty(2 * q8b, dtype=torch.uint8, device="cuda")
+    ws = torch.empty(rmi.gqa_workspace_bytes(max_ctx, n_kv, nsub), dtype=torch.uint8, device="cuda")
+
+    def launch(r):
+        rmi.gqa_flash_decode(q, kv[r, 0], kv[r, 1], pos, gate, gstride, None, 0, q8, q8b, ws, n_head, n_kv, hd, 2,
+                             max_ctx, nsub, 1.0 / 16, stream)
+
+    us, n = time_blocks(stream, launch, nrot)
+    nbytes = 2 * ctx * row * 2
+    return {"kernel": f"attention, 2 queries, ctx {ctx} (rmi_gqa_flash_decode: partial + merge, nsub {nsub})",
+            "per_round": ROUND_ATTN, "algorithmic_bytes": nbytes, "us": round(us, 3),
+            "GB_s": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "launches_timed": n}
+
+
+def run_kernels(args):
+    """Each GEMV shape of the verify round at two columns, on the packed layout the engine runs, over >= 1 GB of
+    rotating replicas (so no launch finds its weights in the 256 MB Infinity Cache): mean launch time from HIP events
+    around blocks of back-to-back launches, algorithmic GB/s and fraction of peak.  Also the workload of the rocprofv3
+    counter passes over the same kernels."""
+    import torch
+
+    import rapier_amd as rmi
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream(device=0)
+    torch.cuda.set_stream(stream)
+    only = set(args.shapes.split(",")) if args.shapes else None
+    out = []
+    for i_shape, (name, n_in, n_out, kind, per_round) in enumerate(ROUND_KERNEL_GEMVS):
+        if only is not None and str(i_shape) not in only:
+            continue
+        wbytes = q6_bytes(n_out, n_in)
+        reps = max(2, -(-1_000_000_000 // wbytes))
+        src = torch.empty(wbytes, dtype=torch.uint8, device="cuda")
+        wp = []
+        for r in range(reps):
+            rmi.gen_q6_k(src, n_out * n_in // 256, seed=7000 + 31 * i_shape + r)
+            w = torch.empty(rmi.q6_k_packed_bytes(n_in, n_out), dtype=torch.uint8, device="cuda")
+            if kind == "swiglu":
+                rmi.q6_k_pack_swiglu(src, w, n_in, n_out // 2, stream)
+            else:
+                rmi.q6_k_pack(src, w, n_in, n_out, stream)
+            wp.append(w)
+        del src
+        x = torch.empty(2 * n_in, device="cuda")
+        rmi.gen_normal(x, x.numel(), seed=11 + i_shape)
+        xq = torch.empty(rmi.native_q8_1_bytes(n_in, 2), dtype=torch.uint8, device="cuda")
+        rmi.native_quantize_q8_1(x, xq, n_in, 2, stream)
+        y = torch.empty(2 * n_out, device="cuda")
+        rmi.gen_normal(y, y.numel(), seed=12 + i_shape)
+        part = torch.empty(2 * (n_out // 4), device="cuda")
+        yq = torch.empty(rmi.native_q8_1_bytes(max(n_out // 2, 32), 2), dtype=torch.uint8, device="cuda")
+
+        def launch(r):
+            if kind == "swiglu":
+                rmi.native_q6_k_swiglu_packed(wp[r], xq, yq, n_in, n_out // 2, 2, stream)
+            elif kind == "res":
+                rmi.native_q6_k_mmvq_packed_res_n(wp[r], xq, y, y, part, n_in, n_out, 2, stream)
+            else:
+                rmi.native_q6_k_mmvq_packed(wp[r], xq, y, n_in, n_out, 2, stream)
+
+        for r in range(reps):
+            launch(r)
+        blocks, per_block = 5, max(2 * reps, 20)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(blocks)]
+        torch.cuda.synchronize()
+        for b in range(blocks):
+            evs[b][0].record(stream)
+            for i in range(per_block):
+                launch(i % reps)
+            evs[b][1].record(stream)
+        torch.cuda.synchronize()
+        us = sum(a.elapsed_time(b) * 1e3 / per_block for a, b in evs) / blocks
+        nbytes = gemv_algorithmic_bytes(n_in, n_out, kind)
+        row = {"gemv": name, "n_in": n_in, "n_out": n_out, "kind": kind, "per_round": per_round,
+               "algorithmic_bytes": nbytes, "us": round(us, 3), "GB_s": round(nbytes / us / 1e3, 1),
+               "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "launches_timed": blocks * per_block}
+        out.append(row)
+        print(json.dumps(row), file=sys.stderr, flush=True)
+        del wp
+        torch.cuda.synchronize()
+    others = []
+    n = len(ROUND_KERNEL_GEMVS)
+    if only is None or str(n) in only:
+        others.append(time_gdn_layer(stream))
+    for i, ctx in enumerate((4096, 65536)):
+        if only is None or str(n + 1 + i) in only:
+            others.append(time_attention(stream, ctx))
+    for r in others:
+        print(json.dumps(r), file=sys.stderr, flush=True)
+    tot_us = sum(r["us"] * r["per_round"] for r in out)
+    tot_b = sum(r["algorithmic_bytes"] * r["per_round"] for r in out)
+    print(json.dumps({"workload": "kernels", "gemvs": out, "others": others,
+                      "round_gemv_us": round(tot_us, 1), "round_gemv_bytes": tot_b,
+                      "round_gemv_frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4) if tot_us else None}),
+          flush=True)
+
 ACCEPT_PATTERNS = {"0": [0], "0.5": [1, 0], "1.0": [1]}
 
 
@@ -407,6 +606,40 @@ def run_mtp_rounds(args, contexts=(4096, 65536)):
         del eng
         torch.cuda.synchronize()
     return table, identical, info
+
+
+def run_round(args):
+    """Verify rounds only, at the first context of --ctx and forced acceptance 0.5: the workload of the whole-round
+    counter passes (HBM bytes per round) and of quick round timings.  The greedy stream is generated first, as every
+    forced MTP run needs it, and the MTP stream is checked against it."""
+    import torch
+
+    import rapier_amd.engine as E
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream(device=0)
+    torch.cuda.set_stream(stream)
+    ctx = int(args.ctx.split(",")[0])
+    K, W = args.steps, args.warmup
+    pat = ACCEPT_PATTERNS["0.5"]
+    eng = E.Engine(E.qwen35_9b_config(), seed=2024, max_ctx=ctx + 2 * (K + W) + 256, stream=stream)
+    info = eng.info()
+    eng.synth_context(ctx, seed=ctx, last_token=1000)
+    pos0, cur0 = eng.state()
+    eng.save_state()
+    ref, _ = eng.generate(tokens_for_rounds([1], K + W), mode=E.GREEDY)
+    eng.restore_state(pos0, cur0)
+    if W:
+        eng.generate(tokens_for_rounds(pat, W), mode=E.MTP_FORCED, ref_tokens=ref, ref_base=pos0 + 1, pattern=pat)
+        eng.restore_state(pos0, cur0)
+    n = tokens_for_rounds(pat, K)
+    toks, st = eng.generate(n, mode=E.MTP_FORCED, ref_tokens=ref, ref_base=pos0 + 1, pattern=pat)
+    eng.close()
+    torch.cuda.synchronize()
+    us = st["gpu_ms"] * 1e3 / st["rounds"]
+    print(json.dumps({"workload": "round", "ctx": ctx, "rounds": st["rounds"], "us_per_round": round(us, 2),
+                      "tok_s": round(n / (st["gpu_ms"] / 1e3), 2), "stream_identical": toks == ref[:n],
+                      "round_weight_bytes": info["round_weight_bytes"], "kv_bytes_per_pos": info["kv_bytes_per_pos"]}),
+          flush=True)
 
 
 def run_ingest(n_prompt=4096, batch=16, n_check=64):
@@ -648,7 +881,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200, help="timed verify rounds per run (mtp_round) or GEMV pairs")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="mtp_round",
-                    choices=["mtp_round", "verify_gemv", "traffic_probe", "gguf_load"])
+                    choices=["mtp_round", "verify_gemv", "traffic_probe", "gguf_load", "kernels", "round"])
+    ap.add_argument("--shapes", default="", help="kernels: comma-separated indices of the GEMV shapes to run")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--plan", default="q6_k", choices=["q6_k", "q5_k_m"], help="gguf_load: the file's type plan")
     ap.add_argument("--ctx", default="4096,65536",
@@ -663,6 +897,12 @@ def main():
         return
     if args.workload == "gguf_load":
         run_gguf_load(args)
+        return
+    if args.workload == "kernels":
+        run_kernels(args)
+        return
+    if args.workload == "round":
+        run_round(args)
         return
     gemv_args =argparse.Namespace(steps=50 if args.workload == "mtp_round" else args.steps,
                                    warmup=10 if args.workload == "mtp_round" else args.warmup)

@@ -134,9 +134,28 @@ __device__ __forceinline__ float sum_row_groups(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// a zero the compiler cannot see through: indexing a uniform address with it keeps the load on the vector path, in
+// issue order with the kernel's other loads (a scalar load gets a wait of its own at the next branch)
+__device__ __forceinline__ int opaque_zero() {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
+// decay and beta of token t from the raw beta|alpha GEMV output (qw:707-715)
+__device__ __forceinline__ void gate_values(float b_raw, float a_raw, float dt, float ssm_a, float& g, float& b) {
+    b = 1.0f / (1.0f + expf(-b_raw));
+    const float vv = a_raw + dt;
+    g = expf((vv > 20.0f ? vv : log1pf(expf(vv))) * ssm_a);
+}
+
 template <int NT, bool RAW, bool CONV>
 __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     constexpr bool SNAP = NT == 2;
+    // decode / verify on the engine path: the launch's loads go out in one batch led by the selector (both history
+    // buffers read, one kept), so the state loads wait for one memory round trip, not three; the gates are derived by
+    // the conv's idle lanes and published by the conv's own barrier
+    constexpr bool FAST = CONV && RAW && NT <= 2;
     __shared__ float cq[NT][S], ck[NT][S], cv[CONV ? NT : 1][S];   // q, k (and v) of every token
     __shared__ float cpart[NT][4];
     __shared__ float gbt[NT][2];                                    // decay, beta per token
@@ -152,11 +171,15 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     const int qh = head % a.h_k;
     const size_t row_stride = static_cast<size_t>(a.h_v) * S;
     const size_t base = (static_cast<size_t>(rg * RPG) * a.h_v + head) * S + col;
-
-    // everything that does not depend on the selector is loaded first, in flight with *sel: the raw q|k|v rows and
-    // conv taps (CONV), z and gamma (the norm lanes), the gate inputs (lane t for token t)
     const int kind = threadIdx.x >> 7;   // CONV prologue: 0 q, 1 k, 2 v, 3 idle
     const int j = threadIdx.x & (S - 1);
+
+    // FAST: the selector is the launch's first load (the state addresses depend on it)
+    int selv = 0;
+    if constexpr (FAST) selv = a.sel[opaque_zero()];
+
+    // everything that does not depend on the selector is loaded next, in flight with it: the raw q|k|v rows and conv
+    // taps (CONV), z and gamma (the norm lanes), the gate inputs, and (FAST) both history buffers
     const float* src = kind == 0 ? a.q + qh * S : kind == 1 ? a.k + qh * S : a.v + head * S;
     const int c = kind == 0 ? qh * S + j : kind == 1 ? (a.h_k + qh) * S + j : (2 * a.h_k + head) * S + j;
     float xr[NT], w0 = 0.0f, w1 = 0.0f, w2 = 0.0f, w3 = 0.0f;
@@ -181,8 +204,9 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
             if (t < ntok) zz[t] = a.z[static_cast<size_t>(t) * a.tok_stride + head * S + col];
     }
     float gin[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int gt = threadIdx.x;   // gate lane: token gt
-    if (gt < ntok) {
+    // gate lane of token gt: lanes 0.. (FAST: the conv's idle lanes 3 S ..)
+    const int gt = FAST ? static_cast<int>(threadIdx.x) - 3 * S : static_cast<int>(threadIdx.x);
+    if (gt >= 0 && gt < ntok) {
         if constexpr (RAW) {
             const float* ab = a.ab + static_cast<size_t>(gt) * a.ab_stride;
             gin[0] = ab[head];
@@ -194,19 +218,32 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
             gin[1] = a.gate[head];
         }
     }
+    // CONV history slot: this head's own copy of the channel (the idle lanes read the q slot and ignore it: no branch
+    // around the loads, so the compiler's wait for them counts the state loads issued after)
+    const int ch = (3 * head + (kind < 3 ? kind : 0)) * S + j;
+    float hA[3] = {0.0f, 0.0f, 0.0f}, hB[3] = {0.0f, 0.0f, 0.0f};
+    if constexpr (FAST) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            hA[i] = a.hist_a[3 * ch + i];
+            hB[i] = a.hist_b[3 * ch + i];
+        }
+    }
 
-    // the selector is read once; the conv history loads go ahead of the state's 32 loads, so the conv (which needs
-    // only the history) does not wait for the state (a wave's loads complete in issue order)
-    const bool sel_b = a.sel != nullptr && *a.sel != 0;
+    // the selector: read once (FAST: it arrived first); the other paths read it here, with the history behind
+    // it and ahead of the state's 32 loads, so the conv (which needs only the history) does not wait for the state
+    // (a wave's loads complete in issue order)
+    const bool sel_b = FAST ? selv != 0 : (a.sel != nullptr && *a.sel != 0);
     float* state = sel_b ? a.state_b : a.state_a;
     float* snap = sel_b ? a.state_a : a.state_b;
     float* hist = sel_b ? a.hist_b : a.hist_a;
     float* hsnap = sel_b ? a.hist_a : a.hist_b;
-    // CONV history slot: this head's own copy of the channel (the idle lanes read the q slot and ignore it: no branch
-    // around the loads, so the compiler's wait for them counts the state loads issued after)
-    const int ch = (3 * head + (kind < 3 ? kind : 0)) * S + j;
     float h0 = 0.0f, h1 = 0.0f, h2 = 0.0f;
-    if constexpr (CONV) {
+    if constexpr (FAST) {
+        h0 = sel_b ? hB[0] : hA[0];
+        h1 = sel_b ? hB[1] : hA[1];
+        h2 = sel_b ? hB[2] : hA[2];
+    } else if constexpr (CONV) {
         h0 = hist[3 * ch];
         h1 = hist[3 * ch + 1];
         h2 = hist[3 * ch + 2];
@@ -218,6 +255,11 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     float s[RPG];
 #pragma unroll
     for (int r = 0; r < RPG; ++r) s[r] = __builtin_nontemporal_load(state + base + r * row_stride);
+
+    // FAST: the gate lanes publish each token's decay and beta with the conv's first barrier
+    if constexpr (FAST) {
+        if (gt >= 0 && gt < ntok) gate_values(gin[0], gin[1], gin[2], gin[3], gbt[gt][0], gbt[gt][1]);
+    }
 
     if constexpr (CONV) {
         float y[NT];
@@ -274,7 +316,7 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
                 hist[3 * ch + 2] = n2;
             }
         }
-        __syncthreads();   // cq / ck / cv are read by other lanes at the top of the token loop
+        if constexpr (FAST) __syncthreads();   // cq / ck / cv are read by other lanes at the top of the token loop
     }
 
     if constexpr (!CONV) {
@@ -293,20 +335,21 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
         for (int t = 0; t < NT; ++t)
             vreg[t] = t < ntok ? a.v[static_cast<size_t>(t) * a.tok_stride + head * S + col] : 0.0f;
     }
-    if (gt < ntok) {
-        float g, b;
-        if constexpr (RAW) {
-            b = 1.0f / (1.0f + expf(-gin[0]));
-            const float vv = gin[1] + gin[2];
-            g = expf((vv > 20.0f ? vv : log1pf(expf(vv))) * gin[3]);
-        } else {
-            b = gin[0];
-            g = expf(gin[1]);
+    if constexpr (!FAST) {
+        // the gate lane of each token publishes its decay and beta (the barrier also publishes cq / ck / cv)
+        if (gt < ntok) {
+            float g, b;
+            if constexpr (RAW) {
+                gate_values(gin[0], gin[1], gin[2], gin[3], g, b);
+            } else {
+                b = gin[0];
+                g = expf(gin[1]);
+            }
+            gbt[gt][0] = g;
+            gbt[gt][1] = b;
         }
-        gbt[gt][0] = g;
-        gbt[gt][1] = b;
+        __syncthreads();
     }
-    __syncthreads();
 
     // The recurrence runs through all tokens without a workgroup barrier: the output norm of token t (a sum over the
     // head's 128 columns, across waves) feeds only y, so each token's o and per-wave sum of squares are kept and the
@@ -420,7 +463,8 @@ extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_
     if (channels % 256 != 0 || qkvz_stride < channels + h_v * S)
         return fail(RMI_ERR_SHAPE, "gdn_layer_tokens: invalid arguments");
     if (!aligned4(state_a) || !aligned4(state_b) || !aligned4(hist_a) || !aligned4(hist_b) || !aligned4(qkvz) ||
-        !aligned4(ab) || !aligned4(conv_w) || !aligned4(dt) || !aligned4(ssm_a) || !aligned4(gamma) || !aligned4(y))
+        !aligned4(ab) || !aligned4(conv_w) || !aligned4(dt) || !aligned4(ssm_a) || !aligned4(gamma) || !aligned4(y) ||
+        !aligned4(sel))
         return fail(RMI_ERR_POINTER, "gdn_layer_tokens: invalid arguments");
     const auto s = static_cast<hipStream_t>(stream);
     StepArgs a{};
