@@ -47,13 +47,20 @@ PAIR_BYTES = UG_BYTES + DN_BYTES                                                
 # the round's up||gate kernel: GEMV + SwiGLU + Q8_1 in one launch (weights, Q8_1 in, Q8_1 out of the 12288 products)
 UGS_BYTES = q6_bytes(UG_ROWS, UG_IN) + 2 * (UG_IN // 32) * 36 + 2 * (UG_ROWS // 2 // 32) * 36  # 82,612,224
 
-# HBM traffic of one fused up||gate + SwiGLU ncols=2 launch, from two rocprofv3 --pmc passes over `bench.py --workload
-# traffic_probe` (profiles/gemv_up_gate_swiglu_traffic.md): FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by
-# what the same counter reads for a copy kernel that reads 256 MiB and writes 256 MiB in the same process.
-PMC_UG_FETCH_KIB, PMC_UG_WRITE_KIB = 40505.75, 48.0
-PMC_COPY_FETCH_KIB, PMC_COPY_WRITE_KIB, COPY_KIB = 131087.625, 262144.0, 262144.0
-UG_TRAFFIC_BYTES = round(1024 * (PMC_UG_FETCH_KIB * COPY_KIB / PMC_COPY_FETCH_KIB
-                                 + PMC_UG_WRITE_KIB * COPY_KIB / PMC_COPY_WRITE_KIB))
+# HBM traffic of one fused up||gate + SwiGLU ncols=2 launch: L2-to-memory request counts from two rocprofv3 --pmc passes
+# over `bench.py --workload traffic_probe` (profiles/gemv_up_gate_swiglu_traffic.md).  On gfx950 a TCC_EA0_RDREQ that is
+# not a 32-byte request moves 128 bytes (the same process's copy kernel reads 256 MiB in 2,097,395 requests), and a
+# TCC_EA0_WRREQ is 64 bytes (TCC_EA0_WRREQ_64B) or 32.
+PMC_UG_RDREQ, PMC_UG_RDREQ_32B = 647995, 0
+PMC_UG_WRREQ, PMC_UG_WRREQ_64B = 1152, 384
+
+
+def ea_bytes(rdreq, rdreq_32b, wrreq, wrreq_64b):
+    """HBM bytes from the TCC/EA request counters: 128-byte and 32-byte reads, 64-byte and 32-byte writes"""
+    return 128 * (rdreq - rdreq_32b) + 32 * rdreq_32b + 64 * wrreq_64b + 32 * (wrreq - wrreq_64b)
+
+
+UG_TRAFFIC_BYTES = ea_bytes(PMC_UG_RDREQ, PMC_UG_RDREQ_32B, PMC_UG_WRREQ, PMC_UG_WRREQ_64B)   # 82,992,512
 
 
 def cpu_model():
@@ -358,7 +365,7 @@ def run_traffic_probe():
                       "copy_write_bytes": b.numel() * 4}), flush=True)
 
 
-COPY_KIB_ELEMS = int(COPY_KIB * 1024 // 4)
+COPY_KIB_ELEMS = 64 * 1024 * 1024   # floats: the probe's copy kernel reads 256 MiB and writes 256 MiB
 
 # the round's Q6_K GEMVs at two columns, as the engine launches them on its packed copies: (name, n_in, n_out, kind,
 # launches per round); kind "res" = residual + partials epilogue, "swiglu" = up||gate + SwiGLU + Q8_1 (n_out = 2 ff)
@@ -400,6 +407,25 @@ def time_blocks(stream, launch, nrot, blocks=5, per_block=None):
         evs[b][1].record(stream)
     torch.cuda.synchronize()
     return sum(a.elapsed_time(b) * 1e3 / per_block for a, b in evs) / blocks, blocks * per_block
+
+
+def time_read_ref(stream, nbytes):
+    """the single-launch streaming-read reference for nbytes (rmi_stream_read, rotating replicas >= 1 GB), best of a
+    few grids: what one kernel that only reads those bytes takes here, launch and ramp included"""
+    import torch
+
+    import rapier_amd as rmi
+    nbytes = nbytes // 16 * 16
+    nrot = max(2, -(-1_000_000_000 // nbytes))
+    bufs = [torch.full((nbytes,), r, dtype=torch.uint8, device="cuda") for r in range(nrot)]
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    best = None
+    for grid in (512, 1024, 2048, 4096):
+        us, _ = time_blocks(stream, lambda r: rmi.stream_read(bufs[r], nbytes, grid, out, stream), nrot, blocks=3)
+        if best is None or us < best[0]:
+            best = (us, grid)
+    del bufs
+    return best
 
 
 def time_gdn_layer(stream):
@@ -536,13 +562,15 @@ def run_kernels(args):
         torch.cuda.synchronize()
         us = sum(a.elapsed_time(b) * 1e3 / per_block for a, b in evs) / blocks
         nbytes = gemv_algorithmic_bytes(n_in, n_out, kind)
-        row = {"gemv": name, "n_in": n_in, "n_out": n_out, "kind": kind, "per_round": per_round,
-               "algorithmic_bytes": nbytes, "us": round(us, 3), "GB_s": round(nbytes / us / 1e3, 1),
-               "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "launches_timed": blocks * per_block}
-        out.append(row)
-        print(json.dumps(row), file=sys.stderr, flush=True)
         del wp
         torch.cuda.synchronize()
+        ref_us, ref_grid = time_read_ref(stream, nbytes)
+        row = {"gemv": name, "n_in": n_in, "n_out": n_out, "kind": kind, "per_round": per_round,
+               "algorithmic_bytes": nbytes, "us": round(us, 3), "GB_s": round(nbytes / us / 1e3, 1),
+               "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "launches_timed": blocks * per_block,
+               "read_ref_us": round(ref_us, 3), "read_ref_grid": ref_grid, "over_read_ref": round(us / ref_us, 3)}
+        out.append(row)
+        print(json.dumps(row), file=sys.stderr, flush=True)
     others = []
     n = len(ROUND_KERNEL_GEMVS)
     if only is None or str(n) in only:

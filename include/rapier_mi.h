@@ -299,6 +299,10 @@ int rmi_gen_q6_k(void* w, size_t nblocks, uint64_t seed, float d_std, void* stre
 int rmi_gen_q8_0(void* w, size_t nblocks, uint64_t seed, float d_std, void* stream);
 int rmi_gen_normal(float* out, size_t n, uint64_t seed, float mean, float std, void* stream);
 int rmi_gen_normal_f16(uint16_t* out, size_t n, uint64_t seed, float mean, float std, void* stream);
+/* Reads `bytes` (a multiple of 16, 16-byte aligned) with grid x 256 lanes of streaming 16-byte loads and discards
+ * them: the single-launch read-bandwidth reference the GEMV legs are set against (no reference counterpart; `out` is
+ * one device word, written only in the unlikely case that the data fold to a sentinel). */
+int rmi_stream_read(const void* p, size_t bytes, int grid, unsigned* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -54,6 +54,7 @@ SIGNATURES = {
     "rmi_gen_q8_0": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
     "rmi_gen_normal": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
     "rmi_gen_normal_f16": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
+    "rmi_stream_read": (_i, [_vp, _sz, _i, _vp, _vp]),
     "rmi_rms_quant_apply": (_i, [_vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
     "rmi_rms_quant_apply_pair": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
     "rmi_rms_norm_out": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
@@ -266,6 +267,11 @@ def gen_normal(out, n: int, seed: int, mean: float = 0.0, std: float = 1.0, stre
 
 def gen_normal_f16(out, n: int, seed: int, mean: float = 0.0, std: float = 1.0, stream=None):
     _call("rmi_gen_normal_f16", _p(out), n, seed, mean, std, _stream(stream))
+
+
+def stream_read(buf, nbytes: int, grid: int, out, stream=None):
+    """the single-launch read-bandwidth reference: streams nbytes of buf with grid x 256 lanes and discards them"""
+    _call("rmi_stream_read", _p(buf), nbytes, grid, _p(out), _stream(stream))
 
 
 # ---- norm / activation epilogues (qw:602-715) ----------------------------------------------------------------------

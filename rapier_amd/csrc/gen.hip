@@ -101,6 +101,28 @@ __global__ __launch_bounds__(256) void gen_normal_f16_kernel(uint16_t* __restric
 
 unsigned grid_of(size_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
+// the read-bandwidth reference of a single launch: grid-stride 16-byte nontemporal loads, eight per lane in flight,
+// folded into one word that is stored only if it equals a sentinel (so the loads stay live)
+typedef unsigned int rd_u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void stream_read_kernel(const rd_u32x4* __restrict__ p, size_t n16, unsigned* out) {
+    constexpr int U = 8;
+    const size_t stride = static_cast<size_t>(gridDim.x) * 256;
+    size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    unsigned acc = 0;
+    for (; i + (U - 1) * stride < n16; i += U * stride) {
+        rd_u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(p + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    for (; i < n16; i += stride) {
+        const rd_u32x4 v = __builtin_nontemporal_load(p + i);
+        acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+    }
+    if (acc == 0x9e3779b9u) out[0] = acc;
+}
+
 }  // namespace
 }  // namespace rmi
 
@@ -136,4 +158,13 @@ extern "C" int rmi_gen_normal_f16(uint16_t* out, size_t n, uint64_t seed, float 
     hipLaunchKernelGGL(gen_normal_f16_kernel, dim3(grid_of(n)), dim3(256), 0, static_cast<hipStream_t>(stream), out,
                        n, seed, mean, std);
     return launch_status("gen_normal_f16");
+}
+
+extern "C" int rmi_stream_read(const void* p, size_t bytes, int grid, unsigned* out, void* stream) {
+    if (!p || (reinterpret_cast<uintptr_t>(p) & 15u) || bytes % 16 || !aligned4(out))
+        return fail(RMI_ERR_POINTER, "rmi_stream_read: 16-byte aligned buffer of whole 16-byte words required");
+    if (grid <= 0) return fail(RMI_ERR_SHAPE, "rmi_stream_read: grid must be positive");
+    hipLaunchKernelGGL(stream_read_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const rd_u32x4*>(p), bytes / 16, out);
+    return launch_status("stream_read");
 }
