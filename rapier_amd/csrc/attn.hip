@@ -147,7 +147,10 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
                                                           int n_kv, int ntok, int nsub, int max_ctx, float scale) {
     __shared__ __attribute__((aligned(16))) uint8_t tiles[WAVES * KTILE];
     __shared__ float wstat[WAVES][2][SLOTS];
-    const int chunk = blockIdx.x, kv = blockIdx.y, s0 = SLOTS * static_cast<int>(blockIdx.z);
+    // the KV heads of one chunk are neighbouring workgroups (dispatched together), so the four 512-byte head rows of a
+    // position are read close in time
+    const int chunk = static_cast<int>(blockIdx.x) / n_kv, kv = static_cast<int>(blockIdx.x) - chunk * n_kv;
+    const int s0 = SLOTS * static_cast<int>(blockIdx.z);
     const int G = n_head / n_kv;
     const int nq = ntok * G;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -172,6 +175,9 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
 
     const int wbase = cbase + wv * wlen;
     const int nsteps = wbase > p_last ? 0 : min(nsub, (p_last - wbase) / STEP + 1);
+    // the wave's own last row: the prefetch after its last step re-reads it instead of the next wave's rows (those
+    // would be a second HBM pass over 1 / nsub of the cache)
+    const int wlast = min(wbase + wlen - 1, p_last);
     uint8_t* kt = tiles + wv * KTILE;
     const int lim = slot < nq ? p0 + slot / G : -1;   // last position slot `slot` may see
 
@@ -187,18 +193,18 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
     const uint16_t* vb = vc + static_cast<size_t>(kv) * HD;
     const int krow = lane >> 5, kcol = lane & 31;
 
-    // rows are clamped to p_last, so every load is in bounds (a wave with no step re-reads row p_last)
+    // rows are clamped to wlast <= p_last, so every load is in bounds (a wave with no step re-reads row p_last)
     u32x32 kreg;   // one vector value (an array carried across iterations would live in scratch)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int p = min(wbase + 2 * j + krow, p_last);
+        const int p = min(wbase + 2 * j + krow, wlast);
         set_u4(kreg, j, load_kv(kb + p * rstride + kcol * 8));
     }
     // V of a step: [2 j + dg] = position sb + 4 g4 + j, dims 128 dg + 8 l16 + [0, 8); also one step ahead
     u32x32 vnext;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint16_t* vr = vb + min(wbase + 4 * g4 + j, p_last) * rstride + 8 * l16;
+        const uint16_t* vr = vb + min(wbase + 4 * g4 + j, wlast) * rstride + 8 * l16;
         set_u4(vnext, 2 * j, load_kv(vr));
         set_u4(vnext, 2 * j + 1, load_kv(vr + 128));
     }
@@ -223,16 +229,16 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
         for (int j = 0; j < 8; ++j) vreg[j] = get_u4(vnext, j);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint16_t* vr = vb + min(sb + STEP + 4 * g4 + j, p_last) * rstride + 8 * l16;
+            const uint16_t* vr = vb + min(sb + STEP + 4 * g4 + j, wlast) * rstride + 8 * l16;
             set_u4(vnext, 2 * j, load_kv(vr));
             set_u4(vnext, 2 * j + 1, load_kv(vr + 128));
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) *reinterpret_cast<uint4*>(kt + (2 * j + krow) * KROW + kcol * 16) = get_u4(kreg, j);
-        // next step's K is in flight during this step's math (after the last step: row p_last again, a cache hit)
+        // next step's K is in flight during this step's math (after the last step: row wlast again, a cache hit)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const int p = min(sb + STEP + 2 * j + krow, p_last);
+            const int p = min(sb + STEP + 2 * j + krow, wlast);
             set_u4(kreg, j, load_kv(kb + p * rstride + kcol * 8));
         }
         lds_wave_sync();
@@ -483,7 +489,7 @@ int flash_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache,
                  int gate_stride, float* y, int y_stride, uint8_t* q8, int q8_stride, float* ws, int slot_stride,
                  int n_head, int n_kv, int ntok, int nchunks, int nsub, int max_ctx, float scale, hipStream_t s) {
     const int groups = (ntok * (n_head / n_kv) + SLOTS - 1) / SLOTS;
-    hipLaunchKernelGGL(gqa_partial_kernel, dim3(nchunks, n_kv, groups), dim3(256), 0, s, q, kcache, vcache, pos, ws,
+    hipLaunchKernelGGL(gqa_partial_kernel, dim3(nchunks * n_kv, 1, groups), dim3(256), 0, s, q, kcache, vcache, pos, ws,
                        slot_stride, n_head, n_kv, ntok, nsub, max_ctx, scale);
     hipLaunchKernelGGL(gqa_merge_kernel, dim3(ntok, n_head), dim3(HD), 0, s, ws, slot_stride, gate_src, gate_stride,
                        pos, y, y_stride, q8, q8_stride, n_head, n_kv, SUB * nsub);
