@@ -975,6 +975,7 @@ def main():
                 (head["us_per_round"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "verify_gemv_pair": {"GB_s": gemv["value"], "us_per_pair": gemv["config"]["us_per_pair"],
                                  "hbm_frac_of_peak": gemv["config"]["hbm_frac_of_peak"]},
+            "config1_gpu": gemv["config"]["config1"],
             "ingest": ingest,
         },
         "roofline": gemv["roofline"],
