@@ -230,6 +230,10 @@ int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_a, float* h
                          int qkvz_stride, const float* ab, int ab_stride, const float* conv_w, const float* dt,
                          const float* ssm_a, const float* gamma, float eps, float* y, int y_stride, uint8_t* q8,
                          int q8_stride, int h_k, int h_v, int ntok, void* stream);
+/* Waits of rmi_gdn_layer_tokens' decode / verify kernel for the other workgroups of a value head that ran out of their
+ * bound (0 in every correct run; a nonzero count means that launch's outputs are not to be trusted).  No reference
+ * counterpart. */
+unsigned int rmi_gdn_exchange_timeouts(void);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * GQA attention over an fp16 KV cache [pos][n_kv][head_dim]

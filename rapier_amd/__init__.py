@@ -55,6 +55,7 @@ SIGNATURES = {
     "rmi_gen_normal": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
     "rmi_gen_normal_f16": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
     "rmi_stream_read": (_i, [_vp, _sz, _i, _vp, _vp]),
+    "rmi_gdn_exchange_timeouts": (ctypes.c_uint, []),
     "rmi_rms_quant_apply": (_i, [_vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
     "rmi_rms_quant_apply_pair": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
     "rmi_rms_norm_out": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
@@ -359,6 +360,11 @@ def fused_gdn_conv_l2(history, qkv, conv_w, h, channels, qk_heads, eps, stream=N
 def fused_gdn_step_norm_silu_q8(state, q, k, v, gate, beta, z, gamma, eps, y, q8, h_k, h_v, stream=None):
     _call("rmi_fused_gdn_step_norm_silu_q8", _p(state), _p(q), _p(k), _p(v), _p(gate), _p(beta), _p(z), _p(gamma),
           eps, _p(y), _p(q8), h_k, h_v, _stream(stream))
+
+
+def gdn_exchange_timeouts() -> int:
+    """bounded waits of the split GDN kernel that ran out (0 in every correct run)"""
+    return lib().rmi_gdn_exchange_timeouts()
 
 
 def gdn_layer_tokens(state_a, state_b, hist_a, hist_b, sel, qkvz, qkvz_stride, ab, ab_stride, conv_w, dt, ssm_a,

@@ -412,6 +412,237 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     for (int r = 0; r < RPG; ++r) __builtin_nontemporal_store(s[r], state + base + r * row_stride);
 }
 
+// ---- decode / verify step split over four workgroups per value head ---------------------------------------------------
+// The engine's 1- and 2-token layer launch (conv + SiLU + L2, gates, delta-rule step, RMSNorm * SiLU gate, Q8_1) with
+// each value head's 128 state columns cut into four parts of 32: workgroup (head, part) holds the part's 32 columns x
+// 128 rows in two waves (lane: column 32 part + 16 w + l % 16, row group l / 16), so 128 CUs carry the state instead
+// of 32 and each SIMD one wave instead of two.  Every per-lane operation, and every reduction order, is that of
+// gdn_step_kernel (the column sums over row groups, the conv's 64-lane L2 partials, the output norm's sum of the eight
+// 16-column wave sums in wave order), so the results are bitwise those of the one-workgroup kernel, which the ingest
+// chunks run.  The part's 32 columns are one Q8_1 block per token.
+// Each part recomputes the head's q and k conv (all 128 channels: the step reads all of them); part 0 writes their
+// history.  The output norm needs the head's eight wave sums: each part publishes its two per token as {bits, epoch}
+// 8-byte words (agent scope: value and tag land together) and reads the other parts' words.  The epoch is the number
+// of launches the head's parts have completed: every launch writes every part's words with the next one, so at the
+// start of a launch all four parts' words carry the same tag, and a part reads it from its own word (which only it
+// writes), waits for the other parts' words to carry tag + 1, and needs no reset.  Workgroups are dispatched in order
+// and the four parts of a head are neighbours, so every wait ends (it is bounded all the same:
+// gdn_exchange_timeouts).  Launches that overlap on one GPU share the exchange words and race.
+constexpr int kParts = 4;
+constexpr int kPartCols = S / kParts;   // 32
+constexpr int kPartLanes = kPartCols * RG;   // 128
+constexpr int kXchHeads = 256;
+__device__ __align__(16) unsigned long long gdn_xch[kXchHeads][kParts][2][2];   // [head][part][token][wave]
+__device__ unsigned int gdn_xch_timeouts;
+
+template <int NT>
+__global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
+    static_assert(NT == 1 || NT == 2, "decode or verify");
+    constexpr bool SNAP = NT == 2;
+    __shared__ float cq[NT][S], ck[NT][S], cv[NT][kPartCols];
+    __shared__ float cpart[NT][2][2];   // [token][q | k][wave]
+    __shared__ float gbt[NT][2];
+    __shared__ float wsum[NT][2];       // this part's two wave sums
+    __shared__ float allw[NT][S * RG / 64];   // the head's eight wave sums, in wave order
+    __shared__ float ybuf[NT][kPartCols];
+    const int head = static_cast<int>(blockIdx.x) / kParts, part = static_cast<int>(blockIdx.x) % kParts;
+    const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+    const int lcol = 16 * wv + (ln & 15);
+    const int col = kPartCols * part + lcol;
+    const int rg = ln >> 4;
+    const int qh = head % a.h_k;
+    const size_t row_stride = static_cast<size_t>(a.h_v) * S;
+    const size_t base = (static_cast<size_t>(rg * RPG) * a.h_v + head) * S + col;
+    const int j = threadIdx.x;                   // q and k channel j of the k-head; lanes < 32: v of column 32 part + j
+    const bool vlane = j < kPartCols;
+    const int jv = kPartCols * part + (vlane ? j : 0);
+
+    const int selv = a.sel[opaque_zero()];      // first: the state addresses depend on it
+    // the exchange epoch of this launch: the tag of this part's own first word (written by no one else)
+    unsigned long long* xh = &gdn_xch[head][0][0][0];
+    const unsigned long long own0 = __hip_atomic_load(xh + part * 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float qx[NT], kx[NT], vx[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        qx[t] = a.q[static_cast<size_t>(t) * a.tok_stride + qh * S + j];
+        kx[t] = a.k[static_cast<size_t>(t) * a.tok_stride + qh * S + j];
+        vx[t] = a.v[static_cast<size_t>(t) * a.tok_stride + head * S + jv];
+    }
+    const int cqc = qh * S + j, ckc = (a.h_k + qh) * S + j, cvc = (2 * a.h_k + head) * S + jv;
+    float wq[4], wk[4], wvv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        wq[i] = a.conv_w[4 * cqc + i];
+        wk[i] = a.conv_w[4 * ckc + i];
+        wvv[i] = a.conv_w[4 * cvc + i];
+    }
+    float zz[NT], gam = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) zz[t] = 0.0f;
+    if (rg == 0) {
+        gam = a.gamma[col];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) zz[t] = a.z[static_cast<size_t>(t) * a.tok_stride + head * S + col];
+    }
+    float gin[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int gt = static_cast<int>(threadIdx.x) - 64;   // gate lane of token gt: the second wave's first lanes
+    if (gt >= 0 && gt < NT) {
+        const float* ab = a.ab + static_cast<size_t>(gt) * a.ab_stride;
+        gin[0] = ab[head];
+        gin[1] = ab[a.h_v + head];
+        gin[2] = a.dt[head];
+        gin[3] = a.ssm_a[head];
+    }
+    // history slots of this value head's copy: q, k (channel j), v (column 32 part + j), both buffers
+    const int chq = (3 * head) * S + j, chk = (3 * head + 1) * S + j, chv = (3 * head + 2) * S + jv;
+    float hq[2][3], hk[2][3], hv[2][3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        hq[0][i] = a.hist_a[3 * chq + i];
+        hq[1][i] = a.hist_b[3 * chq + i];
+        hk[0][i] = a.hist_a[3 * chk + i];
+        hk[1][i] = a.hist_b[3 * chk + i];
+        hv[0][i] = a.hist_a[3 * chv + i];
+        hv[1][i] = a.hist_b[3 * chv + i];
+    }
+    const bool sel_b = selv != 0;
+    float* state = sel_b ? a.state_b : a.state_a;
+    float* snap = sel_b ? a.state_a : a.state_b;
+    float* hist = sel_b ? a.hist_b : a.hist_a;
+    float* hsnap = sel_b ? a.hist_a : a.hist_b;
+    const int sb = sel_b ? 1 : 0;
+    __builtin_amdgcn_sched_barrier(0);
+    float s[RPG];
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) s[r] = __builtin_nontemporal_load(state + base + r * row_stride);
+
+    if (gt >= 0 && gt < NT) gate_values(gin[0], gin[1], gin[2], gin[3], gbt[gt][0], gbt[gt][1]);
+
+    // conv + SiLU over [h0 h1 h2 | x_0 .. x_NT-1] (gdn_step_kernel's arithmetic), L2 of q and k over 128 channels
+    auto conv = [&](const float (&h)[3], const float (&x)[NT], const float (&w)[4], float (&y)[NT]) {
+        auto seq = [&](int i) { return i < 3 ? h[i] : x[i - 3]; };
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            y[t] = silu(__builtin_fmaf(seq(t + 3), w[3],
+                                       __builtin_fmaf(seq(t + 2), w[2], __builtin_fmaf(seq(t + 1), w[1], seq(t) * w[0]))));
+    };
+    float yq[NT], yk[NT], yv[NT];
+    conv(hq[sb], qx, wq, yq);
+    conv(hk[sb], kx, wk, yk);
+    conv(hv[sb], vx, wvv, yv);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float sq = group_sum<64>(yq[t] * yq[t]);
+        const float sk = group_sum<64>(yk[t] * yk[t]);
+        if (ln == 0) {
+            cpart[t][0][wv] = sq;
+            cpart[t][1][wv] = sk;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        cq[t][j] = yq[t] * rsqrtf((cpart[t][0][0] + cpart[t][0][1]) + a.eps);
+        ck[t][j] = yk[t] * rsqrtf((cpart[t][1][0] + cpart[t][1][1]) + a.eps);
+        if (vlane) cv[t][j] = yv[t];
+    }
+    // history: part 0 keeps the head's q / k copies, every part its own v columns
+    auto put_hist = [&](int ch, const float (&h)[3], const float (&x)[NT]) {
+        if constexpr (SNAP) {
+            hsnap[3 * ch] = h[1];
+            hsnap[3 * ch + 1] = h[2];
+            hsnap[3 * ch + 2] = x[0];
+            hist[3 * ch] = h[2];
+            hist[3 * ch + 1] = x[0];
+            hist[3 * ch + 2] = x[NT - 1];
+        } else {
+            hist[3 * ch] = h[1];
+            hist[3 * ch + 1] = h[2];
+            hist[3 * ch + 2] = x[0];
+        }
+    };
+    if (part == 0) {
+        put_hist(chq, hq[sb], qx);
+        put_hist(chk, hk[sb], kx);
+    }
+    if (vlane) put_hist(chv, hv[sb], vx);
+    __syncthreads();
+
+    float occ[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float g = gbt[t][0], beta = gbt[t][1];
+        float kv = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RPG; ++r) kv = __builtin_fmaf(s[r], ck[t][rg * RPG + r], kv);
+        kv = sum_row_groups(kv);
+        const float delta = (cv[t][lcol] - g * kv) * beta;
+        float o = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RPG; ++r) {
+            s[r] = __builtin_fmaf(g, s[r], ck[t][rg * RPG + r] * delta);
+            o = __builtin_fmaf(s[r], cq[t][rg * RPG + r], o);
+        }
+        o = sum_row_groups(o);
+        const float oc = o * 0.08838834764831845f;   // 1 / sqrt(128)
+        if constexpr (SNAP) {
+            if (t == 0) {
+#pragma unroll
+                for (int r = 0; r < RPG; ++r) __builtin_nontemporal_store(s[r], snap + base + r * row_stride);
+            }
+        }
+        const float ss = group_sum<16>(oc * oc);
+        if (ln == 0) wsum[t][wv] = ss;
+        occ[t] = oc;
+    }
+    __syncthreads();
+    // independent of the other parts: the final state goes out and the output gate factor is formed while the
+    // exchange is in flight
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) __builtin_nontemporal_store(s[r], state + base + r * row_stride);
+    // the exchange: publish this part's wave sums, gather the other parts' (wave 0, lane i: part i / (2 NT), token
+    // (i / 2) % NT, wave i % 2)
+    const unsigned long long tag = ((own0 >> 32) + 1ull) << 32;   // this launch's epoch
+    if (threadIdx.x < 4) {   // both tokens' words (a 1-token launch writes token 1's words too, so all stay in step)
+        const int t = threadIdx.x >> 1, w = threadIdx.x & 1;
+        __hip_atomic_store(xh + (part * 2 + t) * 2 + w, tag | __float_as_uint(wsum[t < NT ? t : 0][w]),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (wv == 0) {
+        const int pp = ln / (2 * NT), t = (ln >> 1) % NT, w = ln & 1;
+        const bool other = ln < kParts * 2 * NT && pp != part;
+        unsigned long long v = tag;
+        if (other) v = __hip_atomic_load(xh + (pp * 2 + t) * 2 + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int n = 0;
+        while (!__all(!other || (v >> 32) == (tag >> 32)) && n < (1 << 20)) {
+            if (other && (v >> 32) != (tag >> 32))
+                v = __hip_atomic_load(xh + (pp * 2 + t) * 2 + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ++n;
+        }
+        if (n == (1 << 20) && ln == 0) atomicAdd(&gdn_xch_timeouts, 1u);
+        if (ln < kParts * 2 * NT) allw[t][2 * pp + w] = other ? __uint_as_float(static_cast<uint32_t>(v)) : wsum[t][w];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < S * RG / 64; ++w) tot += allw[t][w];
+        if (rg == 0) {
+            const float scale = rsqrtf(tot / static_cast<float>(S) + a.eps);
+            ybuf[t][lcol] = occ[t] * scale * gam * silu(zz[t]);
+        }
+    }
+    __syncthreads();
+    // y and the part's Q8_1 block per token: lanes 32 t + i (one 32-lane group per token)
+    if (threadIdx.x < kPartCols * NT) {
+        const int t = threadIdx.x / kPartCols, cc = threadIdx.x % kPartCols;
+        const float yv2 = ybuf[t][cc];
+        a.y[static_cast<size_t>(t) * a.y_stride + head * S + kPartCols * part + cc] = yv2;
+        if (a.q8) q8_1_store_lane(yv2, a.q8 + static_cast<size_t>(t) * a.q8_stride + (head * 4 + part) * kQ8_1Bytes);
+    }
+}
+
 }  // namespace
 }  // namespace rmi
 
@@ -477,8 +708,22 @@ extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_
     a.h_k = h_k; a.h_v = h_v;
     a.hist_a = hist_a; a.hist_b = hist_b; a.conv_w = conv_w;
     a.ntok = ntok;
-    if (ntok == 2) hipLaunchKernelGGL((gdn_step_kernel<2, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
-    else if (ntok == 1) hipLaunchKernelGGL((gdn_step_kernel<1, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
-    else hipLaunchKernelGGL((gdn_step_kernel<kMaxCols, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
+    if (ntok <= 2 && h_v <= kXchHeads) {
+        // decode / verify: four workgroups per value head (bitwise the one-workgroup kernel)
+        if (ntok == 2) hipLaunchKernelGGL((gdn_split_kernel<2>), dim3(h_v * kParts), dim3(kPartLanes), 0, s, a);
+        else hipLaunchKernelGGL((gdn_split_kernel<1>), dim3(h_v * kParts), dim3(kPartLanes), 0, s, a);
+    } else if (ntok == 2) {
+        hipLaunchKernelGGL((gdn_step_kernel<2, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
+    } else if (ntok == 1) {
+        hipLaunchKernelGGL((gdn_step_kernel<1, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((gdn_step_kernel<kMaxCols, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
+    }
     return launch_status("gdn_layer_tokens");
+}
+
+extern "C" unsigned int rmi_gdn_exchange_timeouts(void) {
+    unsigned int h = 0;
+    if (hipMemcpyFromSymbol(&h, HIP_SYMBOL(gdn_xch_timeouts), sizeof(h)) != hipSuccess) return 0xffffffffu;
+    return h;
 }

@@ -123,6 +123,27 @@ def test_gdn_two_tokens_bitwise_equal_sequential(orc, rmi, sel_val):
     assert np.array_equal(u(r2["hsnap"]), u(a["hist"])) and np.array_equal(u(r2["hist"]), u(b["hist"]))
 
 
+def test_gdn_split_kernel_bitwise_equal_one_workgroup_kernel(orc, rmi):
+    """Decode / verify launches (1 and 2 tokens) run four workgroups per value head; a 3-token launch runs the
+    one-workgroup-per-head kernel the ingest chunks use.  Token by token the two give the same bits: y, Q8_1, the final
+    state and history.  No exchange between a head's workgroups ran out of its bounded wait."""
+    qkvz3 = orc.normal(3 * QKVZ, seed=700)
+    ab3 = orc.normal(3 * 2 * H_V, seed=701)
+    _, _, conv_w, hist, state, dt, ssm_a, gamma = make_inputs(orc, seed=702)
+    hist = expand_hist(hist)
+    before = rmi.gdn_exchange_timeouts()
+    r3 = run_layer(rmi, qkvz3, ab3, conv_w, hist, state, dt, ssm_a, gamma, ntok=3)
+    a = run_layer(rmi, qkvz3[:2 * QKVZ], ab3[:4 * H_V], conv_w, hist, state, dt, ssm_a, gamma, ntok=2)
+    b = run_layer(rmi, qkvz3[2 * QKVZ:], ab3[4 * H_V:], conv_w, a["hist"], a["state"], dt, ssm_a, gamma, ntok=1)
+    u = lambda v: np.asarray(v).view(np.uint32)  # noqa: E731
+    n = H_V * S
+    assert np.array_equal(u(r3["y"][:2 * n]), u(a["y"])) and np.array_equal(u(r3["y"][2 * n:]), u(b["y"]))
+    blk = n // 32 * 36
+    assert np.array_equal(r3["q8"][:2 * blk], a["q8"]) and np.array_equal(r3["q8"][2 * blk:], b["q8"])
+    assert np.array_equal(u(r3["state"]), u(b["state"])) and np.array_equal(u(r3["hist"]), u(b["hist"]))
+    assert rmi.gdn_exchange_timeouts() == before == 0
+
+
 def test_reference_surface_entry_points(orc, rmi):
     """fused_gdn_conv_l2 + beta_gate + fused_gdn_step_norm_silu_q8 (the reference's 3-launch chain) == layer call."""
     inp = make_inputs(orc, seed=500)
