@@ -429,7 +429,7 @@ def time_read_ref(stream, nbytes):
 
 
 def time_gdn_layer(stream):
-    """the verify round's GDN layer launch (rmi_gdn_layer_tokens, 2 tokens: conv + SiLU + L2, delta-rule step, RMSNorm
+    """the verify round's GDN layer launch (rmi_gdn_layer_tokens_x, 2 tokens: conv + SiLU + L2, delta-rule step, RMSNorm
     * SiLU gate, Q8_1; after-token-0 state to the rollback buffer) at the 9B shapes, rotating over 80 layers' state
     (320 MB, above the Infinity Cache).  Algorithmic bytes: state read + state written twice + history and conv taps
     + inputs + y and its Q8_1."""
@@ -456,14 +456,16 @@ def time_gdn_layer(stream):
     q8b = rmi.native_q8_1_bytes(h_v * S, 1)
     q8 = torch.empty(2 * q8b, dtype=torch.uint8, device="cuda")
 
+    xch = torch.zeros(rmi.gdn_exchange_bytes(h_v), dtype=torch.uint8, device="cuda")
+
     def launch(r):
-        rmi.gdn_layer_tokens(st[r, 0], st[r, 1], hist[r, 0], hist[r, 1], sel, proj, stride, proj[ch + h_v * S:],
-                             stride, conv_w, dt, ssm_a, gamma, 1e-6, y, h_v * S, q8, q8b, h_k, h_v, 2, stream)
+        rmi.gdn_layer_tokens_x(st[r, 0], st[r, 1], hist[r, 0], hist[r, 1], sel, proj, stride, proj[ch + h_v * S:],
+                               stride, conv_w, dt, ssm_a, gamma, 1e-6, y, h_v * S, q8, q8b, h_k, h_v, 2, xch, stream)
 
     us, n = time_blocks(stream, launch, nrot)
     state = S * h_v * S * 4
     nbytes = 3 * state + 2 * 2 * h_v * 3 * S * 3 * 4 + 4 * ch * 4 + 2 * stride * 4 + 2 * (h_v * S * 4 + q8b)
-    return {"kernel": "gdn layer, 2 tokens (rmi_gdn_layer_tokens)", "per_round": ROUND_GDN, "algorithmic_bytes": nbytes,
+    return {"kernel": "gdn layer, 2 tokens (rmi_gdn_layer_tokens_x: four workgroups per value head)", "per_round": ROUND_GDN, "algorithmic_bytes": nbytes,
             "us": round(us, 3), "GB_s": round(nbytes / us / 1e3, 1), "launches_timed": n}
 
 

@@ -230,9 +230,17 @@ int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_a, float* h
                          int qkvz_stride, const float* ab, int ab_stride, const float* conv_w, const float* dt,
                          const float* ssm_a, const float* gamma, float eps, float* y, int y_stride, uint8_t* q8,
                          int q8_stride, int h_k, int h_v, int ntok, void* stream);
-/* Waits of rmi_gdn_layer_tokens' decode / verify kernel for the other workgroups of a value head that ran out of their
- * bound (0 in every correct run; a nonzero count means that launch's outputs are not to be trusted).  No reference
- * counterpart. */
+/* rmi_gdn_layer_tokens with the decode / verify launches (ntok 1 or 2) split over four workgroups per value head, 32
+ * state columns each (bitwise the same results).  The output norm's partial sums cross the head's workgroups through
+ * xch: a caller-owned device buffer of rmi_gdn_exchange_bytes(h_v) bytes, zeroed once before its first use and used
+ * by one stream at a time (launches that overlap on one buffer race).  No reference counterpart. */
+size_t rmi_gdn_exchange_bytes(int h_v);
+int rmi_gdn_layer_tokens_x(float* state_a, float* state_b, float* hist_a, float* hist_b, const int* sel, float* qkvz,
+                           int qkvz_stride, const float* ab, int ab_stride, const float* conv_w, const float* dt,
+                           const float* ssm_a, const float* gamma, float eps, float* y, int y_stride, uint8_t* q8,
+                           int q8_stride, int h_k, int h_v, int ntok, void* xch, void* stream);
+/* Waits of the split kernel for the other workgroups of a value head that ran out of their bound, since the library
+ * was loaded (0 in every correct run; a nonzero count means a launch's outputs are not to be trusted). */
 unsigned int rmi_gdn_exchange_timeouts(void);
 
 /* ---------------------------------------------------------------------------------------------------------------

@@ -56,6 +56,9 @@ SIGNATURES = {
     "rmi_gen_normal_f16": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
     "rmi_stream_read": (_i, [_vp, _sz, _i, _vp, _vp]),
     "rmi_gdn_exchange_timeouts": (ctypes.c_uint, []),
+    "rmi_gdn_exchange_bytes": (_sz, [_i]),
+    "rmi_gdn_layer_tokens_x": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _i, _vp,
+                                    _i, _i, _i, _i, _vp, _vp]),
     "rmi_rms_quant_apply": (_i, [_vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
     "rmi_rms_quant_apply_pair": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
     "rmi_rms_norm_out": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
@@ -365,6 +368,18 @@ def fused_gdn_step_norm_silu_q8(state, q, k, v, gate, beta, z, gamma, eps, y, q8
 def gdn_exchange_timeouts() -> int:
     """bounded waits of the split GDN kernel that ran out (0 in every correct run)"""
     return lib().rmi_gdn_exchange_timeouts()
+
+
+def gdn_exchange_bytes(h_v: int) -> int:
+    return lib().rmi_gdn_exchange_bytes(h_v)
+
+
+def gdn_layer_tokens_x(state_a, state_b, hist_a, hist_b, sel, qkvz, qkvz_stride, ab, ab_stride, conv_w, dt, ssm_a,
+                       gamma, eps, y, y_stride, q8, q8_stride, h_k, h_v, ntok, xch, stream=None):
+    """gdn_layer_tokens with 1 / 2-token launches on four workgroups per value head (xch: zeroed exchange buffer)"""
+    _call("rmi_gdn_layer_tokens_x", _p(state_a), _p(state_b), _p(hist_a), _p(hist_b), _p(sel), _p(qkvz), qkvz_stride,
+          _p(ab), ab_stride, _p(conv_w), _p(dt), _p(ssm_a), _p(gamma), eps, _p(y), y_stride, _p(q8), q8_stride, h_k,
+          h_v, ntok, _p(xch), _stream(stream))
 
 
 def gdn_layer_tokens(state_a, state_b, hist_a, hist_b, sel, qkvz, qkvz_stride, ab, ab_stride, conv_w, dt, ssm_a,

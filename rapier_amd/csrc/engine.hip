@@ -141,6 +141,7 @@ struct Engine {
     float *ex = nullptr, *epart = nullptr, *dx = nullptr, *dpart = nullptr;
     uint8_t *q8a = nullptr, *q8f = nullptr, *q8y = nullptr;
     void *attn_ws = nullptr, *argmax_ws = nullptr, *topk_ws = nullptr;
+    unsigned long long* gdn_xch = nullptr;   // the split GDN step's exchange words (rmi_gdn_exchange_bytes), zeroed once
     int* topk_out = nullptr;        // top-k ids [0, 64) and logits (as float) [64, 128)
     int stream_mode = -1;           // rmi_engine_gen_begin's mode, -1 before it
     // saved GDN state and draft hidden for restore
@@ -528,9 +529,10 @@ int gdn_block(Engine& e, Layer& L, int nc, const float* w_next) {
     RMI_TRY(norm_input(e, e.x, e.part, L.attn_norm, 0, nc, &xq));
     RMI_TRY(norm_gemv(e, L.in_proj, xq, e.part, e.proj, nc));
     const int qkvz = 2 * c.ssm_h_k * kS + 2 * c.ssm_h_v * kS;
-    RMI_TRY(rmi_gdn_layer_tokens(L.state[0], L.state[1], L.hist[0], L.hist[1], e.ints + kSel, e.proj, e.qkvz_rows,
-                                 e.proj + qkvz, e.qkvz_rows, L.conv_w, L.dt, L.ssm_a, L.ssm_norm, c.eps, e.y, e.gdn_v,
-                                 e.q8y, static_cast<int>(q81_bytes(e.gdn_v)), c.ssm_h_k, c.ssm_h_v, nc, e.s));
+    RMI_TRY(rmi_gdn_layer_tokens_x(L.state[0], L.state[1], L.hist[0], L.hist[1], e.ints + kSel, e.proj, e.qkvz_rows,
+                                   e.proj + qkvz, e.qkvz_rows, L.conv_w, L.dt, L.ssm_a, L.ssm_norm, c.eps, e.y, e.gdn_v,
+                                   e.q8y, static_cast<int>(q81_bytes(e.gdn_v)), c.ssm_h_k, c.ssm_h_v, nc, e.gdn_xch,
+                                   e.s));
     RMI_TRY(res_gemv(e, L.out_proj, e.q8y, e.x, e.part, nc, L.post_norm));
     return ffn(e, L, e.x, e.part, nc, w_next);
 }
@@ -1019,6 +1021,11 @@ int alloc_runtime(Engine& e) {
     RMI_TRY(set_int(e, kVocab, c.n_vocab));
     RMI_TRY(set_int(e, kMaxPos, e.max_ctx - 1));
     RMI_TRY(e.alloc(&e.ring, kRingCap));
+    if (c.ssm_h_v > 0) {
+        const size_t xb = rmi_gdn_exchange_bytes(c.ssm_h_v);
+        RMI_TRY(e.alloc(&e.gdn_xch, xb / sizeof(unsigned long long)));
+        HIP_TRY(hipMemsetAsync(e.gdn_xch, 0, xb, e.s));   // once, before any graph is captured
+    }
     RMI_TRY(e.alloc(&e.ref_tok, static_cast<size_t>(e.max_ctx) + 1));
     RMI_TRY(e.alloc(&e.pattern, 4096));
     const size_t np = c.n_embd / 4;

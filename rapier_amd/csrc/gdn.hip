@@ -111,6 +111,7 @@ struct StepArgs {
     float* hist_b;
     const float* conv_w;
     int ntok;              // tokens of this launch (<= the instantiation's NT)
+    unsigned long long* xch;   // the split kernel's exchange words, kXchWords per value head
 };
 
 // CONV (engine path): lanes 0..383 first run the conv of the head's q (k-head qh), k and v channels for all tokens
@@ -427,12 +428,12 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
 // start of a launch all four parts' words carry the same tag, and a part reads it from its own word (which only it
 // writes), waits for the other parts' words to carry tag + 1, and needs no reset.  Workgroups are dispatched in order
 // and the four parts of a head are neighbours, so every wait ends (it is bounded all the same:
-// gdn_exchange_timeouts).  Launches that overlap on one GPU share the exchange words and race.
+// gdn_exchange_timeouts).  The words live in a caller-owned buffer (rmi_gdn_exchange_bytes), zeroed once and used
+// by one stream at a time: launches that overlap on one buffer race.
 constexpr int kParts = 4;
 constexpr int kPartCols = S / kParts;   // 32
 constexpr int kPartLanes = kPartCols * RG;   // 128
-constexpr int kXchHeads = 256;
-__device__ __align__(16) unsigned long long gdn_xch[kXchHeads][kParts][2][2];   // [head][part][token][wave]
+constexpr int kXchWords = kParts * 2 * 2;   // per value head: [part][token][wave]
 __device__ unsigned int gdn_xch_timeouts;
 
 template <int NT>
@@ -459,7 +460,7 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
 
     const int selv = a.sel[opaque_zero()];      // first: the state addresses depend on it
     // the exchange epoch of this launch: the tag of this part's own first word (written by no one else)
-    unsigned long long* xh = &gdn_xch[head][0][0][0];
+    unsigned long long* xh = a.xch + static_cast<size_t>(head) * kXchWords;
     const unsigned long long own0 = __hip_atomic_load(xh + part * 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float qx[NT], kx[NT], vx[NT];
 #pragma unroll
@@ -683,11 +684,11 @@ extern "C" int rmi_fused_gdn_step_norm_silu_q8(float* state, const float* q, con
 // buffers in place (3..16: an ingest chunk, the row-batched step of src/qwythos_ingest.cu).  Per token t: qkvz + t * qkvz_stride holds [q h_k*128 | k h_k*128 | v h_v*128 | z h_v*128]; ab + t * ab_stride holds
 // [beta h_v | alpha h_v] (both read only).  History per value head, [h_v][3 * 128][3].  Output y + t * y_stride, q8
 // + t * q8_stride.
-extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_a, float* hist_b, const int* sel,
-                                    float* qkvz, int qkvz_stride, const float* ab, int ab_stride, const float* conv_w,
-                                    const float* dt, const float* ssm_a, const float* gamma, float eps, float* y,
-                                    int y_stride, uint8_t* q8, int q8_stride, int h_k, int h_v, int ntok,
-                                    void* stream) {
+namespace {
+int gdn_layer(float* state_a, float* state_b, float* hist_a, float* hist_b, const int* sel, float* qkvz,
+              int qkvz_stride, const float* ab, int ab_stride, const float* conv_w, const float* dt, const float* ssm_a,
+              const float* gamma, float eps, float* y, int y_stride, uint8_t* q8, int q8_stride, int h_k, int h_v,
+              int ntok, void* xch, void* stream) {
     if (h_k <= 0 || h_v <= 0 || h_v % h_k || ntok < 1 || ntok > kMaxCols)
         return fail(RMI_ERR_SHAPE, "gdn_layer_tokens: invalid arguments");
     const int channels = 2 * h_k * S + h_v * S;
@@ -708,7 +709,8 @@ extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_
     a.h_k = h_k; a.h_v = h_v;
     a.hist_a = hist_a; a.hist_b = hist_b; a.conv_w = conv_w;
     a.ntok = ntok;
-    if (ntok <= 2 && h_v <= kXchHeads) {
+    a.xch = static_cast<unsigned long long*>(xch);
+    if (ntok <= 2 && xch) {
         // decode / verify: four workgroups per value head (bitwise the one-workgroup kernel)
         if (ntok == 2) hipLaunchKernelGGL((gdn_split_kernel<2>), dim3(h_v * kParts), dim3(kPartLanes), 0, s, a);
         else hipLaunchKernelGGL((gdn_split_kernel<1>), dim3(h_v * kParts), dim3(kPartLanes), 0, s, a);
@@ -720,6 +722,31 @@ extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_
         hipLaunchKernelGGL((gdn_step_kernel<kMaxCols, true, true>), dim3(h_v), dim3(S * RG), 0, s, a);
     }
     return launch_status("gdn_layer_tokens");
+}
+}  // namespace
+
+extern "C" int rmi_gdn_layer_tokens(float* state_a, float* state_b, float* hist_a, float* hist_b, const int* sel,
+                                    float* qkvz, int qkvz_stride, const float* ab, int ab_stride, const float* conv_w,
+                                    const float* dt, const float* ssm_a, const float* gamma, float eps, float* y,
+                                    int y_stride, uint8_t* q8, int q8_stride, int h_k, int h_v, int ntok,
+                                    void* stream) {
+    return gdn_layer(state_a, state_b, hist_a, hist_b, sel, qkvz, qkvz_stride, ab, ab_stride, conv_w, dt, ssm_a, gamma,
+                     eps, y, y_stride, q8, q8_stride, h_k, h_v, ntok, nullptr, stream);
+}
+
+extern "C" size_t rmi_gdn_exchange_bytes(int h_v) {
+    return h_v > 0 ? static_cast<size_t>(h_v) * kXchWords * sizeof(unsigned long long) : 0;
+}
+
+extern "C" int rmi_gdn_layer_tokens_x(float* state_a, float* state_b, float* hist_a, float* hist_b, const int* sel,
+                                      float* qkvz, int qkvz_stride, const float* ab, int ab_stride,
+                                      const float* conv_w, const float* dt, const float* ssm_a, const float* gamma,
+                                      float eps, float* y, int y_stride, uint8_t* q8, int q8_stride, int h_k, int h_v,
+                                      int ntok, void* xch, void* stream) {
+    if (!xch || (reinterpret_cast<uintptr_t>(xch) & 7u))
+        return fail(RMI_ERR_POINTER, "gdn_layer_tokens_x: null or misaligned exchange buffer");
+    return gdn_layer(state_a, state_b, hist_a, hist_b, sel, qkvz, qkvz_stride, ab, ab_stride, conv_w, dt, ssm_a, gamma,
+                     eps, y, y_stride, q8, q8_stride, h_k, h_v, ntok, xch, stream);
 }
 
 extern "C" unsigned int rmi_gdn_exchange_timeouts(void) {

@@ -67,8 +67,9 @@ def oracle_chain(orc, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok=2):
     return ys, states, hists, convs
 
 
-def run_layer(rmi, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok, sel_val=0):
-    """hist in the per-value-head layout (expand_hist)"""
+def run_layer(rmi, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok, sel_val=0, split=False):
+    """hist in the per-value-head layout (expand_hist); split: the engine's entry point (1 / 2-token launches on four
+    workgroups per value head, with a fresh zeroed exchange buffer)"""
     t = torch()
     st_live, st_other = dev(state), t.zeros(S * H_V * S, device="cuda:0")
     hi_live, hi_other = dev(hist), t.zeros(H_V * 3 * S * 3, device="cuda:0")
@@ -77,17 +78,22 @@ def run_layer(rmi, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok, sel_va
     dq = dev(qkvz[:ntok * QKVZ])
     y = empty(ntok * H_V * S)
     q8 = empty(ntok * H_V * S // 32 * 36, "uint8")
-    rmi.gdn_layer_tokens(bufs[0], bufs[1], bufs[2], bufs[3], sel, dq, QKVZ, dev(ab[:ntok * 2 * H_V]), 2 * H_V,
-                         dev(conv_w), dev(dt), dev(ssm_a), dev(gamma), EPS, y, H_V * S, q8, H_V * S // 32 * 36, H_K,
-                         H_V, ntok)
+    args = (bufs[0], bufs[1], bufs[2], bufs[3], sel, dq, QKVZ, dev(ab[:ntok * 2 * H_V]), 2 * H_V, dev(conv_w), dev(dt),
+            dev(ssm_a), dev(gamma), EPS, y, H_V * S, q8, H_V * S // 32 * 36, H_K, H_V, ntok)
+    if split:
+        xch = t.zeros(rmi.gdn_exchange_bytes(H_V), dtype=t.uint8, device="cuda:0")
+        rmi.gdn_layer_tokens_x(*args, xch)
+    else:
+        rmi.gdn_layer_tokens(*args)
     return dict(y=host(y), q8=host(q8), conv=host(dq), state=host(st_live), snap=host(st_other), hist=host(hi_live),
                 hsnap=host(hi_other))
 
 
-def test_gdn_two_tokens_match_oracle(orc, rmi):
+@pytest.mark.parametrize("split", [False, True])
+def test_gdn_two_tokens_match_oracle(orc, rmi, split):
     inp = make_inputs(orc)
     qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma = inp
-    r = run_layer(rmi, qkvz, ab, conv_w, expand_hist(hist), state, dt, ssm_a, gamma, ntok=2)
+    r = run_layer(rmi, qkvz, ab, conv_w, expand_hist(hist), state, dt, ssm_a, gamma, ntok=2, split=split)
     assert np.array_equal(r["conv"], qkvz[:2 * QKVZ]), "the layer call reads q|k|v|z only"
     ys, states, hists, convs = oracle_chain(orc, *inp)
     for t in range(2):
@@ -105,15 +111,17 @@ def test_gdn_two_tokens_match_oracle(orc, rmi):
     assert np.array_equal(r["hist"], expand_hist(hists[1]))
 
 
+@pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("sel_val", [0, 1])
-def test_gdn_two_tokens_bitwise_equal_sequential(orc, rmi, sel_val):
+def test_gdn_two_tokens_bitwise_equal_sequential(orc, rmi, sel_val, split):
     inp = make_inputs(orc, seed=400)
     qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma = inp
     hist = expand_hist(hist)
-    r2 = run_layer(rmi, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok=2, sel_val=sel_val)
-    a = run_layer(rmi, qkvz[:QKVZ], ab[:2 * H_V], conv_w, hist, state, dt, ssm_a, gamma, ntok=1, sel_val=sel_val)
+    r2 = run_layer(rmi, qkvz, ab, conv_w, hist, state, dt, ssm_a, gamma, ntok=2, sel_val=sel_val, split=split)
+    a = run_layer(rmi, qkvz[:QKVZ], ab[:2 * H_V], conv_w, hist, state, dt, ssm_a, gamma, ntok=1, sel_val=sel_val,
+                  split=split)
     b = run_layer(rmi, qkvz[QKVZ:], ab[2 * H_V:], conv_w, a["hist"], a["state"], dt, ssm_a, gamma, ntok=1,
-                  sel_val=sel_val)
+                  sel_val=sel_val, split=split)
     u = lambda v: np.asarray(v).view(np.uint32)  # noqa: E731
     assert np.array_equal(u(r2["y"][:H_V * S]), u(a["y"])) and np.array_equal(u(r2["y"][H_V * S:]), u(b["y"]))
     blk = H_V * S // 32 * 36
@@ -124,23 +132,38 @@ def test_gdn_two_tokens_bitwise_equal_sequential(orc, rmi, sel_val):
 
 
 def test_gdn_split_kernel_bitwise_equal_one_workgroup_kernel(orc, rmi):
-    """Decode / verify launches (1 and 2 tokens) run four workgroups per value head; a 3-token launch runs the
-    one-workgroup-per-head kernel the ingest chunks use.  Token by token the two give the same bits: y, Q8_1, the final
-    state and history.  No exchange between a head's workgroups ran out of its bounded wait."""
+    """The engine's decode / verify launches (1 and 2 tokens, gdn_layer_tokens_x) run four workgroups per value head;
+    a 3-token launch runs the one-workgroup-per-head kernel the ingest chunks use.  Token by token the two give the same
+    bits: y, Q8_1, the final state and history.  No exchange between a head's workgroups ran out of its bounded wait,
+    including on a buffer reused across launches of both token counts."""
     qkvz3 = orc.normal(3 * QKVZ, seed=700)
     ab3 = orc.normal(3 * 2 * H_V, seed=701)
     _, _, conv_w, hist, state, dt, ssm_a, gamma = make_inputs(orc, seed=702)
     hist = expand_hist(hist)
     before = rmi.gdn_exchange_timeouts()
     r3 = run_layer(rmi, qkvz3, ab3, conv_w, hist, state, dt, ssm_a, gamma, ntok=3)
-    a = run_layer(rmi, qkvz3[:2 * QKVZ], ab3[:4 * H_V], conv_w, hist, state, dt, ssm_a, gamma, ntok=2)
-    b = run_layer(rmi, qkvz3[2 * QKVZ:], ab3[4 * H_V:], conv_w, a["hist"], a["state"], dt, ssm_a, gamma, ntok=1)
+    a = run_layer(rmi, qkvz3[:2 * QKVZ], ab3[:4 * H_V], conv_w, hist, state, dt, ssm_a, gamma, ntok=2, split=True)
+    b = run_layer(rmi, qkvz3[2 * QKVZ:], ab3[4 * H_V:], conv_w, a["hist"], a["state"], dt, ssm_a, gamma, ntok=1,
+                  split=True)
     u = lambda v: np.asarray(v).view(np.uint32)  # noqa: E731
     n = H_V * S
     assert np.array_equal(u(r3["y"][:2 * n]), u(a["y"])) and np.array_equal(u(r3["y"][2 * n:]), u(b["y"]))
     blk = n // 32 * 36
     assert np.array_equal(r3["q8"][:2 * blk], a["q8"]) and np.array_equal(r3["q8"][2 * blk:], b["q8"])
     assert np.array_equal(u(r3["state"]), u(b["state"])) and np.array_equal(u(r3["hist"]), u(b["hist"]))
+    # one exchange buffer across launches of 1 and 2 tokens (the engine's use): epochs stay in step
+    t = torch()
+    xch = t.zeros(rmi.gdn_exchange_bytes(H_V), dtype=t.uint8, device="cuda:0")
+    st = [dev(state), t.zeros(S * H_V * S, device="cuda:0")]
+    hi = [dev(hist), t.zeros(H_V * 3 * S * 3, device="cuda:0")]
+    sel = dev(np.array([0], np.int32))
+    y = empty(2 * H_V * S)
+    q8 = empty(2 * H_V * S // 32 * 36, "uint8")
+    for ntok in (2, 1, 1, 2, 2, 1):
+        rmi.gdn_layer_tokens_x(st[0], st[1], hi[0], hi[1], sel, dev(qkvz3[:ntok * QKVZ]), QKVZ,
+                               dev(ab3[:ntok * 2 * H_V]), 2 * H_V, dev(conv_w), dev(dt), dev(ssm_a), dev(gamma), EPS, y,
+                               H_V * S, q8, H_V * S // 32 * 36, H_K, H_V, ntok, xch)
+    t.cuda.synchronize()
     assert rmi.gdn_exchange_timeouts() == before == 0
 
 
