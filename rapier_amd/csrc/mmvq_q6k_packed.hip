@@ -661,25 +661,32 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
 }
 
 // up||gate GEMV with the SwiGLU + Q8_1 epilogue, over a matrix packed in the SwiGLU row order (rows of 4096: two
-// chunks).  Workgroup g (4 waves) owns quads 16 g .. 16 g + 15 = gate and up rows of outputs 32 g .. 32 g + 31; wave w
-// takes quads 16 g + 4 w .. + 3 as the stream kernel takes its quads, two tiles ahead (same per-row arithmetic, so the
-// same row sums as the plain GEMV), parks the row sums in LDS, and one 32-lane group per column forms silu(gate) * up
-// and its Q8_1 block with the quantizer of swiglu_quant: bitwise the GEMV + swiglu_quant pair, one launch and no fp32
-// round trip.  Per launch at 24576 x 4096: 18.2 -> 16.5 us at two columns, 17.4 -> 15.5 us at one (8 waves of two
-// quads each: 17.4 us at two columns, one workgroup per CU at their register count).
+// chunks).  A 16-quad group holds the gate and up rows of 32 outputs; workgroup b (NW waves) owns GPW = NW QPW / 16
+// consecutive groups and wave w takes QPW of their quads as the stream kernel takes its quads, two tiles ahead (same
+// per-row arithmetic, so the same row sums as the plain GEMV), parks the row sums in LDS, and one 32-lane group per
+// (group, column) forms silu(gate) * up and its Q8_1 block with the quantizer of swiglu_quant: bitwise the GEMV +
+// swiglu_quant pair, one launch and no fp32 round trip.
+// The engine's shape runs 8 waves and two groups per workgroup: 192 workgroups at n_ff 12288, one per CU.  With one
+// group per 4-wave workgroup (384) half the CUs hold two, and the second's activation stage queues behind the first's
+// weight tiles in the CU's memory pipeline (per-wave clock stamps: stage at 5.3 us against 1.6 us, its waves last to
+// finish): 24576 x 4096 at two columns 17.2 -> 16.0 us.  Deeper prefetch (3 or 4 tiles ahead) and 16 waves of two
+// quads were slower (17.2, 18.4, 29.6 us).
 // INV: the input is a folded norm's Q8_1(x * w); the gate and up row sums are scaled by inv before the SwiGLU.
-template <int NCOLS, bool INV = false>
-__global__ __launch_bounds__(256) void q6k_packed_swiglu(const uint8_t* __restrict__ wp, const uint8_t* __restrict__ x,
-                                                         uint8_t* __restrict__ out, int n_in, int ff, Fold fold) {
-    constexpr int NW = 4, QPW = 4, NCH = 2, T = QPW * NCH, PD = 2;
+template <int NCOLS, bool INV = false, int NW = 4, int QPW = 4, int PD = 2>
+__global__ __launch_bounds__(64 * NW) void q6k_packed_swiglu(const uint8_t* __restrict__ wp,
+                                                             const uint8_t* __restrict__ x, uint8_t* __restrict__ out,
+                                                             int n_in, int ff, Fold fold) {
+    constexpr int NCH = 2, T = QPW * NCH;
+    constexpr int GPW = NW * QPW / 16;   // 16-quad groups per workgroup
+    static_assert(GPW * 16 == NW * QPW && GPW >= 1, "whole groups per workgroup");
     extern __shared__ uint4 smem[];
     __shared__ float inv_red[INV ? NCOLS : 1][4];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int nbt = n_in / 32, xcs = NCH * kNB;
     uint4* lq = smem;
     uint4* lrec = smem + 2 * NCOLS * nbt;
-    float* lrow = reinterpret_cast<float*>(lrec + NCOLS * nbt);   // [col][64 rows of the group]
-    const int q0 = static_cast<int>(blockIdx.x) * 16 + QPW * w;
+    float* lrow = reinterpret_cast<float*>(lrec + NCOLS * nbt);   // [group][col][64 rows of the group]
+    const int q0 = static_cast<int>(blockIdx.x) * 16 * GPW + QPW * w;
 
     const int nblocks = NCOLS * nbt;   // <= 2 x 128: one block per lane at most
     static_assert(64 * NW >= 2 * 128, "one staged block per lane");
@@ -710,7 +717,9 @@ __global__ __launch_bounds__(256) void q6k_packed_swiglu(const uint8_t* __restri
         issue(i);
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (t < nblocks) stage_one(sv, t, nbt, lq, lrec);
+    // unconditional (lanes past the last block rewrite its slot with the same bytes): under a branch the compiler sinks
+    // the stage's loads into it, behind the first tiles, and the stage then waits for those
+    stage_one(sv, min(t, nblocks - 1), nbt, lq, lrec);
     if constexpr (INV) inv_reduce<NCOLS>(pv, fold, n_in, t, inv_red);
     __syncthreads();
     float inv[NCOLS];
@@ -736,21 +745,23 @@ __global__ __launch_bounds__(256) void q6k_packed_swiglu(const uint8_t* __restri
             __builtin_amdgcn_sched_barrier(0);
         }
         if (c == NCH - 1) {
+            const int lqd = QPW * w + j;   // the quad within the workgroup: group lqd / 16, rows 4 (lqd % 16) + r
 #pragma unroll
             for (int col = 0; col < NCOLS; ++col) {
                 float v = hb_sum(tot[col]);
                 if constexpr (INV) v *= inv[col];
                 tot[col] = 0.0f;
-                if (lane < kQuad) lrow[col * 64 + 4 * (QPW * w + j) + lane] = v;
+                if (lane < kQuad) lrow[((lqd >> 4) * NCOLS + col) * 64 + 4 * (lqd & 15) + lane] = v;
             }
         }
     }
     __syncthreads();
-    // wave 0: lanes 32 c .. 32 c + 31 quantize column c's 32 outputs of this group
-    if (w == 0 && (lane >> 5) < NCOLS) {
+    // wave g: lanes 32 c .. 32 c + 31 quantize column c's 32 outputs of group g
+    if (w < GPW && (lane >> 5) < NCOLS) {
         const int col = lane >> 5, i = lane & 31;
-        const float a = silu(lrow[col * 64 + i]) * lrow[col * 64 + 32 + i];
-        q8_1_store_lane(a, out + (static_cast<size_t>(col) * (ff / 32) + blockIdx.x) * kQ8_1Bytes);
+        const float* rows = lrow + (w * NCOLS + col) * 64;
+        const float a = silu(rows[i]) * rows[32 + i];
+        q8_1_store_lane(a, out + (static_cast<size_t>(col) * (ff / 32) + GPW * blockIdx.x + w) * kQ8_1Bytes);
     }
 }
 
@@ -1026,7 +1037,8 @@ int packed_grid(int nq) {
 //               12352 rows 11.35 -> 10.23 us (10.3 -> 9.4) (split, 4 waves); 24576 rows 16.6 -> 16.1 us
 //               (15.5 -> 14.8) and the 248320-row lm_head 123.9 -> 117.7 us (stream, two quads per wave, both tiles
 //               of the next quad issued while the current one is summed; three quads per wave: 16.2 us)
-//   n_in 8192:  4096 rows 9.15 -> 8.64 us (8.10 -> 7.78) (split, a quad's four chunks on two waves)
+//   n_in 8192:  4096 rows 9.15 -> 8.19 us (stream, one quad per wave, two tiles ahead: one workgroup per CU; a quad's
+//               four chunks on two waves of a split workgroup, two workgroups per CU, 8.64 us)
 //   n_in 12288: 4096 rows 11.8 -> 10.4 us (10.5 -> 9.6) (stream, one quad per wave, two tiles ahead; three ahead
 //               10.8 us, all six 13.2 us, two quads per wave 13.8 us, a quad on two waves 11.2 us)
 // RMI_PACKED_KERNEL=loop runs the loop kernel for every shape.
@@ -1047,7 +1059,7 @@ PackedCfg packed_cfg(int n_in, int n_out, int ncols) {
         if (nq <= 4096) return {PackedCfg::kSplit, 1, 4};
         return {PackedCfg::kStream, 0, 0};
     }
-    if (nch == 4) return {PackedCfg::kSplit, 2, 4};
+    if (nch == 4) return {PackedCfg::kStream, 0, 0};
     if (nch == 6) return {PackedCfg::kStream, 0, 0};
     return {PackedCfg::kLoop, 0, 0};
 }
@@ -1085,6 +1097,8 @@ void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* r
         if (c.kind == PackedCfg::kStream) {
             if (n_in / kChunkElems == 2)
                 return launch_stream<NCOLS, RES, 2, 2, 4, 2, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
+            if (n_in / kChunkElems == 4)
+                return launch_stream<NCOLS, RES, 4, 1, 4, 2, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
             return launch_stream<NCOLS, RES, 6, 1, 4, 2, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
         }
         if (c.kind == PackedCfg::kSplit) {
@@ -1249,15 +1263,20 @@ int swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_
     const auto* x = static_cast<const uint8_t*>(x_q8_1);
     auto* y = static_cast<uint8_t*>(y_q8_1);
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const size_t lds = static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(ncols) * 64 * 4;
-    const dim3 grid(n_ff / 32), block(256);
     const Fold f = fold ? *fold : Fold{};
+    // two 32-output groups per 8-wave workgroup (192 workgroups at n_ff 12288: one per CU) when n_ff allows, else one
+    // per 4-wave workgroup
+    auto go = [&](auto kern, int gpw, int nw) {
+        const size_t lds = static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(gpw) * ncols * 64 * 4;
+        hipLaunchKernelGGL(kern, dim3(n_ff / 32 / gpw), dim3(64 * nw), lds, s, wp, x, y, n_in, n_ff, f);
+    };
+    const bool two = n_ff % 64 == 0;
     if (ncols == 1) {
-        if (fold) hipLaunchKernelGGL((q6k_packed_swiglu<1, true>), grid, block, lds, s, wp, x, y, n_in, n_ff, f);
-        else hipLaunchKernelGGL((q6k_packed_swiglu<1>), grid, block, lds, s, wp, x, y, n_in, n_ff, f);
+        if (two) fold ? go(q6k_packed_swiglu<1, true, 8, 4>, 2, 8) : go(q6k_packed_swiglu<1, false, 8, 4>, 2, 8);
+        else fold ? go(q6k_packed_swiglu<1, true>, 1, 4) : go(q6k_packed_swiglu<1>, 1, 4);
     } else {
-        if (fold) hipLaunchKernelGGL((q6k_packed_swiglu<2, true>), grid, block, lds, s, wp, x, y, n_in, n_ff, f);
-        else hipLaunchKernelGGL((q6k_packed_swiglu<2>), grid, block, lds, s, wp, x, y, n_in, n_ff, f);
+        if (two) fold ? go(q6k_packed_swiglu<2, true, 8, 4>, 2, 8) : go(q6k_packed_swiglu<2, false, 8, 4>, 2, 8);
+        else fold ? go(q6k_packed_swiglu<2, true>, 1, 4) : go(q6k_packed_swiglu<2>, 1, 4);
     }
     return launch_status("q6_k_swiglu_packed");
 }
