@@ -562,14 +562,10 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
             hist[3 * ch + 2] = x[0];
         }
     };
-    if (part == 0) {
-        put_hist(chq, hq[sb], qx);
-        put_hist(chk, hk[sb], kx);
-    }
-    if (vlane) put_hist(chv, hv[sb], vx);
     __syncthreads();
 
     float occ[NT];
+    float s0[SNAP ? RPG : 1];   // the state after token 0 (stored with the others after the exchange)
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const float g = gbt[t][0], beta = gbt[t][1];
@@ -589,7 +585,7 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
         if constexpr (SNAP) {
             if (t == 0) {
 #pragma unroll
-                for (int r = 0; r < RPG; ++r) __builtin_nontemporal_store(s[r], snap + base + r * row_stride);
+                for (int r = 0; r < RPG; ++r) s0[r] = s[r];
             }
         }
         const float ss = group_sum<16>(oc * oc);
@@ -597,17 +593,33 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
         occ[t] = oc;
     }
     __syncthreads();
-    // independent of the other parts: the final state goes out and the output gate factor is formed while the
-    // exchange is in flight
+    // Every global store of the launch (history, the state after token 0, the final state) is issued after the
+    // exchange's loads: stores count in the wave's vector memory counter, so a load issued behind them waits for
+    // their completion, a memory round trip.  The counter is per wave: wave 1, which makes no exchange loads, stores
+    // (and publishes) at once.
+    auto put_all = [&]() {
+        if (part == 0) {
+            put_hist(chq, hq[sb], qx);
+            put_hist(chk, hk[sb], kx);
+        }
+        if (vlane) put_hist(chv, hv[sb], vx);
+        if constexpr (SNAP) {
 #pragma unroll
-    for (int r = 0; r < RPG; ++r) __builtin_nontemporal_store(s[r], state + base + r * row_stride);
-    // the exchange: publish this part's wave sums, gather the other parts' (wave 0, lane i: part i / (2 NT), token
-    // (i / 2) % NT, wave i % 2)
+            for (int r = 0; r < RPG; ++r) __builtin_nontemporal_store(s0[r], snap + base + r * row_stride);
+        }
+#pragma unroll
+        for (int r = 0; r < RPG; ++r) __builtin_nontemporal_store(s[r], state + base + r * row_stride);
+    };
+    // the exchange: wave 1 publishes this part's wave sums and then stores, wave 0 gathers the other parts' (lane i:
+    // part i / (2 NT), token (i / 2) % NT, wave i % 2) and then stores
     const unsigned long long tag = ((own0 >> 32) + 1ull) << 32;   // this launch's epoch
-    if (threadIdx.x < 4) {   // both tokens' words (a 1-token launch writes token 1's words too, so all stay in step)
-        const int t = threadIdx.x >> 1, w = threadIdx.x & 1;
-        __hip_atomic_store(xh + (part * 2 + t) * 2 + w, tag | __float_as_uint(wsum[t < NT ? t : 0][w]),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wv == 1) {
+        if (ln < 4) {   // both tokens' words (a 1-token launch writes token 1's words too, so all stay in step)
+            const int tt = ln >> 1, ww = ln & 1;
+            __hip_atomic_store(xh + (part * 2 + tt) * 2 + ww, tag | __float_as_uint(wsum[tt < NT ? tt : 0][ww]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        put_all();
     }
     if (wv == 0) {
         const int pp = ln / (2 * NT), t = (ln >> 1) % NT, w = ln & 1;
@@ -622,6 +634,7 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
         }
         if (n == (1 << 20) && ln == 0) atomicAdd(&gdn_xch_timeouts, 1u);
         if (ln < kParts * 2 * NT) allw[t][2 * pp + w] = other ? __uint_as_float(static_cast<uint32_t>(v)) : wsum[t][w];
+        put_all();
     }
     __syncthreads();
 #pragma unroll
