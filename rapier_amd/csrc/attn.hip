@@ -365,10 +365,17 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
 }
 
 // ---- merge + sigmoid gate + Q8_1 ---------------------------------------------------------------------------------------
-// Two passes over the query's chunks 0..last: (1) the 256 lanes load every chunk's (m, l) in parallel, M = max m,
-// weights w_c = exp(m_c - M) to LDS, L = sum l_c w_c (lane-strided partial sums, butterfly, waves in order);
-// (2) lane d accumulates O = sum_c w_c o_c[d] in chunk order with the loads issued 8 chunks ahead.
+// Workgroup (token, head, quarter) owns 64 of the head's 256 output dims.  (1) the 256 lanes load every chunk's (m, l)
+// in parallel, M = max m, weights w_c = exp(m_c - M) to LDS, L = sum l_c w_c (lane-strided partial sums, butterfly,
+// waves in order); (2) wave g sums O_g = sum w_c o_c[d] over the chunks c = g mod 4 in ascending order, every load of
+// a batch of 16 issued before the first is used, and O = ((O_0 + O_1) + O_2) + O_3.  The order depends only on the
+// chunk count, so a verify column is bitwise its single-query launch.  Four workgroups per head put the record reads
+// (1 KB per chunk and query) on 4x the CUs with every load of a lane in flight at once: at 64K (129 chunks) the
+// previous form, one workgroup per head walking the chunks 8 loads ahead, was a chain of 16 dependent reads.
 constexpr int kMaxChunks = 2048;
+constexpr int kMergeParts = 4;                 // workgroups per (token, head)
+constexpr int kMergeDims = HD / kMergeParts;   // 64 dims each: two Q8_1 blocks
+constexpr int kMergeBatch = 16;                // record loads in flight per lane
 
 __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__ ws, int slot_stride,
                                                        const float* __restrict__ gsrc, int gstride,
@@ -377,68 +384,70 @@ __global__ __launch_bounds__(HD) void gqa_merge_kernel(const float* __restrict__
                                                        int n_head, int n_kv, int chunk_len) {
     __shared__ float wts[kMaxChunks];
     __shared__ float red[4];
-    const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+    __shared__ float opart[4][kMergeDims];
+    const int t = blockIdx.x, h = blockIdx.y, part = blockIdx.z, tid = threadIdx.x;
+    const int lane = tid & 63, grp = tid >> 6;
+    const int d = kMergeDims * part + lane;   // this lane's output dim
     const int G = n_head / n_kv;
     const int kv = h / G, qv = t * G + (h - kv * G);
     const float g = gsrc[static_cast<size_t>(t) * gstride + h * 2 * HD + HD + d];   // in flight with pos
     const int nchunk = min((pos[0] + t) / chunk_len + 1, kMaxChunks);
     const size_t cstride = static_cast<size_t>(n_kv) * slot_stride * REC;
     const float* base = ws + (static_cast<size_t>(kv) * slot_stride + qv) * REC;
-    // in flight together before the first barrier: the lane's first (m, l) record and the first 8 chunks' o values
+    // in flight together before the first barrier: the lane's first (m, l) record and its group's first o values
     float m0 = 0.0f, l0 = 0.0f;
-    if (d < nchunk) {
-        m0 = base[d * cstride];
-        l0 = base[d * cstride + 1];
+    if (tid < nchunk) {
+        m0 = base[tid * cstride];
+        l0 = base[tid * cstride + 1];
     }
-    float oa[8];   // from clamped chunks (unconditional: a load under a branch gets a wait of its own); k < nchunk used
+    float oa[kMergeBatch];   // chunks grp + 4 k, clamped (unconditional: a load under a branch gets a wait of its own)
 #pragma unroll
-    for (int k = 0; k < 8; ++k) oa[k] = base[min(k, nchunk - 1) * cstride + 4 + d];
+    for (int k = 0; k < kMergeBatch; ++k) oa[k] = base[min(grp + 4 * k, nchunk - 1) * cstride + 4 + d];
     float mloc = -INFINITY;
-    if (d < nchunk) mloc = fmaxf(mloc, m0);
-    for (int c = d + HD; c < nchunk; c += HD) mloc = fmaxf(mloc, base[c * cstride]);
+    if (tid < nchunk) mloc = fmaxf(mloc, m0);
+    for (int c = tid + HD; c < nchunk; c += HD) mloc = fmaxf(mloc, base[c * cstride]);
     mloc = group_max<64>(mloc);
-    if ((d & 63) == 0) red[d >> 6] = mloc;
+    if ((tid & 63) == 0) red[tid >> 6] = mloc;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     float lloc = 0.0f;
-    if (d < nchunk) {
+    if (tid < nchunk) {
         const float w = expf(m0 - M);
-        wts[d] = w;
+        wts[tid] = w;
         lloc = __builtin_fmaf(l0, w, lloc);
     }
-    for (int c = d + HD; c < nchunk; c += HD) {
+    for (int c = tid + HD; c < nchunk; c += HD) {
         const float w = expf(base[c * cstride] - M);
         wts[c] = w;
         lloc = __builtin_fmaf(base[c * cstride + 1], w, lloc);
     }
     const float L = block_sum256(lloc, red);   // includes the barrier that publishes wts
-    // O over the chunks in order; each block of 8 o values is loaded while the previous block is summed
+    // O_grp over chunks grp, grp + 4, ... in ascending order, a batch of 16 loads in flight while the previous is summed
     float O = 0.0f;
-    if (nchunk < 8) {
+    for (int c0 = 0; 4 * c0 < nchunk; c0 += kMergeBatch) {
+        const bool more = 4 * (c0 + kMergeBatch) < nchunk;
+        float nx[kMergeBatch];
+        if (more) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            if (k < nchunk) O = __builtin_fmaf(wts[k], oa[k], O);
-    } else {
-        int c = 0;
-        for (; c + 8 <= nchunk; c += 8) {
-            const bool more = c + 16 <= nchunk;
-            float nx[8];
-            if (more) {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) nx[k] = base[(c + 8 + k) * cstride + 4 + d];
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) O = __builtin_fmaf(wts[c + k], oa[k], O);
-            if (more) {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) oa[k] = nx[k];
-            }
+            for (int k = 0; k < kMergeBatch; ++k)
+                nx[k] = base[min(grp + 4 * (c0 + kMergeBatch + k), nchunk - 1) * cstride + 4 + d];
         }
-        for (; c < nchunk; ++c) O = __builtin_fmaf(wts[c], base[c * cstride + 4 + d], O);
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k) {
+            const int c = grp + 4 * (c0 + k);
+            if (c < nchunk) O = __builtin_fmaf(wts[c], oa[k], O);
+        }
+        if (more) {
+#pragma unroll
+            for (int k = 0; k < kMergeBatch; ++k) oa[k] = nx[k];
+        }
     }
-    const float o = O / L;
-    const float v = o * sigmoid(g);
+    opart[grp][lane] = O;
+    __syncthreads();
+    if (grp != 0) return;
+    const float o = ((opart[0][lane] + opart[1][lane]) + opart[2][lane]) + opart[3][lane];
+    const float v = (o / L) * sigmoid(g);
     if (y) y[static_cast<size_t>(t) * y_stride + h * HD + d] = v;
     if (q8) q8_1_store_lane(v, q8 + static_cast<size_t>(t) * q8_stride + (h * (HD / 32) + d / 32) * kQ8_1Bytes);
 }
@@ -491,7 +500,7 @@ int flash_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache,
     const int groups = (ntok * (n_head / n_kv) + SLOTS - 1) / SLOTS;
     hipLaunchKernelGGL(gqa_partial_kernel, dim3(nchunks * n_kv, 1, groups), dim3(256), 0, s, q, kcache, vcache, pos, ws,
                        slot_stride, n_head, n_kv, ntok, nsub, max_ctx, scale);
-    hipLaunchKernelGGL(gqa_merge_kernel, dim3(ntok, n_head), dim3(HD), 0, s, ws, slot_stride, gate_src, gate_stride,
+    hipLaunchKernelGGL(gqa_merge_kernel, dim3(ntok, n_head, kMergeParts), dim3(HD), 0, s, ws, slot_stride, gate_src, gate_stride,
                        pos, y, y_stride, q8, q8_stride, n_head, n_kv, SUB * nsub);
     return launch_status("gqa_flash_decode");
 }
