@@ -158,14 +158,19 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
     const int slot = s0 + (l16 & 7);   // query slot t * G + gh of this lane's MFMA column / row
     const bool lo_row = l16 >= 8;
 
-    // the query rows do not depend on the position: their loads go out together with pos[0]
-    float4 qraw[16];   // [2 sp + hlf]: dims 32 sp + 8 g4 + 4 hlf + [0, 4) of query slot `slot`
-    {
-        const bool ok = slot < nq;
-        const int t = ok ? slot / G : 0, gh = ok ? slot - (slot / G) * G : 0;
-        const float4* q = reinterpret_cast<const float4*>(qbuf + (static_cast<size_t>(t) * n_head + kv * G + gh) * HD);
+    // The workgroup's 8 query rows (8 KB) are staged once in the K tile area: loaded by every wave (a row read per lane
+    // by each wave would put 16 KB per wave of cache hits ahead of the K / V stream in the CU's memory pipeline).
+    // They do not depend on the position: their loads go out together with pos[0].
+    float4* qst = reinterpret_cast<float4*>(tiles);   // [slot within the group][64 float4]
+    float4 qin[2];   // float4s tid and tid + 256 of the group's rows, written to the stage after the K / V loads issue
 #pragma unroll
-        for (int i = 0; i < 16; ++i) qraw[i] = ok ? q[8 * (i >> 1) + 2 * g4 + (i & 1)] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < 2; ++i) {
+        const int f = static_cast<int>(threadIdx.x) + 256 * i, qs = s0 + (f >> 6);
+        const bool ok = qs < nq;
+        const int t = ok ? qs / G : 0, gh = ok ? qs - (qs / G) * G : 0;
+        const float4* q = reinterpret_cast<const float4*>(qbuf + (static_cast<size_t>(t) * n_head + kv * G + gh) * HD);
+        const float4 v = q[f & 63];   // unconditional (a load under a branch gets a wait of its own)
+        qin[i] = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     const int p0 = pos[0];
     const int p_last = p0 + (min(s0 + SLOTS, nq) - 1) / G;   // the last position this group's slots see
@@ -208,12 +213,16 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
         set_u4(vnext, 2 * j, load_kv(vr));
         set_u4(vnext, 2 * j + 1, load_kv(vr + 128));
     }
-    // B operand of the score MFMAs, from the query rows loaded above: step 2 sp + hlf covers dims
+    // B operand of the score MFMAs, from the staged query rows: step 2 sp + hlf covers dims
     // 32 sp + 8 g4 + 4 hlf + [0, 4); rows 0-7 the fp16 hi part, rows 8-15 the fp16 lo part of the same slot
+#pragma unroll
+    for (int i = 0; i < 2; ++i) qst[static_cast<int>(threadIdx.x) + 256 * i] = qin[i];
+    __syncthreads();   // the staged rows are complete
     half4 qb[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const float xs[4] = {qraw[i].x, qraw[i].y, qraw[i].z, qraw[i].w};
+        const float4 qr = qst[(l16 & 7) * 64 + 8 * (i >> 1) + 2 * g4 + (i & 1)];
+        const float xs[4] = {qr.x, qr.y, qr.z, qr.w};
         half4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -222,6 +231,7 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
         }
         qb[i] = v;
     }
+    __syncthreads();   // every wave has its query rows: the K tiles may overwrite the stage
     for (int s = 0; s < nsteps; ++s) {
         const int sb = wbase + s * STEP;
         uint4 vreg[8];
@@ -306,6 +316,15 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
                 oacc[dg][2 * w + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, b_odd, oacc[dg][2 * w + 1], 0, 0, 0);
             }
         }
+    }
+    // A use of the first step's K / V rows on the path that runs no step: with their only uses inside the loop the
+    // compiler sinks the loads into its preheader, behind the wait for the query rows, and no K / V load would go out
+    // before the queries arrive.
+    if (nsteps == 0) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) x ^= kreg[j] ^ vnext[j];
+        asm volatile("" ::"v"(x));
     }
     // hi rows + lo rows: lanes g4 < 2 end with o[slot 4 g4 + r][128 dg + 8 l16 + e]
 #pragma unroll
