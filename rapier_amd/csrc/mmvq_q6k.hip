@@ -496,6 +496,12 @@ bool full_row(int n_in) {
 template <int NCOLS, bool RES>
 void launch_cols(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in, int n_out,
                  hipStream_t s) {
+    // rows of 4096 / 8192 / 12288: the stream kernel (every column, including the passes of ncols > 4, bitwise its
+    // one-column result and the packed kernels'); RMI_GGUF_STREAM=0 measures the tiled kernel instead
+    static const bool stream_on = env_int("RMI_GGUF_STREAM", 1) != 0;
+    if (NCOLS <= 4 && stream_on &&
+        gguf_stream_gemv(w, x, y, RES ? res : nullptr, RES ? partials : nullptr, n_in, n_out, NCOLS, s) == RMI_OK)
+        return;
     const TileCfg cfg = pick_cfg(n_in, n_out, w);
     const bool full = full_row(n_in);
     if (cfg.rows == 16) {

@@ -660,6 +660,157 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
     }
 }
 
+// ---- the same stream kernel over the GGUF layout (the drop-in entry points' weights) ------------------------------
+// A wave tile is the quad's 4 rows x 8 blocks of one chunk: four 1680-byte row segments, 16-byte aligned when the row
+// length is a multiple of 2048 (rows of 8k blocks are 1680k bytes).  The lane loads 7 of the tile's 420 16-byte units
+// (unit i = lane + 64 m: row i / 105, unit i % 105), fully coalesced per row segment, two tiles ahead in registers.
+// At its step the wave parks the tile in its own LDS rows (no workgroup barrier: only the wave reads them) and each
+// lane reads its half-block (row lane % 4, half-block lane / 4, the packed kernel's ownership) back as aligned dwords
+// realigned with v_alignbyte for the odd blocks' 2-byte offset.  The per-lane arithmetic is step_acc's, so the result
+// is bitwise the packed kernels' (and the 16-row tiled kernel's) on the same matrix.
+constexpr int kGgufUnits = 4 * kChunkBlocks * kQ6KBytes / 16;   // 420 16-byte units per wave tile
+constexpr int kGgufRowUnits = kGgufUnits / 4;                   // 105 per row segment
+constexpr int kGgufLoads = (kGgufUnits + 63) / 64;              // 7 per lane
+constexpr int kGgufRowDw = kChunkBlocks * kQ6KBytes / 4 + 4;    // 424 dwords per parked row (16-byte multiple)
+constexpr int kGgufWaveDw = 4 * kGgufRowDw;                     // 6784 bytes of LDS per wave
+
+struct GTile {
+    u32x4 u[kGgufLoads];
+};
+
+__device__ __forceinline__ void lds_wave_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// pin_tile_after for a raw GGUF tile: its wait covers this tile and the loads issued before it only, and the previous
+// step's arithmetic stays above it
+template <int NCOLS>
+__device__ __forceinline__ void pin_gtile_after(GTile& g, float (&tot)[NCOLS]) {
+#pragma unroll
+    for (int c = 0; c < NCOLS; ++c) asm volatile("" : "+v"(tot[c])::"memory");
+    asm volatile("" : "+v"(g.u[0]), "+v"(g.u[1]), "+v"(g.u[2]), "+v"(g.u[3]), "+v"(g.u[4]), "+v"(g.u[5]),
+                 "+v"(g.u[6])::"memory");
+}
+
+// the lane's half-block of a parked tile as the packed kernel's registers
+__device__ __forceinline__ void gguf_unpack(const GTile& g, uint32_t* lw, int lane, WTile& wt) {
+#pragma unroll
+    for (int m = 0; m < kGgufLoads; ++m) {
+        const int i = min(lane + 64 * m, kGgufUnits - 1);   // lanes past the last unit rewrite it with the same bytes
+        const int r = i / kGgufRowUnits, u = i - r * kGgufRowUnits;
+        *reinterpret_cast<u32x4*>(lw + r * kGgufRowDw + 4 * u) = g.u[m];
+    }
+    lds_wave_fence();
+    const int r = lane & 3, hb = lane >> 2, b = hb >> 1, n = hb & 1;
+    const int row = r * kGgufRowDw * 4 + b * kQ6KBytes;   // byte offset of the lane's block in the parked rows
+    const int mis = row & 3;                              // 0, or 2 for odd blocks
+    const int q0 = (row + 64 * n) >> 2, h0 = (row + 128 + 32 * n) >> 2, s0 = (row + 192 + 8 * n) >> 2;
+    uint32_t tq[17], th[9], ts[3];
+#pragma unroll
+    for (int k = 0; k < 17; ++k) tq[k] = lw[q0 + k];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) th[k] = lw[h0 + k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) ts[k] = lw[s0 + k];
+    const int dbyte = row + 208;
+    const uint32_t dw = lw[dbyte >> 2];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) wt.ql[k >> 2][k & 3] = __builtin_amdgcn_alignbyte(tq[k + 1], tq[k], mis);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) wt.qh[k >> 2][k & 3] = __builtin_amdgcn_alignbyte(th[k + 1], th[k], mis);
+    wt.sc.x = __builtin_amdgcn_alignbyte(ts[1], ts[0], mis);
+    wt.sc.y = __builtin_amdgcn_alignbyte(ts[2], ts[1], mis);
+    const uint32_t d16 = (dw >> (8 * (dbyte & 3))) & 0xffffu;
+    wt.d = (lane & 1) ? d16 << 16 : d16;   // where step_acc takes the lane's scale from
+}
+
+template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD>
+__global__ __launch_bounds__(64 * NW) void q6k_gguf_stream(const uint8_t* __restrict__ w, const uint8_t* __restrict__ x,
+                                                           float* y, const float* res, float* partials, int n_in,
+                                                           int n_out) {
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int nbt = n_in / 32, xcs = NCH * kNB;
+    uint4* lq = smem;
+    uint4* lrec = smem + 2 * NCOLS * nbt;
+    uint32_t* lw = reinterpret_cast<uint32_t*>(lrec + NCOLS * nbt) + (t >> 6) * kGgufWaveDw;
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    const int G = static_cast<int>(gridDim.x) * NW;
+    const int q0 = static_cast<int>(blockIdx.x) * NW + (t >> 6);
+    const size_t rowbytes = static_cast<size_t>(n_in / 256) * kQ6KBytes;
+
+    constexpr int SB = 4;
+    const int nblocks = NCOLS * nbt;
+    uint32_t sv[SB][9];
+#pragma unroll
+    for (int b = 0; b < SB; ++b) {
+        const int J = min(t + b * 64 * NW, nblocks - 1);
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) sv[b][i] = p[i];
+    }
+    float rv[QPW][NCOLS];
+    if constexpr (RES) {
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) load_residual<NCOLS>(rv[j], res, lane, min(q0 + j * G, nq - 1), n_out);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // tile i = (quad j = i / NCH, chunk i % NCH); rows past the last are read from the last row and discarded
+    constexpr int T = QPW * NCH;
+    GTile buf[T];
+    auto issue = [&](int i) {
+        const int j = i / NCH, c = i - j * NCH;
+        const int row0 = kQuad * min(q0 + j * G, nq - 1);
+#pragma unroll
+        for (int m = 0; m < kGgufLoads; ++m) {
+            const int u = min(lane + 64 * m, kGgufUnits - 1);
+            const int r = u / kGgufRowUnits, uu = u - r * kGgufRowUnits;
+            const uint8_t* p = w + static_cast<size_t>(min(row0 + r, n_out - 1)) * rowbytes +
+                               static_cast<size_t>(c) * (kChunkBlocks * kQ6KBytes) + 16 * uu;
+            buf[i].u[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < PD && i < T; ++i) {
+        issue(i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int b = 0; b < SB; ++b) {
+        const int J = t + b * 64 * NW;
+        if (J < nblocks) stage_one(sv[b], J, nbt, lq, lrec);
+    }
+    for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
+        uint32_t wv[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) wv[i] = p[i];
+        stage_one(wv, J, nbt, lq, lrec);
+    }
+    __syncthreads();
+
+    float tot[NCOLS];
+#pragma unroll
+    for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+        const int j = i / NCH, c = i - (i / NCH) * NCH;
+        pin_gtile_after<NCOLS>(buf[i], tot);
+        WTile wt;
+        gguf_unpack(buf[i], lw, lane, wt);
+        float acc[NCOLS];
+        const float d = step_acc<NCOLS>(wt, lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, acc);
+#pragma unroll
+        for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
+        if (i + PD < T) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(i + PD);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (c == NCH - 1 && q0 + j * G < nq)
+            quad_epilogue<NCOLS, RES>(tot, lane, q0 + j * G, y, res, partials, n_out, rv[j]);
+    }
+}
+
 // up||gate GEMV with the SwiGLU + Q8_1 epilogue, over a matrix packed in the SwiGLU row order (rows of 4096: two
 // chunks).  A 16-quad group holds the gate and up rows of 32 outputs; workgroup b (NW waves) owns GPW = NW QPW / 16
 // consecutive groups and wave w takes QPW of their quads as the stream kernel takes its quads, two tiles ahead (same
@@ -1214,6 +1365,61 @@ int validate_packed(const void* wp, const void* x, const float* y, int n_in, int
 }  // namespace rmi
 
 using namespace rmi;
+
+namespace rmi {
+namespace {
+template <int NCOLS, bool RES, int NCH, int QPW, int NW>
+void launch_gguf(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in, int n_out,
+                 hipStream_t s) {
+    constexpr int PD = 2;
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    const size_t lds = static_cast<size_t>(NCOLS) * (n_in / 32) * 48 + static_cast<size_t>(NW) * kGgufWaveDw * 4;
+    hipLaunchKernelGGL((q6k_gguf_stream<NCOLS, RES, NCH, QPW, NW, PD>), dim3((nq + NW * QPW - 1) / (NW * QPW)),
+                       dim3(64 * NW), lds, s, w, x, y, res, partials, n_in, n_out);
+}
+
+// One quad per wave (two tiles in flight), 4-wave workgroups, 8 above 4096 quads.  Measured at two columns (one for
+// the config-1 shape) against the 16-row / 8-row tiled kernel: up||gate 24576 x 4096 18.8 us (tiled 19.9-21.3),
+// FFN down 4096 x 12288 + residual 12.2 us (13.7), 12288 x 4096 + residual 10.3 us (10.8-11.0).  Two or three quads
+// per wave were slower on every shape (with fewer waves the wave's LDS round trips per tile are not hidden).
+template <int NCOLS, bool RES, int NCH>
+void gguf_nch(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in, int n_out,
+              hipStream_t s) {
+    if ((n_out + kQuad - 1) / kQuad > 4096) return launch_gguf<NCOLS, RES, NCH, 1, 8>(w, x, y, res, partials, n_in, n_out, s);
+    return launch_gguf<NCOLS, RES, NCH, 1, 4>(w, x, y, res, partials, n_in, n_out, s);
+}
+
+template <int NCOLS, bool RES>
+int gguf_cols(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in, int n_out,
+              hipStream_t s) {
+    const int nch = n_in / kChunkElems;
+    if (nch == 2) gguf_nch<NCOLS, RES, 2>(w, x, y, res, partials, n_in, n_out, s);
+    else if (nch == 4) gguf_nch<NCOLS, RES, 4>(w, x, y, res, partials, n_in, n_out, s);
+    else gguf_nch<NCOLS, RES, 6>(w, x, y, res, partials, n_in, n_out, s);
+    return RMI_OK;
+}
+}  // namespace
+
+// The drop-in entry points' stream kernel over GGUF-layout weights: rows of 2, 4 or 6 chunks (4096, 8192, 12288
+// elements), one to four columns, a 16-byte aligned matrix.  Returns -1, launching nothing, for any other shape.
+int gguf_stream_gemv(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
+                     int n_out, int ncols, hipStream_t s) {
+    const int nch = n_in / kChunkElems;
+    if (n_in % kChunkElems || (reinterpret_cast<uintptr_t>(w) & 15u) || ncols < 1 || ncols > 4 ||
+        !(nch == 2 || nch == 4 || nch == 6))
+        return -1;
+    switch (ncols) {
+        case 1: return res ? gguf_cols<1, true>(w, x, y, res, partials, n_in, n_out, s)
+                           : gguf_cols<1, false>(w, x, y, res, partials, n_in, n_out, s);
+        case 2: return res ? gguf_cols<2, true>(w, x, y, res, partials, n_in, n_out, s)
+                           : gguf_cols<2, false>(w, x, y, res, partials, n_in, n_out, s);
+        case 3: return res ? gguf_cols<3, true>(w, x, y, res, partials, n_in, n_out, s)
+                           : gguf_cols<3, false>(w, x, y, res, partials, n_in, n_out, s);
+        default: return res ? gguf_cols<4, true>(w, x, y, res, partials, n_in, n_out, s)
+                            : gguf_cols<4, false>(w, x, y, res, partials, n_in, n_out, s);
+    }
+}
+}  // namespace rmi
 
 extern "C" size_t rmi_q6_k_packed_bytes(int n_in, int n_out) {
     if (n_in <= 0 || n_in % kChunkElems != 0 || n_out <= 0) {

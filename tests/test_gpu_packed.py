@@ -1,8 +1,9 @@
 """GPU parity of the packed Q6_K GEMV (caller-owned wave-tiled copy of the weights).
 
 Bars: within 1e-3 relative of the oracle's fp64 GEMV (|err| <= 1e-3 |ref| + 1e-5 max|ref|); bitwise equal to the
-16-row tiled GEMV on the GGUF layout where the dispatcher picks 16-row tiles (same lane ownership and reduction
-tree); ncols = 2 columns bitwise equal to ncols = 1; residual variant bitwise plain + res with partials = sum of the
+drop-in entry points on the GGUF layout, which run the GGUF stream kernel at rows of 4096 / 8192 / 12288 and 16-row
+tiles where the dispatcher picks them (same lane ownership and reduction tree); ncols = 2 columns bitwise equal to
+ncols = 1; residual variant bitwise plain + res with partials = sum of the
 4 rows' squares in row order (src/test_res.cpp:57-112).  Ragged n_out pads the last 4-row group with zeros.
 At one or two columns, n_in = 4096 and 8192 run the split kernel (up to 16384 rows at 4096) or the stream kernel
 (more rows, and n_in = 12288); the other shapes the pipelined loop kernel.  All must give the same bits.
@@ -61,7 +62,7 @@ def test_packed_bitwise_equals_16_row_tiles(orc, rmi, n_in, n_out):
     wp = packed(rmi, wd, n_in, n_out)
     yp, yt = empty(2 * n_out), empty(2 * n_out)
     rmi.native_q6_k_mmvq_packed(wp, xd, yp, n_in, n_out, 2)
-    rmi.native_q6_k_mmvq(wd, xd, yt, n_in, n_out, 2)     # 16-row tiles for these shapes
+    rmi.native_q6_k_mmvq(wd, xd, yt, n_in, n_out, 2)     # the GGUF stream kernel (n_in 4096), 16-row tiles (2048)
     assert np.array_equal(host(yp).view(np.uint32), host(yt).view(np.uint32))
 
 
@@ -200,3 +201,37 @@ def test_fused_swiglu_gemv_bitwise_equals_gemv_then_swiglu(orc, rmi, ff, ncols):
     q = blk[:, :, 4:].view(np.int8).astype(np.float64)
     deq = (q * d[..., None]).reshape(ncols, ff)
     assert np.all(np.abs(deq - a) <= 0.51 * np.repeat(d, 32, axis=1) + 1e-3 * np.abs(a) + 1e-6)
+
+
+# the drop-in GGUF-layout entry points run the GGUF stream kernel at rows of 4096 / 8192 / 12288 (ragged n_out
+# included) for 1-4 columns and in passes of 4 above; (2048, 1001) keeps the 16-row tiled kernel
+@pytest.mark.parametrize("n_in,n_out", [(4096, 12352), (4096, 1001), (8192, 4096), (12288, 4096), (12288, 1001),
+                                        (4096, 24576), (2048, 1001)])
+@pytest.mark.parametrize("ncols", [1, 2, 3, 5])
+def test_gguf_entry_points_bitwise_equal_packed(orc, rmi, n_in, n_out, ncols):
+    """every column of rmi_native_q6_k_mmvq / _res_n on GGUF blocks is bitwise the packed kernel's single-column
+    result on the same matrix, and the residual variant is bitwise plain + res with the packed kernel's partials"""
+    w = orc.gen_q6k(n_out, n_in, seed=3 * n_in + n_out + ncols)
+    xq = orc.quantize_q8_1(orc.normal(ncols * n_in, seed=n_out + 5 * ncols), n_in, ncols)
+    res = orc.normal(ncols * n_out, seed=n_in + 17)
+    wd, xd = dev(w), dev(xq)
+    wp = packed(rmi, wd, n_in, n_out)
+    y = empty(ncols * n_out)
+    rmi.native_q6_k_mmvq(wd, xd, y, n_in, n_out, ncols)
+    yr = dev(res.copy())                                  # y aliases res, as the reference engine calls it
+    np_ = (n_out + 3) // 4
+    part = empty(ncols * np_)
+    rmi.native_q6_k_mmvq_res_n(wd, xd, yr, yr, part, n_in, n_out, ncols)
+    yh, yrh, ph = host(y), host(yr), host(part)
+    xcol = (n_in // 32) * 36
+    for c in range(ncols):
+        xc = dev(xq[c * xcol:(c + 1) * xcol])
+        y1 = empty(n_out)
+        rmi.native_q6_k_mmvq_packed(wp, xc, y1, n_in, n_out, 1)
+        y1r = dev(res[c * n_out:(c + 1) * n_out].copy())
+        p1 = empty(np_)
+        rmi.native_q6_k_mmvq_packed_res_n(wp, xc, y1r, y1r, p1, n_in, n_out, 1)
+        sl = slice(c * n_out, (c + 1) * n_out)
+        assert np.array_equal(yh[sl].view(np.uint32), host(y1).view(np.uint32)), f"plain column {c}"
+        assert np.array_equal(yrh[sl].view(np.uint32), host(y1r).view(np.uint32)), f"residual column {c}"
+        assert np.array_equal(ph[c * np_:(c + 1) * np_].view(np.uint32), host(p1).view(np.uint32)), f"partials {c}"
