@@ -51,8 +51,8 @@ UGS_BYTES = q6_bytes(UG_ROWS, UG_IN) + 2 * (UG_IN // 32) * 36 + 2 * (UG_ROWS // 
 # over `bench.py --workload traffic_probe` (profiles/gemv_up_gate_swiglu_traffic.md).  On gfx950 a TCC_EA0_RDREQ that is
 # not a 32-byte request moves 128 bytes (the same process's copy kernel reads 256 MiB in 2,097,395 requests), and a
 # TCC_EA0_WRREQ is 64 bytes (TCC_EA0_WRREQ_64B) or 32.
-PMC_UG_RDREQ, PMC_UG_RDREQ_32B = 647995, 0
-PMC_UG_WRREQ, PMC_UG_WRREQ_64B = 1152, 384
+PMC_UG_RDREQ, PMC_UG_RDREQ_32B = 648264, 0
+PMC_UG_WRREQ, PMC_UG_WRREQ_64B = 768, 384
 
 
 def ea_bytes(rdreq, rdreq_32b, wrreq, wrreq_64b):
@@ -60,7 +60,7 @@ def ea_bytes(rdreq, rdreq_32b, wrreq, wrreq_64b):
     return 128 * (rdreq - rdreq_32b) + 32 * rdreq_32b + 64 * wrreq_64b + 32 * (wrreq - wrreq_64b)
 
 
-UG_TRAFFIC_BYTES = ea_bytes(PMC_UG_RDREQ, PMC_UG_RDREQ_32B, PMC_UG_WRREQ, PMC_UG_WRREQ_64B)   # 82,992,512
+UG_TRAFFIC_BYTES = ea_bytes(PMC_UG_RDREQ, PMC_UG_RDREQ_32B, PMC_UG_WRREQ, PMC_UG_WRREQ_64B)   # 83,014,656
 
 
 def cpu_model():
@@ -261,8 +261,8 @@ def run_verify_gemv(args):
             "config1": c1,
         },
         "roofline": {
-            "kernel": "q6k_packed_swiglu<2> (up||gate 24576x4096 GEMV + SwiGLU + Q8_1, ncols=2, SwiGLU-packed "
-                      "wave-tile layout)",
+            "kernel": "q6k_packed_swiglu<2, false, 8, 4, 2> (up||gate 24576x4096 GEMV + SwiGLU + Q8_1, ncols=2, "
+                      "SwiGLU-packed wave-tile layout; 192 workgroups of 8 waves, two 32-output groups each)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
@@ -409,6 +409,30 @@ def time_blocks(stream, launch, nrot, blocks=5, per_block=None):
     return sum(a.elapsed_time(b) * 1e3 / per_block for a, b in evs) / blocks, blocks * per_block
 
 
+def time_graph(stream, launch, nrot, blocks=5):
+    """mean launch time (us) of back-to-back launches over nrot rotating buffer sets, captured once into a HIP graph
+    and replayed (the launches of a round are graph nodes too; a host loop of ctypes calls would time the host for
+    kernels of a few microseconds)"""
+    import torch
+    for r in range(nrot):
+        launch(r)
+    torch.cuda.synchronize()
+    per_graph = 2 * nrot
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(per_graph):
+            launch(i % nrot)
+    g.replay()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(blocks)]
+    for b in range(blocks):
+        evs[b][0].record(stream)
+        g.replay()
+        evs[b][1].record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) * 1e3 / per_graph for a, b in evs) / blocks, blocks * per_graph
+
+
 def time_read_ref(stream, nbytes):
     """the single-launch streaming-read reference for nbytes (rmi_stream_read, rotating replicas >= 1 GB), best of a
     few grids: what one kernel that only reads those bytes takes here, launch and ramp included"""
@@ -462,7 +486,7 @@ def time_gdn_layer(stream):
         rmi.gdn_layer_tokens_x(st[r, 0], st[r, 1], hist[r, 0], hist[r, 1], sel, proj, stride, proj[ch + h_v * S:],
                                stride, conv_w, dt, ssm_a, gamma, 1e-6, y, h_v * S, q8, q8b, h_k, h_v, 2, xch, stream)
 
-    us, n = time_blocks(stream, launch, nrot)
+    us, n = time_graph(stream, launch, nrot)
     state = S * h_v * S * 4
     nbytes = 3 * state + 2 * 2 * h_v * 3 * S * 3 * 4 + 4 * ch * 4 + 2 * stride * 4 + 2 * (h_v * S * 4 + q8b)
     return {"kernel": "gdn layer, 2 tokens (rmi_gdn_layer_tokens_x: four workgroups per value head)", "per_round": ROUND_GDN, "algorithmic_bytes": nbytes,
@@ -497,7 +521,7 @@ def time_attention(stream, ctx):
         rmi.gqa_flash_decode(q, kv[r, 0], kv[r, 1], pos, gate, gstride, None, 0, q8, q8b, ws, n_head, n_kv, hd, 2,
                              max_ctx, nsub, 1.0 / 16, stream)
 
-    us, n = time_blocks(stream, launch, nrot)
+    us, n = time_graph(stream, launch, nrot)
     nbytes = 2 * ctx * row * 2
     return {"kernel": f"attention, 2 queries, ctx {ctx} (rmi_gqa_flash_decode: partial + merge, nsub {nsub})",
             "per_round": ROUND_ATTN, "algorithmic_bytes": nbytes, "us": round(us, 3),
