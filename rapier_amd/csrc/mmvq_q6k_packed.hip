@@ -963,13 +963,19 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
 // waves 0..3 reduce the even ones and waves 4..7 the odd ones, each group as the 256 lanes of the norm tree.
 constexpr int kMfmaNormLoads = 4;
 
-template <int NCG, bool RES, int D, bool INV = false>
+// CS = 2: the two waves of a pair share a quad and split its columns (each runs NCG / 2 column groups over the same
+// weight tiles, the second load an L2 hit), so a shape with fewer quads than the grid's waves still fills every CU;
+// a column's arithmetic is unchanged
+template <int NCG, bool RES, int D, bool INV = false, int CS = 1>
 __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t* __restrict__ wp,
                                                                    const uint8_t* __restrict__ x, float* y,
                                                                    const float* res, float* partials, int n_in,
                                                                    int n_out, Fold fold) {
     typedef int i32x4 __attribute__((ext_vector_type(4)));
     static_assert(kWideWaves == 8, "two 256-lane norm trees");
+    static_assert(CS == 1 || (CS == 2 && !INV), "column split: two waves per quad, no folded norm");
+    constexpr int NCW = NCG / CS;            // column groups of this wave
+    constexpr int PG = NCW >= 2 ? 2 : 1;     // column groups per MFMA batch
     extern __shared__ uint4 smem[];
     // INV: the columns' four wave sums after the stage (the stage may take all 160 KB of the CU's LDS otherwise, so
     // the kernel has no static LDS)
@@ -978,8 +984,9 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
     const int nch = n_in / kChunkElems;
     const int nbt = n_in / 32;
     const int nq = (n_out + kQuad - 1) / kQuad;
-    const int GW = static_cast<int>(gridDim.x) * kWideWaves;
-    const int gw = static_cast<int>(blockIdx.x) * kWideWaves + (t >> 6);
+    const int wv = t >> 6, half = CS == 1 ? 0 : (wv & 1);
+    const int GW = static_cast<int>(gridDim.x) * (kWideWaves / CS);
+    const int gw = static_cast<int>(blockIdx.x) * (kWideWaves / CS) + (CS == 1 ? wv : (wv >> 1));
     const int my_quads = gw < nq ? (nq - 1 - gw) / GW + 1 : 0;
     const int nsteps = my_quads * nch;
 
@@ -1025,21 +1032,22 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
     __syncthreads();
 
     const int jj = lane & 3, hb = lane >> 2, b = hb >> 1, n = hb & 1;
-    float invc[NCG];   // inv of the lane's column 4 g + jj
+    float invc[NCW];   // inv of the lane's column 4 g + jj
     if constexpr (INV) {
 #pragma unroll
-        for (int g = 0; g < NCG; ++g) invc[g] = norm_inv(inv_red[4 * g + jj], n_in, fold.eps);
+        for (int g = 0; g < NCW; ++g) invc[g] = norm_inv(inv_red[4 * g + jj], n_in, fold.eps);
     }
-    // stage offsets (uint4 units, 32-bit): column group g at goff[g], the lane's column and half-block at lbase
-    int goff[NCG];
+    // stage offsets (uint4 units, 32-bit): the wave's column group g (group NCW half + g of the stage) at goff[g], the
+    // lane's column and half-block at lbase
+    int goff[NCW];
 #pragma unroll
-    for (int g = 0; g < NCG; ++g) goff[g] = g * nbt * kMStride;
+    for (int g = 0; g < NCW; ++g) goff[g] = (NCW * half + g) * nbt * kMStride;
     const int lbase = (8 * b + 4 * n) * kMStride + jj;
-    float tot[4][NCG];
+    float tot[4][NCW];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int g = 0; g < NCG; ++g) tot[i][g] = 0.0f;
+        for (int g = 0; g < NCW; ++g) tot[i][g] = 0.0f;
 
     for (int f0 = 0; f0 < nsteps; f0 += D) {
 #pragma unroll
@@ -1065,11 +1073,11 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
             dr[0] = half_bits_to_float(quad_bcast<0>(wt.d)); dr[1] = half_bits_to_float(quad_bcast<1>(wt.d));
             dr[2] = half_bits_to_float(quad_bcast<2>(wt.d)); dr[3] = half_bits_to_float(quad_bcast<3>(wt.d));
 
-            float acc[4][NCG];
+            float acc[4][NCW];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int g = 0; g < NCG; ++g) acc[i][g] = 0.0f;
+                for (int g = 0; g < NCW; ++g) acc[i][g] = 0.0f;
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
@@ -1084,19 +1092,21 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
                     // chains interleaved, then the epilogues (no chain waits on its own loads or results)
                     const int lo = lbase + (c * kNB + k) * kMStride;
 #pragma unroll
-                    for (int g0 = 0; g0 < NCG; g0 += 2) {
-                        uint4 qa[2], qb[2], rec[2];
+                    for (int g0 = 0; g0 < NCW; g0 += PG) {
+                        uint4 qa[PG], qb[PG], rec[PG];
 #pragma unroll
-                        for (int h = 0; h < 2; ++h) {
+                        for (int h = 0; h < PG; ++h) {
                             qa[h] = smem[goff[g0 + h] + lo];
                             qb[h] = smem[goff[g0 + h] + lo + 4];
                             rec[h] = smem[goff[g0 + h] + lo + 8];
                         }
-                        i32x4 d0[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}}, d1[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+                        i32x4 d0[PG], d1[PG];
+#pragma unroll
+                        for (int h = 0; h < PG; ++h) d0[h] = d1[h] = i32x4{0, 0, 0, 0};
 #pragma unroll
                         for (int qq = 0; qq < 4; ++qq) {
 #pragma unroll
-                            for (int h = 0; h < 2; ++h) {
+                            for (int h = 0; h < PG; ++h) {
                                 d0[h] = __builtin_amdgcn_mfma_i32_4x4x4i8(v[qq], static_cast<int>(qa[h][qq]), d0[h], 0,
                                                                           0, 0);
                                 d1[h] = __builtin_amdgcn_mfma_i32_4x4x4i8(v[4 + qq], static_cast<int>(qb[h][qq]), d1[h],
@@ -1104,7 +1114,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
                             }
                         }
 #pragma unroll
-                        for (int h = 0; h < 2; ++h) {
+                        for (int h = 0; h < PG; ++h) {
                             const float d8 = __uint_as_float(rec[h].z);
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
@@ -1120,14 +1130,14 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int g = 0; g < NCG; ++g) tot[i][g] = __builtin_fmaf(dr[i], acc[i][g], tot[i][g]);
+                for (int g = 0; g < NCW; ++g) tot[i][g] = __builtin_fmaf(dr[i], acc[i][g], tot[i][g]);
 
             if (c == nch - 1) {   // the quad's rows are complete
                 const int q = gw + qi * GW;
                 const int np = (n_out + 3) / 4;
 #pragma unroll
-                for (int g = 0; g < NCG; ++g) {
-                    const int col = 4 * g + jj;
+                for (int g = 0; g < NCW; ++g) {
+                    const int col = 4 * (NCW * half + g) + jj;
                     float v[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -1286,23 +1296,39 @@ int wide_cols(int n_in, int remaining) {
 
 // 8 / 16 columns in one weight pass on the MFMA ingest kernel: one 8-wave workgroup per CU (the stage takes up to
 // 160 KB of LDS), the quads split evenly over the waves
+// workgroups of a grid whose quad units (one per wave, or per pair of waves at CS = 2) spread evenly over the CUs
+int wide_grid(int nq, int units_per_wg) {
+    const int max_units = cu_count() * units_per_wg;
+    const int qpu = (nq + max_units - 1) / max_units;
+    const int units = (nq + qpu - 1) / qpu;
+    return (units + units_per_wg - 1) / units_per_wg;
+}
+
 template <int NCOLS, bool RES, bool INV = false>
 int launch_packed_wide(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
                        int n_out, const Fold& f, hipStream_t s) {
     constexpr int D = 3;
     auto kern = q6k_packed_mfma<NCOLS / 4, RES, D, INV>;
+    auto kern2 = q6k_packed_mfma<NCOLS / 4, RES, D, false, 2>;
     static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 kWideStageBytes) == hipSuccess &&
+                             hipFuncSetAttribute(reinterpret_cast<const void*>(kern2),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  kWideStageBytes) == hipSuccess;
     if (!attr) return fail(RMI_ERR_LAUNCH, "native_q6_k_mmvq_packed: wide LDS stage not available");
     const int nq = (n_out + kQuad - 1) / kQuad;
     const size_t lds = wide_stage_bytes(n_in, NCOLS) + (INV ? NCOLS * 4 * sizeof(float) : 0);
     if (lds > kWideStageBytes) return fail(RMI_ERR_SHAPE, "native_q6_k_mmvq_packed: wide stage exceeds the LDS");
-    const int max_waves = cu_count() * kWideWaves;
-    const int qpw = (nq + max_waves - 1) / max_waves;
-    const int waves = (nq + qpw - 1) / qpw;
-    const dim3 grid((waves + kWideWaves - 1) / kWideWaves), block(64 * kWideWaves);
-    hipLaunchKernelGGL(kern, grid, block, lds, s, wp, x, y, res, partials, n_in, n_out, f);
+    // a wave per quad unit; when that leaves CUs idle (fewer quads than the CUs' waves: the 4096-row outputs), the
+    // column-split form, a pair of waves per quad, on up to twice the workgroups
+    static const bool split_on = env_int("RMI_WIDE_SPLIT", 1) != 0;
+    const int g1 = wide_grid(nq, kWideWaves), g2 = wide_grid(nq, kWideWaves / 2);
+    const dim3 block(64 * kWideWaves);
+    if (!INV && split_on && 4 * g1 < 3 * cu_count() && g2 > g1)
+        hipLaunchKernelGGL(kern2, dim3(g2), block, lds, s, wp, x, y, res, partials, n_in, n_out, f);
+    else
+        hipLaunchKernelGGL(kern, dim3(g1), block, lds, s, wp, x, y, res, partials, n_in, n_out, f);
     return RMI_OK;
 }
 
