@@ -153,10 +153,10 @@ __device__ __forceinline__ void gate_values(float b_raw, float a_raw, float dt, 
 template <int NT, bool RAW, bool CONV>
 __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     constexpr bool SNAP = NT == 2;
-    // decode / verify on the engine path: the launch's loads go out in one batch led by the selector (both history
-    // buffers read, one kept), so the state loads wait for one memory round trip, not three; the gates are derived by
-    // the conv's idle lanes and published by the conv's own barrier
-    constexpr bool FAST = CONV && RAW && NT <= 2;
+    // the engine path (decode, verify, ingest chunks): the launch's loads go out in one batch led by the selector
+    // (both history buffers read, one kept), so the state loads wait for one memory round trip, not three; the gates
+    // are derived by the conv's idle lanes and published by the conv's own barrier
+    constexpr bool FAST = CONV && RAW;
     __shared__ float cq[NT][S], ck[NT][S], cv[CONV ? NT : 1][S];   // q, k (and v) of every token
     __shared__ float cpart[NT][4];
     __shared__ float gbt[NT][2];                                    // decay, beta per token
@@ -183,26 +183,28 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     // taps (CONV), z and gamma (the norm lanes), the gate inputs, and (FAST) both history buffers
     const float* src = kind == 0 ? a.q + qh * S : kind == 1 ? a.k + qh * S : a.v + head * S;
     const int c = kind == 0 ? qh * S + j : kind == 1 ? (a.h_k + qh) * S + j : (2 * a.h_k + head) * S + j;
+    // every lane loads every token's row (clamped to the last token; kind 3 and row groups 1..3 load and discard):
+    // a load under a per-token branch is issued where it is first used, one memory round trip per token
     float xr[NT], w0 = 0.0f, w1 = 0.0f, w2 = 0.0f, w3 = 0.0f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) xr[t] = 0.0f;
-    if (CONV && kind < 3) {
+    if constexpr (CONV) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-            if (t < ntok) xr[t] = src[static_cast<size_t>(t) * a.tok_stride + j];
+        for (int t = 0; t < NT; ++t) {
+            const float v = src[static_cast<size_t>(min(t, ntok - 1)) * a.tok_stride + j];
+            xr[t] = t < ntok && kind < 3 ? v : 0.0f;
+        }
         w0 = a.conv_w[4 * c];
         w1 = a.conv_w[4 * c + 1];
         w2 = a.conv_w[4 * c + 2];
         w3 = a.conv_w[4 * c + 3];
     }
-    float zz[NT], gam = 0.0f;
+    float zz[NT];
+    const float gam = a.gamma[col];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) zz[t] = 0.0f;
-    if (rg == 0) {
-        gam = a.gamma[col];
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-            if (t < ntok) zz[t] = a.z[static_cast<size_t>(t) * a.tok_stride + head * S + col];
+    for (int t = 0; t < NT; ++t) {
+        const float v = a.z[static_cast<size_t>(min(t, ntok - 1)) * a.tok_stride + head * S + col];
+        zz[t] = t < ntok && rg == 0 ? v : 0.0f;
     }
     float gin[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // gate lane of token gt: lanes 0.. (FAST: the conv's idle lanes 3 S ..)
@@ -355,6 +357,10 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     // The recurrence runs through all tokens without a workgroup barrier: the output norm of token t (a sum over the
     // head's 128 columns, across waves) feeds only y, so each token's o and per-wave sum of squares are kept and the
     // norms are taken after the loop, with the same operations in the same order.
+    // the output gate's SiLU does not depend on the recurrence: taken while the state loads are in flight
+    float sz[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) sz[t] = silu(zz[t]);
     float occ[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) occ[t] = 0.0f;
@@ -396,7 +402,7 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
             for (int w = 0; w < S * RG / 64; ++w) tot += wsum[t][w];
             if (rg == 0) {
                 const float scale = rsqrtf(tot / static_cast<float>(S) + a.eps);
-                ybuf[t][col] = occ[t] * scale * gam * silu(zz[t]);
+                ybuf[t][col] = occ[t] * scale * gam * sz[t];
             }
         }
     }
@@ -564,6 +570,9 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
     };
     __syncthreads();
 
+    float sz[NT];   // the output gate's SiLU, ahead of the recurrence and the exchange
+#pragma unroll
+    for (int t = 0; t < NT; ++t) sz[t] = silu(zz[t]);
     float occ[NT];
     float s0[SNAP ? RPG : 1];   // the state after token 0 (stored with the others after the exchange)
 #pragma unroll
@@ -644,7 +653,7 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
         for (int w = 0; w < S * RG / 64; ++w) tot += allw[t][w];
         if (rg == 0) {
             const float scale = rsqrtf(tot / static_cast<float>(S) + a.eps);
-            ybuf[t][lcol] = occ[t] * scale * gam * silu(zz[t]);
+            ybuf[t][lcol] = occ[t] * scale * gam * sz[t];
         }
     }
     __syncthreads();
