@@ -952,6 +952,36 @@ __device__ __forceinline__ void stage_activations_mfma(const uint8_t* __restrict
     }
 }
 
+// one Q8_1 block (its 9 dwords) into the MFMA stage at (column col, staged block jb), nbs staged blocks per column
+__device__ __forceinline__ void stage_one_mfma(const uint32_t (&wv)[9], int col, int jb, int nbs, uint4* st) {
+    int s0 = 0, s1 = 0;
+#pragma unroll
+    for (int i = 1; i <= 4; ++i) s0 = sdot4(static_cast<int>(wv[i]), 0x01010101, s0);
+#pragma unroll
+    for (int i = 5; i <= 8; ++i) s1 = sdot4(static_cast<int>(wv[i]), 0x01010101, s1);
+    uint4* q = st + static_cast<size_t>((col >> 2) * nbs + jb) * kMStride + (col & 3);
+    q[0] = make_uint4(wv[1], wv[2], wv[3], wv[4]);
+    q[4] = make_uint4(wv[5], wv[6], wv[7], wv[8]);
+    q[8] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1),
+                      __float_as_uint(half_bits_to_float(wv[0])), 0u);
+}
+
+// blocks jb0 .. jb0 + nbs - 1 of every column (nbt blocks per column in x) into the stage
+__device__ __forceinline__ void stage_range_mfma(const uint8_t* __restrict__ x, int ncols, int nbt, int jb0, int nbs,
+                                                 uint4* st, int t, int nthreads) {
+    for (int J = t; J < ncols * nbs; J += nthreads) {
+        const int col = J / nbs, jb = J - col * nbs;
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(col * nbt + jb0 + jb) * kQ8_1Bytes);
+        uint32_t wv[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) wv[i] = p[i];
+        stage_one_mfma(wv, col, jb, nbs, st);
+    }
+}
+
+// KP = 2: the second half of the blocks, held in registers (up to kPhaseRegs blocks per lane) until the phase switch
+constexpr int kPhaseRegs = 6;
+
 // value of lane 4 (l / 4) + i (a broadcast inside each group of four lanes)
 template <int I>
 __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
@@ -965,8 +995,13 @@ constexpr int kMfmaNormLoads = 4;
 
 // CS = 2: the two waves of a pair share a quad and split its columns (each runs NCG / 2 column groups over the same
 // weight tiles, the second load an L2 hit), so a shape with fewer quads than the grid's waves still fills every CU;
-// a column's arithmetic is unchanged
-template <int NCG, bool RES, int D, bool INV = false, int CS = 1>
+// a column's arithmetic is unchanged.
+// KP = 2: the stage holds half of the row (a 16-column stage of a 12288-wide row is 320 KB against the CU's 160 KB).
+// Each wave pair owns one quad (clamped past the last, its stores skipped), runs the first half's chunks, and at the
+// half every wave of the workgroup meets at a barrier, the second half (loaded into registers at the start) replaces
+// the first in the stage, and the chunks go on: one weight pass for 16 columns where two 8-column passes read the
+// weights twice, and the fma chain over the chunks runs in the same order.
+template <int NCG, bool RES, int D, bool INV = false, int CS = 1, int KP = 1, int NCHK = 0>
 __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t* __restrict__ wp,
                                                                    const uint8_t* __restrict__ x, float* y,
                                                                    const float* res, float* partials, int n_in,
@@ -974,6 +1009,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
     typedef int i32x4 __attribute__((ext_vector_type(4)));
     static_assert(kWideWaves == 8, "two 256-lane norm trees");
     static_assert(CS == 1 || (CS == 2 && !INV), "column split: two waves per quad, no folded norm");
+    static_assert(KP == 1 || (KP == 2 && CS == 2 && NCHK % 2 == 0 && NCHK > 0), "two K halves: a wave pair per quad");
     constexpr int NCW = NCG / CS;            // column groups of this wave
     constexpr int PG = NCW >= 2 ? 2 : 1;     // column groups per MFMA batch
     extern __shared__ uint4 smem[];
@@ -987,13 +1023,17 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
     const int wv = t >> 6, half = CS == 1 ? 0 : (wv & 1);
     const int GW = static_cast<int>(gridDim.x) * (kWideWaves / CS);
     const int gw = static_cast<int>(blockIdx.x) * (kWideWaves / CS) + (CS == 1 ? wv : (wv >> 1));
-    const int my_quads = gw < nq ? (nq - 1 - gw) / GW + 1 : 0;
+    // KP = 2: every wave runs one quad's chunks (a pair past the last quad reads the last one's tiles and stores
+    // nothing), so every wave meets the phase barrier
+    const int my_quads = KP == 2 ? 1 : gw < nq ? (nq - 1 - gw) / GW + 1 : 0;
     const int nsteps = my_quads * nch;
+    const int nbs = nbt / KP, cpp = KP == 2 ? NCHK / 2 : nch;   // staged blocks per column, chunks per phase
 
     WTile buf[D];
     auto issue = [&](int f, WTile& b) {
         const int qi = f / nch, c = f - qi * nch;
-        const uint8_t* base = wp + (static_cast<size_t>(gw + qi * GW) * nch + c) * kWaveTile;
+        const int qq = KP == 2 ? min(gw, nq - 1) : gw + qi * GW;
+        const uint8_t* base = wp + (static_cast<size_t>(qq) * nch + c) * kWaveTile;
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             b.ql[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * 1024 + 16 * lane));
@@ -1017,7 +1057,26 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
     for (int s = 0; s < D; ++s)
         if (s < nsteps) issue(s, buf[s]);
 
-    stage_activations_mfma(x, 4 * NCG, nbt, smem, t, 64 * kWideWaves);
+    if constexpr (KP == 1) {
+        stage_activations_mfma(x, 4 * NCG, nbt, smem, t, 64 * kWideWaves);
+    } else {
+        stage_range_mfma(x, 4 * NCG, nbt, 0, nbs, smem, t, 64 * kWideWaves);
+    }
+    // KP = 2: the second half's blocks, loaded one step before the switch (into registers the tiles leave free) and
+    // staged at the switch
+    uint32_t pb[KP == 2 ? kPhaseRegs : 1][9];
+    auto load_half = [&]() {
+        const int nb = 4 * NCG * nbs;
+#pragma unroll
+        for (int m = 0; m < kPhaseRegs; ++m) {
+            const int J = min(t + 64 * kWideWaves * m, nb - 1);
+            const int col = J / nbs, jb = J - col * nbs;
+            const uint32_t* p =
+                reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(col * nbt + nbs + jb) * kQ8_1Bytes);
+#pragma unroll
+            for (int i = 0; i < 9; ++i) pb[m][i] = p[i];
+        }
+    };
     if constexpr (INV) {
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
@@ -1041,7 +1100,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
     // lane's column and half-block at lbase
     int goff[NCW];
 #pragma unroll
-    for (int g = 0; g < NCW; ++g) goff[g] = (NCW * half + g) * nbt * kMStride;
+    for (int g = 0; g < NCW; ++g) goff[g] = (NCW * half + g) * nbs * kMStride;
     const int lbase = (8 * b + 4 * n) * kMStride + jj;
     float tot[4][NCW];
 #pragma unroll
@@ -1049,119 +1108,144 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
 #pragma unroll
         for (int g = 0; g < NCW; ++g) tot[i][g] = 0.0f;
 
-    for (int f0 = 0; f0 < nsteps; f0 += D) {
-#pragma unroll
-        for (int s = 0; s < D; ++s) {
-            const int f = f0 + s;
-            if (f >= nsteps) break;   // uniform across the wave
-            const int qi = f / nch, c = f - qi * nch;
-            const WTile wt = buf[s];
-            if (f + D < nsteps) issue(f + D, buf[s]);
+    // one (quad, chunk) step on tile buffer s
+    auto step = [&](const int f, const int s) {
+        const int qi = f / nch, c = f - qi * nch;
+        const int cs = KP == 2 && c >= cpp ? c - cpp : c;   // the chunk within the staged half
+        const WTile wt = buf[s];
+        if (f + D < nsteps) issue(f + D, buf[s]);
 
-            uint32_t Q[16], H[8];
+        uint32_t Q[16], H[8];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) Q[i] = wt.ql[i >> 2][i & 3];
+        for (int i = 0; i < 16; ++i) Q[i] = wt.ql[i >> 2][i & 3];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) H[i] = wt.qh[i >> 2][i & 3];
-            // the quad's four rows: sub-scale words and block scales
-            uint32_t S0[4], S1[4];
-            float dr[4];
-            S0[0] = quad_bcast<0>(wt.sc.x); S0[1] = quad_bcast<1>(wt.sc.x);
-            S0[2] = quad_bcast<2>(wt.sc.x); S0[3] = quad_bcast<3>(wt.sc.x);
-            S1[0] = quad_bcast<0>(wt.sc.y); S1[1] = quad_bcast<1>(wt.sc.y);
-            S1[2] = quad_bcast<2>(wt.sc.y); S1[3] = quad_bcast<3>(wt.sc.y);
-            dr[0] = half_bits_to_float(quad_bcast<0>(wt.d)); dr[1] = half_bits_to_float(quad_bcast<1>(wt.d));
-            dr[2] = half_bits_to_float(quad_bcast<2>(wt.d)); dr[3] = half_bits_to_float(quad_bcast<3>(wt.d));
+        for (int i = 0; i < 8; ++i) H[i] = wt.qh[i >> 2][i & 3];
+        // the quad's four rows: sub-scale words and block scales
+        uint32_t S0[4], S1[4];
+        float dr[4];
+        S0[0] = quad_bcast<0>(wt.sc.x); S0[1] = quad_bcast<1>(wt.sc.x);
+        S0[2] = quad_bcast<2>(wt.sc.x); S0[3] = quad_bcast<3>(wt.sc.x);
+        S1[0] = quad_bcast<0>(wt.sc.y); S1[1] = quad_bcast<1>(wt.sc.y);
+        S1[2] = quad_bcast<2>(wt.sc.y); S1[3] = quad_bcast<3>(wt.sc.y);
+        dr[0] = half_bits_to_float(quad_bcast<0>(wt.d)); dr[1] = half_bits_to_float(quad_bcast<1>(wt.d));
+        dr[2] = half_bits_to_float(quad_bcast<2>(wt.d)); dr[3] = half_bits_to_float(quad_bcast<3>(wt.d));
 
-            float acc[4][NCW];
+        float acc[4][NCW];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int g = 0; g < NCW; ++g) acc[i][g] = 0.0f;
+            for (int g = 0; g < NCW; ++g) acc[i][g] = 0.0f;
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-                for (int kh = 0; kh < 2; ++kh) {
-                    const int k = kk + 2 * kh;
-                    int v[8];
+            for (int kh = 0; kh < 2; ++kh) {
+                const int k = kk + 2 * kh;
+                int v[8];
 #pragma unroll
-                    for (int ww = 0; ww < 8; ++ww)
-                        v[ww] = static_cast<int>(((Q[8 * kk + ww] >> (4 * kh)) & 0x0f0f0f0fu) |
-                                                 (((H[ww] >> (2 * k)) & 0x03030303u) << 4));
-                    // two column groups at a time: their codes and records first, then the four independent MFMA
-                    // chains interleaved, then the epilogues (no chain waits on its own loads or results)
-                    const int lo = lbase + (c * kNB + k) * kMStride;
+                for (int ww = 0; ww < 8; ++ww)
+                    v[ww] = static_cast<int>(((Q[8 * kk + ww] >> (4 * kh)) & 0x0f0f0f0fu) |
+                                             (((H[ww] >> (2 * k)) & 0x03030303u) << 4));
+                // two column groups at a time: their codes and records first, then the four independent MFMA
+                // chains interleaved, then the epilogues (no chain waits on its own loads or results)
+                const int lo = lbase + (cs * kNB + k) * kMStride;
 #pragma unroll
-                    for (int g0 = 0; g0 < NCW; g0 += PG) {
-                        uint4 qa[PG], qb[PG], rec[PG];
+                for (int g0 = 0; g0 < NCW; g0 += PG) {
+                    uint4 qa[PG], qb[PG], rec[PG];
+#pragma unroll
+                    for (int h = 0; h < PG; ++h) {
+                        qa[h] = smem[goff[g0 + h] + lo];
+                        qb[h] = smem[goff[g0 + h] + lo + 4];
+                        rec[h] = smem[goff[g0 + h] + lo + 8];
+                    }
+                    i32x4 d0[PG], d1[PG];
+#pragma unroll
+                    for (int h = 0; h < PG; ++h) d0[h] = d1[h] = i32x4{0, 0, 0, 0};
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) {
 #pragma unroll
                         for (int h = 0; h < PG; ++h) {
-                            qa[h] = smem[goff[g0 + h] + lo];
-                            qb[h] = smem[goff[g0 + h] + lo + 4];
-                            rec[h] = smem[goff[g0 + h] + lo + 8];
+                            d0[h] = __builtin_amdgcn_mfma_i32_4x4x4i8(v[qq], static_cast<int>(qa[h][qq]), d0[h], 0,
+                                                                      0, 0);
+                            d1[h] = __builtin_amdgcn_mfma_i32_4x4x4i8(v[4 + qq], static_cast<int>(qb[h][qq]), d1[h],
+                                                                      0, 0, 0);
                         }
-                        i32x4 d0[PG], d1[PG];
+                    }
 #pragma unroll
-                        for (int h = 0; h < PG; ++h) d0[h] = d1[h] = i32x4{0, 0, 0, 0};
+                    for (int h = 0; h < PG; ++h) {
+                        const float d8 = __uint_as_float(rec[h].z);
 #pragma unroll
-                        for (int qq = 0; qq < 4; ++qq) {
-#pragma unroll
-                            for (int h = 0; h < PG; ++h) {
-                                d0[h] = __builtin_amdgcn_mfma_i32_4x4x4i8(v[qq], static_cast<int>(qa[h][qq]), d0[h], 0,
-                                                                          0, 0);
-                                d1[h] = __builtin_amdgcn_mfma_i32_4x4x4i8(v[4 + qq], static_cast<int>(qb[h][qq]), d1[h],
-                                                                          0, 0, 0);
-                            }
-                        }
-#pragma unroll
-                        for (int h = 0; h < PG; ++h) {
-                            const float d8 = __uint_as_float(rec[h].z);
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const int sc0 = sc_byte2(S0[i], S1[i], 2 * k), sc1 = sc_byte2(S0[i], S1[i], 2 * k + 1);
-                                const int sd = __mul24(sc0, d0[h][i] + static_cast<int>(rec[h].x)) +
-                                               __mul24(sc1, d1[h][i] + static_cast<int>(rec[h].y));
-                                acc[i][g0 + h] = __builtin_fmaf(d8, static_cast<float>(sd), acc[i][g0 + h]);
-                            }
+                        for (int i = 0; i < 4; ++i) {
+                            const int sc0 = sc_byte2(S0[i], S1[i], 2 * k), sc1 = sc_byte2(S0[i], S1[i], 2 * k + 1);
+                            const int sd = __mul24(sc0, d0[h][i] + static_cast<int>(rec[h].x)) +
+                                           __mul24(sc1, d1[h][i] + static_cast<int>(rec[h].y));
+                            acc[i][g0 + h] = __builtin_fmaf(d8, static_cast<float>(sd), acc[i][g0 + h]);
                         }
                     }
                 }
             }
+        }
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int g = 0; g < NCW; ++g) tot[i][g] = __builtin_fmaf(dr[i], acc[i][g], tot[i][g]);
+            for (int g = 0; g < NCW; ++g) tot[i][g] = __builtin_fmaf(dr[i], acc[i][g], tot[i][g]);
 
-            if (c == nch - 1) {   // the quad's rows are complete
-                const int q = gw + qi * GW;
-                const int np = (n_out + 3) / 4;
+        if (c == nch - 1 && (KP == 1 || gw < nq)) {   // the quad's rows are complete
+            const int q = gw + qi * GW;
+            const int np = (n_out + 3) / 4;
 #pragma unroll
-                for (int g = 0; g < NCW; ++g) {
-                    const int col = 4 * (NCW * half + g) + jj;
-                    float v[4];
+            for (int g = 0; g < NCW; ++g) {
+                const int col = 4 * (NCW * half + g) + jj;
+                float v[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        v[i] = hb_sum(tot[i][g]);
-                        if constexpr (INV) v[i] *= invc[g];
-                        tot[i][g] = 0.0f;
-                        const int row = kQuad * q + i;
-                        if constexpr (RES) {
-                            if (row < n_out) v[i] += res[static_cast<size_t>(col) * n_out + row];
-                        }
-                        if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v[i];
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    v[i] = hb_sum(tot[i][g]);
+                    if constexpr (INV) v[i] *= invc[g];
+                    tot[i][g] = 0.0f;
+                    const int row = kQuad * q + i;
                     if constexpr (RES) {
-                        if (hb == 0) {   // squares of the quad's rows in row order
-                            const int row0 = kQuad * q;
-                            float p = __builtin_fmaf(v[0], v[0], 0.0f);
-                            if (row0 + 1 < n_out) p = __builtin_fmaf(v[1], v[1], p);
-                            if (row0 + 2 < n_out) p = __builtin_fmaf(v[2], v[2], p);
-                            if (row0 + 3 < n_out) p = __builtin_fmaf(v[3], v[3], p);
-                            partials[static_cast<size_t>(col) * np + q] = p;
-                        }
+                        if (row < n_out) v[i] += res[static_cast<size_t>(col) * n_out + row];
+                    }
+                    if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v[i];
+                }
+                if constexpr (RES) {
+                    if (hb == 0) {   // squares of the quad's rows in row order
+                        const int row0 = kQuad * q;
+                        float p = __builtin_fmaf(v[0], v[0], 0.0f);
+                        if (row0 + 1 < n_out) p = __builtin_fmaf(v[1], v[1], p);
+                        if (row0 + 2 < n_out) p = __builtin_fmaf(v[2], v[2], p);
+                        if (row0 + 3 < n_out) p = __builtin_fmaf(v[3], v[3], p);
+                        partials[static_cast<size_t>(col) * np + q] = p;
                     }
                 }
             }
+        }
+    };
+    if constexpr (KP == 1) {
+        for (int f0 = 0; f0 < nsteps; f0 += D) {
+#pragma unroll
+            for (int s = 0; s < D; ++s) {
+                const int f = f0 + s;
+                if (f >= nsteps) break;   // uniform across the wave
+                step(f, s);
+            }
+        }
+    } else {
+        // NCHK chunks in straight-line code: the second half's registers are live only across the last step of the
+        // first half
+#pragma unroll
+        for (int f = 0; f < NCHK; ++f) {
+            if (f == NCHK / 2 - 1) load_half();
+            if (f == NCHK / 2) {
+                __syncthreads();   // the first half's stage is read out
+                const int nb = 4 * NCG * nbs;
+#pragma unroll
+                for (int m = 0; m < kPhaseRegs; ++m) {
+                    const int J = t + 64 * kWideWaves * m;
+                    if (J < nb) stage_one_mfma(pb[m], J / nbs, J - (J / nbs) * nbs, nbs, smem);
+                }
+                __syncthreads();
+            }
+            step(f, f % D);
         }
     }
 }
@@ -1287,9 +1371,18 @@ size_t wide_stage_bytes(int n_in, int ncols) {
     return static_cast<size_t>(ncols / 4) * (n_in / 32) * kMStride * 16;
 }
 
-// the widest ingest pass (16 or 8 columns) whose stage fits kWideStageBytes, or 0
-int wide_cols(int n_in, int remaining) {
-    if (remaining >= 16 && wide_stage_bytes(n_in, 16) <= kWideStageBytes) return 16;
+// 16 columns whose stage is too wide for the LDS in two K halves (q6k_packed_mfma KP = 2): an even chunk count, half
+// the stage in the LDS and the other half in kPhaseRegs blocks per lane, a wave pair per quad at most
+bool wide_halves(int n_in, int n_out, bool inv) {
+    const int nch = n_in / kChunkElems, nq = (n_out + kQuad - 1) / kQuad;
+    static const bool on = env_int("RMI_WIDE_HALVES", 1) != 0;
+    return on && !inv && (nch == 4 || nch == 6) && wide_stage_bytes(n_in, 16) / 2 <= kWideStageBytes &&
+           16 * (n_in / 64) <= 64 * kWideWaves * kPhaseRegs && nq <= cu_count() * (kWideWaves / 2);
+}
+
+// the widest ingest pass (16 or 8 columns) whose stage fits kWideStageBytes (16 also in two K halves), or 0
+int wide_cols(int n_in, int n_out, int remaining, bool inv) {
+    if (remaining >= 16 && (wide_stage_bytes(n_in, 16) <= kWideStageBytes || wide_halves(n_in, n_out, inv))) return 16;
     if (remaining >= 8 && wide_stage_bytes(n_in, 8) <= kWideStageBytes) return 8;
     return 0;
 }
@@ -1310,16 +1403,32 @@ int launch_packed_wide(const uint8_t* wp, const uint8_t* x, float* y, const floa
     constexpr int D = 3;
     auto kern = q6k_packed_mfma<NCOLS / 4, RES, D, INV>;
     auto kern2 = q6k_packed_mfma<NCOLS / 4, RES, D, false, 2>;
-    static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 kWideStageBytes) == hipSuccess &&
-                             hipFuncSetAttribute(reinterpret_cast<const void*>(kern2),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 kWideStageBytes) == hipSuccess;
+    auto lds_attr = [](auto k) {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   kWideStageBytes) == hipSuccess;
+    };
+    static const bool attr = lds_attr(kern) && lds_attr(kern2);
     if (!attr) return fail(RMI_ERR_LAUNCH, "native_q6_k_mmvq_packed: wide LDS stage not available");
     const int nq = (n_out + kQuad - 1) / kQuad;
     const size_t lds = wide_stage_bytes(n_in, NCOLS) + (INV ? NCOLS * 4 * sizeof(float) : 0);
-    if (lds > kWideStageBytes) return fail(RMI_ERR_SHAPE, "native_q6_k_mmvq_packed: wide stage exceeds the LDS");
+    if (lds > kWideStageBytes) {
+        if constexpr (NCOLS == 16) {
+            // two K halves, a wave pair per quad (the second half's blocks take 54 registers: one tile fewer in flight)
+            auto kh4 = q6k_packed_mfma<4, RES, 2, false, 2, 2, 4>;
+            auto kh6 = q6k_packed_mfma<4, RES, 2, false, 2, 2, 6>;
+            static const bool attr_h = lds_attr(kh4) && lds_attr(kh6);
+            if (!attr_h) return fail(RMI_ERR_LAUNCH, "native_q6_k_mmvq_packed: wide LDS stage not available");
+            if (wide_halves(n_in, n_out, INV)) {
+                const dim3 grid((nq + kWideWaves / 2 - 1) / (kWideWaves / 2)), block(64 * kWideWaves);
+                if (n_in / kChunkElems == 4)
+                    hipLaunchKernelGGL(kh4, grid, block, lds / 2, s, wp, x, y, res, partials, n_in, n_out, f);
+                else
+                    hipLaunchKernelGGL(kh6, grid, block, lds / 2, s, wp, x, y, res, partials, n_in, n_out, f);
+                return RMI_OK;
+            }
+        }
+        return fail(RMI_ERR_SHAPE, "native_q6_k_mmvq_packed: wide stage exceeds the LDS");
+    }
     // a wave per quad unit; when that leaves CUs idle (fewer quads than the CUs' waves: the 4096-row outputs), the
     // column-split form, a pair of waves per quad, on up to twice the workgroups
     static const bool split_on = env_int("RMI_WIDE_SPLIT", 1) != 0;
@@ -1350,7 +1459,7 @@ int run_packed(const void* wpv, const void* xv, float* y, const float* res, floa
     const size_t xcol = static_cast<size_t>(n_in / 32) * kQ8_1Bytes;
     const size_t pcol = static_cast<size_t>((n_out + 3) / 4);
     for (int j = 0; j < ncols;) {
-        const int wide = wide_cols(n_in, ncols - j);
+        const int wide = wide_cols(n_in, n_out, ncols - j, INV);
         const int nj = wide ? wide : std::min(per, ncols - j);
         const uint8_t* xj = x + j * xcol;
         float* yj = y + static_cast<size_t>(j) * n_out;
