@@ -1001,7 +1001,11 @@ constexpr int kMfmaNormLoads = 4;
 // half every wave of the workgroup meets at a barrier, the second half (loaded into registers at the start) replaces
 // the first in the stage, and the chunks go on: one weight pass for 16 columns where two 8-column passes read the
 // weights twice, and the fma chain over the chunks runs in the same order.
-template <int NCG, bool RES, int D, bool INV = false, int CS = 1, int KP = 1, int NCHK = 0>
+// LE: the quad's row sums through LDS - each lane parks its 4 x NCW (row, column group) sums of its half-block, and
+// lane (row i, group g, column jj) adds its 16 half-blocks in the xor butterfly's tree (bitwise hb_sum), then owns one
+// output: ~60 instructions per quad where the 16 in-register butterflies take ~300.  Needs 4 KB x NCW of LDS per wave
+// after the stage.
+template <int NCG, bool RES, int D, bool INV = false, int CS = 1, int KP = 1, int NCHK = 0, bool LE = false>
 __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t* __restrict__ wp,
                                                                    const uint8_t* __restrict__ x, float* y,
                                                                    const float* res, float* partials, int n_in,
@@ -1010,6 +1014,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
     static_assert(kWideWaves == 8, "two 256-lane norm trees");
     static_assert(CS == 1 || (CS == 2 && !INV), "column split: two waves per quad, no folded norm");
     static_assert(KP == 1 || (KP == 2 && CS == 2 && NCHK % 2 == 0 && NCHK > 0), "two K halves: a wave pair per quad");
+    static_assert(!LE || (!INV && NCG / CS <= 4), "LDS row sums: no folded norm, at most 64 outputs per wave");
     constexpr int NCW = NCG / CS;            // column groups of this wave
     constexpr int PG = NCW >= 2 ? 2 : 1;     // column groups per MFMA batch
     extern __shared__ uint4 smem[];
@@ -1102,6 +1107,8 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
 #pragma unroll
     for (int g = 0; g < NCW; ++g) goff[g] = (NCW * half + g) * nbs * kMStride;
     const int lbase = (8 * b + 4 * n) * kMStride + jj;
+    // LE: this wave's row-sum scratch, after the stage
+    float* lescr = reinterpret_cast<float*>(smem + static_cast<size_t>(NCG) * nbs * kMStride) + wv * (64 * 4 * NCW);
     float tot[4][NCW];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -1192,29 +1199,77 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
         if (c == nch - 1 && (KP == 1 || gw < nq)) {   // the quad's rows are complete
             const int q = gw + qi * GW;
             const int np = (n_out + 3) / 4;
+            if constexpr (LE) {
+                constexpr int R = 4 * NCW;   // the lane's sums: [row i][group g] at i NCW + g
 #pragma unroll
-            for (int g = 0; g < NCW; ++g) {
-                const int col = 4 * (NCW * half + g) + jj;
-                float v[4];
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    v[i] = hb_sum(tot[i][g]);
-                    if constexpr (INV) v[i] *= invc[g];
-                    tot[i][g] = 0.0f;
-                    const int row = kQuad * q + i;
-                    if constexpr (RES) {
-                        if (row < n_out) v[i] += res[static_cast<size_t>(col) * n_out + row];
+                    for (int g = 0; g < NCW; ++g) {
+                        lescr[lane * R + i * NCW + g] = tot[i][g];
+                        tot[i][g] = 0.0f;
                     }
-                    if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v[i];
-                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                // lane o: row io = o / R, group go = (o / 4) % NCW, column jo = o % 4 (lanes past 16 NCW idle)
+                const bool live = lane < 4 * R;
+                const int oo = live ? lane : 0;
+                const int io = oo / R, go = (oo >> 2) % NCW, jo = oo & 3;
+                float hv[16];
+#pragma unroll
+                for (int h = 0; h < 16; ++h) hv[h] = lescr[(4 * h + jo) * R + io * NCW + go];
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read out before the next quad's sums land
+                // the xor butterfly of hb_sum (partners hb ^ 8, ^ 4, ^ 2, ^ 1), evaluated for half-block 0
+                float a8[8], a4[4], a2[2];
+#pragma unroll
+                for (int h = 0; h < 8; ++h) a8[h] = hv[h] + hv[h + 8];
+#pragma unroll
+                for (int h = 0; h < 4; ++h) a4[h] = a8[h] + a8[h + 4];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) a2[h] = a4[h] + a4[h + 2];
+                float v = a2[0] + a2[1];
+                const int row = kQuad * q + io, col = 4 * (NCW * half + go) + jo;
                 if constexpr (RES) {
-                    if (hb == 0) {   // squares of the quad's rows in row order
+                    if (live && row < n_out) v += res[static_cast<size_t>(col) * n_out + row];
+                }
+                if (live && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v;
+                if constexpr (RES) {
+                    // the quad's four rows of this column sit R lanes apart: squares in row order
+                    const float v1 = xor_lane<R>(v);
+                    const float v2 = xor_lane<2 * R>(v);
+                    const float v3 = xor_lane<2 * R>(v1);
+                    if (live && io == 0) {
                         const int row0 = kQuad * q;
-                        float p = __builtin_fmaf(v[0], v[0], 0.0f);
-                        if (row0 + 1 < n_out) p = __builtin_fmaf(v[1], v[1], p);
-                        if (row0 + 2 < n_out) p = __builtin_fmaf(v[2], v[2], p);
-                        if (row0 + 3 < n_out) p = __builtin_fmaf(v[3], v[3], p);
+                        float p = __builtin_fmaf(v, v, 0.0f);
+                        if (row0 + 1 < n_out) p = __builtin_fmaf(v1, v1, p);
+                        if (row0 + 2 < n_out) p = __builtin_fmaf(v2, v2, p);
+                        if (row0 + 3 < n_out) p = __builtin_fmaf(v3, v3, p);
                         partials[static_cast<size_t>(col) * np + q] = p;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int g = 0; g < NCW; ++g) {
+                    const int col = 4 * (NCW * half + g) + jj;
+                    float v[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        v[i] = hb_sum(tot[i][g]);
+                        if constexpr (INV) v[i] *= invc[g];
+                        tot[i][g] = 0.0f;
+                        const int row = kQuad * q + i;
+                        if constexpr (RES) {
+                            if (row < n_out) v[i] += res[static_cast<size_t>(col) * n_out + row];
+                        }
+                        if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v[i];
+                    }
+                    if constexpr (RES) {
+                        if (hb == 0) {   // squares of the quad's rows in row order
+                            const int row0 = kQuad * q;
+                            float p = __builtin_fmaf(v[0], v[0], 0.0f);
+                            if (row0 + 1 < n_out) p = __builtin_fmaf(v[1], v[1], p);
+                            if (row0 + 2 < n_out) p = __builtin_fmaf(v[2], v[2], p);
+                            if (row0 + 3 < n_out) p = __builtin_fmaf(v[3], v[3], p);
+                            partials[static_cast<size_t>(col) * np + q] = p;
+                        }
                     }
                 }
             }
@@ -1401,29 +1456,39 @@ template <int NCOLS, bool RES, bool INV = false>
 int launch_packed_wide(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
                        int n_out, const Fold& f, hipStream_t s) {
     constexpr int D = 3;
-    auto kern = q6k_packed_mfma<NCOLS / 4, RES, D, INV>;
-    auto kern2 = q6k_packed_mfma<NCOLS / 4, RES, D, false, 2>;
+    constexpr int NCG = NCOLS / 4;
+    auto kern = q6k_packed_mfma<NCG, RES, D, INV>;
+    auto kern2 = q6k_packed_mfma<NCG, RES, D, false, 2>;
+    auto kernl = q6k_packed_mfma<NCG, RES, D, false, 1, 1, 0, true>;
+    auto kern2l = q6k_packed_mfma<NCG, RES, D, false, 2, 1, 0, true>;
     auto lds_attr = [](auto k) {
         return hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    kWideStageBytes) == hipSuccess;
     };
-    static const bool attr = lds_attr(kern) && lds_attr(kern2);
+    static const bool attr = lds_attr(kern) && lds_attr(kern2) && lds_attr(kernl) && lds_attr(kern2l);
     if (!attr) return fail(RMI_ERR_LAUNCH, "native_q6_k_mmvq_packed: wide LDS stage not available");
+    // the LDS row sums (LE) where their scratch, 4 KB per column group of a wave, fits after the stage
+    static const bool le_on = env_int("RMI_WIDE_LE", 1) != 0;
+    auto le_bytes = [](int ncw) { return static_cast<size_t>(kWideWaves) * 64 * 4 * ncw * sizeof(float); };
     const int nq = (n_out + kQuad - 1) / kQuad;
     const size_t lds = wide_stage_bytes(n_in, NCOLS) + (INV ? NCOLS * 4 * sizeof(float) : 0);
     if (lds > kWideStageBytes) {
         if constexpr (NCOLS == 16) {
             // two K halves, a wave pair per quad (the second half's blocks take 54 registers: one tile fewer in flight)
-            auto kh4 = q6k_packed_mfma<4, RES, 2, false, 2, 2, 4>;
+            // (8192-wide rows: the half stage leaves room for the LDS row sums; 12288: it does not)
+            auto kh4 = q6k_packed_mfma<4, RES, 2, false, 2, 2, 4, true>;
             auto kh6 = q6k_packed_mfma<4, RES, 2, false, 2, 2, 6>;
             static const bool attr_h = lds_attr(kh4) && lds_attr(kh6);
             if (!attr_h) return fail(RMI_ERR_LAUNCH, "native_q6_k_mmvq_packed: wide LDS stage not available");
             if (wide_halves(n_in, n_out, INV)) {
                 const dim3 grid((nq + kWideWaves / 2 - 1) / (kWideWaves / 2)), block(64 * kWideWaves);
-                if (n_in / kChunkElems == 4)
-                    hipLaunchKernelGGL(kh4, grid, block, lds / 2, s, wp, x, y, res, partials, n_in, n_out, f);
-                else
+                const size_t lh = lds / 2 + le_bytes(2);
+                if (n_in / kChunkElems == 4 && lh <= kWideStageBytes)
+                    hipLaunchKernelGGL(kh4, grid, block, lh, s, wp, x, y, res, partials, n_in, n_out, f);
+                else if (n_in / kChunkElems == 6)
                     hipLaunchKernelGGL(kh6, grid, block, lds / 2, s, wp, x, y, res, partials, n_in, n_out, f);
+                else
+                    return fail(RMI_ERR_SHAPE, "native_q6_k_mmvq_packed: wide stage exceeds the LDS");
                 return RMI_OK;
             }
         }
@@ -1434,10 +1499,19 @@ int launch_packed_wide(const uint8_t* wp, const uint8_t* x, float* y, const floa
     static const bool split_on = env_int("RMI_WIDE_SPLIT", 1) != 0;
     const int g1 = wide_grid(nq, kWideWaves), g2 = wide_grid(nq, kWideWaves / 2);
     const dim3 block(64 * kWideWaves);
-    if (!INV && split_on && 4 * g1 < 3 * cu_count() && g2 > g1)
-        hipLaunchKernelGGL(kern2, dim3(g2), block, lds, s, wp, x, y, res, partials, n_in, n_out, f);
-    else
-        hipLaunchKernelGGL(kern, dim3(g1), block, lds, s, wp, x, y, res, partials, n_in, n_out, f);
+    if (!INV && split_on && 4 * g1 < 3 * cu_count() && g2 > g1) {
+        const size_t l2 = lds + le_bytes(NCG / 2);
+        if (le_on && NCG >= 2 && l2 <= kWideStageBytes)
+            hipLaunchKernelGGL(kern2l, dim3(g2), block, l2, s, wp, x, y, res, partials, n_in, n_out, f);
+        else
+            hipLaunchKernelGGL(kern2, dim3(g2), block, lds, s, wp, x, y, res, partials, n_in, n_out, f);
+    } else {
+        const size_t l1 = lds + le_bytes(NCG);
+        if (le_on && !INV && l1 <= kWideStageBytes)
+            hipLaunchKernelGGL(kernl, dim3(g1), block, l1, s, wp, x, y, res, partials, n_in, n_out, f);
+        else
+            hipLaunchKernelGGL(kern, dim3(g1), block, lds, s, wp, x, y, res, partials, n_in, n_out, f);
+    }
     return RMI_OK;
 }
 
