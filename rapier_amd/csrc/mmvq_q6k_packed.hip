@@ -1107,8 +1107,11 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
 #pragma unroll
     for (int g = 0; g < NCW; ++g) goff[g] = (NCW * half + g) * nbs * kMStride;
     const int lbase = (8 * b + 4 * n) * kMStride + jj;
-    // LE: this wave's row-sum scratch, after the stage
-    float* lescr = reinterpret_cast<float*>(smem + static_cast<size_t>(NCG) * nbs * kMStride) + wv * (64 * 4 * NCW);
+    // LE: this wave's row-sum scratch, after the stage; with two K halves, the stage itself once every wave is past
+    // its last chunk (the rows complete at the last step of the straight-line chunk order, the same for every wave)
+    constexpr bool LEA = LE && KP == 2;
+    float* lescr = reinterpret_cast<float*>(smem + (LEA ? 0 : static_cast<size_t>(NCG) * nbs * kMStride)) +
+                   wv * (64 * 4 * NCW);
     float tot[4][NCW];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -1196,6 +1199,9 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
 #pragma unroll
             for (int g = 0; g < NCW; ++g) tot[i][g] = __builtin_fmaf(dr[i], acc[i][g], tot[i][g]);
 
+        if constexpr (LEA) {
+            if (c == nch - 1) __syncthreads();   // the stage's last reads are done: the row sums may overwrite it
+        }
         if (c == nch - 1 && (KP == 1 || gw < nq)) {   // the quad's rows are complete
             const int q = gw + qi * GW;
             const int np = (n_out + 3) / 4;
@@ -1475,16 +1481,16 @@ int launch_packed_wide(const uint8_t* wp, const uint8_t* x, float* y, const floa
     if (lds > kWideStageBytes) {
         if constexpr (NCOLS == 16) {
             // two K halves, a wave pair per quad (the second half's blocks take 54 registers: one tile fewer in flight)
-            // (8192-wide rows: the half stage leaves room for the LDS row sums; 12288: it does not)
+            // (the LDS row sums reuse the stage after the last chunk)
             auto kh4 = q6k_packed_mfma<4, RES, 2, false, 2, 2, 4, true>;
-            auto kh6 = q6k_packed_mfma<4, RES, 2, false, 2, 2, 6>;
+            auto kh6 = q6k_packed_mfma<4, RES, 2, false, 2, 2, 6, true>;
             static const bool attr_h = lds_attr(kh4) && lds_attr(kh6);
             if (!attr_h) return fail(RMI_ERR_LAUNCH, "native_q6_k_mmvq_packed: wide LDS stage not available");
             if (wide_halves(n_in, n_out, INV)) {
                 const dim3 grid((nq + kWideWaves / 2 - 1) / (kWideWaves / 2)), block(64 * kWideWaves);
-                const size_t lh = lds / 2 + le_bytes(2);
-                if (n_in / kChunkElems == 4 && lh <= kWideStageBytes)
-                    hipLaunchKernelGGL(kh4, grid, block, lh, s, wp, x, y, res, partials, n_in, n_out, f);
+                if (lds / 2 < le_bytes(2)) return fail(RMI_ERR_SHAPE, "native_q6_k_mmvq_packed: half stage too small");
+                if (n_in / kChunkElems == 4)
+                    hipLaunchKernelGGL(kh4, grid, block, lds / 2, s, wp, x, y, res, partials, n_in, n_out, f);
                 else if (n_in / kChunkElems == 6)
                     hipLaunchKernelGGL(kh6, grid, block, lds / 2, s, wp, x, y, res, partials, n_in, n_out, f);
                 else
