@@ -10,6 +10,9 @@ synthesized from a seed (KV cache fp16 N(0,1), GDN state N(0,0.05^2)) instead of
 ``--workload verify_gemv``: the 2-column verify GEMV pair with both fused epilogues (up||gate 24576x4096 ncols=2,
 then down 4096x12288 ncols=2 with residual + partials), >= 1 GiB of rotating weight replicas.
 
+``--workload ingest``: the prompt-ingest leg alone (4096 seeded tokens in 16-token chunks; also part of mtp_round's
+line), the workload of the ingest kernel trace.
+
 Prints ONE JSON line.  For mtp_round, ``value`` is tok/s at context 4096 and acceptance 0.5; ``roofline`` is the
 up||gate verify GEMV's algorithmic bytes / its mean launch time from HIP events on its launch stream (measured in the
 same run); ``cpu_baseline`` is one verify round on this host's cores: the reference's CPU arithmetic as a SIMD
@@ -935,7 +938,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200, help="timed verify rounds per run (mtp_round) or GEMV pairs")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="mtp_round",
-                    choices=["mtp_round", "verify_gemv", "traffic_probe", "gguf_load", "kernels", "round"])
+                    choices=["mtp_round", "verify_gemv", "traffic_probe", "gguf_load", "kernels", "round", "ingest"])
     ap.add_argument("--shapes", default="", help="kernels: comma-separated indices of the GEMV shapes to run")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--plan", default="q6_k", choices=["q6_k", "q5_k_m"], help="gguf_load: the file's type plan")
@@ -957,6 +960,9 @@ def main():
         return
     if args.workload == "round":
         run_round(args)
+        return
+    if args.workload == "ingest":
+        print(json.dumps({"workload": "ingest", **run_ingest()}), flush=True)
         return
     gemv_args =argparse.Namespace(steps=50 if args.workload == "mtp_round" else args.steps,
                                    warmup=10 if args.workload == "mtp_round" else args.warmup)
