@@ -116,12 +116,14 @@ def test_packed_layout_roundtrip(orc, rmi):
 
 
 
-@pytest.mark.parametrize("n_in,n_out", [(4096, 12352), (12288, 4096), (8192, 4096), (2048, 1001)])
+@pytest.mark.parametrize("n_in,n_out", [(4096, 12352), (12288, 4096), (8192, 4096), (2048, 1001), (12288, 1001),
+                                        (8192, 1001), (4096, 1001)])
 @pytest.mark.parametrize("ncols", [16, 13, 8])
 def test_packed_wide_passes_bitwise_equal_single_column(orc, rmi, n_in, n_out, ncols):
     """ingest widths: 16 / 8 columns in one weight pass (one 8-wave workgroup per CU, up to 160 KB of staged
-    activations), remainders in passes of up to 4; every column bitwise the ncols = 1 result, residual variant
-    bitwise plain + res"""
+    activations; rows of 8192 / 12288 at 16 columns in two K halves, the 4096-row outputs with a wave pair per quad,
+    the row sums through LDS; ragged row counts), remainders in passes of up to 4; every column bitwise the ncols = 1
+    result, residual variant bitwise plain + res"""
     w = orc.gen_q6k(n_out, n_in, seed=n_in + n_out + ncols)
     xq = orc.quantize_q8_1(orc.normal(ncols * n_in, seed=ncols + n_out), n_in, ncols)
     wd, xd = dev(w), dev(xq)
