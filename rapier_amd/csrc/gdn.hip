@@ -162,6 +162,7 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     __shared__ float gbt[NT][2];                                    // decay, beta per token
     __shared__ float wsum[NT][S * RG / 64];                         // per-wave sums of o^2
     __shared__ float ybuf[NT][S];
+    __shared__ float szb[NT][S];                                    // the output gate's SiLU per token and column
     const int ntok = NT <= 2 ? NT : a.ntok;
     const int head = blockIdx.x;
     // lane (wave w, lane l): column 16 w + l % 16, row group l / 16 (rows 32 rg .. 32 rg + 31): a column's four row
@@ -199,12 +200,16 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
         w2 = a.conv_w[4 * c + 2];
         w3 = a.conv_w[4 * c + 3];
     }
-    float zz[NT];
+    // the output gate: lane (column, row group rg) takes tokens RG i + rg, so a lane computes NT / RG SiLUs where the
+    // row-group-0 lanes alone would take all NT (a wave runs every token's code either way)
+    constexpr int ZT = (NT + RG - 1) / RG;
+    float zq[ZT];
     const float gam = a.gamma[col];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
+    for (int i = 0; i < ZT; ++i) {
+        const int t = RG * i + rg;
         const float v = a.z[static_cast<size_t>(min(t, ntok - 1)) * a.tok_stride + head * S + col];
-        zz[t] = t < ntok && rg == 0 ? v : 0.0f;
+        zq[i] = t < ntok ? v : 0.0f;
     }
     float gin[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // gate lane of token gt: lanes 0.. (FAST: the conv's idle lanes 3 S ..)
@@ -357,10 +362,12 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
     // The recurrence runs through all tokens without a workgroup barrier: the output norm of token t (a sum over the
     // head's 128 columns, across waves) feeds only y, so each token's o and per-wave sum of squares are kept and the
     // norms are taken after the loop, with the same operations in the same order.
-    // the output gate's SiLU does not depend on the recurrence: taken while the state loads are in flight
-    float sz[NT];
+    // the output gate's SiLU does not depend on the recurrence: taken before it, read after the loop's barrier
 #pragma unroll
-    for (int t = 0; t < NT; ++t) sz[t] = silu(zz[t]);
+    for (int i = 0; i < ZT; ++i) {
+        const int t = RG * i + rg;
+        if (t < NT) szb[t][col] = silu(zq[i]);
+    }
     float occ[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) occ[t] = 0.0f;
@@ -394,17 +401,22 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
         }
     }
     __syncthreads();
+    // every token's scale in every lane (no per-token divergent branch), the products on the row-group-0 lanes
+    float scl[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        if (t < ntok) {
+        scl[t] = 0.0f;
+        if (t < ntok) {   // uniform
             float tot = 0.0f;
 #pragma unroll
             for (int w = 0; w < S * RG / 64; ++w) tot += wsum[t][w];
-            if (rg == 0) {
-                const float scale = rsqrtf(tot / static_cast<float>(S) + a.eps);
-                ybuf[t][col] = occ[t] * scale * gam * sz[t];
-            }
+            scl[t] = rsqrtf(tot / static_cast<float>(S) + a.eps);
         }
+    }
+    if (rg == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            if (t < ntok) ybuf[t][col] = occ[t] * scl[t] * gam * szb[t][col];
     }
     __syncthreads();
     // y and its Q8_1 blocks: lane -> (token, column); 32-lane groups are whole blocks, and ntok * 128 is a multiple of
