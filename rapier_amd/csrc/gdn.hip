@@ -582,9 +582,17 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
     };
     __syncthreads();
 
-    float sz[NT];   // the output gate's SiLU, ahead of the recurrence and the exchange
+    // the output gate's SiLU is taken inside the exchange (below): wave 0 while its loads of the other parts' words are
+    // in flight, wave 1 before it waits at the barrier.  Left to the compiler it sinks to its use after the exchange,
+    // onto the launch's critical path.
+    float sz[NT];
+    auto gate_silu = [&]() {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) sz[t] = silu(zz[t]);
+        for (int t = 0; t < NT; ++t) {
+            sz[t] = silu(zz[t]);
+            asm volatile("" : "+v"(sz[t]));
+        }
+    };
     float occ[NT];
     float s0[SNAP ? RPG : 1];   // the state after token 0 (stored with the others after the exchange)
 #pragma unroll
@@ -641,12 +649,14 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         put_all();
+        gate_silu();
     }
     if (wv == 0) {
         const int pp = ln / (2 * NT), t = (ln >> 1) % NT, w = ln & 1;
         const bool other = ln < kParts * 2 * NT && pp != part;
         unsigned long long v = tag;
         if (other) v = __hip_atomic_load(xh + (pp * 2 + t) * 2 + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        gate_silu();
         int n = 0;
         while (!__all(!other || (v >> 32) == (tag >> 32)) && n < (1 << 20)) {
             if (other && (v >> 32) != (tag >> 32))
