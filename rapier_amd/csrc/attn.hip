@@ -68,6 +68,13 @@ __global__ __launch_bounds__(HD) void attn_prep_kernel(const float* __restrict__
     const int p = pos[0] + t;
     // held here: the compiler would otherwise sink both loads below the position check, one round trip after it
     asm volatile("" : "+v"(x), "+v"(wn));
+    // the rotary frequency of this lane's pair (fp64 pow, independent of the position) while the loads are in flight:
+    // left in place it runs after the norm's last barrier, on the launch's critical path
+    const int half = n_rot / 2;
+    const int ri = d < half ? d : d - half;
+    double freq = 0.0;
+    if (!is_v && d < n_rot) freq = rope_freq(ri, n_rot, theta);
+    asm volatile("" : "+v"(freq));
     if (p < 0 || p >= max_ctx) return;   // uniform: a position outside the cache stores nothing
     if (is_v) {   // v: straight to the cache
         const int kv = hh - n_head - n_kv;
@@ -79,11 +86,9 @@ __global__ __launch_bounds__(HD) void attn_prep_kernel(const float* __restrict__
     float v = x * inv * wn;
     xs[d] = v;
     __syncthreads();
-    const int half = n_rot / 2;
     if (d < n_rot) {
-        const int i = d < half ? d : d - half;
         float c, s;
-        rope_cos_sin(p, i, n_rot, theta, yarn, &c, &s);
+        rope_cos_sin_f(p, freq, ri, yarn, &c, &s);
         v = d < half ? rope_lo(xs[d], xs[d + half], c, s) : rope_hi(xs[d - half], xs[d], c, s);
     }
     if (is_q) {

@@ -39,10 +39,14 @@ inline bool yarn_setup(const rmi_rope_params& r, int n_rot, Yarn* y) {
     return true;
 }
 
-// cos and sin of pair i at position p (angle in fp64, rounded to fp32 once)
-__device__ __forceinline__ void rope_cos_sin(int p, int i, int n_rot, float theta, const Yarn& yarn, float* c,
-                                             float* s) {
-    double ang = static_cast<double>(p) * pow(static_cast<double>(theta), -2.0 * i / static_cast<double>(n_rot));
+// the frequency of pair i (fp64): theta^(-2 i / n_rot), which does not depend on the position
+__device__ __forceinline__ double rope_freq(int i, int n_rot, float theta) {
+    return pow(static_cast<double>(theta), -2.0 * i / static_cast<double>(n_rot));
+}
+
+// cos and sin of pair i at position p from its frequency (angle in fp64, rounded to fp32 once)
+__device__ __forceinline__ void rope_cos_sin_f(int p, double freq, int i, const Yarn& yarn, float* c, float* s) {
+    double ang = static_cast<double>(p) * freq;
     double sn, cs;
     if (yarn.on) {
         const double y = (static_cast<double>(i) - yarn.low) / fmax(0.001, yarn.high - yarn.low);
@@ -56,6 +60,11 @@ __device__ __forceinline__ void rope_cos_sin(int p, int i, int n_rot, float thet
     }
     *c = static_cast<float>(cs);
     *s = static_cast<float>(sn);
+}
+
+__device__ __forceinline__ void rope_cos_sin(int p, int i, int n_rot, float theta, const Yarn& yarn, float* c,
+                                             float* s) {
+    rope_cos_sin_f(p, rope_freq(i, n_rot, theta), i, yarn, c, s);
 }
 
 // the rotated pair (a, b) = (dim i, dim i + n_rot / 2); explicit fmas, so contraction cannot change the bits
