@@ -15,6 +15,7 @@
 //     column 1 = (c1, hidden of column 1) at pos + 2.  On reject column 0 is the reference's corrected draft step; on
 //     accept column 0 is its KV-fill step and column 1 its next-candidate step.  Both weight passes become one.
 //   * the KV cache is fp16; the token embedding is dequantized on the device.
+#include "epilogue_dev.h"
 #include "rmi_common.h"
 
 #include <cstdlib>
@@ -184,8 +185,8 @@ __global__ void fill_i32_kernel(int* p, size_t n, int v) {
     if (i < n) p[i] = v;
 }
 
-// after a single-token forward: emit the argmax, feed it back, advance one position
-__global__ void advance_single_kernel(int* st, int* ring) {
+// after a single-token forward: emit the argmax, feed it back, advance one position (one thread)
+__device__ void advance_single(int* st, int* ring) {
     const int id = st[kV0];
     const int n = st[kNOut];
     if (n < kRingCap) ring[n] = id;
@@ -194,8 +195,9 @@ __global__ void advance_single_kernel(int* st, int* ring) {
     st[kPos] = min(st[kPos] + 1, st[kMaxPos]);
 }
 
-// after the verify: accept c0 == candidate, roll back the GDN state on reject, emit, set up the draft columns
-__global__ void accept_kernel(int* st, int* ring) {
+// after the verify: accept c0 == candidate, roll back the GDN state on reject, emit, set up the draft columns (one
+// thread)
+__device__ void accept_tokens(int* st, int* ring) {
     const int c0 = st[kV0], c1 = st[kV1];
     const int accept = c0 == st[kTok1];
     int n = st[kNOut];
@@ -232,9 +234,9 @@ __device__ void wg_copy(float* __restrict__ dst, const float* __restrict__ src, 
 
 // after the draft: pick the candidate, advance (1 or 2 positions), apply the forced-acceptance override.  On accept the
 // last fed token is column 1, whose hidden moves to column 0, so that column 0 always holds the hidden of the token
-// before the current one (the input of a later first draft or ingest chunk).
-__global__ void finalize_kernel(int* st, const int* ref_tok, const uint8_t* pattern, float* hsave, float* hpart, int n,
-                                int np) {
+// before the current one (the input of a later first draft or ingest chunk).  One workgroup.
+__device__ void finalize_round(int* st, const int* ref_tok, const uint8_t* pattern, float* hsave, float* hpart, int n,
+                               int np) {
     const int accept = st[kAccept];
     if (accept) {
         wg_copy(hsave, hsave + n, n);
@@ -256,14 +258,83 @@ __global__ void finalize_kernel(int* st, const int* ref_tok, const uint8_t* patt
     st[kRound] = round + 1;
 }
 
-// initial draft candidate (1-column draft with head): cand = draft argmax, or the forced one
-__global__ void first_candidate_kernel(int* st, const int* ref_tok, const uint8_t* pattern) {
+// initial draft candidate (1-column draft with head): cand = draft argmax, or the forced one (one thread)
+__device__ void first_candidate(int* st, const int* ref_tok, const uint8_t* pattern) {
     int cand = st[kC0];
     if (st[kMode] == 1 && st[kPatLen] > 0) {
         const int truth = ref_tok[min(st[kPos] + 1, st[kMaxPos])];
         cand = pattern[0] ? truth : (truth + 1) % st[kVocab];
     }
     st[kTok1] = cand;
+}
+
+// The decode tails: the greedy tokens of the lm_head columns (argmax_final_block over argmax_partial_launch's keys)
+// and the integer bookkeeping that reads them run in one launch; after the trunk's lm_head the same launch also takes
+// the final norm of the hidden (rms_norm_out_block) on workgroups 1.., which neither reads nor writes what workgroup 0
+// does.  Same bits as the separate launches (argmax, rms_norm_out, accept / advance / finalize / first candidate).
+struct NormOut {
+    const float* x;
+    const float* w;
+    const float* part;
+    float* out;
+    float* out_part;
+    int cols;
+    float eps;
+};
+
+__device__ void norm_out_workgroup(const NormOut& no, int b) {
+    const int nb = (no.cols + 255) / 256;
+    rms_norm_out_block(no.x, no.w, no.part, no.out, no.out_part, no.cols, no.eps, no.cols, b / nb, b % nb);
+}
+
+// after the verify's lm_head (2 columns): c0, c1, then the acceptance
+__global__ __launch_bounds__(256) void verify_tail_kernel(int* st, int* ring, const uint64_t* keys, NormOut no) {
+    if (blockIdx.x == 0) {
+        const int c0 = argmax_final_block(keys, 0), c1 = argmax_final_block(keys, 1);
+        if (threadIdx.x == 0) {
+            st[kV0] = c0;
+            st[kV1] = c1;
+            accept_tokens(st, ring);
+        }
+        return;
+    }
+    norm_out_workgroup(no, static_cast<int>(blockIdx.x) - 1);
+}
+
+// after a single-token forward's lm_head: the token, then the advance
+__global__ __launch_bounds__(256) void single_tail_kernel(int* st, int* ring, const uint64_t* keys, NormOut no) {
+    if (blockIdx.x == 0) {
+        const int v0 = argmax_final_block(keys, 0);
+        if (threadIdx.x == 0) {
+            st[kV0] = v0;
+            advance_single(st, ring);
+        }
+        return;
+    }
+    norm_out_workgroup(no, static_cast<int>(blockIdx.x) - 1);
+}
+
+// after the round's 2-column draft head: both candidates, then finalize_round (one workgroup)
+__global__ __launch_bounds__(256) void draft_tail_kernel(int* st, const uint64_t* keys, const int* ref_tok,
+                                                         const uint8_t* pattern, float* hsave, float* hpart, int n,
+                                                         int np) {
+    const int c0 = argmax_final_block(keys, 0), c1 = argmax_final_block(keys, 1);
+    if (threadIdx.x == 0) {
+        st[kC0] = c0;
+        st[kC1] = c1;
+    }
+    __syncthreads();
+    finalize_round(st, ref_tok, pattern, hsave, hpart, n, np);
+}
+
+// after the first draft's head (1 column): the candidate
+__global__ __launch_bounds__(256) void first_tail_kernel(int* st, const uint64_t* keys, const int* ref_tok,
+                                                         const uint8_t* pattern) {
+    const int c0 = argmax_final_block(keys, 0);
+    if (threadIdx.x == 0) {
+        st[kC0] = c0;
+        first_candidate(st, ref_tok, pattern);
+    }
 }
 
 // ingest chunk set-up: nc prompt tokens from position st[kPos]; column c is token prompt[pos + c] at pos + c
@@ -542,7 +613,11 @@ enum Head { kHeadAll, kHeadLast, kHeadNone };
 // trunk for nc columns: tokens tok[c] at positions pos[0] + c (pos: see attn_block).  The head (output norm, lm_head,
 // argmax to ints[kV0 + c]) runs on every column, on the last one only (as ints[kV0]; an ingest chunk, qw:2700-2722),
 // or not at all.  The final-normed hidden goes to h / hp (the draft's input, qw:1235-1237).
-int trunk_cols(Engine& e, int nc, const int* tok, const int* pos, float* h, float* hp, Head head) {
+// what follows the lm_head of a decode forward in the same launch as the final norm (see verify_tail_kernel)
+enum Tail { kTailNone, kTailVerify, kTailSingle };
+
+int trunk_cols(Engine& e, int nc, const int* tok, const int* pos, float* h, float* hp, Head head,
+               Tail tail = kTailNone) {
     const auto& c = e.cfg;
     const size_t np = c.n_embd / 4;
     e.q8a_norm = nullptr;
@@ -560,6 +635,17 @@ int trunk_cols(Engine& e, int nc, const int* tok, const int* pos, float* h, floa
         const uint8_t* xq = nullptr;
         RMI_TRY(norm_input(e, e.x, e.part, e.out_norm, first, ncol, &xq));
         RMI_TRY(norm_gemv(e, e.lm_head, xq, e.part + first * np, e.logits, ncol));
+        if (tail != kTailNone) {   // head on every column (nc 1 or 2): tokens, bookkeeping and final norm in one launch
+            auto* keys = static_cast<uint64_t*>(e.argmax_ws);
+            argmax_partial_launch(e.logits, c.n_vocab, nc, c.n_vocab, keys, e.s);
+            const NormOut no{e.x, e.out_norm, e.part, h, hp, c.n_embd, c.eps};
+            const dim3 grid(1 + nc * ((c.n_embd + 255) / 256));
+            if (tail == kTailVerify)
+                hipLaunchKernelGGL(verify_tail_kernel, grid, dim3(256), 0, e.s, e.ints, e.ring, keys, no);
+            else
+                hipLaunchKernelGGL(single_tail_kernel, grid, dim3(256), 0, e.s, e.ints, e.ring, keys, no);
+            return launch_status("decode tail");
+        }
         RMI_TRY(rmi_argmax(e.logits, c.n_vocab, ncol, c.n_vocab, e.ints + kV0, e.argmax_ws, e.s));
     }
     return rmi_rms_norm_out(e.x, e.out_norm, e.part, h, hp, c.n_embd, c.eps, nc, e.s);
@@ -567,13 +653,18 @@ int trunk_cols(Engine& e, int nc, const int* tok, const int* pos, float* h, floa
 
 // trunk for the decode columns: tokens ints[kTok0 + c] at positions ints[kPos] + c, head on every column
 int trunk(Engine& e, int nc) {
-    return trunk_cols(e, nc, e.ints + kTok0, e.ints + kPos, e.hsave, e.hpart, kHeadAll);
+    return trunk_cols(e, nc, e.ints + kTok0, e.ints + kPos, e.hsave, e.hpart, kHeadAll,
+                      nc == 2 ? kTailVerify : kTailSingle);
 }
 
 // draft (nextn) block for nc columns: tokens tok[c] at positions pos[0] + c (pos: see attn_block), previous hidden
 // h / hp.  eh_proj's input = [enorm(emb) | hnorm(h)] per column (embedding first, qw:1327-1332).  Argmax to
 // ints[kC0 + c] when with_head.
-int draft_cols(Engine& e, const int* tok, const int* pos, const float* h, const float* hp, int nc, bool with_head) {
+// what follows the draft's lm_head (with_head): the round's finalize (2 columns) or the first candidate (1)
+enum DraftTail { kDraftFinalize, kDraftFirst };
+
+int draft_cols(Engine& e, const int* tok, const int* pos, const float* h, const float* hp, int nc, bool with_head,
+               DraftTail dtail = kDraftFinalize) {
     const auto& c = e.cfg;
     e.q8a_norm = nullptr;
     RMI_TRY(rmi_embed(e.emb_type, e.tok_embd, tok, e.ex, e.epart, c.n_embd, c.n_vocab, nc, e.s));
@@ -586,12 +677,20 @@ int draft_cols(Engine& e, const int* tok, const int* pos, const float* h, const 
     const uint8_t* xq = nullptr;
     RMI_TRY(norm_input(e, e.dx, e.dpart, e.shnorm, 0, nc, &xq));
     RMI_TRY(norm_gemv(e, e.lm_head, xq, e.dpart, e.logits, nc));
-    return rmi_argmax(e.logits, c.n_vocab, nc, c.n_vocab, e.ints + kC0, e.argmax_ws, e.s);
+    auto* keys = static_cast<uint64_t*>(e.argmax_ws);
+    argmax_partial_launch(e.logits, c.n_vocab, nc, c.n_vocab, keys, e.s);
+    if (dtail == kDraftFinalize)
+        hipLaunchKernelGGL(draft_tail_kernel, dim3(1), dim3(256), 0, e.s, e.ints, keys, e.ref_tok, e.pattern,
+                           e.hsave, e.hpart, c.n_embd, c.n_embd / 4);
+    else
+        hipLaunchKernelGGL(first_tail_kernel, dim3(1), dim3(256), 0, e.s, e.ints, keys, e.ref_tok, e.pattern);
+    return launch_status("draft tail");
 }
 
 // the decode draft: tokens ints[kD0 + c] at positions ints[kDPos] + c
-int draft_block(Engine& e, const float* h, const float* hp, int nc, bool with_head) {
-    return draft_cols(e, e.ints + kD0, e.ints + kDPos, h, hp, nc, with_head);
+int draft_block(Engine& e, const float* h, const float* hp, int nc, bool with_head,
+                DraftTail dtail = kDraftFinalize) {
+    return draft_cols(e, e.ints + kD0, e.ints + kDPos, h, hp, nc, with_head, dtail);
 }
 
 // One ingest chunk of nc prompt tokens from position ints[kPos] (the row-batched serve_ingest_kernels, qw:2192-2502,
@@ -612,29 +711,23 @@ int ingest_chunk(Engine& e, int nc, bool head) {
     return launch_status("chunk_finish");
 }
 
+// the greedy forward of the current token; its tail launch emits the token and advances
 int single_step(Engine& e) {
-    RMI_TRY(trunk(e, 1));
-    hipLaunchKernelGGL(advance_single_kernel, dim3(1), dim3(1), 0, e.s, e.ints, e.ring);
-    return launch_status("advance_single");
+    return trunk(e, 1);
 }
 
+// the verify round: the trunk on (current, candidate), whose tail launch accepts or rejects, then the 2-column draft,
+// whose tail launch picks the next candidate and advances
 int verify_round(Engine& e) {
     RMI_TRY(trunk(e, 2));
-    hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(1), 0, e.s, e.ints, e.ring);
-    RMI_TRY(launch_status("accept"));
-    RMI_TRY(draft_block(e, e.hsave, e.hpart, 2, true));
-    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(256), 0, e.s, e.ints, e.ref_tok, e.pattern, e.hsave, e.hpart,
-                       e.cfg.n_embd, e.cfg.n_embd / 4);
-    return launch_status("finalize");
+    return draft_block(e, e.hsave, e.hpart, 2, true, kDraftFinalize);
 }
 
 // the first candidate: 1-column draft with head of (current token, hidden of the last forward) at the current position
 int first_draft(Engine& e) {
     HIP_TRY(hipMemcpyAsync(e.ints + kD0, e.ints + kTok0, sizeof(int), hipMemcpyDeviceToDevice, e.s));
     HIP_TRY(hipMemcpyAsync(e.ints + kDPos, e.ints + kPos, sizeof(int), hipMemcpyDeviceToDevice, e.s));
-    RMI_TRY(draft_block(e, e.hsave, e.hpart, 1, true));
-    hipLaunchKernelGGL(first_candidate_kernel, dim3(1), dim3(1), 0, e.s, e.ints, e.ref_tok, e.pattern);
-    return launch_status("first_candidate");
+    return draft_block(e, e.hsave, e.hpart, 1, true, kDraftFirst);
 }
 
 template <typename F>

@@ -6,23 +6,10 @@
 //
 // Norm reduction (rms_quant_apply / rms_norm_out): 256 lanes; lane t adds partials t, t+256, t+512, ... in order,
 // then a 64-lane xor butterfly, then the 4 wave sums in order.  Every workgroup derives the same bits.
-#include "rmi_common.h"
+#include "epilogue_dev.h"
 
 namespace rmi {
 namespace {
-
-// sum of a vector's 4-row partials, by the tree of rmi_common.h (norm_load / norm_wave_sum / norm_inv)
-__device__ float block_sum_partials(const float* __restrict__ p, int np) {
-    __shared__ float red[4];
-    NormLoads pv;
-    norm_load(pv, p, np, static_cast<int>(threadIdx.x));
-    const float s = norm_wave_sum(pv, p, np, static_cast<int>(threadIdx.x));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-    __syncthreads();
-    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
-    __syncthreads();
-    return tot;
-}
 
 __device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
 
@@ -79,31 +66,7 @@ __global__ __launch_bounds__(256) void rms_norm_out_kernel(const float* __restri
                                                            const float* __restrict__ partials, float* __restrict__ out,
                                                            float* __restrict__ out_partials, int cols, float eps,
                                                            int out_stride) {
-    const int c = blockIdx.y;
-    x += static_cast<size_t>(c) * cols;
-    partials += static_cast<size_t>(c) * (cols / 4);
-    out += static_cast<size_t>(c) * out_stride;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const float xv = x[min(i, cols - 1)], wv = w[min(i, cols - 1)];   // in flight with the partials
-    const float ss = block_sum_partials(partials, cols / 4);
-    const float inv = rsqrtf(ss / static_cast<float>(cols) + eps);
-    float v = 0.0f;
-    if (i < cols) {
-        v = (xv * wv) * inv;
-        out[i] = v;
-    }
-    if (out_partials) {
-        // the 4 rows of a partial slot are 4 consecutive lanes: gather them in row order on the first lane
-        const float v0 = quad_lane<0>(v), v1 = quad_lane<1>(v), v2 = quad_lane<2>(v), v3 = quad_lane<3>(v);
-        if ((threadIdx.x & 3) == 0 && i < cols) {
-            float p = 0.0f;
-            p = __builtin_fmaf(v0, v0, p);
-            if (i + 1 < cols) p = __builtin_fmaf(v1, v1, p);
-            if (i + 2 < cols) p = __builtin_fmaf(v2, v2, p);
-            if (i + 3 < cols) p = __builtin_fmaf(v3, v3, p);
-            out_partials[static_cast<size_t>(c) * ((cols + 3) / 4) + i / 4] = p;
-        }
-    }
+    rms_norm_out_block(x, w, partials, out, out_partials, cols, eps, out_stride, blockIdx.y, blockIdx.x);
 }
 
 // partials[g] = sum of squares of rows 4g..4g+3 (reference row_sum_partials_kernel, qw:616-623); optionally x += o
@@ -181,29 +144,7 @@ __global__ __launch_bounds__(64) void beta_gate_kernel(float* __restrict__ ab, c
     ggate[static_cast<size_t>(c) * n + i] = (v > 20.0f ? v : log1pf(expf(v))) * ssm_a[i];
 }
 
-// ---- argmax: lowest index wins ties (qw:70-94: monotonic float bits, n-1-idx packing) -------------------------------
-__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
-    uint32_t b = __float_as_uint(v);
-    b ^= (b >> 31) ? 0xffffffffu : 0x80000000u;
-    return (static_cast<uint64_t>(b) << 32) | static_cast<uint32_t>(0x7fffffff - idx);
-}
-
-__device__ __forceinline__ uint64_t key_max64(uint64_t k) {
-    auto step = [&](uint32_t lo, uint32_t hi) {
-        const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
-        k = o > k ? o : k;
-    };
-    step(xor_lane<32>(static_cast<uint32_t>(k)), xor_lane<32>(static_cast<uint32_t>(k >> 32)));
-    step(xor_lane<16>(static_cast<uint32_t>(k)), xor_lane<16>(static_cast<uint32_t>(k >> 32)));
-    step(xor_lane<8>(static_cast<uint32_t>(k)), xor_lane<8>(static_cast<uint32_t>(k >> 32)));
-    step(xor_lane<4>(static_cast<uint32_t>(k)), xor_lane<4>(static_cast<uint32_t>(k >> 32)));
-    step(xor_lane<2>(static_cast<uint32_t>(k)), xor_lane<2>(static_cast<uint32_t>(k >> 32)));
-    step(xor_lane<1>(static_cast<uint32_t>(k)), xor_lane<1>(static_cast<uint32_t>(k >> 32)));
-    return k;
-}
-
-constexpr int kArgmaxBlocks = 256;
-
+// ---- argmax: lowest index wins ties (qw:70-94: monotonic float bits, n-1-idx packing; keys in epilogue_dev.h) -----
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ l, int n, int col_stride,
                                                              uint64_t* __restrict__ part) {
     __shared__ uint64_t red[4];
@@ -235,17 +176,8 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
 }
 
 __global__ __launch_bounds__(256) void argmax_final_kernel(const uint64_t* __restrict__ part, int* __restrict__ out) {
-    __shared__ uint64_t red[4];
-    const int c = blockIdx.x;
-    uint64_t best = part[static_cast<size_t>(c) * kArgmaxBlocks + threadIdx.x];
-    best = key_max64(best);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint64_t m = red[0];
-        for (int i = 1; i < 4; ++i) m = red[i] > m ? red[i] : m;
-        out[c] = 0x7fffffff - static_cast<int>(static_cast<uint32_t>(m));
-    }
+    const int r = argmax_final_block(part, blockIdx.x);
+    if (threadIdx.x == 0) out[blockIdx.x] = r;
 }
 
 // ---- token embedding: device dequant of one row per token ---------------------------------------------------------
@@ -423,6 +355,12 @@ extern "C" int rmi_beta_gate(float* beta_alpha, const float* dt, const float* ss
     return launch_status("beta_gate");
 }
 
+namespace rmi {
+void argmax_partial_launch(const float* logits, int n, int ncols, int col_stride, uint64_t* part, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxBlocks, ncols), dim3(256), 0, s, logits, n, col_stride, part);
+}
+}  // namespace rmi
+
 extern "C" size_t rmi_argmax_workspace_bytes(int ncols) {
     return static_cast<size_t>(ncols > 0 ? ncols : 1) * kArgmaxBlocks * sizeof(uint64_t);
 }
@@ -433,8 +371,7 @@ extern "C" int rmi_argmax(const float* logits, int n, int ncols, int col_stride,
     if (!aligned4(logits) || !aligned4(out_idx) || !workspace || (reinterpret_cast<uintptr_t>(workspace) & 7u))
         return fail(RMI_ERR_POINTER, "argmax: null or misaligned pointer");
     auto* part = static_cast<uint64_t*>(workspace);
-    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxBlocks, ncols), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), logits, n, col_stride, part);
+    argmax_partial_launch(logits, n, ncols, col_stride, part, static_cast<hipStream_t>(stream));
     hipLaunchKernelGGL(argmax_final_kernel, dim3(ncols), dim3(256), 0, static_cast<hipStream_t>(stream), part, out_idx);
     return launch_status("argmax");
 }
