@@ -237,3 +237,61 @@ def test_gguf_entry_points_bitwise_equal_packed(orc, rmi, n_in, n_out, ncols):
         assert np.array_equal(yh[sl].view(np.uint32), host(y1).view(np.uint32)), f"plain column {c}"
         assert np.array_equal(yrh[sl].view(np.uint32), host(y1r).view(np.uint32)), f"residual column {c}"
         assert np.array_equal(ph[c * np_:(c + 1) * np_].view(np.uint32), host(p1).view(np.uint32)), f"partials {c}"
+
+
+def exact_q6k(n_out, n_in, seed):
+    """Q6_K rows whose GEMV epilogue is exact in fp32: block scale d = 1, sub-scales in [-3, 3], codes 16..47 (every
+    qh field 1 or 2, the ql nibbles free), so each output is an integer below 2^24 when the activations are bounded"""
+    rng = np.random.default_rng(seed)
+    nb = n_out * (n_in // 256)
+    blk = np.empty((nb, 210), np.uint8)
+    blk[:, :128] = rng.integers(0, 256, size=(nb, 128), dtype=np.uint8)
+    f = rng.integers(1, 3, size=(nb, 64, 4), dtype=np.uint8)
+    blk[:, 128:192] = f[..., 0] | (f[..., 1] << 2) | (f[..., 2] << 4) | (f[..., 3] << 6)
+    blk[:, 192:208] = rng.integers(-3, 4, size=(nb, 16)).astype(np.int8).view(np.uint8)
+    blk[:, 208:210] = np.array([1.0], np.float16).view(np.uint8)
+    return blk.reshape(-1)
+
+
+def exact_q8_1(n_in, ncols, bound, seed):
+    """Q8_1 columns with d = 1 and codes in [-bound, bound] (the stored sum is the codes' sum)"""
+    rng = np.random.default_rng(seed)
+    nb = ncols * (n_in // 32)
+    q = rng.integers(-bound, bound + 1, size=(nb, 32)).astype(np.int8)
+    blk = np.empty((nb, 36), np.uint8)
+    blk[:, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    blk[:, 2:4] = q.astype(np.float32).sum(axis=1).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    blk[:, 4:] = q.view(np.uint8)
+    return blk.reshape(-1)
+
+
+@pytest.mark.parametrize("n_in,n_out", [(4096, 12352), (4096, 4096), (12288, 4096), (8192, 4096), (4096, 24576),
+                                        (12288, 1001)])
+@pytest.mark.parametrize("ncols", [1, 2, 8, 16])
+def test_engine_gemvs_integer_exact(orc, rmi, n_in, n_out, ncols):
+    """The engine's GEMV kernels themselves against the oracle's exact integer block dots (the closed form of the
+    Q6_K x Q8_1 dot, pinned in tests/test_oracle.py): with every fp32 scale 1 and the sums below 2^24, each output is
+    the integer sum of its row's block dots, bit for bit - the packed decode kernels (1 / 2 columns), the MFMA ingest
+    kernel (8 / 16 columns), the GGUF-layout stream kernel and the residual variants; a wrong code, sub-scale or
+    correction index changes an integer"""
+    bound = min(63, (1 << 24) // ((n_in // 32) * 2 * 16 * 16 * 3))
+    w = exact_q6k(n_out, n_in, seed=n_in + 7 * n_out)
+    xq = exact_q8_1(n_in, ncols, bound, seed=ncols + n_out)
+    xcol = (n_in // 32) * 36
+    want = np.stack([orc.q6k_block_dots(w, xq[c * xcol:(c + 1) * xcol], n_in, n_out).astype(np.int64).sum(axis=1)
+                     for c in range(ncols)])
+    assert np.abs(want).max() < (1 << 24)
+    want = want.astype(np.float32).reshape(-1)
+    wd, xd = dev(w), dev(xq)
+    wp = packed(rmi, wd, n_in, n_out)
+    y = empty(ncols * n_out)
+    rmi.native_q6_k_mmvq_packed(wp, xd, y, n_in, n_out, ncols)
+    assert np.array_equal(host(y), want), "packed"
+    yg = empty(ncols * n_out)
+    rmi.native_q6_k_mmvq(wd, xd, yg, n_in, n_out, ncols)
+    assert np.array_equal(host(yg), want), "GGUF layout"
+    res = np.random.default_rng(n_out).integers(-1000, 1001, size=ncols * n_out).astype(np.float32)
+    yr = dev(res.copy())
+    part = empty(ncols * ((n_out + 3) // 4))
+    rmi.native_q6_k_mmvq_packed_res_n(wp, xd, yr, yr, part, n_in, n_out, ncols)
+    assert np.array_equal(host(yr), want + res), "packed residual"
