@@ -1003,8 +1003,8 @@ constexpr int kMfmaNormLoads = 4;
 // weights twice, and the fma chain over the chunks runs in the same order.
 // LE: the quad's row sums through LDS - each lane parks its 4 x NCW (row, column group) sums of its half-block, and
 // lane (row i, group g, column jj) adds its 16 half-blocks in the xor butterfly's tree (bitwise hb_sum), then owns one
-// output: ~60 instructions per quad where the 16 in-register butterflies take ~300.  Needs 4 KB x NCW of LDS per wave
-// after the stage.
+// output: ~60 instructions per quad where the 16 in-register butterflies take ~300.  Needs 4 KB x NCW of LDS per wave:
+// after the stage, or with two K halves the stage itself once every wave is past its last chunk.
 template <int NCG, bool RES, int D, bool INV = false, int CS = 1, int KP = 1, int NCHK = 0, bool LE = false>
 __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t* __restrict__ wp,
                                                                    const uint8_t* __restrict__ x, float* y,
