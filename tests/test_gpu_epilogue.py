@@ -193,3 +193,34 @@ def test_q8_0_gemv(orc, rmi, n_in, n_out, ncols):
     ref, pref = orc.q8_0_gemv(w, xq[:n_in // 32 * 36], n_in, n_out, res=res, partials=True)
     assert_close_rel(host(yr), ref, what="q8_0 res")
     assert_close_rel(host(pr), pref, rtol=1e-5, atol_frac=1e-6, what="q8_0 partials")
+
+
+@pytest.mark.parametrize("n_in,n_out,ncols", [(4096, 1000, 2), (12288, 257, 1)])
+def test_q8_0_gemv_integer_exact(orc, rmi, n_in, n_out, ncols):
+    """the Q8_0 GEMV on blocks whose every fp32 step is exact (weight and activation scales 1, codes bounded so the
+    sums stay below 2^24): bitwise the oracle's exact-integer fp64 GEMV, plain and with the residual"""
+    rng = np.random.default_rng(n_in + n_out)
+    nb = n_out * (n_in // 32)
+    wb = np.empty((nb, 34), np.uint8)
+    wb[:, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    wb[:, 2:] = rng.integers(-127, 128, size=(nb, 32)).astype(np.int8).view(np.uint8)
+    w = wb.reshape(-1)
+    bound = min(63, (1 << 24) // (n_in * 127))
+    xb = np.empty((ncols * (n_in // 32), 36), np.uint8)
+    q = rng.integers(-bound, bound + 1, size=(xb.shape[0], 32)).astype(np.int8)
+    xb[:, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    xb[:, 2:4] = q.astype(np.float32).sum(axis=1).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    xb[:, 4:] = q.view(np.uint8)
+    xq = xb.reshape(-1)
+    ref = orc.q8_0_gemv(w, xq, n_in, n_out, ncols=ncols)
+    assert np.all(ref == np.round(ref)) and np.abs(ref).max() < (1 << 24)
+    y = empty(ncols * n_out)
+    dw, dxq = dev(w), dev(xq)
+    rmi._call("rmi_native_mmvq", 8, rmi._p(dw), rmi._p(dxq), rmi._p(y), n_in, n_out, ncols, rmi._stream(None))
+    assert np.array_equal(host(y), ref.astype(np.float32))
+    res = rng.integers(-1000, 1001, size=n_out).astype(np.float32)
+    yr, pr = dev(res.copy()), empty((n_out + 3) // 4)
+    dx1 = dev(xq[:n_in // 32 * 36])
+    rmi._call("rmi_native_q8_0_mmvq_res", rmi._p(dw), rmi._p(dx1), rmi._p(yr), rmi._p(yr), rmi._p(pr), n_in, n_out,
+              rmi._stream(None))
+    assert np.array_equal(host(yr), ref[:n_out].astype(np.float32) + res)
