@@ -157,6 +157,11 @@ int rmi_q6_k_block_dots(const void* w, const void* x_q8_1, int32_t* out, int n_i
 /* Q8_1 of (x * w) * rsqrt(sum(partials) / cols + eps).  Replaces rms_quant_apply_kernel (qw:627-655). */
 int rmi_rms_quant_apply(const float* x, const float* w, const float* partials, void* y_q8_1, int cols, float eps,
                         int ncols, void* stream);
+/* No counterpart in the reference: rmi_row_sum_partials(x) followed by rmi_rms_quant_apply, in one launch and with the
+ * same bytes - each workgroup forms the 4-row partials from x itself.  For a vector whose partials no GEMV epilogue
+ * wrote (x 16-byte aligned). */
+int rmi_rms_quant_apply_self(const float* x, const float* w, void* y_q8_1, int cols, float eps, int ncols,
+                             void* stream);
 /* Two rmi_rms_quant_apply results of cols each into the two halves of one 2 cols Q8_1 row per column (x0 -> blocks
  * [0, cols/32), x1 -> [cols/32, cols/16)).  No counterpart in the reference: it replaces its two rms_norm_out calls
  * and the quantize of their concatenation in the draft's input (qw:1327-1332), with the same bits. */

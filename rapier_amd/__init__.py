@@ -42,6 +42,7 @@ SIGNATURES = {
     "rmi_q6_k_pack": (_i, [_vp, _vp, _i, _i, _vp]),
     "rmi_q6_k_pack_swiglu": (_i, [_vp, _vp, _i, _i, _vp]),
     "rmi_native_q6_k_swiglu_packed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_rms_quant_apply_self": (_i, [_vp, _vp, _vp, _i, _f, _i, _vp]),
     "rmi_native_q6_k_mmvq_packed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_packed_res_n": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_q6_k_block_dots": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
@@ -282,6 +283,11 @@ def stream_read(buf, nbytes: int, grid: int, out, stream=None):
 
 def rms_quant_apply(x, w, partials, y_q8_1, cols, eps, ncols=1, stream=None):
     _call("rmi_rms_quant_apply", _p(x), _p(w), _p(partials), _p(y_q8_1), cols, eps, ncols, _stream(stream))
+
+
+def rms_quant_apply_self(x, w, y_q8_1, cols, eps, ncols=1, stream=None):
+    """row_sum_partials(x) + rms_quant_apply in one launch (same bytes)"""
+    _call("rmi_rms_quant_apply_self", _p(x), _p(w), _p(y_q8_1), cols, eps, ncols, _stream(stream))
 
 
 def rms_quant_apply_pair(x0, w0, partials0, x1, w1, partials1, y_q8_1, cols, eps, ncols=1, stream=None):

@@ -108,6 +108,9 @@ struct Engine {
     // Q8_1(x * w) and scales its rows by inv.  q8a_norm: the norm weights whose Q8_1(x * w) the last residual GEMV's
     // epilogue left in q8a (columns 0..), so the norm site skips its quantize launch.
     bool fold = false;
+    // the next norm forms its vector's partials itself (rmi_rms_quant_apply_self): the draft's eh_proj output, whose
+    // partials no GEMV epilogue writes
+    bool norm_self = false;
     const float* q8a_norm = nullptr;
     hipStream_t s = nullptr;
     bool own_stream = false;
@@ -529,6 +532,10 @@ int norm_input(Engine& e, const float* x, const float* part, const float* w, int
     }
     *xq = e.q8a;
     if (e.fold) return rmi_quantize_q8_1_weighted(x + xs, w, e.q8a, c.n_embd, nc, e.s);
+    if (e.norm_self) {
+        e.norm_self = false;
+        return rmi_rms_quant_apply_self(x + xs, w, e.q8a, c.n_embd, c.eps, nc, e.s);
+    }
     return rmi_rms_quant_apply(x + xs, w, part + ps, e.q8a, c.n_embd, c.eps, nc, e.s);
 }
 
@@ -671,7 +678,10 @@ int draft_cols(Engine& e, const int* tok, const int* pos, const float* h, const 
     // [enorm(emb) | hnorm(h)] straight into the Q8_1 row of eh_proj's input: the bits of norm, norm, quantize
     RMI_TRY(rmi_rms_quant_apply_pair(e.ex, e.enorm, e.epart, h, e.hnorm, hp, e.q8f, c.n_embd, c.eps, nc, e.s));
     RMI_TRY(gemv(e, e.eh_proj, e.q8f, e.dx, nc));
-    RMI_TRY(rmi_row_sum_partials(e.dx, e.dpart, c.n_embd, nc, e.s));
+    // dx's partials: formed by the draft layer's first norm itself (one launch fewer), or here for the folded norms'
+    // scaled GEMV, which reads them
+    if (e.fold) RMI_TRY(rmi_row_sum_partials(e.dx, e.dpart, c.n_embd, nc, e.s));
+    else e.norm_self = true;
     RMI_TRY(attn_block(e, e.draft, e.dx, e.dpart, pos, nc, with_head ? e.shnorm : nullptr));
     if (!with_head) return RMI_OK;
     const uint8_t* xq = nullptr;

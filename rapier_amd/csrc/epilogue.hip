@@ -35,6 +35,47 @@ __global__ __launch_bounds__(256) void rms_quant_apply_kernel(const float* __res
                      y + static_cast<size_t>(c) * (cols / 32) * kQ8_1Bytes, cols, eps);
 }
 
+// rms_quant_apply_kernel with the partials formed from x in the workgroup (slot g = the fma chain of rows 4g..4g+3
+// in row order, as row_sum_partials writes it), then the same tree: the bits of row_sum_partials + rms_quant_apply
+// without the partials launch.  x 16-byte aligned, cols a multiple of 32.
+__device__ __forceinline__ float block_sum_self(const float* __restrict__ x, int cols) {
+    __shared__ float red[4];
+    const int np = cols / 4, t = static_cast<int>(threadIdx.x);
+    float4 v[kNormLoads];
+#pragma unroll
+    for (int k = 0; k < kNormLoads; ++k) v[k] = reinterpret_cast<const float4*>(x)[min(t + 256 * k, np - 1)];
+    auto slot = [](const float4 q) {
+        float p = __builtin_fmaf(q.x, q.x, 0.0f);
+        p = __builtin_fmaf(q.y, q.y, p);
+        p = __builtin_fmaf(q.z, q.z, p);
+        return __builtin_fmaf(q.w, q.w, p);
+    };
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormLoads; ++k)
+        if (t + 256 * k < np) s += slot(v[k]);
+    for (int i = t + 256 * kNormLoads; i < np; i += 256) s += slot(reinterpret_cast<const float4*>(x)[i]);
+    s = group_sum<64>(s);
+    if ((t & 63) == 0) red[t >> 6] = s;
+    __syncthreads();
+    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+    __syncthreads();
+    return tot;
+}
+
+__global__ __launch_bounds__(256) void rms_quant_self_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                             uint8_t* __restrict__ y, int cols, float eps) {
+    const int c = blockIdx.y;
+    x += static_cast<size_t>(c) * cols;
+    y += static_cast<size_t>(c) * (cols / 32) * kQ8_1Bytes;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const float xv = x[min(i, cols - 1)], wv = w[min(i, cols - 1)];
+    const float ss = block_sum_self(x, cols);
+    const float inv = rsqrtf(ss / static_cast<float>(cols) + eps);
+    if (i >= cols) return;   // cols % 32 == 0: whole 32-lane groups leave together
+    q8_1_store_lane((xv * wv) * inv, y + static_cast<size_t>(i / 32) * kQ8_1Bytes);
+}
+
 // Q8_1 of x * w, no inv: a folded norm's GEMV input where no residual GEMV epilogue makes it (the same fp32 product and
 // quantizer as that epilogue, so the same bytes); the GEMV scales its rows by inv
 __global__ __launch_bounds__(256) void quant_weighted_kernel(const float* __restrict__ x, const float* __restrict__ w,
@@ -257,6 +298,16 @@ extern "C" int rmi_rms_quant_apply(const float* x, const float* w, const float* 
     hipLaunchKernelGGL(rms_quant_apply_kernel, dim3((cols + 255) / 256, ncols), dim3(256), 0,
                        static_cast<hipStream_t>(stream), x, w, partials, static_cast<uint8_t*>(y_q8_1), cols, eps);
     return launch_status("rms_quant_apply");
+}
+
+extern "C" int rmi_rms_quant_apply_self(const float* x, const float* w, void* y_q8_1, int cols, float eps, int ncols,
+                                        void* stream) {
+    if (cols <= 0 || cols % 32 != 0 || bad_cols(ncols)) return fail(RMI_ERR_SHAPE, "rms_quant_apply_self: bad shape");
+    if (!aligned16(x) || !aligned4(w) || !aligned4(y_q8_1))
+        return fail(RMI_ERR_POINTER, "rms_quant_apply_self: null or misaligned pointer");
+    hipLaunchKernelGGL(rms_quant_self_kernel, dim3((cols + 255) / 256, ncols), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, w, static_cast<uint8_t*>(y_q8_1), cols, eps);
+    return launch_status("rms_quant_apply_self");
 }
 
 extern "C" int rmi_quantize_q8_1_weighted(const float* x, const float* w, void* y_q8_1, int cols, int ncols,

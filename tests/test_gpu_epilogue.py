@@ -224,3 +224,20 @@ def test_q8_0_gemv_integer_exact(orc, rmi, n_in, n_out, ncols):
     rmi._call("rmi_native_q8_0_mmvq_res", rmi._p(dw), rmi._p(dx1), rmi._p(yr), rmi._p(yr), rmi._p(pr), n_in, n_out,
               rmi._stream(None))
     assert np.array_equal(host(yr), ref[:n_out].astype(np.float32) + res)
+
+
+@pytest.mark.parametrize("cols,ncols", [(4096, 2), (12288, 1), (8192, 3)])
+def test_rms_quant_apply_self_equals_partials_then_norm(orc, rmi, cols, ncols):
+    """rmi_rms_quant_apply_self (the partials formed in the workgroup) == rmi_row_sum_partials then
+    rmi_rms_quant_apply, Q8_1 bytes"""
+    x = orc.normal(ncols * cols, seed=cols + ncols)
+    x[:32] *= 1e4
+    w = (1 + orc.normal(cols, seed=9, std=0.1)).astype(np.float32)
+    xd, wd = dev(x), dev(w)
+    part = empty(ncols * (cols // 4))
+    rmi.row_sum_partials(xd, part, cols, ncols)
+    ref = empty(rmi.native_q8_1_bytes(cols, ncols), "uint8")
+    rmi.rms_quant_apply(xd, wd, part, ref, cols, 1e-6, ncols)
+    got = empty(rmi.native_q8_1_bytes(cols, ncols), "uint8")
+    rmi.rms_quant_apply_self(xd, wd, got, cols, 1e-6, ncols)
+    assert np.array_equal(host(got), host(ref))
