@@ -205,6 +205,12 @@ int rmi_topk(const float* logits, int n, int k, int* out_idx, float* out_val, vo
  * (qw:109-115, 1418-1430); Q3_K and IQ4_XS tables are RMI_ERR_UNSUPPORTED. */
 int rmi_embed(int type, const void* emb, const int* tokens, float* x, float* partials, int n_embd, int n_vocab,
               int ncols, void* stream);
+/* rmi_embed of tokens[c] followed by rmi_rms_quant_apply_pair(emb rows, w0, their partials, x1, w1, partials1) in
+ * one launch: the same Q8_1 bytes, without the fp32 embedding rows in HBM.  The draft's input (eh_proj over
+ * [enorm(emb) | hnorm(h)], qw:1327-1332); cols a multiple of 256. */
+int rmi_embed_quant_apply_pair(int type, const void* emb, const int* tokens, const float* w0, const float* x1,
+                               const float* w1, const float* partials1, void* y_q8_1, int cols, int n_vocab, float eps,
+                               int ncols, void* stream);
 /* rmi_embed with type 14 */
 int rmi_embed_q6_k(const void* emb, const int* tokens, float* x, float* partials, int n_embd, int n_vocab, int ncols,
                    void* stream);

@@ -76,6 +76,7 @@ SIGNATURES = {
     "rmi_topk": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
     "rmi_embed_q6_k": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_embed": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rmi_embed_quant_apply_pair": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _f, _i, _vp]),
     "rmi_fused_gdn_conv_l2": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
     "rmi_fused_gdn_step_norm_silu_q8": (_i, [_vp] * 8 + [_f, _vp, _vp, _i, _i, _vp]),
     "rmi_gdn_layer_tokens": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _i, _vp,
@@ -358,6 +359,13 @@ def embed_q6_k(emb, tokens, x, partials, n_embd, n_vocab, ncols=1, stream=None):
 def embed(ggml_type, emb, tokens, x, partials, n_embd, n_vocab, ncols=1, stream=None):
     """token rows of a GGUF type 14 (Q6_K) / 13 (Q5_K) / 12 (Q4_K) table, dequantized on the device"""
     _call("rmi_embed", ggml_type, _p(emb), _p(tokens), _p(x), _p(partials), n_embd, n_vocab, ncols, _stream(stream))
+
+
+def embed_quant_apply_pair(ggml_type, emb, tokens, w0, x1, w1, partials1, y_q8_1, cols, n_vocab, eps, ncols=1,
+                           stream=None):
+    """embed + rms_quant_apply_pair(embedding rows, w0, .., x1, w1, partials1) in one launch (same bytes)"""
+    _call("rmi_embed_quant_apply_pair", ggml_type, _p(emb), _p(tokens), _p(w0), _p(x1), _p(w1), _p(partials1),
+          _p(y_q8_1), cols, n_vocab, eps, ncols, _stream(stream))
 
 
 # ---- Gated DeltaNet (fgdn:40-133) ----------------------------------------------------------------------------------

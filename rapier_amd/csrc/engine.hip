@@ -142,7 +142,7 @@ struct Engine {
     // writes its hidden to columns 1..nc, so that column c - 1 is the draft input of column c
     float *x = nullptr, *part = nullptr, *proj = nullptr, *ug = nullptr, *y = nullptr, *logits = nullptr;
     float *hsave = nullptr, *hpart = nullptr, *hzero = nullptr, *pzero = nullptr, *qbuf = nullptr;
-    float *ex = nullptr, *epart = nullptr, *dx = nullptr, *dpart = nullptr;
+    float *dx = nullptr, *dpart = nullptr;
     uint8_t *q8a = nullptr, *q8f = nullptr, *q8y = nullptr;
     void *attn_ws = nullptr, *argmax_ws = nullptr, *topk_ws = nullptr;
     unsigned long long* gdn_xch = nullptr;   // the split GDN step's exchange words (rmi_gdn_exchange_bytes), zeroed once
@@ -674,9 +674,10 @@ int draft_cols(Engine& e, const int* tok, const int* pos, const float* h, const 
                DraftTail dtail = kDraftFinalize) {
     const auto& c = e.cfg;
     e.q8a_norm = nullptr;
-    RMI_TRY(rmi_embed(e.emb_type, e.tok_embd, tok, e.ex, e.epart, c.n_embd, c.n_vocab, nc, e.s));
-    // [enorm(emb) | hnorm(h)] straight into the Q8_1 row of eh_proj's input: the bits of norm, norm, quantize
-    RMI_TRY(rmi_rms_quant_apply_pair(e.ex, e.enorm, e.epart, h, e.hnorm, hp, e.q8f, c.n_embd, c.eps, nc, e.s));
+    // [enorm(emb) | hnorm(h)] straight into the Q8_1 row of eh_proj's input, the embedding rows dequantized in the
+    // same launch: the bits of embed, norm, norm, quantize
+    RMI_TRY(rmi_embed_quant_apply_pair(e.emb_type, e.tok_embd, tok, e.enorm, h, e.hnorm, hp, e.q8f, c.n_embd,
+                                       c.n_vocab, c.eps, nc, e.s));
     RMI_TRY(gemv(e, e.eh_proj, e.q8f, e.dx, nc));
     // dx's partials: formed by the draft layer's first norm itself (one launch fewer), or here for the folded norms'
     // scaled GEMV, which reads them
@@ -1148,8 +1149,6 @@ int alloc_runtime(Engine& e) {
     RMI_TRY(zero_f32(e, e.hzero, c.n_embd));
     RMI_TRY(zero_f32(e, e.pzero, np));
     RMI_TRY(e.alloc(&e.qbuf, K * e.attn_q));
-    RMI_TRY(e.alloc(&e.ex, K * c.n_embd));
-    RMI_TRY(e.alloc(&e.epart, K * np));
     RMI_TRY(e.alloc(&e.dx, K * c.n_embd));
     RMI_TRY(e.alloc(&e.dpart, K * np));
     RMI_TRY(e.alloc(&e.q8a, K * q81_bytes(c.n_embd)));

@@ -427,6 +427,70 @@ extern "C" int rmi_argmax(const float* logits, int n, int ncols, int col_stride,
     return launch_status("argmax");
 }
 
+// The draft input in one launch: blockIdx.z = 0 norms the embedding row of token tok[c] (dequantized here; each lane
+// forms the partial slots the norm tree gives it, 4 elements each, as embed_kernel writes them), z = 1 the hidden
+// vector b (its partials given) - the bits of rmi_embed followed by rmi_rms_quant_apply_pair.
+template <int TYPE>
+__global__ __launch_bounds__(256) void embed_quant_pair_kernel(const uint8_t* __restrict__ emb,
+                                                               const int* __restrict__ tok, const float* __restrict__ w0,
+                                                               NormInput b, uint8_t* __restrict__ y, int cols,
+                                                               int n_vocab, float eps) {
+    constexpr int kBytes = TYPE == 14 ? kQ6KBytes : TYPE == 13 ? 176 : 144;
+    const int c = blockIdx.y;
+    uint8_t* yc = y + (static_cast<size_t>(c) * 2 + blockIdx.z) * (cols / 32) * kQ8_1Bytes;
+    if (blockIdx.z == 1) {
+        rms_quant_column(b.x + static_cast<size_t>(c) * cols, b.w, b.partials + static_cast<size_t>(c) * (cols / 4), yc,
+                         cols, eps);
+        return;
+    }
+    __shared__ float red[4];
+    int t = tok[c];
+    t = t < 0 ? 0 : (t >= n_vocab ? n_vocab - 1 : t);   // as embed_kernel: never outside the table
+    const uint8_t* row = emb + static_cast<size_t>(t) * (cols / 256) * kBytes;
+    const int lane = static_cast<int>(threadIdx.x), i = blockIdx.x * 256 + lane;
+    const float wv = w0[min(i, cols - 1)];
+    const float v = embed_value<TYPE>(row + static_cast<size_t>(i / 256) * kBytes, i & 255);
+    // the norm tree over the row's partial slots g = lane + 256 k (elements 4g .. 4g + 3)
+    const int np = cols / 4;
+    float s = 0.0f;
+    for (int g = lane; g < np; g += 256) {
+        float p = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int e = 4 * g + r;
+            const float u = embed_value<TYPE>(row + static_cast<size_t>(e / 256) * kBytes, e & 255);
+            p = __builtin_fmaf(u, u, p);
+        }
+        s += p;
+    }
+    s = group_sum<64>(s);
+    if ((lane & 63) == 0) red[lane >> 6] = s;
+    __syncthreads();
+    const float inv = rsqrtf((((red[0] + red[1]) + red[2]) + red[3]) / static_cast<float>(cols) + eps);
+    if (i >= cols) return;   // cols % 256 == 0 here: whole workgroups
+    q8_1_store_lane((v * wv) * inv, yc + static_cast<size_t>(i / 32) * kQ8_1Bytes);
+}
+
+extern "C" int rmi_embed_quant_apply_pair(int type, const void* emb, const int* tokens, const float* w0,
+                                          const float* x1, const float* w1, const float* partials1, void* y_q8_1,
+                                          int cols, int n_vocab, float eps, int ncols, void* stream) {
+    if (cols <= 0 || cols % 256 != 0 || n_vocab <= 0 || bad_cols(ncols))
+        return fail(RMI_ERR_SHAPE, "embed_quant_apply_pair: bad shape");
+    if (type != 14 && type != 13 && type != 12) return fail(RMI_ERR_UNSUPPORTED, "embed_quant_apply_pair: type");
+    if (!emb || !aligned4(tokens) || !aligned4(w0) || !aligned4(x1) || !aligned4(w1) || !aligned4(partials1) ||
+        !aligned4(y_q8_1))
+        return fail(RMI_ERR_POINTER, "embed_quant_apply_pair: null or misaligned pointer");
+    const auto* e = static_cast<const uint8_t*>(emb);
+    auto* y = static_cast<uint8_t*>(y_q8_1);
+    const dim3 grid(cols / 256, ncols, 2), block(256);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const NormInput b{x1, w1, partials1};
+    if (type == 14) hipLaunchKernelGGL(embed_quant_pair_kernel<14>, grid, block, 0, s, e, tokens, w0, b, y, cols, n_vocab, eps);
+    else if (type == 13) hipLaunchKernelGGL(embed_quant_pair_kernel<13>, grid, block, 0, s, e, tokens, w0, b, y, cols, n_vocab, eps);
+    else hipLaunchKernelGGL(embed_quant_pair_kernel<12>, grid, block, 0, s, e, tokens, w0, b, y, cols, n_vocab, eps);
+    return launch_status("embed_quant_apply_pair");
+}
+
 extern "C" int rmi_embed(int type, const void* emb, const int* tokens, float* x, float* partials, int n_embd,
                          int n_vocab, int ncols, void* stream) {
     if (n_embd <= 0 || n_embd % 256 != 0 || n_vocab <= 0 || bad_cols(ncols))

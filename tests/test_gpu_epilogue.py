@@ -241,3 +241,28 @@ def test_rms_quant_apply_self_equals_partials_then_norm(orc, rmi, cols, ncols):
     got = empty(rmi.native_q8_1_bytes(cols, ncols), "uint8")
     rmi.rms_quant_apply_self(xd, wd, got, cols, 1e-6, ncols)
     assert np.array_equal(host(got), host(ref))
+
+
+@pytest.mark.parametrize("ggml_type,cols,ncols", [(14, 4096, 2), (14, 4096, 1), (13, 1024, 3), (12, 2048, 2)])
+def test_embed_quant_apply_pair_equals_embed_then_pair(orc, rmi, ggml_type, cols, ncols):
+    """rmi_embed_quant_apply_pair (the embedding rows dequantized and their partials formed in the norm's workgroups)
+    == rmi_embed then rmi_rms_quant_apply_pair, Q8_1 bytes; an out-of-range id clamps as in rmi_embed"""
+    from tests.kquant import k_blocks
+    n_vocab = 50
+    if ggml_type == 14:
+        emb = orc.gen_q6k(n_vocab, cols, seed=cols)
+    else:
+        emb, _ = k_blocks(np.random.default_rng(cols), n_vocab * cols // 256, ggml_type == 13)
+    toks = np.array([3, 49, 1000][:ncols], dtype=np.int32)
+    h = orc.normal(ncols * cols, seed=ncols, std=3.0)
+    we = (1 + orc.normal(cols, seed=13, std=0.1)).astype(np.float32)
+    wh = (1 + orc.normal(cols, seed=14, std=0.1)).astype(np.float32)
+    ph = np.concatenate([orc.row_sum_partials(h[c * cols:(c + 1) * cols]) for c in range(ncols)]).astype(np.float32)
+    ed, td, hd, wed, whd, phd = dev(emb), dev(toks), dev(h), dev(we), dev(wh), dev(ph)
+    x, p = empty(ncols * cols), empty(ncols * cols // 4)
+    rmi.embed(ggml_type, ed, td, x, p, cols, n_vocab, ncols)
+    ref = empty(ncols * 2 * cols // 32 * 36, "uint8")
+    rmi.rms_quant_apply_pair(x, wed, p, hd, whd, phd, ref, cols, 1e-6, ncols=ncols)
+    got = empty(ncols * 2 * cols // 32 * 36, "uint8")
+    rmi.embed_quant_apply_pair(ggml_type, ed, td, wed, hd, whd, phd, got, cols, n_vocab, 1e-6, ncols)
+    assert np.array_equal(host(got), host(ref))
