@@ -619,6 +619,11 @@ def run_kernels(args):
 ACCEPT_PATTERNS = {"0": [0], "0.5": [1, 0], "1.0": [1]}
 
 
+def gdn_timeouts():
+    import rapier_amd as rmi
+    return int(rmi.gdn_exchange_timeouts())
+
+
 def tokens_for_rounds(pattern, rounds):
     """tokens a forced run emits in exactly `rounds` rounds (2 per accepted round, 1 per rejected)."""
     return sum(2 if pattern[r % len(pattern)] else 1 for r in range(rounds))
@@ -695,7 +700,8 @@ def run_round(args):
     us = st["gpu_ms"] * 1e3 / st["rounds"]
     print(json.dumps({"workload": "round", "ctx": ctx, "rounds": st["rounds"], "us_per_round": round(us, 2),
                       "tok_s": round(n / (st["gpu_ms"] / 1e3), 2), "stream_identical": toks == ref[:n],
-                      "round_weight_bytes": info["round_weight_bytes"], "kv_bytes_per_pos": info["kv_bytes_per_pos"]}),
+                      "round_weight_bytes": info["round_weight_bytes"], "kv_bytes_per_pos": info["kv_bytes_per_pos"],
+                      "gdn_exchange_timeouts": gdn_timeouts()}),
           flush=True)
 
 
@@ -1009,6 +1015,8 @@ def main():
                                  "hbm_frac_of_peak": gemv["config"]["hbm_frac_of_peak"]},
             "config1_gpu": gemv["config"]["config1"],
             "ingest": ingest,
+            # bounded waits of the GDN layer kernel that ran out in this process (the engine calls fail if any did)
+            "gdn_exchange_timeouts": gdn_timeouts(),
         },
         "roofline": gemv["roofline"],
     }

@@ -29,7 +29,7 @@ enum {
     RMI_ERR_STREAM = 3,      /* std::invalid_argument: null stream where the reference requires one */
     RMI_ERR_LAUNCH = 4,      /* std::runtime_error: the HIP launch failed */
     RMI_ERR_UNSUPPORTED = 5, /* std::invalid_argument: unsupported GGML type */
-    RMI_ERR_STATE = 6        /* engine misuse (context full, bad token, not built) */
+    RMI_ERR_STATE = 6        /* engine misuse (context full, bad token, not built), or a GDN exchange wait that timed out */
 };
 
 const char* rmi_last_error(void);
@@ -112,29 +112,6 @@ int rmi_native_q4_k_mmvq_res_n(const void* w, const void* x_q8_1, float* y, cons
                                int n_in, int n_out, int ncols, void* stream);
 int rmi_native_q5_k_mmvq_res_n(const void* w, const void* x_q8_1, float* y, const float* res, float* partials,
                                int n_in, int n_out, int ncols, void* stream);
-
-/* Folded RMSNorm (no counterpart in the reference; it removes the reference's rms_quant_apply launch between a
- * residual GEMV and the next normed GEMV, qw:627-655).  The normed GEMV's input is Q8_1((x * w) * inv) with
- * inv = rsqrt(sum(partials of x) / n + eps).  Folded, the residual GEMV that produces x also writes Q8_1(x * w_next)
- * of its rows (res_fold), or rmi_quantize_q8_1_weighted makes it from x, and the normed GEMV (scaled) multiplies each
- * row sum by inv, derived from x's 4-row partials with rms_quant_apply's reduction tree (the same inv bits).  The
- * quantization rounds x * w instead of (x * w) * inv: within the GEMV tolerance of the unfolded pair, and every path of
- * an engine that folds (decode, verify, ingest) folds the same way, so their results stay bitwise equal.
- * res_fold: rmi_native_q6_k_mmvq_packed_res_n plus y_q8_1_next = Q8_1(y * w_next) per column (column j at block
- * j * n_out / 32); supported shapes: rmi_q6_k_packed_fold_supported (n_in 4096 or 12288, n_out % 32 == 0, 1 or 2
- * columns), others RMI_ERR_UNSUPPORTED.
- * scaled: y = inv * (W x) per column, partials of column j at + j * n_in / 4 (8 or more columns: n_in <= 4096).
- * swiglu_packed_scaled: rmi_native_q6_k_swiglu_packed with the gate and up rows scaled by inv before the SwiGLU. */
-int rmi_q6_k_packed_fold_supported(int n_in, int n_out, int ncols);
-int rmi_native_q6_k_mmvq_packed_res_fold(const void* w_packed, const void* x_q8_1, float* y, const float* res,
-                                         float* partials, const float* w_next, void* y_q8_1_next, int n_in, int n_out,
-                                         int ncols, void* stream);
-int rmi_native_q6_k_mmvq_packed_scaled(const void* w_packed, const void* x_q8_1, const float* partials, float eps,
-                                       float* y, int n_in, int n_out, int ncols, void* stream);
-int rmi_native_q6_k_swiglu_packed_scaled(const void* w_packed, const void* x_q8_1, const float* partials, float eps,
-                                         void* y_q8_1, int n_in, int n_ff, int ncols, void* stream);
-/* Q8_1 of x * w per column, no inv (the folded norm's GEMV input where no res_fold epilogue makes it) */
-int rmi_quantize_q8_1_weighted(const float* x, const float* w, void* y_q8_1, int cols, int ncols, void* stream);
 
 /* Type-dispatched GEMV (GGML type 14 = Q6_K, 13 = Q5_K, 12 = Q4_K, 8 = Q8_0; others RMI_ERR_UNSUPPORTED).
  * Replaces native_mmvq (mmvq:3787-3818), including its split of more than 16 columns into passes. */
@@ -253,6 +230,10 @@ int rmi_gdn_layer_tokens_x(float* state_a, float* state_b, float* hist_a, float*
 /* Waits of the split kernel for the other workgroups of a value head that ran out of their bound, since the library
  * was loaded (0 in every correct run; a nonzero count means a launch's outputs are not to be trusted). */
 unsigned int rmi_gdn_exchange_timeouts(void);
+/* Test hook (no reference counterpart): set the wait's bound to spin_limit polls (0 = the default, 2^20) and, with
+ * force_miss, make every wait run to that bound and count as timed out, so the error path of the engine calls can be
+ * exercised with every kernel ending normally.  Outputs of launches made meanwhile are not valid.  Synchronous. */
+int rmi_gdn_exchange_test(unsigned int spin_limit, int force_miss);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * GQA attention over an fp16 KV cache [pos][n_kv][head_dim]

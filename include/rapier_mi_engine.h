@@ -50,9 +50,6 @@ typedef struct rmi_engine_info_t {
     size_t token_weight_bytes;   /* one greedy token: trunk + lm_head */
     size_t kv_bytes_per_pos;     /* fp16 K+V of the trunk attention layers per position */
     int gdn_layers, attn_layers, max_ctx, attn_chunk;
-    int norm_fold;               /* 1 (RMI_NORM_FOLD=1 at creation): the norms before the in-projections, the FFNs
-                                    and the heads are folded into their GEMVs (rmi_native_q6_k_mmvq_packed_res_fold /
-                                    _scaled), on every path; 0: rms_quant_apply, the reference's order */
 } rmi_engine_info_t;
 
 enum { RMI_GEN_GREEDY = 0, RMI_GEN_MTP = 1, RMI_GEN_MTP_FORCED = 2 };
@@ -89,6 +86,9 @@ int rmi_engine_synth_context(rmi_engine* e, int n_ctx, uint64_t seed, int last_t
 int rmi_engine_save_state(rmi_engine* e);
 int rmi_engine_restore_state(rmi_engine* e, int pos, int cur_token);
 int rmi_engine_state(rmi_engine* e, int* pos, int* cur_token);
+/* rmi_engine_generate, rmi_engine_ingest (and so the prefills) and rmi_engine_gen_step return RMI_ERR_STATE when a
+ * bounded wait of the GDN layer kernel ran out during the call (rmi_gdn_exchange_timeouts grew): the tokens and the
+ * state it produced are not valid. */
 int rmi_engine_generate(rmi_engine* e, const rmi_gen_request* req, int* out_tokens, rmi_gen_stats* stats);
 
 /* ---- serving: the context continues across calls (serve_loop, qw:2593-2813) ---- */

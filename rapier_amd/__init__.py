@@ -46,17 +46,13 @@ SIGNATURES = {
     "rmi_native_q6_k_mmvq_packed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_packed_res_n": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_q6_k_block_dots": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
-    "rmi_q6_k_packed_fold_supported": (_i, [_i, _i, _i]),
-    "rmi_native_q6_k_mmvq_packed_res_fold": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
-    "rmi_native_q6_k_mmvq_packed_scaled": (_i, [_vp, _vp, _vp, _f, _vp, _i, _i, _i, _vp]),
-    "rmi_native_q6_k_swiglu_packed_scaled": (_i, [_vp, _vp, _vp, _f, _vp, _i, _i, _i, _vp]),
-    "rmi_quantize_q8_1_weighted": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "rmi_gen_q6_k": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
     "rmi_gen_q8_0": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
     "rmi_gen_normal": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
     "rmi_gen_normal_f16": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
     "rmi_stream_read": (_i, [_vp, _sz, _i, _vp, _vp]),
     "rmi_gdn_exchange_timeouts": (ctypes.c_uint, []),
+    "rmi_gdn_exchange_test": (_i, [ctypes.c_uint, _i]),
     "rmi_gdn_exchange_bytes": (_sz, [_i]),
     "rmi_gdn_layer_tokens_x": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _i, _vp,
                                     _i, _i, _i, _i, _vp, _vp]),
@@ -227,31 +223,6 @@ def native_q6_k_mmvq_packed_res_n(w_packed, x_q8_1, y, res, partials, n_in: int,
           ncols, _stream(stream))
 
 
-def native_q6_k_mmvq_packed_res_fold(w_packed, x_q8_1, y, res, partials, w_next, y_q8_1_next, n_in: int, n_out: int,
-                                     ncols: int, stream=None):
-    """residual packed GEMV whose epilogue also writes Q8_1(y * w_next), the next GEMV's folded-norm input"""
-    _call("rmi_native_q6_k_mmvq_packed_res_fold", _p(w_packed), _p(x_q8_1), _p(y), _p(res), _p(partials), _p(w_next),
-          _p(y_q8_1_next), n_in, n_out, ncols, _stream(stream))
-
-
-def native_q6_k_mmvq_packed_scaled(w_packed, x_q8_1, partials, eps, y, n_in: int, n_out: int, ncols: int,
-                                   stream=None):
-    """packed GEMV on a folded norm's Q8_1(x * w): each row sum times inv = rsqrt(sum(partials) / n_in + eps)"""
-    _call("rmi_native_q6_k_mmvq_packed_scaled", _p(w_packed), _p(x_q8_1), _p(partials), eps, _p(y), n_in, n_out,
-          ncols, _stream(stream))
-
-
-def native_q6_k_swiglu_packed_scaled(w_packed, x_q8_1, partials, eps, y_q8_1, n_in: int, n_ff: int, ncols: int,
-                                     stream=None):
-    _call("rmi_native_q6_k_swiglu_packed_scaled", _p(w_packed), _p(x_q8_1), _p(partials), eps, _p(y_q8_1), n_in, n_ff,
-          ncols, _stream(stream))
-
-
-def quantize_q8_1_weighted(x, w, y_q8_1, cols: int, ncols: int = 1, stream=None):
-    """Q8_1 of x * w per column (a folded norm's input, no inv)"""
-    _call("rmi_quantize_q8_1_weighted", _p(x), _p(w), _p(y_q8_1), cols, ncols, _stream(stream))
-
-
 def q6_k_block_dots(w, x_q8_1, out, n_in: int, n_out: int, stream=None):
     _call("rmi_q6_k_block_dots", _p(w), _p(x_q8_1), _p(out), n_in, n_out, _stream(stream))
 
@@ -382,6 +353,11 @@ def fused_gdn_step_norm_silu_q8(state, q, k, v, gate, beta, z, gamma, eps, y, q8
 def gdn_exchange_timeouts() -> int:
     """bounded waits of the split GDN kernel that ran out (0 in every correct run)"""
     return lib().rmi_gdn_exchange_timeouts()
+
+
+def gdn_exchange_test(spin_limit: int = 0, force_miss: bool = False) -> None:
+    """test hook: the split GDN kernel's wait bound (0 = default) and a switch that makes every wait time out"""
+    _call("rmi_gdn_exchange_test", spin_limit, 1 if force_miss else 0)
 
 
 def gdn_exchange_bytes(h_v: int) -> int:

@@ -104,14 +104,9 @@ enum Slot {
 struct Engine {
     rmi_model_config cfg{};
     int max_ctx = 0, nsub = 1;
-    // Folded norms (every path of the engine, so decode, verify and ingest stay bitwise equal): a norm's GEMV reads
-    // Q8_1(x * w) and scales its rows by inv.  q8a_norm: the norm weights whose Q8_1(x * w) the last residual GEMV's
-    // epilogue left in q8a (columns 0..), so the norm site skips its quantize launch.
-    bool fold = false;
     // the next norm forms its vector's partials itself (rmi_rms_quant_apply_self): the draft's eh_proj output, whose
     // partials no GEMV epilogue writes
     bool norm_self = false;
-    const float* q8a_norm = nullptr;
     hipStream_t s = nullptr;
     bool own_stream = false;
     std::vector<void*> allocs;
@@ -517,21 +512,12 @@ __global__ void neg_exp_kernel(float* p, int n) {   // ssm_a = -exp(N(0, 0.5^2))
 }
 
 // ---- the forward building blocks (ncols = 1 or 2; every kernel is column-invariant) --------------------------------
-// A norm feeds its GEMV through q8a.  Unfolded: q8a = Q8_1((x * w) * inv) (rms_quant_apply, qw:627-655) and a plain
-// GEMV.  Folded (e.fold): q8a = Q8_1(x * w) - left by the residual GEMV that produced x when its epilogue could
-// (q8a_norm == w), else one quantize launch - and the GEMV multiplies its rows by inv, derived from x's partials.
-// Returns the Q8_1 of columns col0 .. col0 + nc - 1 (an epilogue wrote every column of its launch).
+// A norm feeds its GEMV through q8a = Q8_1((x * w) * inv) (rms_quant_apply, qw:627-655) of columns
+// col0 .. col0 + nc - 1.
 int norm_input(Engine& e, const float* x, const float* part, const float* w, int col0, int nc, const uint8_t** xq) {
     const auto& c = e.cfg;
     const size_t xs = static_cast<size_t>(col0) * c.n_embd, ps = static_cast<size_t>(col0) * (c.n_embd / 4);
-    const bool left = e.fold && e.q8a_norm == w;
-    e.q8a_norm = nullptr;
-    if (left) {
-        *xq = e.q8a + col0 * q81_bytes(c.n_embd);
-        return RMI_OK;
-    }
     *xq = e.q8a;
-    if (e.fold) return rmi_quantize_q8_1_weighted(x + xs, w, e.q8a, c.n_embd, nc, e.s);
     if (e.norm_self) {
         e.norm_self = false;
         return rmi_rms_quant_apply_self(x + xs, w, e.q8a, c.n_embd, c.eps, nc, e.s);
@@ -539,53 +525,32 @@ int norm_input(Engine& e, const float* x, const float* part, const float* w, int
     return rmi_rms_quant_apply(x + xs, w, part + ps, e.q8a, c.n_embd, c.eps, nc, e.s);
 }
 
-// the GEMV behind a norm: part = the normed vector's partials (columns as xq's)
-int norm_gemv(Engine& e, const Mat& m, const uint8_t* xq, const float* part, float* y, int nc) {
-    if (!e.fold) return gemv(e, m, xq, y, nc);
-    return rmi_native_q6_k_mmvq_packed_scaled(m.w, xq, part, e.cfg.eps, y, m.n_in, m.n_out, nc, e.s);
-}
-
-// residual GEMV x += W xq; folded, with the next norm's weights w_next and a shape its epilogue takes, it also leaves
-// Q8_1(x * w_next) in q8a
-int res_gemv(Engine& e, const Mat& m, const uint8_t* xq, float* x, float* part, int nc, const float* w_next) {
-    if (e.fold && w_next && m.packed && rmi_q6_k_packed_fold_supported(m.n_in, m.n_out, nc)) {
-        RMI_TRY(rmi_native_q6_k_mmvq_packed_res_fold(m.w, xq, x, x, part, w_next, e.q8a, m.n_in, m.n_out, nc, e.s));
-        e.q8a_norm = w_next;
-        return RMI_OK;
-    }
-    e.q8a_norm = nullptr;
-    return gemv_res(e, m, xq, x, part, nc);
-}
-
-// post-attention norm, up||gate + SwiGLU, down with the residual; w_next: the norm after the layer (for the fold)
-int ffn(Engine& e, Layer& L, float* x, float* part, int nc, const float* w_next) {
+// post-attention norm, up||gate + SwiGLU, down with the residual
+int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
     const auto& c = e.cfg;
     const uint8_t* xq = nullptr;
     RMI_TRY(norm_input(e, x, part, L.post_norm, 0, nc, &xq));
     if (L.upgate.swiglu_ff && nc <= 2) {   // up||gate GEMV + SwiGLU + Q8_1 in one launch
-        if (e.fold)
-            RMI_TRY(rmi_native_q6_k_swiglu_packed_scaled(L.upgate.w, xq, part, c.eps, e.q8f, c.n_embd, c.n_ff, nc, e.s));
-        else
-            RMI_TRY(rmi_native_q6_k_swiglu_packed(L.upgate.w, xq, e.q8f, c.n_embd, c.n_ff, nc, e.s));
+        RMI_TRY(rmi_native_q6_k_swiglu_packed(L.upgate.w, xq, e.q8f, c.n_embd, c.n_ff, nc, e.s));
     } else {
-        RMI_TRY(norm_gemv(e, L.upgate, xq, part, e.ug, nc));
+        RMI_TRY(gemv(e, L.upgate, xq, e.ug, nc));
         if (L.upgate.swiglu_ff)
             RMI_TRY(rmi_swiglu_quant_interleaved(e.ug, e.q8f, c.n_ff, nc, 2 * c.n_ff, e.s));
         else
             RMI_TRY(rmi_swiglu_quant(e.ug, e.ug + c.n_ff, e.q8f, c.n_ff, nc, 2 * c.n_ff, e.s));
     }
-    return res_gemv(e, L.down, e.q8f, x, part, nc, w_next);
+    return gemv_res(e, L.down, e.q8f, x, part, nc);
 }
 
 // pos[0] is the position of column 0; with more columns than one attention launch takes (64 query vectors per KV
 // head: 16 tokens at 4 query heads per KV head) pos is an array, pos[c] = pos[0] + c, and the launch for columns
 // c0.. reads pos + c0.  Every KV row of the nc columns is stored before any of them attends, and query c sees
 // positions <= pos[0] + c only, as in the per-token path.
-int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc, const float* w_next) {
+int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc) {
     const auto& c = e.cfg;
     const uint8_t* xq = nullptr;
     RMI_TRY(norm_input(e, x, part, L.attn_norm, 0, nc, &xq));
-    RMI_TRY(norm_gemv(e, L.in_proj, xq, part, e.proj, nc));
+    RMI_TRY(gemv(e, L.in_proj, xq, e.proj, nc));
     RMI_TRY(rmi_attn_prep_rope(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, e.qbuf, c.n_head, c.n_kv, c.head_dim,
                                c.n_rot, &e.rope, c.eps, nc, e.max_ctx, e.s));
     const size_t q8y_col = q81_bytes(e.attn_q);
@@ -597,22 +562,22 @@ int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int n
                                      c.head_dim, std::min(per, nc - c0), e.max_ctx, e.nsub,
                                      1.0f / sqrtf(static_cast<float>(c.head_dim)), e.s));
     }
-    RMI_TRY(res_gemv(e, L.out_proj, e.q8y, x, part, nc, L.post_norm));
-    return ffn(e, L, x, part, nc, w_next);
+    RMI_TRY(gemv_res(e, L.out_proj, e.q8y, x, part, nc));
+    return ffn(e, L, x, part, nc);
 }
 
-int gdn_block(Engine& e, Layer& L, int nc, const float* w_next) {
+int gdn_block(Engine& e, Layer& L, int nc) {
     const auto& c = e.cfg;
     const uint8_t* xq = nullptr;
     RMI_TRY(norm_input(e, e.x, e.part, L.attn_norm, 0, nc, &xq));
-    RMI_TRY(norm_gemv(e, L.in_proj, xq, e.part, e.proj, nc));
+    RMI_TRY(gemv(e, L.in_proj, xq, e.proj, nc));
     const int qkvz = 2 * c.ssm_h_k * kS + 2 * c.ssm_h_v * kS;
     RMI_TRY(rmi_gdn_layer_tokens_x(L.state[0], L.state[1], L.hist[0], L.hist[1], e.ints + kSel, e.proj, e.qkvz_rows,
                                    e.proj + qkvz, e.qkvz_rows, L.conv_w, L.dt, L.ssm_a, L.ssm_norm, c.eps, e.y, e.gdn_v,
                                    e.q8y, static_cast<int>(q81_bytes(e.gdn_v)), c.ssm_h_k, c.ssm_h_v, nc, e.gdn_xch,
                                    e.s));
-    RMI_TRY(res_gemv(e, L.out_proj, e.q8y, e.x, e.part, nc, L.post_norm));
-    return ffn(e, L, e.x, e.part, nc, w_next);
+    RMI_TRY(gemv_res(e, L.out_proj, e.q8y, e.x, e.part, nc));
+    return ffn(e, L, e.x, e.part, nc);
 }
 
 enum Head { kHeadAll, kHeadLast, kHeadNone };
@@ -626,22 +591,19 @@ enum Tail { kTailNone, kTailVerify, kTailSingle };
 int trunk_cols(Engine& e, int nc, const int* tok, const int* pos, float* h, float* hp, Head head,
                Tail tail = kTailNone) {
     const auto& c = e.cfg;
-    const size_t np = c.n_embd / 4;
-    e.q8a_norm = nullptr;
     RMI_TRY(rmi_embed(e.emb_type, e.tok_embd, tok, e.x, e.part, c.n_embd, c.n_vocab, nc, e.s));
     const int nl = static_cast<int>(e.layers.size());
     for (int il = 0; il < nl; ++il) {
         Layer& L = e.layers[il];
-        const float* w_next = il + 1 < nl ? e.layers[il + 1].attn_norm : head != kHeadNone ? e.out_norm : nullptr;
-        if (L.gdn) RMI_TRY(gdn_block(e, L, nc, w_next));
-        else RMI_TRY(attn_block(e, L, e.x, e.part, pos, nc, w_next));
+        if (L.gdn) RMI_TRY(gdn_block(e, L, nc));
+        else RMI_TRY(attn_block(e, L, e.x, e.part, pos, nc));
     }
     if (head != kHeadNone) {
         const int first = head == kHeadAll ? 0 : nc - 1;
         const int ncol = nc - first;
         const uint8_t* xq = nullptr;
         RMI_TRY(norm_input(e, e.x, e.part, e.out_norm, first, ncol, &xq));
-        RMI_TRY(norm_gemv(e, e.lm_head, xq, e.part + first * np, e.logits, ncol));
+        RMI_TRY(gemv(e, e.lm_head, xq, e.logits, ncol));
         if (tail != kTailNone) {   // head on every column (nc 1 or 2): tokens, bookkeeping and final norm in one launch
             auto* keys = static_cast<uint64_t*>(e.argmax_ws);
             argmax_partial_launch(e.logits, c.n_vocab, nc, c.n_vocab, keys, e.s);
@@ -673,21 +635,18 @@ enum DraftTail { kDraftFinalize, kDraftFirst };
 int draft_cols(Engine& e, const int* tok, const int* pos, const float* h, const float* hp, int nc, bool with_head,
                DraftTail dtail = kDraftFinalize) {
     const auto& c = e.cfg;
-    e.q8a_norm = nullptr;
     // [enorm(emb) | hnorm(h)] straight into the Q8_1 row of eh_proj's input, the embedding rows dequantized in the
     // same launch: the bits of embed, norm, norm, quantize
     RMI_TRY(rmi_embed_quant_apply_pair(e.emb_type, e.tok_embd, tok, e.enorm, h, e.hnorm, hp, e.q8f, c.n_embd,
                                        c.n_vocab, c.eps, nc, e.s));
     RMI_TRY(gemv(e, e.eh_proj, e.q8f, e.dx, nc));
-    // dx's partials: formed by the draft layer's first norm itself (one launch fewer), or here for the folded norms'
-    // scaled GEMV, which reads them
-    if (e.fold) RMI_TRY(rmi_row_sum_partials(e.dx, e.dpart, c.n_embd, nc, e.s));
-    else e.norm_self = true;
-    RMI_TRY(attn_block(e, e.draft, e.dx, e.dpart, pos, nc, with_head ? e.shnorm : nullptr));
+    // dx's partials: formed by the draft layer's first norm itself (one launch fewer)
+    e.norm_self = true;
+    RMI_TRY(attn_block(e, e.draft, e.dx, e.dpart, pos, nc));
     if (!with_head) return RMI_OK;
     const uint8_t* xq = nullptr;
     RMI_TRY(norm_input(e, e.dx, e.dpart, e.shnorm, 0, nc, &xq));
-    RMI_TRY(norm_gemv(e, e.lm_head, xq, e.dpart, e.logits, nc));
+    RMI_TRY(gemv(e, e.lm_head, xq, e.logits, nc));
     auto* keys = static_cast<uint64_t*>(e.argmax_ws);
     argmax_partial_launch(e.logits, c.n_vocab, nc, c.n_vocab, keys, e.s);
     if (dtail == kDraftFinalize)
@@ -768,6 +727,31 @@ int get_ints(Engine& e, int* host, int n) {
     HIP_TRY(hipStreamSynchronize(e.s));
     return RMI_OK;
 }
+
+// The split GDN kernel waits, with a bound, for the other workgroups of a value head; a wait that runs out leaves the
+// launch's outputs untrustworthy and bumps a device counter.  Every call that runs the trunk samples the counter
+// before its launches and checks it after its last synchronization, so a timed-out wait is an error of that call
+// instead of silently wrong tokens.
+struct ExchangeGuard {
+    unsigned int before = 0;
+    int begin() {
+        before = rmi_gdn_exchange_timeouts();
+        if (before == 0xffffffffu) return fail(RMI_ERR_LAUNCH, "engine: cannot read the GDN exchange counter");
+        return RMI_OK;
+    }
+    // call after the stream has been synchronized
+    int end(const char* who) const {
+        const unsigned int now = rmi_gdn_exchange_timeouts();
+        if (now == 0xffffffffu) return fail(RMI_ERR_LAUNCH, "engine: cannot read the GDN exchange counter");
+        if (now != before) {
+            char msg[160];
+            std::snprintf(msg, sizeof msg, "%s: %u GDN exchange wait(s) timed out; the generated tokens are not valid",
+                          who, now - before);
+            return fail(RMI_ERR_STATE, msg);
+        }
+        return RMI_OK;
+    }
+};
 
 }  // namespace
 }  // namespace rmi
@@ -1177,17 +1161,6 @@ int alloc_runtime(Engine& e) {
     HIP_TRY(hipEventCreate(&e.ev0));
     HIP_TRY(hipEventCreate(&e.ev1));
     HIP_TRY(hipStreamSynchronize(e.s));
-    // RMI_NORM_FOLD=1 folds the norms (every GEMV behind a norm a packed Q6_K matrix, n_embd <= 4096 for the
-    // 16-column ingest kernel).  Off by default: measured on the 9B round it is slower (the 32-row producer grid
-    // halves the CUs its residual GEMVs use, the scaled GEMVs lose a wave of occupancy) and it moves Q8_1's fp16 d
-    // rounding away from the reference's order.  Read per engine, so one process can hold both kinds.
-    const char* fold_var = std::getenv("RMI_NORM_FOLD");
-    const bool fold_env = fold_var && fold_var[0] == '1';
-    auto scaled_ok = [](const Mat& m) { return m.packed && m.parts.empty(); };
-    bool ok = fold_env && c.n_embd <= 4096 && scaled_ok(e.lm_head) && scaled_ok(e.draft.in_proj) &&
-              scaled_ok(e.draft.upgate);
-    for (const auto& L : e.layers) ok = ok && scaled_ok(L.in_proj) && scaled_ok(L.upgate);
-    e.fold = ok;
     return RMI_OK;
 }
 
@@ -1258,7 +1231,6 @@ extern "C" int rmi_engine_info(const rmi_engine* h, rmi_engine_info_t* info) {
     info->attn_layers = n_attn;
     info->max_ctx = e.max_ctx;
     info->attn_chunk = 64 * e.nsub;
-    info->norm_fold = e.fold ? 1 : 0;
     return RMI_OK;
 }
 
@@ -1351,6 +1323,8 @@ extern "C" int rmi_engine_ingest(rmi_engine* h, const int* tokens, int n, int ba
     if (n < 1 || pos0 + n >= e.max_ctx - 2) return fail(RMI_ERR_STATE, "rmi_engine_ingest: context does not fit");
     RMI_TRY(set_int(e, kNOut, 0));
     e.stream_mode = -1;
+    ExchangeGuard xg;
+    RMI_TRY(xg.begin());
     if (batch == 1) {
         for (int i = 0; i < n; ++i) {
             // draft KV slot p from (token, hidden of position p - 1) - the zero hidden at slot 0
@@ -1378,6 +1352,7 @@ extern "C" int rmi_engine_ingest(rmi_engine* h, const int* tokens, int n, int ba
         }
     }
     RMI_TRY(get_ints(e, st, kNumSlots));   // synchronizes: the host tokens are no longer read
+    RMI_TRY(xg.end("rmi_engine_ingest"));
     if (first_out) *first_out = st[kTok0];
     return RMI_OK;
 }
@@ -1536,6 +1511,8 @@ extern "C" int rmi_engine_generate(rmi_engine* h, const rmi_gen_request* req, in
         else RMI_TRY(capture(e, &e.g_single, [&] { return single_step(e); }));
     }
     HIP_TRY(hipStreamSynchronize(e.s));
+    ExchangeGuard xg;
+    RMI_TRY(xg.begin());
     HIP_TRY(hipEventRecord(e.ev0, e.s));
     if (mtp) RMI_TRY(first_draft(e));
     int emitted = 0, launched = 0;
@@ -1551,6 +1528,7 @@ extern "C" int rmi_engine_generate(rmi_engine* h, const rmi_gen_request* req, in
         emitted = st[kNOut];
         if (launched > 4 * n_gen + 8) return fail(RMI_ERR_STATE, "rmi_engine_generate: no progress");
     }
+    RMI_TRY(xg.end("rmi_engine_generate"));
     float ms = 0.0f;
     HIP_TRY(hipEventElapsedTime(&ms, e.ev0, e.ev1));
     std::vector<int> ring(static_cast<size_t>(emitted));
@@ -1598,8 +1576,11 @@ extern "C" int rmi_engine_gen_step(rmi_engine* h, int* out_tokens, int* n_out) {
     RMI_TRY(get_ints(e, st, kNumSlots));
     if (st[kPos] + 3 >= e.max_ctx) return fail(RMI_ERR_STATE, "context full");
     const bool mtp = e.stream_mode == RMI_GEN_MTP;
+    ExchangeGuard xg;
+    RMI_TRY(xg.begin());
     HIP_TRY(hipGraphLaunch(mtp ? e.g_round : e.g_single, e.s));
     RMI_TRY(get_ints(e, st, kNumSlots));
+    RMI_TRY(xg.end("rmi_engine_gen_step"));
     out_tokens[0] = st[kV0];
     *n_out = 1;
     if (mtp && st[kAccept]) {

@@ -76,17 +76,6 @@ __global__ __launch_bounds__(256) void rms_quant_self_kernel(const float* __rest
     q8_1_store_lane((xv * wv) * inv, y + static_cast<size_t>(i / 32) * kQ8_1Bytes);
 }
 
-// Q8_1 of x * w, no inv: a folded norm's GEMV input where no residual GEMV epilogue makes it (the same fp32 product and
-// quantizer as that epilogue, so the same bytes); the GEMV scales its rows by inv
-__global__ __launch_bounds__(256) void quant_weighted_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                             uint8_t* __restrict__ y, int cols) {
-    const int c = blockIdx.y;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= cols) return;   // cols % 32 == 0: whole 32-lane groups leave together
-    q8_1_store_lane(x[static_cast<size_t>(c) * cols + i] * w[i],
-                    y + (static_cast<size_t>(c) * (cols / 32) + i / 32) * kQ8_1Bytes);
-}
-
 // two normed vectors of a column into the two halves of one Q8_1 row of 2 cols (blockIdx.z = half)
 struct NormInput {
     const float* x;
@@ -308,16 +297,6 @@ extern "C" int rmi_rms_quant_apply_self(const float* x, const float* w, void* y_
     hipLaunchKernelGGL(rms_quant_self_kernel, dim3((cols + 255) / 256, ncols), dim3(256), 0,
                        static_cast<hipStream_t>(stream), x, w, static_cast<uint8_t*>(y_q8_1), cols, eps);
     return launch_status("rms_quant_apply_self");
-}
-
-extern "C" int rmi_quantize_q8_1_weighted(const float* x, const float* w, void* y_q8_1, int cols, int ncols,
-                                          void* stream) {
-    if (cols <= 0 || cols % 32 != 0 || bad_cols(ncols)) return fail(RMI_ERR_SHAPE, "quantize_q8_1_weighted: bad shape");
-    if (!aligned4(x) || !aligned4(w) || !aligned4(y_q8_1))
-        return fail(RMI_ERR_POINTER, "quantize_q8_1_weighted: null or misaligned pointer");
-    hipLaunchKernelGGL(quant_weighted_kernel, dim3((cols + 255) / 256, ncols), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), x, w, static_cast<uint8_t*>(y_q8_1), cols);
-    return launch_status("quantize_q8_1_weighted");
 }
 
 extern "C" int rmi_rms_quant_apply_pair(const float* x0, const float* w0, const float* partials0, const float* x1,

@@ -440,7 +440,7 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
 // 16-column wave sums in wave order), so the results are bitwise those of the one-workgroup kernel, which the ingest
 // chunks run.  The part's 32 columns are one Q8_1 block per token.
 // Each part recomputes the head's q and k conv (all 128 channels: the step reads all of them); part 0 writes their
-// history.  The output norm needs the head's eight wave sums: each part publishes its two per token as {bits, epoch}
+// history once the exchange shows that every other part has used the history it loaded.  The output norm needs the head's eight wave sums: each part publishes its two per token as {bits, epoch}
 // 8-byte words (agent scope: value and tag land together) and reads the other parts' words.  The epoch is the number
 // of launches the head's parts have completed: every launch writes every part's words with the next one, so at the
 // start of a launch all four parts' words carry the same tag, and a part reads it from its own word (which only it
@@ -453,6 +453,10 @@ constexpr int kPartCols = S / kParts;   // 32
 constexpr int kPartLanes = kPartCols * RG;   // 128
 constexpr int kXchWords = kParts * 2 * 2;   // per value head: [part][token][wave]
 __device__ unsigned int gdn_xch_timeouts;
+// The wait's bound (polls per wave) and a test switch that makes every wait miss until the bound: set from the host by
+// rmi_gdn_exchange_test, so a test can drive the timeout path with every kernel still ending normally.
+__device__ unsigned int gdn_xch_spin_limit = 1u << 20;
+__device__ unsigned int gdn_xch_force_miss = 0;
 
 template <int NT>
 __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
@@ -480,6 +484,8 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
     // the exchange epoch of this launch: the tag of this part's own first word (written by no one else)
     unsigned long long* xh = a.xch + static_cast<size_t>(head) * kXchWords;
     const unsigned long long own0 = __hip_atomic_load(xh + part * 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned int spin_limit = gdn_xch_spin_limit;
+    const bool force_miss = gdn_xch_force_miss != 0;
     float qx[NT], kx[NT], vx[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -626,11 +632,17 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
     // exchange's loads: stores count in the wave's vector memory counter, so a load issued behind them waits for
     // their completion, a memory round trip.  The counter is per wave: wave 1, which makes no exchange loads, stores
     // (and publishes) at once.
-    auto put_all = [&]() {
+    // The head's q / k history (part 0's stores) waits until the exchange has seen every other part's words at this
+    // launch's tag: a part publishes only after its conv has consumed the history it loaded at the start, so a part
+    // dispatched late still reads the history of the previous launch.  The other stores touch only the part's own
+    // columns and go out at once.
+    auto put_qk = [&]() {
         if (part == 0) {
             put_hist(chq, hq[sb], qx);
             put_hist(chk, hk[sb], kx);
         }
+    };
+    auto put_all = [&]() {
         if (vlane) put_hist(chv, hv[sb], vx);
         if constexpr (SNAP) {
 #pragma unroll
@@ -657,17 +669,19 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
         unsigned long long v = tag;
         if (other) v = __hip_atomic_load(xh + (pp * 2 + t) * 2 + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         gate_silu();
-        int n = 0;
-        while (!__all(!other || (v >> 32) == (tag >> 32)) && n < (1 << 20)) {
+        unsigned int n = 0;
+        bool arrived;
+        while (!(arrived = __all(!other || ((v >> 32) == (tag >> 32) && !force_miss))) && n < spin_limit) {
             if (other && (v >> 32) != (tag >> 32))
                 v = __hip_atomic_load(xh + (pp * 2 + t) * 2 + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             ++n;
         }
-        if (n == (1 << 20) && ln == 0) atomicAdd(&gdn_xch_timeouts, 1u);
+        if (!arrived && ln == 0) atomicAdd(&gdn_xch_timeouts, 1u);
         if (ln < kParts * 2 * NT) allw[t][2 * pp + w] = other ? __uint_as_float(static_cast<uint32_t>(v)) : wsum[t][w];
         put_all();
     }
-    __syncthreads();
+    __syncthreads();   // wave 0's wait has ended: every other part has published, so its history loads are done
+    put_qk();
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         float tot = 0.0f;
@@ -791,6 +805,15 @@ extern "C" int rmi_gdn_layer_tokens_x(float* state_a, float* state_b, float* his
         return fail(RMI_ERR_POINTER, "gdn_layer_tokens_x: null or misaligned exchange buffer");
     return gdn_layer(state_a, state_b, hist_a, hist_b, sel, qkvz, qkvz_stride, ab, ab_stride, conv_w, dt, ssm_a, gamma,
                      eps, y, y_stride, q8, q8_stride, h_k, h_v, ntok, xch, stream);
+}
+
+extern "C" int rmi_gdn_exchange_test(unsigned int spin_limit, int force_miss) {
+    if (spin_limit == 0) spin_limit = 1u << 20;
+    const unsigned int miss = force_miss ? 1u : 0u;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(gdn_xch_spin_limit), &spin_limit, sizeof(spin_limit)) != hipSuccess ||
+        hipMemcpyToSymbol(HIP_SYMBOL(gdn_xch_force_miss), &miss, sizeof(miss)) != hipSuccess)
+        return fail(RMI_ERR_LAUNCH, "rmi_gdn_exchange_test: cannot set the wait's bound");
+    return RMI_OK;
 }
 
 extern "C" unsigned int rmi_gdn_exchange_timeouts(void) {

@@ -244,10 +244,9 @@ __device__ __forceinline__ void load_residual(float (&rv)[NCOLS], const float* r
     for (int col = 0; col < NCOLS; ++col) rv[col] = res[static_cast<size_t>(col) * n_out + row];
 }
 
-template <int NCOLS, bool RES, bool INV = false>
+template <int NCOLS, bool RES>
 __device__ __forceinline__ void quad_epilogue(float (&tot)[NCOLS], int lane, int q, float* y, const float* res,
-                                              float* partials, int n_out, const float* rv = nullptr,
-                                              const float* inv = nullptr, float* vout = nullptr) {
+                                              float* partials, int n_out, const float* rv = nullptr) {
     const int r = lane & 3, hb = lane >> 2;
     const int row = kQuad * q + r;
     const int np = (n_out + 3) / 4;
@@ -255,11 +254,9 @@ __device__ __forceinline__ void quad_epilogue(float (&tot)[NCOLS], int lane, int
     for (int col = 0; col < NCOLS; ++col) {
         float v = hb_sum(tot[col]);
         tot[col] = 0.0f;
-        if constexpr (INV) v *= inv[col];   // a folded norm: the row sum of Q8_1(x * w), times inv
         if constexpr (RES) {
             if (row < n_out) v += rv ? rv[col] : res[static_cast<size_t>(col) * n_out + row];
         }
-        if (vout) vout[col] = v;
         if (hb == 0 && row < n_out) y[static_cast<size_t>(col) * n_out + row] = v;
         if constexpr (RES) {
             // partial of the quad: squares of its rows in row order (lanes 0, 1, 2, 3)
@@ -279,69 +276,13 @@ __device__ __forceinline__ void quad_epilogue(float (&tot)[NCOLS], int lane, int
     }
 }
 
-// ---- folded RMSNorm ---------------------------------------------------------------------------------------------------
-// The input of a normed GEMV is Q8_1((x * w) * inv) when rms_quant_apply makes it.  Folded, the GEMV before it (a
-// residual GEMV, whose workgroups own whole 32-row groups: FOLD) writes Q8_1(x * w) straight from its output rows, and
-// the normed GEMV (INV) scales every row sum by inv, which it derives from x's 4-row partials with the tree every norm
-// kernel uses (rmi_common.h): the same inv bits as rms_quant_apply, the quantization rounding moved (Q8_1 of x * w
-// instead of (x * w) * inv).  That removes the norm launch between them.
-struct Fold {
-    const float* part;    // INV: the input vector's 4-row partials, column col at + col * (n_in / 4)
-    float eps;
-    const float* w_next;  // FOLD: the next norm's weights over this GEMV's rows
-    uint8_t* q8_next;     // FOLD: Q8_1(y * w_next), column col at + col * (n_out / 32) blocks
-};
-
-// waves 0..3 (whole waves) reduce each column's partials to its four wave sums in red[col]; the caller's next barrier
-// publishes them, then inv[col] = norm_inv(red[col], n_in, eps)
-template <int NCOLS>
-__device__ __forceinline__ void inv_issue(NormLoads (&pv)[NCOLS], const Fold& f, int n_in, int t) {
-    const int np = n_in / 4;
-#pragma unroll
-    for (int col = 0; col < NCOLS; ++col) norm_load(pv[col], f.part + static_cast<size_t>(col) * np, np, t);
-}
-
-template <int NCOLS>
-__device__ __forceinline__ void inv_reduce(const NormLoads (&pv)[NCOLS], const Fold& f, int n_in, int t,
-                                           float (*red)[4]) {
-    const int np = n_in / 4;
-    if (t < 256) {
-#pragma unroll
-        for (int col = 0; col < NCOLS; ++col) {
-            const float s = norm_wave_sum(pv[col], f.part + static_cast<size_t>(col) * np, np, t);
-            if ((t & 63) == 0) red[col][t >> 6] = s;
-        }
-    }
-}
-
-// FOLD tail: the workgroup's 32 rows (rows[col][i] = y of row 32 blockIdx.x + i) into column col's Q8_1 block of
-// y * w_next, by wave 0 (lanes 32 col + i), with the quantizer of rms_quant_apply.  wn = w_next[32 blockIdx.x + t % 32],
-// loaded by the caller with its first loads.
-template <int NCOLS>
-__device__ __forceinline__ float fold_weight(const Fold& f, int t) {
-    return f.w_next[32 * static_cast<int>(blockIdx.x) + (t & 31)];
-}
-
-template <int NCOLS>
-__device__ __forceinline__ void fold_quantize(const float (*rows)[32], float wn, const Fold& f, int n_out, int t) {
-    static_assert(NCOLS <= 2, "one wave quantizes up to two columns");
-    if (t < 32 * NCOLS) {
-        const int col = t >> 5, i = t & 31;
-        q8_1_store_lane(rows[col][i] * wn,
-                        f.q8_next + (static_cast<size_t>(col) * (n_out / 32) + blockIdx.x) * kQ8_1Bytes);
-    }
-}
-
 // NW waves per workgroup share the staged activations: 4 for up to 4 columns (several workgroups per CU), 8 for the
 // 8 / 16-column ingest passes, whose stage fills most of the CU's LDS (one workgroup per CU)
-template <int NCOLS, bool RES, int D, int NW, bool INV = false>
+template <int NCOLS, bool RES, int D, int NW>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __restrict__ wp,
                                                            const uint8_t* __restrict__ x, float* y,
-                                                           const float* res, float* partials, int n_in, int n_out,
-                                                           Fold fold) {
-    static_assert(!INV || NW >= 4, "the norm tree takes four waves");
+                                                           const float* res, float* partials, int n_in, int n_out) {
     extern __shared__ uint4 smem[];
-    __shared__ float inv_red[INV ? NCOLS : 1][4];
     const int t = threadIdx.x, lane = t & 63;
     const int nch = n_in / kChunkElems;
     const int nbt = n_in / 32;                   // Q8_1 blocks per column
@@ -367,20 +308,12 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
         b.sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
         b.d = *reinterpret_cast<const uint32_t*>(base + 6656 + 4 * (2 * (lane >> 3) + ((lane & 3) >> 1)));
     };
-    NormLoads pv[INV ? NCOLS : 1];
-    if constexpr (INV) inv_issue<NCOLS>(pv, fold, n_in, t);
 #pragma unroll
     for (int s = 0; s < D; ++s)
         if (s < nsteps) issue(s, buf[s]);
 
     stage_activations(x, NCOLS * nbt, nbt, lq, lrec, t, 64 * NW);
-    if constexpr (INV) inv_reduce<NCOLS>(pv, fold, n_in, t, inv_red);
     __syncthreads();
-    float inv[NCOLS];
-    if constexpr (INV) {
-#pragma unroll
-        for (int col = 0; col < NCOLS; ++col) inv[col] = norm_inv(inv_red[col], n_in, fold.eps);
-    }
 
     float tot[NCOLS];
 #pragma unroll
@@ -397,7 +330,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
             accumulate_step<NCOLS>(cur, lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, tot);
 
             if (c == nch - 1)
-                quad_epilogue<NCOLS, RES, INV>(tot, lane, gw + qi * GW, y, res, partials, n_out, nullptr, inv);
+                quad_epilogue<NCOLS, RES>(tot, lane, gw + qi * GW, y, res, partials, n_out);
         }
     }
 }
@@ -406,17 +339,12 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
 // chunks, every tile issued at the start, and hand their per-lane (d, acc) pairs through LDS to the quad's first
 // wave, which continues the fma chain over the chunks in order.  The operations and their order are those of one wave
 // walking every chunk, so the result is bitwise that of q6k_packed_gemv.  NW waves per workgroup = QW quads x S.
-// INV: the input is a folded norm's Q8_1(x * w) (row sums times inv).  FOLD (with RES, QW = 8: the workgroup owns 32
-// rows): also Q8_1(y * w_next) of its rows, the next GEMV's folded input.
-template <int NCOLS, bool RES, int CS, int NW, bool INV = false, bool FOLD = false>
+template <int NCOLS, bool RES, int CS, int NW>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* __restrict__ wp,
                                                                  const uint8_t* __restrict__ x, float* y,
                                                                  const float* res, float* partials, int n_in,
-                                                                 int n_out, Fold fold) {
-    static_assert(!FOLD || RES, "the folded norm's producer is a residual GEMV");
+                                                                 int n_out) {
     extern __shared__ uint4 smem[];
-    __shared__ float inv_red[INV ? NCOLS : 1][4];
-    __shared__ float frows[FOLD ? NCOLS : 1][32];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
     const int nbt = n_in / 32, xcs = nch * kNB;
@@ -442,10 +370,6 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
     }
     float rv[NCOLS];
     if constexpr (RES) load_residual<NCOLS>(rv, res, lane, min(q, nq - 1), n_out);
-    NormLoads pv[INV ? NCOLS : 1];
-    if constexpr (INV) inv_issue<NCOLS>(pv, fold, n_in, t);
-    float wn = 0.0f;
-    if constexpr (FOLD) wn = fold_weight<NCOLS>(fold, t);
     __builtin_amdgcn_sched_barrier(0);   // the stage's loads stay ahead of the weight tiles
     // unconditional loads (a wave past the last quad reads the last quad's tiles and discards them): with the loads in
     // a branch the compiler waits for the stage as if no tile had been issued after it.  Every tile is issued here,
@@ -480,13 +404,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
         for (int i = 0; i < 9; ++i) wv[i] = p[i];
         stage_one(wv, J, nbt, lq, lrec);
     }
-    if constexpr (INV) inv_reduce<NCOLS>(pv, fold, n_in, t, inv_red);
     __syncthreads();
-    float inv[NCOLS];
-    if constexpr (INV) {
-#pragma unroll
-        for (int col = 0; col < NCOLS; ++col) inv[col] = norm_inv(inv_red[col], n_in, fold.eps);
-    }
 
     float acc[CS][NCOLS], dd[CS];
     if (live) {
@@ -507,10 +425,8 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
         }
     }
     __syncthreads();
-    if constexpr (!FOLD) {
-        if (!live || sp != 0) return;
-    }
-    if (live && sp == 0) {   // with FOLD every wave goes on to the barrier below
+    if (!live || sp != 0) return;
+    {
         float tot[NCOLS];
 #pragma unroll
         for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
@@ -527,35 +443,20 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
                 for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, o[(col + 1) * 64], tot[col]);
             }
         }
-        float v[NCOLS];
-        quad_epilogue<NCOLS, RES, INV>(tot, lane, q, y, res, partials, n_out, rv, inv, v);
-        if constexpr (FOLD) {
-            if (lane < kQuad) {
-#pragma unroll
-                for (int col = 0; col < NCOLS; ++col) frows[col][kQuad * qg + lane] = v[col];
-            }
-        }
-    }
-    if constexpr (FOLD) {
-        __syncthreads();
-        fold_quantize<NCOLS>(frows, wn, fold, n_out, t);
+        quad_epilogue<NCOLS, RES>(tot, lane, q, y, res, partials, n_out, rv);
     }
 }
 
 // Stream variant: one wave per quad and QPW quads per wave (quads q, q + G, q + 2G, ... with G the grid's wave count),
 // all in straight-line code with PD tiles in flight ahead of the step that uses them.  Every wave is resident from the
 // start (a wave per quad would leave a tail of waves waiting for slots), and the per-quad arithmetic is that of
-// q6k_packed_gemv: the same bits.  INV / FOLD: the folded norm, as in the split variant (FOLD: QPW = 1, NW = 8, so
-// the workgroup's waves hold its 32 rows).
-template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD, bool INV = false, bool FOLD = false>
+// q6k_packed_gemv: the same bits.
+template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t* __restrict__ wp,
                                                                   const uint8_t* __restrict__ x, float* y,
                                                                   const float* res, float* partials, int n_in,
-                                                                  int n_out, Fold fold) {
-    static_assert(!FOLD || (RES && QPW == 1 && NW == 8), "FOLD: a residual GEMV whose 8 waves own 32 rows");
+                                                                  int n_out) {
     extern __shared__ uint4 smem[];
-    __shared__ float inv_red[INV ? NCOLS : 1][4];
-    __shared__ float frows[FOLD ? NCOLS : 1][32];
     const int t = threadIdx.x, lane = t & 63;
     const int nbt = n_in / 32, xcs = NCH * kNB;
     uint4* lq = smem;
@@ -580,10 +481,6 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
 #pragma unroll
         for (int j = 0; j < QPW; ++j) load_residual<NCOLS>(rv[j], res, lane, min(q0 + j * G, nq - 1), n_out);
     }
-    NormLoads pv[INV ? NCOLS : 1];
-    if constexpr (INV) inv_issue<NCOLS>(pv, fold, n_in, t);
-    float wn = 0.0f;
-    if constexpr (FOLD) wn = fold_weight<NCOLS>(fold, t);
     __builtin_amdgcn_sched_barrier(0);
 
     // tile i = (quad j = i / NCH, chunk i % NCH); a quad past the last reads the last quad's tiles and discards them
@@ -619,13 +516,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
         for (int i = 0; i < 9; ++i) wv[i] = p[i];
         stage_one(wv, J, nbt, lq, lrec);
     }
-    if constexpr (INV) inv_reduce<NCOLS>(pv, fold, n_in, t, inv_red);
     __syncthreads();
-    float inv[NCOLS];
-    if constexpr (INV) {
-#pragma unroll
-        for (int col = 0; col < NCOLS; ++col) inv[col] = norm_inv(inv_red[col], n_in, fold.eps);
-    }
 
     float tot[NCOLS];
 #pragma unroll
@@ -643,20 +534,8 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
             issue(i + PD);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (c == NCH - 1 && q0 + j * G < nq) {
-            float v[NCOLS];
-            quad_epilogue<NCOLS, RES, INV>(tot, lane, q0 + j * G, y, res, partials, n_out, rv[j], inv, v);
-            if constexpr (FOLD) {
-                if (lane < kQuad) {
-#pragma unroll
-                    for (int col = 0; col < NCOLS; ++col) frows[col][kQuad * (t >> 6) + lane] = v[col];
-                }
-            }
-        }
-    }
-    if constexpr (FOLD) {
-        __syncthreads();
-        fold_quantize<NCOLS>(frows, wn, fold, n_out, t);
+        if (c == NCH - 1 && q0 + j * G < nq)
+            quad_epilogue<NCOLS, RES>(tot, lane, q0 + j * G, y, res, partials, n_out, rv[j]);
     }
 }
 
@@ -822,16 +701,14 @@ __global__ __launch_bounds__(64 * NW) void q6k_gguf_stream(const uint8_t* __rest
 // weight tiles in the CU's memory pipeline (per-wave clock stamps: stage at 5.3 us against 1.6 us, its waves last to
 // finish): 24576 x 4096 at two columns 17.2 -> 16.0 us.  Deeper prefetch (3 or 4 tiles ahead) and 16 waves of two
 // quads were slower (17.2, 18.4, 29.6 us).
-// INV: the input is a folded norm's Q8_1(x * w); the gate and up row sums are scaled by inv before the SwiGLU.
-template <int NCOLS, bool INV = false, int NW = 4, int QPW = 4, int PD = 2>
+template <int NCOLS, int NW = 4, int QPW = 4, int PD = 2>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_swiglu(const uint8_t* __restrict__ wp,
                                                              const uint8_t* __restrict__ x, uint8_t* __restrict__ out,
-                                                             int n_in, int ff, Fold fold) {
+                                                             int n_in, int ff) {
     constexpr int NCH = 2, T = QPW * NCH;
     constexpr int GPW = NW * QPW / 16;   // 16-quad groups per workgroup
     static_assert(GPW * 16 == NW * QPW && GPW >= 1, "whole groups per workgroup");
     extern __shared__ uint4 smem[];
-    __shared__ float inv_red[INV ? NCOLS : 1][4];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int nbt = n_in / 32, xcs = NCH * kNB;
     uint4* lq = smem;
@@ -847,8 +724,6 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_swiglu(const uint8_t* __re
 #pragma unroll
         for (int i = 0; i < 9; ++i) sv[i] = p[i];
     }
-    NormLoads pv[INV ? NCOLS : 1];
-    if constexpr (INV) inv_issue<NCOLS>(pv, fold, n_in, t);
     __builtin_amdgcn_sched_barrier(0);
     WTile buf[T];
     auto issue = [&](int i) {
@@ -871,13 +746,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_swiglu(const uint8_t* __re
     // unconditional (lanes past the last block rewrite its slot with the same bytes): under a branch the compiler sinks
     // the stage's loads into it, behind the first tiles, and the stage then waits for those
     stage_one(sv, min(t, nblocks - 1), nbt, lq, lrec);
-    if constexpr (INV) inv_reduce<NCOLS>(pv, fold, n_in, t, inv_red);
     __syncthreads();
-    float inv[NCOLS];
-    if constexpr (INV) {
-#pragma unroll
-        for (int col = 0; col < NCOLS; ++col) inv[col] = norm_inv(inv_red[col], n_in, fold.eps);
-    }
 
     float tot[NCOLS];
 #pragma unroll
@@ -899,8 +768,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_swiglu(const uint8_t* __re
             const int lqd = QPW * w + j;   // the quad within the workgroup: group lqd / 16, rows 4 (lqd % 16) + r
 #pragma unroll
             for (int col = 0; col < NCOLS; ++col) {
-                float v = hb_sum(tot[col]);
-                if constexpr (INV) v *= inv[col];
+                const float v = hb_sum(tot[col]);
                 tot[col] = 0.0f;
                 if (lane < kQuad) lrow[((lqd >> 4) * NCOLS + col) * 64 + 4 * (lqd & 15) + lane] = v;
             }
@@ -989,10 +857,6 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
                                                           0xf, false));
 }
 
-// INV: the folded norm (n_in <= 4096: at most four partial slots per lane and column).  The 8 waves split the columns:
-// waves 0..3 reduce the even ones and waves 4..7 the odd ones, each group as the 256 lanes of the norm tree.
-constexpr int kMfmaNormLoads = 4;
-
 // CS = 2: the two waves of a pair share a quad and split its columns (each runs NCG / 2 column groups over the same
 // weight tiles, the second load an L2 hit), so a shape with fewer quads than the grid's waves still fills every CU;
 // a column's arithmetic is unchanged.
@@ -1005,22 +869,18 @@ constexpr int kMfmaNormLoads = 4;
 // lane (row i, group g, column jj) adds its 16 half-blocks in the xor butterfly's tree (bitwise hb_sum), then owns one
 // output: ~60 instructions per quad where the 16 in-register butterflies take ~300.  Needs 4 KB x NCW of LDS per wave:
 // after the stage, or with two K halves the stage itself once every wave is past its last chunk.
-template <int NCG, bool RES, int D, bool INV = false, int CS = 1, int KP = 1, int NCHK = 0, bool LE = false>
+template <int NCG, bool RES, int D, int CS = 1, int KP = 1, int NCHK = 0, bool LE = false>
 __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t* __restrict__ wp,
                                                                    const uint8_t* __restrict__ x, float* y,
                                                                    const float* res, float* partials, int n_in,
-                                                                   int n_out, Fold fold) {
+                                                                   int n_out) {
     typedef int i32x4 __attribute__((ext_vector_type(4)));
-    static_assert(kWideWaves == 8, "two 256-lane norm trees");
-    static_assert(CS == 1 || (CS == 2 && !INV), "column split: two waves per quad, no folded norm");
+    static_assert(CS == 1 || CS == 2, "column split: one or two waves per quad");
     static_assert(KP == 1 || (KP == 2 && CS == 2 && NCHK % 2 == 0 && NCHK > 0), "two K halves: a wave pair per quad");
-    static_assert(!LE || (!INV && NCG / CS <= 4), "LDS row sums: no folded norm, at most 64 outputs per wave");
+    static_assert(!LE || NCG / CS <= 4, "LDS row sums: at most 64 outputs per wave");
     constexpr int NCW = NCG / CS;            // column groups of this wave
     constexpr int PG = NCW >= 2 ? 2 : 1;     // column groups per MFMA batch
-    extern __shared__ uint4 smem[];
-    // INV: the columns' four wave sums after the stage (the stage may take all 160 KB of the CU's LDS otherwise, so
-    // the kernel has no static LDS)
-    float(*inv_red)[4] = reinterpret_cast<float(*)[4]>(smem + static_cast<size_t>(NCG) * (n_in / 32) * kMStride);
+    extern __shared__ uint4 smem[];   // the stage may take all 160 KB of the CU's LDS: no static LDS
     const int t = threadIdx.x, lane = t & 63;
     const int nch = n_in / kChunkElems;
     const int nbt = n_in / 32;
@@ -1048,16 +908,6 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
         b.sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
         b.d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (4 * (lane >> 3) + (lane & 3)));
     };
-    constexpr int NH = INV ? 2 * NCG : 1;   // columns per lane group
-    float pvm[NH][kMfmaNormLoads];
-    const int np = n_in / 4, nu = t & 255, par = t >> 8;
-    if constexpr (INV) {
-#pragma unroll
-        for (int h = 0; h < NH; ++h)
-#pragma unroll
-            for (int k = 0; k < kMfmaNormLoads; ++k)
-                pvm[h][k] = fold.part[static_cast<size_t>(2 * h + par) * np + min(nu + 256 * k, np - 1)];
-    }
 #pragma unroll
     for (int s = 0; s < D; ++s)
         if (s < nsteps) issue(s, buf[s]);
@@ -1082,25 +932,9 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
             for (int i = 0; i < 9; ++i) pb[m][i] = p[i];
         }
     };
-    if constexpr (INV) {
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int k = 0; k < kMfmaNormLoads; ++k)
-                if (nu + 256 * k < np) sum += pvm[h][k];
-            sum = group_sum<64>(sum);
-            if ((t & 63) == 0) inv_red[2 * h + par][(t >> 6) & 3] = sum;
-        }
-    }
     __syncthreads();
 
     const int jj = lane & 3, hb = lane >> 2, b = hb >> 1, n = hb & 1;
-    float invc[NCW];   // inv of the lane's column 4 g + jj
-    if constexpr (INV) {
-#pragma unroll
-        for (int g = 0; g < NCW; ++g) invc[g] = norm_inv(inv_red[4 * g + jj], n_in, fold.eps);
-    }
     // stage offsets (uint4 units, 32-bit): the wave's column group g (group NCW half + g of the stage) at goff[g], the
     // lane's column and half-block at lbase
     int goff[NCW];
@@ -1259,7 +1093,6 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         v[i] = hb_sum(tot[i][g]);
-                        if constexpr (INV) v[i] *= invc[g];
                         tot[i][g] = 0.0f;
                         const int row = kQuad * q + i;
                         if constexpr (RES) {
@@ -1375,56 +1208,56 @@ size_t split_lds(int n_in, int ncols, int cs, int nw) {
     return static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(nw) * cs * (ncols + 1) * 64 * 4;
 }
 
-template <int NCOLS, bool RES, int CS, int NW, bool INV = false, bool FOLD = false>
+template <int NCOLS, bool RES, int CS, int NW>
 void launch_split(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                  int n_out, const Fold& f, hipStream_t s) {
+                  int n_out, hipStream_t s) {
     const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
     const int nq = (n_out + kQuad - 1) / kQuad;
     const dim3 grid((nq + QW - 1) / QW), block(64 * NW);
-    hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW, INV, FOLD>), grid, block,
-                       split_lds(n_in, NCOLS, CS, NW), s, wp, x, y, res, partials, n_in, n_out, f);
+    hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW>), grid, block, split_lds(n_in, NCOLS, CS, NW), s, wp,
+                       x, y, res, partials, n_in, n_out);
 }
 
-template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD, bool INV = false, bool FOLD = false>
+template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD>
 void launch_stream(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                   int n_out, const Fold& f, hipStream_t s) {
+                   int n_out, hipStream_t s) {
     const int nq = (n_out + kQuad - 1) / kQuad;
     const dim3 grid((nq + NW * QPW - 1) / (NW * QPW)), block(64 * NW);
-    hipLaunchKernelGGL((q6k_packed_gemv_stream<NCOLS, RES, NCH, QPW, NW, PD, INV, FOLD>), grid, block,
-                       static_cast<size_t>(NCOLS) * (n_in / 32) * 48, s, wp, x, y, res, partials, n_in, n_out, f);
+    hipLaunchKernelGGL((q6k_packed_gemv_stream<NCOLS, RES, NCH, QPW, NW, PD>), grid, block,
+                       static_cast<size_t>(NCOLS) * (n_in / 32) * 48, s, wp, x, y, res, partials, n_in, n_out);
 }
 
-template <int NCOLS, bool RES, bool INV = false>
+template <int NCOLS, bool RES>
 void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                   int n_out, const Fold& f, hipStream_t s) {
+                   int n_out, hipStream_t s) {
     static const int depth = env_int("RMI_PACKED_DEPTH", 2);
     if constexpr (NCOLS <= 2) {
         const PackedCfg c = packed_cfg(n_in, n_out, NCOLS);
         if (c.kind == PackedCfg::kStream) {
             if (n_in / kChunkElems == 2)
-                return launch_stream<NCOLS, RES, 2, 2, 4, 2, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
+                return launch_stream<NCOLS, RES, 2, 2, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
             if (n_in / kChunkElems == 4)
-                return launch_stream<NCOLS, RES, 4, 1, 4, 2, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
-            return launch_stream<NCOLS, RES, 6, 1, 4, 2, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
+                return launch_stream<NCOLS, RES, 4, 1, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
+            return launch_stream<NCOLS, RES, 6, 1, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
         }
         if (c.kind == PackedCfg::kSplit) {
-            if (c.cs == 2) return launch_split<NCOLS, RES, 2, 4, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
-            if (c.nw == 8) return launch_split<NCOLS, RES, 1, 8, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
-            return launch_split<NCOLS, RES, 1, 4, INV>(wp, x, y, res, partials, n_in, n_out, f, s);
+            if (c.cs == 2) return launch_split<NCOLS, RES, 2, 4>(wp, x, y, res, partials, n_in, n_out, s);
+            if (c.nw == 8) return launch_split<NCOLS, RES, 1, 8>(wp, x, y, res, partials, n_in, n_out, s);
+            return launch_split<NCOLS, RES, 1, 4>(wp, x, y, res, partials, n_in, n_out, s);
         }
     }
     const int nq = (n_out + kQuad - 1) / kQuad;
     const size_t lds = static_cast<size_t>(NCOLS) * (n_in / 32) * 48;
     const dim3 grid(packed_grid(nq)), block(kThreads);
     if (depth >= 4)
-        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 4, 4, INV>), grid, block, lds, s, wp, x, y, res, partials, n_in,
-                           n_out, f);
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 4, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in,
+                           n_out);
     else if (depth == 3)
-        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 3, 4, INV>), grid, block, lds, s, wp, x, y, res, partials, n_in,
-                           n_out, f);
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 3, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in,
+                           n_out);
     else
-        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 2, 4, INV>), grid, block, lds, s, wp, x, y, res, partials, n_in,
-                           n_out, f);
+        hipLaunchKernelGGL((q6k_packed_gemv<NCOLS, RES, 2, 4>), grid, block, lds, s, wp, x, y, res, partials, n_in,
+                           n_out);
 }
 
 // LDS of the ingest stage: kMStride uint4 per (4-column group, block)
@@ -1434,16 +1267,16 @@ size_t wide_stage_bytes(int n_in, int ncols) {
 
 // 16 columns whose stage is too wide for the LDS in two K halves (q6k_packed_mfma KP = 2): an even chunk count, half
 // the stage in the LDS and the other half in kPhaseRegs blocks per lane, a wave pair per quad at most
-bool wide_halves(int n_in, int n_out, bool inv) {
+bool wide_halves(int n_in, int n_out) {
     const int nch = n_in / kChunkElems, nq = (n_out + kQuad - 1) / kQuad;
     static const bool on = env_int("RMI_WIDE_HALVES", 1) != 0;
-    return on && !inv && (nch == 4 || nch == 6) && wide_stage_bytes(n_in, 16) / 2 <= kWideStageBytes &&
+    return on && (nch == 4 || nch == 6) && wide_stage_bytes(n_in, 16) / 2 <= kWideStageBytes &&
            16 * (n_in / 64) <= 64 * kWideWaves * kPhaseRegs && nq <= cu_count() * (kWideWaves / 2);
 }
 
 // the widest ingest pass (16 or 8 columns) whose stage fits kWideStageBytes (16 also in two K halves), or 0
-int wide_cols(int n_in, int n_out, int remaining, bool inv) {
-    if (remaining >= 16 && (wide_stage_bytes(n_in, 16) <= kWideStageBytes || wide_halves(n_in, n_out, inv))) return 16;
+int wide_cols(int n_in, int n_out, int remaining) {
+    if (remaining >= 16 && (wide_stage_bytes(n_in, 16) <= kWideStageBytes || wide_halves(n_in, n_out))) return 16;
     if (remaining >= 8 && wide_stage_bytes(n_in, 8) <= kWideStageBytes) return 8;
     return 0;
 }
@@ -1458,15 +1291,15 @@ int wide_grid(int nq, int units_per_wg) {
     return (units + units_per_wg - 1) / units_per_wg;
 }
 
-template <int NCOLS, bool RES, bool INV = false>
+template <int NCOLS, bool RES>
 int launch_packed_wide(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                       int n_out, const Fold& f, hipStream_t s) {
+                       int n_out, hipStream_t s) {
     constexpr int D = 3;
     constexpr int NCG = NCOLS / 4;
-    auto kern = q6k_packed_mfma<NCG, RES, D, INV>;
-    auto kern2 = q6k_packed_mfma<NCG, RES, D, false, 2>;
-    auto kernl = q6k_packed_mfma<NCG, RES, D, false, 1, 1, 0, true>;
-    auto kern2l = q6k_packed_mfma<NCG, RES, D, false, 2, 1, 0, true>;
+    auto kern = q6k_packed_mfma<NCG, RES, D>;
+    auto kern2 = q6k_packed_mfma<NCG, RES, D, 2>;
+    auto kernl = q6k_packed_mfma<NCG, RES, D, 1, 1, 0, true>;
+    auto kern2l = q6k_packed_mfma<NCG, RES, D, 2, 1, 0, true>;
     auto lds_attr = [](auto k) {
         return hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    kWideStageBytes) == hipSuccess;
@@ -1477,22 +1310,22 @@ int launch_packed_wide(const uint8_t* wp, const uint8_t* x, float* y, const floa
     static const bool le_on = env_int("RMI_WIDE_LE", 1) != 0;
     auto le_bytes = [](int ncw) { return static_cast<size_t>(kWideWaves) * 64 * 4 * ncw * sizeof(float); };
     const int nq = (n_out + kQuad - 1) / kQuad;
-    const size_t lds = wide_stage_bytes(n_in, NCOLS) + (INV ? NCOLS * 4 * sizeof(float) : 0);
+    const size_t lds = wide_stage_bytes(n_in, NCOLS);
     if (lds > kWideStageBytes) {
         if constexpr (NCOLS == 16) {
             // two K halves, a wave pair per quad (the second half's blocks take 54 registers: one tile fewer in flight)
             // (the LDS row sums reuse the stage after the last chunk)
-            auto kh4 = q6k_packed_mfma<4, RES, 2, false, 2, 2, 4, true>;
-            auto kh6 = q6k_packed_mfma<4, RES, 2, false, 2, 2, 6, true>;
+            auto kh4 = q6k_packed_mfma<4, RES, 2, 2, 2, 4, true>;
+            auto kh6 = q6k_packed_mfma<4, RES, 2, 2, 2, 6, true>;
             static const bool attr_h = lds_attr(kh4) && lds_attr(kh6);
             if (!attr_h) return fail(RMI_ERR_LAUNCH, "native_q6_k_mmvq_packed: wide LDS stage not available");
-            if (wide_halves(n_in, n_out, INV)) {
+            if (wide_halves(n_in, n_out)) {
                 const dim3 grid((nq + kWideWaves / 2 - 1) / (kWideWaves / 2)), block(64 * kWideWaves);
                 if (lds / 2 < le_bytes(2)) return fail(RMI_ERR_SHAPE, "native_q6_k_mmvq_packed: half stage too small");
                 if (n_in / kChunkElems == 4)
-                    hipLaunchKernelGGL(kh4, grid, block, lds / 2, s, wp, x, y, res, partials, n_in, n_out, f);
+                    hipLaunchKernelGGL(kh4, grid, block, lds / 2, s, wp, x, y, res, partials, n_in, n_out);
                 else if (n_in / kChunkElems == 6)
-                    hipLaunchKernelGGL(kh6, grid, block, lds / 2, s, wp, x, y, res, partials, n_in, n_out, f);
+                    hipLaunchKernelGGL(kh6, grid, block, lds / 2, s, wp, x, y, res, partials, n_in, n_out);
                 else
                     return fail(RMI_ERR_SHAPE, "native_q6_k_mmvq_packed: wide stage exceeds the LDS");
                 return RMI_OK;
@@ -1505,18 +1338,18 @@ int launch_packed_wide(const uint8_t* wp, const uint8_t* x, float* y, const floa
     static const bool split_on = env_int("RMI_WIDE_SPLIT", 1) != 0;
     const int g1 = wide_grid(nq, kWideWaves), g2 = wide_grid(nq, kWideWaves / 2);
     const dim3 block(64 * kWideWaves);
-    if (!INV && split_on && 4 * g1 < 3 * cu_count() && g2 > g1) {
+    if (split_on && 4 * g1 < 3 * cu_count() && g2 > g1) {
         const size_t l2 = lds + le_bytes(NCG / 2);
         if (le_on && NCG >= 2 && l2 <= kWideStageBytes)
-            hipLaunchKernelGGL(kern2l, dim3(g2), block, l2, s, wp, x, y, res, partials, n_in, n_out, f);
+            hipLaunchKernelGGL(kern2l, dim3(g2), block, l2, s, wp, x, y, res, partials, n_in, n_out);
         else
-            hipLaunchKernelGGL(kern2, dim3(g2), block, lds, s, wp, x, y, res, partials, n_in, n_out, f);
+            hipLaunchKernelGGL(kern2, dim3(g2), block, lds, s, wp, x, y, res, partials, n_in, n_out);
     } else {
         const size_t l1 = lds + le_bytes(NCG);
-        if (le_on && !INV && l1 <= kWideStageBytes)
-            hipLaunchKernelGGL(kernl, dim3(g1), block, l1, s, wp, x, y, res, partials, n_in, n_out, f);
+        if (le_on && l1 <= kWideStageBytes)
+            hipLaunchKernelGGL(kernl, dim3(g1), block, l1, s, wp, x, y, res, partials, n_in, n_out);
         else
-            hipLaunchKernelGGL(kern, dim3(g1), block, lds, s, wp, x, y, res, partials, n_in, n_out, f);
+            hipLaunchKernelGGL(kern, dim3(g1), block, lds, s, wp, x, y, res, partials, n_in, n_out);
     }
     return RMI_OK;
 }
@@ -1528,35 +1361,32 @@ int cols_per_pass(int n_in) {
 }
 
 // Columns are cut into passes (16 or 8 wide, then up to 4); each pass reads the weights once.  The pass width never
-// changes a column's result: lane ownership and reduction order depend on the shape only.  INV: the input columns are
-// a folded norm's Q8_1(x * w); f.part holds x's partials, column j at + j * n_in / 4.
-template <bool RES, bool INV = false>
+// changes a column's result: lane ownership and reduction order depend on the shape only.
+template <bool RES>
 int run_packed(const void* wpv, const void* xv, float* y, const float* res, float* partials, int n_in, int n_out,
-               int ncols, const Fold& fold, hipStream_t s) {
+               int ncols, hipStream_t s) {
     const auto* wp = static_cast<const uint8_t*>(wpv);
     const auto* x = static_cast<const uint8_t*>(xv);
     const int per = cols_per_pass(n_in);
     const size_t xcol = static_cast<size_t>(n_in / 32) * kQ8_1Bytes;
     const size_t pcol = static_cast<size_t>((n_out + 3) / 4);
     for (int j = 0; j < ncols;) {
-        const int wide = wide_cols(n_in, n_out, ncols - j, INV);
+        const int wide = wide_cols(n_in, n_out, ncols - j);
         const int nj = wide ? wide : std::min(per, ncols - j);
         const uint8_t* xj = x + j * xcol;
         float* yj = y + static_cast<size_t>(j) * n_out;
         const float* rj = RES ? res + static_cast<size_t>(j) * n_out : nullptr;
         float* pj = RES ? partials + j * pcol : nullptr;
-        Fold fj = fold;
-        if (INV) fj.part = fold.part + static_cast<size_t>(j) * (n_in / 4);
         switch (nj) {
-            case 1: launch_packed<1, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s); break;
-            case 2: launch_packed<2, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s); break;
-            case 3: launch_packed<3, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s); break;
-            case 4: launch_packed<4, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s); break;
+            case 1: launch_packed<1, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
+            case 2: launch_packed<2, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
+            case 3: launch_packed<3, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
+            case 4: launch_packed<4, RES>(wp, xj, yj, rj, pj, n_in, n_out, s); break;
             case 8:
-                if (const int rc = launch_packed_wide<8, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s)) return rc;
+                if (const int rc = launch_packed_wide<8, RES>(wp, xj, yj, rj, pj, n_in, n_out, s)) return rc;
                 break;
             default:
-                if (const int rc = launch_packed_wide<16, RES, INV>(wp, xj, yj, rj, pj, n_in, n_out, fj, s)) return rc;
+                if (const int rc = launch_packed_wide<16, RES>(wp, xj, yj, rj, pj, n_in, n_out, s)) return rc;
                 break;
         }
         if (const int rc = launch_status("native_q6_k_mmvq_packed")) return rc;
@@ -1674,81 +1504,46 @@ extern "C" int rmi_q6_k_pack_swiglu(const void* w, void* w_packed, int n_in, int
 namespace rmi {
 namespace {
 int swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_in, int n_ff, int ncols,
-                  const Fold* fold, void* stream) {
+                  void* stream) {
     if (n_in != 2 * kChunkElems || n_ff <= 0 || n_ff % 32 != 0 || ncols < 1 || ncols > 2)
         return fail(RMI_ERR_SHAPE, "q6_k_swiglu_packed: n_in must be 4096, n_ff a positive multiple of 32, ncols 1 or 2");
-    if (!aligned16(w_packed) || !aligned4(x_q8_1) || !aligned4(y_q8_1) || (fold && !aligned4(fold->part)))
+    if (!aligned16(w_packed) || !aligned4(x_q8_1) || !aligned4(y_q8_1))
         return fail(RMI_ERR_POINTER, "q6_k_swiglu_packed: null or misaligned pointer");
     if (!stream) return fail(RMI_ERR_STREAM, "native MMVQ requires an explicit non-null CUDA stream");
     const auto* wp = static_cast<const uint8_t*>(w_packed);
     const auto* x = static_cast<const uint8_t*>(x_q8_1);
     auto* y = static_cast<uint8_t*>(y_q8_1);
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const Fold f = fold ? *fold : Fold{};
     // two 32-output groups per 8-wave workgroup (192 workgroups at n_ff 12288: one per CU) when n_ff allows, else one
     // per 4-wave workgroup
     auto go = [&](auto kern, int gpw, int nw) {
         const size_t lds = static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(gpw) * ncols * 64 * 4;
-        hipLaunchKernelGGL(kern, dim3(n_ff / 32 / gpw), dim3(64 * nw), lds, s, wp, x, y, n_in, n_ff, f);
+        hipLaunchKernelGGL(kern, dim3(n_ff / 32 / gpw), dim3(64 * nw), lds, s, wp, x, y, n_in, n_ff);
     };
     const bool two = n_ff % 64 == 0;
     if (ncols == 1) {
-        if (two) fold ? go(q6k_packed_swiglu<1, true, 8, 4>, 2, 8) : go(q6k_packed_swiglu<1, false, 8, 4>, 2, 8);
-        else fold ? go(q6k_packed_swiglu<1, true>, 1, 4) : go(q6k_packed_swiglu<1>, 1, 4);
+        if (two) go(q6k_packed_swiglu<1, 8, 4>, 2, 8);
+        else go(q6k_packed_swiglu<1>, 1, 4);
     } else {
-        if (two) fold ? go(q6k_packed_swiglu<2, true, 8, 4>, 2, 8) : go(q6k_packed_swiglu<2, false, 8, 4>, 2, 8);
-        else fold ? go(q6k_packed_swiglu<2, true>, 1, 4) : go(q6k_packed_swiglu<2>, 1, 4);
+        if (two) go(q6k_packed_swiglu<2, 8, 4>, 2, 8);
+        else go(q6k_packed_swiglu<2>, 1, 4);
     }
     return launch_status("q6_k_swiglu_packed");
 }
 
-// the residual GEMVs that carry the next norm's Q8_1 in their epilogue: rows of 4096 (split, 8 quads per workgroup)
-// and of 12288 (stream, 8 waves of one quad), 1 or 2 columns, n_out a multiple of 32
-bool fold_shape(int n_in, int n_out, int ncols) {
-    return (n_in == 2 * kChunkElems || n_in == 6 * kChunkElems) && n_out > 0 && n_out % 32 == 0 && ncols >= 1 &&
-           ncols <= 2;
-}
-
-template <int NCOLS>
-void launch_res_fold(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                     int n_out, const Fold& f, hipStream_t s) {
-    static const int split_waves = env_int("RMI_FOLD_SPLIT_WAVES", 16);
-    if (n_in == 6 * kChunkElems)
-        return launch_stream<NCOLS, true, 6, 1, 8, 2, false, true>(wp, x, y, res, partials, n_in, n_out, f, s);
-    if (split_waves == 8)   // a quad's two chunks on one wave
-        return launch_split<NCOLS, true, 2, 8, false, true>(wp, x, y, res, partials, n_in, n_out, f, s);
-    return launch_split<NCOLS, true, 1, 16, false, true>(wp, x, y, res, partials, n_in, n_out, f, s);
-}
 }  // namespace
 }  // namespace rmi
 
 extern "C" int rmi_native_q6_k_swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_in, int n_ff,
                                              int ncols, void* stream) {
-    return swiglu_packed(w_packed, x_q8_1, y_q8_1, n_in, n_ff, ncols, nullptr, stream);
-}
-
-extern "C" int rmi_native_q6_k_swiglu_packed_scaled(const void* w_packed, const void* x_q8_1, const float* partials,
-                                                    float eps, void* y_q8_1, int n_in, int n_ff, int ncols,
-                                                    void* stream) {
-    const Fold f{partials, eps, nullptr, nullptr};
-    return swiglu_packed(w_packed, x_q8_1, y_q8_1, n_in, n_ff, ncols, &f, stream);
+    return swiglu_packed(w_packed, x_q8_1, y_q8_1, n_in, n_ff, ncols, stream);
 }
 
 extern "C" int rmi_native_q6_k_mmvq_packed(const void* w_packed, const void* x_q8_1, float* y, int n_in, int n_out,
                                            int ncols, void* stream) {
     if (int rc = validate_packed(w_packed, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
-    return run_packed<false>(w_packed, x_q8_1, y, nullptr, nullptr, n_in, n_out, ncols, Fold{},
+    return run_packed<false>(w_packed, x_q8_1, y, nullptr, nullptr, n_in, n_out, ncols,
                              static_cast<hipStream_t>(stream));
-}
-
-extern "C" int rmi_native_q6_k_mmvq_packed_scaled(const void* w_packed, const void* x_q8_1, const float* partials,
-                                                  float eps, float* y, int n_in, int n_out, int ncols, void* stream) {
-    if (int rc = validate_packed(w_packed, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
-    if (!aligned4(partials)) return fail(RMI_ERR_POINTER, "packed scaled GEMV: null or misaligned partials");
-    if (n_in > 4 * 1024 && ncols >= 8)
-        return fail(RMI_ERR_SHAPE, "packed scaled GEMV: 8 or more columns need n_in <= 4096");
-    return run_packed<false, true>(w_packed, x_q8_1, y, nullptr, nullptr, n_in, n_out, ncols,
-                                   Fold{partials, eps, nullptr, nullptr}, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int rmi_native_q6_k_mmvq_packed_res_n(const void* w_packed, const void* x_q8_1, float* y, const float* res,
@@ -1756,28 +1551,5 @@ extern "C" int rmi_native_q6_k_mmvq_packed_res_n(const void* w_packed, const voi
     if (int rc = validate_packed(w_packed, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
     if (!aligned4(res) || !aligned4(partials))
         return fail(RMI_ERR_POINTER, "native MMVQ requires non-null 4-byte aligned device pointers");
-    return run_packed<true>(w_packed, x_q8_1, y, res, partials, n_in, n_out, ncols, Fold{},
-                            static_cast<hipStream_t>(stream));
-}
-
-extern "C" int rmi_q6_k_packed_fold_supported(int n_in, int n_out, int ncols) {
-    return fold_shape(n_in, n_out, ncols) ? 1 : 0;
-}
-
-extern "C" int rmi_native_q6_k_mmvq_packed_res_fold(const void* w_packed, const void* x_q8_1, float* y,
-                                                    const float* res, float* partials, const float* w_next,
-                                                    void* y_q8_1_next, int n_in, int n_out, int ncols, void* stream) {
-    if (int rc = validate_packed(w_packed, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
-    if (!fold_shape(n_in, n_out, ncols))
-        return fail(RMI_ERR_UNSUPPORTED, "packed residual GEMV with the next norm: n_in 4096 or 12288, n_out a "
-                                         "multiple of 32, 1 or 2 columns");
-    if (!aligned4(res) || !aligned4(partials) || !aligned4(w_next) || !aligned4(y_q8_1_next))
-        return fail(RMI_ERR_POINTER, "native MMVQ requires non-null 4-byte aligned device pointers");
-    const Fold f{nullptr, 0.0f, w_next, static_cast<uint8_t*>(y_q8_1_next)};
-    const auto* wp = static_cast<const uint8_t*>(w_packed);
-    const auto* x = static_cast<const uint8_t*>(x_q8_1);
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (ncols == 1) launch_res_fold<1>(wp, x, y, res, partials, n_in, n_out, f, s);
-    else launch_res_fold<2>(wp, x, y, res, partials, n_in, n_out, f, s);
-    return launch_status("native_q6_k_mmvq_packed_res_fold");
+    return run_packed<true>(w_packed, x_q8_1, y, res, partials, n_in, n_out, ncols, static_cast<hipStream_t>(stream));
 }

@@ -25,7 +25,7 @@ class ModelConfig(ctypes.Structure):
 class EngineInfo(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in ("trunk_weight_bytes", "lm_head_bytes", "draft_block_bytes",
                                                "round_weight_bytes", "token_weight_bytes", "kv_bytes_per_pos")] + \
-               [(n, ctypes.c_int) for n in ("gdn_layers", "attn_layers", "max_ctx", "attn_chunk", "norm_fold")]
+               [(n, ctypes.c_int) for n in ("gdn_layers", "attn_layers", "max_ctx", "attn_chunk")]
 
 
 class GenRequest(ctypes.Structure):

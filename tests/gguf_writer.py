@@ -58,6 +58,6 @@ def write_gguf(path, meta, tensors, alignment=32, version=3):
         pos = 0
         for o, data in blobs:
             f.write(b"\0" * (o - pos))
-            f.write(data.tobytes())
+            f.write(memoryview(data))   # the array's own memory: no copy of a multi-GB tensor
             pos = o + data.size
     return path

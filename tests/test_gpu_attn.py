@@ -40,7 +40,9 @@ def flash(rmi, q, kc, vc, p0, gate, ntok, max_ctx, nsub):
     return host(y), host(q8)
 
 
-@pytest.mark.parametrize("ctx,nsub", [(4096, 1), (32768, 4), (65536, 4)])
+# nsub 2 at ctx 4096 and 8 at ctx 65536 are the chunkings the engine picks (clamp(max_ctx / 8192, 2, 16): 128- and
+# 512-position chunks), so the merge path the round runs is checked against the oracle at its real chunk counts
+@pytest.mark.parametrize("ctx,nsub", [(4096, 1), (4096, 2), (32768, 4), (65536, 4), (65536, 8)])
 def test_flash_decode_matches_oracle(orc, rmi, ctx, nsub):
     kc, vc = kv_cache(orc, ctx, seed=ctx)
     q = orc.normal(2 * NH * HD, seed=ctx + 7)

@@ -73,20 +73,22 @@ def test_small_model_eager_equals_graph(eng_mod):
 
 def test_qwen35_9b_mtp_stream_bit_identical_at_4k(eng_mod):
     """config 5 at full size: random-init 9B-class qwen35 (32 layers, 24 GDN + 8 GQA, hidden 4096, FFN 12288, vocab
-    248320, nextn block), synthetic 4K context, greedy vs MTP at forced acceptance 0 / 0.5 / 1.0."""
+    248320, nextn block), synthetic 4K context, the config's 400 generated tokens: greedy vs MTP at forced acceptance
+    0 / 0.5 / 1.0 and with the natural draft (README.md:80-82, bench/RESULTS.md:81-82 diff 400-token streams)."""
     E = eng_mod
-    eng = E.Engine(E.qwen35_9b_config(), seed=2024, max_ctx=4096 + 256)
+    eng = E.Engine(E.qwen35_9b_config(), seed=2024, max_ctx=4096 + 512)
     info = eng.info()
     assert info["gdn_layers"] == 24 and info["attn_layers"] == 8
-    assert info["norm_fold"] == 0   # the reference's norm order (RMI_NORM_FOLD=1 folds them)
     # one weight pass per round: trunk 5,675,335,680 + lm_head 834,355,200 + draft block 199,557,120 + lm_head
     assert info["trunk_weight_bytes"] == 5_675_335_680 and info["lm_head_bytes"] == 834_355_200
     assert info["round_weight_bytes"] == 7_543_603_200
     first = eng.synth_context(4096, seed=11, last_token=12345)
     pos0, cur0 = eng.state()
     assert pos0 == 4096 and cur0 == first
-    ref, res = streams_agree(E, eng, pos0, cur0, 64, natural=False)
-    assert res["accept1"]["rounds"] == 32 and res["accept0"]["rounds"] == 64
+    ref, res = streams_agree(E, eng, pos0, cur0, 400, natural=True)
+    assert len(set(ref)) > 3, "degenerate stream"
+    assert res["accept1"]["rounds"] == 200 and res["accept0"]["rounds"] == 400
+    assert res["accept05"]["accepted"] == (res["accept05"]["rounds"] + 1) // 2
     eng.close()
 
 
@@ -100,26 +102,17 @@ def engine_64k(eng_mod):
 
 def test_qwen35_9b_mtp_stream_bit_identical_at_64k(eng_mod, engine_64k):
     """config 5 at ctx 65536: synthetic context of 64K positions (attention over 512-position chunks, 128 of them per
-    query), greedy vs MTP at forced acceptance 0 / 0.5 / 1.0 for 64 tokens, then the config's 400 generated tokens at
-    acceptance 0.5 and with the natural draft."""
+    query), the config's 400 generated tokens: greedy vs MTP at forced acceptance 0 / 0.5 / 1.0 and with the natural
+    draft."""
     E, eng = eng_mod, engine_64k
     ctx = 65536 - 512
     first = eng.synth_context(ctx, seed=13, last_token=4321)
     pos0, cur0 = eng.state()
     assert pos0 == ctx and cur0 == first
-    ref, res = streams_agree(E, eng, pos0, cur0, 64, natural=False)
-    assert res["accept1"]["rounds"] == 32 and res["accept0"]["rounds"] == 64
-    # 400 generated tokens (bench/RESULTS.md:81-82 diff the 400-token stream against greedy)
-    eng.restore_state(pos0, cur0)
-    long_ref, _ = eng.generate(400, mode=E.GREEDY)
-    assert long_ref[:64] == ref
-    eng.restore_state(pos0, cur0)
-    toks, st = eng.generate(400, mode=E.MTP_FORCED, ref_tokens=long_ref, ref_base=pos0 + 1, pattern=[1, 0])
-    assert toks == long_ref, f"400-token MTP stream differs at {next(i for i in range(400) if toks[i] != long_ref[i])}"
-    assert st["accepted"] == (st["rounds"] + 1) // 2
-    eng.restore_state(pos0, cur0)
-    toks, _ = eng.generate(400, mode=E.MTP)
-    assert toks == long_ref, "400-token MTP stream (natural draft) differs from greedy"
+    ref, res = streams_agree(E, eng, pos0, cur0, 400, natural=True)
+    assert len(set(ref)) > 3, "degenerate stream"
+    assert res["accept1"]["rounds"] == 200 and res["accept0"]["rounds"] == 400
+    assert res["accept05"]["accepted"] == (res["accept05"]["rounds"] + 1) // 2
 
 
 def test_qwen35_9b_mtp_after_ingest_past_32k(eng_mod, engine_64k):
@@ -134,33 +127,28 @@ def test_qwen35_9b_mtp_after_ingest_past_32k(eng_mod, engine_64k):
     assert len(set(ref)) > 3, "degenerate stream"
 
 
-def test_small_model_folded_norms_follow_the_unfolded_engine(eng_mod, monkeypatch):
-    """the folded norms (RMI_NORM_FOLD=1: Q8_1(x * w) into a GEMV that scales by inv) against the same seeded model
-    with the default rms_quant_apply (the reference's rounding order).  The two round a few activations to
-    neighbouring Q8_1 codes, and the GDN state carries each such flip to later tokens, so the bar is the multi-layer one
-    of tests/test_gpu_gguf.py: after a 7-token prompt through 4 layers, logits and hidden within 5e-2 of max|.| and
-    correlated > 0.999.  The folded engine's MTP stream equals its own greedy stream."""
+def test_gdn_exchange_timeout_is_an_error(eng_mod):
+    """a bounded wait of the GDN layer kernel that runs out makes the engine call fail (RMI_ERR_STATE) instead of
+    returning tokens computed from stale sums.  The timeout is forced from the host (a 4-poll bound and every wait
+    made to miss), so every kernel still ends normally; the normal bound then gives a clean call again."""
+    import rapier_amd as rmi
     E = eng_mod
-    monkeypatch.delenv("RMI_NORM_FOLD", raising=False)
-    ref = E.Engine(E.small_config(), seed=21, max_ctx=256)
-    monkeypatch.setenv("RMI_NORM_FOLD", "1")
-    fold = E.Engine(E.small_config(), seed=21, max_ctx=256)
-    monkeypatch.delenv("RMI_NORM_FOLD")
-    assert ref.info()["norm_fold"] == 0 and fold.info()["norm_fold"] == 1
-    prompt = [int(t) for t in np.random.default_rng(8).integers(0, 5000, size=7)]
-    f_ref, f_fold = ref.prefill(prompt, batch=1), fold.prefill(prompt, batch=16)
-    n_v, n_e = 5000, 2048
-    lr = ref.read(E.BUF_LOGITS, 0, 4 * n_v).view(np.float32).astype(np.float64)
-    lf = fold.read(E.BUF_LOGITS, 0, 4 * n_v).view(np.float32).astype(np.float64)
-    assert np.abs(lf - lr).max() <= 5e-2 * np.abs(lr).max()
-    assert np.corrcoef(lf, lr)[0, 1] > 0.999
-    hr = ref.read(E.BUF_HIDDEN, 0, 4 * n_e).view(np.float32).astype(np.float64)
-    hf = fold.read(E.BUF_HIDDEN, 0, 4 * n_e).view(np.float32).astype(np.float64)
-    assert np.abs(hf - hr).max() <= 5e-2 * np.abs(hr).max()
-    top = np.sort(lr)[-2:]
-    if top[1] - top[0] > 1e-1 * np.abs(lr).max():
-        assert f_fold == f_ref
-    pos0, cur0 = fold.state()
-    streams_agree(E, fold, pos0, cur0, 24)
-    ref.close()
-    fold.close()
+    eng = E.Engine(E.small_config(), seed=5, max_ctx=256)
+    eng.prefill([1, 2, 3, 4])
+    pos0, cur0 = eng.state()
+    eng.save_state()
+    ref, _ = eng.generate(8, mode=E.MTP)
+    before = rmi.gdn_exchange_timeouts()
+    eng.restore_state(pos0, cur0)
+    try:
+        rmi.gdn_exchange_test(4, True)
+        with pytest.raises(rmi.RapierError, match="GDN exchange"):
+            eng.generate(8, mode=E.MTP)
+    finally:
+        rmi.gdn_exchange_test(0, False)
+    grown = rmi.gdn_exchange_timeouts() - before
+    assert grown > 0
+    eng.restore_state(pos0, cur0)
+    toks, _ = eng.generate(8, mode=E.MTP)
+    assert toks == ref and rmi.gdn_exchange_timeouts() - before == grown
+    eng.close()

@@ -164,7 +164,7 @@ def test_gdn_split_kernel_bitwise_equal_one_workgroup_kernel(orc, rmi):
                                dev(ab3[:ntok * 2 * H_V]), 2 * H_V, dev(conv_w), dev(dt), dev(ssm_a), dev(gamma), EPS, y,
                                H_V * S, q8, H_V * S // 32 * 36, H_K, H_V, ntok, xch)
     t.cuda.synchronize()
-    assert rmi.gdn_exchange_timeouts() == before == 0
+    assert rmi.gdn_exchange_timeouts() == before   # none during this test (a forced-timeout test may have run)
 
 
 def test_reference_surface_entry_points(orc, rmi):

@@ -16,6 +16,8 @@ by about (amax / 127) / (sqrt(n) rms), ~1e-3 of their scale, and later tokens an
 - the first greedy token equal to the oracle's argmax wherever the oracle's top-2 margin exceeds twice the bound; along
   a greedy stream (the oracle fed the engine's tokens) every token whose oracle margin exceeds 3e-2 of max|logit|
   (3x the observed error) equal to the oracle's argmax; MTP after a GGUF load bit-identical to greedy."""
+import os
+
 import numpy as np
 import pytest
 
@@ -303,4 +305,91 @@ def test_gguf_draft_head_matches_oracle(orc, E, tmp_path, pattern, emb_type):
             checked += 1
     assert s["cand"] == (s["c1"] if s["accept"] else s["c0"])
     assert checked >= 1, "no draft step with a clear oracle margin"
+    eng.close()
+
+
+# ---- full width: the 9B shapes (hidden 4096, FFN 12288, vocab 248320, 16 / 32 GDN heads, 16 / 4 attention heads) ----
+FULL = dict(N_EMBD=4096, N_FF=12288, N_VOCAB=248320, H_K=16, H_V=32, N_HEAD=16, N_KV=4)
+
+
+@pytest.fixture(scope="module")
+def full_width(orc, tmp_path_factory):
+    """a 2.6 GB file of the 9B widths with three GDN layers, one attention layer and the nextn block: every GEMV at
+    its round shape (in-projections 12352 / 10240 x 4096, up||gate 24576 x 4096, down 4096 x 12288, eh_proj
+    4096 x 8192, lm_head 248320 x 4096) and the embedding / argmax / top-k over the full vocabulary"""
+    import sys
+    mod = sys.modules[__name__]
+    saved = {k: getattr(mod, k) for k in FULL}
+    for k, v in FULL.items():
+        setattr(mod, k, v)
+    try:
+        t, meta = build_model(orc, seed=31, pattern=(0, 0, 0, 1))
+        path = write(t, meta, tmp_path_factory.mktemp("full") / "full.gguf")
+    finally:
+        for k, v in saved.items():
+            setattr(mod, k, v)
+    yield t, path
+    os.unlink(path)
+
+
+@pytest.mark.timeout(400)
+def test_gguf_full_width_matches_oracle_model(orc, E, full_width):
+    """qw:1773-1824 at full width: a 5-token prompt through the engine and through oracle/model.py; logits, hidden and
+    GDN states within the 4-layer bars of this module (5e-2 of max|.|, correlation > 0.999), K/V rows within 6e-2, the
+    first token the oracle's argmax where its margin is clear; the chunked ingest leaves the per-token state"""
+    t, path = full_width
+    V, D = FULL["N_VOCAB"], FULL["N_EMBD"]
+    eng = E.Engine.from_gguf(str(path), max_ctx=512)
+    c = eng.cfg
+    assert (c.n_embd, c.n_ff, c.n_vocab, c.ssm_h_k, c.ssm_h_v, c.n_head, c.n_kv) == \
+        (D, FULL["N_FF"], V, FULL["H_K"], FULL["H_V"], FULL["N_HEAD"], FULL["N_KV"])
+    m = oracle_model(orc, t, 4)
+    prompt = [5, 77, 12345, 248000, 9]
+    first = eng.prefill(prompt, batch=1)
+    lo, h = m.prefill(prompt)
+    logits = eng.read(E.BUF_LOGITS, 0, 4 * V).view(np.float32)
+    close(logits, lo, 5e-2, "logits")
+    assert np.corrcoef(logits, lo)[0, 1] > 0.999
+    close(eng.read(E.BUF_HIDDEN, 0, 4 * D).view(np.float32), h, 5e-2, "hidden")
+    if clear_margin(lo, 5e-2):
+        assert first == int(np.argmax(lo))
+    for il in range(3):
+        st = eng.read(E.BUF_GDN_STATE, il, 4 * 128 * FULL["H_V"] * 128).view(np.float32)
+        close(st, m.state[il], 5e-2, f"GDN state of layer {il}")
+    n = len(prompt) * FULL["N_KV"] * HD
+    for il in (3, 4):   # the trunk attention layer and the draft block
+        for which, ref in ((E.BUF_K_CACHE, m.kc[il]), (E.BUF_V_CACHE, m.vc[il])):
+            got = eng.read(which, il, 2 * n).view(np.float16).astype(np.float64)
+            check_rows(got, ref[:n].view(np.float16).astype(np.float64), FULL["N_KV"] * HD, 0.0, 6e-2,
+                       f"cache {which} layer {il}")
+    h1 = eng.read(E.BUF_HIDDEN, 0, 4 * D)
+    assert eng.prefill(prompt, batch=16) == first
+    assert np.array_equal(eng.read(E.BUF_HIDDEN, 0, 4 * D), h1)
+    eng.close()
+
+
+@pytest.mark.timeout(400)
+def test_gguf_full_width_greedy_and_mtp(orc, E, full_width):
+    """greedy tokens at full width follow the oracle model where its top-2 margin is clear (the oracle fed the
+    engine's tokens), and MTP on the same file reproduces the greedy stream"""
+    t, path = full_width
+    eng = E.Engine.from_gguf(str(path), max_ctx=512)
+    m = oracle_model(orc, t, 4)
+    prompt = [11, 222, 3333, 44]
+    first = eng.prefill(prompt, batch=4)
+    m.prefill(prompt)
+    pos0, cur0 = eng.state()
+    eng.save_state()
+    toks, _ = eng.generate(6, mode=E.GREEDY)
+    stream = [first] + toks
+    checked = 0
+    for i in range(len(toks)):
+        lo, _ = m.forward(stream[i], len(prompt) + i)
+        if clear_margin(lo, 1.5e-2):
+            assert stream[i + 1] == int(np.argmax(lo)), f"greedy token {i}"
+            checked += 1
+    assert checked >= 2, "too few tokens with a clear margin"
+    eng.restore_state(pos0, cur0)
+    mtp, _ = eng.generate(6, mode=E.MTP)
+    assert mtp == toks
     eng.close()

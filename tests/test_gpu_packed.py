@@ -52,6 +52,30 @@ def test_packed_matches_oracle_and_columns(orc, rmi, n_in, n_out):
         assert np.array_equal(host(y1).view(np.uint32), y2h[c * n_out:(c + 1) * n_out].view(np.uint32))
 
 
+def test_lm_head_shape_matches_oracle(orc, rmi):
+    """the round's lm_head launch at its full shape (248320 x 4096 Q6_K, 834 MB, two columns: the stream kernel with
+    two quads per wave on the packed copy, qw:1591-1597) and the drop-in entry point on the GGUF blocks, against the
+    oracle's fp64 GEMV; columns bitwise the 1-column launch, both layouts bitwise equal"""
+    n_in, n_out = 4096, 248320
+    w = orc.gen_q6k(n_out, n_in, seed=248320)
+    xq = orc.quantize_q8_1(orc.normal(2 * n_in, seed=4097), n_in, 2)
+    ref = orc.q6k_gemv(w, xq, n_in, n_out, ncols=2)
+    wd, xd = dev(w), dev(xq)
+    wp = packed(rmi, wd, n_in, n_out)
+    y2 = empty(2 * n_out)
+    rmi.native_q6_k_mmvq_packed(wp, xd, y2, n_in, n_out, 2)
+    y2h = host(y2)
+    for c in range(2):
+        assert_close_rel(y2h[c * n_out:(c + 1) * n_out], ref[c * n_out:(c + 1) * n_out], what=f"lm_head col {c}")
+    y1 = empty(n_out)
+    rmi.native_q6_k_mmvq_packed(wp, dev(xq[(n_in // 32) * 36:]), y1, n_in, n_out, 1)
+    assert np.array_equal(host(y1).view(np.uint32), y2h[n_out:].view(np.uint32))
+    del wp
+    yg = empty(2 * n_out)
+    rmi.native_q6_k_mmvq(wd, xd, yg, n_in, n_out, 2)
+    assert np.array_equal(host(yg).view(np.uint32), y2h.view(np.uint32))
+
+
 # n_in 4096: the split kernel (a quad's two chunks on two waves) up to 16384 rows, the stream kernel (two quads per
 # wave) above, ragged at 33001; (2048, 1001) the pipelined loop kernel
 @pytest.mark.parametrize("n_in,n_out", [(4096, 12352), (4096, 10240), (2048, 1001), (4096, 24576), (4096, 33001)])

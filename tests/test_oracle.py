@@ -372,6 +372,32 @@ def _norm_out(orc, x, w, eps):
     return orc.rms_norm_out(x, w, orc.rms_inv(orc.row_sum_partials(x), x.size, eps))
 
 
+def test_swiglu_special_cases(orc):
+    """swiglu_quant's value silu(gate) * up (qw:676-689), pinned without retyping it: gate 0 gives 0, a gate of 40
+    gives 40 * up exactly (sigmoid(40) rounds to 1 in fp64), -40 gives ~0, silu(g) - silu(-g) = g, and the hand-worked
+    silu(1) * 2 = 2 sigmoid(1) (an up / gate swap would give silu(2) * 1 = 1.7616)"""
+    up = np.array([0.5, -3.0, 7.25, 2.0], np.float32)
+    assert np.array_equal(orc.swiglu(up, np.zeros(4, np.float32)), np.zeros(4))
+    assert np.array_equal(orc.swiglu(up, np.full(4, 40.0, np.float32)), 40.0 * up.astype(np.float64))
+    assert np.abs(orc.swiglu(up, np.full(4, -40.0, np.float32))).max() < 1e-14
+    g = np.array([0.3, -1.7, 4.0, 9.5], np.float32)
+    one = np.ones(4, np.float32)
+    np.testing.assert_allclose(orc.swiglu(one, g) - orc.swiglu(one, -g), g.astype(np.float64), rtol=0, atol=1e-15)
+    assert abs(orc.swiglu(np.array([2.0], np.float32), np.array([1.0], np.float32))[0] - 1.4621171572600098) < 1e-15
+
+
+def test_sig_mul_special_cases(orc):
+    """sig_mul_quant's value o * sigmoid(g) (qw:692-704): g 0 halves o exactly, 40 keeps it, -40 gives ~0,
+    sig_mul(o, g) + sig_mul(o, -g) = o, and the hand-worked 2 * sigmoid(1) (an o / g swap gives sigmoid(2) = 0.8808)"""
+    o = np.array([0.5, -3.0, 7.25, 1e4], np.float32)
+    assert np.array_equal(orc.sig_mul(o, np.zeros(4, np.float32)), 0.5 * o.astype(np.float64))
+    assert np.array_equal(orc.sig_mul(o, np.full(4, 40.0, np.float32)), o.astype(np.float64))
+    assert np.abs(orc.sig_mul(o, np.full(4, -40.0, np.float32))).max() < 1e-13
+    g = np.array([0.3, -1.7, 4.0, 9.5], np.float32)
+    np.testing.assert_allclose(orc.sig_mul(o, g) + orc.sig_mul(o, -g), o.astype(np.float64), rtol=1e-15, atol=0)
+    assert abs(orc.sig_mul(np.array([2.0], np.float32), np.array([1.0], np.float32))[0] - 1.4621171572600098) < 1e-15
+
+
 def test_rms_norm_out_matches_definition(orc):
     for n, seed in ((4096, 150), (12288, 151), (8, 152)):
         x = orc.normal(n, seed=seed, std=3.0)
