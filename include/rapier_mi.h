@@ -85,6 +85,18 @@ int rmi_q6_k_pack_swiglu(const void* w, void* w_packed, int n_in, int n_ff, void
  * launch and with no fp32 up / gate rows in memory. */
 int rmi_native_q6_k_swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_in, int n_ff,
                                   int ncols, void* stream);
+/* The reference's norm + GEMV launch pair, rms_quant_apply_kernel (qw:627-655) then native_q6_k_mmvq (mmvq:3627) or
+ * the up / gate GEMVs with swiglu_quant_kernel (qw:676-689), as one launch: the GEMV's workgroups quantize
+ * (x * w_norm) * inv, inv = rsqrt(sum of x's 4-row partials / n_in + eps) by rms_quant_apply's reduction tree, straight
+ * into their activation stage.  Bitwise equal to rmi_rms_quant_apply followed by rmi_native_q6_k_mmvq_packed /
+ * rmi_native_q6_k_swiglu_packed on its Q8_1 output.  x: ncols fp32 columns of n_in (column j at x + j n_in), 16-byte
+ * aligned, as is w_norm; partials: ncols columns of n_in / 4 slots.  n_in = 4096, ncols 1 or 2 (and n_out <= 32768 for
+ * the plain GEMV). */
+int rmi_native_q6_k_mmvq_packed_norm(const void* w_packed, const float* x, const float* w_norm, const float* partials,
+                                     float eps, float* y, int n_in, int n_out, int ncols, void* stream);
+int rmi_native_q6_k_swiglu_packed_norm(const void* w_packed, const float* x, const float* w_norm,
+                                       const float* partials, float eps, void* y_q8_1, int n_in, int n_ff, int ncols,
+                                       void* stream);
 int rmi_native_q6_k_mmvq_packed(const void* w_packed, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                                 void* stream);
 int rmi_native_q6_k_mmvq_packed_res_n(const void* w_packed, const void* x_q8_1, float* y, const float* res,

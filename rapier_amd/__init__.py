@@ -46,6 +46,8 @@ SIGNATURES = {
     "rmi_native_q6_k_mmvq_packed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_packed_res_n": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_q6_k_block_dots": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "rmi_native_q6_k_mmvq_packed_norm": (_i, [_vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _vp]),
+    "rmi_native_q6_k_swiglu_packed_norm": (_i, [_vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _vp]),
     "rmi_gen_q6_k": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
     "rmi_gen_q8_0": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
     "rmi_gen_normal": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
@@ -215,6 +217,20 @@ def native_q6_k_swiglu_packed(w_packed, x_q8_1, y_q8_1, n_in: int, n_ff: int, nc
 
 def native_q6_k_mmvq_packed(w_packed, x_q8_1, y, n_in: int, n_out: int, ncols: int, stream=None):
     _call("rmi_native_q6_k_mmvq_packed", _p(w_packed), _p(x_q8_1), _p(y), n_in, n_out, ncols, _stream(stream))
+
+
+def native_q6_k_mmvq_packed_norm(w_packed, x, w_norm, partials, eps, y, n_in: int, n_out: int, ncols: int,
+                                 stream=None):
+    """rms_quant_apply + packed GEMV in one launch (the norm quantized in the GEMV's stage); same bits as the pair"""
+    _call("rmi_native_q6_k_mmvq_packed_norm", _p(w_packed), _p(x), _p(w_norm), _p(partials), eps, _p(y), n_in, n_out,
+          ncols, _stream(stream))
+
+
+def native_q6_k_swiglu_packed_norm(w_packed, x, w_norm, partials, eps, y_q8_1, n_in: int, n_ff: int, ncols: int,
+                                   stream=None):
+    """rms_quant_apply + the fused up||gate SwiGLU GEMV in one launch; same bits as the pair"""
+    _call("rmi_native_q6_k_swiglu_packed_norm", _p(w_packed), _p(x), _p(w_norm), _p(partials), eps, _p(y_q8_1), n_in,
+          n_ff, ncols, _stream(stream))
 
 
 def native_q6_k_mmvq_packed_res_n(w_packed, x_q8_1, y, res, partials, n_in: int, n_out: int, ncols: int,

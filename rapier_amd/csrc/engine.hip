@@ -107,6 +107,9 @@ struct Engine {
     // the next norm forms its vector's partials itself (rmi_rms_quant_apply_self): the draft's eh_proj output, whose
     // partials no GEMV epilogue writes
     bool norm_self = false;
+    // a norm and the packed GEMV that reads it run as one launch where the GEMV takes the norm in its stage
+    // (RMI_FUSE_NORM=0: two launches, for measurement; the same bits either way)
+    bool fuse_norm = true;
     hipStream_t s = nullptr;
     bool own_stream = false;
     std::vector<void*> allocs;
@@ -525,9 +528,29 @@ int norm_input(Engine& e, const float* x, const float* part, const float* w, int
     return rmi_rms_quant_apply(x + xs, w, part + ps, e.q8a, c.n_embd, c.eps, nc, e.s);
 }
 
+// A norm and the GEMV behind it in one launch (rms_quant_apply quantized into the GEMV's own stage, the same bits):
+// a packed single-type matrix of 4096-wide rows at one or two columns, whose norm has its partials at hand
+bool norm_fusable(const Engine& e, const Mat& m, int nc) {
+    return e.fuse_norm && !e.norm_self && m.packed && m.parts.empty() && m.n_in == 4096 && nc <= 2;
+}
+
+// norm(x) -> GEMV into y (columns 0 .. nc - 1)
+int norm_gemv(Engine& e, const Mat& m, const float* x, const float* part, const float* w, float* y, int nc) {
+    if (norm_fusable(e, m, nc))
+        return rmi_native_q6_k_mmvq_packed_norm(m.w, x, w, part, e.cfg.eps, y, m.n_in, m.n_out, nc, e.s);
+    const uint8_t* xq = nullptr;
+    RMI_TRY(norm_input(e, x, part, w, 0, nc, &xq));
+    return gemv(e, m, xq, y, nc);
+}
+
 // post-attention norm, up||gate + SwiGLU, down with the residual
 int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
     const auto& c = e.cfg;
+    if (L.upgate.swiglu_ff && nc <= 2 && norm_fusable(e, L.upgate, nc)) {   // norm, up||gate, SwiGLU, Q8_1: one launch
+        RMI_TRY(rmi_native_q6_k_swiglu_packed_norm(L.upgate.w, x, L.post_norm, part, c.eps, e.q8f, c.n_embd, c.n_ff, nc,
+                                                   e.s));
+        return gemv_res(e, L.down, e.q8f, x, part, nc);
+    }
     const uint8_t* xq = nullptr;
     RMI_TRY(norm_input(e, x, part, L.post_norm, 0, nc, &xq));
     if (L.upgate.swiglu_ff && nc <= 2) {   // up||gate GEMV + SwiGLU + Q8_1 in one launch
@@ -548,9 +571,7 @@ int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
 // positions <= pos[0] + c only, as in the per-token path.
 int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc) {
     const auto& c = e.cfg;
-    const uint8_t* xq = nullptr;
-    RMI_TRY(norm_input(e, x, part, L.attn_norm, 0, nc, &xq));
-    RMI_TRY(gemv(e, L.in_proj, xq, e.proj, nc));
+    RMI_TRY(norm_gemv(e, L.in_proj, x, part, L.attn_norm, e.proj, nc));
     RMI_TRY(rmi_attn_prep_rope(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, e.qbuf, c.n_head, c.n_kv, c.head_dim,
                                c.n_rot, &e.rope, c.eps, nc, e.max_ctx, e.s));
     const size_t q8y_col = q81_bytes(e.attn_q);
@@ -568,9 +589,7 @@ int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int n
 
 int gdn_block(Engine& e, Layer& L, int nc) {
     const auto& c = e.cfg;
-    const uint8_t* xq = nullptr;
-    RMI_TRY(norm_input(e, e.x, e.part, L.attn_norm, 0, nc, &xq));
-    RMI_TRY(gemv(e, L.in_proj, xq, e.proj, nc));
+    RMI_TRY(norm_gemv(e, L.in_proj, e.x, e.part, L.attn_norm, e.proj, nc));
     const int qkvz = 2 * c.ssm_h_k * kS + 2 * c.ssm_h_v * kS;
     RMI_TRY(rmi_gdn_layer_tokens_x(L.state[0], L.state[1], L.hist[0], L.hist[1], e.ints + kSel, e.proj, e.qkvz_rows,
                                    e.proj + qkvz, e.qkvz_rows, L.conv_w, L.dt, L.ssm_a, L.ssm_norm, c.eps, e.y, e.gdn_v,
@@ -798,6 +817,10 @@ int validate_config(const rmi_model_config& c, int max_ctx) {
 int setup(Engine& e, const rmi_model_config& c, int max_ctx, void* stream) {
     e.cfg = c;
     e.max_ctx = (max_ctx + 63) / 64 * 64;
+    {
+        const char* v = std::getenv("RMI_FUSE_NORM");
+        e.fuse_norm = !(v && v[0] == '0');
+    }
     // attention chunk = 64 * nsub positions: 128 at 4K-class caches, 512 at 64K (one partial wave per SIMD pair)
     e.nsub = std::max(2, std::min(16, e.max_ctx / 8192));
     if (stream) {

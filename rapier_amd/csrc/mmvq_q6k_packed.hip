@@ -48,8 +48,6 @@ constexpr int kWideWaves = 8;                             // waves per workgroup
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ int swz(int u) { return u ^ ((u >> 3) & 7); }
-
 __device__ __forceinline__ int sc_byte2(uint32_t s0, uint32_t s1, int i) {
     const uint32_t w = i < 4 ? s0 : s1;
     return static_cast<int>(static_cast<int8_t>((w >> (8 * (i & 3))) & 0xffu));
@@ -118,28 +116,40 @@ struct WTile {
 };
 
 // ---- shared pieces -------------------------------------------------------------------------------------------------
-// whole-row activations, staged once per workgroup while the first weight steps are in flight: block J of column
-// col (chunk c = jb / 64, j = jb % 64) -> codes lq[2 (col * nbt + 64 c) + swz(2j), +1], record lrec[...]
-__device__ __forceinline__ void stage_one(const uint32_t (&wv)[9], int J, int nbt, uint4* lq, uint4* lrec) {
+// The activation stage: whole-row activations, staged once per workgroup while the first weight steps are in flight,
+// in three regions of NCOLS * nbt uint4 - codes 0..15 of a Q8_1 block | codes 16..31 | its record {-32 sum(codes
+// 0..15), -32 sum(codes 16..31), d8, 0}.  Block jb = 64 c + 4 hb + k of column col (chunk c, sub-step k, the
+// half-block hb that reads it) sits at slot ((4 c + k) NCOLS + col) 16 + hb of each region: the 16 half-blocks of a
+// wave's read take 256 contiguous bytes (every LDS bank once), and a lane's 24 reads of a step are immediate offsets
+// from one address per chunk, so the step spends no VALU on LDS addresses.
+template <int NCOLS>
+__device__ __forceinline__ int stage_slot(int col, int jb) {
+    const int c = jb >> 6, j = jb & 63;
+    return (((4 * c + (j & 3)) * NCOLS + col) << 4) + (j >> 2);
+}
+
+// block J (column J / nbt, block J % nbt of the column) into the stage st
+template <int NCOLS>
+__device__ __forceinline__ void stage_one(const uint32_t (&wv)[9], int J, int nbt, uint4* st) {
     const int col = J / nbt, jb = J - col * nbt;
-    const int c = jb / kNB, j = jb - c * kNB;
     int s0 = 0, s1 = 0;
 #pragma unroll
     for (int i = 1; i <= 4; ++i) s0 = sdot4(static_cast<int>(wv[i]), 0x01010101, s0);
 #pragma unroll
     for (int i = 5; i <= 8; ++i) s1 = sdot4(static_cast<int>(wv[i]), 0x01010101, s1);
-    uint4* q = lq + 2 * (col * nbt + c * kNB);
-    q[swz(2 * j)] = make_uint4(wv[1], wv[2], wv[3], wv[4]);
-    q[swz(2 * j + 1)] = make_uint4(wv[5], wv[6], wv[7], wv[8]);
-    lrec[col * nbt + c * kNB + swz(j)] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1),
-                                                    __float_as_uint(half_bits_to_float(wv[0])), 0u);
+    const int rs = NCOLS * nbt, i = stage_slot<NCOLS>(col, jb);
+    st[i] = make_uint4(wv[1], wv[2], wv[3], wv[4]);
+    st[rs + i] = make_uint4(wv[5], wv[6], wv[7], wv[8]);
+    st[2 * rs + i] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1),
+                                __float_as_uint(half_bits_to_float(wv[0])), 0u);
 }
 
 // Blocks are taken up to 4 per lane at a time, every load of a batch issued before the first is used (768 blocks of a
 // 12288-row at two columns: one batch per lane).  Measured against one block per iteration: 12288 x 4096 residual
 // 12.1 -> 12.0 us, 4096 x 4096 residual 7.1 -> 6.9 us (the weight loads issued before the staging hide most of it).
-__device__ __forceinline__ void stage_activations(const uint8_t* __restrict__ x, int nblocks, int nbt, uint4* lq,
-                                                  uint4* lrec, int t, int nthreads) {
+template <int NCOLS>
+__device__ __forceinline__ void stage_activations(const uint8_t* __restrict__ x, int nblocks, int nbt, uint4* st, int t,
+                                                  int nthreads) {
     constexpr int B = 4;
     for (int J0 = t; J0 < nblocks; J0 += B * nthreads) {
         uint32_t wv[B][9];
@@ -155,7 +165,150 @@ __device__ __forceinline__ void stage_activations(const uint8_t* __restrict__ x,
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const int J = J0 + b * nthreads;
-            if (J < nblocks) stage_one(wv[b], J, nbt, lq, lrec);
+            if (J < nblocks) stage_one<NCOLS>(wv[b], J, nbt, st);
+        }
+    }
+}
+
+// a lane's read addresses into the stage: the three regions at its half-block (add kNB * NCOLS per chunk)
+struct StageLane {
+    const uint4* a;
+    const uint4* b;
+    const uint4* r;
+};
+template <int NCOLS>
+__device__ __forceinline__ StageLane stage_lane(const uint4* st, int nbt, int lane) {
+    const uint4* a = st + (lane >> 2);
+    return {a, a + NCOLS * nbt, a + 2 * NCOLS * nbt};
+}
+
+// ---- a normed vector quantized straight into the stage ------------------------------------------------------------
+// The GEMV's input as rms_quant_apply makes it (qw:627-655): Q8_1 of (x * w) * inv per column, inv = rsqrt(sum of x's
+// 4-row partials / n + eps) by the norm kernels' tree (rmi_common.h), quantized into the activation stage instead of
+// HBM.  The codes, the fp16 block scale and the stage record are those of rms_quant_apply followed by stage_one, bit
+// for bit, and the norm's own launch (a graph node and a dependent memory level) is gone.  Two lanes per Q8_1 block,
+// 16 elements each: the block's amax and the second half's code sum cross by one lane exchange, and q8_round_fast
+// replaces the block's divides.  norm_issue loads ahead of the weight tiles, norm_stage computes after they are issued.
+struct NormIn {
+    const float* x;      // NCOLS columns of n_in (column c at + c n_in), 16-byte aligned
+    const float* w;      // the norm weights (n_in), 16-byte aligned
+    const float* part;   // x's 4-row partials (column c at + c n_in / 4)
+    float eps;
+};
+
+template <int NCOLS, int NCH, int NW>
+struct NormLanes {
+    static constexpr int kNbt = NCH * kNB;                              // Q8_1 blocks per column
+    static constexpr int kHalves = 2 * NCOLS * kNbt;                     // half-blocks of the stage
+    static constexpr int kHPL = (kHalves + 64 * NW - 1) / (64 * NW);     // half-blocks per lane
+    static constexpr int kTreeCols = NW >= 8 ? 1 : NCOLS;                // columns a lane's four-wave group reduces
+    NormLoads pv[kTreeCols];
+    float4 xv[kHPL][4], wv[kHPL][4];
+};
+
+// the norm tree runs on 256 lanes per column: waves 0..3 (column 0) and 4..7 (column 1) of an 8-wave workgroup, or
+// waves 0..3 for every column of a 4-wave one
+template <int NCOLS, int NCH, int NW>
+__device__ __forceinline__ void norm_issue(NormLanes<NCOLS, NCH, NW>& L, const NormIn& ni, int t) {
+    static_assert(NW == 4 || NW == 8, "the norm tree takes four waves per column");
+    using NL = NormLanes<NCOLS, NCH, NW>;
+    constexpr int n = NCH * kChunkElems, np = n / 4;
+    const int tt = t & 255;
+#pragma unroll
+    for (int k = 0; k < NL::kTreeCols; ++k) {
+        const int col = NW >= 8 ? min(t >> 8, NCOLS - 1) : k;
+        norm_load(L.pv[k], ni.part + static_cast<size_t>(col) * np, np, tt);
+    }
+#pragma unroll
+    for (int h = 0; h < NL::kHPL; ++h) {
+        const int g = min(t + 64 * NW * h, NL::kHalves - 1);
+        const int J = g >> 1, col = J / NL::kNbt, blk = J - col * NL::kNbt;
+        const int e0 = 32 * blk + 16 * (g & 1);
+        const float4* xp = reinterpret_cast<const float4*>(ni.x + static_cast<size_t>(col) * n + e0);
+        const float4* wp = reinterpret_cast<const float4*>(ni.w + e0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            L.xv[h][i] = xp[i];
+            L.wv[h][i] = wp[i];
+        }
+    }
+}
+
+// inv per column, then every half-block into the stage; red: NCOLS x 4 floats of LDS.  Ends before the caller's
+// stage barrier (it contains one barrier of its own, after the tree).
+template <int NCOLS, int NCH, int NW>
+__device__ __forceinline__ void norm_stage(const NormLanes<NCOLS, NCH, NW>& L, const NormIn& ni, uint4* st, int t,
+                                           float (*red)[4]) {
+    using NL = NormLanes<NCOLS, NCH, NW>;
+    constexpr int n = NCH * kChunkElems, np = n / 4;
+    const int tt = t & 255;
+#pragma unroll
+    for (int k = 0; k < NL::kTreeCols; ++k) {
+        const int col = NW >= 8 ? t >> 8 : k;
+        if (col < NCOLS && t < (NW >= 8 ? 64 * NW : 256)) {   // whole waves
+            const float sw = norm_wave_sum(L.pv[k], ni.part + static_cast<size_t>(col) * np, np, tt);
+            if ((t & 63) == 0) red[col][tt >> 6] = sw;
+        }
+    }
+    __syncthreads();
+    float inv[NCOLS];
+#pragma unroll
+    for (int c = 0; c < NCOLS; ++c) inv[c] = norm_inv(red[c], n, ni.eps);
+    const int rs = NCOLS * NL::kNbt;
+#pragma unroll
+    for (int h = 0; h < NL::kHPL; ++h) {
+        const int g0 = t + 64 * NW * h;
+        const bool live = g0 < NL::kHalves;   // pairs (2 J, 2 J + 1) are live together
+        const int g = min(g0, NL::kHalves - 1);
+        const int J = g >> 1, col = J / NL::kNbt, blk = J - col * NL::kNbt, half = g & 1;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[4 * i + 0] = (L.xv[h][i].x * L.wv[h][i].x) * inv[col];
+            v[4 * i + 1] = (L.xv[h][i].y * L.wv[h][i].y) * inv[col];
+            v[4 * i + 2] = (L.xv[h][i].z * L.wv[h][i].z) * inv[col];
+            v[4 * i + 3] = (L.xv[h][i].w * L.wv[h][i].w) * inv[col];
+        }
+        float am = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(v[e]));
+        am = fmaxf(am, xor_lane<1>(am));
+        const float d = am / 127.0f;
+        const float inv_d = 1.0f / d;
+        float r[16];
+        uint32_t slow = 0;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            bool sl;
+            r[e] = q8_round_fast(v[e], d, inv_d, sl);
+            slow |= static_cast<uint32_t>(sl) << e;
+        }
+        if (__builtin_amdgcn_ballot_w64(slow != 0)) {   // rare: the true divide for the flagged values
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                if (slow >> e & 1u) r[e] = v[e] / d;
+        }
+        uint32_t dw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int q = am == 0.0f ? 0 : static_cast<int>(roundf(r[4 * i + e]));
+                word |= (static_cast<uint32_t>(q) & 0xffu) << (8 * e);
+            }
+            dw[i] = word;
+        }
+        int sc = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc = sdot4(static_cast<int>(dw[i]), 0x01010101, sc);
+        const int sc_other = static_cast<int>(xor_lane<1>(static_cast<uint32_t>(sc)));
+        if (live) {
+            const int slot = stage_slot<NCOLS>(col, blk);
+            st[half * rs + slot] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+            if (half == 0)
+                st[2 * rs + slot] = make_uint4(static_cast<uint32_t>(-32 * sc), static_cast<uint32_t>(-32 * sc_other),
+                                               __float_as_uint(half_bits_to_float(float_to_half_sat(d))), 0u);
         }
     }
 }
@@ -181,18 +334,21 @@ __device__ __forceinline__ void pin_tile_after(WTile& w, float (&tot)[NCOLS]) {
                      "+v"(w.sc), "+v"(w.d), "+v"(tot[0]), "+v"(tot[1])::"memory");
 }
 
-// one wave tile step of lane l: its half-block (row l / 16, half-block l % 16) against every column's staged chunk
-// (the tile's block scale d, the lane's sum acc[col]) of one step; the step adds fma(d, acc[col], tot[col])
+// one wave tile step of lane l: its half-block (row l / 16, half-block l % 16) against every column's staged chunk c
+// (sl: the lane's stage addresses, c: the chunk; the tile's block scale d is returned, the lane's sum in acc[col]);
+// the step adds fma(d, acc[col], tot[col])
 template <int NCOLS>
-__device__ __forceinline__ float step_acc(const WTile& wt, int lane, const uint4* lqc, const uint4* lrc, int xcs,
-                                          float (&acc)[NCOLS]) {
-    const int hb = lane >> 2, b = hb >> 1, n = hb & 1;
+__device__ __forceinline__ float step_acc(const WTile& wt, int lane, const StageLane& sl, int c, float (&acc)[NCOLS]) {
     uint32_t Q[16], H[8];
 #pragma unroll
     for (int i = 0; i < 16; ++i) Q[i] = wt.ql[i >> 2][i & 3];
 #pragma unroll
     for (int i = 0; i < 8; ++i) H[i] = wt.qh[i >> 2][i & 3];
     const uint32_t S0 = wt.sc.x, S1 = wt.sc.y;
+    const int cb = c * kNB * NCOLS;
+    const uint4* pa = sl.a + cb;
+    const uint4* pb = sl.b + cb;
+    const uint4* pr = sl.r + cb;
 
 #pragma unroll
     for (int col = 0; col < NCOLS; ++col) acc[col] = 0.0f;
@@ -207,12 +363,12 @@ __device__ __forceinline__ float step_acc(const WTile& wt, int lane, const uint4
                 v[ww] = static_cast<int>(((Q[8 * kk + ww] >> (4 * kh)) & 0x0f0f0f0fu) |
                                          (((H[ww] >> (2 * k)) & 0x03030303u) << 4));
             const int sc0 = sc_byte2(S0, S1, 2 * k), sc1 = sc_byte2(S0, S1, 2 * k + 1);
-            const int j = 8 * b + 4 * n + k;
 #pragma unroll
             for (int col = 0; col < NCOLS; ++col) {
-                const uint4 qa = lqc[2 * col * xcs + swz(2 * j)];
-                const uint4 qb = lqc[2 * col * xcs + swz(2 * j + 1)];
-                const uint4 rec = lrc[col * xcs + swz(j)];
+                const int o = (k * NCOLS + col) * 16;
+                const uint4 qa = pa[o];
+                const uint4 qb = pb[o];
+                const uint4 rec = pr[o];
                 const int u[8] = {static_cast<int>(qa.x), static_cast<int>(qa.y), static_cast<int>(qa.z),
                                   static_cast<int>(qa.w), static_cast<int>(qb.x), static_cast<int>(qb.y),
                                   static_cast<int>(qb.z), static_cast<int>(qb.w)};
@@ -225,10 +381,10 @@ __device__ __forceinline__ float step_acc(const WTile& wt, int lane, const uint4
 }
 
 template <int NCOLS>
-__device__ __forceinline__ void accumulate_step(const WTile& wt, int lane, const uint4* lqc, const uint4* lrc, int xcs,
+__device__ __forceinline__ void accumulate_step(const WTile& wt, int lane, const StageLane& sl, int c,
                                                 float (&tot)[NCOLS]) {
     float acc[NCOLS];
-    const float d = step_acc<NCOLS>(wt, lane, lqc, lrc, xcs, acc);
+    const float d = step_acc<NCOLS>(wt, lane, sl, c, acc);
 #pragma unroll
     for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
 }
@@ -286,9 +442,8 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
     const int t = threadIdx.x, lane = t & 63;
     const int nch = n_in / kChunkElems;
     const int nbt = n_in / 32;                   // Q8_1 blocks per column
-    const int xcs = nch * kNB;                   // staged blocks between columns (= nbt)
-    uint4* lq = smem;                            // codes: 2 units per block
-    uint4* lrec = smem + 2 * NCOLS * nbt;        // records
+    uint4* st = smem;                            // the activation stage (stage_slot)
+    const StageLane sl = stage_lane<NCOLS>(st, nbt, lane);
     const int nq = (n_out + kQuad - 1) / kQuad;
     const int GW = static_cast<int>(gridDim.x) * NW;
     const int gw = static_cast<int>(blockIdx.x) * NW + (t >> 6);
@@ -312,7 +467,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
     for (int s = 0; s < D; ++s)
         if (s < nsteps) issue(s, buf[s]);
 
-    stage_activations(x, NCOLS * nbt, nbt, lq, lrec, t, 64 * NW);
+    stage_activations<NCOLS>(x, NCOLS * nbt, nbt, st, t, 64 * NW);
     __syncthreads();
 
     float tot[NCOLS];
@@ -327,7 +482,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
             const int qi = f / nch, c = f - qi * nch;
             const WTile cur = buf[s];
             if (f + D < nsteps) issue(f + D, buf[s]);
-            accumulate_step<NCOLS>(cur, lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, tot);
+            accumulate_step<NCOLS>(cur, lane, sl, c, tot);
 
             if (c == nch - 1)
                 quad_epilogue<NCOLS, RES>(tot, lane, gw + qi * GW, y, res, partials, n_out);
@@ -336,21 +491,27 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
 }
 
 // Split-chunk variant for grids with few quads per CU: the S = nch / CS waves of a quad each take CS consecutive
-// chunks, every tile issued at the start, and hand their per-lane (d, acc) pairs through LDS to the quad's first
-// wave, which continues the fma chain over the chunks in order.  The operations and their order are those of one wave
-// walking every chunk, so the result is bitwise that of q6k_packed_gemv.  NW waves per workgroup = QW quads x S.
-template <int NCOLS, bool RES, int CS, int NW>
+// chunks, every tile issued at the start, and park their per-lane (d, acc) pairs in LDS; the quad's last wave to
+// finish (an LDS counter per quad, so no workgroup barrier waits for the other quads of the workgroup) forms the fma
+// chain over the chunks in chunk order.  The operations and their order are those of one wave walking every chunk,
+// so the result is bitwise that of q6k_packed_gemv.  NW waves per workgroup = QW quads x S.
+// SB: activation blocks per lane loaded ahead of the tiles (the rest, if any, after them); sized to the shape by the
+// launcher, since every block held here is a register live across the tile loads (SB 4 at a 4096-wide row left the
+// kernel at 89 VGPRs: five 4-wave workgroups per CU, so a sixth waited a whole round for a slot).
+template <int NCOLS, bool RES, int CS, int NW, int SB = 4>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* __restrict__ wp,
                                                                  const uint8_t* __restrict__ x, float* y,
                                                                  const float* res, float* partials, int n_in,
                                                                  int n_out) {
     extern __shared__ uint4 smem[];
+    __shared__ int qdone[NW];   // per quad: waves that have parked their sums
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
-    const int nbt = n_in / 32, xcs = nch * kNB;
-    uint4* lq = smem;
-    uint4* lrec = smem + 2 * NCOLS * nbt;
-    float* lx = reinterpret_cast<float*>(lrec + NCOLS * nbt);   // [wave][chunk][d, acc[0..NCOLS)][lane]
+    const int nbt = n_in / 32;
+    uint4* st = smem;   // the activation stage (stage_slot)
+    const StageLane sl = stage_lane<NCOLS>(st, nbt, lane);
+    float* lx = reinterpret_cast<float*>(st + 3 * NCOLS * nbt);   // [wave][chunk][d, acc[0..NCOLS)][lane]
+    if (t < NW) qdone[t] = 0;   // published by the staging barrier
     const int nq = (n_out + kQuad - 1) / kQuad;
     const int qg = w / S, sp = w - qg * S;
     const int q = static_cast<int>(blockIdx.x) * QW + qg;
@@ -358,7 +519,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
 
     // the activation loads go first: a wave's loads return in issue order, so a stage issued after the weight tiles
     // would wait for all of them before the first step could start
-    constexpr int SB = 4;
+
     const int nblocks = NCOLS * nbt;
     uint32_t sv[SB][9];
 #pragma unroll
@@ -395,80 +556,84 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
 #pragma unroll
     for (int b = 0; b < SB; ++b) {
         const int J = t + b * 64 * NW;
-        if (J < nblocks) stage_one(sv[b], J, nbt, lq, lrec);
+        if (J < nblocks) stage_one<NCOLS>(sv[b], J, nbt, st);
     }
     for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
         const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
         uint32_t wv[9];
 #pragma unroll
         for (int i = 0; i < 9; ++i) wv[i] = p[i];
-        stage_one(wv, J, nbt, lq, lrec);
+        stage_one<NCOLS>(wv, J, nbt, st);
     }
     __syncthreads();
 
+    if (!live) return;   // a quad's waves are all live or all past the last quad
     float acc[CS][NCOLS], dd[CS];
-    if (live) {
 #pragma unroll
-        for (int c = 0; c < CS; ++c) {
-            const int ch = sp * CS + c;
-            pin_tile(buf[c]);
-            dd[c] = step_acc<NCOLS>(buf[c], lane, lq + 2 * ch * kNB, lrec + ch * kNB, xcs, acc[c]);
-        }
-        if (sp != 0) {
-#pragma unroll
-            for (int c = 0; c < CS; ++c) {
-                float* o = lx + (w * CS + c) * (NCOLS + 1) * 64 + lane;
-                o[0] = dd[c];
-#pragma unroll
-                for (int col = 0; col < NCOLS; ++col) o[(col + 1) * 64] = acc[c][col];
-            }
-        }
+    for (int c = 0; c < CS; ++c) {
+        const int ch = sp * CS + c;
+        pin_tile(buf[c]);
+        dd[c] = step_acc<NCOLS>(buf[c], lane, sl, ch, acc[c]);
     }
-    __syncthreads();
-    if (!live || sp != 0) return;
-    {
-        float tot[NCOLS];
+    float tot[NCOLS];
 #pragma unroll
-        for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
+    for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
+    if (S == 1) {
 #pragma unroll
         for (int c = 0; c < CS; ++c)
 #pragma unroll
             for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(dd[c], acc[c][col], tot[col]);
-        for (int s2 = 1; s2 < S; ++s2) {
+    } else {
+#pragma unroll
+        for (int c = 0; c < CS; ++c) {
+            float* o = lx + (w * CS + c) * (NCOLS + 1) * 64 + lane;
+            o[0] = dd[c];
+#pragma unroll
+            for (int col = 0; col < NCOLS; ++col) o[(col + 1) * 64] = acc[c][col];
+        }
+        // the release orders this wave's parked sums before its count; the last wave's acquire orders its reads after
+        int prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(&qdone[qg], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (__builtin_amdgcn_readfirstlane(prev) != S - 1) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");   // every lane's reads below stay after the count
+        for (int s2 = 0; s2 < S; ++s2) {   // chunk order: waves qg S .. qg S + S - 1, their chunks in order
 #pragma unroll
             for (int c = 0; c < CS; ++c) {
-                const float* o = lx + ((w + s2) * CS + c) * (NCOLS + 1) * 64 + lane;
+                const float* o = lx + ((qg * S + s2) * CS + c) * (NCOLS + 1) * 64 + lane;
                 const float d = o[0];
 #pragma unroll
                 for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, o[(col + 1) * 64], tot[col]);
             }
         }
-        quad_epilogue<NCOLS, RES>(tot, lane, q, y, res, partials, n_out, rv);
     }
+    quad_epilogue<NCOLS, RES>(tot, lane, q, y, res, partials, n_out, rv);
 }
 
 // Stream variant: one wave per quad and QPW quads per wave (quads q, q + G, q + 2G, ... with G the grid's wave count),
 // all in straight-line code with PD tiles in flight ahead of the step that uses them.  Every wave is resident from the
 // start (a wave per quad would leave a tail of waves waiting for slots), and the per-quad arithmetic is that of
-// q6k_packed_gemv: the same bits.
-template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD>
+// q6k_packed_gemv: the same bits.  NORM: the input is a normed vector quantized in the stage (norm_stage; x unused).
+template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD, bool NORM = false>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t* __restrict__ wp,
                                                                   const uint8_t* __restrict__ x, float* y,
                                                                   const float* res, float* partials, int n_in,
-                                                                  int n_out) {
+                                                                  int n_out, NormIn ni) {
     extern __shared__ uint4 smem[];
+    __shared__ float nred[NORM ? NCOLS : 1][4];
     const int t = threadIdx.x, lane = t & 63;
-    const int nbt = n_in / 32, xcs = NCH * kNB;
-    uint4* lq = smem;
-    uint4* lrec = smem + 2 * NCOLS * nbt;
+    const int nbt = n_in / 32;
+    uint4* st = smem;   // the activation stage (stage_slot)
+    const StageLane sl = stage_lane<NCOLS>(st, nbt, lane);
     const int nq = (n_out + kQuad - 1) / kQuad;
     const int G = static_cast<int>(gridDim.x) * NW;
     const int q0 = static_cast<int>(blockIdx.x) * NW + (t >> 6);
 
     // activation loads first (a wave's loads return in issue order), clamped so that none sits in a branch
-    constexpr int SB = 4;
+    // activation blocks per lane loaded ahead of the tiles: the whole row where four per lane hold it, else four
+    constexpr int SB = NORM ? 0 : std::min(4, (NCOLS * NCH * kNB + 64 * NW - 1) / (64 * NW));
     const int nblocks = NCOLS * nbt;
-    uint32_t sv[SB][9];
+    uint32_t sv[SB > 0 ? SB : 1][9];
 #pragma unroll
     for (int b = 0; b < SB; ++b) {
         const int J = min(t + b * 64 * NW, nblocks - 1);
@@ -476,6 +641,8 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
 #pragma unroll
         for (int i = 0; i < 9; ++i) sv[b][i] = p[i];
     }
+    NormLanes<NCOLS, NCH, NW> nl;
+    if constexpr (NORM) norm_issue<NCOLS, NCH, NW>(nl, ni, t);
     float rv[QPW][NCOLS];
     if constexpr (RES) {
 #pragma unroll
@@ -504,17 +671,21 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
         issue(i);
         __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (NORM) {
+        norm_stage<NCOLS, NCH, NW>(nl, ni, st, t, nred);
+    } else {
 #pragma unroll
-    for (int b = 0; b < SB; ++b) {
-        const int J = t + b * 64 * NW;
-        if (J < nblocks) stage_one(sv[b], J, nbt, lq, lrec);
-    }
-    for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
-        uint32_t wv[9];
+        for (int b = 0; b < SB; ++b) {
+            const int J = t + b * 64 * NW;
+            if (J < nblocks) stage_one<NCOLS>(sv[b], J, nbt, st);
+        }
+        for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
+            const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
+            uint32_t wv[9];
 #pragma unroll
-        for (int i = 0; i < 9; ++i) wv[i] = p[i];
-        stage_one(wv, J, nbt, lq, lrec);
+            for (int i = 0; i < 9; ++i) wv[i] = p[i];
+            stage_one<NCOLS>(wv, J, nbt, st);
+        }
     }
     __syncthreads();
 
@@ -526,7 +697,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
         const int j = i / NCH, c = i - (i / NCH) * NCH;
         pin_tile_after<NCOLS>(buf[i], tot);
         float acc[NCOLS];
-        const float d = step_acc<NCOLS>(buf[i], lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, acc);
+        const float d = step_acc<NCOLS>(buf[i], lane, sl, c, acc);
 #pragma unroll
         for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
         if (i + PD < T) {
@@ -607,16 +778,17 @@ __global__ __launch_bounds__(64 * NW) void q6k_gguf_stream(const uint8_t* __rest
                                                            int n_out) {
     extern __shared__ uint4 smem[];
     const int t = threadIdx.x, lane = t & 63;
-    const int nbt = n_in / 32, xcs = NCH * kNB;
-    uint4* lq = smem;
-    uint4* lrec = smem + 2 * NCOLS * nbt;
-    uint32_t* lw = reinterpret_cast<uint32_t*>(lrec + NCOLS * nbt) + (t >> 6) * kGgufWaveDw;
+    const int nbt = n_in / 32;
+    uint4* st = smem;   // the activation stage (stage_slot)
+    const StageLane sl = stage_lane<NCOLS>(st, nbt, lane);
+    uint32_t* lw = reinterpret_cast<uint32_t*>(st + 3 * NCOLS * nbt) + (t >> 6) * kGgufWaveDw;
     const int nq = (n_out + kQuad - 1) / kQuad;
     const int G = static_cast<int>(gridDim.x) * NW;
     const int q0 = static_cast<int>(blockIdx.x) * NW + (t >> 6);
     const size_t rowbytes = static_cast<size_t>(n_in / 256) * kQ6KBytes;
 
-    constexpr int SB = 4;
+    // activation blocks per lane loaded ahead of the tiles: the whole row where four per lane hold it, else four
+    constexpr int SB = std::min(4, (NCOLS * NCH * kNB + 64 * NW - 1) / (64 * NW));
     const int nblocks = NCOLS * nbt;
     uint32_t sv[SB][9];
 #pragma unroll
@@ -656,14 +828,14 @@ __global__ __launch_bounds__(64 * NW) void q6k_gguf_stream(const uint8_t* __rest
 #pragma unroll
     for (int b = 0; b < SB; ++b) {
         const int J = t + b * 64 * NW;
-        if (J < nblocks) stage_one(sv[b], J, nbt, lq, lrec);
+        if (J < nblocks) stage_one<NCOLS>(sv[b], J, nbt, st);
     }
     for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
         const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
         uint32_t wv[9];
 #pragma unroll
         for (int i = 0; i < 9; ++i) wv[i] = p[i];
-        stage_one(wv, J, nbt, lq, lrec);
+        stage_one<NCOLS>(wv, J, nbt, st);
     }
     __syncthreads();
 
@@ -677,7 +849,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_gguf_stream(const uint8_t* __rest
         WTile wt;
         gguf_unpack(buf[i], lw, lane, wt);
         float acc[NCOLS];
-        const float d = step_acc<NCOLS>(wt, lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, acc);
+        const float d = step_acc<NCOLS>(wt, lane, sl, c, acc);
 #pragma unroll
         for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
         if (i + PD < T) {
@@ -701,25 +873,30 @@ __global__ __launch_bounds__(64 * NW) void q6k_gguf_stream(const uint8_t* __rest
 // weight tiles in the CU's memory pipeline (per-wave clock stamps: stage at 5.3 us against 1.6 us, its waves last to
 // finish): 24576 x 4096 at two columns 17.2 -> 16.0 us.  Deeper prefetch (3 or 4 tiles ahead) and 16 waves of two
 // quads were slower (17.2, 18.4, 29.6 us).
-template <int NCOLS, int NW = 4, int QPW = 4, int PD = 2>
+// NORM: the input is a normed vector quantized in the stage (norm_stage; x unused).
+template <int NCOLS, int NW = 4, int QPW = 4, int PD = 2, bool NORM = false>
 __global__ __launch_bounds__(64 * NW) void q6k_packed_swiglu(const uint8_t* __restrict__ wp,
                                                              const uint8_t* __restrict__ x, uint8_t* __restrict__ out,
-                                                             int n_in, int ff) {
+                                                             int n_in, int ff, NormIn ni) {
     constexpr int NCH = 2, T = QPW * NCH;
     constexpr int GPW = NW * QPW / 16;   // 16-quad groups per workgroup
     static_assert(GPW * 16 == NW * QPW && GPW >= 1, "whole groups per workgroup");
     extern __shared__ uint4 smem[];
+    __shared__ float nred[NORM ? NCOLS : 1][4];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int nbt = n_in / 32, xcs = NCH * kNB;
-    uint4* lq = smem;
-    uint4* lrec = smem + 2 * NCOLS * nbt;
-    float* lrow = reinterpret_cast<float*>(lrec + NCOLS * nbt);   // [group][col][64 rows of the group]
+    const int nbt = n_in / 32;
+    uint4* st = smem;   // the activation stage (stage_slot)
+    const StageLane sl = stage_lane<NCOLS>(st, nbt, lane);
+    float* lrow = reinterpret_cast<float*>(st + 3 * NCOLS * nbt);   // [group][col][64 rows of the group]
     const int q0 = static_cast<int>(blockIdx.x) * 16 * GPW + QPW * w;
 
     const int nblocks = NCOLS * nbt;   // <= 2 x 128: one block per lane at most
     static_assert(64 * NW >= 2 * 128, "one staged block per lane");
     uint32_t sv[9];
-    {
+    NormLanes<NCOLS, NCH, NW> nl;
+    if constexpr (NORM) {
+        norm_issue<NCOLS, NCH, NW>(nl, ni, t);
+    } else {
         const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(min(t, nblocks - 1)) * kQ8_1Bytes);
 #pragma unroll
         for (int i = 0; i < 9; ++i) sv[i] = p[i];
@@ -745,7 +922,8 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_swiglu(const uint8_t* __re
     }
     // unconditional (lanes past the last block rewrite its slot with the same bytes): under a branch the compiler sinks
     // the stage's loads into it, behind the first tiles, and the stage then waits for those
-    stage_one(sv, min(t, nblocks - 1), nbt, lq, lrec);
+    if constexpr (NORM) norm_stage<NCOLS, NCH, NW>(nl, ni, st, t, nred);
+    else stage_one<NCOLS>(sv, min(t, nblocks - 1), nbt, st);
     __syncthreads();
 
     float tot[NCOLS];
@@ -756,7 +934,7 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_swiglu(const uint8_t* __re
         const int j = i / NCH, c = i - (i / NCH) * NCH;
         pin_tile_after<NCOLS>(buf[i], tot);
         float acc[NCOLS];
-        const float d = step_acc<NCOLS>(buf[i], lane, lq + 2 * c * kNB, lrec + c * kNB, xcs, acc);
+        const float d = step_acc<NCOLS>(buf[i], lane, sl, c, acc);
 #pragma unroll
         for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, acc[col], tot[col]);
         if (i + PD < T) {
@@ -1214,8 +1392,13 @@ void launch_split(const uint8_t* wp, const uint8_t* x, float* y, const float* re
     const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
     const int nq = (n_out + kQuad - 1) / kQuad;
     const dim3 grid((nq + QW - 1) / QW), block(64 * NW);
-    hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW>), grid, block, split_lds(n_in, NCOLS, CS, NW), s, wp,
-                       x, y, res, partials, n_in, n_out);
+    const size_t lds = split_lds(n_in, NCOLS, CS, NW);
+    if (NCOLS * (n_in / 32) <= 64 * NW)   // one block per lane
+        hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW, 1>), grid, block, lds, s, wp, x, y, res, partials,
+                           n_in, n_out);
+    else
+        hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW>), grid, block, lds, s, wp, x, y, res, partials,
+                           n_in, n_out);
 }
 
 template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD>
@@ -1224,7 +1407,7 @@ void launch_stream(const uint8_t* wp, const uint8_t* x, float* y, const float* r
     const int nq = (n_out + kQuad - 1) / kQuad;
     const dim3 grid((nq + NW * QPW - 1) / (NW * QPW)), block(64 * NW);
     hipLaunchKernelGGL((q6k_packed_gemv_stream<NCOLS, RES, NCH, QPW, NW, PD>), grid, block,
-                       static_cast<size_t>(NCOLS) * (n_in / 32) * 48, s, wp, x, y, res, partials, n_in, n_out);
+                       static_cast<size_t>(NCOLS) * (n_in / 32) * 48, s, wp, x, y, res, partials, n_in, n_out, NormIn{});
 }
 
 template <int NCOLS, bool RES>
@@ -1503,11 +1686,12 @@ extern "C" int rmi_q6_k_pack_swiglu(const void* w, void* w_packed, int n_in, int
 
 namespace rmi {
 namespace {
+// norm: the normed-input form (x_q8_1 unused)
 int swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_in, int n_ff, int ncols,
-                  void* stream) {
+                  const NormIn* norm, void* stream) {
     if (n_in != 2 * kChunkElems || n_ff <= 0 || n_ff % 32 != 0 || ncols < 1 || ncols > 2)
         return fail(RMI_ERR_SHAPE, "q6_k_swiglu_packed: n_in must be 4096, n_ff a positive multiple of 32, ncols 1 or 2");
-    if (!aligned16(w_packed) || !aligned4(x_q8_1) || !aligned4(y_q8_1))
+    if (!aligned16(w_packed) || !(norm || aligned4(x_q8_1)) || !aligned4(y_q8_1))
         return fail(RMI_ERR_POINTER, "q6_k_swiglu_packed: null or misaligned pointer");
     if (!stream) return fail(RMI_ERR_STREAM, "native MMVQ requires an explicit non-null CUDA stream");
     const auto* wp = static_cast<const uint8_t*>(w_packed);
@@ -1518,17 +1702,30 @@ int swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_
     // per 4-wave workgroup
     auto go = [&](auto kern, int gpw, int nw) {
         const size_t lds = static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(gpw) * ncols * 64 * 4;
-        hipLaunchKernelGGL(kern, dim3(n_ff / 32 / gpw), dim3(64 * nw), lds, s, wp, x, y, n_in, n_ff);
+        hipLaunchKernelGGL(kern, dim3(n_ff / 32 / gpw), dim3(64 * nw), lds, s, wp, x, y, n_in, n_ff,
+                           norm ? *norm : NormIn{});
     };
     const bool two = n_ff % 64 == 0;
-    if (ncols == 1) {
+    if (norm) {
+        if (ncols == 1) two ? go(q6k_packed_swiglu<1, 8, 4, 2, true>, 2, 8) : go(q6k_packed_swiglu<1, 4, 4, 2, true>, 1, 4);
+        else two ? go(q6k_packed_swiglu<2, 8, 4, 2, true>, 2, 8) : go(q6k_packed_swiglu<2, 4, 4, 2, true>, 1, 4);
+    } else if (ncols == 1) {
         if (two) go(q6k_packed_swiglu<1, 8, 4>, 2, 8);
         else go(q6k_packed_swiglu<1>, 1, 4);
     } else {
         if (two) go(q6k_packed_swiglu<2, 8, 4>, 2, 8);
         else go(q6k_packed_swiglu<2>, 1, 4);
     }
-    return launch_status("q6_k_swiglu_packed");
+    return launch_status(norm ? "q6_k_swiglu_packed_norm" : "q6_k_swiglu_packed");
+}
+
+// the normed-input packed GEMV: rows of 4096, one or two columns, one 8-wave workgroup per 8 QPW quads
+template <int NCOLS, int QPW>
+void launch_norm_gemv(const uint8_t* wp, float* y, int n_out, const NormIn& ni, hipStream_t s) {
+    const int nq = (n_out + kQuad - 1) / kQuad;
+    hipLaunchKernelGGL((q6k_packed_gemv_stream<NCOLS, false, 2, QPW, 8, 2, true>), dim3((nq + 8 * QPW - 1) / (8 * QPW)),
+                       dim3(512), static_cast<size_t>(NCOLS) * (2 * kChunkElems / 32) * 48, s, wp, nullptr, y, nullptr,
+                       nullptr, 2 * kChunkElems, n_out, ni);
 }
 
 }  // namespace
@@ -1536,7 +1733,44 @@ int swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_
 
 extern "C" int rmi_native_q6_k_swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_in, int n_ff,
                                              int ncols, void* stream) {
-    return swiglu_packed(w_packed, x_q8_1, y_q8_1, n_in, n_ff, ncols, stream);
+    return swiglu_packed(w_packed, x_q8_1, y_q8_1, n_in, n_ff, ncols, nullptr, stream);
+}
+
+namespace {
+int check_norm_in(const float* x, const float* w_norm, const float* partials) {
+    if (!aligned16(x) || !aligned16(w_norm) || !aligned4(partials))
+        return fail(RMI_ERR_POINTER, "normed-input GEMV: x and the norm weights 16-byte aligned, partials 4-byte aligned");
+    return RMI_OK;
+}
+}  // namespace
+
+extern "C" int rmi_native_q6_k_swiglu_packed_norm(const void* w_packed, const float* x, const float* w_norm,
+                                                  const float* partials, float eps, void* y_q8_1, int n_in, int n_ff,
+                                                  int ncols, void* stream) {
+    if (int rc = check_norm_in(x, w_norm, partials)) return rc;
+    const NormIn ni{x, w_norm, partials, eps};
+    return swiglu_packed(w_packed, nullptr, y_q8_1, n_in, n_ff, ncols, &ni, stream);
+}
+
+extern "C" int rmi_native_q6_k_mmvq_packed_norm(const void* w_packed, const float* x, const float* w_norm,
+                                                const float* partials, float eps, float* y, int n_in, int n_out,
+                                                int ncols, void* stream) {
+    if (n_in != 2 * kChunkElems || ncols < 1 || ncols > 2 || n_out <= 0 || n_out > 4 * 8 * 4 * 256)
+        return fail(RMI_ERR_SHAPE, "q6_k_mmvq_packed_norm: n_in must be 4096, ncols 1 or 2, 0 < n_out <= 32768");
+    if (!aligned16(w_packed) || !aligned4(y)) return fail(RMI_ERR_POINTER, "q6_k_mmvq_packed_norm: null or misaligned pointer");
+    if (int rc = check_norm_in(x, w_norm, partials)) return rc;
+    if (!stream) return fail(RMI_ERR_STREAM, "native MMVQ requires an explicit non-null CUDA stream");
+    const NormIn ni{x, w_norm, partials, eps};
+    const auto* wp = static_cast<const uint8_t*>(w_packed);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    // quads per wave: every quad's wave resident at once on the CUs' 8-wave workgroups (one per CU up to 2048 quads)
+    const int nq = (n_out + kQuad - 1) / kQuad, qpw = (nq + 8 * cu_count() - 1) / (8 * cu_count());
+    auto go = [&](auto one, auto two) { ncols == 1 ? one() : two(); };
+    if (qpw <= 1) go([&] { launch_norm_gemv<1, 1>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 1>(wp, y, n_out, ni, s); });
+    else if (qpw == 2) go([&] { launch_norm_gemv<1, 2>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 2>(wp, y, n_out, ni, s); });
+    else if (qpw == 3) go([&] { launch_norm_gemv<1, 3>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 3>(wp, y, n_out, ni, s); });
+    else go([&] { launch_norm_gemv<1, 4>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 4>(wp, y, n_out, ni, s); });
+    return launch_status("q6_k_mmvq_packed_norm");
 }
 
 extern "C" int rmi_native_q6_k_mmvq_packed(const void* w_packed, const void* x_q8_1, float* y, int n_in, int n_out,
