@@ -48,6 +48,7 @@ SIGNATURES = {
     "rmi_q6_k_block_dots": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "rmi_native_q6_k_mmvq_packed_norm": (_i, [_vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _vp]),
     "rmi_native_q6_k_swiglu_packed_norm": (_i, [_vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _vp]),
+    "rmi_q6_k_packed_norm_preferred": (_i, [_i, _i, _i]),
     "rmi_gen_q6_k": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
     "rmi_gen_q8_0": (_i, [_vp, _sz, ctypes.c_uint64, _f, _vp]),
     "rmi_gen_normal": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),

@@ -534,9 +534,9 @@ bool norm_fusable(const Engine& e, const Mat& m, int nc) {
     return e.fuse_norm && !e.norm_self && m.packed && m.parts.empty() && m.n_in == 4096 && nc <= 2;
 }
 
-// norm(x) -> GEMV into y (columns 0 .. nc - 1)
+// norm(x) -> GEMV into y (columns 0 .. nc - 1); one launch where the shape favours it
 int norm_gemv(Engine& e, const Mat& m, const float* x, const float* part, const float* w, float* y, int nc) {
-    if (norm_fusable(e, m, nc))
+    if (norm_fusable(e, m, nc) && rmi_q6_k_packed_norm_preferred(m.n_in, m.n_out, nc))
         return rmi_native_q6_k_mmvq_packed_norm(m.w, x, w, part, e.cfg.eps, y, m.n_in, m.n_out, nc, e.s);
     const uint8_t* xq = nullptr;
     RMI_TRY(norm_input(e, x, part, w, 0, nc, &xq));

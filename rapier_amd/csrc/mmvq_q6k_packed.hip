@@ -202,22 +202,27 @@ struct NormLanes {
     static constexpr int kHalves = 2 * NCOLS * kNbt;                     // half-blocks of the stage
     static constexpr int kHPL = (kHalves + 64 * NW - 1) / (64 * NW);     // half-blocks per lane
     static constexpr int kTreeCols = NW >= 8 ? 1 : NCOLS;                // columns a lane's four-wave group reduces
-    NormLoads pv[kTreeCols];
+    static constexpr int kNp = NCH * kChunkElems / 4;                    // partial slots per column
+    static constexpr int kPL = kNp / 256;                                // partial slots per tree lane
+    float pv[kTreeCols][kPL];
     float4 xv[kHPL][4], wv[kHPL][4];
 };
 
-// the norm tree runs on 256 lanes per column: waves 0..3 (column 0) and 4..7 (column 1) of an 8-wave workgroup, or
-// waves 0..3 for every column of a 4-wave one
+// the norm tree runs on 256 lanes per column: waves 0..3 (column 0) and 4..7 (column 1) of a workgroup of 8 or more
+// waves, or waves 0..3 for every column of a 4-wave one
 template <int NCOLS, int NCH, int NW>
 __device__ __forceinline__ void norm_issue(NormLanes<NCOLS, NCH, NW>& L, const NormIn& ni, int t) {
-    static_assert(NW == 4 || NW == 8, "the norm tree takes four waves per column");
+    static_assert(NW == 4 || NW % 8 == 0, "the norm tree takes four waves per column");
     using NL = NormLanes<NCOLS, NCH, NW>;
-    constexpr int n = NCH * kChunkElems, np = n / 4;
+    static_assert(NL::kNp % 256 == 0, "whole tree lanes");
+    constexpr int n = NCH * kChunkElems;
     const int tt = t & 255;
 #pragma unroll
     for (int k = 0; k < NL::kTreeCols; ++k) {
         const int col = NW >= 8 ? min(t >> 8, NCOLS - 1) : k;
-        norm_load(L.pv[k], ni.part + static_cast<size_t>(col) * np, np, tt);
+        const float* p = ni.part + static_cast<size_t>(col) * NL::kNp;
+#pragma unroll
+        for (int i = 0; i < NL::kPL; ++i) L.pv[k][i] = p[tt + 256 * i];
     }
 #pragma unroll
     for (int h = 0; h < NL::kHPL; ++h) {
@@ -235,20 +240,39 @@ __device__ __forceinline__ void norm_issue(NormLanes<NCOLS, NCH, NW>& L, const N
 }
 
 // inv per column, then every half-block into the stage; red: NCOLS x 4 floats of LDS.  Ends before the caller's
-// stage barrier (it contains one barrier of its own, after the tree).
+// stage barrier (it contains one barrier of its own, after the tree).  The products x * w and their block maximum
+// are formed while the tree's partials are summed: the block's amax, max |RN((x * w) * inv)|, is RN(max |x * w| * inv)
+// (rounding is monotonic), so only the scaling waits for inv.
 template <int NCOLS, int NCH, int NW>
 __device__ __forceinline__ void norm_stage(const NormLanes<NCOLS, NCH, NW>& L, const NormIn& ni, uint4* st, int t,
                                            float (*red)[4]) {
     using NL = NormLanes<NCOLS, NCH, NW>;
-    constexpr int n = NCH * kChunkElems, np = n / 4;
-    const int tt = t & 255;
+    constexpr int n = NCH * kChunkElems;
 #pragma unroll
     for (int k = 0; k < NL::kTreeCols; ++k) {
         const int col = NW >= 8 ? t >> 8 : k;
-        if (col < NCOLS && t < (NW >= 8 ? 64 * NW : 256)) {   // whole waves
-            const float sw = norm_wave_sum(L.pv[k], ni.part + static_cast<size_t>(col) * np, np, tt);
-            if ((t & 63) == 0) red[col][tt >> 6] = sw;
+        if (col < NCOLS && (NW >= 8 || t < 256)) {   // whole waves
+            float sw = 0.0f;   // the lane's slots in order, then the wave's butterfly (norm_wave_sum)
+#pragma unroll
+            for (int i = 0; i < NL::kPL; ++i) sw += L.pv[k][i];
+            sw = group_sum<64>(sw);
+            if ((t & 63) == 0) red[col][(t >> 6) & 3] = sw;
         }
+    }
+    float xw[NL::kHPL][16], mx[NL::kHPL];
+#pragma unroll
+    for (int h = 0; h < NL::kHPL; ++h) {
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xw[h][4 * i + 0] = L.xv[h][i].x * L.wv[h][i].x;
+            xw[h][4 * i + 1] = L.xv[h][i].y * L.wv[h][i].y;
+            xw[h][4 * i + 2] = L.xv[h][i].z * L.wv[h][i].z;
+            xw[h][4 * i + 3] = L.xv[h][i].w * L.wv[h][i].w;
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) m = fmaxf(m, fabsf(xw[h][e]));
+        mx[h] = fmaxf(m, xor_lane<1>(m));
     }
     __syncthreads();
     float inv[NCOLS];
@@ -261,32 +285,23 @@ __device__ __forceinline__ void norm_stage(const NormLanes<NCOLS, NCH, NW>& L, c
         const bool live = g0 < NL::kHalves;   // pairs (2 J, 2 J + 1) are live together
         const int g = min(g0, NL::kHalves - 1);
         const int J = g >> 1, col = J / NL::kNbt, blk = J - col * NL::kNbt, half = g & 1;
-        float v[16];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[4 * i + 0] = (L.xv[h][i].x * L.wv[h][i].x) * inv[col];
-            v[4 * i + 1] = (L.xv[h][i].y * L.wv[h][i].y) * inv[col];
-            v[4 * i + 2] = (L.xv[h][i].z * L.wv[h][i].z) * inv[col];
-            v[4 * i + 3] = (L.xv[h][i].w * L.wv[h][i].w) * inv[col];
-        }
-        float am = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(v[e]));
-        am = fmaxf(am, xor_lane<1>(am));
+        const float iv = inv[col];
+        const float am = mx[h] * iv;
         const float d = am / 127.0f;
         const float inv_d = 1.0f / d;
-        float r[16];
+        float v[16], r[16];
         uint32_t slow = 0;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
+            v[e] = xw[h][e] * iv;
             bool sl;
             r[e] = q8_round_fast(v[e], d, inv_d, sl);
             slow |= static_cast<uint32_t>(sl) << e;
         }
-        if (__builtin_amdgcn_ballot_w64(slow != 0)) {   // rare: the true divide for the flagged values
+        if (__builtin_amdgcn_ballot_w64(slow != 0)) {   // rare: roundf of the true quotient for the flagged values
 #pragma unroll
             for (int e = 0; e < 16; ++e)
-                if (slow >> e & 1u) r[e] = v[e] / d;
+                if (slow >> e & 1u) r[e] = roundf(v[e] / d);
         }
         uint32_t dw[4];
 #pragma unroll
@@ -294,7 +309,7 @@ __device__ __forceinline__ void norm_stage(const NormLanes<NCOLS, NCH, NW>& L, c
             uint32_t word = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int q = am == 0.0f ? 0 : static_cast<int>(roundf(r[4 * i + e]));
+                const int q = am == 0.0f ? 0 : static_cast<int>(r[4 * i + e]);
                 word |= (static_cast<uint32_t>(q) & 0xffu) << (8 * e);
             }
             dw[i] = word;
@@ -1750,6 +1765,16 @@ extern "C" int rmi_native_q6_k_swiglu_packed_norm(const void* w_packed, const fl
     if (int rc = check_norm_in(x, w_norm, partials)) return rc;
     const NormIn ni{x, w_norm, partials, eps};
     return swiglu_packed(w_packed, nullptr, y_q8_1, n_in, n_ff, ncols, &ni, stream);
+}
+
+// Whether the normed-input GEMV is the faster way to run norm + GEMV at this shape.  It runs one 8-wave workgroup per
+// 16 quads (a CU each), so rows that leave many CUs idle lose to the two launches: measured in pairs led by a residual
+// GEMV (graph replay, two columns), 12352 rows 17.6 against 18.2 us, 10240 rows 17.6 against 17.2 us (160 of 256 CUs).
+extern "C" int rmi_q6_k_packed_norm_preferred(int n_in, int n_out, int ncols) {
+    if (n_in != 2 * kChunkElems || ncols < 1 || ncols > 2 || n_out <= 0 || n_out > 4 * 8 * 4 * 256) return 0;
+    const int nq = (n_out + kQuad - 1) / kQuad, qpw = (nq + 8 * cu_count() - 1) / (8 * cu_count());
+    const int wgs = (nq + 8 * qpw - 1) / (8 * qpw);
+    return 4 * wgs >= 3 * cu_count() ? 1 : 0;
 }
 
 extern "C" int rmi_native_q6_k_mmvq_packed_norm(const void* w_packed, const float* x, const float* w_norm,

@@ -120,22 +120,22 @@ __device__ __forceinline__ void q8_1_store_lane(float v, uint8_t* block) {
 
 // roundf(v / d) of the Q8_1 quantizer (d = amax / 127 with |v| <= amax) with a multiply in place of the divide:
 // y = v * inv_d, inv_d = 1 / d correctly rounded once per block, lies within 2.3e-5 of the correctly rounded quotient,
-// so roundf(y) is roundf(v / d) unless y is within 2^-14 of a half-integer.  Returns the candidate and sets slow when the
-// caller must take the true divide instead (those values, and blocks whose d is not a normal number).  Checked for
-// every float v with |v| <= 128 d at a spread of d against roundf(v / d) (tests/cpp/q8_round_check.c).
+// so rounding y gives roundf(v / d) unless y is within 2^-14 of a half-integer - and away from the half-integers
+// round-half-even (rint, one instruction) and roundf's round-half-away agree.  Returns rint(y) and sets slow when the
+// caller must take roundf(v / d) instead (those values, and blocks whose d is not a normal number).  Checked for every
+// float v with |v| <= 128 d at a spread of d against roundf(v / d) (tests/cpp/q8_round_check.c).
 __device__ __forceinline__ float q8_round_fast(float v, float d, float inv_d, bool& slow) {
     const float y = v * inv_d;
-    const float a = fabsf(y);
-    const float fr = a - floorf(a);
+    const float fr = __builtin_amdgcn_fractf(fabsf(y));   // |y| - floor(|y|), exact for |y| >= 0
     slow = !(fabsf(fr - 0.5f) > 0x1p-14f) || !(d >= 0x1p-126f && d <= 0x1p126f);
-    return y;
+    return __builtin_rintf(y);
 }
 
 // ---- the row-norm reduction over 4-row partials ------------------------------------------------------------------
 // One tree for every kernel that derives a norm's inv = rsqrt(sum / cols + eps) from a vector's 4-row partials
-// (rms_quant_apply, rms_norm_out, and the GEMVs that take a folded norm), so they all get the same bits: 256 lanes
-// (waves 0..3); lane t adds slots t, t + 256, t + 512, ... in order starting from 0, a 64-lane xor butterfly, then the
-// four wave sums in wave order.  A lane's first kNormLoads slots are loaded before the first add (clamped,
+// (rms_quant_apply, rms_norm_out, and the GEMVs that quantize a norm in their stage), so they all get the same bits:
+// 256 lanes (waves 0..3); lane t adds slots t, t + 256, t + 512, ... in order starting from 0, a 64-lane xor butterfly,
+// then the four wave sums in wave order.  A lane's first kNormLoads slots are loaded before the first add (clamped,
 // unconditional: a strided loop or a load under a branch waits on each load in turn).
 constexpr int kNormLoads = 8;
 

@@ -1,6 +1,6 @@
 /* Exhaustive CPU check of the divide-free Q8_1 rounding used by the GEMV kernels that quantize a normed vector in
  * their activation stage (rmi_common.h q8_round): for a block scale d = amax / 127 and every float v with |v| <= 128 d,
- * the fast path roundf(v * (1 / d)) - taken unless the product lies within 2^-14 of a half-integer - must equal
+ * the fast path rint(v * (1 / d)) - taken unless the product lies within 2^-14 of a half-integer - must equal
  * roundf(v / d), the quantizer of the norm kernels.  The arithmetic below is the device's, operation for operation
  * (IEEE single, round to nearest, no contraction).
  *
@@ -20,7 +20,7 @@ static int fast_path(float v, float d, float inv_d, int* q) {
     const float a = fabsf(y);
     const float fr = a - floorf(a);
     if (!(fabsf(fr - 0.5f) > 0x1p-14f) || !(d >= 0x1p-126f && d <= 0x1p126f)) return 0;
-    *q = (int) roundf(y);
+    *q = (int) rintf(y);   /* round half to even (the default mode): equal to roundf away from the ties */
     return 1;
 }
 
