@@ -296,6 +296,16 @@ int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, const uint16_t*
                          const float* gate_src, int gate_stride, float* y, int y_stride, uint8_t* q8, int q8_stride,
                          void* workspace, int n_head, int n_kv, int head_dim, int ntok, int max_ctx, int nsub,
                          float scale, void* stream);
+/* attn_prep (the per-head RMSNorm, RoPE and fp16 K / V store of the new rows; split_qg_kernel, rms, native_rope_apply
+ * and store_kv2_kernel, qw:320-345, 971-975, 1535-1548) folded into rmi_gqa_flash_decode for decode and verify (ntok x
+ * n_head / n_kv <= 8, an even n_head / n_kv, n_rot = 64): q3 is attn_prep's input (per token [n_head x (q | gate) |
+ * k | v], stride q3_stride), which also supplies the gate.  Bitwise rmi_attn_prep_rope followed by
+ * rmi_gqa_flash_decode, in two launches instead of three. */
+int rmi_gqa_flash_decode_prep(const float* q3, int q3_stride, const float* qn, const float* kn, uint16_t* kcache,
+                              uint16_t* vcache, const int* pos, float* y, int y_stride, uint8_t* q8, int q8_stride,
+                              void* workspace, int n_head, int n_kv, int head_dim, int n_rot,
+                              const rmi_rope_params* rope, float eps, int ntok, int max_ctx, int nsub, float scale,
+                              void* stream);
 
 /* rmi_gqa_flash_decode without the workspace argument, for callers that cannot allocate (code under HIP graph
  * capture, serving loops that forbid hipMalloc).  No counterpart in the reference.  The split-K records go to the

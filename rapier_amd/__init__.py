@@ -82,6 +82,8 @@ SIGNATURES = {
                                   _i, _i, _i, _i, _vp]),
     "rmi_attn_prep": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _f, _i, _i, _vp]),
     "rmi_attn_prep_rope": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _f, _i, _i, _vp]),
+    "rmi_gqa_flash_decode_prep": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp,
+                                       _f, _i, _i, _i, _f, _vp]),
     "rmi_rms_norm_weighted": (_i, [_vp, _vp, _i, _i, _f, _vp]),
     "rmi_native_rope_apply": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "rmi_add_inplace": (_i, [_vp, _vp, _i, _vp]),
@@ -416,6 +418,16 @@ def attn_prep_rope(q3, q3_stride, qn, kn, kcache, vcache, pos, qout, n_head, n_k
     rope = RopeParams(freq_base, factor, orig_ctx, ext_factor, attn_factor, beta_fast, beta_slow)
     _call("rmi_attn_prep_rope", _p(q3), q3_stride, _p(qn), _p(kn), _p(kcache), _p(vcache), _p(pos), _p(qout), n_head,
           n_kv, head_dim, n_rot, ctypes.byref(rope), eps, ntok, max_ctx, _stream(stream))
+
+
+def gqa_flash_decode_prep(q3, q3_stride, qn, kn, kcache, vcache, pos, y, y_stride, q8, q8_stride, workspace, n_head,
+                          n_kv, head_dim, n_rot, freq_base, factor, orig_ctx, eps, ntok, max_ctx, nsub, scale,
+                          ext_factor=1.0, attn_factor=1.0, beta_fast=32.0, beta_slow=1.0, stream=None):
+    """attn_prep folded into the split-K decode attention (one slot group: decode and verify)"""
+    rope = RopeParams(freq_base, factor, orig_ctx, ext_factor, attn_factor, beta_fast, beta_slow)
+    _call("rmi_gqa_flash_decode_prep", _p(q3), q3_stride, _p(qn), _p(kn), _p(kcache), _p(vcache), _p(pos), _p(y),
+          y_stride, _p(q8), q8_stride, _p(workspace), n_head, n_kv, head_dim, n_rot, ctypes.byref(rope), eps, ntok,
+          max_ctx, nsub, scale, _stream(stream))
 
 
 def rms_norm_weighted(x, w, rows, cols, eps, stream=None):

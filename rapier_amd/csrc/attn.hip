@@ -146,12 +146,32 @@ __device__ __forceinline__ uint32_t word_of(const uint4& v, int w) {
     return w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w;
 }
 
+// attn_prep folded into the partial (decode and verify: one slot group).  pr.q3 is the GEMV output attn_prep reads;
+// every workgroup norms and ropes its own query rows (attn_prep's reduction tree and rotation, so the same bits) into
+// the query stage, and the workgroup whose chunk holds a new position writes that row's K (normed, roped) and V to the
+// cache before it issues any K / V load (a workgroup barrier orders its stores before its waves' loads; no other
+// workgroup reads the row).
+struct PrepIn {
+    const float* q3;   // per token: [n_head x (q HD | gate HD) | k n_kv HD | v n_kv HD]
+    int q3_stride;
+    const float* qn;
+    const float* kn;
+    uint16_t* kc;      // the caches, written
+    uint16_t* vc;
+    int n_rot;
+    float theta, eps;
+    Yarn yarn;
+};
+
+template <bool PREP>
 __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __restrict__ qbuf, const uint16_t* __restrict__ kc,
                                                           const uint16_t* __restrict__ vc, const int* __restrict__ pos,
                                                           float* __restrict__ ws, int slot_stride, int n_head,
-                                                          int n_kv, int ntok, int nsub, int max_ctx, float scale) {
+                                                          int n_kv, int ntok, int nsub, int max_ctx, float scale,
+                                                          PrepIn pr) {
     __shared__ __attribute__((aligned(16))) uint8_t tiles[WAVES * KTILE];
     __shared__ float wstat[WAVES][2][SLOTS];
+    __shared__ float pred[PREP ? 2 : 1][WAVES];   // PREP: wave sums of the new K rows
     // the KV heads of one chunk are neighbouring workgroups (dispatched together), so the four 512-byte head rows of a
     // position are read close in time
     const int chunk = static_cast<int>(blockIdx.x) / n_kv, kv = static_cast<int>(blockIdx.x) - chunk * n_kv;
@@ -168,20 +188,90 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
     // They do not depend on the position: their loads go out together with pos[0].
     float4* qst = reinterpret_cast<float4*>(tiles);   // [slot within the group][64 float4]
     float4 qin[2];   // float4s tid and tid + 256 of the group's rows, written to the stage after the K / V loads issue
+    const int d = static_cast<int>(threadIdx.x);   // PREP: this lane's dim of every query row and new K / V row
+    // PREP query rows: wave w holds slots 2 w and 2 w + 1, lane l dims l + 64 k (k = 0..3) of each
+    float xq[PREP ? 2 : 1][4], wq4[4], xk[PREP ? 2 : 1], xv[PREP ? 2 : 1], wk = 0.0f;
+    double freq = 0.0, qfreq = 0.0;
+    if constexpr (PREP) {
+        // raw rows, independent of the position: in flight together with pos
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int f = static_cast<int>(threadIdx.x) + 256 * i, qs = s0 + (f >> 6);
-        const bool ok = qs < nq;
-        const int t = ok ? qs / G : 0, gh = ok ? qs - (qs / G) * G : 0;
-        const float4* q = reinterpret_cast<const float4*>(qbuf + (static_cast<size_t>(t) * n_head + kv * G + gh) * HD);
-        const float4 v = q[f & 63];   // unconditional (a load under a branch gets a wait of its own)
-        qin[i] = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int r = 0; r < 2; ++r) {
+            const int qs = min(s0 + 2 * wv + r, nq - 1), t = qs / G, gh = qs - t * G;
+            const float* row = pr.q3 + static_cast<size_t>(t) * pr.q3_stride + (kv * G + gh) * 2 * HD;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xq[r][k] = row[lane + 64 * k];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) wq4[k] = pr.qn[lane + 64 * k];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const float* src = pr.q3 + static_cast<size_t>(min(t, ntok - 1)) * pr.q3_stride + 2 * n_head * HD;
+            xk[t] = src[kv * HD + d];
+            xv[t] = src[n_kv * HD + kv * HD + d];
+        }
+        wk = pr.kn[d];
+        if (d < pr.n_rot) freq = rope_freq(d < pr.n_rot / 2 ? d : d - pr.n_rot / 2, pr.n_rot, pr.theta);
+        // the query rows' rotated dims: lane l of group 0 (n_rot = 64)
+        if (lane < pr.n_rot) qfreq = rope_freq(lane < pr.n_rot / 2 ? lane : lane - pr.n_rot / 2, pr.n_rot, pr.theta);
+        asm volatile("" : "+v"(freq), "+v"(qfreq));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int f = static_cast<int>(threadIdx.x) + 256 * i, qs = s0 + (f >> 6);
+            const bool ok = qs < nq;
+            const int t = ok ? qs / G : 0, gh = ok ? qs - (qs / G) * G : 0;
+            const float4* q = reinterpret_cast<const float4*>(qbuf + (static_cast<size_t>(t) * n_head + kv * G + gh) * HD);
+            const float4 v = q[f & 63];   // unconditional (a load under a branch gets a wait of its own)
+            qin[i] = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     }
     const int p0 = pos[0];
     const int p_last = p0 + (min(s0 + SLOTS, nq) - 1) / G;   // the last position this group's slots see
     const int wlen = STEP * nsub;
     const int cbase = chunk * WAVES * wlen;
     if (cbase > p_last || p0 < 0 || p_last >= max_ctx) return;   // uniform: no visible position (or a bad pos)
+    // attn_prep's rotation of dim d (and d +- n_rot / 2) of a normed row staged in LDS (row) at position p (the angle
+    // in fp64, as attn_prep)
+    auto rope_row = [&](const float* row, float v, int p) {
+        if (d < pr.n_rot) {
+            const int half = pr.n_rot / 2;
+            float c, sn;
+            rope_cos_sin_f(p, freq, d < half ? d : d - half, pr.yarn, &c, &sn);
+            v = d < half ? rope_lo(row[d], row[d + half], c, sn) : rope_hi(row[d - half], row[d], c, sn);
+        }
+        return v;
+    };
+    if constexpr (PREP) {
+        // the new rows of this chunk (tokens t < ntok at p0 + t within [cbase, cbase + WAVES wlen)): K normed (the
+        // norm tree of attn_prep: 64-lane butterfly per wave, then the four wave sums in order) and roped, V as is
+        const int cend = cbase + WAVES * wlen;
+        const int tfirst = max(0, cbase - p0), tlast = min(ntok, cend - p0);   // tokens [tfirst, tlast)
+        if (tfirst < tlast) {   // uniform
+            float* krow = reinterpret_cast<float*>(tiles);   // [2][HD] normed K rows
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float sq = group_sum<64>(xk[t] * xk[t]);
+                if ((d & 63) == 0) pred[t][d >> 6] = sq;
+            }
+            __syncthreads();
+            float kvn[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float ss = ((pred[t][0] + pred[t][1]) + pred[t][2]) + pred[t][3];
+                kvn[t] = xk[t] * rsqrtf(ss / static_cast<float>(HD) + pr.eps) * wk;
+                krow[t * HD + d] = kvn[t];
+            }
+            __syncthreads();
+            for (int t = tfirst; t < tlast; ++t) {
+                const int p = p0 + t;
+                const float kr = rope_row(krow + t * HD, kvn[t], p);
+                pr.kc[(static_cast<size_t>(p) * n_kv + kv) * HD + d] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(kr));
+                pr.vc[(static_cast<size_t>(p) * n_kv + kv) * HD + d] =
+                    __builtin_bit_cast(uint16_t, static_cast<_Float16>(t == 0 ? xv[0] : xv[1]));
+            }
+            __syncthreads();   // the rows are stored (workgroup scope) before any wave issues its K / V loads
+        }
+    }
 
     const int wbase = cbase + wv * wlen;
     const int nsteps = wbase > p_last ? 0 : min(nsub, (p_last - wbase) / STEP + 1);
@@ -220,8 +310,35 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
     }
     // B operand of the score MFMAs, from the staged query rows: step 2 sp + hlf covers dims
     // 32 sp + 8 g4 + 4 hlf + [0, 4); rows 0-7 the fp16 hi part, rows 8-15 the fp16 lo part of the same slot
+    if constexpr (PREP) {
+        // the wave's two query rows: attn_prep's norm (the four 64-lane butterflies of a row, summed in order), weights,
+        // then its rotation (n_rot 64: dims l and l +- 32 of group 0 meet by one lane exchange), into the stage
+        float* qf = reinterpret_cast<float*>(tiles);   // [slot][HD]
+        const int tq = min(s0 + 2 * wv, nq - 1) / G;    // both rows' token (G >= 2)
+        float qc = 1.0f, qs = 0.0f;
+        if (lane < pr.n_rot) rope_cos_sin_f(p0 + tq, qfreq, lane < pr.n_rot / 2 ? lane : lane - pr.n_rot / 2, pr.yarn, &qc, &qs);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) qst[static_cast<int>(threadIdx.x) + 256 * i] = qin[i];
+        for (int r = 0; r < 2; ++r) {
+            // lane 0's butterfly result, as attn_prep takes it: with the square contracted into the first step's add
+            // (fma(x, x, partner^2)) the lanes of a wave do not all end with the same sum
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                ss += __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(group_sum<64>(xq[r][k] * xq[r][k]))));
+            const float inv = rsqrtf(ss / static_cast<float>(HD) + pr.eps);
+            float v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = xq[r][k] * inv * wq4[k];
+            const float other = xor_lane<32>(v[0]);
+            if (lane < pr.n_rot) v[0] = lane < pr.n_rot / 2 ? rope_lo(v[0], other, qc, qs) : rope_hi(other, v[0], qc, qs);
+            const bool live = s0 + 2 * wv + r < nq;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qf[(2 * wv + r) * HD + lane + 64 * k] = live ? v[k] : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) qst[static_cast<int>(threadIdx.x) + 256 * i] = qin[i];
+    }
     __syncthreads();   // the staged rows are complete
     half4 qb[16];
 #pragma unroll
@@ -522,8 +639,8 @@ int flash_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache,
                  int gate_stride, float* y, int y_stride, uint8_t* q8, int q8_stride, float* ws, int slot_stride,
                  int n_head, int n_kv, int ntok, int nchunks, int nsub, int max_ctx, float scale, hipStream_t s) {
     const int groups = (ntok * (n_head / n_kv) + SLOTS - 1) / SLOTS;
-    hipLaunchKernelGGL(gqa_partial_kernel, dim3(nchunks * n_kv, 1, groups), dim3(256), 0, s, q, kcache, vcache, pos, ws,
-                       slot_stride, n_head, n_kv, ntok, nsub, max_ctx, scale);
+    hipLaunchKernelGGL(gqa_partial_kernel<false>, dim3(nchunks * n_kv, 1, groups), dim3(256), 0, s, q, kcache, vcache, pos,
+                       ws, slot_stride, n_head, n_kv, ntok, nsub, max_ctx, scale, PrepIn{});
     hipLaunchKernelGGL(gqa_merge_kernel, dim3(ntok, n_head, kMergeParts), dim3(HD), 0, s, ws, slot_stride, gate_src, gate_stride,
                        pos, y, y_stride, q8, q8_stride, n_head, n_kv, SUB * nsub);
     return launch_status("gqa_flash_decode");
@@ -591,6 +708,33 @@ extern "C" int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, cons
     return flash_decode(q, kcache, vcache, pos, gate_src, gate_stride, y, y_stride, q8, q8_stride,
                         static_cast<float*>(workspace), kMaxSlots, n_head, n_kv, ntok, nchunks, nsub, max_ctx, scale,
                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rmi_gqa_flash_decode_prep(const float* q3, int q3_stride, const float* qn, const float* kn,
+                                         uint16_t* kcache, uint16_t* vcache, const int* pos, float* y, int y_stride,
+                                         uint8_t* q8, int q8_stride, void* workspace, int n_head, int n_kv,
+                                         int head_dim, int n_rot, const rmi_rope_params* rope, float eps, int ntok,
+                                         int max_ctx, int nsub, float scale, void* stream) {
+    if (head_dim != HD || n_head <= 0 || n_kv <= 0 || n_head % n_kv || ntok < 1 || ntok * (n_head / n_kv) > SLOTS ||
+        max_ctx <= 0 || max_ctx % SUB || nsub <= 0 || n_rot != 64 || (n_head / n_kv) % 2 || !rope ||
+        !(rope->freq_base > 1.0f))
+        return fail(RMI_ERR_SHAPE, "gqa_flash_decode_prep: invalid arguments (one slot group: ntok x heads per KV head "
+                                   "<= 8, an even number of heads per KV head, 64 rotary dims)");
+    if (!aligned4(q3) || !aligned4(qn) || !aligned4(kn) || !aligned16(kcache) || !aligned16(vcache) ||
+        !aligned4(pos) || !aligned16(workspace) || (!y && !q8))
+        return fail(RMI_ERR_POINTER, "gqa_flash_decode_prep: invalid arguments");
+    const int chunk_len = SUB * nsub, nchunks = (max_ctx + chunk_len - 1) / chunk_len;
+    if (nchunks > kMaxChunks) return fail(RMI_ERR_SHAPE, "gqa_flash_decode_prep: max_ctx / (64 * nsub) exceeds 2048 chunks");
+    Yarn yarn{};
+    if (!yarn_setup(*rope, n_rot, &yarn)) return fail(RMI_ERR_SHAPE, "gqa_flash_decode_prep: invalid YaRN parameters");
+    const PrepIn pr{q3, q3_stride, qn, kn, kcache, vcache, n_rot, rope->freq_base, eps, yarn};
+    const auto s = static_cast<hipStream_t>(stream);
+    auto* ws = static_cast<float*>(workspace);
+    hipLaunchKernelGGL(gqa_partial_kernel<true>, dim3(nchunks * n_kv, 1, 1), dim3(256), 0, s, nullptr, kcache, vcache,
+                       pos, ws, kMaxSlots, n_head, n_kv, ntok, nsub, max_ctx, scale, pr);
+    hipLaunchKernelGGL(gqa_merge_kernel, dim3(ntok, n_head, kMergeParts), dim3(HD), 0, s, ws, kMaxSlots, q3, q3_stride,
+                       pos, y, y_stride, q8, q8_stride, n_head, n_kv, SUB * nsub);
+    return launch_status("gqa_flash_decode_prep");
 }
 
 extern "C" size_t rmi_gqa_noalloc_scratch_bytes(int max_ctx, int n_kv, int nsub, int slots) {

@@ -572,9 +572,18 @@ int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
 int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc) {
     const auto& c = e.cfg;
     RMI_TRY(norm_gemv(e, L.in_proj, x, part, L.attn_norm, e.proj, nc));
+    const size_t q8y_col = q81_bytes(e.attn_q);
+    if (nc * (c.n_head / c.n_kv) <= 8 && c.n_rot == 64 && (c.n_head / c.n_kv) % 2 == 0) {
+        // decode / verify: the per-head norm, RoPE and K / V store in the attention's partial launch
+        RMI_TRY(rmi_gqa_flash_decode_prep(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, nullptr, 0, e.q8y,
+                                          static_cast<int>(q8y_col), e.attn_ws, c.n_head, c.n_kv, c.head_dim, c.n_rot,
+                                          &e.rope, c.eps, nc, e.max_ctx, e.nsub,
+                                          1.0f / sqrtf(static_cast<float>(c.head_dim)), e.s));
+        RMI_TRY(gemv_res(e, L.out_proj, e.q8y, x, part, nc));
+        return ffn(e, L, x, part, nc);
+    }
     RMI_TRY(rmi_attn_prep_rope(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, e.qbuf, c.n_head, c.n_kv, c.head_dim,
                                c.n_rot, &e.rope, c.eps, nc, e.max_ctx, e.s));
-    const size_t q8y_col = q81_bytes(e.attn_q);
     const int per = std::max(1, kAttnSlots / (c.n_head / c.n_kv));   // tokens per attention launch
     for (int c0 = 0; c0 < nc; c0 += per) {
         RMI_TRY(rmi_gqa_flash_decode(e.qbuf + static_cast<size_t>(c0) * e.attn_q, L.kc, L.vc, pos + c0,

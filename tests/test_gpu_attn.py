@@ -209,3 +209,34 @@ def test_elementwise_inplace(orc, rmi):
     rmi.silu_inplace(x, n)
     ref = a.astype(np.float64) / (1 + np.exp(-a.astype(np.float64)))
     assert_close_rel(host(x), ref, rtol=1e-6, atol_frac=1e-7, what="silu")
+
+
+@pytest.mark.parametrize("ctx,nsub,p0,ntok,factor", [(4096, 2, 4096 - 300, 2, 1.0), (4096, 2, 255, 2, 1.0),
+                                                     (65536, 8, 65536 - 700, 2, 1.0), (320, 1, 0, 2, 1.0),
+                                                     (4096, 2, 1000, 1, 1.0), (8192, 2, 5000, 2, 4.0)])
+def test_flash_decode_prep_bitwise_equals_prep_then_flash(orc, rmi, ctx, nsub, p0, ntok, factor):
+    """rmi_gqa_flash_decode_prep (attn_prep folded into the partial) against rmi_attn_prep_rope followed by
+    rmi_gqa_flash_decode on copies of the same caches: y and Q8_1 bitwise, and the caches bitwise after the call (the
+    new K / V rows written, nothing else).  p0 = 255 puts the verify pair on both sides of a 128-position chunk
+    boundary; p0 = 0 is a context of one position; factor 4 is YaRN."""
+    t_ = torch()
+    kc, vc = kv_cache(orc, ctx, seed=ctx + p0)
+    q3 = orc.normal(ntok * Q3, seed=p0 + 990)
+    qn = (1 + orc.normal(HD, seed=991, std=0.1)).astype(np.float32)
+    kn = (1 + orc.normal(HD, seed=992, std=0.1)).astype(np.float32)
+    dq3, dqn, dkn, dpos = dev(q3), dev(qn), dev(kn), dev(np.array([p0], np.int32))
+    ka, va, kb, vb = dev(kc), dev(vc), dev(kc), dev(vc)
+    ws = empty(rmi.gqa_workspace_bytes(ctx, NKV, nsub), "uint8")
+    qo = empty(ntok * NH * HD)
+    rmi.attn_prep_rope(dq3, Q3, dqn, dkn, ka, va, dpos, qo, NH, NKV, HD, 64, 1e7, factor, 4096.0, 1e-6, ntok, ctx)
+    ya, q8a = empty(ntok * NH * HD), empty(ntok * NH * HD // 32 * 36, "uint8")
+    rmi.gqa_flash_decode(qo, ka, va, dpos, dq3, Q3, ya, NH * HD, q8a, NH * HD // 32 * 36, ws, NH, NKV, HD, ntok, ctx,
+                         nsub, SCALE)
+    ws2 = empty(rmi.gqa_workspace_bytes(ctx, NKV, nsub), "uint8")
+    yb, q8b = empty(ntok * NH * HD), empty(ntok * NH * HD // 32 * 36, "uint8")
+    rmi.gqa_flash_decode_prep(dq3, Q3, dqn, dkn, kb, vb, dpos, yb, NH * HD, q8b, NH * HD // 32 * 36, ws2, NH, NKV, HD,
+                              64, 1e7, factor, 4096.0, 1e-6, ntok, ctx, nsub, SCALE)
+    t_.cuda.synchronize()
+    assert np.array_equal(host(yb).view(np.uint32), host(ya).view(np.uint32))
+    assert np.array_equal(host(q8b), host(q8a))
+    assert np.array_equal(host(kb), host(ka)) and np.array_equal(host(vb), host(va))
