@@ -52,9 +52,9 @@ UGS_BYTES = q6_bytes(UG_ROWS, UG_IN) + 2 * (UG_IN // 32) * 36 + 2 * (UG_ROWS // 
 
 # HBM traffic of one fused up||gate + SwiGLU ncols=2 launch: L2-to-memory request counts from two rocprofv3 --pmc passes
 # over `bench.py --workload traffic_probe` (profiles/gemv_up_gate_swiglu_traffic.md).  On gfx950 a TCC_EA0_RDREQ that is
-# not a 32-byte request moves 128 bytes (the same process's copy kernel reads 256 MiB in 2,097,395 requests), and a
+# not a 32-byte request moves 128 bytes (the same process's copy kernel reads 256 MiB in 2,097,401 requests), and a
 # TCC_EA0_WRREQ is 64 bytes (TCC_EA0_WRREQ_64B) or 32.
-PMC_UG_RDREQ, PMC_UG_RDREQ_32B = 648264, 0
+PMC_UG_RDREQ, PMC_UG_RDREQ_32B = 648172, 0
 PMC_UG_WRREQ, PMC_UG_WRREQ_64B = 768, 384
 
 
@@ -63,7 +63,7 @@ def ea_bytes(rdreq, rdreq_32b, wrreq, wrreq_64b):
     return 128 * (rdreq - rdreq_32b) + 32 * rdreq_32b + 64 * wrreq_64b + 32 * (wrreq - wrreq_64b)
 
 
-UG_TRAFFIC_BYTES = ea_bytes(PMC_UG_RDREQ, PMC_UG_RDREQ_32B, PMC_UG_WRREQ, PMC_UG_WRREQ_64B)   # 83,014,656
+UG_TRAFFIC_BYTES = ea_bytes(PMC_UG_RDREQ, PMC_UG_RDREQ_32B, PMC_UG_WRREQ, PMC_UG_WRREQ_64B)   # 83,002,880
 
 
 def cpu_model():
@@ -264,7 +264,7 @@ def run_verify_gemv(args):
             "config1": c1,
         },
         "roofline": {
-            "kernel": "q6k_packed_swiglu<2, false, 8, 4, 2> (up||gate 24576x4096 GEMV + SwiGLU + Q8_1, ncols=2, "
+            "kernel": "q6k_packed_swiglu<2, 8, 4, 2, false> (up||gate 24576x4096 GEMV + SwiGLU + Q8_1, ncols=2, "
                       "SwiGLU-packed wave-tile layout; 192 workgroups of 8 waves, two 32-output groups each)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
@@ -497,36 +497,43 @@ def time_gdn_layer(stream):
 
 
 def time_attention(stream, ctx):
-    """the verify round's attention launch pair (rmi_gqa_flash_decode: split-K partial + merge with the sigmoid gate
-    and Q8_1) for 2 queries at positions ctx - 2, ctx - 1 over a fp16 KV cache of the 9B shapes (4 KV heads x 256),
-    rotating over enough caches to exceed the Infinity Cache.  Algorithmic bytes: K + V rows read once."""
+    """the verify round's attention launch pair as the engine runs it (rmi_gqa_flash_decode_prep: the per-head norm,
+    RoPE and the new K / V rows in the split-K partial, then the merge with the sigmoid gate and Q8_1) for 2 queries at
+    positions ctx - 2, ctx - 1 over a fp16 KV cache of the 9B shapes (4 KV heads x 256), with the engine's chunk size
+    (a full cache is one partial workgroup per CU), rotating over enough caches to exceed the Infinity Cache.
+    Algorithmic bytes: K + V rows read once."""
     import torch
 
     import rapier_amd as rmi
     n_head, n_kv, hd = 16, 4, 256
     max_ctx = ctx + 512
-    nsub = max(2, min(16, max_ctx // 8192))
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    chunks = max(1, cus // n_kv)
+    nsub = max(2, min(16, -(-max_ctx // (64 * chunks))))
     row = n_kv * hd
     nrot = max(2, -(-400_000_000 // (2 * max_ctx * row * 2)))
     kv = torch.empty(nrot, 2, max_ctx * row, dtype=torch.float16, device="cuda")
     rmi.gen_normal_f16(kv, kv.numel(), seed=41)
-    q = torch.empty(2 * n_head * hd, device="cuda")
-    rmi.gen_normal(q, q.numel(), seed=42)
-    gstride = 2 * n_head * hd + 2 * row
-    gate = torch.empty(2 * gstride, device="cuda")
-    rmi.gen_normal(gate, gate.numel(), seed=43)
+    q3_stride = 2 * n_head * hd + 2 * row   # per token [n_head x (q | gate) | k | v], the qkv GEMV's output
+    q3 = torch.empty(2 * q3_stride, device="cuda")
+    rmi.gen_normal(q3, q3.numel(), seed=42)
+    qn = torch.ones(hd, device="cuda")
+    kn = torch.ones(hd, device="cuda")
     pos = torch.tensor([ctx - 2], dtype=torch.int32, device="cuda")
+    yb = torch.empty(2 * n_head * hd, device="cuda")
     q8b = rmi.native_q8_1_bytes(n_head * hd, 1)
     q8 = torch.empty(2 * q8b, dtype=torch.uint8, device="cuda")
     ws = torch.empty(rmi.gqa_workspace_bytes(max_ctx, n_kv, nsub), dtype=torch.uint8, device="cuda")
 
     def launch(r):
-        rmi.gqa_flash_decode(q, kv[r, 0], kv[r, 1], pos, gate, gstride, None, 0, q8, q8b, ws, n_head, n_kv, hd, 2,
-                             max_ctx, nsub, 1.0 / 16, stream)
+        rmi.gqa_flash_decode_prep(q3, q3_stride, qn, kn, kv[r, 0], kv[r, 1], pos, yb, n_head * hd, q8, q8b, ws,
+                                  n_head, n_kv, hd, 64, 1e7, 1.0, 4096.0, 1e-6, 2, max_ctx, nsub, 1.0 / 16,
+                                  stream=stream)
 
     us, n = time_graph(stream, launch, nrot)
     nbytes = 2 * ctx * row * 2
-    return {"kernel": f"attention, 2 queries, ctx {ctx} (rmi_gqa_flash_decode: partial + merge, nsub {nsub})",
+    return {"kernel": f"attention, 2 queries, ctx {ctx} (rmi_gqa_flash_decode_prep: norm + RoPE + partial, then "
+                      f"merge; nsub {nsub})",
             "per_round": ROUND_ATTN, "algorithmic_bytes": nbytes, "us": round(us, 3),
             "GB_s": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
             "launches_timed": n}

@@ -5,8 +5,9 @@
  *
  * Reference: src/qwythos.cpp - Engine / alloc_primary / load_model (152-281, 1838-2134), forward_token (1773-1824),
  * draft_predict (1316-1406), launch_token_verify (1412-1618), the MTP accept / rollback loop (3182-3241, serve
- * 2761-2808) and capture_graph (1757-1771).  Weights are seeded random-init Q6_K of the qwen35 shapes (there is no
- * GGUF reader); everything else follows the reference's engine.
+ * 2761-2808) and capture_graph (1757-1771).  Weights are either seeded random-init Q6_K of the qwen35 shapes
+ * (rmi_engine_create, the benchmark configs) or a qwen35 GGUF file (rmi_engine_create_gguf, load_model's tensor names
+ * and metadata keys); everything else follows the reference's engine.
  *
  * Unlike the kernel entry points, the engine owns its memory: rmi_engine_create allocates the model, the caches and
  * the round buffers once; generation allocates nothing on the device.
