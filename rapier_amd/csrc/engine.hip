@@ -831,20 +831,21 @@ int setup(Engine& e, const rmi_model_config& c, int max_ctx, void* stream) {
         e.fuse_norm = !(v && v[0] == '0');
     }
     // attention chunk = 64 * nsub positions, sized so that a full cache is one partial workgroup per CU (n_kv heads
-    // per chunk), at least 128 positions: nsub 2 at 4K-class caches, 16 at 64K on 256 CUs.  Measured on the 9B
-    // round at 64K: nsub 4 / 6 / 8 / 12 / 16 -> 2655 / 2571 / 2603 / 2589 / 2540 us; at 4K nsub 1 / 2 / 3 / 4 ->
-    // 2223 / 2191 / 2203 / 2210 us.
+    // per chunk), at least 128 positions: nsub 2 at 4K-class caches, 16 at 65536 positions, 17 at 66048 on 256 CUs.
+    // Measured on the 9B round at 64K: nsub 4 / 6 / 8 / 12 / 16 -> 2655 / 2571 / 2603 / 2589 / 2540 us; at 4K nsub
+    // 1 / 2 / 3 / 4 -> 2223 / 2191 / 2203 / 2210 us.  No upper clamp below 64: a 66048-position cache at nsub 16 is 65
+    // chunks, 260 workgroups, and four CUs then run two of them (64K round 2518 -> 2496 us at nsub 17).
     {
         int cus = 0, dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
         const int chunks = std::max(1, cus / std::max(1, c.n_kv));
-        e.nsub = std::max(2, std::min(16, (e.max_ctx + 64 * chunks - 1) / (64 * chunks)));
+        e.nsub = std::max(2, std::min(64, (e.max_ctx + 64 * chunks - 1) / (64 * chunks)));
     }
     {
-        const char* v = std::getenv("RMI_ATTN_NSUB");   // an explicit chunk size (64 x 1..16 positions)
-        if (v && *v) e.nsub = std::max(1, std::min(16, std::atoi(v)));
+        const char* v = std::getenv("RMI_ATTN_NSUB");   // an explicit chunk size (64 x 1..64 positions)
+        if (v && *v) e.nsub = std::max(1, std::min(64, std::atoi(v)));
     }
     if (stream) {
         e.s = static_cast<hipStream_t>(stream);

@@ -40,10 +40,12 @@ def flash(rmi, q, kc, vc, p0, gate, ntok, max_ctx, nsub):
     return host(y), host(q8)
 
 
-# nsub 2 at ctx 4096 and 16 at ctx 65536 are the chunkings the engine picks on 256 CUs (a full cache is one partial
-# workgroup per CU, clamped to 2..16: 128- and 1024-position chunks), so the merge path the round runs is checked
-# against the oracle at its real chunk counts
-@pytest.mark.parametrize("ctx,nsub", [(4096, 1), (4096, 2), (32768, 4), (65536, 4), (65536, 8), (65536, 16)])
+# The engine sizes the chunk so that a full cache is one partial workgroup per CU (at least 128 positions): nsub 2 at
+# 4K-class caches, 16 at a 65536-position cache and 17 at the 66048 positions a 64K context with room for generation
+# takes (1088-position chunks, the last one 768 long) on 256 CUs, so the merge path the round runs is checked against
+# the oracle at its real chunk counts
+@pytest.mark.parametrize("ctx,nsub", [(4096, 1), (4096, 2), (32768, 4), (65536, 4), (65536, 8), (65536, 16),
+                                      (66048, 17)])
 def test_flash_decode_matches_oracle(orc, rmi, ctx, nsub):
     kc, vc = kv_cache(orc, ctx, seed=ctx)
     q = orc.normal(2 * NH * HD, seed=ctx + 7)
@@ -112,7 +114,8 @@ def test_attn_prep_matches_oracle(orc, rmi, ntok):
     assert not host(kc)[(p0 + ntok) * NKV * HD:].any(), "attn_prep wrote outside its positions"
 
 
-@pytest.mark.parametrize("ctx,nsub,ntok", [(4096, 2, 16), (2048, 1, 13), (65536, 8, 16), (65536, 16, 16)])
+@pytest.mark.parametrize("ctx,nsub,ntok", [(4096, 2, 16), (2048, 1, 13), (65536, 8, 16), (65536, 16, 16),
+                                           (66048, 17, 16)])
 def test_flash_decode_chunk_bitwise_equals_single_queries(orc, rmi, ctx, nsub, ntok):
     """an ingest chunk: ntok query tokens (ntok * 4 = up to 64 query vectors per KV head, 8 slot groups) in one launch;
     each token's y and Q8_1 are bitwise the 1-token launch at its position; token 0 within 1e-3 of the oracle"""
@@ -214,6 +217,7 @@ def test_elementwise_inplace(orc, rmi):
 
 @pytest.mark.parametrize("ctx,nsub,p0,ntok,factor", [(4096, 2, 4096 - 300, 2, 1.0), (4096, 2, 255, 2, 1.0),
                                                      (65536, 16, 65536 - 700, 2, 1.0), (320, 1, 0, 2, 1.0),
+                                                     (66048, 17, 65279, 2, 1.0),
                                                      (4096, 2, 1000, 1, 1.0), (8192, 2, 5000, 2, 4.0)])
 def test_flash_decode_prep_bitwise_equals_prep_then_flash(orc, rmi, ctx, nsub, p0, ntok, factor):
     """rmi_gqa_flash_decode_prep (attn_prep folded into the partial) against rmi_attn_prep_rope followed by
