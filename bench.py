@@ -214,6 +214,24 @@ def run_verify_gemv(args):
     ms_per_step = total_ms / args.steps
     value = PAIR_BYTES / (ms_per_step * 1e-3) / 1e9
 
+    # the same pair through the same entry points once native_q6_k_pack has given every replica a library-owned
+    # packed copy (the reference's opt-in registry, mmvq:2930-2960, looked up at mmvq:3629): the packed kernels, the
+    # same bits
+    for i in range(reps):
+        assert rmi.native_q6_k_pack(ug[i], UG_IN, UG_ROWS) and rmi.native_q6_k_pack(dn[i], DN_IN, DN_ROWS)
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    reg_ms_per_step = t_start.elapsed_time(t_end) / args.steps
+    for i in range(reps):
+        rmi.native_q6_k_unpack(ug[i])
+        rmi.native_q6_k_unpack(dn[i])
+
     # roofline leg: the round's up||gate kernel (GEMV + SwiGLU + Q8_1, one launch) on SwiGLU-packed (wave-tiled)
     # copies of the up||gate replicas, as the engine packs them.  Blocks of back-to-back launches over the rotating
     # replicas, one HIP event pair per block on the launch stream (per-launch event pairs would add the event's own
@@ -259,6 +277,8 @@ def run_verify_gemv(args):
             "algorithmic_bytes_per_step": PAIR_BYTES,
             "us_per_pair": round(ms_per_step * 1e3, 2),
             "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+            "registry_packed_us_per_pair": round(reg_ms_per_step * 1e3, 2),
+            "registry_packed_hbm_frac_of_peak": round(PAIR_BYTES / (reg_ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "weight_replicas": reps,
             "rotated_bytes": reps * (q6_bytes(UG_ROWS, UG_IN) + q6_bytes(DN_ROWS, DN_IN)),
             "config1": c1,
@@ -319,6 +339,11 @@ def run_config1(stream, blocks=5):
         return sum(a.elapsed_time(b) * 1e3 / (2 * reps) for a, b in evs) / blocks
 
     gguf_us = time_it(lambda i: rmi.native_q6_k_mmvq_res(ws[i], xq, y, y, part, C1_IN, C1_ROWS, stream))
+    for i in range(reps):   # the reference's call again, on library-owned packed copies (native_q6_k_pack)
+        assert rmi.native_q6_k_pack(ws[i], C1_IN, C1_ROWS)
+    reg_us = time_it(lambda i: rmi.native_q6_k_mmvq_res(ws[i], xq, y, y, part, C1_IN, C1_ROWS, stream))
+    for i in range(reps):
+        rmi.native_q6_k_unpack(ws[i])
     wp = [torch.empty(rmi.q6_k_packed_bytes(C1_IN, C1_ROWS), dtype=torch.uint8, device="cuda") for _ in range(reps)]
     for i in range(reps):
         rmi.q6_k_pack(ws[i], wp[i], C1_IN, C1_ROWS, stream)
@@ -328,6 +353,7 @@ def run_config1(stream, blocks=5):
     return {"workload": "config 1: Q6_K 12288x4096 GEMV, ncols=1, residual + partials (y aliases res)",
             "algorithmic_bytes": C1_BYTES,
             "gguf_layout_us": round(gguf_us, 2), "gguf_layout_GB_s": round(C1_BYTES / gguf_us / 1e3, 1),
+            "registry_packed_us": round(reg_us, 2), "registry_packed_GB_s": round(C1_BYTES / reg_us / 1e3, 1),
             "packed_us": round(packed_us, 2), "packed_GB_s": round(C1_BYTES / packed_us / 1e3, 1)}
 
 
@@ -1019,7 +1045,10 @@ def main():
                 (info["round_weight_bytes"] + info["kv_bytes_per_pos"] * ctxs[0]) /
                 (head["us_per_round"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "verify_gemv_pair": {"GB_s": gemv["value"], "us_per_pair": gemv["config"]["us_per_pair"],
-                                 "hbm_frac_of_peak": gemv["config"]["hbm_frac_of_peak"]},
+                                 "hbm_frac_of_peak": gemv["config"]["hbm_frac_of_peak"],
+                                 "registry_packed_us_per_pair": gemv["config"]["registry_packed_us_per_pair"],
+                                 "registry_packed_hbm_frac_of_peak":
+                                     gemv["config"]["registry_packed_hbm_frac_of_peak"]},
             "config1_gpu": gemv["config"]["config1"],
             "ingest": ingest,
             # bounded waits of the GDN layer kernel that ran out in this process (the engine calls fail if any did)

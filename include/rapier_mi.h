@@ -74,6 +74,17 @@ int rmi_native_q6_k_mmvq_res_n(const void* w, const void* x_q8_1, float* y, cons
  * ncols >= 2 call equal to the ncols = 1 call; _res_n equal to plain + res with one partial per 4 rows). */
 size_t rmi_q6_k_packed_bytes(int n_in, int n_out);
 int rmi_q6_k_pack(const void* w, void* w_packed, int n_in, int n_out, void* stream);
+/* The reference's registry-owned copy itself (native_q6_k_pack, mmvq:2930-2960; native_q6_k_unpack, mmvq:3042-3048):
+ * the library packs the GGUF-layout matrix w into a copy of its own (synchronously: every stream of the device drains
+ * first, as the reference's host round trip does), and from then on rmi_native_q6_k_mmvq, _res and _res_n called with
+ * w and the same shape run the packed kernels on that copy (the same bits), as native_q6_k_mmvq looks up its registry
+ * first (mmvq:3629).  RMI_OK when packed or packed already; RMI_ERR_UNSUPPORTED for shapes the packed layout does not
+ * take (n_in not a multiple of 2048: the GGUF-layout kernels keep running); RMI_ERR_STATE when w is packed with
+ * another shape.  rmi_native_q6_k_unpack frees the copy (a no-op for weights without one) after draining the device.
+ * rmi_native_q6_k_packed_copies counts the copies held. */
+int rmi_native_q6_k_pack_copy(const void* w, int n_in, int n_out);
+int rmi_native_q6_k_unpack(const void* w);
+int rmi_native_q6_k_packed_copies(void);
 /* No counterpart in the reference (a fusion of its up/gate GEMVs, mmvq:1261-1356, with swiglu_quant_kernel,
  * qw:676-689).  Packs an up||gate Q6_K matrix (2 n_ff rows: up rows, then gate rows) in the SwiGLU row order:
  * packed rows 64 G .. 64 G + 31 are gate rows 32 G .., rows 64 G + 32 .. 64 G + 63 up rows 32 G ...  n_ff a multiple

@@ -55,6 +55,26 @@ inline void native_q6_k_mmvq_res(const void* w, const void* x_q8_1, float* y, co
                                  int n_in, int n_out, void* stream) {
     rmi_detail::check_mmvq(rmi_native_q6_k_mmvq_res(w, x_q8_1, y, res, partials, n_in, n_out, stream));
 }
+// mmvq:2922-2928: the opt-in switch the reference's engine reads before it packs (STRATA_Q6_PACKED=1)
+inline bool native_q6_k_packed_enabled() {
+    static const bool enabled = [] {
+        const char* v = std::getenv("STRATA_Q6_PACKED");
+        return v && v[0] == '1' && v[1] == '\0';
+    }();
+    return enabled;
+}
+// mmvq:2930-2960: a library-owned packed copy that native_q6_k_mmvq / _res then run on; false where the packed layout
+// does not take the shape or the copy could not be made (the GGUF-layout kernels keep running), one stderr line per copy
+inline bool native_q6_k_pack(const void* weights, int n_in, int n_out, const char* what) {
+    const int before = rmi_native_q6_k_packed_copies();
+    if (rmi_native_q6_k_pack_copy(weights, n_in, n_out) != RMI_OK) return false;
+    if (rmi_native_q6_k_packed_copies() != before)
+        std::fprintf(stderr, "rapier_mi: packed the %s (%d x %d) into a wave-tile copy\n", what ? what : "matrix", n_out,
+                     n_in);
+    return true;
+}
+// mmvq:3042-3048
+inline void native_q6_k_unpack(const void* weights) { rmi_detail::check_mmvq(rmi_native_q6_k_unpack(weights)); }
 // mmvq:3732-3736
 inline void native_q8_0_mmvq(const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                              void* stream) {

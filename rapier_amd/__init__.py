@@ -40,6 +40,9 @@ SIGNATURES = {
     "rmi_native_q5_k_mmvq_res": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
     "rmi_q6_k_packed_bytes": (_sz, [_i, _i]),
     "rmi_q6_k_pack": (_i, [_vp, _vp, _i, _i, _vp]),
+    "rmi_native_q6_k_pack_copy": (_i, [_vp, _i, _i]),
+    "rmi_native_q6_k_unpack": (_i, [_vp]),
+    "rmi_native_q6_k_packed_copies": (_i, []),
     "rmi_q6_k_pack_swiglu": (_i, [_vp, _vp, _i, _i, _vp]),
     "rmi_native_q6_k_swiglu_packed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "rmi_rms_quant_apply_self": (_i, [_vp, _vp, _vp, _i, _f, _i, _vp]),
@@ -136,13 +139,16 @@ def last_error() -> str:
     return lib().rmi_last_error().decode()
 
 
-def _call(name, *args):
-    rc = getattr(lib(), name)(*args)
+def _check(rc):
     if rc != RMI_OK:
         msg = last_error()
         if rc in (RMI_ERR_SHAPE, RMI_ERR_POINTER, RMI_ERR_STREAM, RMI_ERR_UNSUPPORTED):
             raise ValueError(msg)
         raise RapierError(msg)
+
+
+def _call(name, *args):
+    _check(getattr(lib(), name)(*args))
 
 
 def _p(t):
@@ -206,6 +212,25 @@ def q6_k_packed_bytes(n_in: int, n_out: int) -> int:
 
 def q6_k_pack(w, w_packed, n_in: int, n_out: int, stream=None):
     _call("rmi_q6_k_pack", _p(w), _p(w_packed), n_in, n_out, _stream(stream))
+
+
+def native_q6_k_pack(w, n_in: int, n_out: int) -> bool:
+    """native_q6_k_pack (mmvq:2930-2960): a library-owned packed copy of the GGUF-layout matrix ``w`` that
+    native_q6_k_mmvq / _res / _res_n then run on (the same bits); False where the packed layout does not take the
+    shape, as the reference returns false."""
+    rc = lib().rmi_native_q6_k_pack_copy(_p(w), n_in, n_out)
+    if rc == RMI_ERR_UNSUPPORTED:
+        return False
+    _check(rc)
+    return True
+
+
+def native_q6_k_unpack(w):
+    _call("rmi_native_q6_k_unpack", _p(w))
+
+
+def native_q6_k_packed_copies() -> int:
+    return int(lib().rmi_native_q6_k_packed_copies())
 
 
 def q6_k_pack_swiglu(w, w_packed, n_in: int, n_ff: int, stream=None):

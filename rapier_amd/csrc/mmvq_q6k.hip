@@ -561,6 +561,8 @@ using namespace rmi;
 extern "C" int rmi_native_q6_k_mmvq(const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                                     void* stream) {
     if (int rc = validate(w, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
+    // a library-owned packed copy of these weights first, as the reference looks up its registry (mmvq:3629)
+    if (const int rc = registry_mmvq(w, x_q8_1, y, nullptr, nullptr, n_in, n_out, ncols, stream); rc >= 0) return rc;
     return launch<false>(w, x_q8_1, y, nullptr, nullptr, n_in, n_out, ncols, static_cast<hipStream_t>(stream));
 }
 
@@ -569,6 +571,7 @@ extern "C" int rmi_native_q6_k_mmvq_res_n(const void* w, const void* x_q8_1, flo
     if (int rc = validate(w, x_q8_1, y, n_in, n_out, ncols, stream)) return rc;
     if (!aligned4(res) || !aligned4(partials))
         return fail(RMI_ERR_POINTER, "native MMVQ requires non-null 4-byte aligned device pointers");
+    if (const int rc = registry_mmvq(w, x_q8_1, y, res, partials, n_in, n_out, ncols, stream); rc >= 0) return rc;
     return launch<true>(w, x_q8_1, y, res, partials, n_in, n_out, ncols, static_cast<hipStream_t>(stream));
 }
 

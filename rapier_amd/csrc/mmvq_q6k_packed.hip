@@ -30,8 +30,11 @@
 #include "rmi_common.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
+#include <mutex>
 #include <string>
+#include <unordered_map>
 
 namespace rmi {
 namespace {
@@ -1811,4 +1814,86 @@ extern "C" int rmi_native_q6_k_mmvq_packed_res_n(const void* w_packed, const voi
     if (!aligned4(res) || !aligned4(partials))
         return fail(RMI_ERR_POINTER, "native MMVQ requires non-null 4-byte aligned device pointers");
     return run_packed<true>(w_packed, x_q8_1, y, res, partials, n_in, n_out, ncols, static_cast<hipStream_t>(stream));
+}
+
+// ---- packed copies owned by the library, behind the drop-in entry points -----------------------------------------------
+// The reference keeps an opt-in registry of re-laid Q6_K copies keyed by the GGUF weight pointer (native_q6_k_pack,
+// mmvq:2930-2960; native_q6_k_mmvq looks it up first, mmvq:2752-2770 and 3629; native_q6_k_unpack frees, mmvq:3042-3048).
+// Here the copy is the packed wave-tile layout, and rmi_native_q6_k_mmvq / _res / _res_n run the packed kernels on it:
+// the same bits as the GGUF-layout kernels (every kernel of both layouts gives the 16-row tiled kernel's results).
+namespace rmi {
+namespace {
+struct PackedCopy {
+    void* packed;
+    int n_in, n_out;
+};
+std::mutex g_reg_mu;
+std::unordered_map<const void*, PackedCopy> g_reg;
+std::atomic<int> g_reg_size{0};   // an empty registry costs the hot path one relaxed load
+}  // namespace
+
+int registry_mmvq(const void* w, const void* x_q8_1, float* y, const float* res, float* partials, int n_in, int n_out,
+                  int ncols, void* stream) {
+    if (g_reg_size.load(std::memory_order_relaxed) == 0) return -1;
+    void* packed = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_reg_mu);
+        const auto it = g_reg.find(w);
+        if (it == g_reg.end() || it->second.n_in != n_in || it->second.n_out != n_out) return -1;
+        packed = it->second.packed;
+    }
+    const auto s = static_cast<hipStream_t>(stream);
+    return res ? run_packed<true>(packed, x_q8_1, y, res, partials, n_in, n_out, ncols, s)
+               : run_packed<false>(packed, x_q8_1, y, nullptr, nullptr, n_in, n_out, ncols, s);
+}
+}  // namespace rmi
+
+extern "C" int rmi_native_q6_k_pack_copy(const void* w, int n_in, int n_out) {
+    if (n_in <= 0 || n_in % kChunkElems != 0 || n_out <= 0)
+        return fail(RMI_ERR_UNSUPPORTED, "native_q6_k_pack: n_in must be a positive multiple of 2048 and n_out positive");
+    if (!aligned4(w)) return fail(RMI_ERR_POINTER, "native_q6_k_pack: null or misaligned weights");
+    std::lock_guard<std::mutex> lock(g_reg_mu);
+    const auto it = g_reg.find(w);
+    if (it != g_reg.end()) {
+        if (it->second.n_in == n_in && it->second.n_out == n_out) return RMI_OK;   // packed already
+        return fail(RMI_ERR_STATE, "native_q6_k_pack: these weights are packed with another shape");
+    }
+    // as the reference's copy (synchronous, the caller's weights complete): every stream of the device drains first
+    if (hipDeviceSynchronize() != hipSuccess) return fail(RMI_ERR_LAUNCH, "native_q6_k_pack: device synchronize failed");
+    void* packed = nullptr;
+    if (hipMalloc(&packed, rmi_q6_k_packed_bytes(n_in, n_out)) != hipSuccess) {
+        (void) hipGetLastError();
+        return fail(RMI_ERR_LAUNCH, "native_q6_k_pack: out of device memory for the packed copy");
+    }
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+        (void) hipFree(packed);
+        return fail(RMI_ERR_LAUNCH, "native_q6_k_pack: cannot create a stream");
+    }
+    int rc = pack(w, packed, n_in, n_out, 0, s);
+    if (rc == RMI_OK && hipStreamSynchronize(s) != hipSuccess) rc = fail(RMI_ERR_LAUNCH, "native_q6_k_pack: pack failed");
+    (void) hipStreamDestroy(s);
+    if (rc != RMI_OK) {
+        (void) hipFree(packed);
+        return rc;
+    }
+    g_reg.emplace(w, PackedCopy{packed, n_in, n_out});
+    g_reg_size.store(static_cast<int>(g_reg.size()), std::memory_order_relaxed);
+    return RMI_OK;
+}
+
+extern "C" int rmi_native_q6_k_unpack(const void* w) {
+    std::lock_guard<std::mutex> lock(g_reg_mu);
+    const auto it = g_reg.find(w);
+    if (it == g_reg.end()) return RMI_OK;
+    // the copy may still be read by launches in flight on any stream
+    if (hipDeviceSynchronize() != hipSuccess) return fail(RMI_ERR_LAUNCH, "native_q6_k_unpack: device synchronize failed");
+    (void) hipFree(it->second.packed);
+    g_reg.erase(it);
+    g_reg_size.store(static_cast<int>(g_reg.size()), std::memory_order_relaxed);
+    return RMI_OK;
+}
+
+extern "C" int rmi_native_q6_k_packed_copies(void) {
+    return g_reg_size.load(std::memory_order_relaxed);
 }

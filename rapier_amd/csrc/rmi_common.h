@@ -167,6 +167,11 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amd
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
+// The drop-in entry points' packed copy (rmi_native_q6_k_pack_copy): runs the packed GEMV (res null: plain) when w has
+// a registered copy of this shape, else returns -1 and launches nothing
+int registry_mmvq(const void* w, const void* x_q8_1, float* y, const float* res, float* partials, int n_in, int n_out,
+                  int ncols, void* stream);
+
 // GGUF-layout stream GEMV (mmvq_q6k_packed.hip) for the drop-in entry points: returns -1, launching nothing, for shapes
 // it does not take (rows other than 4096 / 8192 / 12288 elements, more than four columns, a matrix not 16-byte aligned)
 int gguf_stream_gemv(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in,

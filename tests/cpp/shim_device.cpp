@@ -147,6 +147,18 @@ int main(int argc, char** argv) {
         check(part_ok, "native_q6_k_mmvq_res partials == 4-row sums of y^2 (1e-6 rel)");
     }
 
+    // the registry-owned packed copy (native_q6_k_pack, mmvq:2930-2960): the same entry points, the same bits
+    {
+        const bool packed = sk::native_q6_k_pack(w.p, n_in, n_out, "test matrix");
+        Buf yp(2 * col_y), yrp(res.host()), partp((n_out / 4) * sizeof(float));
+        sk::native_q6_k_mmvq(w.p, xq.p, yp.f(), n_in, n_out, 2, st);
+        sk::native_q6_k_mmvq_res(w.p, xq.p, yrp.f(), yrp.f(), partp.f(), n_in, n_out, st);
+        sk::native_q6_k_unpack(w.p);
+        check(packed && same(yp.host(), y2_h, 0, 0, 2 * col_y) && same(yrp.host(), yr_h, 0, 0, col_y) &&
+                  same(partp.host(), part_h, 0, 0, (n_out / 4) * sizeof(float)),
+              "native_q6_k_pack: native_q6_k_mmvq / _res on the packed copy == the GGUF-layout results (bitwise)");
+    }
+
     Buf y8(col_y);
     sk::native_q8_0_mmvq(w8.p, xq.p, y8.f(), n_in, n_out, 1, st);
     const auto y8_h = y8.host();

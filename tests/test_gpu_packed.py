@@ -319,3 +319,54 @@ def test_engine_gemvs_integer_exact(orc, rmi, n_in, n_out, ncols):
     part = empty(ncols * ((n_out + 3) // 4))
     rmi.native_q6_k_mmvq_packed_res_n(wp, xd, yr, yr, part, n_in, n_out, ncols)
     assert np.array_equal(host(yr), want + res), "packed residual"
+
+
+@pytest.mark.parametrize("n_in,n_out", [(4096, 24576), (12288, 4096), (4096, 1001)])
+@pytest.mark.parametrize("ncols", [1, 2, 5])
+def test_registry_copy_behind_drop_in_entry_points(orc, rmi, n_in, n_out, ncols):
+    """native_q6_k_pack's library-owned copy (mmvq:2930-2960, looked up by native_q6_k_mmvq at mmvq:3629): once the
+    GGUF matrix is packed, rmi_native_q6_k_mmvq / _res_n on the same pointer and shape give bitwise the results of
+    the GGUF-layout kernels; another shape on the same pointer keeps the GGUF kernels; unpack frees the copy"""
+    w = orc.gen_q6k(n_out, n_in, seed=n_in + 7 * n_out + ncols)
+    x = orc.normal(ncols * n_in, seed=n_out + 5)
+    xq = orc.quantize_q8_1(x, n_in, ncols)
+    r = orc.normal(ncols * n_out, seed=n_out + 6)
+    wd, xd = dev(w), dev(xq)
+    npart = ncols * ((n_out + 3) // 4)
+
+    def run():
+        y = empty(ncols * n_out)
+        rmi.native_q6_k_mmvq(wd, xd, y, n_in, n_out, ncols)
+        yr, pr = dev(r), empty(npart)
+        rmi.native_q6_k_mmvq_res_n(wd, xd, yr, yr, pr, n_in, n_out, ncols)
+        return host(y), host(yr), host(pr)
+
+    base = run()
+    n0 = rmi.native_q6_k_packed_copies()
+    assert rmi.native_q6_k_pack(wd, n_in, n_out)
+    assert rmi.native_q6_k_pack(wd, n_in, n_out)          # packed already: no second copy
+    assert rmi.native_q6_k_packed_copies() == n0 + 1
+    got = run()
+    for a, b in zip(base, got):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # the copy is keyed by pointer and shape: the first rows of the same matrix still run (on the GGUF kernels)
+    rows = max(1, n_out // 2)
+    y0, y1 = empty(rows), empty(rows)
+    rmi.native_q6_k_mmvq(wd, xd, y1, n_in, rows, 1)
+    rmi.native_q6_k_unpack(wd)
+    assert rmi.native_q6_k_packed_copies() == n0
+    rmi.native_q6_k_mmvq(wd, xd, y0, n_in, rows, 1)
+    assert np.array_equal(host(y0).view(np.uint32), host(y1).view(np.uint32))
+    got = run()                                            # after unpack: the GGUF kernels again, same bits
+    for a, b in zip(base, got):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    rmi.native_q6_k_unpack(wd)                             # no copy: a no-op
+
+
+def test_registry_copy_shapes_it_does_not_take(orc, rmi):
+    """n_in not a multiple of 2048: native_q6_k_pack returns False, as the reference does for shapes its packed kernel
+    does not take, and the drop-in entry point keeps the GGUF kernels"""
+    w = dev(orc.gen_q6k(64, 1024, seed=11))
+    n0 = rmi.native_q6_k_packed_copies()
+    assert not rmi.native_q6_k_pack(w, 1024, 64)
+    assert rmi.native_q6_k_packed_copies() == n0

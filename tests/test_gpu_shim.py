@@ -62,7 +62,7 @@ def test_shim_device_program(orc, tmp_path):
     r = subprocess.run([BIN, d], capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr, flush=True)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert r.stdout.count("PASS") == 7 and "FAIL" not in r.stdout
+    assert r.stdout.count("PASS") == 8 and "FAIL" not in r.stdout
 
     xq = orc.quantize_q8_1(x, N_IN, 2)
     assert np.array_equal(got(d, "xq", np.uint8), xq), "Q8_1 bytes"
