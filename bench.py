@@ -536,7 +536,7 @@ def time_attention(stream, ctx):
     max_ctx = ctx + 512
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     chunks = max(1, cus // n_kv)
-    nsub = max(2, min(16, -(-max_ctx // (64 * chunks))))
+    nsub = max(2, min(64, -(-max_ctx // (64 * chunks))))
     row = n_kv * hd
     nrot = max(2, -(-400_000_000 // (2 * max_ctx * row * 2)))
     kv = torch.empty(nrot, 2, max_ctx * row, dtype=torch.float16, device="cuda")
