@@ -108,8 +108,9 @@ int rmi_native_q6_k_mmvq_packed_norm(const void* w_packed, const float* x, const
 int rmi_native_q6_k_swiglu_packed_norm(const void* w_packed, const float* x, const float* w_norm,
                                        const float* partials, float eps, void* y_q8_1, int n_in, int n_ff, int ncols,
                                        void* stream);
-/* 1 where rmi_native_q6_k_mmvq_packed_norm is measured faster than the two launches it replaces (its one workgroup per
- * 16 row quads must cover at least 3/4 of the CUs), else 0 (also for shapes it does not take). */
+/* 1 where rmi_native_q6_k_mmvq_packed_norm is measured faster than the two launches it replaces (its 8-wave workgroups
+ * of 16 row quads cover at least 3/4 of the CUs, or 4-wave workgroups of up to 4 quads per wave can), else 0 (also for
+ * shapes it does not take). */
 int rmi_q6_k_packed_norm_preferred(int n_in, int n_out, int ncols);
 int rmi_native_q6_k_mmvq_packed(const void* w_packed, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                                 void* stream);

@@ -1738,12 +1738,21 @@ int swiglu_packed(const void* w_packed, const void* x_q8_1, void* y_q8_1, int n_
 }
 
 // the normed-input packed GEMV: rows of 4096, one or two columns, one 8-wave workgroup per 8 QPW quads
-template <int NCOLS, int QPW>
+template <int NCOLS, int QPW, int NW = 8>
 void launch_norm_gemv(const uint8_t* wp, float* y, int n_out, const NormIn& ni, hipStream_t s) {
     const int nq = (n_out + kQuad - 1) / kQuad;
-    hipLaunchKernelGGL((q6k_packed_gemv_stream<NCOLS, false, 2, QPW, 8, 2, true>), dim3((nq + 8 * QPW - 1) / (8 * QPW)),
-                       dim3(512), static_cast<size_t>(NCOLS) * (2 * kChunkElems / 32) * 48, s, wp, nullptr, y, nullptr,
-                       nullptr, 2 * kChunkElems, n_out, ni);
+    hipLaunchKernelGGL((q6k_packed_gemv_stream<NCOLS, false, 2, QPW, NW, 2, true>), dim3((nq + NW * QPW - 1) / (NW * QPW)),
+                       dim3(64 * NW), static_cast<size_t>(NCOLS) * (2 * kChunkElems / 32) * 48, s, wp, nullptr, y,
+                       nullptr, nullptr, 2 * kChunkElems, n_out, ni);
+}
+
+// 4-wave workgroups for the normed GEMV where 8-wave ones would leave a quarter of the CUs idle (the attention qkv,
+// 10240 rows: 214 workgroups of 3 quads per wave instead of 160 of 2); RMI_NORM_NW4=0 keeps the 8-wave form
+bool norm_nw4(int nq) {
+    static const bool on = env_int("RMI_NORM_NW4", 1) != 0;
+    const int qpw8 = (nq + 8 * cu_count() - 1) / (8 * cu_count());
+    const int wgs8 = (nq + 8 * qpw8 - 1) / (8 * qpw8);
+    return on && 4 * wgs8 < 3 * cu_count() && (nq + 4 * cu_count() - 1) / (4 * cu_count()) <= 4;
 }
 
 }  // namespace
@@ -1777,7 +1786,7 @@ extern "C" int rmi_q6_k_packed_norm_preferred(int n_in, int n_out, int ncols) {
     if (n_in != 2 * kChunkElems || ncols < 1 || ncols > 2 || n_out <= 0 || n_out > 4 * 8 * 4 * 256) return 0;
     const int nq = (n_out + kQuad - 1) / kQuad, qpw = (nq + 8 * cu_count() - 1) / (8 * cu_count());
     const int wgs = (nq + 8 * qpw - 1) / (8 * qpw);
-    return 4 * wgs >= 3 * cu_count() ? 1 : 0;
+    return 4 * wgs >= 3 * cu_count() || norm_nw4(nq) ? 1 : 0;
 }
 
 extern "C" int rmi_native_q6_k_mmvq_packed_norm(const void* w_packed, const float* x, const float* w_norm,
@@ -1794,6 +1803,14 @@ extern "C" int rmi_native_q6_k_mmvq_packed_norm(const void* w_packed, const floa
     // quads per wave: every quad's wave resident at once on the CUs' 8-wave workgroups (one per CU up to 2048 quads)
     const int nq = (n_out + kQuad - 1) / kQuad, qpw = (nq + 8 * cu_count() - 1) / (8 * cu_count());
     auto go = [&](auto one, auto two) { ncols == 1 ? one() : two(); };
+    if (norm_nw4(nq)) {
+        const int q4 = (nq + 4 * cu_count() - 1) / (4 * cu_count());
+        if (q4 <= 1) go([&] { launch_norm_gemv<1, 1, 4>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 1, 4>(wp, y, n_out, ni, s); });
+        else if (q4 == 2) go([&] { launch_norm_gemv<1, 2, 4>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 2, 4>(wp, y, n_out, ni, s); });
+        else if (q4 == 3) go([&] { launch_norm_gemv<1, 3, 4>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 3, 4>(wp, y, n_out, ni, s); });
+        else go([&] { launch_norm_gemv<1, 4, 4>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 4, 4>(wp, y, n_out, ni, s); });
+        return launch_status("q6_k_mmvq_packed_norm");
+    }
     if (qpw <= 1) go([&] { launch_norm_gemv<1, 1>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 1>(wp, y, n_out, ni, s); });
     else if (qpw == 2) go([&] { launch_norm_gemv<1, 2>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 2>(wp, y, n_out, ni, s); });
     else if (qpw == 3) go([&] { launch_norm_gemv<1, 3>(wp, y, n_out, ni, s); }, [&] { launch_norm_gemv<2, 3>(wp, y, n_out, ni, s); });
