@@ -7,9 +7,10 @@
 //
 // Two launches.  topk_lists: one wave per 64*E consecutive logits; each lane sorts its E keys in registers (a bitonic
 // network, compile-time indices), then k rounds of a wave max over the lanes' heads pop the wave's k largest into a
-// sorted list.  topk_merge: one 512-lane workgroup, lane t owns list t; k rounds of a workgroup max over the heads (a
-// DPP wave max, one LDS exchange and one barrier per round) pop the global k largest.  The winning lane refills its
-// head from a four-entry register cache, which it tops up from its list with a load that has four pops to land.
+// sorted list (one key per lane, 0 past k); the four waves of a workgroup then merge their lists into one.
+// topk_merge: one 512-lane workgroup merges the workgroups' lists pairwise, level by level, in LDS.  Two sorted lists
+// merge in one wave: lane l takes max(A[l], B[63 - l]), the top half of the bitonic sequence A | reverse(B), i.e. the
+// 64 largest keys of both, and a bitonic half-cleaner network (lane strides 32 .. 1) sorts them.
 #include "rmi_common.h"
 
 namespace rmi {
@@ -17,7 +18,8 @@ namespace {
 
 constexpr int kTopkMax = 64;       // largest k
 constexpr int kListStride = 64;    // keys per list in the workspace
-constexpr int kMergeLanes = 512;   // lists the merge workgroup can own
+constexpr int kMergeLanes = 512;   // waves of the list pass at most (4 per workgroup list)
+constexpr int kMaxLists = kMergeLanes / 4;   // workgroup lists the merge holds in LDS (64 KB)
 
 __device__ __forceinline__ uint64_t topk_key(float v, uint32_t idx) {
     uint32_t b = __float_as_uint(v);
@@ -55,17 +57,47 @@ __device__ __forceinline__ uint64_t wave_max64(uint64_t k) {
     return max64(max64(readlane64(k, 0), readlane64(k, 16)), max64(readlane64(k, 32), readlane64(k, 48)));
 }
 
+// key of lane l ^ K (the VALU lane exchange of rmi_common.h on both halves)
+template <int K>
+__device__ __forceinline__ uint64_t xor64(uint64_t v) {
+    const uint32_t lo = xor_lane<K>(static_cast<uint32_t>(v)), hi = xor_lane<K>(static_cast<uint32_t>(v >> 32));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+template <int K>
+__device__ __forceinline__ uint64_t half_clean(uint64_t v, int lane) {
+    const uint64_t o = xor64<K>(v);
+    return (lane & K) ? (v < o ? v : o) : (v > o ? v : o);
+}
+
+// The 64 largest keys of two descending lists, descending, one per lane: a = A[lane], b = B[63 - lane].  Called with
+// every lane of the wave active.
+__device__ __forceinline__ uint64_t merge_lists(uint64_t a, uint64_t b) {
+    const int lane = __lane_id();
+    uint64_t v = a > b ? a : b;
+    v = half_clean<32>(v, lane);
+    v = half_clean<16>(v, lane);
+    v = half_clean<8>(v, lane);
+    v = half_clean<4>(v, lane);
+    v = half_clean<2>(v, lane);
+    return half_clean<1>(v, lane);
+}
+
 template <int E>
 __global__ __launch_bounds__(256) void topk_lists_kernel(const float* __restrict__ x, int n, int k,
                                                          uint64_t* __restrict__ lists) {
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int64_t base = static_cast<int64_t>(wave) * 64 * E;
+    // every load issued before the first use, from clamped indices (a load under a branch gets a wait of its own)
+    float xv[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) xv[j] = x[min(base + lane + 64 * j, static_cast<int64_t>(n) - 1)];
     uint64_t v[E];
 #pragma unroll
     for (int j = 0; j < E; ++j) {
         const int64_t i = base + lane + 64 * j;
-        v[j] = i < n ? topk_key(x[i], static_cast<uint32_t>(i)) : 0ull;
+        v[j] = i < n ? topk_key(xv[j], static_cast<uint32_t>(i)) : 0ull;
     }
     // bitonic sort of the lane's E keys, descending
 #pragma unroll
@@ -95,43 +127,61 @@ __global__ __launch_bounds__(256) void topk_lists_kernel(const float* __restrict
             v[E - 1] = 0;
         }
     }
-    if (lane < k) lists[static_cast<size_t>(wave) * kListStride + lane] = mine;
+    // the workgroup's four lists into one: waves 0 / 1 merge lists (0, 1) / (2, 3), then wave 0 merges the two
+    __shared__ uint64_t wl[4][64];
+    const int w = threadIdx.x >> 6;
+    wl[w][lane] = mine;
+    __syncthreads();
+    uint64_t m2 = 0;
+    if (w < 2) m2 = merge_lists(wl[2 * w][lane], wl[2 * w + 1][63 - lane]);
+    __syncthreads();
+    if (w < 2) wl[w][lane] = m2;
+    __syncthreads();
+    if (w == 0) lists[static_cast<size_t>(blockIdx.x) * kListStride + lane] = merge_lists(wl[0][lane], wl[1][63 - lane]);
 }
 
+// Workgroup lists merged pairwise: each level reads every pair into registers (wave w takes pairs w, w + 8, ...), passes
+// a barrier, and writes the merged lists to the first half of the slots; an odd last list moves down with them.
 __global__ __launch_bounds__(kMergeLanes) void topk_merge_kernel(const float* __restrict__ x,
                                                                  const uint64_t* __restrict__ lists, int nlists, int k,
                                                                  int* __restrict__ out_idx, float* __restrict__ out_val) {
-    __shared__ uint64_t wmax[2][kMergeLanes / 64];
-    __shared__ uint64_t picked[kTopkMax];
+    __shared__ uint64_t buf[kMaxLists * kListStride];
+    constexpr int kWaves = kMergeLanes / 64;
+    constexpr int kPer = kMaxLists / 2 / kWaves;   // pairs per wave at the widest level
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const uint64_t* list = lists + static_cast<size_t>(t) * kListStride;
-    const bool own = t < nlists;
-    uint64_t h = own ? list[0] : 0;
-    uint64_t c0 = own && k > 1 ? list[1] : 0, c1 = own && k > 2 ? list[2] : 0;
-    uint64_t c2 = own && k > 3 ? list[3] : 0, c3 = own && k > 4 ? list[4] : 0;
-    int next = 5;
-    for (int it = 0; it < k; ++it) {
-        // the two LDS rows alternate: a row is rewritten two rounds later, after every lane has passed the barrier of
-        // the round in between, i.e. after every lane has read it
-        const uint64_t m = wave_max64(h);
-        if (lane == 0) wmax[it & 1][w] = m;
-        __syncthreads();
-        uint64_t g = wmax[it & 1][0];
+    {   // every list entry of the lane loaded before the first store (a strided loop waits on each load in turn)
+        constexpr int kLoads = kMaxLists * kListStride / kMergeLanes;
+        const int total = nlists * kListStride;
+        uint64_t lv[kLoads];
 #pragma unroll
-        for (int i = 1; i < kMergeLanes / 64; ++i) g = wmax[it & 1][i] > g ? wmax[it & 1][i] : g;
-        if (t == 0) picked[it] = g;
-        if (g != 0 && h == g) {         // only an owned list holds a nonzero key
-            h = c0;
-            c0 = c1;
-            c1 = c2;
-            c2 = c3;
-            c3 = next < k ? list[next] : 0;
-            ++next;
-        }
+        for (int r = 0; r < kLoads; ++r) lv[r] = lists[min(t + kMergeLanes * r, total - 1)];
+#pragma unroll
+        for (int r = 0; r < kLoads; ++r)
+            if (t + kMergeLanes * r < total) buf[t + kMergeLanes * r] = lv[r];
     }
     __syncthreads();
+    for (int n = nlists; n > 1;) {
+        const int pairs = n >> 1;
+        uint64_t res[kPer], last = 0;
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) {
+            const int p = w + kWaves * r;
+            res[r] = p < pairs ? merge_lists(buf[(2 * p) * kListStride + lane], buf[(2 * p + 1) * kListStride + 63 - lane])
+                               : 0;
+        }
+        if ((n & 1) && w == 0) last = buf[(n - 1) * kListStride + lane];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) {
+            const int p = w + kWaves * r;
+            if (p < pairs) buf[p * kListStride + lane] = res[r];
+        }
+        if ((n & 1) && w == 0) buf[pairs * kListStride + lane] = last;
+        __syncthreads();
+        n = pairs + (n & 1);
+    }
     if (t < k) {
-        const uint64_t key = picked[t];
+        const uint64_t key = buf[t];
         const int idx = key ? static_cast<int>(0xffffffffu - static_cast<uint32_t>(key)) : -1;
         out_idx[t] = idx;
         out_val[t] = idx >= 0 ? x[idx] : 0.0f;
@@ -176,7 +226,6 @@ extern "C" int rmi_topk(const float* logits, int n, int k, int* out_idx, float* 
     else hipLaunchKernelGGL(topk_lists_kernel<32>, dim3(blocks), dim3(256), 0, s, logits, n, k, lists);
     const int rc = launch_status("topk_lists");
     if (rc != RMI_OK) return rc;
-    hipLaunchKernelGGL(topk_merge_kernel, dim3(1), dim3(kMergeLanes), 0, s, logits, lists, blocks * 4, k, out_idx,
-                       out_val);
+    hipLaunchKernelGGL(topk_merge_kernel, dim3(1), dim3(kMergeLanes), 0, s, logits, lists, blocks, k, out_idx, out_val);
     return launch_status("topk_merge");
 }
