@@ -444,10 +444,13 @@ __global__ __launch_bounds__(S * RG) void gdn_step_kernel(StepArgs a) {
 // 8-byte words (agent scope: value and tag land together) and reads the other parts' words.  The epoch is the number
 // of launches the head's parts have completed: every launch writes every part's words with the next one, so at the
 // start of a launch all four parts' words carry the same tag, and a part reads it from its own word (which only it
-// writes), waits for the other parts' words to carry tag + 1, and needs no reset.  Workgroups are dispatched in order
-// and the four parts of a head are neighbours, so every wait ends (it is bounded all the same:
-// gdn_exchange_timeouts).  The words live in a caller-owned buffer (rmi_gdn_exchange_bytes), zeroed once and used
-// by one stream at a time: launches that overlap on one buffer race.
+// writes), waits for the other parts' words to carry tag + 1, and needs no reset.  The grid is part-major (workgroup
+// part * h_v + head): workgroups go to the XCDs round robin, so with h_v a multiple of 8 the four parts of a head run
+// on one XCD (with h_k one too, the heads that share its k-head, head % h_k: h and h + 16 at the 9B shapes) and read
+// the head's q / k rows, conv taps and history through one L2 (a head-major grid put the parts on four XCDs: 7.28 ->
+// 6.70 us per 2-token layer).  Every workgroup of the grid is resident at once (h_v * 4 workgroups of 128 lanes), so
+// every wait ends (it is bounded all the same: gdn_exchange_timeouts).  The words live in a caller-owned buffer
+// (rmi_gdn_exchange_bytes), zeroed once and used by one stream at a time: launches that overlap on one buffer race.
 constexpr int kParts = 4;
 constexpr int kPartCols = S / kParts;   // 32
 constexpr int kPartLanes = kPartCols * RG;   // 128
@@ -468,7 +471,7 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
     __shared__ float wsum[NT][2];       // this part's two wave sums
     __shared__ float allw[NT][S * RG / 64];   // the head's eight wave sums, in wave order
     __shared__ float ybuf[NT][kPartCols];
-    const int head = static_cast<int>(blockIdx.x) / kParts, part = static_cast<int>(blockIdx.x) % kParts;
+    const int head = static_cast<int>(blockIdx.x) % a.h_v, part = static_cast<int>(blockIdx.x) / a.h_v;
     const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
     const int lcol = 16 * wv + (ln & 15);
     const int col = kPartCols * part + lcol;
