@@ -318,6 +318,18 @@ int rmi_gqa_flash_decode_prep(const float* q3, int q3_stride, const float* qn, c
                               void* workspace, int n_head, int n_kv, int head_dim, int n_rot,
                               const rmi_rope_params* rope, float eps, int ntok, int max_ctx, int nsub, float scale,
                               void* stream);
+/* rmi_gqa_flash_decode_prep with a table of the rotation's (cos, sin), for the attention layers of one forward pass,
+ * which all rotate at the same positions.  No counterpart in the reference (the engine's form of the call above).
+ * rope_table holds rmi_gqa_rope_table_bytes(n_rot) bytes, 8-byte aligned: [2 tokens][n_rot / 2 pairs] (cos, sin) at
+ * positions pos[0] + t.  table_mode 0: the launch computes its rotation (rmi_gqa_flash_decode_prep); 1: it also
+ * stores the table; 2: it loads the table instead of computing it (the pass's later layers, with the same pos and
+ * ntok as the mode-1 launch before them on the stream).  Every mode gives the bits of rmi_gqa_flash_decode_prep. */
+size_t rmi_gqa_rope_table_bytes(int n_rot);
+int rmi_gqa_flash_decode_prep_rt(const float* q3, int q3_stride, const float* qn, const float* kn, uint16_t* kcache,
+                                 uint16_t* vcache, const int* pos, float* y, int y_stride, uint8_t* q8, int q8_stride,
+                                 void* workspace, int n_head, int n_kv, int head_dim, int n_rot,
+                                 const rmi_rope_params* rope, float eps, int ntok, int max_ctx, int nsub, float scale,
+                                 float* rope_table, int table_mode, void* stream);
 
 /* rmi_gqa_flash_decode without the workspace argument, for callers that cannot allocate (code under HIP graph
  * capture, serving loops that forbid hipMalloc).  No counterpart in the reference.  The split-K records go to the

@@ -87,6 +87,9 @@ SIGNATURES = {
     "rmi_attn_prep_rope": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _f, _i, _i, _vp]),
     "rmi_gqa_flash_decode_prep": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp,
                                        _f, _i, _i, _i, _f, _vp]),
+    "rmi_gqa_rope_table_bytes": (ctypes.c_size_t, [_i]),
+    "rmi_gqa_flash_decode_prep_rt": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i,
+                                          _vp, _f, _i, _i, _i, _f, _vp, _i, _vp]),
     "rmi_rms_norm_weighted": (_i, [_vp, _vp, _i, _i, _f, _vp]),
     "rmi_native_rope_apply": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "rmi_add_inplace": (_i, [_vp, _vp, _i, _vp]),
@@ -453,6 +456,21 @@ def gqa_flash_decode_prep(q3, q3_stride, qn, kn, kcache, vcache, pos, y, y_strid
     _call("rmi_gqa_flash_decode_prep", _p(q3), q3_stride, _p(qn), _p(kn), _p(kcache), _p(vcache), _p(pos), _p(y),
           y_stride, _p(q8), q8_stride, _p(workspace), n_head, n_kv, head_dim, n_rot, ctypes.byref(rope), eps, ntok,
           max_ctx, nsub, scale, _stream(stream))
+
+
+def gqa_rope_table_bytes(n_rot: int) -> int:
+    return lib().rmi_gqa_rope_table_bytes(n_rot)
+
+
+def gqa_flash_decode_prep_rt(q3, q3_stride, qn, kn, kcache, vcache, pos, y, y_stride, q8, q8_stride, workspace,
+                             n_head, n_kv, head_dim, n_rot, freq_base, factor, orig_ctx, eps, ntok, max_ctx, nsub,
+                             scale, rope_table, table_mode, ext_factor=1.0, attn_factor=1.0, beta_fast=32.0,
+                             beta_slow=1.0, stream=None):
+    """gqa_flash_decode_prep with the forward pass's RoPE table (table_mode 0 compute, 1 compute and store, 2 load)"""
+    rope = RopeParams(freq_base, factor, orig_ctx, ext_factor, attn_factor, beta_fast, beta_slow)
+    _call("rmi_gqa_flash_decode_prep_rt", _p(q3), q3_stride, _p(qn), _p(kn), _p(kcache), _p(vcache), _p(pos), _p(y),
+          y_stride, _p(q8), q8_stride, _p(workspace), n_head, n_kv, head_dim, n_rot, ctypes.byref(rope), eps, ntok,
+          max_ctx, nsub, scale, _p(rope_table), table_mode, _stream(stream))
 
 
 def rms_norm_weighted(x, w, rows, cols, eps, stream=None):

@@ -161,7 +161,14 @@ struct PrepIn {
     int n_rot;
     float theta, eps;
     Yarn yarn;
+    // the rotation's (cos, sin) per token and pair, [2][n_rot / 2] float2 at positions pos[0] + t: kRopeOwn computes
+    // them (no table), kRopeWrite computes them and workgroup 0 stores them, kRopeRead loads them with the launch's
+    // first loads (every attention layer of one trunk pass rotates at the same positions: the first writes, the others
+    // read the same bits, and the fp64 angle and sincos leave their critical paths)
+    float2* cs;
+    int cs_mode;
 };
+constexpr int kRopeOwn = 0, kRopeWrite = 1, kRopeRead = 2;
 
 template <bool PREP>
 __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __restrict__ qbuf, const uint16_t* __restrict__ kc,
@@ -192,6 +199,7 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
     // PREP query rows: wave w holds slots 2 w and 2 w + 1, lane l dims l + 64 k (k = 0..3) of each
     float xq[PREP ? 2 : 1][4], wq4[4], xk[PREP ? 2 : 1], xv[PREP ? 2 : 1], wk = 0.0f;
     double freq = 0.0, qfreq = 0.0;
+    float2 kcs[2] = {make_float2(1.0f, 0.0f), make_float2(1.0f, 0.0f)}, qcs = make_float2(1.0f, 0.0f);   // kRopeRead
     if constexpr (PREP) {
         // raw rows, independent of the position: in flight together with pos
 #pragma unroll
@@ -210,10 +218,23 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
             xv[t] = src[n_kv * HD + kv * HD + d];
         }
         wk = pr.kn[d];
-        if (d < pr.n_rot) freq = rope_freq(d < pr.n_rot / 2 ? d : d - pr.n_rot / 2, pr.n_rot, pr.theta);
-        // the query rows' rotated dims: lane l of group 0 (n_rot = 64)
-        if (lane < pr.n_rot) qfreq = rope_freq(lane < pr.n_rot / 2 ? lane : lane - pr.n_rot / 2, pr.n_rot, pr.theta);
-        asm volatile("" : "+v"(freq), "+v"(qfreq));
+        {
+            // the table's entries, loaded unconditionally (a load under a branch gets a wait of its own, at the branch's
+            // end): from the table in kRopeRead, else from qn (any 2 n_rot floats of valid memory; the values go unused)
+            const int half = pr.n_rot / 2;
+            const int kp = min(d < half ? d : d - half, half - 1), qp = min(lane < half ? lane : lane - half, half - 1);
+            const int tq = min(s0 + 2 * wv, nq - 1) / G;
+            const float2* tab = pr.cs_mode == kRopeRead ? pr.cs : reinterpret_cast<const float2*>(pr.qn);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) kcs[t] = tab[min(t, ntok - 1) * half + kp];
+            qcs = tab[tq * half + qp];
+        }
+        if (pr.cs_mode != kRopeRead) {
+            if (d < pr.n_rot) freq = rope_freq(d < pr.n_rot / 2 ? d : d - pr.n_rot / 2, pr.n_rot, pr.theta);
+            // the query rows' rotated dims: lane l of group 0 (n_rot = 64)
+            if (lane < pr.n_rot) qfreq = rope_freq(lane < pr.n_rot / 2 ? lane : lane - pr.n_rot / 2, pr.n_rot, pr.theta);
+            asm volatile("" : "+v"(freq), "+v"(qfreq));
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -232,11 +253,17 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
     if (cbase > p_last || p0 < 0 || p_last >= max_ctx) return;   // uniform: no visible position (or a bad pos)
     // attn_prep's rotation of dim d (and d +- n_rot / 2) of a normed row staged in LDS (row) at position p (the angle
     // in fp64, as attn_prep)
-    auto rope_row = [&](const float* row, float v, int p) {
+    auto rope_row = [&](const float* row, float v, int p, int t) {
         if (d < pr.n_rot) {
             const int half = pr.n_rot / 2;
             float c, sn;
-            rope_cos_sin_f(p, freq, d < half ? d : d - half, pr.yarn, &c, &sn);
+            if (pr.cs_mode == kRopeRead) {
+                const float2 e = t == 0 ? kcs[0] : kcs[1];   // selected, not indexed (an indexed array goes to memory)
+                c = e.x;
+                sn = e.y;
+            } else {
+                rope_cos_sin_f(p, freq, d < half ? d : d - half, pr.yarn, &c, &sn);
+            }
             v = d < half ? rope_lo(row[d], row[d + half], c, sn) : rope_hi(row[d - half], row[d], c, sn);
         }
         return v;
@@ -264,7 +291,7 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
             __syncthreads();
             for (int t = tfirst; t < tlast; ++t) {
                 const int p = p0 + t;
-                const float kr = rope_row(krow + t * HD, kvn[t], p);
+                const float kr = rope_row(krow + t * HD, kvn[t], p, t);
                 pr.kc[(static_cast<size_t>(p) * n_kv + kv) * HD + d] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(kr));
                 pr.vc[(static_cast<size_t>(p) * n_kv + kv) * HD + d] =
                     __builtin_bit_cast(uint16_t, static_cast<_Float16>(t == 0 ? xv[0] : xv[1]));
@@ -316,7 +343,16 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
         float* qf = reinterpret_cast<float*>(tiles);   // [slot][HD]
         const int tq = min(s0 + 2 * wv, nq - 1) / G;    // both rows' token (G >= 2)
         float qc = 1.0f, qs = 0.0f;
-        if (lane < pr.n_rot) rope_cos_sin_f(p0 + tq, qfreq, lane < pr.n_rot / 2 ? lane : lane - pr.n_rot / 2, pr.yarn, &qc, &qs);
+        if (pr.cs_mode == kRopeRead) {
+            qc = qcs.x;
+            qs = qcs.y;
+        } else if (lane < pr.n_rot) {
+            rope_cos_sin_f(p0 + tq, qfreq, lane < pr.n_rot / 2 ? lane : lane - pr.n_rot / 2, pr.yarn, &qc, &qs);
+            // the table of the launches that follow: workgroup 0's waves, each its rows' token (tokens 0 and 1 from
+            // waves 0 and 2 at two tokens; equal values from the others)
+            if (pr.cs_mode == kRopeWrite && blockIdx.x == 0 && lane < pr.n_rot / 2)
+                pr.cs[tq * (pr.n_rot / 2) + lane] = make_float2(qc, qs);
+        }
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             // lane 0's butterfly result, as attn_prep takes it: with the square contracted into the first step's add
@@ -710,11 +746,13 @@ extern "C" int rmi_gqa_flash_decode(const float* q, const uint16_t* kcache, cons
                         static_cast<hipStream_t>(stream));
 }
 
-extern "C" int rmi_gqa_flash_decode_prep(const float* q3, int q3_stride, const float* qn, const float* kn,
-                                         uint16_t* kcache, uint16_t* vcache, const int* pos, float* y, int y_stride,
-                                         uint8_t* q8, int q8_stride, void* workspace, int n_head, int n_kv,
-                                         int head_dim, int n_rot, const rmi_rope_params* rope, float eps, int ntok,
-                                         int max_ctx, int nsub, float scale, void* stream) {
+namespace rmi {
+namespace {
+int flash_decode_prep(const float* q3, int q3_stride, const float* qn, const float* kn, uint16_t* kcache,
+                      uint16_t* vcache, const int* pos, float* y, int y_stride, uint8_t* q8, int q8_stride,
+                      void* workspace, int n_head, int n_kv, int head_dim, int n_rot, const rmi_rope_params* rope,
+                      float eps, int ntok, int max_ctx, int nsub, float scale, float* rope_cs, int cs_mode,
+                      void* stream) {
     if (head_dim != HD || n_head <= 0 || n_kv <= 0 || n_head % n_kv || ntok < 1 || ntok * (n_head / n_kv) > SLOTS ||
         max_ctx <= 0 || max_ctx % SUB || nsub <= 0 || n_rot != 64 || (n_head / n_kv) % 2 || !rope ||
         !(rope->freq_base > 1.0f))
@@ -727,7 +765,10 @@ extern "C" int rmi_gqa_flash_decode_prep(const float* q3, int q3_stride, const f
     if (nchunks > kMaxChunks) return fail(RMI_ERR_SHAPE, "gqa_flash_decode_prep: max_ctx / (64 * nsub) exceeds 2048 chunks");
     Yarn yarn{};
     if (!yarn_setup(*rope, n_rot, &yarn)) return fail(RMI_ERR_SHAPE, "gqa_flash_decode_prep: invalid YaRN parameters");
-    const PrepIn pr{q3, q3_stride, qn, kn, kcache, vcache, n_rot, rope->freq_base, eps, yarn};
+    if (cs_mode != kRopeOwn && (!rope_cs || (reinterpret_cast<uintptr_t>(rope_cs) & 7u) || cs_mode > kRopeRead))
+        return fail(RMI_ERR_POINTER, "gqa_flash_decode_prep: rope table mode 1 or 2 needs an 8-byte aligned table");
+    const PrepIn pr{q3,  q3_stride, qn,   kn, kcache, vcache, n_rot, rope->freq_base, eps, yarn,
+                    reinterpret_cast<float2*>(rope_cs), cs_mode};
     const auto s = static_cast<hipStream_t>(stream);
     auto* ws = static_cast<float*>(workspace);
     hipLaunchKernelGGL(gqa_partial_kernel<true>, dim3(nchunks * n_kv, 1, 1), dim3(256), 0, s, nullptr, kcache, vcache,
@@ -735,6 +776,34 @@ extern "C" int rmi_gqa_flash_decode_prep(const float* q3, int q3_stride, const f
     hipLaunchKernelGGL(gqa_merge_kernel, dim3(ntok, n_head, kMergeParts), dim3(HD), 0, s, ws, kMaxSlots, q3, q3_stride,
                        pos, y, y_stride, q8, q8_stride, n_head, n_kv, SUB * nsub);
     return launch_status("gqa_flash_decode_prep");
+}
+}  // namespace
+}  // namespace rmi
+
+extern "C" int rmi_gqa_flash_decode_prep(const float* q3, int q3_stride, const float* qn, const float* kn,
+                                         uint16_t* kcache, uint16_t* vcache, const int* pos, float* y, int y_stride,
+                                         uint8_t* q8, int q8_stride, void* workspace, int n_head, int n_kv,
+                                         int head_dim, int n_rot, const rmi_rope_params* rope, float eps, int ntok,
+                                         int max_ctx, int nsub, float scale, void* stream) {
+    return flash_decode_prep(q3, q3_stride, qn, kn, kcache, vcache, pos, y, y_stride, q8, q8_stride, workspace, n_head,
+                             n_kv, head_dim, n_rot, rope, eps, ntok, max_ctx, nsub, scale, nullptr, kRopeOwn, stream);
+}
+
+extern "C" size_t rmi_gqa_rope_table_bytes(int n_rot) {
+    return n_rot > 0 && n_rot % 2 == 0 ? static_cast<size_t>(2) * (n_rot / 2) * 2 * sizeof(float) : 0;
+}
+
+extern "C" int rmi_gqa_flash_decode_prep_rt(const float* q3, int q3_stride, const float* qn, const float* kn,
+                                            uint16_t* kcache, uint16_t* vcache, const int* pos, float* y,
+                                            int y_stride, uint8_t* q8, int q8_stride, void* workspace, int n_head,
+                                            int n_kv, int head_dim, int n_rot, const rmi_rope_params* rope, float eps,
+                                            int ntok, int max_ctx, int nsub, float scale, float* rope_table,
+                                            int table_mode, void* stream) {
+    if (table_mode < kRopeOwn || table_mode > kRopeRead)
+        return fail(RMI_ERR_SHAPE, "gqa_flash_decode_prep_rt: table_mode must be 0, 1 or 2");
+    return flash_decode_prep(q3, q3_stride, qn, kn, kcache, vcache, pos, y, y_stride, q8, q8_stride, workspace, n_head,
+                             n_kv, head_dim, n_rot, rope, eps, ntok, max_ctx, nsub, scale, rope_table, table_mode,
+                             stream);
 }
 
 extern "C" size_t rmi_gqa_noalloc_scratch_bytes(int max_ctx, int n_kv, int nsub, int slots) {

@@ -143,6 +143,7 @@ struct Engine {
     float *dx = nullptr, *dpart = nullptr;
     uint8_t *q8a = nullptr, *q8f = nullptr, *q8y = nullptr;
     void *attn_ws = nullptr, *argmax_ws = nullptr, *topk_ws = nullptr;
+    float* rope_cs = nullptr;   // the trunk pass's RoPE (cos, sin) table: written by its first attention layer
     unsigned long long* gdn_xch = nullptr;   // the split GDN step's exchange words (rmi_gdn_exchange_bytes), zeroed once
     int* topk_out = nullptr;        // top-k ids [0, 64) and logits (as float) [64, 128)
     int stream_mode = -1;           // rmi_engine_gen_begin's mode, -1 before it
@@ -568,17 +569,18 @@ int ffn(Engine& e, Layer& L, float* x, float* part, int nc) {
 // pos[0] is the position of column 0; with more columns than one attention launch takes (64 query vectors per KV
 // head: 16 tokens at 4 query heads per KV head) pos is an array, pos[c] = pos[0] + c, and the launch for columns
 // c0.. reads pos + c0.  Every KV row of the nc columns is stored before any of them attends, and query c sees
-// positions <= pos[0] + c only, as in the per-token path.
-int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc) {
+// positions <= pos[0] + c only, as in the per-token path.  rope_mode (decode / verify): 0 the launch computes its
+// rotation, 1 it also writes the trunk pass's table e.rope_cs, 2 it reads the table (the same bits).
+int attn_block(Engine& e, Layer& L, float* x, float* part, const int* pos, int nc, int rope_mode = 0) {
     const auto& c = e.cfg;
     RMI_TRY(norm_gemv(e, L.in_proj, x, part, L.attn_norm, e.proj, nc));
     const size_t q8y_col = q81_bytes(e.attn_q);
     if (nc * (c.n_head / c.n_kv) <= 8 && c.n_rot == 64 && (c.n_head / c.n_kv) % 2 == 0) {
         // decode / verify: the per-head norm, RoPE and K / V store in the attention's partial launch
-        RMI_TRY(rmi_gqa_flash_decode_prep(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, nullptr, 0, e.q8y,
-                                          static_cast<int>(q8y_col), e.attn_ws, c.n_head, c.n_kv, c.head_dim, c.n_rot,
-                                          &e.rope, c.eps, nc, e.max_ctx, e.nsub,
-                                          1.0f / sqrtf(static_cast<float>(c.head_dim)), e.s));
+        RMI_TRY(rmi_gqa_flash_decode_prep_rt(e.proj, e.q3_rows, L.qn, L.kn, L.kc, L.vc, pos, nullptr, 0, e.q8y,
+                                             static_cast<int>(q8y_col), e.attn_ws, c.n_head, c.n_kv, c.head_dim,
+                                             c.n_rot, &e.rope, c.eps, nc, e.max_ctx, e.nsub,
+                                             1.0f / sqrtf(static_cast<float>(c.head_dim)), e.rope_cs, rope_mode, e.s));
         RMI_TRY(gemv_res(e, L.out_proj, e.q8y, x, part, nc));
         return ffn(e, L, x, part, nc);
     }
@@ -621,10 +623,15 @@ int trunk_cols(Engine& e, int nc, const int* tok, const int* pos, float* h, floa
     const auto& c = e.cfg;
     RMI_TRY(rmi_embed(e.emb_type, e.tok_embd, tok, e.x, e.part, c.n_embd, c.n_vocab, nc, e.s));
     const int nl = static_cast<int>(e.layers.size());
+    int rope_mode = 1;   // every attention layer of the pass rotates at pos: the first writes the table, the rest read
     for (int il = 0; il < nl; ++il) {
         Layer& L = e.layers[il];
-        if (L.gdn) RMI_TRY(gdn_block(e, L, nc));
-        else RMI_TRY(attn_block(e, L, e.x, e.part, pos, nc));
+        if (L.gdn) {
+            RMI_TRY(gdn_block(e, L, nc));
+        } else {
+            RMI_TRY(attn_block(e, L, e.x, e.part, pos, nc, rope_mode));
+            rope_mode = 2;
+        }
     }
     if (head != kHeadNone) {
         const int first = head == kHeadAll ? 0 : nc - 1;
@@ -1188,6 +1195,7 @@ int alloc_runtime(Engine& e) {
     uint8_t* ws = nullptr;
     RMI_TRY(e.alloc(&ws, rmi_gqa_workspace_bytes(e.max_ctx, c.n_kv, e.nsub)));
     e.attn_ws = ws;
+    RMI_TRY(e.alloc(&e.rope_cs, rmi_gqa_rope_table_bytes(c.n_rot) / sizeof(float)));
     uint8_t* aw = nullptr;
     RMI_TRY(e.alloc(&aw, rmi_argmax_workspace_bytes(2)));
     e.argmax_ws = aw;

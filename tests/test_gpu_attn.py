@@ -245,3 +245,45 @@ def test_flash_decode_prep_bitwise_equals_prep_then_flash(orc, rmi, ctx, nsub, p
     assert np.array_equal(host(yb).view(np.uint32), host(ya).view(np.uint32))
     assert np.array_equal(host(q8b), host(q8a))
     assert np.array_equal(host(kb), host(ka)) and np.array_equal(host(vb), host(va))
+
+
+@pytest.mark.parametrize("ctx,nsub,p0,ntok,factor", [(4096, 2, 4096 - 300, 2, 1.0), (4096, 2, 1000, 1, 1.0),
+                                                     (66048, 17, 65279, 2, 1.0), (8192, 2, 5000, 2, 4.0),
+                                                     (320, 1, 0, 2, 1.0)])
+def test_flash_decode_prep_rope_table_bitwise(orc, rmi, ctx, nsub, p0, ntok, factor):
+    """rmi_gqa_flash_decode_prep_rt as a forward pass runs it: layer A in table mode 1 (computes its rotation and stores
+    the table), then layer B (other rows, weights and caches, same positions) in mode 2 (loads the table).  Both
+    bitwise the table-free call on copies of the same inputs (y, Q8_1, the caches after the call); the table holds the
+    (cos, sin) of the fp64 angle at pos + t, within 1e-6 of numpy's."""
+    t_ = torch()
+    half = 32
+    table = empty(rmi.gqa_rope_table_bytes(64) // 4)
+    assert rmi.gqa_rope_table_bytes(64) == 2 * half * 2 * 4
+    dpos = dev(np.array([p0], np.int32))
+    outs = {}
+    for layer, mode in (("a", 1), ("b", 2)):
+        seed = 1200 + (0 if layer == "a" else 50)
+        kc, vc = kv_cache(orc, ctx, seed=seed)
+        q3 = orc.normal(ntok * Q3, seed=seed + 1)
+        qn = (1 + orc.normal(HD, seed=seed + 2, std=0.1)).astype(np.float32)
+        kn = (1 + orc.normal(HD, seed=seed + 3, std=0.1)).astype(np.float32)
+        dq3, dqn, dkn = dev(q3), dev(qn), dev(kn)
+        res = []
+        for m in (0, mode):
+            k_, v_ = dev(kc), dev(vc)
+            ws = empty(rmi.gqa_workspace_bytes(ctx, NKV, nsub), "uint8")
+            y, q8 = empty(ntok * NH * HD), empty(ntok * NH * HD // 32 * 36, "uint8")
+            rmi.gqa_flash_decode_prep_rt(dq3, Q3, dqn, dkn, k_, v_, dpos, y, NH * HD, q8, NH * HD // 32 * 36, ws, NH,
+                                         NKV, HD, 64, 1e7, factor, 4096.0, 1e-6, ntok, ctx, nsub, SCALE, table, m)
+            t_.cuda.synchronize()
+            res.append((host(y).view(np.uint32), host(q8), host(k_), host(v_)))
+        for a, b in zip(res[0], res[1]):
+            assert np.array_equal(a, b), f"layer {layer}, table mode {mode}"
+        outs[layer] = res[1]
+    tab = host(table).reshape(2, half, 2)
+    for t in range(ntok):
+        i = np.arange(half)
+        ang = (p0 + t) * np.power(1e7, -2.0 * i / 64)
+        if factor > 1.0:
+            continue   # the YaRN ramp is checked through the bitwise comparison above
+        assert np.allclose(tab[t, :, 0], np.cos(ang), atol=1e-6) and np.allclose(tab[t, :, 1], np.sin(ang), atol=1e-6)
