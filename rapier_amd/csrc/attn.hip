@@ -335,6 +335,10 @@ __global__ __launch_bounds__(256, 2) void gqa_partial_kernel(const float* __rest
         set_u4(vnext, 2 * j, load_kv(vr));
         set_u4(vnext, 2 * j + 1, load_kv(vr + 128));
     }
+    // the new rows' inputs and the table's K entries stay live until the K / V loads are out: reusing their registers
+    // for the K / V addresses made those loads wait for every load of the prologue
+    if constexpr (PREP)
+        asm volatile("" ::"v"(xk[0]), "v"(xk[1]), "v"(xv[0]), "v"(xv[1]), "v"(wk), "v"(kcs[0]), "v"(kcs[1]));
     // B operand of the score MFMAs, from the staged query rows: step 2 sp + hlf covers dims
     // 32 sp + 8 g4 + 4 hlf + [0, 4); rows 0-7 the fp16 hi part, rows 8-15 the fp16 lo part of the same slot
     if constexpr (PREP) {
