@@ -507,15 +507,16 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
     float zz[NT], gam = 0.0f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) zz[t] = 0.0f;
-    if (rg == 0) {
-        gam = a.gamma[col];
+    // z, gamma and the gate inputs are loaded by every lane (the same addresses in range for all of them) and used by
+    // the lanes that own them: loads under a branch make the wait for the selector, at the join, cover every load
+    // issued before the branch
+    gam = a.gamma[col];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) zz[t] = a.z[static_cast<size_t>(t) * a.tok_stride + head * S + col];
-    }
-    float gin[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < NT; ++t) zz[t] = a.z[static_cast<size_t>(t) * a.tok_stride + head * S + col];
+    float gin[4];
     const int gt = static_cast<int>(threadIdx.x) - 64;   // gate lane of token gt: the second wave's first lanes
-    if (gt >= 0 && gt < NT) {
-        const float* ab = a.ab + static_cast<size_t>(gt) * a.ab_stride;
+    {
+        const float* ab = a.ab + static_cast<size_t>(min(max(gt, 0), NT - 1)) * a.ab_stride;
         gin[0] = ab[head];
         gin[1] = ab[a.h_v + head];
         gin[2] = a.dt[head];
