@@ -571,11 +571,10 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* 
         issue(c);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // unconditional (lanes past the last block rewrite its slot with the same bytes): under a branch the compiler sinks
+    // the stage's loads into it, behind the first tiles, and the stage then waits for those
 #pragma unroll
-    for (int b = 0; b < SB; ++b) {
-        const int J = t + b * 64 * NW;
-        if (J < nblocks) stage_one<NCOLS>(sv[b], J, nbt, st);
-    }
+    for (int b = 0; b < SB; ++b) stage_one<NCOLS>(sv[b], min(t + b * 64 * NW, nblocks - 1), nbt, st);
     for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
         const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
         uint32_t wv[9];
@@ -692,11 +691,10 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_stream(const uint8_t*
     if constexpr (NORM) {
         norm_stage<NCOLS, NCH, NW>(nl, ni, st, t, nred);
     } else {
+        // unconditional (lanes past the last block rewrite its slot with the same bytes): under a branch the compiler
+        // sinks the stage's loads into it, behind the first tiles, and the stage then waits for those
 #pragma unroll
-        for (int b = 0; b < SB; ++b) {
-            const int J = t + b * 64 * NW;
-            if (J < nblocks) stage_one<NCOLS>(sv[b], J, nbt, st);
-        }
+        for (int b = 0; b < SB; ++b) stage_one<NCOLS>(sv[b], min(t + b * 64 * NW, nblocks - 1), nbt, st);
         for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
             const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
             uint32_t wv[9];
@@ -843,11 +841,10 @@ __global__ __launch_bounds__(64 * NW) void q6k_gguf_stream(const uint8_t* __rest
         issue(i);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // unconditional (lanes past the last block rewrite its slot with the same bytes): under a branch the compiler sinks
+    // the stage's loads into it, behind the first tiles, and the stage then waits for those
 #pragma unroll
-    for (int b = 0; b < SB; ++b) {
-        const int J = t + b * 64 * NW;
-        if (J < nblocks) stage_one<NCOLS>(sv[b], J, nbt, st);
-    }
+    for (int b = 0; b < SB; ++b) stage_one<NCOLS>(sv[b], min(t + b * 64 * NW, nblocks - 1), nbt, st);
     for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
         const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
         uint32_t wv[9];
