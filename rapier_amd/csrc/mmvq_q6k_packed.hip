@@ -1387,7 +1387,7 @@ PackedCfg packed_cfg(int n_in, int n_out, int ncols) {
     const int nch = n_in / kChunkElems, nq = (n_out + kQuad - 1) / kQuad;
     if (loop_only || ncols > 2) return {PackedCfg::kLoop, 0, 0};
     if (nch == 2) {
-        if (nq <= 1024) return {PackedCfg::kSplit, 1, 8};
+        if (nq <= 1024) return {PackedCfg::kStream, 0, 0};   // one quad per wave (the output projections)
         if (nq <= 4096) return {PackedCfg::kSplit, 1, 4};
         return {PackedCfg::kStream, 0, 0};
     }
@@ -1432,15 +1432,17 @@ void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* r
     if constexpr (NCOLS <= 2) {
         const PackedCfg c = packed_cfg(n_in, n_out, NCOLS);
         if (c.kind == PackedCfg::kStream) {
-            if (n_in / kChunkElems == 2)
+            if (n_in / kChunkElems == 2) {
+                if ((n_out + kQuad - 1) / kQuad <= 1024)
+                    return launch_stream<NCOLS, RES, 2, 1, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
                 return launch_stream<NCOLS, RES, 2, 2, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
+            }
             if (n_in / kChunkElems == 4)
                 return launch_stream<NCOLS, RES, 4, 1, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
             return launch_stream<NCOLS, RES, 6, 1, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
         }
         if (c.kind == PackedCfg::kSplit) {
             if (c.cs == 2) return launch_split<NCOLS, RES, 2, 4>(wp, x, y, res, partials, n_in, n_out, s);
-            if (c.nw == 8) return launch_split<NCOLS, RES, 1, 8>(wp, x, y, res, partials, n_in, n_out, s);
             return launch_split<NCOLS, RES, 1, 4>(wp, x, y, res, partials, n_in, n_out, s);
         }
     }
