@@ -992,27 +992,6 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_swiglu(const uint8_t* __re
 // one LDS pass (4 half-blocks x 4 columns) hit distinct banks.
 constexpr int kMStride = 13;   // uint4 per (cg, block)
 
-__device__ __forceinline__ void stage_activations_mfma(const uint8_t* __restrict__ x, int ncols, int nbt, uint4* st,
-                                                       int t, int nthreads) {
-    for (int J = t; J < ncols * nbt; J += nthreads) {
-        const int col = J / nbt, jb = J - col * nbt;
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
-        uint32_t wv[9];
-#pragma unroll
-        for (int i = 0; i < 9; ++i) wv[i] = p[i];
-        int s0 = 0, s1 = 0;
-#pragma unroll
-        for (int i = 1; i <= 4; ++i) s0 = sdot4(static_cast<int>(wv[i]), 0x01010101, s0);
-#pragma unroll
-        for (int i = 5; i <= 8; ++i) s1 = sdot4(static_cast<int>(wv[i]), 0x01010101, s1);
-        uint4* q = st + static_cast<size_t>((col >> 2) * nbt + jb) * kMStride + (col & 3);
-        q[0] = make_uint4(wv[1], wv[2], wv[3], wv[4]);
-        q[4] = make_uint4(wv[5], wv[6], wv[7], wv[8]);
-        q[8] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1),
-                          __float_as_uint(half_bits_to_float(wv[0])), 0u);
-    }
-}
-
 // one Q8_1 block (its 9 dwords) into the MFMA stage at (column col, staged block jb), nbs staged blocks per column
 __device__ __forceinline__ void stage_one_mfma(const uint32_t (&wv)[9], int col, int jb, int nbs, uint4* st) {
     int s0 = 0, s1 = 0;
@@ -1025,19 +1004,6 @@ __device__ __forceinline__ void stage_one_mfma(const uint32_t (&wv)[9], int col,
     q[4] = make_uint4(wv[5], wv[6], wv[7], wv[8]);
     q[8] = make_uint4(static_cast<uint32_t>(-32 * s0), static_cast<uint32_t>(-32 * s1),
                       __float_as_uint(half_bits_to_float(wv[0])), 0u);
-}
-
-// blocks jb0 .. jb0 + nbs - 1 of every column (nbt blocks per column in x) into the stage
-__device__ __forceinline__ void stage_range_mfma(const uint8_t* __restrict__ x, int ncols, int nbt, int jb0, int nbs,
-                                                 uint4* st, int t, int nthreads) {
-    for (int J = t; J < ncols * nbs; J += nthreads) {
-        const int col = J / nbs, jb = J - col * nbs;
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(col * nbt + jb0 + jb) * kQ8_1Bytes);
-        uint32_t wv[9];
-#pragma unroll
-        for (int i = 0; i < 9; ++i) wv[i] = p[i];
-        stage_one_mfma(wv, col, jb, nbs, st);
-    }
 }
 
 // KP = 2: the second half of the blocks, held in registers (up to kPhaseRegs blocks per lane) until the phase switch
@@ -1087,10 +1053,26 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
     const int nsteps = my_quads * nch;
     const int nbs = nbt / KP, cpp = KP == 2 ? NCHK / 2 : nch;   // staged blocks per column, chunks per phase
 
+    // the first kStageRegs activation blocks of each lane go out ahead of the weight tiles (a wave's loads return in
+    // issue order: a stage loaded after the tiles waits for them)
+    constexpr int kStageRegs = 4;
+    const int nb_stage = 4 * NCG * (KP == 2 ? nbs : nbt);
+    const int nbs_stage = KP == 2 ? nbs : nbt;
+    uint32_t sv[kStageRegs][9];
+#pragma unroll
+    for (int m = 0; m < kStageRegs; ++m) {
+        const int J = min(t + 64 * kWideWaves * m, nb_stage - 1);
+        const int col = J / nbs_stage, jb = J - col * nbs_stage;
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(col * nbt + jb) * kQ8_1Bytes);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) sv[m][i] = p[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     WTile buf[D];
     auto issue = [&](int f, WTile& b) {
         const int qi = f / nch, c = f - qi * nch;
-        const int qq = KP == 2 ? min(gw, nq - 1) : gw + qi * GW;
+        const int qq = KP == 2 ? min(gw, nq - 1) : min(gw + qi * GW, nq - 1);   // clamped: the prefetch below
         const uint8_t* base = wp + (static_cast<size_t>(qq) * nch + c) * kWaveTile;
 #pragma unroll
         for (int u = 0; u < 4; ++u)
@@ -1101,14 +1083,25 @@ __global__ __launch_bounds__(64 * kWideWaves) void q6k_packed_mfma(const uint8_t
         b.sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
         b.d = *reinterpret_cast<const uint16_t*>(base + 6656 + 2 * (4 * (lane >> 3) + (lane & 3)));
     };
+    // unconditional (a wave with fewer steps re-reads its last, or the grid's last quad's, tile and discards it): with
+    // the loads under a branch the wait for the staged blocks below would also cover the tiles
 #pragma unroll
-    for (int s = 0; s < D; ++s)
-        if (s < nsteps) issue(s, buf[s]);
+    for (int s = 0; s < D; ++s) issue(min(s, max(nsteps - 1, 0)), buf[s]);
 
-    if constexpr (KP == 1) {
-        stage_activations_mfma(x, 4 * NCG, nbt, smem, t, 64 * kWideWaves);
-    } else {
-        stage_range_mfma(x, 4 * NCG, nbt, 0, nbs, smem, t, 64 * kWideWaves);
+    // the blocks held in registers (lanes past the last block rewrite its slot with the same bytes), then the rest
+#pragma unroll
+    for (int m = 0; m < kStageRegs; ++m) {
+        const int J = min(t + 64 * kWideWaves * m, nb_stage - 1);
+        const int col = J / nbs_stage, jb = J - col * nbs_stage;
+        stage_one_mfma(sv[m], col, jb, nbs_stage, smem);
+    }
+    for (int J = t + 64 * kWideWaves * kStageRegs; J < nb_stage; J += 64 * kWideWaves) {
+        const int col = J / nbs_stage, jb = J - col * nbs_stage;
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(col * nbt + jb) * kQ8_1Bytes);
+        uint32_t wv[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) wv[i] = p[i];
+        stage_one_mfma(wv, col, jb, nbs_stage, smem);
     }
     // KP = 2: the second half's blocks, loaded one step before the switch (into registers the tiles leave free) and
     // staged at the switch
