@@ -504,13 +504,11 @@ __global__ __launch_bounds__(kPartLanes) void gdn_split_kernel(StepArgs a) {
         wk[i] = a.conv_w[4 * ckc + i];
         wvv[i] = a.conv_w[4 * cvc + i];
     }
-    float zz[NT], gam = 0.0f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) zz[t] = 0.0f;
     // z, gamma and the gate inputs are loaded by every lane (the same addresses in range for all of them) and used by
     // the lanes that own them: loads under a branch make the wait for the selector, at the join, cover every load
     // issued before the branch
-    gam = a.gamma[col];
+    const float gam = a.gamma[col];
+    float zz[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) zz[t] = a.z[static_cast<size_t>(t) * a.tok_stride + head * S + col];
     float gin[4];
