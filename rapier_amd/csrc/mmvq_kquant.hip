@@ -35,12 +35,52 @@ __device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2,
     }
 }
 
-template <int TYPE, int NCOLS, bool RES>
+// A lane's weight loads for one block (scales, its 32 quant bytes, Q5_K's 32 high-bit bytes)
+template <int TYPE>
+struct KBlock {
+    uint32_t dm, s0, s1, s2;
+    uint4 qa, qb, ha, hb;
+};
+
+template <int TYPE>
+__device__ __forceinline__ void kblock_load(KBlock<TYPE>& k, const uint8_t* blk, int p) {
+    constexpr int kQs = TYPE == 13 ? 48 : 16;
+    k.dm = *reinterpret_cast<const uint32_t*>(blk);
+    k.s0 = *reinterpret_cast<const uint32_t*>(blk + 4);
+    k.s1 = *reinterpret_cast<const uint32_t*>(blk + 8);
+    k.s2 = *reinterpret_cast<const uint32_t*>(blk + 12);
+    k.qa = *reinterpret_cast<const uint4*>(blk + kQs + 32 * p);
+    k.qb = *reinterpret_cast<const uint4*>(blk + kQs + 32 * p + 16);
+    if constexpr (TYPE == 13) {
+        k.ha = *reinterpret_cast<const uint4*>(blk + 16);
+        k.hb = *reinterpret_cast<const uint4*>(blk + 32);
+    }
+}
+
+// one Q8_1 block (its 9 dwords) into the stage: codes and {sum of codes, d8}
+__device__ __forceinline__ void kstage_one(const uint32_t (&wq)[9], int J, uint4* lq, uint2* lr) {
+    int su = 0;
+#pragma unroll
+    for (int i = 1; i <= 8; ++i) su = sdot4(static_cast<int>(wq[i]), 0x01010101, su);
+    lq[2 * J] = make_uint4(wq[1], wq[2], wq[3], wq[4]);
+    lq[2 * J + 1] = make_uint4(wq[5], wq[6], wq[7], wq[8]);
+    lr[J] = make_uint2(static_cast<uint32_t>(su), __float_as_uint(half_bits_to_float(wq[0])));
+}
+
+// Issue order (a wave's loads return in issue order): the lane's first kSB activation blocks, then its weight blocks
+// of the first NI steps (NI = 1..3, sized by the launch to the row: every step of rows up to 12288 wide), then the
+// stage is written;
+// every load is unconditional from a clamped address (rows past the last and blocks past the row's end re-read the
+// last ones and are not used), so no wait covers loads it does not need.  The arithmetic, block by block in ascending
+// order per lane, is unchanged: the same bits as one step at a time.
+template <int TYPE, int NCOLS, bool RES, int NI>
 __global__ __launch_bounds__(256) void kquant_gemv_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ x,
                                                           float* y, const float* res, float* partials, int n_in,
                                                           int n_out) {
     constexpr int kBytes = TYPE == 13 ? 176 : 144;
-    constexpr int kQs = TYPE == 13 ? 48 : 16;
+    constexpr int kNI = NI;
+    // staged blocks per lane held in registers: NCOLS x 8 x 16 NI blocks over 256 lanes, at most 4
+    constexpr int kSB = (NCOLS * NI + 1) / 2 < 4 ? (NCOLS * NI + 1) / 2 : 4;
     extern __shared__ uint4 smem[];
     __shared__ float vout[NCOLS][4];
     const int nbq = n_in / 32, nb = n_in / 256;
@@ -49,79 +89,90 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const uint8_t* __restr
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int row = blockIdx.x * 4 + wv;
     const int p = lane & 3;
-    for (int J = threadIdx.x; J < NCOLS * nbq; J += 256) {
+    const int nstage = NCOLS * nbq;
+
+    uint32_t sv[kSB][9];
+#pragma unroll
+    for (int m = 0; m < kSB; ++m) {
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(
+            x + static_cast<size_t>(min(static_cast<int>(threadIdx.x) + 256 * m, nstage - 1)) * kQ8_1Bytes);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) sv[m][i] = q[i];
+    }
+    const uint8_t* wrow = w + static_cast<size_t>(min(row, n_out - 1)) * nb * kBytes;
+    KBlock<TYPE> kb[kNI];
+#pragma unroll
+    for (int i = 0; i < kNI; ++i) kblock_load<TYPE>(kb[i], wrow + static_cast<size_t>(min((lane >> 2) + 16 * i, nb - 1)) * kBytes, p);
+#pragma unroll
+    for (int m = 0; m < kSB; ++m) kstage_one(sv[m], min(static_cast<int>(threadIdx.x) + 256 * m, nstage - 1), lq, lr);
+    for (int J = threadIdx.x + 256 * kSB; J < nstage; J += 256) {
         const uint32_t* q = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
         uint32_t wq[9];
 #pragma unroll
         for (int i = 0; i < 9; ++i) wq[i] = q[i];
-        int su = 0;
-#pragma unroll
-        for (int i = 1; i <= 8; ++i) su = sdot4(static_cast<int>(wq[i]), 0x01010101, su);
-        lq[2 * J] = make_uint4(wq[1], wq[2], wq[3], wq[4]);
-        lq[2 * J + 1] = make_uint4(wq[5], wq[6], wq[7], wq[8]);
-        lr[J] = make_uint2(static_cast<uint32_t>(su), __float_as_uint(half_bits_to_float(wq[0])));
+        kstage_one(wq, J, lq, lr);
     }
     __syncthreads();
 
     float acc[NCOLS];
 #pragma unroll
     for (int c = 0; c < NCOLS; ++c) acc[c] = 0.0f;
-    if (row < n_out) {
-        for (int b = lane >> 2; b < nb; b += 16) {
-            const uint8_t* blk = w + (static_cast<size_t>(row) * nb + b) * kBytes;
-            const uint32_t dm = *reinterpret_cast<const uint32_t*>(blk);
-            const uint32_t s0 = *reinterpret_cast<const uint32_t*>(blk + 4);
-            const uint32_t s1 = *reinterpret_cast<const uint32_t*>(blk + 8);
-            const uint32_t s2 = *reinterpret_cast<const uint32_t*>(blk + 12);
-            const uint4 qa = *reinterpret_cast<const uint4*>(blk + kQs + 32 * p);
-            const uint4 qb = *reinterpret_cast<const uint4*>(blk + kQs + 32 * p + 16);
-            uint32_t Q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-            uint32_t H[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    // block b of the lane: sub-blocks 2 p and 2 p + 1 against every column
+    auto block_dot = [&](const KBlock<TYPE>& k, int b) {
+        uint32_t Q[8] = {k.qa.x, k.qa.y, k.qa.z, k.qa.w, k.qb.x, k.qb.y, k.qb.z, k.qb.w};
+        uint32_t H[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if constexpr (TYPE == 13) {
+            H[0] = k.ha.x; H[1] = k.ha.y; H[2] = k.ha.z; H[3] = k.ha.w;
+            H[4] = k.hb.x; H[5] = k.hb.y; H[6] = k.hb.z; H[7] = k.hb.w;
+        }
+        int sc0, m0, sc1, m1;
+        scale_min(k.s0, k.s1, k.s2, 2 * p, sc0, m0);
+        scale_min(k.s0, k.s1, k.s2, 2 * p + 1, sc1, m1);
+        const float d = half_bits_to_float(k.dm & 0xffffu), dmin = half_bits_to_float(k.dm >> 16);
+        int v0[8], v1[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v0[i] = static_cast<int>(Q[i] & 0x0f0f0f0fu);
+            v1[i] = static_cast<int>((Q[i] >> 4) & 0x0f0f0f0fu);
             if constexpr (TYPE == 13) {
-                const uint4 ha = *reinterpret_cast<const uint4*>(blk + 16);
-                const uint4 hb = *reinterpret_cast<const uint4*>(blk + 32);
-                H[0] = ha.x; H[1] = ha.y; H[2] = ha.z; H[3] = ha.w;
-                H[4] = hb.x; H[5] = hb.y; H[6] = hb.z; H[7] = hb.w;
+                v0[i] |= static_cast<int>(((H[i] >> (2 * p)) & 0x01010101u) << 4);
+                v1[i] |= static_cast<int>(((H[i] >> (2 * p + 1)) & 0x01010101u) << 4);
             }
-            int sc0, m0, sc1, m1;
-            scale_min(s0, s1, s2, 2 * p, sc0, m0);
-            scale_min(s0, s1, s2, 2 * p + 1, sc1, m1);
-            const float d = half_bits_to_float(dm & 0xffffu), dmin = half_bits_to_float(dm >> 16);
-            int v0[8], v1[8];
+        }
+        const int j = 8 * b + 2 * p;   // Q8_1 block of sub-block 2 p
+#pragma unroll
+        for (int c = 0; c < NCOLS; ++c) {
+            const uint4* cq = lq + 2 * (c * nbq + j);
+            const uint4 u0a = cq[0], u0b = cq[1], u1a = cq[2], u1b = cq[3];
+            const int u0[8] = {static_cast<int>(u0a.x), static_cast<int>(u0a.y), static_cast<int>(u0a.z),
+                               static_cast<int>(u0a.w), static_cast<int>(u0b.x), static_cast<int>(u0b.y),
+                               static_cast<int>(u0b.z), static_cast<int>(u0b.w)};
+            const int u1[8] = {static_cast<int>(u1a.x), static_cast<int>(u1a.y), static_cast<int>(u1a.z),
+                               static_cast<int>(u1a.w), static_cast<int>(u1b.x), static_cast<int>(u1b.y),
+                               static_cast<int>(u1b.z), static_cast<int>(u1b.w)};
+            int dot0 = 0, dot1 = 0;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                v0[i] = static_cast<int>(Q[i] & 0x0f0f0f0fu);
-                v1[i] = static_cast<int>((Q[i] >> 4) & 0x0f0f0f0fu);
-                if constexpr (TYPE == 13) {
-                    v0[i] |= static_cast<int>(((H[i] >> (2 * p)) & 0x01010101u) << 4);
-                    v1[i] |= static_cast<int>(((H[i] >> (2 * p + 1)) & 0x01010101u) << 4);
-                }
+                dot0 = sdot4(v0[i], u0[i], dot0);
+                dot1 = sdot4(v1[i], u1[i], dot1);
             }
-            const int j = 8 * b + 2 * p;   // Q8_1 block of sub-block 2 p
+            const uint2 r0 = lr[c * nbq + j], r1 = lr[c * nbq + j + 1];
+            const float d80 = __uint_as_float(r0.y), d81 = __uint_as_float(r1.y);
+            float sumf_d = d80 * static_cast<float>(dot0 * sc0);
+            sumf_d = __builtin_fmaf(d81, static_cast<float>(dot1 * sc1), sumf_d);
+            float sumf_m = d80 * static_cast<float>(static_cast<int>(r0.x) * m0);
+            sumf_m = __builtin_fmaf(d81, static_cast<float>(static_cast<int>(r1.x) * m1), sumf_m);
+            acc[c] += __builtin_fmaf(d, sumf_d, -(dmin * sumf_m));
+        }
+    };
+    if (row < n_out) {
 #pragma unroll
-            for (int c = 0; c < NCOLS; ++c) {
-                const uint4* cq = lq + 2 * (c * nbq + j);
-                const uint4 u0a = cq[0], u0b = cq[1], u1a = cq[2], u1b = cq[3];
-                const int u0[8] = {static_cast<int>(u0a.x), static_cast<int>(u0a.y), static_cast<int>(u0a.z),
-                                   static_cast<int>(u0a.w), static_cast<int>(u0b.x), static_cast<int>(u0b.y),
-                                   static_cast<int>(u0b.z), static_cast<int>(u0b.w)};
-                const int u1[8] = {static_cast<int>(u1a.x), static_cast<int>(u1a.y), static_cast<int>(u1a.z),
-                                   static_cast<int>(u1a.w), static_cast<int>(u1b.x), static_cast<int>(u1b.y),
-                                   static_cast<int>(u1b.z), static_cast<int>(u1b.w)};
-                int dot0 = 0, dot1 = 0;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    dot0 = sdot4(v0[i], u0[i], dot0);
-                    dot1 = sdot4(v1[i], u1[i], dot1);
-                }
-                const uint2 r0 = lr[c * nbq + j], r1 = lr[c * nbq + j + 1];
-                const float d80 = __uint_as_float(r0.y), d81 = __uint_as_float(r1.y);
-                float sumf_d = d80 * static_cast<float>(dot0 * sc0);
-                sumf_d = __builtin_fmaf(d81, static_cast<float>(dot1 * sc1), sumf_d);
-                float sumf_m = d80 * static_cast<float>(static_cast<int>(r0.x) * m0);
-                sumf_m = __builtin_fmaf(d81, static_cast<float>(static_cast<int>(r1.x) * m1), sumf_m);
-                acc[c] += __builtin_fmaf(d, sumf_d, -(dmin * sumf_m));
-            }
+        for (int i = 0; i < kNI; ++i)
+            if ((lane >> 2) + 16 * i < nb) block_dot(kb[i], (lane >> 2) + 16 * i);
+        for (int b = (lane >> 2) + 16 * kNI; b < nb; b += 16) {   // rows wider than 16 kNI blocks
+            KBlock<TYPE> k;
+            kblock_load<TYPE>(k, wrow + static_cast<size_t>(b) * kBytes, p);
+            block_dot(k, b);
         }
     }
 #pragma unroll
@@ -151,8 +202,17 @@ template <int TYPE, int NCOLS, bool RES>
 void launch_cols(const uint8_t* w, const uint8_t* x, float* y, const float* res, float* partials, int n_in, int n_out,
                  hipStream_t s) {
     const size_t lds = static_cast<size_t>(NCOLS) * (n_in / 32) * 40;
-    hipLaunchKernelGGL((kquant_gemv_kernel<TYPE, NCOLS, RES>), dim3((n_out + 3) / 4), dim3(256), lds, s, w, x, y, res,
-                       partials, n_in, n_out);
+    const int nb = n_in / 256;
+    const dim3 grid((n_out + 3) / 4);
+    if (nb <= 16)
+        hipLaunchKernelGGL((kquant_gemv_kernel<TYPE, NCOLS, RES, 1>), grid, dim3(256), lds, s, w, x, y, res, partials,
+                           n_in, n_out);
+    else if (nb <= 32)
+        hipLaunchKernelGGL((kquant_gemv_kernel<TYPE, NCOLS, RES, 2>), grid, dim3(256), lds, s, w, x, y, res, partials,
+                           n_in, n_out);
+    else
+        hipLaunchKernelGGL((kquant_gemv_kernel<TYPE, NCOLS, RES, 3>), grid, dim3(256), lds, s, w, x, y, res, partials,
+                           n_in, n_out);
 }
 
 template <int TYPE, bool RES>
