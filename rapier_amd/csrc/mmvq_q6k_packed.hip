@@ -23,10 +23,9 @@
 // reduction tree are those of the 16-row tiled kernel, so the results are bitwise the same, every column of an
 // ncols >= 2 call is bitwise the ncols = 1 result, and the residual variant is bitwise plain + res.
 //
-// Rows of 4096, 8192 and 12288 (two, four and six chunks) run a split-chunk variant: a quad's chunks go to one or two
-// waves of one workgroup, in straight-line code with the tiles issued behind the activation loads (all at once, or two
-// ahead of the step for six chunks); a second wave hands its per-lane (scale, sum) pairs to the first through LDS,
-// which continues the same fma chain - the same bits, more loads in flight.
+// Rows of 4096, 8192 and 12288 (two, four and six chunks) run a stream variant: one wave per quad (two quads per wave
+// for the lm_head's 62080 quads), in straight-line code with the tiles issued behind the activation loads, two tiles
+// ahead of the step - the same bits, more loads in flight.
 #include "rmi_common.h"
 
 #include <algorithm>
@@ -333,14 +332,9 @@ __device__ __forceinline__ void norm_stage(const NormLanes<NCOLS, NCH, NW>& L, c
 
 // Marks the point where a tile's registers are first used: no computation on them moves above it and no load moves
 // across it, so the wait placed here covers this tile and the loads issued before it only (loads complete in issue
-// order).  Without it the compiler converts a tile's scale right after its load and the wait stalls later loads.
-__device__ __forceinline__ void pin_tile(WTile& w) {
-    asm volatile("" : "+v"(w.ql[0]), "+v"(w.ql[1]), "+v"(w.ql[2]), "+v"(w.ql[3]), "+v"(w.qh[0]), "+v"(w.qh[1]),
-                 "+v"(w.sc), "+v"(w.d)::"memory");
-}
-
-// pin_tile that also keeps the previous step's arithmetic above it (the running sums pass through the asm): without it
-// the compiler may hoist this pin, and the wait for this tile, above the previous step's compute
+// order), and the previous step's arithmetic stays above it (the running sums pass through the asm).  Without it the
+// compiler converts a tile's scale right after its load, or hoists the wait for this tile above the previous step's
+// compute, and the wait stalls later loads.
 template <int NCOLS>
 __device__ __forceinline__ void pin_tile_after(WTile& w, float (&tot)[NCOLS]) {
     static_assert(NCOLS == 1 || NCOLS == 2, "one or two columns");
@@ -506,125 +500,6 @@ __global__ __launch_bounds__(64 * NW) void q6k_packed_gemv(const uint8_t* __rest
                 quad_epilogue<NCOLS, RES>(tot, lane, gw + qi * GW, y, res, partials, n_out);
         }
     }
-}
-
-// Split-chunk variant for grids with few quads per CU: the S = nch / CS waves of a quad each take CS consecutive
-// chunks, every tile issued at the start, and park their per-lane (d, acc) pairs in LDS; the quad's last wave to
-// finish (an LDS counter per quad, so no workgroup barrier waits for the other quads of the workgroup) forms the fma
-// chain over the chunks in chunk order.  The operations and their order are those of one wave walking every chunk,
-// so the result is bitwise that of q6k_packed_gemv.  NW waves per workgroup = QW quads x S.
-// SB: activation blocks per lane loaded ahead of the tiles (the rest, if any, after them); sized to the shape by the
-// launcher, since every block held here is a register live across the tile loads (SB 4 at a 4096-wide row left the
-// kernel at 89 VGPRs: five 4-wave workgroups per CU, so a sixth waited a whole round for a slot).
-template <int NCOLS, bool RES, int CS, int NW, int SB = 4>
-__global__ __launch_bounds__(64 * NW) void q6k_packed_gemv_split(const uint8_t* __restrict__ wp,
-                                                                 const uint8_t* __restrict__ x, float* y,
-                                                                 const float* res, float* partials, int n_in,
-                                                                 int n_out) {
-    extern __shared__ uint4 smem[];
-    __shared__ int qdone[NW];   // per quad: waves that have parked their sums
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
-    const int nbt = n_in / 32;
-    uint4* st = smem;   // the activation stage (stage_slot)
-    const StageLane sl = stage_lane<NCOLS>(st, nbt, lane);
-    float* lx = reinterpret_cast<float*>(st + 3 * NCOLS * nbt);   // [wave][chunk][d, acc[0..NCOLS)][lane]
-    if (t < NW) qdone[t] = 0;   // published by the staging barrier
-    const int nq = (n_out + kQuad - 1) / kQuad;
-    const int qg = w / S, sp = w - qg * S;
-    const int q = static_cast<int>(blockIdx.x) * QW + qg;
-    const bool live = qg < QW && q < nq;   // uniform across the wave
-
-    // the activation loads go first: a wave's loads return in issue order, so a stage issued after the weight tiles
-    // would wait for all of them before the first step could start
-
-    const int nblocks = NCOLS * nbt;
-    uint32_t sv[SB][9];
-#pragma unroll
-    for (int b = 0; b < SB; ++b) {   // unconditional (clamped) loads: no branch for the compiler to wait inside
-        const int J = min(t + b * 64 * NW, nblocks - 1);
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
-#pragma unroll
-        for (int i = 0; i < 9; ++i) sv[b][i] = p[i];
-    }
-    float rv[NCOLS];
-    if constexpr (RES) load_residual<NCOLS>(rv, res, lane, min(q, nq - 1), n_out);
-    __builtin_amdgcn_sched_barrier(0);   // the stage's loads stay ahead of the weight tiles
-    // unconditional loads (a wave past the last quad reads the last quad's tiles and discards them): with the loads in
-    // a branch the compiler waits for the stage as if no tile had been issued after it.  Every tile is issued here,
-    // tile by tile in order.
-    WTile buf[CS];
-    const int qld = min(q, nq - 1);
-    auto issue = [&](int c) {
-        const uint8_t* base = wp + (static_cast<size_t>(qld) * nch + sp * CS + c) * kWaveTile;
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            buf[c].ql[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * 1024 + 16 * lane));
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-            buf[c].qh[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + 4096 + u * 1024 + 16 * lane));
-        buf[c].sc = *reinterpret_cast<const uint2*>(base + 6144 + 8 * lane);
-        buf[c].d = *reinterpret_cast<const uint32_t*>(base + 6656 + 4 * (2 * (lane >> 3) + ((lane & 3) >> 1)));
-    };
-#pragma unroll
-    for (int c = 0; c < CS; ++c) {
-        issue(c);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    // unconditional (lanes past the last block rewrite its slot with the same bytes): under a branch the compiler sinks
-    // the stage's loads into it, behind the first tiles, and the stage then waits for those
-#pragma unroll
-    for (int b = 0; b < SB; ++b) stage_one<NCOLS>(sv[b], min(t + b * 64 * NW, nblocks - 1), nbt, st);
-    for (int J = t + SB * 64 * NW; J < nblocks; J += 64 * NW) {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(J) * kQ8_1Bytes);
-        uint32_t wv[9];
-#pragma unroll
-        for (int i = 0; i < 9; ++i) wv[i] = p[i];
-        stage_one<NCOLS>(wv, J, nbt, st);
-    }
-    __syncthreads();
-
-    if (!live) return;   // a quad's waves are all live or all past the last quad
-    float acc[CS][NCOLS], dd[CS];
-#pragma unroll
-    for (int c = 0; c < CS; ++c) {
-        const int ch = sp * CS + c;
-        pin_tile(buf[c]);
-        dd[c] = step_acc<NCOLS>(buf[c], lane, sl, ch, acc[c]);
-    }
-    float tot[NCOLS];
-#pragma unroll
-    for (int col = 0; col < NCOLS; ++col) tot[col] = 0.0f;
-    if (S == 1) {
-#pragma unroll
-        for (int c = 0; c < CS; ++c)
-#pragma unroll
-            for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(dd[c], acc[c][col], tot[col]);
-    } else {
-#pragma unroll
-        for (int c = 0; c < CS; ++c) {
-            float* o = lx + (w * CS + c) * (NCOLS + 1) * 64 + lane;
-            o[0] = dd[c];
-#pragma unroll
-            for (int col = 0; col < NCOLS; ++col) o[(col + 1) * 64] = acc[c][col];
-        }
-        // the release orders this wave's parked sums before its count; the last wave's acquire orders its reads after
-        int prev = 0;
-        if (lane == 0)
-            prev = __hip_atomic_fetch_add(&qdone[qg], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (__builtin_amdgcn_readfirstlane(prev) != S - 1) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");   // every lane's reads below stay after the count
-        for (int s2 = 0; s2 < S; ++s2) {   // chunk order: waves qg S .. qg S + S - 1, their chunks in order
-#pragma unroll
-            for (int c = 0; c < CS; ++c) {
-                const float* o = lx + ((qg * S + s2) * CS + c) * (NCOLS + 1) * 64 + lane;
-                const float d = o[0];
-#pragma unroll
-                for (int col = 0; col < NCOLS; ++col) tot[col] = __builtin_fmaf(d, o[(col + 1) * 64], tot[col]);
-            }
-        }
-    }
-    quad_epilogue<NCOLS, RES>(tot, lane, q, y, res, partials, n_out, rv);
 }
 
 // Stream variant: one wave per quad and QPW quads per wave (quads q, q + G, q + 2G, ... with G the grid's wave count),
@@ -1358,18 +1233,18 @@ int packed_grid(int nq) {
 
 // Kernel choice for one or two columns (more columns, and shapes without an entry, run the pipelined loop kernel).
 // Measured per launch at two columns (one column in brackets) against the loop kernel:
-//   n_in 4096:  4096 rows 6.80 -> 5.71 us (split, 8 waves per workgroup), 10240 rows 9.92 -> 8.98 us (9.0 -> 8.2),
-//               12352 rows 11.35 -> 10.23 us (10.3 -> 9.4) (split, 4 waves); 24576 rows 16.6 -> 16.1 us
-//               (15.5 -> 14.8) and the 248320-row lm_head 123.9 -> 117.7 us (stream, two quads per wave, both tiles
-//               of the next quad issued while the current one is summed; three quads per wave: 16.2 us)
+//   n_in 4096:  the stream kernel, one quad per wave up to 4096 quads: 4096 rows 6.80 -> 4.93 us, 12288 rows one
+//               column with the residual 8.9 -> 8.6 us against a form that split a quad's two chunks over two waves
+//               (once the staged blocks were loaded outside a branch; 10240 / 12352 rows two columns the same either
+//               way); 24576 rows 16.6 -> 16.1 us (15.5 -> 14.8) and the 248320-row lm_head 123.9 -> 117.7 us (two
+//               quads per wave, both tiles of the next quad issued while the current one is summed; three: 16.2 us)
 //   n_in 8192:  4096 rows 9.15 -> 8.19 us (stream, one quad per wave, two tiles ahead: one workgroup per CU; a quad's
-//               four chunks on two waves of a split workgroup, two workgroups per CU, 8.64 us)
+//               four chunks on two waves of one workgroup, two workgroups per CU, 8.64 us)
 //   n_in 12288: 4096 rows 11.8 -> 10.4 us (10.5 -> 9.6) (stream, one quad per wave, two tiles ahead; three ahead
 //               10.8 us, all six 13.2 us, two quads per wave 13.8 us, a quad on two waves 11.2 us)
 // RMI_PACKED_KERNEL=loop runs the loop kernel for every shape.
 struct PackedCfg {
-    enum Kind { kLoop, kSplit, kStream } kind;
-    int cs, nw;   // split: chunks per wave, waves per workgroup
+    enum Kind { kLoop, kStream } kind;
 };
 
 PackedCfg packed_cfg(int n_in, int n_out, int ncols) {
@@ -1377,36 +1252,10 @@ PackedCfg packed_cfg(int n_in, int n_out, int ncols) {
         const char* v = std::getenv("RMI_PACKED_KERNEL");
         return v && std::string(v) == "loop";
     }();
-    const int nch = n_in / kChunkElems, nq = (n_out + kQuad - 1) / kQuad;
-    if (loop_only || ncols > 2) return {PackedCfg::kLoop, 0, 0};
-    if (nch == 2) {
-        if (nq <= 1024) return {PackedCfg::kStream, 0, 0};   // one quad per wave (the output projections)
-        if (nq <= 4096) return {PackedCfg::kSplit, 1, 4};
-        return {PackedCfg::kStream, 0, 0};
-    }
-    if (nch == 4) return {PackedCfg::kStream, 0, 0};
-    if (nch == 6) return {PackedCfg::kStream, 0, 0};
-    return {PackedCfg::kLoop, 0, 0};
-}
-
-// the stage plus the (scale, sum) hand-over of the quads' second waves
-size_t split_lds(int n_in, int ncols, int cs, int nw) {
-    return static_cast<size_t>(ncols) * (n_in / 32) * 48 + static_cast<size_t>(nw) * cs * (ncols + 1) * 64 * 4;
-}
-
-template <int NCOLS, bool RES, int CS, int NW>
-void launch_split(const uint8_t* wp, const uint8_t* x, float* y, const float* res, float* partials, int n_in,
-                  int n_out, hipStream_t s) {
-    const int nch = n_in / kChunkElems, S = nch / CS, QW = NW / S;
-    const int nq = (n_out + kQuad - 1) / kQuad;
-    const dim3 grid((nq + QW - 1) / QW), block(64 * NW);
-    const size_t lds = split_lds(n_in, NCOLS, CS, NW);
-    if (NCOLS * (n_in / 32) <= 64 * NW)   // one block per lane
-        hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW, 1>), grid, block, lds, s, wp, x, y, res, partials,
-                           n_in, n_out);
-    else
-        hipLaunchKernelGGL((q6k_packed_gemv_split<NCOLS, RES, CS, NW>), grid, block, lds, s, wp, x, y, res, partials,
-                           n_in, n_out);
+    const int nch = n_in / kChunkElems;
+    if (loop_only || ncols > 2) return {PackedCfg::kLoop};
+    if (nch == 2 || nch == 4 || nch == 6) return {PackedCfg::kStream};
+    return {PackedCfg::kLoop};
 }
 
 template <int NCOLS, bool RES, int NCH, int QPW, int NW, int PD>
@@ -1425,18 +1274,14 @@ void launch_packed(const uint8_t* wp, const uint8_t* x, float* y, const float* r
     if constexpr (NCOLS <= 2) {
         const PackedCfg c = packed_cfg(n_in, n_out, NCOLS);
         if (c.kind == PackedCfg::kStream) {
-            if (n_in / kChunkElems == 2) {
-                if ((n_out + kQuad - 1) / kQuad <= 1024)
+            if (n_in / kChunkElems == 2) {   // one quad per wave up to 4096 quads, two above (the lm_heads)
+                if ((n_out + kQuad - 1) / kQuad <= 4096)
                     return launch_stream<NCOLS, RES, 2, 1, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
                 return launch_stream<NCOLS, RES, 2, 2, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
             }
             if (n_in / kChunkElems == 4)
                 return launch_stream<NCOLS, RES, 4, 1, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
             return launch_stream<NCOLS, RES, 6, 1, 4, 2>(wp, x, y, res, partials, n_in, n_out, s);
-        }
-        if (c.kind == PackedCfg::kSplit) {
-            if (c.cs == 2) return launch_split<NCOLS, RES, 2, 4>(wp, x, y, res, partials, n_in, n_out, s);
-            return launch_split<NCOLS, RES, 1, 4>(wp, x, y, res, partials, n_in, n_out, s);
         }
     }
     const int nq = (n_out + kQuad - 1) / kQuad;
